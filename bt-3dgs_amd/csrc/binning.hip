@@ -1,0 +1,558 @@
+// Tile binning: which Gaussians touch which 2D tile / 3D brick, as a list
+// sorted by (tile key, record id) plus per-tile lower-bound offsets.
+//
+//   count   one thread per record: the clamped tile rectangle/box and its
+//           area (r2splat/cuda/csrc/IsectTilesKernel.cu:57-113,
+//           IsectTiles3DKernel.cu:49-104), then an int64 exclusive scan.
+//   emit    wave-cooperative: the 64 records of a wave are expanded one after
+//           another by all 64 lanes, so a Gaussian covering thousands of
+//           tiles costs ceil(tiles/64) coalesced store rounds instead of a
+//           serial per-thread loop.  Emission order is the reference's
+//           (record id, then rows / z-y-x), keys are 32-bit.
+//   sort    stable LSD radix sort on bits [0, end_bit), 8-bit digits.  Per
+//           pass: LDS digit histogram per 4096-item tile, device scan of the
+//           digit-major histogram table, stable scatter with per-wave ranks
+//           from ballot-based digit matching (no per-item atomics).  The last
+//           pass widens keys to int64 on the way out.
+//   offsets lower_bound of every key in the sorted list (binary search).
+//
+// Because emission is in ascending record id and every pass is stable, the
+// output is the lexicographic (key, id) order -- identical to the
+// reference's CUB sort of the same records.
+#pragma clang fp contract(off)
+
+#include "r2s_common.h"
+#include "r2s_scan.h"
+
+namespace r2s {
+namespace {
+
+// ------------------------------------------------------------ geometry ---
+
+// IsectTilesKernel.cu:30-40: non-finite or <= 0 -> 0, >= upper -> upper.
+template <typename T>
+__device__ __forceinline__ uint32_t clamp_tile_bound(T v, uint32_t upper) {
+  if (!isfinite(v) || v <= static_cast<T>(0)) return 0u;
+  if (v >= static_cast<T>(upper)) return upper;
+  return static_cast<uint32_t>(v);
+}
+
+// Saturating float -> uint32 (the CUDA conversion used by the 3D bounds).
+template <typename T>
+__device__ __forceinline__ uint32_t sat_u32(T v) {
+  if (!(v > static_cast<T>(0))) return 0u;  // NaN and non-positive
+  if (v >= static_cast<T>(4294967295.0)) return 0xffffffffu;
+  return static_cast<uint32_t>(v);
+}
+
+struct Rect {
+  uint32_t x0, x1, y0, y1;
+};
+
+// Tile rectangle [x0,x1) x [y0,y1) and its area (0 = emits nothing).
+template <typename T>
+__device__ __forceinline__ uint32_t rect_2d(const T *__restrict__ means2d,
+                                            const int32_t *__restrict__ radii, int rect,
+                                            int64_t idx, uint32_t ts, uint32_t tw, uint32_t th,
+                                            Rect &r) {
+  r = {0, 0, 0, 0};
+  const T rx = static_cast<T>(rect ? radii[2 * idx] : radii[idx]);
+  const T ry = static_cast<T>(rect ? radii[2 * idx + 1] : radii[idx]);
+  if (rx <= static_cast<T>(0) || ry <= static_cast<T>(0)) return 0;
+  const T mx = means2d[2 * idx], my = means2d[2 * idx + 1];
+  if (!isfinite(mx) || !isfinite(my)) return 0;
+  const T tsf = static_cast<T>(ts);
+  const T trx = rx / tsf, tyr = ry / tsf, tx = mx / tsf, ty = my / tsf;
+  r.x0 = clamp_tile_bound(floor(tx - trx), tw);
+  r.y0 = clamp_tile_bound(floor(ty - tyr), th);
+  r.x1 = clamp_tile_bound(ceil(tx + trx), tw);
+  r.y1 = clamp_tile_bound(ceil(ty + tyr), th);
+  if (r.x1 <= r.x0 || r.y1 <= r.y0) return 0;
+  return (r.y1 - r.y0) * (r.x1 - r.x0);
+}
+
+struct Box {
+  uint32_t lo[3], hi[3];  // (dim2, dim1, dim0)
+};
+
+template <typename T>
+__device__ __forceinline__ uint32_t box_3d(const T *__restrict__ means3d,
+                                           const int32_t *__restrict__ radii, int64_t idx,
+                                           uint32_t ts, const uint32_t n[3], Box &b) {
+#pragma unroll
+  for (int a = 0; a < 3; ++a) b.lo[a] = b.hi[a] = 0;
+  const T r0 = static_cast<T>(radii[3 * idx]), r1 = static_cast<T>(radii[3 * idx + 1]),
+          r2 = static_cast<T>(radii[3 * idx + 2]);
+  if (r0 <= static_cast<T>(0) || r1 <= static_cast<T>(0) || r2 <= static_cast<T>(0)) return 0;
+  const T tsf = static_cast<T>(ts);
+  const T rr[3] = {r0, r1, r2};
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    const T c = means3d[3 * idx + a] / tsf;
+    const T rt = rr[a] / tsf;
+    b.lo[a] = min(sat_u32(floor(c - rt)), n[a]);
+    b.hi[a] = min(sat_u32(ceil(c + rt)), n[a]);
+  }
+  return (b.hi[2] - b.lo[2]) * (b.hi[1] - b.lo[1]) * (b.hi[0] - b.lo[0]);
+}
+
+// --------------------------------------------------------------- count ---
+
+template <typename T>
+__global__ __launch_bounds__(256) void count_2d_kernel(const T *__restrict__ means2d,
+                                                       const int32_t *__restrict__ radii,
+                                                       int rect, int64_t M, uint32_t ts,
+                                                       uint32_t tw, uint32_t th,
+                                                       int32_t *__restrict__ counts) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= M) return;
+  Rect r;
+  counts[idx] = static_cast<int32_t>(rect_2d(means2d, radii, rect, idx, ts, tw, th, r));
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void count_3d_kernel(const T *__restrict__ means3d,
+                                                       const int32_t *__restrict__ radii,
+                                                       int64_t N, uint32_t ts, uint32_t n2,
+                                                       uint32_t n1, uint32_t n0,
+                                                       int32_t *__restrict__ counts) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= N) return;
+  const uint32_t n[3] = {n2, n1, n0};
+  Box b;
+  counts[idx] = static_cast<int32_t>(box_3d(means3d, radii, idx, ts, n, b));
+}
+
+// ---------------------------------------------------------------- emit ---
+
+template <typename T>
+__global__ __launch_bounds__(256) void emit_2d_kernel(
+    const T *__restrict__ means2d, const int32_t *__restrict__ radii, int rect, int64_t M,
+    int64_t N, uint32_t ts, uint32_t tw, uint32_t th, const int64_t *__restrict__ offsets,
+    uint32_t *__restrict__ keys, uint32_t *__restrict__ vals) {
+  const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + (threadIdx.x & ~63u);
+  const int64_t idx = wave_first + lane_id();
+  Rect r = {0, 0, 0, 0};
+  uint32_t cnt = 0;
+  int64_t off = 0;
+  if (idx < M) {
+    cnt = rect_2d(means2d, radii, rect, idx, ts, tw, th, r);
+    off = offsets[idx];
+  }
+  const uint32_t n_tiles = tw * th;
+  const uint32_t width = r.x1 - r.x0;
+  uint64_t todo = ballot(cnt > 0);
+  while (todo) {
+    const uint32_t j = static_cast<uint32_t>(__builtin_ctzll(todo));
+    todo &= todo - 1;
+    const uint32_t cj = readlane_u32(cnt, j);
+    const uint32_t wj = readlane_u32(width, j);
+    const uint32_t x0 = readlane_u32(r.x0, j), y0 = readlane_u32(r.y0, j);
+    const int64_t base = readlane_i64(off, j);
+    const int64_t gid = wave_first + j;
+    const uint32_t kbase = static_cast<uint32_t>(gid / N) * n_tiles;
+    for (uint32_t k = lane_id(); k < cj; k += 64) {
+      const uint32_t row = k / wj, col = k - row * wj;
+      keys[base + k] = kbase + (y0 + row) * tw + (x0 + col);
+      vals[base + k] = static_cast<uint32_t>(gid);
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void emit_3d_kernel(
+    const T *__restrict__ means3d, const int32_t *__restrict__ radii, int64_t N, uint32_t ts,
+    uint32_t n2, uint32_t n1, uint32_t n0, const int64_t *__restrict__ offsets,
+    uint32_t *__restrict__ keys, uint32_t *__restrict__ vals) {
+  const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + (threadIdx.x & ~63u);
+  const int64_t idx = wave_first + lane_id();
+  const uint32_t n[3] = {n2, n1, n0};
+  Box b;
+  uint32_t cnt = 0;
+  int64_t off = 0;
+  if (idx < N) {
+    cnt = box_3d(means3d, radii, idx, ts, n, b);
+    off = offsets[idx];
+  } else {
+#pragma unroll
+    for (int a = 0; a < 3; ++a) b.lo[a] = b.hi[a] = 0;
+  }
+  const uint32_t e2 = b.hi[0] - b.lo[0], e1 = b.hi[1] - b.lo[1];
+  uint64_t todo = ballot(cnt > 0);
+  while (todo) {
+    const uint32_t j = static_cast<uint32_t>(__builtin_ctzll(todo));
+    todo &= todo - 1;
+    const uint32_t cj = readlane_u32(cnt, j);
+    const uint32_t e2j = readlane_u32(e2, j), e1j = readlane_u32(e1, j);
+    const uint32_t l2 = readlane_u32(b.lo[0], j), l1 = readlane_u32(b.lo[1], j),
+                   l0 = readlane_u32(b.lo[2], j);
+    const int64_t base = readlane_i64(off, j);
+    const uint32_t gid = static_cast<uint32_t>(wave_first + j);
+    const uint32_t plane = e2j * e1j;
+    for (uint32_t k = lane_id(); k < cj; k += 64) {
+      const uint32_t t0 = k / plane, rem = k - t0 * plane;
+      const uint32_t t1 = rem / e2j, t2 = rem - t1 * e2j;
+      keys[base + k] = (l0 + t0) * (n1 * n2) + (l1 + t1) * n2 + (l2 + t2);
+      vals[base + k] = gid;
+    }
+  }
+}
+
+// ---------------------------------------------------------- radix sort ---
+
+constexpr int kSortThreads = 256;                       // 4 waves
+constexpr int kSortRounds = 16;                         // 64-item rounds per wave
+constexpr int kSortWaveItems = 64 * kSortRounds;        // 1024
+constexpr int kSortTile = 4 * kSortWaveItems;           // 4096 items per block
+constexpr int kRadixBits = 8;
+constexpr int kRadix = 1 << kRadixBits;
+
+__global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(const uint32_t *__restrict__ keys,
+                                                                  int64_t n, uint32_t shift,
+                                                                  uint32_t mask,
+                                                                  uint32_t *__restrict__ hist,
+                                                                  uint32_t nblocks) {
+  __shared__ uint32_t h[kRadix];
+  h[threadIdx.x] = 0;
+  __syncthreads();
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kSortTile;
+  for (int i = threadIdx.x; i < kSortTile; i += kSortThreads) {
+    const int64_t k = base + i;
+    if (k < n) atomicAdd(&h[(keys[k] >> shift) & mask], 1u);
+  }
+  __syncthreads();
+  hist[static_cast<int64_t>(threadIdx.x) * nblocks + blockIdx.x] = h[threadIdx.x];
+}
+
+template <bool kFinal>
+__global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
+    const uint32_t *__restrict__ keys_in, const uint32_t *__restrict__ vals_in, int64_t n,
+    uint32_t shift, uint32_t bits, const uint32_t *__restrict__ digit_offsets, uint32_t nblocks,
+    uint32_t *__restrict__ keys_out, uint32_t *__restrict__ vals_out,
+    int64_t *__restrict__ keys_out64, int32_t *__restrict__ vals_out32) {
+  __shared__ uint32_t cnt[4][kRadix];
+  __shared__ uint32_t wbase[4][kRadix];
+  const uint32_t w = threadIdx.x / 64, lane = threadIdx.x % 64;
+  for (int k = threadIdx.x; k < 4 * kRadix; k += kSortThreads) (&cnt[0][0])[k] = 0;
+  __syncthreads();
+  const uint32_t mask = (1u << bits) - 1u;
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * kSortTile + w * kSortWaveItems;
+  const uint64_t lt = lanemask_lt();
+  uint32_t key[kSortRounds], val[kSortRounds], rank[kSortRounds];
+#pragma unroll
+  for (int r = 0; r < kSortRounds; ++r) {
+    const int64_t i = first + r * 64 + lane;
+    const bool valid = i < n;
+    key[r] = valid ? keys_in[i] : 0u;
+    val[r] = valid ? vals_in[i] : 0u;
+    const uint32_t d = (key[r] >> shift) & mask;
+    // Lanes holding the same digit: intersect the ballots of every digit bit.
+    uint64_t peers = ballot(valid);
+    for (uint32_t b = 0; b < bits; ++b) {
+      const bool bit = (d >> b) & 1u;
+      const uint64_t bal = ballot(bit);
+      peers &= bit ? bal : ~bal;
+    }
+    uint32_t c = 0;
+    if (valid) c = cnt[w][d];
+    rank[r] = c + static_cast<uint32_t>(__popcll(peers & lt));
+    // The highest lane of each digit group advances that digit's counter.
+    if (valid && lane == 63u - static_cast<uint32_t>(__clzll(peers)))
+      cnt[w][d] = c + static_cast<uint32_t>(__popcll(peers));
+  }
+  __syncthreads();
+  {
+    const uint32_t d = threadIdx.x;
+    uint32_t s = 0;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) {
+      wbase[ww][d] = s;
+      s += cnt[ww][d];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < kSortRounds; ++r) {
+    const int64_t i = first + r * 64 + lane;
+    if (i < n) {
+      const uint32_t d = (key[r] >> shift) & mask;
+      const int64_t dest = static_cast<int64_t>(digit_offsets[static_cast<int64_t>(d) * nblocks +
+                                                              blockIdx.x]) +
+                           wbase[w][d] + rank[r];
+      if (kFinal) {
+        keys_out64[dest] = static_cast<int64_t>(key[r]);
+        vals_out32[dest] = static_cast<int32_t>(val[r]);
+      } else {
+        keys_out[dest] = key[r];
+        vals_out[dest] = val[r];
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------- offsets ---
+
+__global__ __launch_bounds__(256) void offset_encode_kernel(const int64_t *__restrict__ ids,
+                                                            int64_t n, int64_t n_keys,
+                                                            int32_t *__restrict__ out) {
+  const int64_t k = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (k >= n_keys) return;
+  int64_t lo = 0, hi = n;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (ids[mid] < k)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  out[k] = static_cast<int32_t>(lo);
+}
+
+// ----------------------------------------------------------- workspace ---
+
+struct SortSpace {
+  uint32_t *ka, *va, *kb, *vb, *hist, *hist_scan, *partials;
+  int64_t nblocks, n_hist;
+};
+
+SortSpace carve_sort(Carver &cv, int64_t n) {
+  SortSpace s;
+  s.nblocks = ceil_div(n, kSortTile);
+  s.n_hist = s.nblocks * kRadix;
+  s.ka = cv.take<uint32_t>(n);
+  s.va = cv.take<uint32_t>(n);
+  s.kb = cv.take<uint32_t>(n);
+  s.vb = cv.take<uint32_t>(n);
+  s.hist = cv.take<uint32_t>(s.n_hist);
+  s.hist_scan = cv.take<uint32_t>(s.n_hist);
+  s.partials = cv.take<uint32_t>(scan_partials_count(s.n_hist));
+  return s;
+}
+
+int64_t count_space_bytes(int64_t n_items) {
+  Carver cv(nullptr);
+  cv.take<int64_t>(scan_partials_count(n_items));
+  return static_cast<int64_t>(cv.used);
+}
+
+int64_t sort_space_bytes(int64_t n) {
+  Carver cv(nullptr);
+  carve_sort(cv, n);
+  return static_cast<int64_t>(cv.used);
+}
+
+// Sorts the emitted (keys, vals) held in s.ka / s.va into the final outputs.
+int radix_sort(SortSpace &s, int64_t n, uint32_t end_bit, int64_t *keys64, int32_t *vals32,
+               hipStream_t stream) {
+  const int passes = static_cast<int>((end_bit + kRadixBits - 1) / kRadixBits);
+  uint32_t *kin = s.ka, *vin = s.va, *kout = s.kb, *vout = s.vb;
+  const uint32_t nb = static_cast<uint32_t>(s.nblocks);
+  for (int p = 0; p < passes; ++p) {
+    const uint32_t shift = static_cast<uint32_t>(p * kRadixBits);
+    const uint32_t bits = min(static_cast<uint32_t>(kRadixBits), end_bit - shift);
+    const uint32_t mask = (1u << bits) - 1u;
+    radix_hist_kernel<<<dim3(nb), dim3(kSortThreads), 0, stream>>>(kin, n, shift, mask, s.hist, nb);
+    R2S_RETURN_IF(device_exclusive_scan<uint32_t, uint32_t>(s.hist, s.n_hist, s.hist_scan,
+                                                            nullptr, s.partials, stream,
+                                                            "isect sort scan"));
+    if (p == passes - 1) {
+      radix_scatter_kernel<true><<<dim3(nb), dim3(kSortThreads), 0, stream>>>(
+          kin, vin, n, shift, bits, s.hist_scan, nb, nullptr, nullptr, keys64, vals32);
+    } else {
+      radix_scatter_kernel<false><<<dim3(nb), dim3(kSortThreads), 0, stream>>>(
+          kin, vin, n, shift, bits, s.hist_scan, nb, kout, vout, nullptr, nullptr);
+      uint32_t *tk = kin, *tv = vin;
+      kin = kout;
+      vin = vout;
+      kout = tk;
+      vout = tv;
+    }
+    R2S_RETURN_IF(check_launch("isect sort pass"));
+  }
+  return R2S_OK;
+}
+
+// ---------------------------------------------------------------- host ---
+
+int check_workspace(void *ws, size_t have, int64_t need, const char *name) {
+  if (need > 0 && (ws == nullptr || static_cast<int64_t>(have) < need)) {
+    set_error("%s: workspace of %zu bytes, %lld required", name, have, (long long)need);
+    return R2S_EWORKSPACE;
+  }
+  return R2S_OK;
+}
+
+template <typename T>
+int count_2d_impl(const T *means2d, const int32_t *radii, int rect, int64_t C, int64_t N,
+                  uint32_t ts, uint32_t tw, uint32_t th, int32_t *counts, int64_t *offsets,
+                  void *ws, size_t ws_bytes, r2s_stream_t st) {
+  clear_error();
+  const char *name = "isect_tiles";
+  R2S_REQUIRE(C >= 0 && N >= 0 && C * N <= kInt32Max, "%s: bad size C=%lld N=%lld", name,
+              (long long)C, (long long)N);
+  R2S_REQUIRE(ts > 0, "%s: tile_size must be positive", name);
+  R2S_REQUIRE(static_cast<uint64_t>(C) * tw * th <= 0xffffffffull,
+              "%s: C * n_tiles exceeds 32 bits", name);
+  R2S_REQUIRE(offsets != nullptr, "%s: null offsets", name);
+  const int64_t M = C * N;
+  hipStream_t stream = as_stream(st);
+  if (M == 0) return device_fill<int64_t>(offsets, 1, 0, stream, name);
+  R2S_REQUIRE(means2d && radii && counts, "%s: null pointer", name);
+  R2S_RETURN_IF(check_workspace(ws, ws_bytes, count_space_bytes(M), name));
+  Carver cv(ws);
+  int64_t *partials = cv.take<int64_t>(scan_partials_count(M));
+  count_2d_kernel<T><<<dim3(static_cast<uint32_t>(ceil_div(M, 256))), dim3(256), 0, stream>>>(
+      means2d, radii, rect, M, ts, tw, th, counts);
+  R2S_RETURN_IF(check_launch(name));
+  return device_exclusive_scan<int32_t, int64_t>(counts, M, offsets, offsets + M, partials,
+                                                 stream, name);
+}
+
+template <typename T>
+int count_3d_impl(const T *means3d, const int32_t *radii, int64_t N, uint32_t ts, uint32_t n2,
+                  uint32_t n1, uint32_t n0, int32_t *counts, int64_t *offsets, void *ws,
+                  size_t ws_bytes, r2s_stream_t st) {
+  clear_error();
+  const char *name = "isect_tiles_3d";
+  R2S_REQUIRE(N >= 0 && N <= kInt32Max, "%s: bad size N=%lld", name, (long long)N);
+  R2S_REQUIRE(ts > 0, "%s: tile_size must be positive", name);
+  R2S_REQUIRE(static_cast<uint64_t>(n2) * n1 * n0 <= 0xffffffffull,
+              "%s: n_tiles exceeds 32 bits", name);
+  R2S_REQUIRE(offsets != nullptr, "%s: null offsets", name);
+  hipStream_t stream = as_stream(st);
+  if (N == 0) return device_fill<int64_t>(offsets, 1, 0, stream, name);
+  R2S_REQUIRE(means3d && radii && counts, "%s: null pointer", name);
+  R2S_RETURN_IF(check_workspace(ws, ws_bytes, count_space_bytes(N), name));
+  Carver cv(ws);
+  int64_t *partials = cv.take<int64_t>(scan_partials_count(N));
+  count_3d_kernel<T><<<dim3(static_cast<uint32_t>(ceil_div(N, 256))), dim3(256), 0, stream>>>(
+      means3d, radii, N, ts, n2, n1, n0, counts);
+  R2S_RETURN_IF(check_launch(name));
+  return device_exclusive_scan<int32_t, int64_t>(counts, N, offsets, offsets + N, partials,
+                                                 stream, name);
+}
+
+int check_sort_args(int64_t n_isects, uint32_t end_bit, int64_t n_keys, void *ws,
+                    size_t ws_bytes, int64_t *keys, int32_t *vals, const char *name) {
+  R2S_REQUIRE(n_isects >= 0, "%s: negative n_isects", name);
+  if (n_isects > kInt32Max) {
+    set_error("%s: %lld intersections exceed the int32 offset range", name,
+              (long long)n_isects);
+    return R2S_ERANGE;
+  }
+  R2S_REQUIRE(end_bit >= 1 && end_bit <= 32, "%s: end_bit %u out of range", name, end_bit);
+  R2S_REQUIRE(n_keys <= (1ll << end_bit), "%s: end_bit %u too small for %lld keys", name,
+              end_bit, (long long)n_keys);
+  if (n_isects == 0) return R2S_OK;
+  R2S_REQUIRE(keys && vals, "%s: null output", name);
+  return check_workspace(ws, ws_bytes, sort_space_bytes(n_isects), name);
+}
+
+template <typename T>
+int emit_sort_2d_impl(const T *means2d, const int32_t *radii, int rect, int64_t C, int64_t N,
+                      uint32_t ts, uint32_t tw, uint32_t th, const int64_t *offsets,
+                      int64_t n_isects, uint32_t end_bit, int64_t *keys, int32_t *vals,
+                      void *ws, size_t ws_bytes, r2s_stream_t st) {
+  clear_error();
+  const char *name = "isect_tiles";
+  R2S_REQUIRE(C >= 0 && N >= 0 && C * N <= kInt32Max, "%s: bad size", name);
+  R2S_REQUIRE(ts > 0, "%s: tile_size must be positive", name);
+  R2S_RETURN_IF(check_sort_args(n_isects, end_bit, C * tw * th, ws, ws_bytes, keys, vals, name));
+  if (n_isects == 0) return R2S_OK;
+  R2S_REQUIRE(means2d && radii && offsets, "%s: null pointer", name);
+  hipStream_t stream = as_stream(st);
+  Carver cv(ws);
+  SortSpace s = carve_sort(cv, n_isects);
+  const int64_t M = C * N;
+  emit_2d_kernel<T><<<dim3(static_cast<uint32_t>(ceil_div(M, 256))), dim3(256), 0, stream>>>(
+      means2d, radii, rect, M, N, ts, tw, th, offsets, s.ka, s.va);
+  R2S_RETURN_IF(check_launch(name));
+  return radix_sort(s, n_isects, end_bit, keys, vals, stream);
+}
+
+template <typename T>
+int emit_sort_3d_impl(const T *means3d, const int32_t *radii, int64_t N, uint32_t ts,
+                      uint32_t n2, uint32_t n1, uint32_t n0, const int64_t *offsets,
+                      int64_t n_isects, uint32_t end_bit, int64_t *keys, int32_t *vals,
+                      void *ws, size_t ws_bytes, r2s_stream_t st) {
+  clear_error();
+  const char *name = "isect_tiles_3d";
+  R2S_REQUIRE(N >= 0 && N <= kInt32Max, "%s: bad size", name);
+  R2S_REQUIRE(ts > 0, "%s: tile_size must be positive", name);
+  R2S_RETURN_IF(check_sort_args(n_isects, end_bit, static_cast<int64_t>(n2) * n1 * n0, ws,
+                                ws_bytes, keys, vals, name));
+  if (n_isects == 0) return R2S_OK;
+  R2S_REQUIRE(means3d && radii && offsets, "%s: null pointer", name);
+  hipStream_t stream = as_stream(st);
+  Carver cv(ws);
+  SortSpace s = carve_sort(cv, n_isects);
+  emit_3d_kernel<T><<<dim3(static_cast<uint32_t>(ceil_div(N, 256))), dim3(256), 0, stream>>>(
+      means3d, radii, N, ts, n2, n1, n0, offsets, s.ka, s.va);
+  R2S_RETURN_IF(check_launch(name));
+  return radix_sort(s, n_isects, end_bit, keys, vals, stream);
+}
+
+}  // namespace
+}  // namespace r2s
+
+extern "C" {
+
+int64_t r2s_isect_workspace_bytes(int64_t n_items, int64_t n_isects, uint32_t end_bit) {
+  (void)end_bit;
+  const int64_t a = n_items > 0 ? r2s::count_space_bytes(n_items) : 0;
+  const int64_t b = n_isects > 0 ? r2s::sort_space_bytes(n_isects) : 0;
+  return a > b ? a : b;
+}
+
+#define R2S_BIN_API(SUF, T)                                                                   \
+  int r2s_isect_count_2d_##SUF(const T *means2d, const int32_t *radii, int rect, int64_t C,   \
+                               int64_t N, uint32_t ts, uint32_t tw, uint32_t th,              \
+                               int32_t *counts, int64_t *offsets, void *ws, size_t ws_bytes,  \
+                               r2s_stream_t st) {                                             \
+    return r2s::count_2d_impl<T>(means2d, radii, rect, C, N, ts, tw, th, counts, offsets, ws, \
+                                 ws_bytes, st);                                               \
+  }                                                                                           \
+  int r2s_isect_emit_sort_2d_##SUF(const T *means2d, const int32_t *radii, int rect,          \
+                                   int64_t C, int64_t N, uint32_t ts, uint32_t tw,            \
+                                   uint32_t th, const int64_t *offsets, int64_t n_isects,     \
+                                   uint32_t end_bit, int64_t *keys, int32_t *vals, void *ws,  \
+                                   size_t ws_bytes, r2s_stream_t st) {                        \
+    return r2s::emit_sort_2d_impl<T>(means2d, radii, rect, C, N, ts, tw, th, offsets,         \
+                                     n_isects, end_bit, keys, vals, ws, ws_bytes, st);        \
+  }                                                                                           \
+  int r2s_isect_count_3d_##SUF(const T *means3d, const int32_t *radii, int64_t N,            \
+                               uint32_t ts, uint32_t n2, uint32_t n1, uint32_t n0,            \
+                               int32_t *counts, int64_t *offsets, void *ws, size_t ws_bytes,  \
+                               r2s_stream_t st) {                                             \
+    return r2s::count_3d_impl<T>(means3d, radii, N, ts, n2, n1, n0, counts, offsets, ws,      \
+                                 ws_bytes, st);                                               \
+  }                                                                                           \
+  int r2s_isect_emit_sort_3d_##SUF(const T *means3d, const int32_t *radii, int64_t N,        \
+                                   uint32_t ts, uint32_t n2, uint32_t n1, uint32_t n0,        \
+                                   const int64_t *offsets, int64_t n_isects,                  \
+                                   uint32_t end_bit, int64_t *keys, int32_t *vals, void *ws,  \
+                                   size_t ws_bytes, r2s_stream_t st) {                        \
+    return r2s::emit_sort_3d_impl<T>(means3d, radii, N, ts, n2, n1, n0, offsets, n_isects,    \
+                                     end_bit, keys, vals, ws, ws_bytes, st);                  \
+  }
+
+R2S_BIN_API(f32, float)
+R2S_BIN_API(f64, double)
+
+#undef R2S_BIN_API
+
+int r2s_isect_offset_encode(const int64_t *ids, int64_t n_isects, int64_t n_keys,
+                            int32_t *out, r2s_stream_t st) {
+  r2s::clear_error();
+  R2S_REQUIRE(n_isects >= 0 && n_keys >= 0, "isect_offset_encode: negative size");
+  if (n_keys == 0) return R2S_OK;
+  R2S_REQUIRE(out != nullptr, "isect_offset_encode: null output");
+  hipStream_t stream = r2s::as_stream(st);
+  if (n_isects == 0) return r2s::device_fill<int32_t>(out, n_keys, 0, stream, "isect_offset_encode");
+  R2S_REQUIRE(ids != nullptr, "isect_offset_encode: null isect_ids");
+  r2s::offset_encode_kernel<<<dim3(static_cast<uint32_t>(r2s::ceil_div(n_keys, 256))), dim3(256), 0,
+                              stream>>>(ids, n_isects, n_keys, out);
+  return r2s::check_launch("isect_offset_encode");
+}
+
+}  // extern "C"

@@ -1,0 +1,120 @@
+// Shared helpers of the r2splat HIP library (gfx950, wave64).
+//
+// Host side: status codes, the per-thread error message, launch checking and
+// a bump allocator that carves caller-provided workspace.  Device side:
+// wave-level primitives used by the binning sort, the compaction scan and
+// the reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "r2splat_hip.h"
+
+namespace r2s {
+
+// ---------------------------------------------------------------- host ----
+
+void set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+
+// Returns R2S_OK, or R2S_EHIP with the message set, after a launch sequence.
+int check_launch(const char *what);
+
+inline hipStream_t as_stream(r2s_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+#define R2S_REQUIRE(cond, ...)            \
+  do {                                    \
+    if (!(cond)) {                        \
+      ::r2s::set_error(__VA_ARGS__);      \
+      return R2S_EINVAL;                  \
+    }                                     \
+  } while (0)
+
+#define R2S_RETURN_IF(...)                \
+  do {                                    \
+    int _st = (__VA_ARGS__);              \
+    if (_st != R2S_OK) return _st;        \
+  } while (0)
+
+constexpr int64_t kInt32Max = 2147483647LL;
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Carves 256-byte aligned sub-buffers out of a caller-provided workspace.
+// `base == nullptr` measures only (used by the *_workspace_bytes queries).
+struct Carver {
+  char *base;
+  size_t used = 0;
+  explicit Carver(void *b) : base(static_cast<char *>(b)) {}
+  template <typename T>
+  T *take(int64_t count) {
+    size_t off = align_up(used, 256);
+    used = off + static_cast<size_t>(count > 0 ? count : 0) * sizeof(T);
+    return base ? reinterpret_cast<T *>(base + off) : nullptr;
+  }
+};
+
+// Block-id swizzle so that consecutive logical tiles land on the same XCD.
+// Hardware dispatches workgroup b to XCD (b % 8); logical id L is mapped to
+// a contiguous range per XCD.  A bijection on [0, n).
+__device__ __forceinline__ uint32_t xcd_swizzle(uint32_t b, uint32_t n) {
+  constexpr uint32_t kXcd = 8;
+  const uint32_t q = n / kXcd, r = n % kXcd;
+  const uint32_t x = b % kXcd, k = b / kXcd;
+  return (x < r) ? x * (q + 1) + k : r * (q + 1) + (x - r) * q + k;
+}
+
+// ------------------------------------------------------------- device ----
+
+__device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
+
+// Mask of lanes strictly below the calling lane.
+__device__ __forceinline__ uint64_t lanemask_lt() {
+  const uint32_t l = __lane_id();
+  return (l == 0) ? 0ull : ((~0ull) >> (64u - l));
+}
+
+// Number of set bits of `mask` below the calling lane (v_mbcnt pair).
+__device__ __forceinline__ uint32_t mbcnt(uint64_t mask) {
+  uint32_t lo = __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u);
+  return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32), lo);
+}
+
+__device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
+
+// Value of `v` in lane `src` (src must be wave-uniform).
+__device__ __forceinline__ uint32_t readlane_u32(uint32_t v, uint32_t src) {
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), static_cast<int>(src)));
+}
+__device__ __forceinline__ int64_t readlane_i64(int64_t v, uint32_t src) {
+  uint32_t lo = readlane_u32(static_cast<uint32_t>(v), src);
+  uint32_t hi = readlane_u32(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32), src);
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// Wave64 inclusive prefix sum (Hillis-Steele over lane shuffles).
+template <typename T>
+__device__ __forceinline__ T wave_inclusive_scan(T v) {
+  const uint32_t l = __lane_id();
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    T o = __shfl_up(v, off, 64);
+    if (l >= static_cast<uint32_t>(off)) v += o;
+  }
+  return v;
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Hardware float atomics (no CAS loop; built with -munsafe-fp-atomics).
+__device__ __forceinline__ void atomic_add(float *p, float v) { unsafeAtomicAdd(p, v); }
+__device__ __forceinline__ void atomic_add(double *p, double v) { unsafeAtomicAdd(p, v); }
+
+}  // namespace r2s

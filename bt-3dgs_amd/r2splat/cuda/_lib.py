@@ -1,0 +1,83 @@
+"""ctypes bindings of ``libr2splat_hip.so`` (declarations in include/r2splat_hip.h)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+__all__ = ["LIB_PATH", "load", "SYMBOLS"]
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "lib",
+                        "libr2splat_hip.so")
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_u32 = ctypes.c_uint32
+_i32 = ctypes.c_int
+_f32 = ctypes.c_float
+_f64 = ctypes.c_double
+_sz = ctypes.c_size_t
+
+# name -> (restype, argtypes); the f32/f64 pairs share argument kinds.
+_FLOAT_OPS = {
+    "parameter_transform_fwd": [_p, _p, _f64, _f64, _p, _p, _i64, _p],
+    "parameter_transform_bwd": [_p, _p, _f64, _f64, _p, _p, _p, _i64, _p],
+    "prepare_gaussians": [_p, _p, _p, _f64, _f64, _p, _p, _p, _i64, _p],
+    "opacity_bwd": [_p, _p, _p, _p, _i64, _i64, _p],
+    "world_to_image_projection_fwd": [_p, _p, _p, _p, _u32, _u32, _f32, _f32, _p, _p, _p,
+                                      _i64, _i64, _p],
+    "world_to_image_projection_bwd": [_p, _p, _p, _p, _u32, _u32, _p, _p, _p, _p, _i64, _i64, _p],
+    "conics_mu_fwd": [_p, _f64, _p, _p, _i64, _p],
+    "conics_mu_bwd": [_p, _f64, _p, _p, _p, _p, _p, _i64, _p],
+    "project_gaussians_fwd": [_p, _p, _p, _p, _p, _u32, _u32, _f64, _f32, _p, _p, _p, _p, _p,
+                              _p, _i64, _i64, _p],
+    "project_gaussians_bwd": [_p, _p, _p, _p, _u32, _u32, _f64, _p, _p, _p, _p, _p, _p, _p, _p,
+                              _i64, _i64, _p],
+    "isect_count_2d": [_p, _p, _i32, _i64, _i64, _u32, _u32, _u32, _p, _p, _p, _sz, _p],
+    "isect_emit_sort_2d": [_p, _p, _i32, _i64, _i64, _u32, _u32, _u32, _p, _i64, _u32, _p, _p,
+                           _p, _sz, _p],
+    "isect_count_3d": [_p, _p, _i64, _u32, _u32, _u32, _u32, _p, _p, _p, _sz, _p],
+    "isect_emit_sort_3d": [_p, _p, _i64, _u32, _u32, _u32, _u32, _p, _i64, _u32, _p, _p, _p,
+                           _sz, _p],
+    "rasterize_fwd": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _u32, _u32, _u32, _u32, _u32,
+                      _p, _p, _sz, _p],
+    "rasterize_bwd": [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _u32, _u32, _u32, _u32,
+                      _u32, _p, _p, _p, _p, _p, _p],
+    "world_to_volume_mapping_fwd": [_p, _p, _p, _p, _u32, _u32, _u32, _f64, _f64, _p, _p, _p,
+                                    _i64, _p],
+    "world_to_volume_mapping_bwd": [_p, _p, _p, _p, _u32, _u32, _u32, _f64, _p, _p, _p, _p,
+                                    _i64, _p],
+    "voxelize_fwd": [_p, _p, _p, _p, _p, _i64, _i64, _u32, _u32, _u32, _u32, _u32, _u32, _u32,
+                     _p, _p],
+    "voxelize_bwd": [_p, _p, _p, _p, _p, _p, _i64, _p, _i64, _u32, _u32, _u32, _u32, _u32, _u32,
+                     _u32, _p, _p, _p, _p],
+}
+
+_PLAIN = {
+    "r2s_last_error": (ctypes.c_char_p, []),
+    "r2s_abi_version": (_i32, []),
+    "r2s_isect_workspace_bytes": (_i64, [_i64, _i64, _u32]),
+    "r2s_isect_offset_encode": (_i32, [_p, _i64, _i64, _p, _p]),
+    "r2s_rasterize_workspace_bytes": (_i64, [_i64, _i64, _u32, _i32]),
+    "r2s_mask_workspace_bytes": (_i64, [_i64]),
+    "r2s_mask_split": (_i32, [_p, _i64, _p, _p, _p, _sz, _p]),
+}
+
+SYMBOLS = sorted(list(_PLAIN) + [f"r2s_{n}_{s}" for n in _FLOAT_OPS for s in ("f32", "f64")])
+
+ABI_VERSION = 1
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """dlopen the library and attach the C signatures of every exported symbol."""
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in _PLAIN.items():
+        fn = getattr(lib, name)
+        fn.restype, fn.argtypes = res, args
+    for name, args in _FLOAT_OPS.items():
+        for suffix in ("f32", "f64"):
+            fn = getattr(lib, f"r2s_{name}_{suffix}")
+            fn.restype, fn.argtypes = _i32, args
+    if lib.r2s_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"{path}: ABI version {lib.r2s_abi_version()} != {ABI_VERSION}")
+    return lib

@@ -1,0 +1,766 @@
+"""Tensor-level operators over the HIP C ABI.
+
+Each function keeps the name, argument order, return tuple and input checks
+of the reference pybind operator it replaces (``r2splat/cuda/include/Ops.h``
+and the ``*.cpp`` tensor wrappers in ``r2splat/cuda/csrc``).  Outputs and
+scratch space are allocated with torch's caching allocator on the input's
+device; work is enqueued on torch's current stream of that device.  There is
+no CPU fallback: without the library every call raises ``RuntimeError``.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+
+from . import _backend
+
+Tensor = torch.Tensor
+
+
+# ---------------------------------------------------------------- plumbing --
+
+def _lib():
+    return _backend.library()
+
+
+def _check_input(t: Tensor, name: str) -> None:
+    # common.h:25-30 R2SPLAT_CHECK_INPUT
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise RuntimeError(f"{name} must be a CUDA tensor")
+    if not t.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous")
+
+
+def _check(cond: bool, *msg) -> None:
+    if not cond:
+        raise RuntimeError("".join(str(m) for m in msg))
+
+
+def _suffix(t: Tensor, op: str) -> str:
+    # AT_DISPATCH_FLOATING_TYPES: float32 and float64 only.
+    if t.dtype == torch.float32:
+        return "f32"
+    if t.dtype == torch.float64:
+        return "f64"
+    raise RuntimeError(f'"{op}" not implemented for \'{t.dtype}\'')
+
+
+def _ptr(t: Optional[Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _call(name: str, *args) -> None:
+    lib = _lib()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.r2s_last_error().decode(errors="replace")
+        raise RuntimeError(f"{name} failed ({rc}): {msg}")
+
+
+def _workspace(nbytes: int, device: torch.device) -> Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def _end_bit(n_keys: int) -> int:
+    # IsectTiles.cpp:146-147
+    return int(math.ceil(math.log2(float(n_keys + 1))))
+
+
+# ------------------------------------------------------ parameter transform --
+
+def parameter_transform_fwd(quats: Tensor, scale_ori: Tensor, scale_min: float,
+                            scale_max: float) -> Tuple[Tensor, Tensor]:
+    """ParameterTransform.cpp:34-84 -> (covars [N,6], max_scales [N])."""
+    _check_input(quats, "quats")
+    _check_input(scale_ori, "scale_ori")
+    _check(quats.dim() == 2 and quats.size(1) == 4,
+           "quats must be 2D [N, 4], got shape ", list(quats.shape))
+    _check(scale_ori.dim() == 2 and scale_ori.size(1) == 3,
+           "scale_ori must be 2D [N, 3], got shape ", list(scale_ori.shape))
+    N = quats.size(0)
+    _check(scale_ori.size(0) == N, "scale_ori batch dim (", scale_ori.size(0),
+           ") doesn't match quats N=", N)
+    covars = torch.empty((N, 6), dtype=quats.dtype, device=quats.device)
+    max_scales = torch.empty((N,), dtype=quats.dtype, device=quats.device)
+    if N == 0:
+        return covars, max_scales
+    _check(scale_ori.dtype == quats.dtype, "quats and scale_ori must share a dtype")
+    sfx = _suffix(quats, "parameter_transform_fwd")
+    with torch.cuda.device(quats.device):
+        _call(f"r2s_parameter_transform_fwd_{sfx}", _ptr(quats), _ptr(scale_ori),
+              float(scale_min), float(scale_max), _ptr(covars), _ptr(max_scales), N,
+              _stream(quats.device))
+    return covars, max_scales
+
+
+def parameter_transform_bwd(quats: Tensor, scale_ori: Tensor, scale_min: float,
+                            scale_max: float, v_covars: Tensor) -> Tuple[Tensor, Tensor]:
+    """ParameterTransform.cpp:90-144 -> (v_quats [N,4], v_scale_ori [N,3])."""
+    for t, n in ((quats, "quats"), (scale_ori, "scale_ori"), (v_covars, "v_covars")):
+        _check_input(t, n)
+    _check(quats.dim() == 2 and quats.size(1) == 4, "quats must be 2D [N, 4]")
+    _check(scale_ori.dim() == 2 and scale_ori.size(1) == 3, "scale_ori must be 2D [N, 3]")
+    _check(v_covars.dim() == 2 and v_covars.size(1) == 6, "v_covars must be 2D [N, 6]")
+    N = quats.size(0)
+    _check(scale_ori.size(0) == N and v_covars.size(0) == N, "Batch dimension mismatch")
+    v_quats = torch.empty((N, 4), dtype=quats.dtype, device=quats.device)
+    v_scale = torch.empty((N, 3), dtype=quats.dtype, device=quats.device)
+    if N == 0:
+        return v_quats, v_scale
+    _check(scale_ori.dtype == quats.dtype and v_covars.dtype == quats.dtype,
+           "quats, scale_ori and v_covars must share a dtype")
+    sfx = _suffix(quats, "parameter_transform_bwd")
+    with torch.cuda.device(quats.device):
+        _call(f"r2s_parameter_transform_bwd_{sfx}", _ptr(quats), _ptr(scale_ori),
+              float(scale_min), float(scale_max), _ptr(v_covars), _ptr(v_quats), _ptr(v_scale),
+              N, _stream(quats.device))
+    return v_quats, v_scale
+
+
+def prepare_gaussians(quats: Tensor, raw_scales: Tensor, raw_opacities: Tensor,
+                      scale_min: float, scale_max: float) -> Tuple[Tensor, Tensor, Tensor]:
+    """Fused parameter_transform_fwd + softplus (r2splat/ops/direct.py:85-91)."""
+    for t, n in ((quats, "quats"), (raw_scales, "scale_ori"), (raw_opacities, "raw_opacities")):
+        _check_input(t, n)
+    _check(quats.dim() == 2 and quats.size(1) == 4,
+           "quats must be 2D [N, 4], got shape ", list(quats.shape))
+    _check(raw_scales.dim() == 2 and raw_scales.size(1) == 3,
+           "scale_ori must be 2D [N, 3], got shape ", list(raw_scales.shape))
+    N = quats.size(0)
+    _check(raw_scales.size(0) == N, "scale_ori batch dim (", raw_scales.size(0),
+           ") doesn't match quats N=", N)
+    _check(raw_opacities.dim() == 1 and raw_opacities.size(0) == N,
+           "raw_opacities must be 1D [N]")
+    _check(raw_scales.dtype == quats.dtype and raw_opacities.dtype == quats.dtype,
+           "quats, scale_ori and raw_opacities must share a dtype")
+    dev, dt = quats.device, quats.dtype
+    covars = torch.empty((N, 6), dtype=dt, device=dev)
+    max_scales = torch.empty((N,), dtype=dt, device=dev)
+    opac = torch.empty((N,), dtype=dt, device=dev)
+    if N == 0:
+        return covars, max_scales, opac
+    sfx = _suffix(quats, "prepare_gaussians")
+    with torch.cuda.device(dev):
+        _call(f"r2s_prepare_gaussians_{sfx}", _ptr(quats), _ptr(raw_scales), _ptr(raw_opacities),
+              float(scale_min), float(scale_max), _ptr(covars), _ptr(max_scales), _ptr(opac), N,
+              _stream(dev))
+    return covars, max_scales, opac
+
+
+def opacity_bwd(raw_opacities: Tensor, v_opacity_cn: Optional[Tensor],
+                v_opacity_3d: Optional[Tensor]) -> Tensor:
+    """v_raw = (sum_c v_opacity_cn[c] + v_opacity_3d) * sigmoid(raw) (explicit.py:319,370,379)."""
+    _check_input(raw_opacities, "raw_opacities")
+    N = raw_opacities.size(0)
+    C = 0
+    if v_opacity_cn is not None:
+        _check_input(v_opacity_cn, "v_opacity")
+        _check(v_opacity_cn.dim() == 2 and v_opacity_cn.size(1) == N, "v_opacity must be [C, N]")
+        C = v_opacity_cn.size(0)
+    if v_opacity_3d is not None:
+        _check_input(v_opacity_3d, "v_opacity_3d")
+        _check(v_opacity_3d.shape == (N,), "v_opacity_3d must be [N]")
+    out = torch.empty_like(raw_opacities)
+    if N == 0:
+        return out
+    sfx = _suffix(raw_opacities, "opacity_bwd")
+    with torch.cuda.device(raw_opacities.device):
+        _call(f"r2s_opacity_bwd_{sfx}", _ptr(raw_opacities), _ptr(v_opacity_cn),
+              _ptr(v_opacity_3d), _ptr(out), C, N, _stream(raw_opacities.device))
+    return out
+
+
+# ------------------------------------------------------------- projection --
+
+def _check_cameras(means, covars, viewmats, Ks):
+    _check(means.dim() == 2 and means.size(1) == 3,
+           "means must be 2D [N, 3], got shape ", list(means.shape))
+    _check(covars.dim() == 2 and covars.size(1) == 6,
+           "covars must be 2D [N, 6], got shape ", list(covars.shape))
+    _check(viewmats.dim() == 3 and viewmats.size(1) == 4 and viewmats.size(2) == 4,
+           "viewmats must be 3D [C, 4, 4], got shape ", list(viewmats.shape))
+    _check(Ks.dim() == 3 and Ks.size(1) == 3 and Ks.size(2) == 3,
+           "Ks must be 3D [C, 3, 3], got shape ", list(Ks.shape))
+    N, C = means.size(0), viewmats.size(0)
+    _check(covars.size(0) == N, "covars dim 0 (", covars.size(0), ") doesn't match N=", N)
+    _check(Ks.size(0) == C, "Ks batch dim (", Ks.size(0), ") doesn't match C=", C)
+    return C, N
+
+
+def world_to_image_projection_fwd(means: Tensor, covars: Tensor, viewmats: Tensor, Ks: Tensor,
+                                  dim1: int, dim0: int, eps_blur: float,
+                                  radius_clip: float) -> Tuple[Tensor, Tensor, Tensor]:
+    """WorldToImageProjection.cpp:38-119 -> (means2d [C,N,2], cov2d [C,N,6], radii [C,N,2])."""
+    for t, n in ((means, "means"), (covars, "covars"), (viewmats, "viewmats"), (Ks, "Ks")):
+        _check_input(t, n)
+    C, N = _check_cameras(means, covars, viewmats, Ks)
+    _check(float(radius_clip) > 0.0, "radius_clip must be positive, got ", float(radius_clip))
+    dev, dt = means.device, means.dtype
+    means2d = torch.empty((C, N, 2), dtype=dt, device=dev)
+    cov2d = torch.empty((C, N, 6), dtype=dt, device=dev)
+    radii = torch.zeros((C, N, 2), dtype=torch.int32, device=dev)
+    if C * N == 0:
+        return means2d, cov2d, radii
+    sfx = _suffix(means, "world_to_image_projection_fwd")
+    with torch.cuda.device(dev):
+        _call(f"r2s_world_to_image_projection_fwd_{sfx}", _ptr(means), _ptr(covars),
+              _ptr(viewmats), _ptr(Ks), int(dim1), int(dim0), float(eps_blur),
+              float(radius_clip), _ptr(means2d), _ptr(cov2d), _ptr(radii), C, N, _stream(dev))
+    return means2d, cov2d, radii
+
+
+def world_to_image_projection_bwd(means: Tensor, covars: Tensor, viewmats: Tensor, Ks: Tensor,
+                                  dim1: int, dim0: int, v_means2d: Tensor,
+                                  v_cov2d_3x3: Tensor) -> Tuple[Tensor, Tensor]:
+    """WorldToImageProjection.cpp:127-206 -> (v_means [N,3], v_covars [N,6])."""
+    for t, n in ((means, "means"), (covars, "covars"), (viewmats, "viewmats"), (Ks, "Ks"),
+                 (v_means2d, "v_means2d"), (v_cov2d_3x3, "v_cov2d_3x3")):
+        _check_input(t, n)
+    _check(means.dim() == 2 and means.size(1) == 3, "means must be 2D [N, 3]")
+    _check(covars.dim() == 2 and covars.size(1) == 6, "covars must be 2D [N, 6]")
+    _check(viewmats.dim() == 3 and viewmats.size(1) == 4 and viewmats.size(2) == 4,
+           "viewmats must be 3D [C, 4, 4]")
+    _check(Ks.dim() == 3 and Ks.size(1) == 3 and Ks.size(2) == 3, "Ks must be 3D [C, 3, 3]")
+    _check(v_means2d.dim() == 3 and v_means2d.size(2) == 2, "v_means2d must be 3D [C, N, 2]")
+    _check(v_cov2d_3x3.dim() == 3 and v_cov2d_3x3.size(2) == 6,
+           "v_cov2d_3x3 must be 3D [C, N, 6]")
+    N, C = means.size(0), viewmats.size(0)
+    _check(covars.size(0) == N, "covars dim 0 mismatch")
+    _check(v_means2d.size(0) == C and v_means2d.size(1) == N, "v_means2d shape mismatch")
+    _check(v_cov2d_3x3.size(0) == C and v_cov2d_3x3.size(1) == N, "v_cov2d_3x3 shape mismatch")
+    dev, dt = means.device, means.dtype
+    v_means = torch.empty((N, 3), dtype=dt, device=dev)
+    v_covars = torch.empty((N, 6), dtype=dt, device=dev)
+    if C * N == 0:
+        # The reference returns uninitialised tensors here; zeros are the sum
+        # over an empty camera set.
+        return v_means.zero_(), v_covars.zero_()
+    sfx = _suffix(means, "world_to_image_projection_bwd")
+    with torch.cuda.device(dev):
+        _call(f"r2s_world_to_image_projection_bwd_{sfx}", _ptr(means), _ptr(covars),
+              _ptr(viewmats), _ptr(Ks), int(dim1), int(dim0), _ptr(v_means2d),
+              _ptr(v_cov2d_3x3), _ptr(v_means), _ptr(v_covars), C, N, _stream(dev))
+    return v_means, v_covars
+
+
+def conics_mu_fwd(cov2d_3x3: Tensor, eps: float) -> Tuple[Tensor, Tensor]:
+    """ConicsMu.cpp:35-80 -> (conics [C,N,3], mus [C,N])."""
+    _check_input(cov2d_3x3, "cov2d_3x3")
+    _check(cov2d_3x3.dim() == 3, "cov2d_3x3 must be 3D [C, N, 6], got dim=", cov2d_3x3.dim())
+    _check(cov2d_3x3.size(2) == 6, "cov2d_3x3 last dim must be 6, got ", cov2d_3x3.size(2))
+    C, N = cov2d_3x3.size(0), cov2d_3x3.size(1)
+    dev, dt = cov2d_3x3.device, cov2d_3x3.dtype
+    conics = torch.empty((C, N, 3), dtype=dt, device=dev)
+    mus = torch.empty((C, N), dtype=dt, device=dev)
+    if C * N == 0:
+        return conics, mus
+    sfx = _suffix(cov2d_3x3, "conics_mu_fwd")
+    with torch.cuda.device(dev):
+        _call(f"r2s_conics_mu_fwd_{sfx}", _ptr(cov2d_3x3), float(eps), _ptr(conics), _ptr(mus),
+              C * N, _stream(dev))
+    return conics, mus
+
+
+def conics_mu_bwd(cov2d_3x3: Tensor, eps: float, conics: Tensor, mus: Tensor, v_conics: Tensor,
+                  v_mus: Tensor) -> Tensor:
+    """ConicsMu.cpp:87-159 -> v_cov2d_3x3 [C,N,6]."""
+    for t, n in ((cov2d_3x3, "cov2d_3x3"), (conics, "conics"), (mus, "mus"),
+                 (v_conics, "v_conics"), (v_mus, "v_mus")):
+        _check_input(t, n)
+    _check(cov2d_3x3.dim() == 3, "cov2d_3x3 must be 3D [C, N, 6]")
+    _check(conics.dim() == 3, "conics must be 3D [C, N, 3]")
+    _check(mus.dim() == 2, "mus must be 2D [C, N]")
+    _check(v_conics.dim() == 3, "v_conics must be 3D [C, N, 3]")
+    _check(v_mus.dim() == 2, "v_mus must be 2D [C, N]")
+    C, N = cov2d_3x3.size(0), cov2d_3x3.size(1)
+    _check(cov2d_3x3.size(2) == 6, "cov2d_3x3 last dim must be 6")
+    _check(tuple(conics.shape) == (C, N, 3), "conics shape must be [C, N, 3]")
+    _check(tuple(mus.shape) == (C, N), "mus shape must be [C, N]")
+    _check(tuple(v_conics.shape) == (C, N, 3), "v_conics shape must be [C, N, 3]")
+    _check(tuple(v_mus.shape) == (C, N), "v_mus shape must be [C, N]")
+    out = torch.empty((C, N, 6), dtype=cov2d_3x3.dtype, device=cov2d_3x3.device)
+    if C * N == 0:
+        return out
+    sfx = _suffix(cov2d_3x3, "conics_mu_bwd")
+    with torch.cuda.device(cov2d_3x3.device):
+        _call(f"r2s_conics_mu_bwd_{sfx}", _ptr(cov2d_3x3), float(eps), _ptr(conics), _ptr(mus),
+              _ptr(v_conics), _ptr(v_mus), _ptr(out), C * N, _stream(cov2d_3x3.device))
+    return out
+
+
+def project_gaussians_fwd(means: Tensor, covars: Tensor, opacities: Tensor, viewmats: Tensor,
+                          Ks: Tensor, img_w: int, img_h: int, eps2d: float, radius_clip: float):
+    """Fused world_to_image_projection_fwd + conics_mu_fwd + opacity broadcast
+    (r2splat/ops/direct.py:149-161) -> (means2d, cov2d, radii, conics, mus, opacity[C,N])."""
+    for t, n in ((means, "means"), (covars, "covars"), (opacities, "opacities"),
+                 (viewmats, "viewmats"), (Ks, "Ks")):
+        _check_input(t, n)
+    C, N = _check_cameras(means, covars, viewmats, Ks)
+    _check(opacities.dim() == 1 and opacities.size(0) == N, "opacities must be 1D [N]")
+    _check(float(radius_clip) > 0.0, "radius_clip must be positive, got ", float(radius_clip))
+    dev, dt = means.device, means.dtype
+    means2d = torch.empty((C, N, 2), dtype=dt, device=dev)
+    cov2d = torch.empty((C, N, 6), dtype=dt, device=dev)
+    radii = torch.empty((C, N, 2), dtype=torch.int32, device=dev)
+    conics = torch.empty((C, N, 3), dtype=dt, device=dev)
+    mus = torch.empty((C, N), dtype=dt, device=dev)
+    opac = torch.empty((C, N), dtype=dt, device=dev)
+    if C * N == 0:
+        return means2d, cov2d, radii, conics, mus, opac
+    sfx = _suffix(means, "project_gaussians_fwd")
+    with torch.cuda.device(dev):
+        _call(f"r2s_project_gaussians_fwd_{sfx}", _ptr(means), _ptr(covars), _ptr(opacities),
+              _ptr(viewmats), _ptr(Ks), int(img_w), int(img_h), float(eps2d),
+              float(radius_clip), _ptr(means2d), _ptr(cov2d), _ptr(radii), _ptr(conics),
+              _ptr(mus), _ptr(opac), C, N, _stream(dev))
+    return means2d, cov2d, radii, conics, mus, opac
+
+
+def project_gaussians_bwd(means: Tensor, covars: Tensor, viewmats: Tensor, Ks: Tensor,
+                          img_w: int, img_h: int, eps2d: float, cov2d: Tensor, conics: Tensor,
+                          mus: Tensor, v_means2d: Tensor, v_conics: Tensor,
+                          v_mus: Tensor) -> Tuple[Tensor, Tensor]:
+    """Fused conics_mu_bwd + world_to_image_projection_bwd (explicit.py:299-316)."""
+    for t, n in ((means, "means"), (covars, "covars"), (viewmats, "viewmats"), (Ks, "Ks"),
+                 (cov2d, "cov2d_3x3"), (conics, "conics"), (mus, "mus"),
+                 (v_means2d, "v_means2d"), (v_conics, "v_conics"), (v_mus, "v_mus")):
+        _check_input(t, n)
+    C, N = _check_cameras(means, covars, viewmats, Ks)
+    for t, shape, n in ((cov2d, (C, N, 6), "cov2d_3x3"), (conics, (C, N, 3), "conics"),
+                        (mus, (C, N), "mus"), (v_means2d, (C, N, 2), "v_means2d"),
+                        (v_conics, (C, N, 3), "v_conics"), (v_mus, (C, N), "v_mus")):
+        _check(tuple(t.shape) == shape, f"{n} shape must be {list(shape)}")
+    dev, dt = means.device, means.dtype
+    v_means = torch.empty((N, 3), dtype=dt, device=dev)
+    v_covars = torch.empty((N, 6), dtype=dt, device=dev)
+    if N == 0:
+        return v_means, v_covars
+    sfx = _suffix(means, "project_gaussians_bwd")
+    with torch.cuda.device(dev):
+        _call(f"r2s_project_gaussians_bwd_{sfx}", _ptr(means), _ptr(covars), _ptr(viewmats),
+              _ptr(Ks), int(img_w), int(img_h), float(eps2d), _ptr(cov2d), _ptr(conics),
+              _ptr(mus), _ptr(v_means2d), _ptr(v_conics), _ptr(v_mus), _ptr(v_means),
+              _ptr(v_covars), C, N, _stream(dev))
+    return v_means, v_covars
+
+
+# ---------------------------------------------------------------- binning --
+
+def isect_tiles(means2d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim1: int,
+                n_tiles_dim0: int) -> Tuple[Tensor, Tensor, Tensor]:
+    """IsectTiles.cpp:31-170 -> (tiles_per_gauss [C,N], isect_ids i64, flatten_ids i32)."""
+    _check_input(means2d, "means2d")
+    _check_input(radii, "radii")
+    _check(means2d.dim() == 3, "means2d must be 3D [C, N, 2]")
+    _check(radii.dim() == 2 or (radii.dim() == 3 and radii.size(2) == 2),
+           "radii must be 2D [C, N] or 3D [C, N, 2]")
+    _check(means2d.size(2) == 2, "means2d last dim must be 2")
+    _check(means2d.size(0) == radii.size(0), "C dimension must match")
+    _check(means2d.size(1) == radii.size(1), "N dimension must match")
+    _check(radii.dtype == torch.int32, "radii must be int32")
+    C, N = means2d.size(0), means2d.size(1)
+    dev = means2d.device
+    tw, th, ts = int(n_tiles_dim1), int(n_tiles_dim0), int(tile_size)
+    tiles_per_gauss = torch.empty((C, N), dtype=torch.int32, device=dev)
+    empty_ids = (torch.empty((0,), dtype=torch.int64, device=dev),
+                 torch.empty((0,), dtype=torch.int32, device=dev))
+    if C * N == 0:
+        return (tiles_per_gauss,) + empty_ids
+    lib = _lib()
+    sfx = _suffix(means2d, "isect_tiles")
+    rect = 1 if radii.dim() == 3 else 0
+    with torch.cuda.device(dev):
+        st = _stream(dev)
+        offsets = torch.empty((C * N + 1,), dtype=torch.int64, device=dev)
+        ws = _workspace(lib.r2s_isect_workspace_bytes(C * N, 0, 0), dev)
+        _call(f"r2s_isect_count_2d_{sfx}", _ptr(means2d), _ptr(radii), rect, C, N, ts, tw, th,
+              _ptr(tiles_per_gauss), _ptr(offsets), _ptr(ws), ws.numel(), st)
+        n_isects = int(offsets[-1].item())  # the one host read-back (IsectTiles.cpp:100)
+        if n_isects == 0:
+            return (tiles_per_gauss,) + empty_ids
+        end_bit = _end_bit(C * tw * th)
+        isect_ids = torch.empty((n_isects,), dtype=torch.int64, device=dev)
+        flatten_ids = torch.empty((n_isects,), dtype=torch.int32, device=dev)
+        ws = _workspace(lib.r2s_isect_workspace_bytes(0, n_isects, end_bit), dev)
+        _call(f"r2s_isect_emit_sort_2d_{sfx}", _ptr(means2d), _ptr(radii), rect, C, N, ts, tw,
+              th, _ptr(offsets), n_isects, end_bit, _ptr(isect_ids), _ptr(flatten_ids),
+              _ptr(ws), ws.numel(), st)
+    return tiles_per_gauss, isect_ids, flatten_ids
+
+
+def isect_offset_encode(isect_ids: Tensor, C: int, n_tiles_dim1: int,
+                        n_tiles_dim0: int) -> Tensor:
+    """IsectTiles.cpp:176-215 -> tile_offsets [C, n_tiles_dim0, n_tiles_dim1] int32."""
+    _check_input(isect_ids, "isect_ids")
+    _check(isect_ids.dtype == torch.int64, "isect_ids must be int64")
+    dev = isect_ids.device
+    C, tw, th = int(C), int(n_tiles_dim1), int(n_tiles_dim0)
+    offsets = torch.empty((C, th, tw), dtype=torch.int32, device=dev)
+    if offsets.numel() == 0:
+        return offsets
+    with torch.cuda.device(dev):
+        _call("r2s_isect_offset_encode", _ptr(isect_ids), isect_ids.numel(), C * tw * th,
+              _ptr(offsets), _stream(dev))
+    return offsets
+
+
+def isect_tiles_3d(means3d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim2: int,
+                   n_tiles_dim1: int, n_tiles_dim0: int) -> Tuple[Tensor, Tensor, Tensor]:
+    """IsectTiles3D.cpp:31-162 -> (tiles_per_gauss [N], isect_ids i64, flatten_ids i32)."""
+    _check_input(means3d, "means3d")
+    _check_input(radii, "radii")
+    _check(means3d.dim() == 2, "means3d must be 2D [N, 3]")
+    _check(radii.dim() == 2, "radii must be 2D [N, 3]")
+    _check(means3d.size(1) == 3, "means3d last dim must be 3")
+    _check(radii.size(1) == 3, "radii last dim must be 3")
+    _check(means3d.size(0) == radii.size(0), "N dimension must match")
+    _check(radii.dtype == torch.int32, "radii must be int32")
+    N = means3d.size(0)
+    dev = means3d.device
+    n2, n1, n0, ts = int(n_tiles_dim2), int(n_tiles_dim1), int(n_tiles_dim0), int(tile_size)
+    tiles_per_gauss = torch.empty((N,), dtype=torch.int32, device=dev)
+    empty_ids = (torch.empty((0,), dtype=torch.int64, device=dev),
+                 torch.empty((0,), dtype=torch.int32, device=dev))
+    if N == 0:
+        return (tiles_per_gauss,) + empty_ids
+    lib = _lib()
+    sfx = _suffix(means3d, "isect_tiles_3d")
+    with torch.cuda.device(dev):
+        st = _stream(dev)
+        offsets = torch.empty((N + 1,), dtype=torch.int64, device=dev)
+        ws = _workspace(lib.r2s_isect_workspace_bytes(N, 0, 0), dev)
+        _call(f"r2s_isect_count_3d_{sfx}", _ptr(means3d), _ptr(radii), N, ts, n2, n1, n0,
+              _ptr(tiles_per_gauss), _ptr(offsets), _ptr(ws), ws.numel(), st)
+        n_isects = int(offsets[-1].item())  # IsectTiles3D.cpp:96
+        if n_isects == 0:
+            return (tiles_per_gauss,) + empty_ids
+        end_bit = _end_bit(n2 * n1 * n0)
+        isect_ids = torch.empty((n_isects,), dtype=torch.int64, device=dev)
+        flatten_ids = torch.empty((n_isects,), dtype=torch.int32, device=dev)
+        ws = _workspace(lib.r2s_isect_workspace_bytes(0, n_isects, end_bit), dev)
+        _call(f"r2s_isect_emit_sort_3d_{sfx}", _ptr(means3d), _ptr(radii), N, ts, n2, n1, n0,
+              _ptr(offsets), n_isects, end_bit, _ptr(isect_ids), _ptr(flatten_ids), _ptr(ws),
+              ws.numel(), st)
+    return tiles_per_gauss, isect_ids, flatten_ids
+
+
+def isect_offset_encode_3d(isect_ids: Tensor, n_tiles_dim2: int, n_tiles_dim1: int,
+                           n_tiles_dim0: int) -> Tensor:
+    """IsectTiles3D.cpp:168-204 -> tile_offsets [n0, n1, n2] int32."""
+    _check_input(isect_ids, "isect_ids")
+    _check(isect_ids.dtype == torch.int64, "isect_ids must be int64")
+    dev = isect_ids.device
+    n2, n1, n0 = int(n_tiles_dim2), int(n_tiles_dim1), int(n_tiles_dim0)
+    offsets = torch.empty((n0, n1, n2), dtype=torch.int32, device=dev)
+    if offsets.numel() == 0:
+        return offsets
+    with torch.cuda.device(dev):
+        _call("r2s_isect_offset_encode", _ptr(isect_ids), isect_ids.numel(), n0 * n1 * n2,
+              _ptr(offsets), _stream(dev))
+    return offsets
+
+
+# -------------------------------------------------------------- rasterizer --
+
+def _check_raster(means2d, conics, opacities, mus, tile_offsets, flatten_ids):
+    _check(means2d.dim() == 3, "means2d must be 3D [C, N, 2]")
+    _check(conics.dim() == 3, "conics must be 3D [C, N, 3]")
+    _check(opacities.dim() == 2, "opacities must be 2D [C, N]")
+    _check(mus.dim() == 2, "mus must be 2D [C, N]")
+    _check(tile_offsets.dim() == 3, "tile_offsets must be 3D [C, n_tiles_dim0, n_tiles_dim1]")
+    _check(flatten_ids.dim() == 1, "flatten_ids must be 1D [n_isects]")
+    _check(means2d.size(2) == 2, "means2d last dim must be 2")
+    _check(conics.size(2) == 3, "conics last dim must be 3")
+    C, N = means2d.size(0), means2d.size(1)
+    _check(conics.size(0) == C and conics.size(1) == N, "conics shape must match means2d [C, N, 3]")
+    _check(opacities.size(0) == C and opacities.size(1) == N, "opacities shape must match [C, N]")
+    _check(mus.size(0) == C and mus.size(1) == N, "mus shape must match [C, N]")
+    _check(tile_offsets.size(0) == C, "tile_offsets C dimension must match")
+    _check(tile_offsets.dtype == torch.int32 and flatten_ids.dtype == torch.int32,
+           "tile_offsets and flatten_ids must be int32")
+    for t in (conics, opacities, mus):
+        _check(t.dtype == means2d.dtype, "means2d, conics, opacities and mus must share a dtype")
+    return C, N
+
+
+def rasterize_to_pixels_fwd(means2d: Tensor, conics: Tensor, opacities: Tensor, mus: Tensor,
+                            tile_offsets: Tensor, flatten_ids: Tensor, dim1: int, dim0: int,
+                            tile_size: int) -> Tensor:
+    """RasterizeToPixels.cpp:25-114 -> image [C, dim0, dim1]."""
+    for t, n in ((means2d, "means2d"), (conics, "conics"), (opacities, "opacities"),
+                 (mus, "mus"), (tile_offsets, "tile_offsets"), (flatten_ids, "flatten_ids")):
+        _check_input(t, n)
+    C, N = _check_raster(means2d, conics, opacities, mus, tile_offsets, flatten_ids)
+    W, H, ts = int(dim1), int(dim0), int(tile_size)
+    th, tw = tile_offsets.size(1), tile_offsets.size(2)
+    dev = means2d.device
+    out = torch.empty((C, H, W), dtype=means2d.dtype, device=dev)
+    n_isects = flatten_ids.numel()
+    if C == 0 or N == 0 or n_isects == 0:
+        return out.zero_()
+    sfx = _suffix(means2d, "rasterize_to_pixels_fwd")
+    with torch.cuda.device(dev):
+        _call(f"r2s_rasterize_fwd_{sfx}", _ptr(means2d), _ptr(conics), _ptr(opacities),
+              _ptr(mus), _ptr(tile_offsets), _ptr(flatten_ids), n_isects, C, N, W, H, ts, tw, th,
+              _ptr(out), None, 0, _stream(dev))
+    return out
+
+
+def _raster_bwd(means2d, conics, opacities, mus, tile_offsets, isect_ids, flatten_ids,
+                v_render, dim1, dim0, tile_size, absgrad, op):
+    C, N = _check_raster(means2d, conics, opacities, mus, tile_offsets, flatten_ids)
+    _check(v_render.dim() == 3, "v_render_output must be 3D [C, dim0, dim1]")
+    W, H, ts = int(dim1), int(dim0), int(tile_size)
+    _check(v_render.size(0) == C and v_render.size(1) == H and v_render.size(2) == W,
+           "v_render_output shape must be [C, dim0, dim1]")
+    th, tw = tile_offsets.size(1), tile_offsets.size(2)
+    v_means2d = torch.zeros_like(means2d)
+    v_abs = torch.zeros_like(means2d) if absgrad else None
+    v_conics = torch.zeros_like(conics)
+    v_opac = torch.zeros_like(opacities)
+    v_mus = torch.zeros_like(mus)
+    n_isects = flatten_ids.numel()
+    if C == 0 or N == 0 or n_isects == 0:
+        return v_abs, v_means2d, v_conics, v_opac, v_mus
+    sfx = _suffix(means2d, op)
+    dev = means2d.device
+    with torch.cuda.device(dev):
+        _call(f"r2s_rasterize_bwd_{sfx}", _ptr(means2d), _ptr(conics), _ptr(opacities),
+              _ptr(mus), _ptr(tile_offsets), _ptr(isect_ids), _ptr(flatten_ids), n_isects,
+              _ptr(v_render), C, N, W, H, ts, tw, th, _ptr(v_abs), _ptr(v_means2d),
+              _ptr(v_conics), _ptr(v_opac), _ptr(v_mus), _stream(dev))
+    return v_abs, v_means2d, v_conics, v_opac, v_mus
+
+
+def rasterize_to_pixels_bwd(means2d: Tensor, conics: Tensor, opacities: Tensor, mus: Tensor,
+                            tile_offsets: Tensor, flatten_ids: Tensor, v_render_output: Tensor,
+                            dim1: int, dim0: int, tile_size: int, absgrad: bool):
+    """RasterizeToPixels.cpp:122-222 (pixel mode) ->
+    (v_means2d_abs or None, v_means2d, v_conics, v_opacities, v_mus)."""
+    for t, n in ((means2d, "means2d"), (conics, "conics"), (opacities, "opacities"),
+                 (mus, "mus"), (tile_offsets, "tile_offsets"), (flatten_ids, "flatten_ids"),
+                 (v_render_output, "v_render_output")):
+        _check_input(t, n)
+    return _raster_bwd(means2d, conics, opacities, mus, tile_offsets, None, flatten_ids,
+                       v_render_output, dim1, dim0, tile_size, bool(absgrad),
+                       "rasterize_to_pixels_bwd")
+
+
+def rasterize_to_pixels_bwd_per_gaussian(means2d: Tensor, conics: Tensor, opacities: Tensor,
+                                         mus: Tensor, tile_offsets: Tensor, isect_ids: Tensor,
+                                         flatten_ids: Tensor, v_render_output: Tensor, dim1: int,
+                                         dim0: int, tile_size: int, absgrad: bool):
+    """RasterizeToPixels.cpp:226-317 (primitive mode, the default)."""
+    for t, n in ((means2d, "means2d"), (conics, "conics"), (opacities, "opacities"),
+                 (mus, "mus"), (tile_offsets, "tile_offsets"), (isect_ids, "isect_ids"),
+                 (flatten_ids, "flatten_ids"), (v_render_output, "v_render_output")):
+        _check_input(t, n)
+    _check(isect_ids.dim() == 1, "isect_ids must be 1D [n_isects]")
+    _check(isect_ids.dtype == torch.int64, "isect_ids must be int64")
+    _check(isect_ids.size(0) == flatten_ids.size(0),
+           "isect_ids and flatten_ids must have the same length")
+    return _raster_bwd(means2d, conics, opacities, mus, tile_offsets, isect_ids, flatten_ids,
+                       v_render_output, dim1, dim0, tile_size, bool(absgrad),
+                       "rasterize_to_pixels_bwd_per_gaussian")
+
+
+# ------------------------------------------------------------ voxelization --
+
+def world_to_volume_mapping_fwd(means: Tensor, covars: Tensor, max_scales: Tensor,
+                                ranges: Tensor, centers: Tensor, dim2: int, dim1: int,
+                                dim0: int, eps3d: float,
+                                radius_clip: float) -> Tuple[Tensor, Tensor, Tensor]:
+    """WorldToVolumeMapping.cpp:37-112 -> (means3d [N,3], conics [N,6], radii [N,3])."""
+    for t, n in ((means, "means"), (covars, "covars"), (max_scales, "max_scales"),
+                 (ranges, "ranges"), (centers, "centers")):
+        _check_input(t, n)
+    _check(means.dim() == 2 and means.size(1) == 3,
+           "means must be 2D [N, 3], got shape ", list(means.shape))
+    _check(covars.dim() == 2 and covars.size(1) == 6,
+           "covars must be 2D [N, 6], got shape ", list(covars.shape))
+    _check(max_scales.dim() == 1, "max_scales must be 1D [N], got dim ", max_scales.dim())
+    _check(ranges.dim() == 1 and ranges.size(0) == 3,
+           "ranges must be 1D [3], got shape ", list(ranges.shape))
+    _check(centers.dim() == 1 and centers.size(0) == 3,
+           "centers must be 1D [3], got shape ", list(centers.shape))
+    N = means.size(0)
+    _check(covars.size(0) == N, "covars batch dim (", covars.size(0), ") doesn't match N=", N)
+    _check(max_scales.size(0) == N, "max_scales batch dim (", max_scales.size(0),
+           ") doesn't match N=", N)
+    dev, dt = means.device, means.dtype
+    means3d = torch.empty((N, 3), dtype=dt, device=dev)
+    conics = torch.empty((N, 6), dtype=dt, device=dev)
+    radii = torch.empty((N, 3), dtype=torch.int32, device=dev)
+    if N == 0:
+        return means3d, conics, radii
+    _check(covars.dtype == dt and ranges.dtype == dt and centers.dtype == dt,
+           "means, covars, ranges and centers must share a dtype")
+    sfx = _suffix(means, "world_to_volume_mapping_fwd")
+    with torch.cuda.device(dev):
+        _call(f"r2s_world_to_volume_mapping_fwd_{sfx}", _ptr(means), _ptr(covars),
+              _ptr(ranges), _ptr(centers), int(dim2), int(dim1), int(dim0),
+              float(eps3d), float(radius_clip), _ptr(means3d), _ptr(conics), _ptr(radii), N,
+              _stream(dev))
+    return means3d, conics, radii
+
+
+def world_to_volume_mapping_bwd(means: Tensor, covars: Tensor, ranges: Tensor, centers: Tensor,
+                                dim2: int, dim1: int, dim0: int, eps3d: float,
+                                v_means3d_v: Tensor, v_conics: Tensor) -> Tuple[Tensor, Tensor]:
+    """WorldToVolumeMapping.cpp:119-192 -> (v_means [N,3], v_covars [N,6])."""
+    for t, n in ((means, "means"), (covars, "covars"), (ranges, "ranges"), (centers, "centers"),
+                 (v_means3d_v, "v_means3d_v"), (v_conics, "v_conics")):
+        _check_input(t, n)
+    _check(means.dim() == 2 and means.size(1) == 3, "means must be 2D [N, 3]")
+    _check(covars.dim() == 2 and covars.size(1) == 6, "covars must be 2D [N, 6]")
+    _check(ranges.dim() == 1 and ranges.size(0) == 3, "ranges must be 1D [3]")
+    _check(centers.dim() == 1 and centers.size(0) == 3, "centers must be 1D [3]")
+    _check(v_means3d_v.dim() == 2 and v_means3d_v.size(1) == 3, "v_means3d_v must be 2D [N, 3]")
+    _check(v_conics.dim() == 2 and v_conics.size(1) == 6, "v_conics must be 2D [N, 6]")
+    N = means.size(0)
+    _check(covars.size(0) == N, "covars shape mismatch")
+    _check(v_means3d_v.size(0) == N, "v_means3d_v shape mismatch")
+    _check(v_conics.size(0) == N, "v_conics shape mismatch")
+    dev, dt = means.device, means.dtype
+    v_means = torch.empty((N, 3), dtype=dt, device=dev)
+    v_covars = torch.empty((N, 6), dtype=dt, device=dev)
+    if N == 0:
+        return v_means, v_covars
+    _check(all(t.dtype == dt for t in (covars, ranges, centers, v_means3d_v, v_conics)),
+           "world_to_volume_mapping_bwd inputs must share a dtype")
+    sfx = _suffix(means, "world_to_volume_mapping_bwd")
+    with torch.cuda.device(dev):
+        _call(f"r2s_world_to_volume_mapping_bwd_{sfx}", _ptr(means), _ptr(covars),
+              _ptr(ranges), _ptr(centers), int(dim2), int(dim1), int(dim0),
+              float(eps3d), _ptr(v_means3d_v), _ptr(v_conics), _ptr(v_means), _ptr(v_covars), N,
+              _stream(dev))
+    return v_means, v_covars
+
+
+def _check_voxel(means3d, conics, opacities, tile_offsets, flatten_ids):
+    _check(means3d.dim() == 2, "means3d must be 2D [N, 3]")
+    _check(conics.dim() == 2, "conics must be 2D [N, 6]")
+    _check(opacities.dim() == 1, "opacities must be 1D [N]")
+    _check(tile_offsets.dim() == 3,
+           "tile_offsets must be 3D [n_tiles_dim0, n_tiles_dim1, n_tiles_dim2]")
+    _check(flatten_ids.dim() == 1, "flatten_ids must be 1D [n_isects]")
+    _check(means3d.size(1) == 3, "means3d last dim must be 3")
+    _check(conics.size(1) == 6, "conics last dim must be 6")
+    N = means3d.size(0)
+    _check(conics.size(0) == N, "conics first dim must match N")
+    _check(opacities.size(0) == N, "opacities first dim must match N")
+    _check(tile_offsets.dtype == torch.int32 and flatten_ids.dtype == torch.int32,
+           "tile_offsets and flatten_ids must be int32")
+    for t in (conics, opacities):
+        _check(t.dtype == means3d.dtype, "means3d, conics and opacities must share a dtype")
+    return N
+
+
+def voxelize_to_voxels_fwd(means3d: Tensor, conics: Tensor, opacities: Tensor,
+                           tile_offsets: Tensor, flatten_ids: Tensor, dim2: int, dim1: int,
+                           dim0: int, tile_size: int) -> Tensor:
+    """VoxelizeToVoxels.cpp:31-108 -> volume [dim0, dim1, dim2]."""
+    for t, n in ((means3d, "means3d"), (conics, "conics"), (opacities, "opacities"),
+                 (tile_offsets, "tile_offsets"), (flatten_ids, "flatten_ids")):
+        _check_input(t, n)
+    N = _check_voxel(means3d, conics, opacities, tile_offsets, flatten_ids)
+    d2, d1, d0, ts = int(dim2), int(dim1), int(dim0), int(tile_size)
+    n0, n1, n2 = tile_offsets.size(0), tile_offsets.size(1), tile_offsets.size(2)
+    dev = means3d.device
+    n_isects = flatten_ids.numel()
+    if N == 0 or n_isects == 0:
+        return torch.zeros((d0, d1, d2), dtype=means3d.dtype, device=dev)
+    out = torch.empty((d0, d1, d2), dtype=means3d.dtype, device=dev)
+    sfx = _suffix(means3d, "voxelize_to_voxels_fwd")
+    with torch.cuda.device(dev):
+        _call(f"r2s_voxelize_fwd_{sfx}", _ptr(means3d), _ptr(conics), _ptr(opacities),
+              _ptr(tile_offsets), _ptr(flatten_ids), n_isects, N, d2, d1, d0, ts, n2, n1, n0,
+              _ptr(out), _stream(dev))
+    return out
+
+
+def _voxel_bwd(means3d, conics, opacities, tile_offsets, isect_ids, flatten_ids, v_render,
+               dim2, dim1, dim0, tile_size, op):
+    N = _check_voxel(means3d, conics, opacities, tile_offsets, flatten_ids)
+    _check(v_render.dim() == 3, "v_render_output must be 3D [dim0, dim1, dim2]")
+    d2, d1, d0, ts = int(dim2), int(dim1), int(dim0), int(tile_size)
+    n0, n1, n2 = tile_offsets.size(0), tile_offsets.size(1), tile_offsets.size(2)
+    v_means3d = torch.zeros_like(means3d)
+    v_conics = torch.zeros_like(conics)
+    v_opac = torch.zeros_like(opacities)
+    n_isects = flatten_ids.numel()
+    if N == 0 or n_isects == 0:
+        return v_means3d, v_conics, v_opac
+    _check(tuple(v_render.shape) == (d0, d1, d2), "v_render_output shape must be [dim0, dim1, dim2]")
+    sfx = _suffix(means3d, op)
+    dev = means3d.device
+    with torch.cuda.device(dev):
+        _call(f"r2s_voxelize_bwd_{sfx}", _ptr(means3d), _ptr(conics), _ptr(opacities),
+              _ptr(tile_offsets), _ptr(isect_ids), _ptr(flatten_ids), n_isects, _ptr(v_render),
+              N, d2, d1, d0, ts, n2, n1, n0, _ptr(v_means3d), _ptr(v_conics), _ptr(v_opac),
+              _stream(dev))
+    return v_means3d, v_conics, v_opac
+
+
+def voxelize_to_voxels_bwd(means3d: Tensor, conics: Tensor, opacities: Tensor,
+                           tile_offsets: Tensor, flatten_ids: Tensor, v_render_output: Tensor,
+                           dim2: int, dim1: int, dim0: int, tile_size: int):
+    """VoxelizeToVoxels.cpp:115-192 (pixel mode) -> (v_means3d, v_conics, v_opacities)."""
+    for t, n in ((means3d, "means3d"), (conics, "conics"), (opacities, "opacities"),
+                 (tile_offsets, "tile_offsets"), (flatten_ids, "flatten_ids"),
+                 (v_render_output, "v_render_output")):
+        _check_input(t, n)
+    return _voxel_bwd(means3d, conics, opacities, tile_offsets, None, flatten_ids,
+                      v_render_output, dim2, dim1, dim0, tile_size, "voxelize_to_voxels_bwd")
+
+
+def voxelize_to_voxels_bwd_per_gaussian(means3d: Tensor, conics: Tensor, opacities: Tensor,
+                                        tile_offsets: Tensor, isect_ids: Tensor,
+                                        flatten_ids: Tensor, v_render_output: Tensor, dim2: int,
+                                        dim1: int, dim0: int, tile_size: int):
+    """VoxelizeToVoxels.cpp:195-278 (primitive mode, the default)."""
+    for t, n in ((means3d, "means3d"), (conics, "conics"), (opacities, "opacities"),
+                 (tile_offsets, "tile_offsets"), (isect_ids, "isect_ids"),
+                 (flatten_ids, "flatten_ids"), (v_render_output, "v_render_output")):
+        _check_input(t, n)
+    _check(isect_ids.dim() == 1, "isect_ids must be 1D")
+    _check(isect_ids.dtype == torch.int64, "isect_ids must be int64")
+    _check(isect_ids.size(0) == flatten_ids.size(0),
+           "isect_ids and flatten_ids must have the same length")
+    return _voxel_bwd(means3d, conics, opacities, tile_offsets, isect_ids, flatten_ids,
+                      v_render_output, dim2, dim1, dim0, tile_size,
+                      "voxelize_to_voxels_bwd_per_gaussian")
+
+
+# -------------------------------------------------------------- compaction --
+
+def mask_split(mask: Tensor) -> Tuple[Tensor, int]:
+    """(indices, n_true): ascending indices of true entries, then of false entries.
+
+    ``indices[:n_true]`` equals ``torch.where(mask)[0]`` and
+    ``indices[n_true:]`` equals ``torch.where(~mask)[0]``
+    (src/strategies/binary_tree.py:68,101-102,158).
+    """
+    _check(isinstance(mask, torch.Tensor) and mask.is_cuda, "mask must be a CUDA tensor")
+    m = mask.reshape(-1)
+    if m.dtype != torch.bool and m.dtype != torch.uint8:
+        m = m != 0
+    m = m.contiguous().view(torch.uint8)
+    n = m.numel()
+    dev = m.device
+    out = torch.empty((n,), dtype=torch.int64, device=dev)
+    count = torch.empty((1,), dtype=torch.int64, device=dev)
+    lib = _lib()
+    with torch.cuda.device(dev):
+        ws = _workspace(lib.r2s_mask_workspace_bytes(n), dev)
+        _call("r2s_mask_split", _ptr(m) if n else None, n, _ptr(out) if n else None,
+              _ptr(count), _ptr(ws), ws.numel(), _stream(dev))
+        n_true = int(count.item())
+    return out, n_true

@@ -1,0 +1,404 @@
+/*
+ * r2splat_hip.h -- C ABI of the MI355X (gfx950) Gaussian backend.
+ *
+ * Every entry point takes device pointers that the caller owns, plain sizes
+ * and scalars, and a hipStream_t passed as `void*`.  Work is enqueued on that
+ * stream; nothing here allocates or frees device memory: scratch space is a
+ * caller-provided workspace whose size is returned by the *_workspace_bytes
+ * queries.  Every function returns R2S_OK (0) on success, otherwise a status
+ * code; r2s_last_error() then holds a message for the calling thread.
+ *
+ * Layouts follow the reference operators (row-major, contiguous):
+ *   covariances are packed upper-triangular (00, 01, 02, 11, 12, 22);
+ *   quaternions are (w, x, y, z); images are [C, H, W]; volumes are
+ *   [dim0, dim1, dim2] with x <-> dim2 fastest.
+ *
+ * The comment above each declaration names the reference interface it
+ * replaces (paths relative to the BT-3DGS source tree).
+ */
+#ifndef R2SPLAT_HIP_H
+#define R2SPLAT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *r2s_stream_t; /* hipStream_t */
+
+#define R2S_OK 0
+#define R2S_EINVAL 1001    /* invalid argument (shape, size, pointer)      */
+#define R2S_ERANGE 1002    /* size exceeds the int32 index limits          */
+#define R2S_EHIP 1003      /* HIP runtime / launch error                    */
+#define R2S_EWORKSPACE 1004 /* workspace smaller than the queried size      */
+
+/* Message describing the last failure on the calling thread ("" if none). */
+const char *r2s_last_error(void);
+/* ABI revision of this header; bumped whenever a signature changes. */
+int r2s_abi_version(void);
+
+/* ---------------------------------------------------------------------- */
+/* Parameter transform                                                    */
+/* ---------------------------------------------------------------------- */
+
+/* r2splat/cuda/csrc/ParameterTransform.cpp:34-84 parameter_transform_fwd_tensor:
+ * quats [n,4], raw_scales [n,3] -> covars [n,6], max_scales [n]. */
+int r2s_parameter_transform_fwd_f32(const float *quats, const float *raw_scales,
+                                    double scale_min, double scale_max,
+                                    float *covars, float *max_scales,
+                                    int64_t n, r2s_stream_t stream);
+int r2s_parameter_transform_fwd_f64(const double *quats, const double *raw_scales,
+                                    double scale_min, double scale_max,
+                                    double *covars, double *max_scales,
+                                    int64_t n, r2s_stream_t stream);
+
+/* ParameterTransform.cpp:90-144 parameter_transform_bwd_tensor:
+ * v_covars [n,6] -> v_quats [n,4], v_raw_scales [n,3]. */
+int r2s_parameter_transform_bwd_f32(const float *quats, const float *raw_scales,
+                                    double scale_min, double scale_max,
+                                    const float *v_covars, float *v_quats,
+                                    float *v_raw_scales, int64_t n,
+                                    r2s_stream_t stream);
+int r2s_parameter_transform_bwd_f64(const double *quats, const double *raw_scales,
+                                    double scale_min, double scale_max,
+                                    const double *v_covars, double *v_quats,
+                                    double *v_raw_scales, int64_t n,
+                                    r2s_stream_t stream);
+
+/* r2splat/ops/direct.py:72-96 _prepare_forward_parameters, fused:
+ * parameter_transform_fwd plus softplus(raw_opacities) -> opacities [n]. */
+int r2s_prepare_gaussians_f32(const float *quats, const float *raw_scales,
+                              const float *raw_opacities, double scale_min,
+                              double scale_max, float *covars, float *max_scales,
+                              float *opacities, int64_t n, r2s_stream_t stream);
+int r2s_prepare_gaussians_f64(const double *quats, const double *raw_scales,
+                              const double *raw_opacities, double scale_min,
+                              double scale_max, double *covars, double *max_scales,
+                              double *opacities, int64_t n, r2s_stream_t stream);
+
+/* r2splat/ops/explicit.py:379 v_raw_opacities = v_opacity * sigmoid(raw),
+ * with v_opacity = sum over cameras of v_opac_cn [C,n] plus optional
+ * v_opac_3d [n] (explicit.py:319,370).  Either input may be NULL. */
+int r2s_opacity_bwd_f32(const float *raw_opacities, const float *v_opac_cn,
+                        const float *v_opac_3d, float *v_raw_opacities,
+                        int64_t C, int64_t n, r2s_stream_t stream);
+int r2s_opacity_bwd_f64(const double *raw_opacities, const double *v_opac_cn,
+                        const double *v_opac_3d, double *v_raw_opacities,
+                        int64_t C, int64_t n, r2s_stream_t stream);
+
+/* ---------------------------------------------------------------------- */
+/* Cone-beam projection                                                   */
+/* ---------------------------------------------------------------------- */
+
+/* r2splat/cuda/csrc/WorldToImageProjection.cpp:38-119
+ * world_to_image_projection_fwd_tensor: means [N,3], covars [N,6],
+ * viewmats [C,4,4], Ks [C,3,3] -> means2d [C,N,2], cov2d [C,N,6],
+ * radii [C,N,2] (int32).  `eps2d` and `radius_clip` are single precision in
+ * the reference signature and are rounded to float before use. */
+int r2s_world_to_image_projection_fwd_f32(
+    const float *means, const float *covars, const float *viewmats,
+    const float *Ks, uint32_t width, uint32_t height, float eps2d,
+    float radius_clip, float *means2d, float *cov2d, int32_t *radii,
+    int64_t C, int64_t N, r2s_stream_t stream);
+int r2s_world_to_image_projection_fwd_f64(
+    const double *means, const double *covars, const double *viewmats,
+    const double *Ks, uint32_t width, uint32_t height, float eps2d,
+    float radius_clip, double *means2d, double *cov2d, int32_t *radii,
+    int64_t C, int64_t N, r2s_stream_t stream);
+
+/* WorldToImageProjection.cpp:127-206 world_to_image_projection_bwd_tensor:
+ * v_means2d [C,N,2], v_cov2d [C,N,6] -> v_means [N,3], v_covars [N,6]
+ * (summed over cameras; fully written, no zero-init needed). */
+int r2s_world_to_image_projection_bwd_f32(
+    const float *means, const float *covars, const float *viewmats,
+    const float *Ks, uint32_t width, uint32_t height, const float *v_means2d,
+    const float *v_cov2d, float *v_means, float *v_covars, int64_t C,
+    int64_t N, r2s_stream_t stream);
+int r2s_world_to_image_projection_bwd_f64(
+    const double *means, const double *covars, const double *viewmats,
+    const double *Ks, uint32_t width, uint32_t height, const double *v_means2d,
+    const double *v_cov2d, double *v_means, double *v_covars, int64_t C,
+    int64_t N, r2s_stream_t stream);
+
+/* r2splat/cuda/csrc/ConicsMu.cpp:35-80 conics_mu_fwd_tensor:
+ * cov2d [total,6] -> conics [total,3], mus [total]. */
+int r2s_conics_mu_fwd_f32(const float *cov2d, double eps, float *conics,
+                          float *mus, int64_t total, r2s_stream_t stream);
+int r2s_conics_mu_fwd_f64(const double *cov2d, double eps, double *conics,
+                          double *mus, int64_t total, r2s_stream_t stream);
+
+/* ConicsMu.cpp:87-159 conics_mu_bwd_tensor -> v_cov2d [total,6]. */
+int r2s_conics_mu_bwd_f32(const float *cov2d, double eps, const float *conics,
+                          const float *mus, const float *v_conics,
+                          const float *v_mus, float *v_cov2d, int64_t total,
+                          r2s_stream_t stream);
+int r2s_conics_mu_bwd_f64(const double *cov2d, double eps, const double *conics,
+                          const double *mus, const double *v_conics,
+                          const double *v_mus, double *v_cov2d, int64_t total,
+                          r2s_stream_t stream);
+
+/* r2splat/ops/direct.py:149-161, fused: world_to_image_projection_fwd,
+ * conics_mu_fwd and the opacity broadcast to [C,N], one pass.  As in the
+ * reference, the radii use eps2d rounded to float and conics/mu use eps2d. */
+int r2s_project_gaussians_fwd_f32(
+    const float *means, const float *covars, const float *opacities,
+    const float *viewmats, const float *Ks, uint32_t width, uint32_t height,
+    double eps2d, float radius_clip, float *means2d, float *cov2d,
+    int32_t *radii, float *conics, float *mus, float *opacity_cn, int64_t C,
+    int64_t N, r2s_stream_t stream);
+int r2s_project_gaussians_fwd_f64(
+    const double *means, const double *covars, const double *opacities,
+    const double *viewmats, const double *Ks, uint32_t width, uint32_t height,
+    double eps2d, float radius_clip, double *means2d, double *cov2d,
+    int32_t *radii, double *conics, double *mus, double *opacity_cn,
+    int64_t C, int64_t N, r2s_stream_t stream);
+
+/* r2splat/ops/explicit.py:299-316, fused: conics_mu_bwd followed by
+ * world_to_image_projection_bwd (v_cov2d never touches HBM). */
+int r2s_project_gaussians_bwd_f32(
+    const float *means, const float *covars, const float *viewmats,
+    const float *Ks, uint32_t width, uint32_t height, double eps2d,
+    const float *cov2d, const float *conics, const float *mus,
+    const float *v_means2d, const float *v_conics, const float *v_mus,
+    float *v_means, float *v_covars, int64_t C, int64_t N,
+    r2s_stream_t stream);
+int r2s_project_gaussians_bwd_f64(
+    const double *means, const double *covars, const double *viewmats,
+    const double *Ks, uint32_t width, uint32_t height, double eps2d,
+    const double *cov2d, const double *conics, const double *mus,
+    const double *v_means2d, const double *v_conics, const double *v_mus,
+    double *v_means, double *v_covars, int64_t C, int64_t N,
+    r2s_stream_t stream);
+
+/* ---------------------------------------------------------------------- */
+/* Tile binning                                                           */
+/* ---------------------------------------------------------------------- */
+
+/* Workspace for r2s_isect_count_* (n_items Gaussians) and
+ * r2s_isect_emit_sort_* (n_isects records, keys on bits [0,end_bit)). */
+int64_t r2s_isect_workspace_bytes(int64_t n_items, int64_t n_isects,
+                                  uint32_t end_bit);
+
+/* r2splat/cuda/csrc/IsectTiles.cpp:76-100 (count pass + int64 cumsum):
+ * means2d [C,N,2], radii [C,N] or [C,N,2] -> tiles_per_gauss [C*N] (int32),
+ * offsets [C*N+1] (int64, exclusive; offsets[C*N] = number of records). */
+int r2s_isect_count_2d_f32(const float *means2d, const int32_t *radii,
+                           int radii_is_rect, int64_t C, int64_t N,
+                           uint32_t tile_size, uint32_t n_tiles_w,
+                           uint32_t n_tiles_h, int32_t *tiles_per_gauss,
+                           int64_t *offsets, void *workspace,
+                           size_t workspace_bytes, r2s_stream_t stream);
+int r2s_isect_count_2d_f64(const double *means2d, const int32_t *radii,
+                           int radii_is_rect, int64_t C, int64_t N,
+                           uint32_t tile_size, uint32_t n_tiles_w,
+                           uint32_t n_tiles_h, int32_t *tiles_per_gauss,
+                           int64_t *offsets, void *workspace,
+                           size_t workspace_bytes, r2s_stream_t stream);
+
+/* IsectTiles.cpp:113-169 (emit + stable radix sort on bits [0,end_bit)):
+ * writes isect_ids [n_isects] (int64 key cid*T + ty*tw + tx) and
+ * flatten_ids [n_isects] (int32 cid*N + g), ordered by (key, id). */
+int r2s_isect_emit_sort_2d_f32(const float *means2d, const int32_t *radii,
+                               int radii_is_rect, int64_t C, int64_t N,
+                               uint32_t tile_size, uint32_t n_tiles_w,
+                               uint32_t n_tiles_h, const int64_t *offsets,
+                               int64_t n_isects, uint32_t end_bit,
+                               int64_t *isect_ids, int32_t *flatten_ids,
+                               void *workspace, size_t workspace_bytes,
+                               r2s_stream_t stream);
+int r2s_isect_emit_sort_2d_f64(const double *means2d, const int32_t *radii,
+                               int radii_is_rect, int64_t C, int64_t N,
+                               uint32_t tile_size, uint32_t n_tiles_w,
+                               uint32_t n_tiles_h, const int64_t *offsets,
+                               int64_t n_isects, uint32_t end_bit,
+                               int64_t *isect_ids, int32_t *flatten_ids,
+                               void *workspace, size_t workspace_bytes,
+                               r2s_stream_t stream);
+
+/* r2splat/cuda/csrc/IsectTiles3D.cpp:72-96 (3D count + cumsum):
+ * means3d [N,3], radii [N,3] -> tiles_per_gauss [N], offsets [N+1]. */
+int r2s_isect_count_3d_f32(const float *means3d, const int32_t *radii,
+                           int64_t N, uint32_t tile_size, uint32_t n_tiles_d2,
+                           uint32_t n_tiles_d1, uint32_t n_tiles_d0,
+                           int32_t *tiles_per_gauss, int64_t *offsets,
+                           void *workspace, size_t workspace_bytes,
+                           r2s_stream_t stream);
+int r2s_isect_count_3d_f64(const double *means3d, const int32_t *radii,
+                           int64_t N, uint32_t tile_size, uint32_t n_tiles_d2,
+                           uint32_t n_tiles_d1, uint32_t n_tiles_d0,
+                           int32_t *tiles_per_gauss, int64_t *offsets,
+                           void *workspace, size_t workspace_bytes,
+                           r2s_stream_t stream);
+
+/* IsectTiles3D.cpp:109-161 (3D emit z->y->x + stable sort). */
+int r2s_isect_emit_sort_3d_f32(const float *means3d, const int32_t *radii,
+                               int64_t N, uint32_t tile_size,
+                               uint32_t n_tiles_d2, uint32_t n_tiles_d1,
+                               uint32_t n_tiles_d0, const int64_t *offsets,
+                               int64_t n_isects, uint32_t end_bit,
+                               int64_t *isect_ids, int32_t *flatten_ids,
+                               void *workspace, size_t workspace_bytes,
+                               r2s_stream_t stream);
+int r2s_isect_emit_sort_3d_f64(const double *means3d, const int32_t *radii,
+                               int64_t N, uint32_t tile_size,
+                               uint32_t n_tiles_d2, uint32_t n_tiles_d1,
+                               uint32_t n_tiles_d0, const int64_t *offsets,
+                               int64_t n_isects, uint32_t end_bit,
+                               int64_t *isect_ids, int32_t *flatten_ids,
+                               void *workspace, size_t workspace_bytes,
+                               r2s_stream_t stream);
+
+/* IsectTiles.cpp:176-215 isect_offset_encode_tensor and
+ * IsectTiles3D.cpp:168-204 isect_offset_encode_3d_tensor:
+ * tile_offsets[k] = lower_bound(isect_ids, k) for k in [0, n_keys). */
+int r2s_isect_offset_encode(const int64_t *isect_ids, int64_t n_isects,
+                            int64_t n_keys, int32_t *tile_offsets,
+                            r2s_stream_t stream);
+
+/* ---------------------------------------------------------------------- */
+/* Line-integral rasterizer                                               */
+/* ---------------------------------------------------------------------- */
+
+/* Workspace for r2s_rasterize_fwd_* / r2s_rasterize_bwd_*. */
+int64_t r2s_rasterize_workspace_bytes(int64_t n_keys, int64_t n_isects,
+                                      uint32_t tile_size, int dtype_bytes);
+
+/* r2splat/cuda/csrc/RasterizeToPixels.cpp:25-114 rasterize_to_pixels_fwd_tensor:
+ * image [C,H,W] = per pixel sum over the tile list of
+ * opacity*mu*exp(-sigma), skipping sigma < 0 and |alpha| < 1e-5. */
+int r2s_rasterize_fwd_f32(const float *means2d, const float *conics,
+                          const float *opacities, const float *mus,
+                          const int32_t *tile_offsets,
+                          const int32_t *flatten_ids, int64_t n_isects,
+                          int64_t C, int64_t N, uint32_t width, uint32_t height,
+                          uint32_t tile_size, uint32_t n_tiles_w,
+                          uint32_t n_tiles_h, float *image, void *workspace,
+                          size_t workspace_bytes, r2s_stream_t stream);
+int r2s_rasterize_fwd_f64(const double *means2d, const double *conics,
+                          const double *opacities, const double *mus,
+                          const int32_t *tile_offsets,
+                          const int32_t *flatten_ids, int64_t n_isects,
+                          int64_t C, int64_t N, uint32_t width, uint32_t height,
+                          uint32_t tile_size, uint32_t n_tiles_w,
+                          uint32_t n_tiles_h, double *image, void *workspace,
+                          size_t workspace_bytes, r2s_stream_t stream);
+
+/* RasterizeToPixels.cpp:226-317 rasterize_to_pixels_bwd_per_gaussian_tensor
+ * (isect_ids != NULL) and RasterizeToPixels.cpp:122-222
+ * rasterize_to_pixels_bwd_tensor (isect_ids == NULL: the tile of each record
+ * comes from tile_offsets).  Outputs are accumulated (+=): the caller zeroes
+ * them.  v_means2d_abs may be NULL (absgrad off). */
+int r2s_rasterize_bwd_f32(const float *means2d, const float *conics,
+                          const float *opacities, const float *mus,
+                          const int32_t *tile_offsets, const int64_t *isect_ids,
+                          const int32_t *flatten_ids, int64_t n_isects,
+                          const float *v_image, int64_t C, int64_t N,
+                          uint32_t width, uint32_t height, uint32_t tile_size,
+                          uint32_t n_tiles_w, uint32_t n_tiles_h,
+                          float *v_means2d_abs, float *v_means2d,
+                          float *v_conics, float *v_opacities, float *v_mus,
+                          r2s_stream_t stream);
+int r2s_rasterize_bwd_f64(const double *means2d, const double *conics,
+                          const double *opacities, const double *mus,
+                          const int32_t *tile_offsets, const int64_t *isect_ids,
+                          const int32_t *flatten_ids, int64_t n_isects,
+                          const double *v_image, int64_t C, int64_t N,
+                          uint32_t width, uint32_t height, uint32_t tile_size,
+                          uint32_t n_tiles_w, uint32_t n_tiles_h,
+                          double *v_means2d_abs, double *v_means2d,
+                          double *v_conics, double *v_opacities, double *v_mus,
+                          r2s_stream_t stream);
+
+/* ---------------------------------------------------------------------- */
+/* Volume mapping and voxelizer                                           */
+/* ---------------------------------------------------------------------- */
+
+/* r2splat/cuda/csrc/WorldToVolumeMapping.cpp:37-112
+ * world_to_volume_mapping_fwd_tensor: means [N,3], covars [N,6],
+ * ranges [3], centers [3] -> means3d [N,3], conics [N,6], radii [N,3].
+ * (The reference's max_scales argument is unused and is not taken here.) */
+int r2s_world_to_volume_mapping_fwd_f32(
+    const float *means, const float *covars, const float *ranges,
+    const float *centers, uint32_t dim2, uint32_t dim1, uint32_t dim0,
+    double eps3d, double radius_clip, float *means3d, float *conics,
+    int32_t *radii, int64_t N, r2s_stream_t stream);
+int r2s_world_to_volume_mapping_fwd_f64(
+    const double *means, const double *covars, const double *ranges,
+    const double *centers, uint32_t dim2, uint32_t dim1, uint32_t dim0,
+    double eps3d, double radius_clip, double *means3d, double *conics,
+    int32_t *radii, int64_t N, r2s_stream_t stream);
+
+/* WorldToVolumeMapping.cpp:119-192 world_to_volume_mapping_bwd_tensor. */
+int r2s_world_to_volume_mapping_bwd_f32(
+    const float *means, const float *covars, const float *ranges,
+    const float *centers, uint32_t dim2, uint32_t dim1, uint32_t dim0,
+    double eps3d, const float *v_means3d, const float *v_conics,
+    float *v_means, float *v_covars, int64_t N, r2s_stream_t stream);
+int r2s_world_to_volume_mapping_bwd_f64(
+    const double *means, const double *covars, const double *ranges,
+    const double *centers, uint32_t dim2, uint32_t dim1, uint32_t dim0,
+    double eps3d, const double *v_means3d, const double *v_conics,
+    double *v_means, double *v_covars, int64_t N, r2s_stream_t stream);
+
+/* r2splat/cuda/csrc/VoxelizeToVoxels.cpp:31-108 voxelize_to_voxels_fwd_tensor:
+ * volume [dim0,dim1,dim2] = per voxel sum of opacity*exp(-sigma) over the
+ * brick list, skipping sigma < 0 and |alpha| < 1e-6.  Fully written. */
+int r2s_voxelize_fwd_f32(const float *means3d, const float *conics,
+                         const float *opacities, const int32_t *tile_offsets,
+                         const int32_t *flatten_ids, int64_t n_isects, int64_t N,
+                         uint32_t dim2, uint32_t dim1, uint32_t dim0,
+                         uint32_t tile_size, uint32_t n_tiles_d2,
+                         uint32_t n_tiles_d1, uint32_t n_tiles_d0,
+                         float *volume, r2s_stream_t stream);
+int r2s_voxelize_fwd_f64(const double *means3d, const double *conics,
+                         const double *opacities, const int32_t *tile_offsets,
+                         const int32_t *flatten_ids, int64_t n_isects, int64_t N,
+                         uint32_t dim2, uint32_t dim1, uint32_t dim0,
+                         uint32_t tile_size, uint32_t n_tiles_d2,
+                         uint32_t n_tiles_d1, uint32_t n_tiles_d0,
+                         double *volume, r2s_stream_t stream);
+
+/* VoxelizeToVoxels.cpp:195-278 voxelize_to_voxels_bwd_per_gaussian_tensor
+ * (isect_ids != NULL) and VoxelizeToVoxels.cpp:115-192
+ * voxelize_to_voxels_bwd_tensor (isect_ids == NULL).  Accumulates (+=). */
+int r2s_voxelize_bwd_f32(const float *means3d, const float *conics,
+                         const float *opacities, const int32_t *tile_offsets,
+                         const int64_t *isect_ids, const int32_t *flatten_ids,
+                         int64_t n_isects, const float *v_volume, int64_t N,
+                         uint32_t dim2, uint32_t dim1, uint32_t dim0,
+                         uint32_t tile_size, uint32_t n_tiles_d2,
+                         uint32_t n_tiles_d1, uint32_t n_tiles_d0,
+                         float *v_means3d, float *v_conics, float *v_opacities,
+                         r2s_stream_t stream);
+int r2s_voxelize_bwd_f64(const double *means3d, const double *conics,
+                         const double *opacities, const int32_t *tile_offsets,
+                         const int64_t *isect_ids, const int32_t *flatten_ids,
+                         int64_t n_isects, const double *v_volume, int64_t N,
+                         uint32_t dim2, uint32_t dim1, uint32_t dim0,
+                         uint32_t tile_size, uint32_t n_tiles_d2,
+                         uint32_t n_tiles_d1, uint32_t n_tiles_d0,
+                         double *v_means3d, double *v_conics,
+                         double *v_opacities, r2s_stream_t stream);
+
+/* ---------------------------------------------------------------------- */
+/* Densify / prune index compaction                                        */
+/* ---------------------------------------------------------------------- */
+
+/* Workspace for r2s_mask_split. */
+int64_t r2s_mask_workspace_bytes(int64_t n);
+
+/* src/strategies/binary_tree.py:68,101-102,158 (torch.where(mask)[0] and
+ * torch.where(~mask)[0]): mask [n] (bytes, nonzero = true) ->
+ * out [n] int64 = ascending indices of true entries followed by ascending
+ * indices of false entries; *n_true_dev (device int64) = number of trues. */
+int r2s_mask_split(const uint8_t *mask, int64_t n, int64_t *out,
+                   int64_t *n_true_dev, void *workspace,
+                   size_t workspace_bytes, r2s_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* R2SPLAT_HIP_H */

@@ -1,0 +1,31 @@
+"""CPU oracle for the r2splat Gaussian backend -- TEST INFRASTRUCTURE ONLY.
+
+This package restates, on the CPU, the algorithms of the BT-3DGS ``r2splat``
+CUDA operators (``r2splat/cuda/csrc/*.cu`` in the reference tree).  Each
+function cites the reference ``file:line`` it follows.  It is the checker for
+the HIP kernels, never part of the product: only ``tests/``,
+``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import
+it, and the shipped ``r2splat`` package never does.
+
+Modules
+-------
+``ops``      numpy restatements of the element-wise operators (parameter
+             transform, cone-beam projection, conics/mu, volume mapping),
+             written in the reference kernels' operation order so that fp32
+             results are reproducible bit-for-bit where no transcendental
+             function is involved.
+``binning``  integer tile binning (count, emit, stable sort, offsets), 2D and
+             3D, plus the densify/prune index compaction.
+``native``   ctypes bindings of ``oracle/c/r2s_oracle.c``: the sequential
+             rasterizer and voxelizer (forward and both backward modes).
+``compose``  the ``r2splat.ops`` forward/backward composition on top of the
+             above (explicit.py / direct.py restated).
+``dense``    the dense PyTorch-CPU formulation of the reference's op tests
+             (autograd backward), used as the CPU baseline and as an
+             independent end-to-end check.
+``scenes``   seeded synthetic inputs shared by tests and the CPU baseline.
+
+How each function is pinned (golden vectors, closed forms, brute force,
+invariants) is listed in ``tests/test_oracle_*.py``.  Functions without such
+a check say "parity unpinned" in their docstring.
+"""

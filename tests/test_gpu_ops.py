@@ -1,0 +1,305 @@
+"""HIP operators vs the CPU oracle on seeded inputs (op level).
+
+Bit-exact where the kernel has no transcendental function (projection,
+conics/mu, volume mapping, their VJPs, binning, offsets, compaction);
+rel 1e-4 / abs 1e-5 otherwise.  Every call goes through the C ABI via
+r2splat.cuda._wrapper.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_close, assert_equal, make_scene, np32
+from oracle import binning, native, ops
+from r2splat.cuda import _wrapper as W
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _prepared(n, seed, dtype=torch.float32, **kw):
+    raw, viewmats, Ks, g = make_scene(n, seed, **kw)
+    covars, max_scales = ops.parameter_transform_fwd(
+        raw.quats.double().numpy(), raw.raw_scales.double().numpy(), 5e-4, 1.0)
+    t = lambda a: torch.as_tensor(a, dtype=dtype, device=DEV).contiguous()  # noqa: E731
+    return dict(raw=raw, means=t(raw.means.numpy()), covars=t(covars), viewmats=t(viewmats),
+                Ks=t(Ks), opac=t(ops.softplus(raw.raw_opacities.double().numpy())), gen=g)
+
+
+def test_library_loaded():
+    assert W.is_cuda_extension_available(), "libr2splat_hip.so failed to load"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_parameter_transform(dtype):
+    raw, _, _, g = make_scene(3000, 1)
+    q = raw.quats.to(dtype) * 0.7
+    s = raw.raw_scales.to(dtype)
+    o = raw.raw_opacities.to(dtype)
+    qd, sd, od = q.to(DEV), s.to(DEV), o.to(DEV)
+    cov, ms = W.parameter_transform_fwd(qd, sd, 5e-4, 1.0)
+    cov_o, ms_o = ops.parameter_transform_fwd(q.numpy(), s.numpy(), 5e-4, 1.0)
+    assert_close(np32(cov), cov_o, "covars")
+    assert_close(np32(ms), ms_o, "max_scales")
+    cov2, ms2, op2 = W.prepare_gaussians(qd, sd, od, 5e-4, 1.0)
+    assert_equal(np32(cov2), np32(cov), "fused covars")
+    assert_equal(np32(ms2), np32(ms), "fused max_scales")
+    assert_close(np32(op2), np32(torch.nn.functional.softplus(od)), "softplus")
+    v = torch.randn(3000, 6, generator=g, dtype=dtype)
+    vq, vs = W.parameter_transform_bwd(qd, sd, 5e-4, 1.0, v.to(DEV))
+    vq_o, vs_o = ops.parameter_transform_bwd(q.numpy(), s.numpy(), 5e-4, 1.0, v.numpy())
+    assert_close(np32(vq), vq_o, "v_quats", atol=1e-4 if dtype == torch.float32 else 1e-9)
+    assert_close(np32(vs), vs_o, "v_raw_scales", atol=1e-4 if dtype == torch.float32 else 1e-9)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("n_views", [1, 3])
+def test_projection_bit_exact(dtype, n_views):
+    d = _prepared(4000, 2, dtype, n_det=96, n_views=n_views)
+    m2, c2, r = W.world_to_image_projection_fwd(d["means"], d["covars"], d["viewmats"], d["Ks"],
+                                                96, 96, 1e-8, 3.0)
+    m2o, c2o, ro = ops.world_to_image_projection_fwd(np32(d["means"]), np32(d["covars"]),
+                                                     np32(d["viewmats"]), np32(d["Ks"]), 96, 96,
+                                                     1e-8, 3.0)
+    assert_equal(np32(m2), m2o, "means2d")
+    assert_equal(np32(c2), c2o, "cov2d")
+    assert_equal(np32(r), ro, "radii")
+    assert int((ro > 0).any(-1).sum()) > 100
+    con, mu = W.conics_mu_fwd(c2, 1e-8)
+    cono, muo = ops.conics_mu_fwd(c2o, 1e-8)
+    assert_equal(np32(con), cono, "conics")
+    assert_equal(np32(mu), muo, "mus")
+    # Fused forward = the three separate passes.
+    fm2, fc2, fr, fcon, fmu, fop = W.project_gaussians_fwd(
+        d["means"], d["covars"], d["opac"], d["viewmats"], d["Ks"], 96, 96, 1e-8, 3.0)
+    for a, b, n in ((fm2, m2, "means2d"), (fc2, c2, "cov2d"), (fr, r, "radii"),
+                    (fcon, con, "conics"), (fmu, mu, "mus")):
+        assert_equal(np32(a), np32(b), f"fused {n}")
+    assert_equal(np32(fop), np.broadcast_to(np32(d["opac"]), fop.shape), "opacity[C,N]")
+    # VJPs.
+    g = d["gen"]
+    C, N = n_views, 4000
+    vm2 = torch.randn(C, N, 2, generator=g, dtype=dtype)
+    vcon = torch.randn(C, N, 3, generator=g, dtype=dtype)
+    vmu = torch.randn(C, N, generator=g, dtype=dtype)
+    vcov = W.conics_mu_bwd(c2, 1e-8, con, mu, vcon.to(DEV), vmu.to(DEV))
+    vcovo = ops.conics_mu_bwd(c2o, 1e-8, cono, muo, vcon.numpy(), vmu.numpy())
+    assert_equal(np32(vcov), vcovo, "v_cov2d")
+    vmean, vcovar = W.world_to_image_projection_bwd(d["means"], d["covars"], d["viewmats"],
+                                                    d["Ks"], 96, 96, vm2.to(DEV), vcov)
+    vmeano, vcovaro = ops.world_to_image_projection_bwd(
+        np32(d["means"]), np32(d["covars"]), np32(d["viewmats"]), np32(d["Ks"]), 96, 96,
+        vm2.numpy(), vcovo)
+    assert_equal(np32(vmean), vmeano, "v_means")
+    assert_equal(np32(vcovar), vcovaro, "v_covars")
+    fvm, fvc = W.project_gaussians_bwd(d["means"], d["covars"], d["viewmats"], d["Ks"], 96, 96,
+                                       1e-8, c2, con, mu, vm2.to(DEV), vcon.to(DEV), vmu.to(DEV))
+    assert_equal(np32(fvm), vmeano, "fused v_means")
+    assert_equal(np32(fvc), vcovaro, "fused v_covars")
+
+
+@pytest.mark.parametrize("rect", [True, False])
+@pytest.mark.parametrize("n_views", [1, 2])
+def test_isect_tiles_bit_exact(rect, n_views):
+    d = _prepared(6000, 3, n_det=100, n_views=n_views, log_mu=-3.5)
+    m2, _, r, _, _, _ = W.project_gaussians_fwd(d["means"], d["covars"], d["opac"],
+                                                d["viewmats"], d["Ks"], 100, 100, 1e-8, 3.0)
+    radii = r if rect else r.amax(-1).contiguous()
+    tw = th = 7
+    tpg, ids, fl = W.isect_tiles(m2, radii, 16, tw, th)
+    tpg_o, ids_o, fl_o = binning.isect_tiles(np32(m2), np32(radii), 16, tw, th)
+    assert ids_o.size > 1000
+    assert_equal(np32(tpg), tpg_o, "tiles_per_gauss")
+    assert_equal(np32(ids), ids_o, "isect_ids")
+    assert_equal(np32(fl), fl_o, "flatten_ids")
+    off = W.isect_offset_encode(ids, n_views, tw, th)
+    assert_equal(np32(off), binning.isect_offset_encode(ids_o, n_views, tw, th), "tile_offsets")
+
+
+def test_isect_tiles_large_footprints_and_degenerate():
+    # Huge radii, non-finite means and zero radii: the emit loop and clamps.
+    g = torch.Generator().manual_seed(4)
+    N = 5000
+    m2 = (torch.rand(1, N, 2, generator=g) * 1400 - 200).float()
+    r = torch.randint(0, 400, (1, N, 2), generator=g).int()
+    m2[0, :7, 0] = float("nan")
+    m2[0, 7:14, 1] = float("inf")
+    r[0, 14:40] = 0
+    m2d, rd = m2.to(DEV), r.to(DEV)
+    tpg, ids, fl = W.isect_tiles(m2d, rd, 16, 64, 64)
+    tpg_o, ids_o, fl_o = binning.isect_tiles(m2.numpy(), r.numpy(), 16, 64, 64)
+    assert ids_o.size > 1_000_000
+    assert_equal(np32(tpg), tpg_o, "tiles_per_gauss")
+    assert_equal(np32(ids), ids_o, "isect_ids")
+    assert_equal(np32(fl), fl_o, "flatten_ids")
+
+
+def test_isect_tiles_empty():
+    m2 = torch.zeros(1, 10, 2, device=DEV)
+    r = torch.zeros(1, 10, 2, dtype=torch.int32, device=DEV)
+    tpg, ids, fl = W.isect_tiles(m2, r, 16, 4, 4)
+    assert ids.numel() == 0 and fl.numel() == 0 and int(tpg.abs().sum()) == 0
+    off = W.isect_offset_encode(ids, 1, 4, 4)
+    assert off.shape == (1, 4, 4) and int(off.abs().sum()) == 0
+    tpg, ids, fl = W.isect_tiles(torch.zeros(1, 0, 2, device=DEV),
+                                 torch.zeros(1, 0, 2, dtype=torch.int32, device=DEV), 16, 4, 4)
+    assert tpg.shape == (1, 0) and ids.numel() == 0
+
+
+def test_isect_tiles_3d_bit_exact():
+    d = _prepared(5000, 5, log_mu=-3.0)
+    ranges = torch.full((3,), 2.0, device=DEV)
+    centers = torch.zeros(3, device=DEV)
+    m3, con, r3 = W.world_to_volume_mapping_fwd(d["means"], d["covars"], d["opac"], ranges,
+                                                centers, 40, 36, 44, 1e-8, 3.0)
+    n2, n1, n0 = 5, 5, 6
+    tpg, ids, fl = W.isect_tiles_3d(m3, r3, 8, n2, n1, n0)
+    tpg_o, ids_o, fl_o = binning.isect_tiles_3d(np32(m3), np32(r3), 8, n2, n1, n0)
+    assert ids_o.size > 5000
+    assert_equal(np32(tpg), tpg_o, "tiles_per_gauss")
+    assert_equal(np32(ids), ids_o, "isect_ids")
+    assert_equal(np32(fl), fl_o, "flatten_ids")
+    off = W.isect_offset_encode_3d(ids, n2, n1, n0)
+    assert_equal(np32(off), binning.isect_offset_encode_3d(ids_o, n2, n1, n0), "tile_offsets")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_volume_mapping_bit_exact(dtype):
+    d = _prepared(4000, 6, dtype, log_mu=-3.0)
+    ranges = torch.tensor([2.0, 1.5, 2.5], dtype=dtype, device=DEV)
+    centers = torch.tensor([0.1, -0.2, 0.0], dtype=dtype, device=DEV)
+    m3, con, r3 = W.world_to_volume_mapping_fwd(d["means"], d["covars"], d["opac"], ranges,
+                                                centers, 48, 40, 56, 1e-8, 3.0)
+    m3o, cono, r3o = ops.world_to_volume_mapping_fwd(np32(d["means"]), np32(d["covars"]),
+                                                     np32(ranges), np32(centers), 48, 40, 56,
+                                                     1e-8, 3.0)
+    assert_equal(np32(m3), m3o, "means3d")
+    assert_equal(np32(con), cono, "conics3d")
+    assert_equal(np32(r3), r3o, "radii3d")
+    g = d["gen"]
+    vm3 = torch.randn(4000, 3, generator=g, dtype=dtype)
+    vc3 = torch.randn(4000, 6, generator=g, dtype=dtype)
+    vm, vc = W.world_to_volume_mapping_bwd(d["means"], d["covars"], ranges, centers, 48, 40, 56,
+                                           1e-8, vm3.to(DEV), vc3.to(DEV))
+    vmo, vco = ops.world_to_volume_mapping_bwd(np32(d["means"]), np32(d["covars"]), np32(ranges),
+                                               np32(centers), 48, 40, 56, 1e-8, vm3.numpy(),
+                                               vc3.numpy())
+    assert_equal(np32(vm), vmo, "v_means (volume)")
+    assert_equal(np32(vc), vco, "v_covars (volume)")
+
+
+def _raster_case(n, seed, W_img, H_img, ts, n_views=1, dtype=torch.float32, log_mu=-3.6):
+    d = _prepared(n, seed, dtype, n_det=max(W_img, H_img), n_views=n_views, log_mu=log_mu)
+    Ks = d["Ks"].clone()
+    Ks[:, 0, 2] = W_img / 2
+    Ks[:, 1, 2] = H_img / 2
+    m2, c2, r, con, mu, op = W.project_gaussians_fwd(d["means"], d["covars"], d["opac"],
+                                                     d["viewmats"], Ks, W_img, H_img, 1e-8, 3.0)
+    tw, th = -(-W_img // ts), -(-H_img // ts)
+    _, ids, fl = W.isect_tiles(m2, r, ts, tw, th)
+    off = W.isect_offset_encode(ids, n_views, tw, th)
+    return d, m2, con, mu, op, ids, fl, off
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("shape", [(64, 64, 16), (70, 45, 16), (40, 40, 8)])
+def test_rasterize_fwd_bwd(dtype, shape):
+    W_img, H_img, ts = shape
+    d, m2, con, mu, op, ids, fl, off = _raster_case(3000, 7, W_img, H_img, ts, 2, dtype)
+    assert fl.numel() > 500
+    img = W.rasterize_to_pixels_fwd(m2, con, op, mu, off, fl, W_img, H_img, ts)
+    img_o = native.raster_fwd(np32(m2), np32(con), np32(op), np32(mu), np32(off), np32(fl),
+                              W_img, H_img, ts)
+    f32 = dtype == torch.float32
+    tol = dict(rtol=1e-4, atol=1e-5) if f32 else dict(rtol=1e-9, atol=1e-12)
+    assert_close(np32(img), img_o, "image", max_outliers=img_o.size // 1000 if f32 else 0,
+                 outlier_atol=3e-5 if f32 else None, **tol)
+    v = torch.randn(img.shape, generator=d["gen"], dtype=dtype)
+    ref = native.raster_bwd(np32(m2), np32(con), np32(op), np32(mu), np32(off), np32(fl),
+                            v.numpy(), W_img, H_img, ts, True)
+    names = ("v_means2d_abs", "v_means2d", "v_conics", "v_opacities", "v_mus")
+    for mode in ("primitive", "pixel"):
+        if mode == "primitive":
+            got = W.rasterize_to_pixels_bwd_per_gaussian(m2, con, op, mu, off, ids, fl,
+                                                         v.to(DEV), W_img, H_img, ts, True)
+        else:
+            got = W.rasterize_to_pixels_bwd(m2, con, op, mu, off, fl, v.to(DEV), W_img, H_img,
+                                            ts, True)
+        for a, e, n in zip(got, ref, names):
+            scale = float(np.abs(e).max()) + 1e-30
+            assert_close(np32(a), e, f"{mode} {n}", rtol=tol["rtol"],
+                         atol=max(tol["atol"], (3e-6 if f32 else 1e-12) * scale),
+                         max_outliers=e.size // 500 if f32 else 0,
+                         outlier_atol=2e-4 * scale if f32 else None)
+    no_abs = W.rasterize_to_pixels_bwd_per_gaussian(m2, con, op, mu, off, ids, fl, v.to(DEV),
+                                                    W_img, H_img, ts, False)
+    assert no_abs[0] is None
+
+
+def test_rasterize_empty():
+    m2 = torch.zeros(1, 3, 2, device=DEV)
+    z3 = torch.zeros(1, 3, 3, device=DEV)
+    z = torch.zeros(1, 3, device=DEV)
+    off = torch.zeros(1, 2, 2, dtype=torch.int32, device=DEV)
+    fl = torch.zeros(0, dtype=torch.int32, device=DEV)
+    img = W.rasterize_to_pixels_fwd(m2, z3, z, z, off, fl, 30, 20, 16)
+    assert img.shape == (1, 20, 30) and float(img.abs().sum()) == 0.0
+    g = W.rasterize_to_pixels_bwd(m2, z3, z, z, off, fl, torch.ones(1, 20, 30, device=DEV), 30,
+                                  20, 16, True)
+    assert all(float(t.abs().sum()) == 0.0 for t in g)
+
+
+def _voxel_case(n, seed, dims, ts, dtype=torch.float32, log_mu=-3.2):
+    d = _prepared(n, seed, dtype, log_mu=log_mu)
+    ranges = torch.full((3,), 2.0, dtype=dtype, device=DEV)
+    centers = torch.zeros(3, dtype=dtype, device=DEV)
+    d2, d1, d0 = dims
+    m3, con, r3 = W.world_to_volume_mapping_fwd(d["means"], d["covars"], d["opac"], ranges,
+                                                centers, d2, d1, d0, 1e-8, 3.0)
+    n2, n1, n0 = (-(-x // ts) for x in dims)
+    _, ids, fl = W.isect_tiles_3d(m3, r3, ts, n2, n1, n0)
+    off = W.isect_offset_encode_3d(ids, n2, n1, n0)
+    return d, m3, con, ids, fl, off
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("dims,ts", [((32, 32, 32), 8), ((30, 20, 26), 8), ((24, 24, 24), 4)])
+def test_voxelize_fwd_bwd(dtype, dims, ts):
+    d, m3, con, ids, fl, off = _voxel_case(2500, 8, dims, ts, dtype)
+    d2, d1, d0 = dims
+    assert fl.numel() > 500
+    op = d["opac"]
+    vol = W.voxelize_to_voxels_fwd(m3, con, op, off, fl, d2, d1, d0, ts)
+    vol_o = native.voxel_fwd(np32(m3), np32(con), np32(op), np32(off), np32(fl), d2, d1, d0, ts)
+    f32 = dtype == torch.float32
+    tol = dict(rtol=1e-4, atol=1e-5) if f32 else dict(rtol=1e-9, atol=1e-12)
+    assert_close(np32(vol), vol_o, "volume", max_outliers=vol_o.size // 1000 if f32 else 0,
+                 outlier_atol=3e-6 if f32 else None, **tol)
+    v = torch.randn(vol.shape, generator=d["gen"], dtype=dtype)
+    ref = native.voxel_bwd(np32(m3), np32(con), np32(op), np32(off), np32(fl), v.numpy(), d2, d1,
+                           d0, ts)
+    for mode in ("primitive", "pixel"):
+        if mode == "primitive":
+            got = W.voxelize_to_voxels_bwd_per_gaussian(m3, con, op, off, ids, fl, v.to(DEV), d2,
+                                                        d1, d0, ts)
+        else:
+            got = W.voxelize_to_voxels_bwd(m3, con, op, off, fl, v.to(DEV), d2, d1, d0, ts)
+        for a, e, n in zip(got, ref, ("v_means3d", "v_conics", "v_opacities")):
+            scale = float(np.abs(e).max()) + 1e-30
+            assert_close(np32(a), e, f"{mode} {n}", rtol=tol["rtol"],
+                         atol=max(tol["atol"], (3e-6 if f32 else 1e-12) * scale),
+                         max_outliers=e.size // 500 if f32 else 0,
+                         outlier_atol=2e-4 * scale if f32 else None)
+
+
+@pytest.mark.parametrize("n", [0, 1, 63, 64, 65, 4095, 4096, 4097, 100_003, 2_000_000])
+def test_mask_split_matches_torch_where(n):
+    g = torch.Generator().manual_seed(n)
+    for p in (0.0, 0.3, 1.0):
+        mask = (torch.rand(n, generator=g) < p).to(DEV)
+        out, n_true = W.mask_split(mask)
+        sel, rest = torch.where(mask)[0], torch.where(~mask)[0]
+        assert n_true == sel.numel()
+        assert torch.equal(out[:n_true], sel) and torch.equal(out[n_true:], rest)
