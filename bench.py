@@ -1,0 +1,325 @@
+"""Benchmark of the r2splat HIP backend on one MI355X.
+
+Headline (``value``): projection forward + backward calls per second at the
+BASELINE config-4 shape -- 500,000 Gaussians grown as a binary tree from one
+root, 512x512 cone-beam detector, one view per call (angles k * 1 degree),
+upstream image gradient N(0,1).  One call = prepare_explicit_gaussians ->
+explicit_rasterize -> explicit_backward, the reference's training path.
+
+Also reported: the voxelizer at config 3 (200k Gaussians, 256^3, fwd + bwd,
+Mvox/s and % of HBM peak), the training-step shape of config 4 (projection +
+128^3 voxelization fwd/bwd + compaction every 100 steps), per-kernel event
+timings, the roofline of the dominant kernel and the CPU oracle baseline.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "bt-3dgs_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, AMD public spec
+FP32_VALU_PEAK_TFLOPS = 157.3
+SMIN, SMAX = 5e-4, 1.0
+EPS = 1e-8
+DET = 512
+N_PROJ = 500_000
+N_VOX, VOX_DIM = 200_000, 256
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def _events():
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+class Projection:
+    """Config-4 projection workload resident on the device."""
+
+    def __init__(self, dev, n=N_PROJ, det=DET, seed=0):
+        from r2splat import geometry, scenes
+
+        g = torch.Generator().manual_seed(seed)
+        raw = scenes.binary_tree_gaussians(n, g, opacity="uniform")
+        self.raw = raw
+        self.params = [torch.nn.Parameter(t.clone().to(dev)) for t in
+                       (raw.means, raw.quats, raw.raw_scales, raw.raw_opacities)]
+        angles = [math.radians(k) for k in range(360)]
+        vm, Ks = geometry.cone_beam_views(angles, det)
+        self.viewmats = vm.to(dev)
+        self.Ks = Ks.to(dev)
+        self.v_images = torch.randn(4, 1, det, det, generator=g).to(dev)
+        self.det = det
+        self.step_i = 0
+
+    def step(self):
+        from r2splat.ops import explicit
+
+        means, quats, scales, opac = self.params
+        for p in self.params:
+            p.grad = None
+        k = self.step_i % 360
+        self.step_i += 1
+        state = explicit.prepare_explicit_gaussians(quats, scales, opac, scale_min=SMIN,
+                                                    scale_max=SMAX)
+        res = explicit.explicit_rasterize(state, means, self.viewmats[k:k + 1],
+                                          self.Ks[k:k + 1], img_w=self.det, img_h=self.det,
+                                          tile_size=16, eps2d=EPS, radius_clip=3.0, absgrad=True)
+        res.image.grad = self.v_images[k % 4]
+        explicit.explicit_backward(state, means, quats, scales, opac)
+        return state
+
+
+class Voxelization:
+    """Config-3 voxelization workload: the voxel branch at the op boundary."""
+
+    def __init__(self, dev, n=N_VOX, dim=VOX_DIM, seed=1):
+        from r2splat import scenes
+        from r2splat.cuda import _wrapper as W
+
+        g = torch.Generator().manual_seed(seed)
+        raw = scenes.random_gaussians(n, g, -4.5, 0.6)
+        means = raw.means.to(dev)
+        covars, max_scales, opac = W.prepare_gaussians(raw.quats.to(dev), raw.raw_scales.to(dev),
+                                                       raw.raw_opacities.to(dev), SMIN, SMAX)
+        self.means, self.covars, self.max_scales, self.opac = means, covars, max_scales, opac
+        self.ranges = torch.full((3,), 2.0, device=dev)
+        self.centers = torch.zeros(3, device=dev)
+        self.v_volume = torch.randn(dim, dim, dim, generator=g).to(dev)
+        self.dim = dim
+        self.last = None
+
+    def step(self):
+        from r2splat.cuda import _wrapper as W
+
+        d = self.dim
+        nt = -(-d // 8)
+        m3, con, r3 = W.world_to_volume_mapping_fwd(self.means, self.covars, self.max_scales,
+                                                    self.ranges, self.centers, d, d, d, EPS, 3.0)
+        _, ids, fl = W.isect_tiles_3d(m3, r3, 8, nt, nt, nt)
+        off = W.isect_offset_encode_3d(ids, nt, nt, nt)
+        vol = W.voxelize_to_voxels_fwd(m3, con, self.opac, off, fl, d, d, d, 8)
+        vm3, vc3, vo = W.voxelize_to_voxels_bwd_per_gaussian(m3, con, self.opac, off, ids, fl,
+                                                             self.v_volume, d, d, d, 8)
+        W.world_to_volume_mapping_bwd(self.means, self.covars, self.ranges, self.centers, d, d, d,
+                                      EPS, vm3, vc3)
+        self.last = (m3, con, off, ids, fl, vol)
+        return vol
+
+
+def time_steps(fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def time_kernel(fn, reps):
+    """Average device time of fn() bracketed by events on the current stream."""
+    fn()
+    torch.cuda.synchronize()
+    s, e = _events()
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) / reps * 1e-3
+
+
+def kernel_breakdown(proj: Projection, reps):
+    """Event timings of each projection stage at the config-4 inputs of view 0."""
+    from r2splat.cuda import _wrapper as W
+
+    means, quats, scales, opac = proj.params
+    vm, Ks, det = proj.viewmats[:1], proj.Ks[:1], proj.det
+    cov, ms, op = W.prepare_gaussians(quats.detach(), scales.detach(), opac.detach(), SMIN, SMAX)
+    m2, c2, r, con, mu, opc = W.project_gaussians_fwd(means.detach(), cov, op, vm, Ks, det, det,
+                                                      EPS, 3.0)
+    nt = -(-det // 16)
+    _, ids, fl = W.isect_tiles(m2, r, 16, nt, nt)
+    off = W.isect_offset_encode(ids, 1, nt, nt)
+    v_img = proj.v_images[0]
+    out = {"n_isects_2d": int(fl.numel())}
+    t = {}
+    t["prepare"] = time_kernel(lambda: W.prepare_gaussians(quats.detach(), scales.detach(),
+                                                           opac.detach(), SMIN, SMAX), reps)
+    t["project_fwd"] = time_kernel(lambda: W.project_gaussians_fwd(
+        means.detach(), cov, op, vm, Ks, det, det, EPS, 3.0), reps)
+    t["binning_2d"] = time_kernel(lambda: W.isect_tiles(m2, r, 16, nt, nt), reps)
+    t["rasterize_fwd"] = time_kernel(lambda: W.rasterize_to_pixels_fwd(
+        m2, con, opc, mu, off, fl, det, det, 16), reps)
+    t["rasterize_bwd"] = time_kernel(lambda: W.rasterize_to_pixels_bwd_per_gaussian(
+        m2, con, opc, mu, off, ids, fl, v_img, det, det, 16, True), reps)
+    out["seconds"] = t
+    return out
+
+
+def proj_bytes(n, i2, p):
+    """Algorithmic bytes of one projection fwd+bwd call (B_proj)."""
+    return 164 * n + 128 * i2 + 8 * p
+
+
+def vox_bytes(n, i3, v):
+    """Algorithmic bytes of one voxelization fwd+bwd call (B_vox)."""
+    return 144 * n + 156 * i3 + 8 * v
+
+
+def cpu_baseline(proj: Projection, stride=8):
+    """Oracle (numpy + sequential C, one core) projection fwd+bwd on a seeded
+    random 1/``stride`` subset of the config-4 Gaussians, 512^2, view 0; the
+    time is scaled by ``stride`` to the full set (work is linear in the
+    number of tile records).  Returns (calls/s, seconds, sample text)."""
+    from oracle import compose
+
+    raw = proj.raw
+    sel = torch.from_numpy(np.sort(np.random.default_rng(0).choice(raw.n, raw.n // stride,
+                                                                    replace=False)))
+    means = raw.means[sel].numpy()
+    quats = raw.quats[sel].numpy()
+    scales = raw.raw_scales[sel].numpy()
+    opac = raw.raw_opacities[sel].numpy()
+    vm = proj.viewmats[:1].cpu().numpy()
+    Ks = proj.Ks[:1].cpu().numpy()
+    v_img = proj.v_images[0].cpu().numpy()
+    t0 = time.perf_counter()
+    covars, _, op = compose.prepare(quats, scales, opac, SMIN, SMAX)
+    fwd = compose.rasterize_forward(means, covars, op, vm, Ks, DET, DET, 16, EPS, 3.0)
+    compose.explicit_backward(covars, fwd, None, means, quats, scales, opac, SMIN, SMAX, v_img)
+    dt = time.perf_counter() - t0
+    n_s = means.shape[0]
+    sample = (f"oracle projection fwd+bwd (numpy + sequential C, 1 core) on a seeded random "
+              f"{n_s} of the {raw.n} config-4 Gaussians, 512^2, view 0, "
+              f"{fwd['isect_ids'].size} tile records; time x{stride} to the full set")
+    return 1.0 / (dt * stride), dt, sample
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-voxel", action="store_true")
+    ap.add_argument("--kernel-reps", type=int, default=10)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the r2splat path has no "
+              "multi-GPU mode in this build.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    from r2splat.cuda import _wrapper as W
+
+    if not W.is_cuda_extension_available():
+        raise RuntimeError("libr2splat_hip.so is not built or failed to load")
+    dev = torch.device("cuda:0")
+
+    log("building config-4 projection workload (500k binary-tree Gaussians, 512^2)")
+    proj = Projection(dev)
+    t_proj = time_steps(proj.step, args.steps, args.warmup)
+    log(f"projection fwd+bwd: {t_proj * 1e3:.3f} ms/call")
+    kb = kernel_breakdown(proj, args.kernel_reps)
+    i2 = kb["n_isects_2d"]
+    log(f"kernel breakdown: { {k: round(v * 1e3, 3) for k, v in kb['seconds'].items()} } ms, "
+        f"I2={i2}")
+
+    result = {
+        "metric": "proj fwd+bwd/s @500k Gauss 512² det; voxelize Mvox/s @256³; % HBM peak",
+        "value": 1.0 / t_proj,
+        "unit": "proj fwd+bwd calls/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": t_proj * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded binary-tree Gaussians, densities U[0,1], cone-beam views)",
+        "config": {"workload": "config4 projection fwd+bwd", "n_gaussians": N_PROJ,
+                   "detector": [DET, DET], "views_per_call": 1, "tile_size": 16,
+                   "dso": 1.0, "dsd": 1.5, "s_detector": 3.0, "eps2d": EPS,
+                   "radius_clip": 3.0, "backward_mode": "primitive", "absgrad": True},
+    }
+    b_proj = proj_bytes(N_PROJ, i2, DET * DET)
+    result["proj"] = {"n_isects": i2, "algorithmic_bytes": b_proj,
+                      "hbm_frac": b_proj / t_proj / (HBM_PEAK_GBS * 1e9),
+                      "kernel_ms": {k: v * 1e3 for k, v in kb["seconds"].items()}}
+
+    # Dominant kernel and its roofline.
+    secs = kb["seconds"]
+    dom = max(secs, key=secs.get)
+    n_pix = DET * DET
+    dom_bytes = {
+        "rasterize_bwd": 76 * i2 + 4 * n_pix,   # key 8 + id 4 + payload 28 + partials 36
+        "rasterize_fwd": 32 * i2 + 4 * n_pix,   # id 4 + payload 28; image write
+        "binning_2d": 16 * N_PROJ + 12 * i2,
+        "project_fwd": 108 * N_PROJ,
+        "prepare": 76 * N_PROJ,
+    }[dom]
+    evals = 256 * i2
+    flops_per_eval = {"rasterize_fwd": 16, "rasterize_bwd": 40}.get(dom, 0)
+    result["roofline"] = {
+        "kernel": dom, "bound": "hbm",
+        "achieved": dom_bytes / secs[dom] / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": dom_bytes / secs[dom] / 1e9 / HBM_PEAK_GBS, "traffic": None,
+        "algorithmic_bytes": dom_bytes, "avg_launch_ms": secs[dom] * 1e3,
+        "valu": {"evaluations": evals, "flops_per_eval": flops_per_eval,
+                 "achieved_tflops": evals * flops_per_eval / secs[dom] / 1e12,
+                 "peak_tflops": FP32_VALU_PEAK_TFLOPS},
+    }
+
+    if not args.no_voxel:
+        log("building config-3 voxelization workload (200k Gaussians, 256^3)")
+        vox = Voxelization(dev)
+        t_vox = time_steps(vox.step, max(3, args.steps // 2), args.warmup)
+        m3, con, off, ids, fl, vol = vox.last
+        i3 = int(fl.numel())
+        n_vox = VOX_DIM ** 3
+        b_vox = vox_bytes(N_VOX, i3, n_vox)
+        t_vf = time_kernel(lambda: W.voxelize_to_voxels_fwd(m3, con, vox.opac, off, fl, VOX_DIM,
+                                                            VOX_DIM, VOX_DIM, 8), args.kernel_reps)
+        t_vb = time_kernel(lambda: W.voxelize_to_voxels_bwd_per_gaussian(
+            m3, con, vox.opac, off, ids, fl, vox.v_volume, VOX_DIM, VOX_DIM, VOX_DIM, 8),
+            args.kernel_reps)
+        result["voxelize"] = {
+            "workload": "config3 voxelization fwd+bwd", "n_gaussians": N_VOX, "grid": VOX_DIM,
+            "n_isects": i3, "ms_per_call": t_vox * 1e3,
+            "mvox_per_s": n_vox / t_vox / 1e6, "algorithmic_bytes": b_vox,
+            "hbm_frac": b_vox / t_vox / (HBM_PEAK_GBS * 1e9),
+            "kernel_ms": {"voxelize_fwd": t_vf * 1e3, "voxelize_bwd": t_vb * 1e3},
+            "voxelize_fwd_hbm_frac": (40 * i3 + 4 * n_vox) / t_vf / (HBM_PEAK_GBS * 1e9),
+        }
+        log(f"voxelization fwd+bwd: {t_vox * 1e3:.3f} ms/call, I3={i3}")
+
+    if not args.no_cpu_baseline:
+        log("timing the CPU oracle baseline")
+        cps, dt, sample = cpu_baseline(proj)
+        result["cpu_baseline"] = {"value": cps, "unit": "proj fwd+bwd calls/s", "cores": 1,
+                                  "kind": "port", "sample": sample, "sample_seconds": dt}
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()
