@@ -1,0 +1,70 @@
+"""The C ABI library on the CPU: it loads, exports every declared symbol,
+and rejects invalid arguments before touching any device."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from r2splat.cuda import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
+                      "r2splat_hip.h")
+
+
+def _declared():
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    return sorted(set(re.findall(r"\b(r2s_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    assert os.path.exists(_lib.LIB_PATH), "build the library first (python bt-3dgs_amd/build.py)"
+    return _lib.load()
+
+
+def test_exports_every_declared_symbol(lib):
+    declared = _declared()
+    assert len(declared) >= 40
+    for name in declared:
+        assert hasattr(lib, name), f"{name} missing from {_lib.LIB_PATH}"
+    assert sorted(_lib.SYMBOLS) == declared, "ctypes table and header disagree"
+    assert lib.r2s_abi_version() == _lib.ABI_VERSION
+
+
+def test_invalid_arguments_are_rejected_without_a_device(lib):
+    rc = lib.r2s_parameter_transform_fwd_f32(None, None, 5e-4, 1.0, None, None, -1, None)
+    assert rc == 1001
+    assert b"negative" in lib.r2s_last_error()
+    # Empty inputs are a no-op that succeeds.
+    assert lib.r2s_parameter_transform_fwd_f32(None, None, 5e-4, 1.0, None, None, 0, None) == 0
+    assert lib.r2s_last_error() == b""
+    rc = lib.r2s_world_to_image_projection_fwd_f32(None, None, None, None, 16, 16, 1e-8, 0.0,
+                                                   None, None, None, 1, 4, None)
+    assert rc == 1001 and b"radius_clip must be positive" in lib.r2s_last_error()
+    rc = lib.r2s_rasterize_fwd_f32(None, None, None, None, None, None, 0, 1, 1, 64, 64, 40, 2, 2,
+                                   None, None, 0, None)
+    assert rc == 1001 and b"tile_size" in lib.r2s_last_error()
+    rc = lib.r2s_isect_emit_sort_2d_f32(None, None, 1, 1, 10, 16, 4, 4, None, 1 << 31, 5, None,
+                                        None, None, 0, None)
+    assert rc == 1002  # beyond the int32 offset range
+    rc = lib.r2s_isect_emit_sort_2d_f32(None, None, 1, 1, 10, 16, 4, 4, None, 100, 3, None, None,
+                                        None, 0, None)
+    assert rc == 1001 and b"end_bit" in lib.r2s_last_error()
+    rc = lib.r2s_voxelize_fwd_f32(None, None, None, None, None, 0, 1, 8, 8, 8, 11, 1, 1, 1, None,
+                                  None)
+    assert rc == 1001 and b"tile_size" in lib.r2s_last_error()
+
+
+def test_workspace_queries(lib):
+    assert lib.r2s_isect_workspace_bytes(0, 0, 11) == 0
+    small = lib.r2s_isect_workspace_bytes(0, 1000, 11)
+    big = lib.r2s_isect_workspace_bytes(0, 10_000_000, 11)
+    assert 16 * 1000 <= small < big and big >= 16 * 10_000_000
+    assert lib.r2s_isect_workspace_bytes(500_000, 0, 0) > 0
+    assert lib.r2s_mask_workspace_bytes(1_000_000) > 0
+    buf = ctypes.create_string_buffer(16)
+    rc = lib.r2s_isect_emit_sort_2d_f32(None, None, 1, 1, 10, 16, 4, 4, None, 100, 5, buf, buf,
+                                        buf, 16, None)
+    assert rc in (1001, 1004)
