@@ -129,7 +129,7 @@ template <typename T>
 __global__ __launch_bounds__(256) void emit_2d_kernel(
     const T *__restrict__ means2d, const int32_t *__restrict__ radii, int rect, int64_t M,
     int64_t N, uint32_t ts, uint32_t tw, uint32_t th, const int64_t *__restrict__ offsets,
-    uint32_t *__restrict__ keys, uint32_t *__restrict__ vals) {
+    uint32_t *__restrict__ keys, uint32_t *__restrict__ vals, int32_t *__restrict__ emit_ids) {
   const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + (threadIdx.x & ~63u);
   const int64_t idx = wave_first + lane_id();
   Rect r = {0, 0, 0, 0};
@@ -154,7 +154,12 @@ __global__ __launch_bounds__(256) void emit_2d_kernel(
     for (uint32_t k = lane_id(); k < cj; k += 64) {
       const uint32_t row = k / wj, col = k - row * wj;
       keys[base + k] = kbase + (y0 + row) * tw + (x0 + col);
-      vals[base + k] = static_cast<uint32_t>(gid);
+      if (emit_ids != nullptr) {
+        vals[base + k] = static_cast<uint32_t>(base + k);
+        emit_ids[base + k] = static_cast<int32_t>(gid);
+      } else {
+        vals[base + k] = static_cast<uint32_t>(gid);
+      }
     }
   }
 }
@@ -163,7 +168,7 @@ template <typename T>
 __global__ __launch_bounds__(256) void emit_3d_kernel(
     const T *__restrict__ means3d, const int32_t *__restrict__ radii, int64_t N, uint32_t ts,
     uint32_t n2, uint32_t n1, uint32_t n0, const int64_t *__restrict__ offsets,
-    uint32_t *__restrict__ keys, uint32_t *__restrict__ vals) {
+    uint32_t *__restrict__ keys, uint32_t *__restrict__ vals, int32_t *__restrict__ emit_ids) {
   const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + (threadIdx.x & ~63u);
   const int64_t idx = wave_first + lane_id();
   const uint32_t n[3] = {n2, n1, n0};
@@ -193,7 +198,12 @@ __global__ __launch_bounds__(256) void emit_3d_kernel(
       const uint32_t t0 = k / plane, rem = k - t0 * plane;
       const uint32_t t1 = rem / e2j, t2 = rem - t1 * e2j;
       keys[base + k] = (l0 + t0) * (n1 * n2) + (l1 + t1) * n2 + (l2 + t2);
-      vals[base + k] = gid;
+      if (emit_ids != nullptr) {
+        vals[base + k] = static_cast<uint32_t>(base + k);
+        emit_ids[base + k] = static_cast<int32_t>(gid);
+      } else {
+        vals[base + k] = gid;
+      }
     }
   }
 }
@@ -229,7 +239,8 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     const uint32_t *__restrict__ keys_in, const uint32_t *__restrict__ vals_in, int64_t n,
     uint32_t shift, uint32_t bits, const uint32_t *__restrict__ digit_offsets, uint32_t nblocks,
     uint32_t *__restrict__ keys_out, uint32_t *__restrict__ vals_out,
-    int64_t *__restrict__ keys_out64, int32_t *__restrict__ vals_out32) {
+    int64_t *__restrict__ keys_out64, int32_t *__restrict__ vals_out32,
+    const int32_t *__restrict__ emit_ids, int32_t *__restrict__ src_out) {
   __shared__ uint32_t cnt[4][kRadix];
   __shared__ uint32_t wbase[4][kRadix];
   const uint32_t w = threadIdx.x / 64, lane = threadIdx.x % 64;
@@ -281,7 +292,12 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
                            wbase[w][d] + rank[r];
       if (kFinal) {
         keys_out64[dest] = static_cast<int64_t>(key[r]);
-        vals_out32[dest] = static_cast<int32_t>(val[r]);
+        if (emit_ids != nullptr) {  // val = emission index of the record
+          vals_out32[dest] = emit_ids[val[r]];
+          src_out[dest] = static_cast<int32_t>(val[r]);
+        } else {
+          vals_out32[dest] = static_cast<int32_t>(val[r]);
+        }
       } else {
         keys_out[dest] = key[r];
         vals_out[dest] = val[r];
@@ -341,11 +357,16 @@ int64_t sort_space_bytes(int64_t n) {
   return static_cast<int64_t>(cv.used);
 }
 
-// Sorts the emitted (keys, vals) held in s.ka / s.va into the final outputs.
-int radix_sort(SortSpace &s, int64_t n, uint32_t end_bit, int64_t *keys64, int32_t *vals32,
-               hipStream_t stream) {
+// Sorts the emitted (keys, vals) held in (kin0, vin0) into the final outputs;
+// intermediate passes ping-pong between s.kb/s.vb and s.ka/s.va.  With
+// emit_ids, vals are emission indices: the final pass writes
+// vals32[r] = emit_ids[val] and src[r] = val.
+int radix_sort(SortSpace &s, const uint32_t *kin0, const uint32_t *vin0, int64_t n,
+               uint32_t end_bit, int64_t *keys64, int32_t *vals32, const int32_t *emit_ids,
+               int32_t *src, hipStream_t stream) {
   const int passes = static_cast<int>((end_bit + kRadixBits - 1) / kRadixBits);
-  uint32_t *kin = s.ka, *vin = s.va, *kout = s.kb, *vout = s.vb;
+  const uint32_t *kin = kin0, *vin = vin0;
+  uint32_t *kout = s.kb, *vout = s.vb, *kalt = s.ka, *valt = s.va;
   const uint32_t nb = static_cast<uint32_t>(s.nblocks);
   for (int p = 0; p < passes; ++p) {
     const uint32_t shift = static_cast<uint32_t>(p * kRadixBits);
@@ -357,15 +378,18 @@ int radix_sort(SortSpace &s, int64_t n, uint32_t end_bit, int64_t *keys64, int32
                                                             "isect sort scan"));
     if (p == passes - 1) {
       radix_scatter_kernel<true><<<dim3(nb), dim3(kSortThreads), 0, stream>>>(
-          kin, vin, n, shift, bits, s.hist_scan, nb, nullptr, nullptr, keys64, vals32);
+          kin, vin, n, shift, bits, s.hist_scan, nb, nullptr, nullptr, keys64, vals32, emit_ids,
+          src);
     } else {
       radix_scatter_kernel<false><<<dim3(nb), dim3(kSortThreads), 0, stream>>>(
-          kin, vin, n, shift, bits, s.hist_scan, nb, kout, vout, nullptr, nullptr);
-      uint32_t *tk = kin, *tv = vin;
+          kin, vin, n, shift, bits, s.hist_scan, nb, kout, vout, nullptr, nullptr, nullptr,
+          nullptr);
       kin = kout;
       vin = vout;
-      kout = tk;
-      vout = tv;
+      kout = kalt;
+      vout = valt;
+      kalt = const_cast<uint32_t *>(kin);
+      valt = const_cast<uint32_t *>(vin);
     }
     R2S_RETURN_IF(check_launch("isect sort pass"));
   }
@@ -452,7 +476,8 @@ template <typename T>
 int emit_sort_2d_impl(const T *means2d, const int32_t *radii, int rect, int64_t C, int64_t N,
                       uint32_t ts, uint32_t tw, uint32_t th, const int64_t *offsets,
                       int64_t n_isects, uint32_t end_bit, int64_t *keys, int32_t *vals,
-                      void *ws, size_t ws_bytes, r2s_stream_t st) {
+                      int32_t *emit_ids, int32_t *isect_src, void *ws, size_t ws_bytes,
+                      r2s_stream_t st) {
   clear_error();
   const char *name = "isect_tiles";
   R2S_REQUIRE(C >= 0 && N >= 0 && C * N <= kInt32Max, "%s: bad size", name);
@@ -463,18 +488,21 @@ int emit_sort_2d_impl(const T *means2d, const int32_t *radii, int rect, int64_t 
   hipStream_t stream = as_stream(st);
   Carver cv(ws);
   SortSpace s = carve_sort(cv, n_isects);
+  R2S_REQUIRE((emit_ids == nullptr) == (isect_src == nullptr),
+              "%s: emit_ids and isect_src must be given together", name);
   const int64_t M = C * N;
   emit_2d_kernel<T><<<dim3(static_cast<uint32_t>(ceil_div(M, 256))), dim3(256), 0, stream>>>(
-      means2d, radii, rect, M, N, ts, tw, th, offsets, s.ka, s.va);
+      means2d, radii, rect, M, N, ts, tw, th, offsets, s.ka, s.va, emit_ids);
   R2S_RETURN_IF(check_launch(name));
-  return radix_sort(s, n_isects, end_bit, keys, vals, stream);
+  return radix_sort(s, s.ka, s.va, n_isects, end_bit, keys, vals, emit_ids, isect_src, stream);
 }
 
 template <typename T>
 int emit_sort_3d_impl(const T *means3d, const int32_t *radii, int64_t N, uint32_t ts,
                       uint32_t n2, uint32_t n1, uint32_t n0, const int64_t *offsets,
                       int64_t n_isects, uint32_t end_bit, int64_t *keys, int32_t *vals,
-                      void *ws, size_t ws_bytes, r2s_stream_t st) {
+                      int32_t *emit_ids, int32_t *isect_src, void *ws, size_t ws_bytes,
+                      r2s_stream_t st) {
   clear_error();
   const char *name = "isect_tiles_3d";
   R2S_REQUIRE(N >= 0 && N <= kInt32Max, "%s: bad size", name);
@@ -486,10 +514,12 @@ int emit_sort_3d_impl(const T *means3d, const int32_t *radii, int64_t N, uint32_
   hipStream_t stream = as_stream(st);
   Carver cv(ws);
   SortSpace s = carve_sort(cv, n_isects);
+  R2S_REQUIRE((emit_ids == nullptr) == (isect_src == nullptr),
+              "%s: emit_ids and isect_src must be given together", name);
   emit_3d_kernel<T><<<dim3(static_cast<uint32_t>(ceil_div(N, 256))), dim3(256), 0, stream>>>(
-      means3d, radii, N, ts, n2, n1, n0, offsets, s.ka, s.va);
+      means3d, radii, N, ts, n2, n1, n0, offsets, s.ka, s.va, emit_ids);
   R2S_RETURN_IF(check_launch(name));
-  return radix_sort(s, n_isects, end_bit, keys, vals, stream);
+  return radix_sort(s, s.ka, s.va, n_isects, end_bit, keys, vals, emit_ids, isect_src, stream);
 }
 
 }  // namespace
@@ -515,10 +545,12 @@ int64_t r2s_isect_workspace_bytes(int64_t n_items, int64_t n_isects, uint32_t en
   int r2s_isect_emit_sort_2d_##SUF(const T *means2d, const int32_t *radii, int rect,          \
                                    int64_t C, int64_t N, uint32_t ts, uint32_t tw,            \
                                    uint32_t th, const int64_t *offsets, int64_t n_isects,     \
-                                   uint32_t end_bit, int64_t *keys, int32_t *vals, void *ws,  \
+                                   uint32_t end_bit, int64_t *keys, int32_t *vals,            \
+                                   int32_t *emit_ids, int32_t *isect_src, void *ws,          \
                                    size_t ws_bytes, r2s_stream_t st) {                        \
     return r2s::emit_sort_2d_impl<T>(means2d, radii, rect, C, N, ts, tw, th, offsets,         \
-                                     n_isects, end_bit, keys, vals, ws, ws_bytes, st);        \
+                                     n_isects, end_bit, keys, vals, emit_ids, isect_src, ws,  \
+                                     ws_bytes, st);                                           \
   }                                                                                           \
   int r2s_isect_count_3d_##SUF(const T *means3d, const int32_t *radii, int64_t N,            \
                                uint32_t ts, uint32_t n2, uint32_t n1, uint32_t n0,            \
@@ -530,10 +562,12 @@ int64_t r2s_isect_workspace_bytes(int64_t n_items, int64_t n_isects, uint32_t en
   int r2s_isect_emit_sort_3d_##SUF(const T *means3d, const int32_t *radii, int64_t N,        \
                                    uint32_t ts, uint32_t n2, uint32_t n1, uint32_t n0,        \
                                    const int64_t *offsets, int64_t n_isects,                  \
-                                   uint32_t end_bit, int64_t *keys, int32_t *vals, void *ws,  \
+                                   uint32_t end_bit, int64_t *keys, int32_t *vals,            \
+                                   int32_t *emit_ids, int32_t *isect_src, void *ws,          \
                                    size_t ws_bytes, r2s_stream_t st) {                        \
     return r2s::emit_sort_3d_impl<T>(means3d, radii, N, ts, n2, n1, n0, offsets, n_isects,    \
-                                     end_bit, keys, vals, ws, ws_bytes, st);                  \
+                                     end_bit, keys, vals, emit_ids, isect_src, ws, ws_bytes,  \
+                                     st);                                                     \
   }
 
 R2S_BIN_API(f32, float)

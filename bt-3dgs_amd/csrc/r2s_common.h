@@ -84,6 +84,11 @@ __device__ __forceinline__ uint32_t mbcnt(uint64_t mask) {
 
 __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
 
+// Index of the calling wave in its workgroup, as a wave-uniform (scalar) value.
+__device__ __forceinline__ uint32_t wave_index() {
+  return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6)));
+}
+
 // Value of `v` in lane `src` (src must be wave-uniform).
 __device__ __forceinline__ uint32_t readlane_u32(uint32_t v, uint32_t src) {
   return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), static_cast<int>(src)));
@@ -116,5 +121,39 @@ __device__ __forceinline__ T wave_sum(T v) {
 // Hardware float atomics (no CAS loop; built with -munsafe-fp-atomics).
 __device__ __forceinline__ void atomic_add(float *p, float v) { unsafeAtomicAdd(p, v); }
 __device__ __forceinline__ void atomic_add(double *p, double v) { unsafeAtomicAdd(p, v); }
+
+// Segments of a wave: runs of equal `seg` over consecutive lanes.
+// suffix_sum(x) returns the sum of x over the caller's segment from the
+// caller onwards, so the first lane of a segment receives its total.
+struct WaveSegments {
+  uint32_t same;  // bit s set: lane + 2^s is in the caller's segment
+  __device__ __forceinline__ explicit WaveSegments(int32_t seg) : same(0) {
+    const uint32_t lane = lane_id();
+#pragma unroll
+    for (int s = 0; s < 6; ++s) {
+      const int32_t sy = __shfl_down(seg, 1 << s, 64);
+      if (lane + (1u << s) < 64u && sy == seg) same |= 1u << s;
+    }
+  }
+  template <typename T>
+  __device__ __forceinline__ T suffix_sum(T x) const {
+#pragma unroll
+    for (int s = 0; s < 6; ++s) {
+      const T y = __shfl_down(x, 1 << s, 64);
+      if ((same >> s) & 1u) x += y;
+    }
+    return x;
+  }
+};
+
+// Adds `v` to `out[i]` from the first lane of a segment: a plain
+// read-modify-write when this wave holds the whole segment, else an atomic.
+template <typename T>
+__device__ __forceinline__ void segment_store(T *out, int64_t i, T v, bool shared) {
+  if (shared)
+    atomic_add(out + i, v);
+  else
+    out[i] += v;
+}
 
 }  // namespace r2s

@@ -1,0 +1,158 @@
+// Analytic culling of Gaussian footprints for the rasterizer and voxelizer.
+//
+// A (pixel|voxel, Gaussian) pair contributes only if alpha = w exp(-sigma)
+// passes |alpha| >= thr with sigma >= 0, where sigma = 1/2 d^T P d.  For a
+// positive-definite P that can only happen inside the ellipsoid
+// sigma <= s*, s* = ln(|w| / thr).  These helpers walk that ellipsoid as
+// slices -> rows -> a segment along the contiguous axis, using the
+// completed-square forms
+//   2D: sigma = 1/2 a (x - xc(y))^2 + 1/2 (det / a) y^2,      xc = -(b / a) y
+//   3D: sigma = 1/2 p00 (x - xc(y, z))^2 + 1/2 a2 (y - yc(z))^2 + 1/2 c3 z^2
+// (a2, c3 Schur complements), whose terms are all non-negative, so the
+// remaining budget s - (terms so far) carries no cancellation error.  Every
+// range is conservative:
+//   * s* is enlarged by a relative 1e-3 and an absolute 1e-3;
+//   * every interval end is widened by kCullMargin (0.125) pixel/voxel.
+// Elements inside a range are still evaluated with the per-element test, so
+// culling only removes elements that cannot pass it.  Determinants and Schur
+// complements are computed in double.
+#pragma once
+
+#include "r2s_common.h"
+
+namespace r2s {
+
+constexpr double kCullMargin = 0.125;
+constexpr double kLog2e = 1.4426950408889634074;
+
+// 2^-x: one v_exp_f32 for float (the kernels pre-scale sigma by log2(e), so
+// exp(-sigma) = 2^-(sigma log2 e)); the library exp2 for double.
+__device__ __forceinline__ float neg_exp2(float x) { return __builtin_amdgcn_exp2f(-x); }
+__device__ __forceinline__ double neg_exp2(double x) { return exp2(-x); }
+
+// Keys of the records of a wave: `rb` is the wave's first record (uniform),
+// `r` the lane's; the key of record r is the last k with offsets[k] <= r
+// (offsets[0] = 0, non-decreasing).  One uniform binary search for rb, then a
+// uniform walk over the boundaries inside the wave's 64 records.
+__device__ __forceinline__ uint32_t wave_record_key(const int32_t *__restrict__ offsets,
+                                                    uint32_t n_keys, int64_t n_isects, int64_t rb,
+                                                    int64_t r) {
+  uint32_t lo = 0, hi = n_keys;
+  while (hi - lo > 1) {
+    const uint32_t mid = (lo + hi) >> 1;
+    if (static_cast<int64_t>(offsets[mid]) <= rb)
+      lo = mid;
+    else
+      hi = mid;
+  }
+  const int64_t r_last = min(rb + 63, n_isects - 1);
+  uint32_t key = lo;
+  for (uint32_t k = lo + 1; k < n_keys; ++k) {
+    const int64_t bnd = offsets[k];
+    if (bnd > r_last) break;
+    if (r >= bnd) key = k;
+  }
+  return key;
+}
+
+// Enlarged ln(|w| / thr); the float log is ample against the 1e-3 slack.
+__device__ __forceinline__ float sigma_bound(float w_abs, double thr) {
+  return (logf(w_abs) - static_cast<float>(log(thr))) * (1.0f + 1e-3f) + 1e-3f;
+}
+__device__ __forceinline__ double sigma_bound(double w_abs, double thr) {
+  return log(w_abs / thr) * (1.0 + 1e-3) + 1e-3;
+}
+
+// Integer indices j with (j + 0.5) in [c + lo, c + hi], clamped to [j0, j1].
+// Returns false when empty.  Inputs may be non-finite (empty or clamped).
+template <typename T>
+__device__ __forceinline__ bool index_range(T c, T lo, T hi, int j0, int j1, int &a, int &b) {
+  const T flo = ceil(c + lo - static_cast<T>(0.5 + kCullMargin));
+  const T fhi = floor(c + hi - static_cast<T>(0.5 - kCullMargin));
+  const T cl = fmax(flo, static_cast<T>(j0));
+  const T ch = fmin(fhi, static_cast<T>(j1));
+  if (!(cl <= ch)) return false;
+  a = static_cast<int>(cl);
+  b = static_cast<int>(ch);
+  return true;
+}
+
+// Indices j of [j0, j1] with (j + 0.5 - c - centre)^2 <= 2 budget / p, i.e.
+// the segment where 1/2 p (u - centre)^2 <= budget.
+template <typename T>
+__device__ __forceinline__ bool budget_range(T c, T centre, T budget, T inv_p, int j0, int j1,
+                                             int &a, int &b) {
+  if (!(budget >= static_cast<T>(0))) return false;
+  const T h = sqrt(static_cast<T>(2) * budget * inv_p);
+  return index_range<T>(c, centre - h, centre + h, j0, j1, a, b);
+}
+
+// 2D footprint of conic (a, b, c) = P for weight |w|.
+template <typename T>
+struct Cull2 {
+  bool ok;   // positive definite and finite: the analytic ranges apply
+  T s;       // sigma bound
+  T hy;      // half extent along y
+  T inv_a;   // 1 / a
+  T bx;      // x centre per unit y: xc = -bx y  (b / a)
+  T c2;      // det / a: row minimum 1/2 c2 y^2
+};
+
+template <typename T>
+__device__ __forceinline__ Cull2<T> cull2_setup(T a, T b, T c, T w_abs, double thr) {
+  Cull2<T> r;
+  const double da = a, db = b, dc = c;
+  const double det = da * dc - db * db;
+  r.ok = (da > 0.0) && (det > 0.0) && isfinite(det) && isfinite(da) &&
+         isfinite(static_cast<double>(w_abs));
+  r.s = r.hy = r.inv_a = r.bx = r.c2 = 0;
+  if (r.ok) {
+    const double s = static_cast<double>(sigma_bound(w_abs, thr));
+    r.s = static_cast<T>(s);
+    r.hy = static_cast<T>(s > 0.0 ? sqrt(2.0 * s * da / det) : 0.0);
+    r.inv_a = static_cast<T>(1.0 / da);
+    r.bx = static_cast<T>(db / da);
+    r.c2 = static_cast<T>(det / da);
+  }
+  return r;
+}
+
+// 3D footprint of the packed conic q = (p00, p01, p02, p11, p12, p22), axis 0
+// of the conic = x (contiguous), 1 = y, 2 = z.
+template <typename T>
+struct Cull3 {
+  bool ok;
+  T s;
+  T hz;          // half extent along z
+  T inv_p;       // 1 / p00
+  T a2, inv_a2;  // p11 - p01^2 / p00 and its inverse
+  T ky;          // y centre per unit z: yc = -ky z
+  T c3;          // det / (p00 a2): slice minimum 1/2 c3 z^2
+};
+
+template <typename T>
+__device__ __forceinline__ Cull3<T> cull3_setup(const T q[6], T w_abs, double thr) {
+  Cull3<T> r;
+  const double p00 = q[0], p01 = q[1], p02 = q[2], p11 = q[3], p12 = q[4], p22 = q[5];
+  const double m2 = p00 * p11 - p01 * p01;
+  const double det = p00 * (p11 * p22 - p12 * p12) - p01 * (p01 * p22 - p12 * p02) +
+                     p02 * (p01 * p12 - p11 * p02);
+  r.ok = (p00 > 0.0) && (m2 > 0.0) && (det > 0.0) && isfinite(det) && isfinite(m2) &&
+         isfinite(static_cast<double>(w_abs));
+  r.s = r.hz = r.inv_p = r.a2 = r.inv_a2 = r.ky = r.c3 = 0;
+  if (r.ok) {
+    const double s = static_cast<double>(sigma_bound(w_abs, thr));
+    const double a2 = m2 / p00;
+    const double k1 = p12 - p01 * p02 / p00;
+    r.s = static_cast<T>(s);
+    r.hz = static_cast<T>(s > 0.0 ? sqrt(2.0 * s * m2 / det) : 0.0);
+    r.inv_p = static_cast<T>(1.0 / p00);
+    r.a2 = static_cast<T>(a2);
+    r.inv_a2 = static_cast<T>(1.0 / a2);
+    r.ky = static_cast<T>(k1 / a2);
+    r.c3 = static_cast<T>(det / m2);
+  }
+  return r;
+}
+
+}  // namespace r2s

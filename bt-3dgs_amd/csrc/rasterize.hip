@@ -10,14 +10,20 @@
 // reference does.  Workgroups are XCD-swizzled so neighbouring tiles, which
 // share most of their Gaussians, run on the same L2.
 //
-// Backward: one lane per intersection record.  The lane walks the ts^2
-// pixels of its record's tile and accumulates the nine partials of that
-// Gaussian in registers -- no cross-lane reduction -- then issues one
-// hardware float atomic per partial.  Records of one tile are adjacent, so
-// the upstream-gradient loads of a wave hit the same cache lines.  The tile
-// of a record comes from isect_ids (per-Gaussian mode) or from a binary
-// search of tile_offsets (pixel mode); both modes compute the same sums.
+// Backward: one workgroup per (camera, tile) with the tile's upstream
+// gradient staged in LDS, one lane per record of the tile's list.  A lane
+// visits only the pixels that can pass the alpha test -- the rows of the
+// ellipse sigma <= ln(|o mu| / 1e-5) and the x-segment of each row
+// (r2s_cull.h) -- and accumulates, per row, the moments sum(w), sum(w dx),
+// sum(w dx^2) of w = v exp(-sigma) over passing pixels (plus the per-pixel
+// absolute mean gradients), folded into the nine partials once per row.
+// Then one hardware float atomic per partial.  Along a row sigma is
+// evaluated as (a dx / 2 + b dy) dx + c dy^2 / 2.  The two reference
+// backward variants (per pixel, per Gaussian) compute the same sums and
+// share this kernel.
 #include "r2s_common.h"
+#include "r2s_cull.h"
+#include "r2s_rows.h"
 #include "r2s_scan.h"
 
 namespace r2s {
@@ -38,6 +44,9 @@ struct Vec<double> {
 
 __device__ __forceinline__ float fast_exp(float x) { return __expf(x); }
 __device__ __forceinline__ double fast_exp(double x) { return exp(x); }
+
+constexpr double kThr2 = 1e-5;
+constexpr int kBwdThreads = 256;
 
 template <typename T>
 __global__ __launch_bounds__(1024) void raster_fwd_kernel(
@@ -65,7 +74,7 @@ __global__ __launch_bounds__(1024) void raster_fwd_kernel(
 
   const int64_t start = tile_offsets[key];
   const int64_t end = (key == n_keys - 1) ? n_isects : static_cast<int64_t>(tile_offsets[key + 1]);
-  const T thr = static_cast<T>(1e-5);
+  const T thr = static_cast<T>(kThr2);
   T acc = 0;
   for (int64_t b = start; b < end; b += bs) {
     __syncthreads();
@@ -99,93 +108,158 @@ __global__ __launch_bounds__(1024) void raster_fwd_kernel(
   if (inside) image[static_cast<int64_t>(cam) * H * W + static_cast<int64_t>(i) * W + j] = acc;
 }
 
-// Key of record r from the offsets: the last k with tile_offsets[k] <= r.
-__device__ __forceinline__ uint32_t key_of_record(const int32_t *__restrict__ offsets,
-                                                  uint32_t n_keys, int64_t r) {
-  uint32_t lo = 0, hi = n_keys;  // invariant: offsets[lo] <= r < offsets[hi] (hi virtual)
-  while (hi - lo > 1) {
-    const uint32_t mid = (lo + hi) >> 1;
-    if (static_cast<int64_t>(offsets[mid]) <= r)
-      lo = mid;
-    else
-      hi = mid;
-  }
-  return lo;
-}
+// One backward record in registers.
+template <typename T>
+struct RasterRecord {
+  bool live;          // a valid record whose pixels can pass the alpha test
+  T mx, my, a, b, c, o, mu, om;
+  T ha, hb, hc;       // a/2, b, c/2 pre-scaled by log2(e)
+  int i0, i1;         // rows the alpha-test ellipse reaches (all rows when not PD)
+};
 
 template <typename T>
-__global__ __launch_bounds__(256) void raster_bwd_kernel(
+__device__ __forceinline__ void load_raster_record(
+    const T *__restrict__ means2d, const T *__restrict__ conics, const T *__restrict__ opac,
+    const T *__restrict__ mus, int64_t g, int64_t n_items, bool in_list, int oy, int y1,
+    RasterRecord<T> &rec) {
+  rec.live = in_list && g >= 0 && g < n_items;
+  rec.o = rec.live ? opac[g] : static_cast<T>(0);
+  rec.mu = rec.live ? mus[g] : static_cast<T>(0);
+  rec.om = rec.o * rec.mu;
+  // |alpha| <= |o mu| for sigma >= 0: nothing passes (non-finite stays live).
+  if (fabs(rec.om) < static_cast<T>(kThr2)) rec.live = false;
+  if (!rec.live) {
+    rec.o = rec.mu = rec.om = 0;
+    rec.mx = rec.my = rec.a = rec.b = rec.c = rec.ha = rec.hb = rec.hc = 0;
+    rec.i0 = 0;
+    rec.i1 = -1;
+    return;
+  }
+  rec.mx = means2d[2 * g];
+  rec.my = means2d[2 * g + 1];
+  rec.a = conics[3 * g];
+  rec.b = conics[3 * g + 1];
+  rec.c = conics[3 * g + 2];
+  rec.ha = static_cast<T>(0.5 * kLog2e) * rec.a;
+  rec.hb = static_cast<T>(kLog2e) * rec.b;
+  rec.hc = static_cast<T>(0.5 * kLog2e) * rec.c;
+  const Cull2<T> cu = cull2_setup(rec.a, rec.b, rec.c, fabs(rec.om), kThr2);
+  rec.i0 = oy;
+  rec.i1 = y1;
+  if (cu.ok && !index_range<T>(rec.my, -cu.hy, cu.hy, oy, y1, rec.i0, rec.i1)) rec.live = false;
+}
+
+// Records in tile order (tile_offsets, flatten_ids; isect_ids optional), one
+// lane per record.  kRows = false: each record's nine partials go out
+// through global atomics.  kRows = true: they are stored as the row
+// isect_src[r] of `rows` (see r2s_rows.h), zeros included.
+template <typename T, int R, bool kAbs, bool kRows>
+__global__ __launch_bounds__(kBwdThreads) void raster_bwd_kernel(
     const T *__restrict__ means2d, const T *__restrict__ conics, const T *__restrict__ opac,
     const T *__restrict__ mus, const int32_t *__restrict__ tile_offsets,
     const int64_t *__restrict__ isect_ids, const int32_t *__restrict__ flatten_ids,
-    int64_t n_isects, uint32_t n_keys, int64_t n_items, const T *__restrict__ v_image,
-    uint32_t W, uint32_t H, uint32_t ts, uint32_t tw, uint32_t th, T *__restrict__ v_xy_abs,
-    T *__restrict__ v_xy, T *__restrict__ v_conic, T *__restrict__ v_opac,
-    T *__restrict__ v_mu) {
-  const int64_t r = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (r >= n_isects) return;
+    const int32_t *__restrict__ isect_src, int64_t n_isects, uint32_t n_keys, int64_t n_items,
+    const T *__restrict__ v_image, uint32_t W, uint32_t H, uint32_t ts, uint32_t tw,
+    uint32_t th, T *__restrict__ v_xy_abs, T *__restrict__ v_xy, T *__restrict__ v_conic,
+    T *__restrict__ v_opac, T *__restrict__ v_mu, T *__restrict__ rows) {
+  const int64_t rb = static_cast<int64_t>(blockIdx.x) * kBwdThreads + 64 * wave_index();
+  if (rb >= n_isects) return;  // uniform per wave
+  const int64_t r = rb + lane_id();
+  const bool in_list = r < n_isects;
   uint32_t key;
+  bool key_ok = in_list;
   if (isect_ids != nullptr) {
-    const int64_t k = isect_ids[r];
-    if (k < 0 || k >= static_cast<int64_t>(n_keys)) return;
-    key = static_cast<uint32_t>(k);
+    const int64_t k = in_list ? isect_ids[r] : 0;
+    key_ok = key_ok && k >= 0 && k < static_cast<int64_t>(n_keys);
+    key = key_ok ? static_cast<uint32_t>(k) : 0u;
   } else {
-    key = key_of_record(tile_offsets, n_keys, r);
+    key = wave_record_key(tile_offsets, n_keys, n_isects, rb, r);
   }
-  const int64_t g = flatten_ids[r];
-  if (g < 0 || g >= n_items) return;
+  const int64_t g = key_ok ? static_cast<int64_t>(flatten_ids[r]) : -1;
   const uint32_t n_tiles = tw * th;
   const uint32_t cam = key / n_tiles, t = key - cam * n_tiles;
   const uint32_t ty = t / tw, tx = t - ty * tw;
-  const uint32_t ox = tx * ts, oy = ty * ts;
+  const int ox = static_cast<int>(tx * ts), oy = static_cast<int>(ty * ts);
+  const int nx = static_cast<int>(min(ts, W - tx * ts));
+  const int ny = static_cast<int>(min(ts, H - ty * ts));
   const T *__restrict__ vimg = v_image + static_cast<int64_t>(cam) * H * W;
-
-  const T mx = means2d[2 * g], my = means2d[2 * g + 1];
-  const T a = conics[3 * g], b = conics[3 * g + 1], c = conics[3 * g + 2];
-  const T o = opac[g], mu = mus[g];
-  const T om = o * mu;
-  const T thr = static_cast<T>(1e-5), half = static_cast<T>(0.5);
-  // Pixel centres are exact in T: (ox + lx) + 0.5 == (ox + 0.5) + lx.
-  const T fx0 = static_cast<T>(ox) + half, fy0 = static_cast<T>(oy) + half;
-
-  T ax = 0, ay = 0, aax = 0, aay = 0, ca = 0, cb = 0, cc = 0, ao = 0, am = 0;
-  for (uint32_t ly = 0; ly < ts; ++ly) {
-    const uint32_t i = oy + ly;
-    if (i >= H) break;
-    const T dy = (fy0 + static_cast<T>(ly)) - my;
-    const T *__restrict__ vrow = vimg + static_cast<int64_t>(i) * W;
-#pragma unroll 4
-    for (uint32_t lx = 0; lx < ts; ++lx) {
-      const uint32_t jx = ox + lx;
-      if (jx >= W) break;
-      const T dx = (fx0 + static_cast<T>(lx)) - mx;
-      const T sigma = half * (a * dx * dx + c * dy * dy) + b * dx * dy;
-      const T vis_raw = fast_exp(-sigma);
-      const T alpha_raw = om * vis_raw;
-      const bool valid = !((sigma < static_cast<T>(0)) || (fabs(alpha_raw) < thr));
-      const T vis = valid ? vis_raw : static_cast<T>(0);
-      const T alpha = valid ? alpha_raw : static_cast<T>(0);
-      const T v = vrow[jx];
-      const T v_sigma = -v * alpha;
-      const T gx = -v_sigma * (a * dx + b * dy);
-      const T gy = -v_sigma * (c * dy + b * dx);
-      ax += gx;
-      ay += gy;
-      aax += fabs(gx);
-      aay += fabs(gy);
-      ca += v_sigma * half * dx * dx;
-      cb += v_sigma * dx * dy;
-      cc += v_sigma * half * dy * dy;
-      ao += v * mu * vis;
-      am += v * o * vis;
+  RasterRecord<T> rec;
+  load_raster_record(means2d, conics, opac, mus, g, n_items, key_ok, oy, oy + ny - 1, rec);
+  const T thr = static_cast<T>(kThr2), half = static_cast<T>(0.5);
+  const T px0 = static_cast<T>(ox) + half;
+  // T_k = sum over rows of s_k = sum(w dx^k); Y0 = sum dy s0, Y1 = sum dy s1,
+  // YY = sum dy^2 s0; PX, PY = sums of |w (P d)_x|, |w (P d)_y|.
+  T T0 = 0, T1 = 0, T2 = 0, Y0 = 0, Y1 = 0, YY = 0, PX = 0, PY = 0;
+  if (ballot(rec.live) != 0) {
+    for (int ly = 0; ly < R; ++ly) {
+      if (ly >= static_cast<int>(ts)) break;
+      const int i = oy + ly;
+      const bool in_row = rec.live && i >= rec.i0 && i <= rec.i1;
+      if (ballot(in_row) == 0) continue;
+      const T dy = (static_cast<T>(i) + half) - rec.my;
+      const T B = rec.hb * dy, C = rec.hc * dy * dy;
+      const T bdy = rec.b * dy, cdy = rec.c * dy;
+      const T *__restrict__ vrow = vimg + static_cast<int64_t>(in_row ? i : 0) * W + ox;
+      T s0 = 0, s1 = 0, s2 = 0, px = 0, py = 0;
+#pragma unroll
+      for (int k = 0; k < R; ++k) {
+        if (k >= static_cast<int>(ts)) break;
+        const bool here = in_row && k < nx;
+        const T v = here ? vrow[k] : static_cast<T>(0);
+        const T dx = (px0 + static_cast<T>(k)) - rec.mx;
+        const T sl = (rec.ha * dx + B) * dx + C;
+        const T e = neg_exp2(sl);
+        const bool skip = !here || (sl < static_cast<T>(0)) || (fabs(rec.om * e) < thr);
+        const T w = skip ? static_cast<T>(0) : v * e;
+        s0 += w;
+        const T wx = w * dx;
+        s1 += wx;
+        s2 += wx * dx;
+        if (kAbs) {
+          px += fabs(w * (rec.a * dx + bdy));
+          py += fabs(w * (rec.b * dx + cdy));
+        }
+      }
+      T0 += s0;
+      T1 += s1;
+      T2 += s2;
+      const T dys0 = dy * s0;
+      Y0 += dys0;
+      YY += dy * dys0;
+      Y1 += dy * s1;
+      if (kAbs) {
+        PX += px;
+        PY += py;
+      }
     }
   }
+  if (!key_ok) return;
+  // Per-pixel terms of RasterizeToPixelsBwd.cu summed over the tile, with
+  // v_sigma = -v alpha, d sigma / d mean = -(P d) and
+  // d sigma / d conic = (dx^2 / 2, dx dy, dy^2 / 2).  Zero for dead records.
+  const T om = rec.om;
+  const T ax = om * (rec.a * T1 + rec.b * Y0);
+  const T ay = om * (rec.c * Y0 + rec.b * T1);
+  const T ca = -half * om * T2, cb = -om * Y1, cc = -half * om * YY;
+  const T ao = rec.mu * T0, am = rec.o * T0;
+  const T aax = fabs(om) * PX, aay = fabs(om) * PY;
+  if (kRows) {
+    if (kAbs) {
+      const T v[9] = {ax, ay, ca, cb, cc, ao, am, aax, aay};
+      store_row(rows, isect_src[r], v);
+    } else {
+      const T v[7] = {ax, ay, ca, cb, cc, ao, am};
+      store_row(rows, isect_src[r], v);
+    }
+    return;
+  }
+  if (!rec.live) return;
   if (ax == 0 && ay == 0 && aax == 0 && aay == 0 && ca == 0 && cb == 0 && cc == 0 && ao == 0 &&
       am == 0)
     return;  // nothing to add
   atomic_add(v_xy + 2 * g, ax);
   atomic_add(v_xy + 2 * g + 1, ay);
-  if (v_xy_abs != nullptr) {
+  if (kAbs) {
     atomic_add(v_xy_abs + 2 * g, aax);
     atomic_add(v_xy_abs + 2 * g + 1, aay);
   }
@@ -234,24 +308,90 @@ int raster_fwd_impl(const T *means2d, const T *conics, const T *opac, const T *m
   return check_launch(name);
 }
 
+template <typename T, int R>
+void launch_raster_bwd(const T *means2d, const T *conics, const T *opac, const T *mus,
+                       const int32_t *tile_offsets, const int64_t *isect_ids,
+                       const int32_t *flatten_ids, const int32_t *isect_src, int64_t n_isects,
+                       uint32_t n_keys, int64_t n_items, const T *v_image, uint32_t W,
+                       uint32_t H, uint32_t ts, uint32_t tw, uint32_t th, T *v_xy_abs, T *v_xy,
+                       T *v_conic, T *v_opac, T *v_mu, T *rows, hipStream_t stream) {
+  const dim3 grid(static_cast<uint32_t>(ceil_div(n_isects, kBwdThreads)));
+  const dim3 block(kBwdThreads);
+#define R2S_RASTER_BWD_LAUNCH(ABS, ROWS)                                                         \
+  raster_bwd_kernel<T, R, ABS, ROWS><<<grid, block, 0, stream>>>(                              \
+      means2d, conics, opac, mus, tile_offsets, isect_ids, flatten_ids, isect_src, n_isects,     \
+      n_keys, n_items, v_image, W, H, ts, tw, th, v_xy_abs, v_xy, v_conic, v_opac, v_mu, rows)
+  if (v_xy_abs != nullptr) {
+    if (rows != nullptr)
+      R2S_RASTER_BWD_LAUNCH(true, true);
+    else
+      R2S_RASTER_BWD_LAUNCH(true, false);
+  } else {
+    if (rows != nullptr)
+      R2S_RASTER_BWD_LAUNCH(false, true);
+    else
+      R2S_RASTER_BWD_LAUNCH(false, false);
+  }
+#undef R2S_RASTER_BWD_LAUNCH
+}
+
+int64_t raster_rows_bytes(int64_t n_isects, int dtype_bytes) {
+  return n_isects * kRowStride * static_cast<int64_t>(dtype_bytes);
+}
+
+// emit_ids / isect_src / ws non-null: the two-pass form (r2s_rows.h).
 template <typename T>
 int raster_bwd_impl(const T *means2d, const T *conics, const T *opac, const T *mus,
                     const int32_t *tile_offsets, const int64_t *isect_ids,
-                    const int32_t *flatten_ids, int64_t n_isects, const T *v_image, int64_t C,
+                    const int32_t *flatten_ids, const int32_t *emit_ids,
+                    const int32_t *isect_src, int64_t n_isects, const T *v_image, int64_t C,
                     int64_t N, uint32_t W, uint32_t H, uint32_t ts, uint32_t tw, uint32_t th,
-                    T *v_xy_abs, T *v_xy, T *v_conic, T *v_opac, T *v_mu, r2s_stream_t st) {
+                    T *v_xy_abs, T *v_xy, T *v_conic, T *v_opac, T *v_mu, void *ws,
+                    size_t ws_bytes, bool two_pass, r2s_stream_t st) {
   clear_error();
-  const char *name = isect_ids ? "rasterize_to_pixels_bwd_per_gaussian" : "rasterize_to_pixels_bwd";
+  const char *name = two_pass   ? "rasterize_to_pixels_bwd (two-pass)"
+                     : isect_ids ? "rasterize_to_pixels_bwd_per_gaussian"
+                                 : "rasterize_to_pixels_bwd";
   R2S_RETURN_IF(check_raster_args(n_isects, C, N, W, H, ts, tw, th, name));
   if (C * N == 0 || n_isects == 0) return R2S_OK;
-  R2S_REQUIRE(means2d && conics && opac && mus && tile_offsets && flatten_ids && v_image &&
-                  v_xy && v_conic && v_opac && v_mu,
+  R2S_REQUIRE(tile_offsets && flatten_ids, "%s: null tile lists", name);
+  R2S_REQUIRE(means2d && conics && opac && mus && v_image && v_xy && v_conic && v_opac && v_mu,
               "%s: null pointer", name);
+  T *rows = nullptr;
+  if (two_pass) {
+    R2S_REQUIRE(emit_ids && isect_src, "%s: null emit_ids / isect_src", name);
+    const int64_t need = raster_rows_bytes(n_isects, sizeof(T));
+    if (ws == nullptr || static_cast<int64_t>(ws_bytes) < need) {
+      set_error("%s: workspace of %zu bytes, %lld required", name, ws_bytes, (long long)need);
+      return R2S_EWORKSPACE;
+    }
+    rows = static_cast<T *>(ws);
+  }
   const uint32_t n_keys = static_cast<uint32_t>(C) * tw * th;
-  raster_bwd_kernel<T><<<dim3(static_cast<uint32_t>(ceil_div(n_isects, 256))), dim3(256), 0,
-                         as_stream(st)>>>(means2d, conics, opac, mus, tile_offsets, isect_ids,
-                                          flatten_ids, n_isects, n_keys, C * N, v_image, W, H,
-                                          ts, tw, th, v_xy_abs, v_xy, v_conic, v_opac, v_mu);
+  hipStream_t stream = as_stream(st);
+#define R2S_RASTER_BWD_R(RR)                                                                     \
+  launch_raster_bwd<T, RR>(means2d, conics, opac, mus, tile_offsets, isect_ids, flatten_ids,     \
+                           isect_src, n_isects, n_keys, C * N, v_image, W, H, ts, tw, th,        \
+                           v_xy_abs, v_xy, v_conic, v_opac, v_mu, rows, stream)
+  if (ts <= 8)
+    R2S_RASTER_BWD_R(8);
+  else if (ts <= 16)
+    R2S_RASTER_BWD_R(16);
+  else
+    R2S_RASTER_BWD_R(32);
+#undef R2S_RASTER_BWD_R
+  R2S_RETURN_IF(check_launch(name));
+  if (!two_pass) return R2S_OK;
+  if (v_xy_abs != nullptr) {
+    RowTargets<T, 9> tg = {{v_xy, v_xy + 1, v_conic, v_conic + 1, v_conic + 2, v_opac, v_mu,
+                            v_xy_abs, v_xy_abs + 1},
+                           {2, 2, 3, 3, 3, 1, 1, 2, 2}};
+    launch_row_reduce(rows, emit_ids, n_isects, C * N, tg, stream);
+  } else {
+    RowTargets<T, 7> tg = {{v_xy, v_xy + 1, v_conic, v_conic + 1, v_conic + 2, v_opac, v_mu},
+                           {2, 2, 3, 3, 3, 1, 1}};
+    launch_row_reduce(rows, emit_ids, n_isects, C * N, tg, stream);
+  }
   return check_launch(name);
 }
 
@@ -259,6 +399,11 @@ int raster_bwd_impl(const T *means2d, const T *conics, const T *opac, const T *m
 }  // namespace r2s
 
 extern "C" {
+
+int64_t r2s_rasterize_bwd_workspace_bytes(int64_t n_isects, int dtype_bytes) {
+  if (n_isects <= 0 || (dtype_bytes != 4 && dtype_bytes != 8)) return 0;
+  return r2s::raster_rows_bytes(n_isects, dtype_bytes);
+}
 
 int64_t r2s_rasterize_workspace_bytes(int64_t n_keys, int64_t n_isects, uint32_t tile_size,
                                       int dtype_bytes) {
@@ -287,8 +432,21 @@ int64_t r2s_rasterize_workspace_bytes(int64_t n_keys, int64_t n_isects, uint32_t
                               uint32_t tw, uint32_t th, T *v_xy_abs, T *v_xy, T *v_conic,     \
                               T *v_opac, T *v_mu, r2s_stream_t st) {                          \
     return r2s::raster_bwd_impl<T>(means2d, conics, opac, mus, tile_offsets, isect_ids,       \
-                                   flatten_ids, n_isects, v_image, C, N, W, H, ts, tw, th,    \
-                                   v_xy_abs, v_xy, v_conic, v_opac, v_mu, st);                \
+                                   flatten_ids, nullptr, nullptr, n_isects, v_image, C, N, W, \
+                                   H, ts, tw, th, v_xy_abs, v_xy, v_conic, v_opac, v_mu,      \
+                                   nullptr, 0, false, st);                                    \
+  }                                                                                           \
+  int r2s_rasterize_bwd_emit_##SUF(                                                           \
+      const T *means2d, const T *conics, const T *opac, const T *mus,                         \
+      const int32_t *tile_offsets, const int64_t *isect_ids, const int32_t *flatten_ids,      \
+      const int32_t *emit_ids, const int32_t *isect_src, int64_t n_isects, const T *v_image,  \
+      int64_t C, int64_t N, uint32_t W, uint32_t H, uint32_t ts, uint32_t tw, uint32_t th,    \
+      T *v_xy_abs, T *v_xy, T *v_conic, T *v_opac, T *v_mu, void *ws, size_t ws_bytes,        \
+      r2s_stream_t st) {                                                                      \
+    return r2s::raster_bwd_impl<T>(means2d, conics, opac, mus, tile_offsets, isect_ids,       \
+                                   flatten_ids, emit_ids, isect_src, n_isects, v_image, C, N, \
+                                   W, H, ts, tw, th, v_xy_abs, v_xy, v_conic, v_opac, v_mu,   \
+                                   ws, ws_bytes, true, st);                                   \
   }
 
 R2S_RASTER_API(f32, float)

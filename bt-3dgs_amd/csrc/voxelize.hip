@@ -3,19 +3,40 @@
 // and |alpha| < 1e-6 (r2splat/cuda/csrc/VoxelizeToVoxelsFwd.cu:69-221), and
 // its VJP (VoxelizeToVoxelsBwd.cu:71-441).
 //
-// Forward: one workgroup per brick, one voxel per thread with the lane index
-// running along dim2 (the contiguous axis) so stores are coalesced -- the
-// reference maps threadIdx.x to dim0.  Gaussians are staged in LDS in
-// batches ({mean, opacity}, {c00..c11}, {c12, c22}), read as broadcasts;
-// each voxel sums in list order.
+// sigma is evaluated along x-rows of a brick: with dy, dz fixed per row,
+//   sigma log2(e) = (h0 dx + B) dx + C,  h0 = p00 log2(e) / 2,
+// two FMAs per voxel and one v_exp_f32 for exp(-sigma) = 2^-(sigma log2 e).
 //
-// Backward: one lane per intersection record walking the ts^3 voxels of its
-// brick with the ten partials in registers, then ten hardware float atomics.
+// Forward: one workgroup per brick; each thread owns R consecutive voxels of
+// one x-row (R = ts for ts = 8, 16; R = 1 otherwise) and sums the brick's list
+// in list order, as the reference does, so the result is deterministic.
+// Records are staged in LDS in batches with their conics pre-scaled and read
+// as broadcasts.
+//
+// Backward: one lane per record of the sorted list, so a wave takes 64
+// consecutive records (nearly always of one brick) and the work is balanced
+// whatever the list lengths.  All lanes walk the brick-local rows together,
+// skipping every slice and row that no lane's alpha-test ellipsoid reaches
+// (r2s_cull.h, wave ballots); a lane loads the upstream-gradient row of its
+// own brick (lanes of one brick share the cache lines).  Per row a lane accumulates
+// the moments s_k = sum(w dx^k), k = 0..2, of w = v exp(-sigma) over passing
+// voxels, and per record the ten sums
+//   T_k = sum s_k,  Y0 = sum dy s0, Z0 = sum dz s0, Y1 = sum dy s1,
+//   Z1 = sum dz s1, YY = sum dy^2 s0, YZ = sum dy dz s0, ZZ = sum dz^2 s0,
+// from which the ten partials follow; then ten hardware float atomics.
+// The two reference backward variants (per voxel, per Gaussian) compute the
+// same sums and share this kernel.
 #include "r2s_common.h"
+#include "r2s_cull.h"
+#include "r2s_rows.h"
 #include "r2s_scan.h"
 
 namespace r2s {
 namespace {
+
+constexpr double kThr3 = 1e-6;
+constexpr int kBwdThreads = 256;
+constexpr uint32_t kFwdBatch = 256;
 
 template <typename T>
 struct Vec;
@@ -30,162 +51,280 @@ struct Vec<double> {
   using v4 = double4;
 };
 
-__device__ __forceinline__ float fast_exp(float x) { return __expf(x); }
-__device__ __forceinline__ double fast_exp(double x) { return exp(x); }
+struct Brick {
+  int oi, oj, ok;  // origin (dim0, dim1, dim2)
+  int ni, nj, nk;  // extent inside the volume
+};
 
+__device__ __forceinline__ Brick brick_of(uint32_t key, uint32_t n2, uint32_t n1, uint32_t ts,
+                                          uint32_t D2, uint32_t D1, uint32_t D0) {
+  const uint32_t b0 = key / (n1 * n2), rem = key - b0 * (n1 * n2);
+  const uint32_t b1 = rem / n2, b2 = rem - b1 * n2;
+  Brick b;
+  b.oi = static_cast<int>(b0 * ts);
+  b.oj = static_cast<int>(b1 * ts);
+  b.ok = static_cast<int>(b2 * ts);
+  b.ni = static_cast<int>(min(ts, D0 - b0 * ts));
+  b.nj = static_cast<int>(min(ts, D1 - b1 * ts));
+  b.nk = static_cast<int>(min(ts, D2 - b2 * ts));
+  return b;
+}
+
+// Pre-scaled conic: sigma log2(e) = (h0 dx + h1 dy + h2 dz) dx
+//                                  + (h3 dy + h4 dz) dy + h5 dz^2.
 template <typename T>
+__device__ __forceinline__ void scaled_conic(const T q[6], T h[6]) {
+  const T l = static_cast<T>(kLog2e), hl = static_cast<T>(0.5 * kLog2e);
+  h[0] = hl * q[0];
+  h[1] = l * q[1];
+  h[2] = l * q[2];
+  h[3] = hl * q[3];
+  h[4] = l * q[4];
+  h[5] = hl * q[5];
+}
+
+template <typename T, int R>
 __global__ __launch_bounds__(1024) void voxel_fwd_kernel(
     const T *__restrict__ means3d, const T *__restrict__ conics, const T *__restrict__ opac,
     const int32_t *__restrict__ tile_offsets, const int32_t *__restrict__ flatten_ids,
-    int64_t n_isects, uint32_t n_keys, uint32_t D2, uint32_t D1, uint32_t D0, uint32_t ts,
-    uint32_t n2, uint32_t n1, T *__restrict__ volume) {
+    int64_t n_isects, uint32_t n_keys, int64_t N, uint32_t D2, uint32_t D1, uint32_t D0,
+    uint32_t ts, uint32_t n2, uint32_t n1, T *__restrict__ volume) {
   using V2 = typename Vec<T>::v2;
   using V4 = typename Vec<T>::v4;
   extern __shared__ double smem_raw[];
-  const uint32_t bs = ts * ts * ts;
-  V4 *s_mo = reinterpret_cast<V4 *>(smem_raw);
-  V4 *s_c0 = s_mo + bs;
-  V2 *s_c1 = reinterpret_cast<V2 *>(s_c0 + bs);
+  const uint32_t nt = blockDim.x;
+  const uint32_t nb = min(nt, kFwdBatch);            // records staged per batch
+  V4 *s_mo = reinterpret_cast<V4 *>(smem_raw);  // {mx, my, mz, o}
+  V4 *s_h0 = s_mo + nb;                           // {h0, h1, h2, h3}
+  V2 *s_h1 = reinterpret_cast<V2 *>(s_h0 + nb);   // {h4, h5}
 
   const uint32_t key = xcd_swizzle(blockIdx.x, n_keys);
-  const uint32_t b0 = key / (n1 * n2), rem = key - b0 * (n1 * n2);
-  const uint32_t b1 = rem / n2, b2 = rem - b1 * n2;
-  const uint32_t tr = threadIdx.x;
-  const uint32_t lk = tr % ts, lj = (tr / ts) % ts, li = tr / (ts * ts);
-  const uint32_t i = b0 * ts + li, j = b1 * ts + lj, k = b2 * ts + lk;
-  const bool inside = (i < D0) && (j < D1) && (k < D2);
-  const T px = static_cast<T>(k) + static_cast<T>(0.5);
-  const T py = static_cast<T>(j) + static_cast<T>(0.5);
-  const T pz = static_cast<T>(i) + static_cast<T>(0.5);
+  const Brick b = brick_of(key, n2, n1, ts, D2, D1, D0);
+  const uint32_t tid = threadIdx.x;
+  const uint32_t per_row = ts / R;
+  const int lk0 = static_cast<int>((tid % per_row) * R);
+  const int lj = static_cast<int>((tid / per_row) % ts);
+  const int li = static_cast<int>(tid / (per_row * ts));
+  const T half = static_cast<T>(0.5);
+  const T py = static_cast<T>(b.oj + lj) + half;
+  const T pz = static_cast<T>(b.oi + li) + half;
+  const T px0 = static_cast<T>(b.ok + lk0) + half;
 
   const int64_t start = tile_offsets[key];
   const int64_t end = (key == n_keys - 1) ? n_isects : static_cast<int64_t>(tile_offsets[key + 1]);
-  const T thr = static_cast<T>(1e-6), half = static_cast<T>(0.5);
-  T acc = 0;
-  for (int64_t b = start; b < end; b += bs) {
+  const T thr = static_cast<T>(kThr3);
+  T acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0;
+  for (int64_t base = start; base < end; base += nb) {
     __syncthreads();
-    const int64_t idx = b + tr;
-    if (idx < end) {
-      const int64_t g = flatten_ids[idx];
-      V4 mo;
-      mo.x = means3d[3 * g];
-      mo.y = means3d[3 * g + 1];
-      mo.z = means3d[3 * g + 2];
-      mo.w = opac[g];
-      s_mo[tr] = mo;
-      const T *q = conics + 6 * g;
-      V4 c0;
-      c0.x = q[0];
-      c0.y = q[1];
-      c0.z = q[2];
-      c0.w = q[3];
-      s_c0[tr] = c0;
-      V2 c1;
-      c1.x = q[4];
-      c1.y = q[5];
-      s_c1[tr] = c1;
+    const int64_t idx = base + tid;
+    if (tid < nb && idx < end) {
+      int64_t g = flatten_ids[idx];
+      V4 mo, h0;
+      V2 h1;
+      if (g >= 0 && g < N) {
+        T q[6], h[6];
+#pragma unroll
+        for (int c = 0; c < 6; ++c) q[c] = conics[6 * g + c];
+        scaled_conic(q, h);
+        mo.x = means3d[3 * g];
+        mo.y = means3d[3 * g + 1];
+        mo.z = means3d[3 * g + 2];
+        mo.w = opac[g];
+        h0.x = h[0];
+        h0.y = h[1];
+        h0.z = h[2];
+        h0.w = h[3];
+        h1.x = h[4];
+        h1.y = h[5];
+      } else {  // never passes: alpha = 0
+        mo.x = mo.y = mo.z = mo.w = 0;
+        h0.x = h0.y = h0.z = h0.w = 0;
+        h1.x = h1.y = 0;
+      }
+      s_mo[tid] = mo;
+      s_h0[tid] = h0;
+      s_h1[tid] = h1;
     }
     __syncthreads();
-    const int cnt = static_cast<int>(min(static_cast<int64_t>(bs), end - b));
-    if (inside) {
-#pragma unroll 2
-      for (int t = 0; t < cnt; ++t) {
-        const V4 mo = s_mo[t];
-        const V4 c0 = s_c0[t];
-        const V2 c1 = s_c1[t];
-        const T dx = px - mo.x, dy = py - mo.y, dz = pz - mo.z;
-        const T sigma = half * (c0.x * dx * dx + c0.w * dy * dy + c1.y * dz * dz) +
-                        c0.y * dx * dy + c0.z * dx * dz + c1.x * dy * dz;
-        const T alpha = mo.w * fast_exp(-sigma);
-        const bool skip = (sigma < static_cast<T>(0)) || (fabs(alpha) < thr);
-        acc += skip ? static_cast<T>(0) : alpha;
+    const int cnt = static_cast<int>(min(static_cast<int64_t>(nb), end - base));
+    for (int t = 0; t < cnt; ++t) {
+      const V4 mo = s_mo[t];
+      const V4 h0 = s_h0[t];
+      const V2 h1 = s_h1[t];
+      const T dy = py - mo.y, dz = pz - mo.z;
+      const T B = h0.y * dy + h0.z * dz;
+      const T C = (h0.w * dy + h1.x * dz) * dy + h1.y * dz * dz;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const T dx = (px0 + static_cast<T>(r)) - mo.x;
+        const T sl = (h0.x * dx + B) * dx + C;
+        const T alpha = mo.w * neg_exp2(sl);
+        acc[r] += ((sl < static_cast<T>(0)) || (fabs(alpha) < thr)) ? static_cast<T>(0) : alpha;
       }
     }
   }
-  if (inside)
-    volume[static_cast<int64_t>(i) * D1 * D2 + static_cast<int64_t>(j) * D2 + k] = acc;
+  if (li < b.ni && lj < b.nj) {
+    T *out = volume + static_cast<int64_t>(b.oi + li) * D1 * D2 +
+             static_cast<int64_t>(b.oj + lj) * D2 + (b.ok + lk0);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (lk0 + r < b.nk) out[r] = acc[r];
+  }
 }
 
-__device__ __forceinline__ uint32_t key_of_record(const int32_t *__restrict__ offsets,
-                                                  uint32_t n_keys, int64_t r) {
-  uint32_t lo = 0, hi = n_keys;
-  while (hi - lo > 1) {
-    const uint32_t mid = (lo + hi) >> 1;
-    if (static_cast<int64_t>(offsets[mid]) <= r)
-      lo = mid;
-    else
-      hi = mid;
-  }
-  return lo;
-}
+// One backward record in registers.
+template <typename T>
+struct BwdRecord {
+  bool live;     // a valid record whose voxels can pass the alpha test
+  T m[3], q[6], h[6], o;
+  Cull3<T> cu;
+  int i0, i1;    // slice range (all slices when !cu.ok)
+};
 
 template <typename T>
-__global__ __launch_bounds__(256) void voxel_bwd_kernel(
+__device__ __forceinline__ void load_bwd_record(const T *__restrict__ means3d,
+                                                const T *__restrict__ conics,
+                                                const T *__restrict__ opac, int64_t g, int64_t N,
+                                                bool in_list, const Brick &b, BwdRecord<T> &rec) {
+  rec.live = in_list && g >= 0 && g < N;
+  rec.o = rec.live ? opac[g] : static_cast<T>(0);
+  // |alpha| <= |o| for sigma >= 0: nothing passes (non-finite o stays live).
+  if (fabs(rec.o) < static_cast<T>(kThr3)) rec.live = false;
+  if (!rec.live) {
+    rec.o = 0;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) rec.m[c] = 0;
+#pragma unroll
+    for (int c = 0; c < 6; ++c) rec.q[c] = rec.h[c] = 0;
+    rec.cu.ok = false;
+    rec.i0 = 0;
+    rec.i1 = -1;
+    return;
+  }
+#pragma unroll
+  for (int c = 0; c < 3; ++c) rec.m[c] = means3d[3 * g + c];
+#pragma unroll
+  for (int c = 0; c < 6; ++c) rec.q[c] = conics[6 * g + c];
+  scaled_conic(rec.q, rec.h);
+  rec.cu = cull3_setup(rec.q, fabs(rec.o), kThr3);
+  rec.i0 = b.oi;
+  rec.i1 = b.oi + b.ni - 1;
+  if (rec.cu.ok &&
+      !index_range<T>(rec.m[2], -rec.cu.hz, rec.cu.hz, b.oi, b.oi + b.ni - 1, rec.i0, rec.i1))
+    rec.live = false;
+}
+
+// Records in brick order (tile_offsets, flatten_ids; isect_ids optional),
+// one lane per record.  kRows = false: each record's ten partials go out
+// through global atomics.  kRows = true: they are stored as the row
+// isect_src[r] of `rows` (see r2s_rows.h), zeros included.
+template <typename T, int R, bool kRows>
+__global__ __launch_bounds__(kBwdThreads) void voxel_bwd_kernel(
     const T *__restrict__ means3d, const T *__restrict__ conics, const T *__restrict__ opac,
     const int32_t *__restrict__ tile_offsets, const int64_t *__restrict__ isect_ids,
-    const int32_t *__restrict__ flatten_ids, int64_t n_isects, uint32_t n_keys, int64_t N,
-    const T *__restrict__ v_vol, uint32_t D2, uint32_t D1, uint32_t D0, uint32_t ts,
-    uint32_t n2, uint32_t n1, T *__restrict__ v_means, T *__restrict__ v_conics,
-    T *__restrict__ v_opac) {
-  const int64_t r = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (r >= n_isects) return;
+    const int32_t *__restrict__ flatten_ids, const int32_t *__restrict__ isect_src,
+    int64_t n_isects, uint32_t n_keys, int64_t N, const T *__restrict__ v_vol, uint32_t D2,
+    uint32_t D1, uint32_t D0, uint32_t ts, uint32_t n2, uint32_t n1, T *__restrict__ v_means,
+    T *__restrict__ v_conics, T *__restrict__ v_opac, T *__restrict__ rows) {
+  const int64_t rb = static_cast<int64_t>(blockIdx.x) * kBwdThreads + 64 * wave_index();
+  if (rb >= n_isects) return;  // uniform per wave
+  const int64_t r = rb + lane_id();
+  const bool in_list = r < n_isects;
   uint32_t key;
+  bool key_ok = in_list;
   if (isect_ids != nullptr) {
-    const int64_t kk = isect_ids[r];
-    if (kk < 0 || kk >= static_cast<int64_t>(n_keys)) return;
-    key = static_cast<uint32_t>(kk);
+    const int64_t k = in_list ? isect_ids[r] : 0;
+    key_ok = key_ok && k >= 0 && k < static_cast<int64_t>(n_keys);
+    key = key_ok ? static_cast<uint32_t>(k) : 0u;
   } else {
-    key = key_of_record(tile_offsets, n_keys, r);
+    key = wave_record_key(tile_offsets, n_keys, n_isects, rb, r);
   }
-  const int64_t g = flatten_ids[r];
-  if (g < 0 || g >= N) return;
-  const uint32_t b0 = key / (n1 * n2), rem = key - b0 * (n1 * n2);
-  const uint32_t b1 = rem / n2, b2 = rem - b1 * n2;
-  const uint32_t oi = b0 * ts, oj = b1 * ts, ok = b2 * ts;
-  const T mx = means3d[3 * g], my = means3d[3 * g + 1], mz = means3d[3 * g + 2];
-  const T *q = conics + 6 * g;
-  const T a = q[0], p = q[1], qq = q[2], bb = q[3], rr = q[4], cz = q[5];
-  const T o = opac[g];
-  const T half = static_cast<T>(0.5), thr = static_cast<T>(1e-6);
-  const T fx0 = static_cast<T>(ok) + half, fy0 = static_cast<T>(oj) + half,
-          fz0 = static_cast<T>(oi) + half;
-  T gx = 0, gy = 0, gz = 0, g0 = 0, g1 = 0, g2 = 0, g3 = 0, g4 = 0, g5 = 0, go = 0;
-  for (uint32_t li = 0; li < ts; ++li) {
-    const uint32_t i = oi + li;
-    if (i >= D0) break;
-    const T d3 = (fz0 + static_cast<T>(li)) - mz;
-    for (uint32_t lj = 0; lj < ts; ++lj) {
-      const uint32_t j = oj + lj;
-      if (j >= D1) break;
-      const T d2 = (fy0 + static_cast<T>(lj)) - my;
-      const T *__restrict__ vrow =
-          v_vol + static_cast<int64_t>(i) * D1 * D2 + static_cast<int64_t>(j) * D2;
-#pragma unroll 4
-      for (uint32_t lk = 0; lk < ts; ++lk) {
-        const uint32_t kx = ok + lk;
-        if (kx >= D2) break;
-        const T d1 = (fx0 + static_cast<T>(lk)) - mx;
-        const T sigma = half * (a * d1 * d1 + bb * d2 * d2 + cz * d3 * d3) + p * d1 * d2 +
-                        qq * d1 * d3 + rr * d2 * d3;
-        const T vis_raw = fast_exp(-sigma);
-        const bool valid = !((sigma < static_cast<T>(0)) || (fabs(o * vis_raw) < thr));
-        const T vis = valid ? vis_raw : static_cast<T>(0);
-        const T v = vrow[kx];
-        const T v_sigma = -v * o * vis;
-        const T oI = o * vis;
-        go += v * vis;
-        g0 += v_sigma * half * d1 * d1;
-        g1 += v_sigma * d1 * d2;
-        g2 += v_sigma * d1 * d3;
-        g3 += v_sigma * half * d2 * d2;
-        g4 += v_sigma * d2 * d3;
-        g5 += v_sigma * half * d3 * d3;
-        gx += v * oI * (a * d1 + p * d2 + qq * d3);
-        gy += v * oI * (bb * d2 + p * d1 + rr * d3);
-        gz += v * oI * (cz * d3 + qq * d1 + rr * d2);
+  const int64_t g = key_ok ? static_cast<int64_t>(flatten_ids[r]) : -1;
+  const Brick b = brick_of(key, n2, n1, ts, D2, D1, D0);
+  BwdRecord<T> rec;
+  load_bwd_record(means3d, conics, opac, g, N, key_ok, b, rec);
+  const T thr = static_cast<T>(kThr3), half = static_cast<T>(0.5);
+  const T px0 = static_cast<T>(b.ok) + half;
+  const int64_t plane = static_cast<int64_t>(D1) * D2;
+  T T0 = 0, T1 = 0, T2 = 0, Y0 = 0, Z0 = 0, Y1 = 0, Z1 = 0, YY = 0, YZ = 0, ZZ = 0;
+  if (ballot(rec.live) != 0) {
+    for (int li = 0; li < R; ++li) {
+      if (li >= static_cast<int>(ts)) break;
+      const int i = b.oi + li;
+      const bool in_slice = rec.live && i >= rec.i0 && i <= rec.i1;
+      if (ballot(in_slice) == 0) continue;
+      const T dz = (static_cast<T>(i) + half) - rec.m[2];
+      // Rows of this slice the lane's ellipsoid can reach.
+      int j0 = b.oj, j1 = b.oj + b.nj - 1;
+      if (!in_slice) {
+        j1 = j0 - 1;
+      } else if (rec.cu.ok) {
+        const T bud_z = rec.cu.s - half * rec.cu.c3 * dz * dz;
+        if (!budget_range<T>(rec.m[1], -rec.cu.ky * dz, bud_z, rec.cu.inv_a2, b.oj,
+                             b.oj + b.nj - 1, j0, j1))
+          j1 = j0 - 1;
+      }
+      const T h4dz = rec.h[4] * dz, h5dzz = rec.h[5] * dz * dz, Bz = rec.h[2] * dz;
+      for (int lj = 0; lj < R; ++lj) {
+        if (lj >= static_cast<int>(ts)) break;
+        const int j = b.oj + lj;
+        const bool in_row = j >= j0 && j <= j1;
+        if (ballot(in_row) == 0) continue;
+        const T dy = (static_cast<T>(j) + half) - rec.m[1];
+        const T B = rec.h[1] * dy + Bz;
+        const T C = (rec.h[3] * dy + h4dz) * dy + h5dzz;
+        const T *__restrict__ vrow =
+            v_vol +
+            (in_row ? static_cast<int64_t>(i) * plane + static_cast<int64_t>(j) * D2 : 0) + b.ok;
+        T s0 = 0, s1 = 0, s2 = 0;
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+          if (k >= static_cast<int>(ts)) break;
+          const bool here = in_row && k < b.nk;
+          const T v = here ? vrow[k] : static_cast<T>(0);
+          const T dx = (px0 + static_cast<T>(k)) - rec.m[0];
+          const T sl = (rec.h[0] * dx + B) * dx + C;
+          const T e = neg_exp2(sl);
+          const bool skip = !here || (sl < static_cast<T>(0)) || (fabs(rec.o * e) < thr);
+          const T w = skip ? static_cast<T>(0) : v * e;
+          s0 += w;
+          const T wx = w * dx;
+          s1 += wx;
+          s2 += wx * dx;
+        }
+        T0 += s0;
+        T1 += s1;
+        T2 += s2;
+        const T dys0 = dy * s0, dzs0 = dz * s0;
+        Y0 += dys0;
+        Z0 += dzs0;
+        YY += dy * dys0;
+        YZ += dz * dys0;
+        ZZ += dz * dzs0;
+        Y1 += dy * s1;
+        Z1 += dz * s1;
       }
     }
   }
+  if (!key_ok) return;
+  // Per-voxel terms of VoxelizeToVoxelsBwd.cu:409-421 summed over the brick
+  // (zero for dead records).
+  const T o = rec.o;
+  const T *q = rec.q;
+  const T gx = o * (q[0] * T1 + q[1] * Y0 + q[2] * Z0);
+  const T gy = o * (q[3] * Y0 + q[4] * Z0 + q[1] * T1);
+  const T gz = o * (q[5] * Z0 + q[4] * Y0 + q[2] * T1);
+  const T g0 = -half * o * T2, g1 = -o * Y1, g2 = -o * Z1;
+  const T g3 = -half * o * YY, g4 = -o * YZ, g5 = -half * o * ZZ;
+  const T go = T0;
+  if (kRows) {
+    const T v[10] = {gx, gy, gz, g0, g1, g2, g3, g4, g5, go};
+    store_row(rows, isect_src[r], v);
+    return;
+  }
+  if (!rec.live) return;
   if (gx == 0 && gy == 0 && gz == 0 && g0 == 0 && g1 == 0 && g2 == 0 && g3 == 0 && g4 == 0 &&
       g5 == 0 && go == 0)
     return;
@@ -210,8 +349,25 @@ int check_voxel_args(int64_t n_isects, int64_t N, uint32_t D2, uint32_t D1, uint
   R2S_REQUIRE(static_cast<uint64_t>(n2) * ts >= D2 && static_cast<uint64_t>(n1) * ts >= D1 &&
                   static_cast<uint64_t>(n0) * ts >= D0,
               "%s: brick grid does not cover the volume", name);
-  R2S_REQUIRE(static_cast<uint64_t>(n2) * n1 * n0 <= 0xffffffffull, "%s: too many bricks", name);
+  R2S_REQUIRE(static_cast<uint64_t>(n2) * ts <= 0x7fffffffull &&
+                  static_cast<uint64_t>(n1) * ts <= 0x7fffffffull &&
+                  static_cast<uint64_t>(n0) * ts <= 0x7fffffffull,
+              "%s: brick grid too large", name);
+  R2S_REQUIRE(static_cast<uint64_t>(n2) * n1 * n0 <= 0x7fffffffull, "%s: too many bricks", name);
   return R2S_OK;
+}
+
+template <typename T, int R>
+void launch_voxel_fwd(const T *means3d, const T *conics, const T *opac,
+                      const int32_t *tile_offsets, const int32_t *flatten_ids, int64_t n_isects,
+                      uint32_t n_keys, int64_t N, uint32_t D2, uint32_t D1, uint32_t D0,
+                      uint32_t ts, uint32_t n2, uint32_t n1, T *volume, hipStream_t stream) {
+  const uint32_t nt = ts * ts * (ts / R);
+  const size_t smem =
+      min(nt, kFwdBatch) * (2 * sizeof(typename Vec<T>::v4) + sizeof(typename Vec<T>::v2));
+  voxel_fwd_kernel<T, R><<<dim3(n_keys), dim3(nt), smem, stream>>>(
+      means3d, conics, opac, tile_offsets, flatten_ids, n_isects, n_keys, N, D2, D1, D0, ts, n2,
+      n1, volume);
 }
 
 template <typename T>
@@ -229,32 +385,89 @@ int voxel_fwd_impl(const T *means3d, const T *conics, const T *opac,
   if (N == 0 || n_isects == 0) return device_fill<T>(volume, n_vox, static_cast<T>(0), stream, name);
   R2S_REQUIRE(means3d && conics && opac && tile_offsets && flatten_ids, "%s: null pointer", name);
   const uint32_t n_keys = n2 * n1 * n0;
-  const uint32_t bs = ts * ts * ts;
-  const size_t smem = 2 * bs * sizeof(typename Vec<T>::v4) + bs * sizeof(typename Vec<T>::v2);
-  voxel_fwd_kernel<T><<<dim3(n_keys), dim3(bs), smem, stream>>>(
-      means3d, conics, opac, tile_offsets, flatten_ids, n_isects, n_keys, D2, D1, D0, ts, n2, n1,
-      volume);
+  if (ts == 8)
+    launch_voxel_fwd<T, 8>(means3d, conics, opac, tile_offsets, flatten_ids, n_isects, n_keys, N,
+                           D2, D1, D0, ts, n2, n1, volume, stream);
+  else if (ts == 16)
+    launch_voxel_fwd<T, 16>(means3d, conics, opac, tile_offsets, flatten_ids, n_isects, n_keys,
+                            N, D2, D1, D0, ts, n2, n1, volume, stream);
+  else
+    launch_voxel_fwd<T, 1>(means3d, conics, opac, tile_offsets, flatten_ids, n_isects, n_keys, N,
+                           D2, D1, D0, ts, n2, n1, volume, stream);
   return check_launch(name);
 }
 
+template <typename T, int R>
+void launch_voxel_bwd(const T *means3d, const T *conics, const T *opac,
+                      const int32_t *tile_offsets, const int64_t *isect_ids,
+                      const int32_t *flatten_ids, const int32_t *isect_src, int64_t n_isects,
+                      uint32_t n_keys, int64_t N, const T *v_vol, uint32_t D2, uint32_t D1,
+                      uint32_t D0, uint32_t ts, uint32_t n2, uint32_t n1, T *v_means,
+                      T *v_conics, T *v_opac, T *rows, hipStream_t stream) {
+  const dim3 grid(static_cast<uint32_t>(ceil_div(n_isects, kBwdThreads)));
+  if (rows != nullptr)
+    voxel_bwd_kernel<T, R, true><<<grid, dim3(kBwdThreads), 0, stream>>>(
+        means3d, conics, opac, tile_offsets, isect_ids, flatten_ids, isect_src, n_isects, n_keys,
+        N, v_vol, D2, D1, D0, ts, n2, n1, v_means, v_conics, v_opac, rows);
+  else
+    voxel_bwd_kernel<T, R, false><<<grid, dim3(kBwdThreads), 0, stream>>>(
+        means3d, conics, opac, tile_offsets, isect_ids, flatten_ids, isect_src, n_isects, n_keys,
+        N, v_vol, D2, D1, D0, ts, n2, n1, v_means, v_conics, v_opac, rows);
+}
+
+int64_t voxel_rows_bytes(int64_t n_isects, int dtype_bytes) {
+  return n_isects * kRowStride * static_cast<int64_t>(dtype_bytes);
+}
+
+// two_pass: emit_ids / isect_src / ws give the two-pass form (r2s_rows.h).
 template <typename T>
 int voxel_bwd_impl(const T *means3d, const T *conics, const T *opac,
                    const int32_t *tile_offsets, const int64_t *isect_ids,
-                   const int32_t *flatten_ids, int64_t n_isects, const T *v_vol, int64_t N,
+                   const int32_t *flatten_ids, const int32_t *emit_ids,
+                   const int32_t *isect_src, int64_t n_isects, const T *v_vol, int64_t N,
                    uint32_t D2, uint32_t D1, uint32_t D0, uint32_t ts, uint32_t n2, uint32_t n1,
-                   uint32_t n0, T *v_means, T *v_conics, T *v_opac, r2s_stream_t st) {
+                   uint32_t n0, T *v_means, T *v_conics, T *v_opac, void *ws, size_t ws_bytes,
+                   bool two_pass, r2s_stream_t st) {
   clear_error();
-  const char *name = isect_ids ? "voxelize_to_voxels_bwd_per_gaussian" : "voxelize_to_voxels_bwd";
+  const char *name = two_pass   ? "voxelize_to_voxels_bwd (two-pass)"
+                     : isect_ids ? "voxelize_to_voxels_bwd_per_gaussian"
+                                 : "voxelize_to_voxels_bwd";
   R2S_RETURN_IF(check_voxel_args(n_isects, N, D2, D1, D0, ts, n2, n1, n0, name));
   if (N == 0 || n_isects == 0) return R2S_OK;
-  R2S_REQUIRE(means3d && conics && opac && tile_offsets && flatten_ids && v_vol && v_means &&
-                  v_conics && v_opac,
+  const int64_t n_vox = static_cast<int64_t>(D2) * D1 * D0;
+  if (n_vox == 0) return R2S_OK;
+  R2S_REQUIRE(tile_offsets && flatten_ids, "%s: null brick lists", name);
+  R2S_REQUIRE(means3d && conics && opac && v_vol && v_means && v_conics && v_opac,
               "%s: null pointer", name);
+  T *rows = nullptr;
+  if (two_pass) {
+    R2S_REQUIRE(emit_ids && isect_src, "%s: null emit_ids / isect_src", name);
+    const int64_t need = voxel_rows_bytes(n_isects, sizeof(T));
+    if (ws == nullptr || static_cast<int64_t>(ws_bytes) < need) {
+      set_error("%s: workspace of %zu bytes, %lld required", name, ws_bytes, (long long)need);
+      return R2S_EWORKSPACE;
+    }
+    rows = static_cast<T *>(ws);
+  }
   const uint32_t n_keys = n2 * n1 * n0;
-  voxel_bwd_kernel<T><<<dim3(static_cast<uint32_t>(ceil_div(n_isects, 256))), dim3(256), 0,
-                        as_stream(st)>>>(means3d, conics, opac, tile_offsets, isect_ids,
-                                         flatten_ids, n_isects, n_keys, N, v_vol, D2, D1, D0, ts,
-                                         n2, n1, v_means, v_conics, v_opac);
+  hipStream_t stream = as_stream(st);
+#define R2S_VOXEL_BWD_R(RR)                                                                    \
+  launch_voxel_bwd<T, RR>(means3d, conics, opac, tile_offsets, isect_ids, flatten_ids,         \
+                          isect_src, n_isects, n_keys, N, v_vol, D2, D1, D0, ts, n2, n1,       \
+                          v_means, v_conics, v_opac, rows, stream)
+  if (ts <= 4)
+    R2S_VOXEL_BWD_R(4);
+  else if (ts <= 8)
+    R2S_VOXEL_BWD_R(8);
+  else
+    R2S_VOXEL_BWD_R(16);
+#undef R2S_VOXEL_BWD_R
+  R2S_RETURN_IF(check_launch(name));
+  if (!two_pass) return R2S_OK;
+  RowTargets<T, 10> tg = {{v_means, v_means + 1, v_means + 2, v_conics, v_conics + 1,
+                           v_conics + 2, v_conics + 3, v_conics + 4, v_conics + 5, v_opac},
+                          {3, 3, 3, 6, 6, 6, 6, 6, 6, 1}};
+  launch_row_reduce(rows, emit_ids, n_isects, N, tg, stream);
   return check_launch(name);
 }
 
@@ -262,6 +475,11 @@ int voxel_bwd_impl(const T *means3d, const T *conics, const T *opac,
 }  // namespace r2s
 
 extern "C" {
+
+int64_t r2s_voxelize_bwd_workspace_bytes(int64_t n_isects, int dtype_bytes) {
+  if (n_isects <= 0 || (dtype_bytes != 4 && dtype_bytes != 8)) return 0;
+  return r2s::voxel_rows_bytes(n_isects, dtype_bytes);
+}
 
 #define R2S_VOXEL_API(SUF, T)                                                                  \
   int r2s_voxelize_fwd_##SUF(const T *means3d, const T *conics, const T *opac,                 \
@@ -279,8 +497,18 @@ extern "C" {
                              uint32_t n2, uint32_t n1, uint32_t n0, T *v_means, T *v_conics,   \
                              T *v_opac, r2s_stream_t st) {                                     \
     return r2s::voxel_bwd_impl<T>(means3d, conics, opac, tile_offsets, isect_ids, flatten_ids, \
-                                  n_isects, v_vol, N, D2, D1, D0, ts, n2, n1, n0, v_means,     \
-                                  v_conics, v_opac, st);                                       \
+                                  nullptr, nullptr, n_isects, v_vol, N, D2, D1, D0, ts, n2,    \
+                                  n1, n0, v_means, v_conics, v_opac, nullptr, 0, false, st);   \
+  }                                                                                            \
+  int r2s_voxelize_bwd_emit_##SUF(                                                             \
+      const T *means3d, const T *conics, const T *opac, const int32_t *tile_offsets,           \
+      const int64_t *isect_ids, const int32_t *flatten_ids, const int32_t *emit_ids,           \
+      const int32_t *isect_src, int64_t n_isects, const T *v_vol, int64_t N, uint32_t D2,      \
+      uint32_t D1, uint32_t D0, uint32_t ts, uint32_t n2, uint32_t n1, uint32_t n0,            \
+      T *v_means, T *v_conics, T *v_opac, void *ws, size_t ws_bytes, r2s_stream_t st) {        \
+    return r2s::voxel_bwd_impl<T>(means3d, conics, opac, tile_offsets, isect_ids, flatten_ids, \
+                                  emit_ids, isect_src, n_isects, v_vol, N, D2, D1, D0, ts, n2, \
+                                  n1, n0, v_means, v_conics, v_opac, ws, ws_bytes, true, st);  \
   }
 
 R2S_VOXEL_API(f32, float)

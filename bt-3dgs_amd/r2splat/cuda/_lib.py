@@ -35,14 +35,16 @@ _FLOAT_OPS = {
                               _i64, _i64, _p],
     "isect_count_2d": [_p, _p, _i32, _i64, _i64, _u32, _u32, _u32, _p, _p, _p, _sz, _p],
     "isect_emit_sort_2d": [_p, _p, _i32, _i64, _i64, _u32, _u32, _u32, _p, _i64, _u32, _p, _p,
-                           _p, _sz, _p],
+                           _p, _p, _p, _sz, _p],
     "isect_count_3d": [_p, _p, _i64, _u32, _u32, _u32, _u32, _p, _p, _p, _sz, _p],
     "isect_emit_sort_3d": [_p, _p, _i64, _u32, _u32, _u32, _u32, _p, _i64, _u32, _p, _p, _p,
-                           _sz, _p],
+                           _p, _p, _sz, _p],
     "rasterize_fwd": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _u32, _u32, _u32, _u32, _u32,
                       _p, _p, _sz, _p],
     "rasterize_bwd": [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _u32, _u32, _u32, _u32,
                       _u32, _p, _p, _p, _p, _p, _p],
+    "rasterize_bwd_emit": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _u32, _u32,
+                           _u32, _u32, _u32, _p, _p, _p, _p, _p, _p, _sz, _p],
     "world_to_volume_mapping_fwd": [_p, _p, _p, _p, _u32, _u32, _u32, _f64, _f64, _p, _p, _p,
                                     _i64, _p],
     "world_to_volume_mapping_bwd": [_p, _p, _p, _p, _u32, _u32, _u32, _f64, _p, _p, _p, _p,
@@ -51,6 +53,8 @@ _FLOAT_OPS = {
                      _p, _p],
     "voxelize_bwd": [_p, _p, _p, _p, _p, _p, _i64, _p, _i64, _u32, _u32, _u32, _u32, _u32, _u32,
                      _u32, _p, _p, _p, _p],
+    "voxelize_bwd_emit": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _u32, _u32, _u32, _u32,
+                          _u32, _u32, _u32, _p, _p, _p, _p, _sz, _p],
 }
 
 _PLAIN = {
@@ -59,13 +63,15 @@ _PLAIN = {
     "r2s_isect_workspace_bytes": (_i64, [_i64, _i64, _u32]),
     "r2s_isect_offset_encode": (_i32, [_p, _i64, _i64, _p, _p]),
     "r2s_rasterize_workspace_bytes": (_i64, [_i64, _i64, _u32, _i32]),
+    "r2s_rasterize_bwd_workspace_bytes": (_i64, [_i64, _i32]),
+    "r2s_voxelize_bwd_workspace_bytes": (_i64, [_i64, _i32]),
     "r2s_mask_workspace_bytes": (_i64, [_i64]),
     "r2s_mask_split": (_i32, [_p, _i64, _p, _p, _p, _sz, _p]),
 }
 
 SYMBOLS = sorted(list(_PLAIN) + [f"r2s_{n}_{s}" for n in _FLOAT_OPS for s in ("f32", "f64")])
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 def load(path: str = LIB_PATH) -> ctypes.CDLL:

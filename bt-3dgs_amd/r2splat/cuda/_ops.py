@@ -73,6 +73,35 @@ def _end_bit(n_keys: int) -> int:
     return int(math.ceil(math.log2(float(n_keys + 1))))
 
 
+# The binning ops also describe their records in emission order (id-major,
+# before the sort by tile) on the flatten_ids tensor they return: emit_ids[e]
+# is the id of emitted record e, isect_src[r] the emission index of sorted
+# record r.  The backward ops then run the two-pass kernels, which store each
+# record's partials at its emission index and sum them per Gaussian, instead
+# of one device-scope atomic per record and partial.  Any other flatten_ids
+# (built elsewhere, or modified in place since) takes the one-pass kernels.
+USE_EMISSION_ORDER = True
+_EMIT_ATTR = "_r2s_emission_order"
+
+
+def _keep_emission_order(flatten_ids: Tensor, emit_ids: Tensor, isect_src: Tensor,
+                         n_keys: int) -> None:
+    setattr(flatten_ids, _EMIT_ATTR, (emit_ids, isect_src, flatten_ids._version, int(n_keys)))
+
+
+def _emission_order(flatten_ids: Tensor, n_keys: int):
+    """(emit_ids, isect_src) kept by the binning op for this flatten_ids, or None."""
+    if not USE_EMISSION_ORDER:
+        return None
+    rec = getattr(flatten_ids, _EMIT_ATTR, None)
+    if rec is None:
+        return None
+    ids, src, version, nk = rec
+    if version != flatten_ids._version or nk != int(n_keys) or ids.numel() != flatten_ids.numel():
+        return None
+    return ids, src
+
+
 # ------------------------------------------------------ parameter transform --
 
 def parameter_transform_fwd(quats: Tensor, scale_ori: Tensor, scale_min: float,
@@ -388,10 +417,13 @@ def isect_tiles(means2d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim1: in
         end_bit = _end_bit(C * tw * th)
         isect_ids = torch.empty((n_isects,), dtype=torch.int64, device=dev)
         flatten_ids = torch.empty((n_isects,), dtype=torch.int32, device=dev)
+        emit_ids = torch.empty((n_isects,), dtype=torch.int32, device=dev)
+        isect_src = torch.empty((n_isects,), dtype=torch.int32, device=dev)
         ws = _workspace(lib.r2s_isect_workspace_bytes(0, n_isects, end_bit), dev)
         _call(f"r2s_isect_emit_sort_2d_{sfx}", _ptr(means2d), _ptr(radii), rect, C, N, ts, tw,
               th, _ptr(offsets), n_isects, end_bit, _ptr(isect_ids), _ptr(flatten_ids),
-              _ptr(ws), ws.numel(), st)
+              _ptr(emit_ids), _ptr(isect_src), _ptr(ws), ws.numel(), st)
+    _keep_emission_order(flatten_ids, emit_ids, isect_src, C * tw * th)
     return tiles_per_gauss, isect_ids, flatten_ids
 
 
@@ -444,10 +476,13 @@ def isect_tiles_3d(means3d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim2:
         end_bit = _end_bit(n2 * n1 * n0)
         isect_ids = torch.empty((n_isects,), dtype=torch.int64, device=dev)
         flatten_ids = torch.empty((n_isects,), dtype=torch.int32, device=dev)
+        emit_ids = torch.empty((n_isects,), dtype=torch.int32, device=dev)
+        isect_src = torch.empty((n_isects,), dtype=torch.int32, device=dev)
         ws = _workspace(lib.r2s_isect_workspace_bytes(0, n_isects, end_bit), dev)
         _call(f"r2s_isect_emit_sort_3d_{sfx}", _ptr(means3d), _ptr(radii), N, ts, n2, n1, n0,
-              _ptr(offsets), n_isects, end_bit, _ptr(isect_ids), _ptr(flatten_ids), _ptr(ws),
-              ws.numel(), st)
+              _ptr(offsets), n_isects, end_bit, _ptr(isect_ids), _ptr(flatten_ids),
+              _ptr(emit_ids), _ptr(isect_src), _ptr(ws), ws.numel(), st)
+    _keep_emission_order(flatten_ids, emit_ids, isect_src, n2 * n1 * n0)
     return tiles_per_gauss, isect_ids, flatten_ids
 
 
@@ -531,11 +566,21 @@ def _raster_bwd(means2d, conics, opacities, mus, tile_offsets, isect_ids, flatte
         return v_abs, v_means2d, v_conics, v_opac, v_mus
     sfx = _suffix(means2d, op)
     dev = means2d.device
+    emit = _emission_order(flatten_ids, C * tw * th)
     with torch.cuda.device(dev):
-        _call(f"r2s_rasterize_bwd_{sfx}", _ptr(means2d), _ptr(conics), _ptr(opacities),
-              _ptr(mus), _ptr(tile_offsets), _ptr(isect_ids), _ptr(flatten_ids), n_isects,
-              _ptr(v_render), C, N, W, H, ts, tw, th, _ptr(v_abs), _ptr(v_means2d),
-              _ptr(v_conics), _ptr(v_opac), _ptr(v_mus), _stream(dev))
+        if emit is not None:
+            ws = _workspace(_lib().r2s_rasterize_bwd_workspace_bytes(n_isects,
+                                                                     means2d.element_size()), dev)
+            _call(f"r2s_rasterize_bwd_emit_{sfx}", _ptr(means2d), _ptr(conics), _ptr(opacities),
+                  _ptr(mus), _ptr(tile_offsets), _ptr(isect_ids), _ptr(flatten_ids),
+                  _ptr(emit[0]), _ptr(emit[1]), n_isects, _ptr(v_render), C, N, W, H, ts, tw,
+                  th, _ptr(v_abs), _ptr(v_means2d), _ptr(v_conics), _ptr(v_opac), _ptr(v_mus),
+                  _ptr(ws), ws.numel(), _stream(dev))
+        else:
+            _call(f"r2s_rasterize_bwd_{sfx}", _ptr(means2d), _ptr(conics), _ptr(opacities),
+                  _ptr(mus), _ptr(tile_offsets), _ptr(isect_ids), _ptr(flatten_ids), n_isects,
+                  _ptr(v_render), C, N, W, H, ts, tw, th, _ptr(v_abs), _ptr(v_means2d),
+                  _ptr(v_conics), _ptr(v_opac), _ptr(v_mus), _stream(dev))
     return v_abs, v_means2d, v_conics, v_opac, v_mus
 
 
@@ -701,11 +746,21 @@ def _voxel_bwd(means3d, conics, opacities, tile_offsets, isect_ids, flatten_ids,
     _check(tuple(v_render.shape) == (d0, d1, d2), "v_render_output shape must be [dim0, dim1, dim2]")
     sfx = _suffix(means3d, op)
     dev = means3d.device
+    emit = _emission_order(flatten_ids, n2 * n1 * n0)
     with torch.cuda.device(dev):
-        _call(f"r2s_voxelize_bwd_{sfx}", _ptr(means3d), _ptr(conics), _ptr(opacities),
-              _ptr(tile_offsets), _ptr(isect_ids), _ptr(flatten_ids), n_isects, _ptr(v_render),
-              N, d2, d1, d0, ts, n2, n1, n0, _ptr(v_means3d), _ptr(v_conics), _ptr(v_opac),
-              _stream(dev))
+        if emit is not None:
+            ws = _workspace(_lib().r2s_voxelize_bwd_workspace_bytes(n_isects,
+                                                                    means3d.element_size()), dev)
+            _call(f"r2s_voxelize_bwd_emit_{sfx}", _ptr(means3d), _ptr(conics), _ptr(opacities),
+                  _ptr(tile_offsets), _ptr(isect_ids), _ptr(flatten_ids), _ptr(emit[0]),
+                  _ptr(emit[1]), n_isects, _ptr(v_render), N, d2, d1, d0, ts, n2, n1, n0,
+                  _ptr(v_means3d), _ptr(v_conics), _ptr(v_opac), _ptr(ws), ws.numel(),
+                  _stream(dev))
+        else:
+            _call(f"r2s_voxelize_bwd_{sfx}", _ptr(means3d), _ptr(conics), _ptr(opacities),
+                  _ptr(tile_offsets), _ptr(isect_ids), _ptr(flatten_ids), n_isects,
+                  _ptr(v_render), N, d2, d1, d0, ts, n2, n1, n0, _ptr(v_means3d),
+                  _ptr(v_conics), _ptr(v_opac), _stream(dev))
     return v_means3d, v_conics, v_opac
 
 

@@ -199,13 +199,20 @@ int r2s_isect_count_2d_f64(const double *means2d, const int32_t *radii,
 
 /* IsectTiles.cpp:113-169 (emit + stable radix sort on bits [0,end_bit)):
  * writes isect_ids [n_isects] (int64 key cid*T + ty*tw + tx) and
- * flatten_ids [n_isects] (int32 cid*N + g), ordered by (key, id). */
+ * flatten_ids [n_isects] (int32 cid*N + g), ordered by (key, id).
+ * emit_ids / isect_src (both or neither may be NULL; int32 [n_isects] each)
+ * describe the records in emission order -- id-major, the records of one id
+ * consecutive -- which the reference does not output: emit_ids[e] is the id
+ * of emitted record e and isect_src[r] the emission index of sorted record
+ * r.  The two-pass backward kernels (r2s_rasterize_bwd_emit_*,
+ * r2s_voxelize_bwd_emit_*) take them. */
 int r2s_isect_emit_sort_2d_f32(const float *means2d, const int32_t *radii,
                                int radii_is_rect, int64_t C, int64_t N,
                                uint32_t tile_size, uint32_t n_tiles_w,
                                uint32_t n_tiles_h, const int64_t *offsets,
                                int64_t n_isects, uint32_t end_bit,
                                int64_t *isect_ids, int32_t *flatten_ids,
+                               int32_t *emit_ids, int32_t *isect_src,
                                void *workspace, size_t workspace_bytes,
                                r2s_stream_t stream);
 int r2s_isect_emit_sort_2d_f64(const double *means2d, const int32_t *radii,
@@ -214,6 +221,7 @@ int r2s_isect_emit_sort_2d_f64(const double *means2d, const int32_t *radii,
                                uint32_t n_tiles_h, const int64_t *offsets,
                                int64_t n_isects, uint32_t end_bit,
                                int64_t *isect_ids, int32_t *flatten_ids,
+                               int32_t *emit_ids, int32_t *isect_src,
                                void *workspace, size_t workspace_bytes,
                                r2s_stream_t stream);
 
@@ -232,13 +240,15 @@ int r2s_isect_count_3d_f64(const double *means3d, const int32_t *radii,
                            void *workspace, size_t workspace_bytes,
                            r2s_stream_t stream);
 
-/* IsectTiles3D.cpp:109-161 (3D emit z->y->x + stable sort). */
+/* IsectTiles3D.cpp:109-161 (3D emit z->y->x + stable sort); emit_ids /
+ * isect_src as for the 2D variant. */
 int r2s_isect_emit_sort_3d_f32(const float *means3d, const int32_t *radii,
                                int64_t N, uint32_t tile_size,
                                uint32_t n_tiles_d2, uint32_t n_tiles_d1,
                                uint32_t n_tiles_d0, const int64_t *offsets,
                                int64_t n_isects, uint32_t end_bit,
                                int64_t *isect_ids, int32_t *flatten_ids,
+                               int32_t *emit_ids, int32_t *isect_src,
                                void *workspace, size_t workspace_bytes,
                                r2s_stream_t stream);
 int r2s_isect_emit_sort_3d_f64(const double *means3d, const int32_t *radii,
@@ -247,6 +257,7 @@ int r2s_isect_emit_sort_3d_f64(const double *means3d, const int32_t *radii,
                                uint32_t n_tiles_d0, const int64_t *offsets,
                                int64_t n_isects, uint32_t end_bit,
                                int64_t *isect_ids, int32_t *flatten_ids,
+                               int32_t *emit_ids, int32_t *isect_src,
                                void *workspace, size_t workspace_bytes,
                                r2s_stream_t stream);
 
@@ -310,6 +321,40 @@ int r2s_rasterize_bwd_f64(const double *means2d, const double *conics,
                           double *v_means2d_abs, double *v_means2d,
                           double *v_conics, double *v_opacities, double *v_mus,
                           r2s_stream_t stream);
+
+/* Workspace of r2s_rasterize_bwd_emit_*: one row of 16 values of
+ * dtype_bytes per record. */
+int64_t r2s_rasterize_bwd_workspace_bytes(int64_t n_isects, int dtype_bytes);
+
+/* The same VJP as r2s_rasterize_bwd_* (RasterizeToPixelsBwd.cu:77-480) in
+ * two passes, without one device-scope atomic per record and partial: the
+ * records are walked in tile order and each record's partials are stored as
+ * a row of the workspace at its emission index (isect_src); a second pass
+ * walks the rows in emission order, where each Gaussian's records are
+ * consecutive (emit_ids), sums them and writes each Gaussian once.
+ * Deterministic.  isect_ids may be NULL.  Outputs accumulated (+=). */
+int r2s_rasterize_bwd_emit_f32(const float *means2d, const float *conics,
+                               const float *opacities, const float *mus,
+                               const int32_t *tile_offsets, const int64_t *isect_ids,
+                               const int32_t *flatten_ids, const int32_t *emit_ids,
+                               const int32_t *isect_src, int64_t n_isects,
+                               const float *v_image, int64_t C, int64_t N,
+                               uint32_t width, uint32_t height, uint32_t tile_size,
+                               uint32_t n_tiles_w, uint32_t n_tiles_h,
+                               float *v_means2d_abs, float *v_means2d, float *v_conics,
+                               float *v_opacities, float *v_mus, void *workspace,
+                               size_t workspace_bytes, r2s_stream_t stream);
+int r2s_rasterize_bwd_emit_f64(const double *means2d, const double *conics,
+                               const double *opacities, const double *mus,
+                               const int32_t *tile_offsets, const int64_t *isect_ids,
+                               const int32_t *flatten_ids, const int32_t *emit_ids,
+                               const int32_t *isect_src, int64_t n_isects,
+                               const double *v_image, int64_t C, int64_t N,
+                               uint32_t width, uint32_t height, uint32_t tile_size,
+                               uint32_t n_tiles_w, uint32_t n_tiles_h,
+                               double *v_means2d_abs, double *v_means2d, double *v_conics,
+                               double *v_opacities, double *v_mus, void *workspace,
+                               size_t workspace_bytes, r2s_stream_t stream);
 
 /* ---------------------------------------------------------------------- */
 /* Volume mapping and voxelizer                                           */
@@ -381,6 +426,35 @@ int r2s_voxelize_bwd_f64(const double *means3d, const double *conics,
                          uint32_t n_tiles_d1, uint32_t n_tiles_d0,
                          double *v_means3d, double *v_conics,
                          double *v_opacities, r2s_stream_t stream);
+
+/* Workspace of r2s_voxelize_bwd_emit_*: one row of 16 values of
+ * dtype_bytes per record. */
+int64_t r2s_voxelize_bwd_workspace_bytes(int64_t n_isects, int dtype_bytes);
+
+/* The same VJP as r2s_voxelize_bwd_* (VoxelizeToVoxelsBwd.cu:71-441) in two
+ * passes, as r2s_rasterize_bwd_emit_*: per-record rows stored at their
+ * emission index, then summed per Gaussian and written once.
+ * Deterministic.  isect_ids may be NULL.  Outputs accumulated (+=). */
+int r2s_voxelize_bwd_emit_f32(const float *means3d, const float *conics,
+                              const float *opacities, const int32_t *tile_offsets,
+                              const int64_t *isect_ids, const int32_t *flatten_ids,
+                              const int32_t *emit_ids, const int32_t *isect_src,
+                              int64_t n_isects, const float *v_volume, int64_t N,
+                              uint32_t dim2, uint32_t dim1, uint32_t dim0,
+                              uint32_t tile_size, uint32_t n_tiles_d2,
+                              uint32_t n_tiles_d1, uint32_t n_tiles_d0, float *v_means3d,
+                              float *v_conics, float *v_opacities, void *workspace,
+                              size_t workspace_bytes, r2s_stream_t stream);
+int r2s_voxelize_bwd_emit_f64(const double *means3d, const double *conics,
+                              const double *opacities, const int32_t *tile_offsets,
+                              const int64_t *isect_ids, const int32_t *flatten_ids,
+                              const int32_t *emit_ids, const int32_t *isect_src,
+                              int64_t n_isects, const double *v_volume, int64_t N,
+                              uint32_t dim2, uint32_t dim1, uint32_t dim0,
+                              uint32_t tile_size, uint32_t n_tiles_d2,
+                              uint32_t n_tiles_d1, uint32_t n_tiles_d0, double *v_means3d,
+                              double *v_conics, double *v_opacities, void *workspace,
+                              size_t workspace_bytes, r2s_stream_t stream);
 
 /* ---------------------------------------------------------------------- */
 /* Densify / prune index compaction                                        */

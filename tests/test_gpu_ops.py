@@ -12,9 +12,15 @@ import torch
 
 from helpers import assert_close, assert_equal, make_scene, np32
 from oracle import binning, native, ops
+from r2splat.cuda import _ops
 from r2splat.cuda import _wrapper as W
 
 pytestmark = pytest.mark.gpu
+
+
+def fl_keys(tile_offsets):
+    """Number of tile / brick keys of a tile_offsets tensor."""
+    return tile_offsets.numel()
 
 DEV = "cuda"
 
@@ -203,9 +209,10 @@ def _raster_case(n, seed, W_img, H_img, ts, n_views=1, dtype=torch.float32, log_
     return d, m2, con, mu, op, ids, fl, off
 
 
+@pytest.mark.parametrize("order", ["emission", "tile"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
 @pytest.mark.parametrize("shape", [(64, 64, 16), (70, 45, 16), (40, 40, 8)])
-def test_rasterize_fwd_bwd(dtype, shape):
+def test_rasterize_fwd_bwd(dtype, shape, order):
     W_img, H_img, ts = shape
     d, m2, con, mu, op, ids, fl, off = _raster_case(3000, 7, W_img, H_img, ts, 2, dtype)
     assert fl.numel() > 500
@@ -220,6 +227,9 @@ def test_rasterize_fwd_bwd(dtype, shape):
     ref = native.raster_bwd(np32(m2), np32(con), np32(op), np32(mu), np32(off), np32(fl),
                             v.numpy(), W_img, H_img, ts, True)
     names = ("v_means2d_abs", "v_means2d", "v_conics", "v_opacities", "v_mus")
+    if order == "tile":
+        fl = fl.clone()  # no emission-order records: the tile-order kernels run
+    assert (_ops._emission_order(fl, fl_keys(off)) is not None) == (order == "emission")
     for mode in ("primitive", "pixel"):
         if mode == "primitive":
             got = W.rasterize_to_pixels_bwd_per_gaussian(m2, con, op, mu, off, ids, fl,
@@ -264,9 +274,10 @@ def _voxel_case(n, seed, dims, ts, dtype=torch.float32, log_mu=-3.2):
     return d, m3, con, ids, fl, off
 
 
+@pytest.mark.parametrize("order", ["emission", "tile"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
 @pytest.mark.parametrize("dims,ts", [((32, 32, 32), 8), ((30, 20, 26), 8), ((24, 24, 24), 4)])
-def test_voxelize_fwd_bwd(dtype, dims, ts):
+def test_voxelize_fwd_bwd(dtype, dims, ts, order):
     d, m3, con, ids, fl, off = _voxel_case(2500, 8, dims, ts, dtype)
     d2, d1, d0 = dims
     assert fl.numel() > 500
@@ -280,6 +291,9 @@ def test_voxelize_fwd_bwd(dtype, dims, ts):
     v = torch.randn(vol.shape, generator=d["gen"], dtype=dtype)
     ref = native.voxel_bwd(np32(m3), np32(con), np32(op), np32(off), np32(fl), v.numpy(), d2, d1,
                            d0, ts)
+    if order == "tile":
+        fl = fl.clone()  # no emission-order records: the tile-order kernels run
+    assert (_ops._emission_order(fl, fl_keys(off)) is not None) == (order == "emission")
     for mode in ("primitive", "pixel"):
         if mode == "primitive":
             got = W.voxelize_to_voxels_bwd_per_gaussian(m3, con, op, off, ids, fl, v.to(DEV), d2,
@@ -303,3 +317,20 @@ def test_mask_split_matches_torch_where(n):
         sel, rest = torch.where(mask)[0], torch.where(~mask)[0]
         assert n_true == sel.numel()
         assert torch.equal(out[:n_true], sel) and torch.equal(out[n_true:], rest)
+
+
+def test_emission_order_backward_is_deterministic():
+    d, m2, con, mu, op, ids, fl, off = _raster_case(3000, 9, 64, 64, 16, 2, torch.float32)
+    v = torch.randn((2, 64, 64), generator=d["gen"]).to(DEV)
+    runs = [W.rasterize_to_pixels_bwd_per_gaussian(m2, con, op, mu, off, ids, fl, v, 64, 64, 16,
+                                                   True) for _ in range(3)]
+    for a, b in zip(runs[0], runs[1]):
+        assert torch.equal(a, b)
+    for a, b in zip(runs[0], runs[2]):
+        assert torch.equal(a, b)
+    d, m3, con3, ids3, fl3, off3 = _voxel_case(2500, 10, (32, 32, 32), 8)
+    v3 = torch.randn((32, 32, 32), generator=d["gen"]).to(DEV)
+    runs = [W.voxelize_to_voxels_bwd(m3, con3, d["opac"], off3, fl3, v3, 32, 32, 32, 8)
+            for _ in range(2)]
+    for a, b in zip(runs[0], runs[1]):
+        assert torch.equal(a, b)
