@@ -146,14 +146,4 @@ struct WaveSegments {
   }
 };
 
-// Adds `v` to `out[i]` from the first lane of a segment: a plain
-// read-modify-write when this wave holds the whole segment, else an atomic.
-template <typename T>
-__device__ __forceinline__ void segment_store(T *out, int64_t i, T v, bool shared) {
-  if (shared)
-    atomic_add(out + i, v);
-  else
-    out[i] += v;
-}
-
 }  // namespace r2s

@@ -153,7 +153,7 @@ __device__ __forceinline__ void load_raster_record(
 // lane per record.  kRows = false: each record's nine partials go out
 // through global atomics.  kRows = true: they are stored as the row
 // isect_src[r] of `rows` (see r2s_rows.h), zeros included.
-template <typename T, int R, bool kAbs, bool kRows>
+template <typename T, int R, bool kAbs, bool kRows, bool kVec>
 __global__ __launch_bounds__(kBwdThreads) void raster_bwd_kernel(
     const T *__restrict__ means2d, const T *__restrict__ conics, const T *__restrict__ opac,
     const T *__restrict__ mus, const int32_t *__restrict__ tile_offsets,
@@ -200,12 +200,14 @@ __global__ __launch_bounds__(kBwdThreads) void raster_bwd_kernel(
       const T B = rec.hb * dy, C = rec.hc * dy * dy;
       const T bdy = rec.b * dy, cdy = rec.c * dy;
       const T *__restrict__ vrow = vimg + static_cast<int64_t>(in_row ? i : 0) * W + ox;
+      T vv[R];
+      load_grad_row<T, R, kVec>(vrow, in_row, nx, static_cast<int>(ts), vv);
       T s0 = 0, s1 = 0, s2 = 0, px = 0, py = 0;
 #pragma unroll
       for (int k = 0; k < R; ++k) {
         if (k >= static_cast<int>(ts)) break;
         const bool here = in_row && k < nx;
-        const T v = here ? vrow[k] : static_cast<T>(0);
+        const T v = vv[k];
         const T dx = (px0 + static_cast<T>(k)) - rec.mx;
         const T sl = (rec.ha * dx + B) * dx + C;
         const T e = neg_exp2(sl);
@@ -308,7 +310,7 @@ int raster_fwd_impl(const T *means2d, const T *conics, const T *opac, const T *m
   return check_launch(name);
 }
 
-template <typename T, int R>
+template <typename T, int R, bool kVec>
 void launch_raster_bwd(const T *means2d, const T *conics, const T *opac, const T *mus,
                        const int32_t *tile_offsets, const int64_t *isect_ids,
                        const int32_t *flatten_ids, const int32_t *isect_src, int64_t n_isects,
@@ -318,7 +320,7 @@ void launch_raster_bwd(const T *means2d, const T *conics, const T *opac, const T
   const dim3 grid(static_cast<uint32_t>(ceil_div(n_isects, kBwdThreads)));
   const dim3 block(kBwdThreads);
 #define R2S_RASTER_BWD_LAUNCH(ABS, ROWS)                                                         \
-  raster_bwd_kernel<T, R, ABS, ROWS><<<grid, block, 0, stream>>>(                              \
+  raster_bwd_kernel<T, R, ABS, ROWS, kVec><<<grid, block, 0, stream>>>(                        \
       means2d, conics, opac, mus, tile_offsets, isect_ids, flatten_ids, isect_src, n_isects,     \
       n_keys, n_items, v_image, W, H, ts, tw, th, v_xy_abs, v_xy, v_conic, v_opac, v_mu, rows)
   if (v_xy_abs != nullptr) {
@@ -365,20 +367,34 @@ int raster_bwd_impl(const T *means2d, const T *conics, const T *opac, const T *m
       set_error("%s: workspace of %zu bytes, %lld required", name, ws_bytes, (long long)need);
       return R2S_EWORKSPACE;
     }
+    R2S_REQUIRE(reinterpret_cast<uintptr_t>(ws) % 16 == 0, "%s: workspace not 16-byte aligned",
+                name);
     rows = static_cast<T *>(ws);
   }
   const uint32_t n_keys = static_cast<uint32_t>(C) * tw * th;
   hipStream_t stream = as_stream(st);
-#define R2S_RASTER_BWD_R(RR)                                                                     \
-  launch_raster_bwd<T, RR>(means2d, conics, opac, mus, tile_offsets, isect_ids, flatten_ids,     \
-                           isect_src, n_isects, n_keys, C * N, v_image, W, H, ts, tw, th,        \
-                           v_xy_abs, v_xy, v_conic, v_opac, v_mu, rows, stream)
-  if (ts <= 8)
-    R2S_RASTER_BWD_R(8);
-  else if (ts <= 16)
-    R2S_RASTER_BWD_R(16);
-  else
-    R2S_RASTER_BWD_R(32);
+  // 16-byte loads of gradient rows when every row segment starts aligned.
+  const bool vec = vec_rows_ok<T>(v_image, W, ts);
+#define R2S_RASTER_BWD_R(RR, VEC)                                                                \
+  launch_raster_bwd<T, RR, VEC>(means2d, conics, opac, mus, tile_offsets, isect_ids,             \
+                                flatten_ids, isect_src, n_isects, n_keys, C * N, v_image, W, H,  \
+                                ts, tw, th, v_xy_abs, v_xy, v_conic, v_opac, v_mu, rows, stream)
+  if (ts <= 8) {
+    if (vec)
+      R2S_RASTER_BWD_R(8, true);
+    else
+      R2S_RASTER_BWD_R(8, false);
+  } else if (ts <= 16) {
+    if (vec)
+      R2S_RASTER_BWD_R(16, true);
+    else
+      R2S_RASTER_BWD_R(16, false);
+  } else {
+    if (vec)
+      R2S_RASTER_BWD_R(32, true);
+    else
+      R2S_RASTER_BWD_R(32, false);
+  }
 #undef R2S_RASTER_BWD_R
   R2S_RETURN_IF(check_launch(name));
   if (!two_pass) return R2S_OK;

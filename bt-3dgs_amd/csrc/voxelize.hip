@@ -220,7 +220,7 @@ __device__ __forceinline__ void load_bwd_record(const T *__restrict__ means3d,
 // one lane per record.  kRows = false: each record's ten partials go out
 // through global atomics.  kRows = true: they are stored as the row
 // isect_src[r] of `rows` (see r2s_rows.h), zeros included.
-template <typename T, int R, bool kRows>
+template <typename T, int R, bool kRows, bool kVec>
 __global__ __launch_bounds__(kBwdThreads) void voxel_bwd_kernel(
     const T *__restrict__ means3d, const T *__restrict__ conics, const T *__restrict__ opac,
     const int32_t *__restrict__ tile_offsets, const int64_t *__restrict__ isect_ids,
@@ -278,12 +278,14 @@ __global__ __launch_bounds__(kBwdThreads) void voxel_bwd_kernel(
         const T *__restrict__ vrow =
             v_vol +
             (in_row ? static_cast<int64_t>(i) * plane + static_cast<int64_t>(j) * D2 : 0) + b.ok;
+        T vv[R];
+        load_grad_row<T, R, kVec>(vrow, in_row, b.nk, static_cast<int>(ts), vv);
         T s0 = 0, s1 = 0, s2 = 0;
 #pragma unroll
         for (int k = 0; k < R; ++k) {
           if (k >= static_cast<int>(ts)) break;
           const bool here = in_row && k < b.nk;
-          const T v = here ? vrow[k] : static_cast<T>(0);
+          const T v = vv[k];
           const T dx = (px0 + static_cast<T>(k)) - rec.m[0];
           const T sl = (rec.h[0] * dx + B) * dx + C;
           const T e = neg_exp2(sl);
@@ -397,7 +399,7 @@ int voxel_fwd_impl(const T *means3d, const T *conics, const T *opac,
   return check_launch(name);
 }
 
-template <typename T, int R>
+template <typename T, int R, bool kVec>
 void launch_voxel_bwd(const T *means3d, const T *conics, const T *opac,
                       const int32_t *tile_offsets, const int64_t *isect_ids,
                       const int32_t *flatten_ids, const int32_t *isect_src, int64_t n_isects,
@@ -406,11 +408,11 @@ void launch_voxel_bwd(const T *means3d, const T *conics, const T *opac,
                       T *v_conics, T *v_opac, T *rows, hipStream_t stream) {
   const dim3 grid(static_cast<uint32_t>(ceil_div(n_isects, kBwdThreads)));
   if (rows != nullptr)
-    voxel_bwd_kernel<T, R, true><<<grid, dim3(kBwdThreads), 0, stream>>>(
+    voxel_bwd_kernel<T, R, true, kVec><<<grid, dim3(kBwdThreads), 0, stream>>>(
         means3d, conics, opac, tile_offsets, isect_ids, flatten_ids, isect_src, n_isects, n_keys,
         N, v_vol, D2, D1, D0, ts, n2, n1, v_means, v_conics, v_opac, rows);
   else
-    voxel_bwd_kernel<T, R, false><<<grid, dim3(kBwdThreads), 0, stream>>>(
+    voxel_bwd_kernel<T, R, false, kVec><<<grid, dim3(kBwdThreads), 0, stream>>>(
         means3d, conics, opac, tile_offsets, isect_ids, flatten_ids, isect_src, n_isects, n_keys,
         N, v_vol, D2, D1, D0, ts, n2, n1, v_means, v_conics, v_opac, rows);
 }
@@ -447,20 +449,34 @@ int voxel_bwd_impl(const T *means3d, const T *conics, const T *opac,
       set_error("%s: workspace of %zu bytes, %lld required", name, ws_bytes, (long long)need);
       return R2S_EWORKSPACE;
     }
+    R2S_REQUIRE(reinterpret_cast<uintptr_t>(ws) % 16 == 0, "%s: workspace not 16-byte aligned",
+                name);
     rows = static_cast<T *>(ws);
   }
   const uint32_t n_keys = n2 * n1 * n0;
   hipStream_t stream = as_stream(st);
-#define R2S_VOXEL_BWD_R(RR)                                                                    \
-  launch_voxel_bwd<T, RR>(means3d, conics, opac, tile_offsets, isect_ids, flatten_ids,         \
-                          isect_src, n_isects, n_keys, N, v_vol, D2, D1, D0, ts, n2, n1,       \
-                          v_means, v_conics, v_opac, rows, stream)
-  if (ts <= 4)
-    R2S_VOXEL_BWD_R(4);
-  else if (ts <= 8)
-    R2S_VOXEL_BWD_R(8);
-  else
-    R2S_VOXEL_BWD_R(16);
+  // 16-byte loads of gradient rows when every row segment starts aligned.
+  const bool vec = vec_rows_ok<T>(v_vol, D2, ts);
+#define R2S_VOXEL_BWD_R(RR, VEC)                                                               \
+  launch_voxel_bwd<T, RR, VEC>(means3d, conics, opac, tile_offsets, isect_ids, flatten_ids,    \
+                               isect_src, n_isects, n_keys, N, v_vol, D2, D1, D0, ts, n2, n1,  \
+                               v_means, v_conics, v_opac, rows, stream)
+  if (ts <= 4) {
+    if (vec)
+      R2S_VOXEL_BWD_R(4, true);
+    else
+      R2S_VOXEL_BWD_R(4, false);
+  } else if (ts <= 8) {
+    if (vec)
+      R2S_VOXEL_BWD_R(8, true);
+    else
+      R2S_VOXEL_BWD_R(8, false);
+  } else {
+    if (vec)
+      R2S_VOXEL_BWD_R(16, true);
+    else
+      R2S_VOXEL_BWD_R(16, false);
+  }
 #undef R2S_VOXEL_BWD_R
   R2S_RETURN_IF(check_launch(name));
   if (!two_pass) return R2S_OK;

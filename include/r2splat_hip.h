@@ -331,8 +331,10 @@ int64_t r2s_rasterize_bwd_workspace_bytes(int64_t n_isects, int dtype_bytes);
  * records are walked in tile order and each record's partials are stored as
  * a row of the workspace at its emission index (isect_src); a second pass
  * walks the rows in emission order, where each Gaussian's records are
- * consecutive (emit_ids), sums them and writes each Gaussian once.
- * Deterministic.  isect_ids may be NULL.  Outputs accumulated (+=). */
+ * consecutive (emit_ids), sums them and stores each Gaussian's sums once.
+ * Deterministic.  isect_ids may be NULL.  Outputs are stored, not
+ * accumulated: the caller zeroes them (Gaussians without records are not
+ * written). */
 int r2s_rasterize_bwd_emit_f32(const float *means2d, const float *conics,
                                const float *opacities, const float *mus,
                                const int32_t *tile_offsets, const int64_t *isect_ids,
@@ -433,8 +435,9 @@ int64_t r2s_voxelize_bwd_workspace_bytes(int64_t n_isects, int dtype_bytes);
 
 /* The same VJP as r2s_voxelize_bwd_* (VoxelizeToVoxelsBwd.cu:71-441) in two
  * passes, as r2s_rasterize_bwd_emit_*: per-record rows stored at their
- * emission index, then summed per Gaussian and written once.
- * Deterministic.  isect_ids may be NULL.  Outputs accumulated (+=). */
+ * emission index, then summed per Gaussian and stored once.
+ * Deterministic.  isect_ids may be NULL.  Outputs are stored, not
+ * accumulated: the caller zeroes them. */
 int r2s_voxelize_bwd_emit_f32(const float *means3d, const float *conics,
                               const float *opacities, const int32_t *tile_offsets,
                               const int64_t *isect_ids, const int32_t *flatten_ids,
