@@ -20,12 +20,11 @@ Modules
              rasterizer and voxelizer (forward and both backward modes).
 ``compose``  the ``r2splat.ops`` forward/backward composition on top of the
              above (explicit.py / direct.py restated).
-``dense``    the dense PyTorch-CPU formulation of the reference's op tests
-             (autograd backward), used as the CPU baseline and as an
-             independent end-to-end check.
-``scenes``   seeded synthetic inputs shared by tests and the CPU baseline.
 
-How each function is pinned (golden vectors, closed forms, brute force,
-invariants) is listed in ``tests/test_oracle_*.py``.  Functions without such
-a check say "parity unpinned" in their docstring.
+Seeded synthetic inputs come from ``r2splat.scenes`` / ``r2splat.geometry``
+(host-side generators, no device code).  How each function is pinned (the
+reference's known-answer tests, closed forms, autograd, finite differences,
+brute force, invariants) is listed in ``tests/test_oracle_*.py``; every
+function has at least one such check, so none is "parity unpinned".
+Fixtures produced by this oracle are committed under ``tests/golden/``.
 """
