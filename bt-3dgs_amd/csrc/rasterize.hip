@@ -47,6 +47,9 @@ __device__ __forceinline__ double fast_exp(double x) { return exp(x); }
 
 constexpr double kThr2 = 1e-5;
 constexpr int kBwdThreads = 256;
+// Pixels of a row evaluated together: an unrolled 8-pixel body in a rolled
+// loop keeps the kernel at 62 VGPRs (8 waves per SIMD) without spills.
+constexpr int kChunk = 8;
 
 template <typename T>
 __global__ __launch_bounds__(1024) void raster_fwd_kernel(
@@ -108,6 +111,102 @@ __global__ __launch_bounds__(1024) void raster_fwd_kernel(
   if (inside) image[static_cast<int64_t>(cam) * H * W + static_cast<int64_t>(i) * W + j] = acc;
 }
 
+// Forward for tile sizes 8, 16 and 32: kFwdWaves waves per (view, tile),
+// each covering all TS^2 pixels of the tile with R = TS^2 / 64 consecutive
+// pixels of one row per lane, and taking every kFwdWaves-th record of each
+// LDS batch.  A record's row terms (dy, b dy, c dy^2) are shared by the R
+// pixels; sigma log2(e) = (h_a dx + h_b dy) dx + h_c dy^2 with pre-scaled
+// coefficients, so a pixel costs two FMAs, one v_exp_f32 and the alpha test.
+// The waves' partial images are summed in a fixed order at the end, so the
+// result is deterministic (the per-pixel order differs from a plain
+// list-order sum only by rounding).
+constexpr int kFwdWaves = 8;
+constexpr int kFwdBatch = 64 * kFwdWaves;
+
+template <typename T, int TS>
+__global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
+    const T *__restrict__ means2d, const T *__restrict__ conics, const T *__restrict__ opac,
+    const T *__restrict__ mus, const int32_t *__restrict__ tile_offsets,
+    const int32_t *__restrict__ flatten_ids, int64_t n_isects, uint32_t n_keys, int64_t n_items,
+    uint32_t W, uint32_t H, uint32_t tw, uint32_t th, T *__restrict__ image) {
+  using V2 = typename Vec<T>::v2;
+  using V4 = typename Vec<T>::v4;
+  constexpr int R = TS * TS / 64;   // pixels per lane
+  constexpr int LPR = TS / R;       // lanes per tile row
+  static_assert(R * 64 == TS * TS && LPR * R == TS, "unsupported tile size");
+  __shared__ V4 s_p[kFwdBatch];     // {x, y, h_a, h_b}
+  __shared__ V2 s_q[kFwdBatch];     // {h_c, opacity * mu}
+  __shared__ T s_part[kFwdWaves][TS * TS];
+
+  const uint32_t key = xcd_swizzle(blockIdx.x, n_keys);
+  const uint32_t n_tiles = tw * th;
+  const uint32_t cam = key / n_tiles, t = key - cam * n_tiles;
+  const uint32_t ty = t / tw, tx = t - ty * tw;
+  const int tid = static_cast<int>(threadIdx.x);
+  const int wave = static_cast<int>(wave_index()), lane = static_cast<int>(lane_id());
+  const int ly = lane / LPR, lx0 = (lane % LPR) * R;
+  const T half = static_cast<T>(0.5);
+  const T py = static_cast<T>(static_cast<int>(ty) * TS + ly) + half;
+  const T px0 = static_cast<T>(static_cast<int>(tx) * TS + lx0) + half;
+  const T thr = static_cast<T>(kThr2);
+  const T l = static_cast<T>(kLog2e), hl = static_cast<T>(0.5 * kLog2e);
+
+  const int64_t start = tile_offsets[key];
+  const int64_t end = (key == n_keys - 1) ? n_isects : static_cast<int64_t>(tile_offsets[key + 1]);
+  T acc[R];
+#pragma unroll
+  for (int q = 0; q < R; ++q) acc[q] = 0;
+  for (int64_t base = start; base < end; base += kFwdBatch) {
+    __syncthreads();
+    const int64_t idx = base + tid;
+    if (idx < end) {
+      const int64_t g = flatten_ids[idx];
+      V4 p;
+      V2 q;
+      if (g >= 0 && g < n_items) {
+        const V2 xy = *reinterpret_cast<const V2 *>(means2d + 2 * g);
+        p.x = xy.x;
+        p.y = xy.y;
+        p.z = hl * conics[3 * g];
+        p.w = l * conics[3 * g + 1];
+        q.x = hl * conics[3 * g + 2];
+        q.y = opac[g] * mus[g];
+      } else {  // never passes: alpha = 0
+        p.x = p.y = p.z = p.w = 0;
+        q.x = q.y = 0;
+      }
+      s_p[tid] = p;
+      s_q[tid] = q;
+    }
+    __syncthreads();
+    const int cnt = static_cast<int>(min(static_cast<int64_t>(kFwdBatch), end - base));
+    for (int j = wave; j < cnt; j += kFwdWaves) {
+      const V4 p = s_p[j];
+      const V2 q = s_q[j];
+      const T dy = py - p.y;
+      const T B = p.w * dy, C = q.x * dy * dy;
+#pragma unroll
+      for (int k = 0; k < R; ++k) {
+        const T dx = (px0 + static_cast<T>(k)) - p.x;
+        const T sl = (p.z * dx + B) * dx + C;
+        const T alpha = q.y * neg_exp2(sl);
+        acc[k] += ((sl < static_cast<T>(0)) || (fabs(alpha) < thr)) ? static_cast<T>(0) : alpha;
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < R; ++k) s_part[wave][ly * TS + lx0 + k] = acc[k];
+  __syncthreads();
+  for (int pix = tid; pix < TS * TS; pix += kFwdBatch) {
+    T sum = s_part[0][pix];
+#pragma unroll
+    for (int w = 1; w < kFwdWaves; ++w) sum += s_part[w][pix];
+    const int i = static_cast<int>(ty) * TS + pix / TS, j = static_cast<int>(tx) * TS + pix % TS;
+    if (i < static_cast<int>(H) && j < static_cast<int>(W))
+      image[static_cast<int64_t>(cam) * H * W + static_cast<int64_t>(i) * W + j] = sum;
+  }
+}
+
 // One backward record in registers.
 template <typename T>
 struct RasterRecord {
@@ -115,6 +214,7 @@ struct RasterRecord {
   T mx, my, a, b, c, o, mu, om;
   T ha, hb, hc;       // a/2, b, c/2 pre-scaled by log2(e)
   int i0, i1;         // rows the alpha-test ellipse reaches (all rows when not PD)
+  bool pd;            // conic positive definite and finite (sigma finite, >= 0 up to rounding)
 };
 
 template <typename T>
@@ -133,6 +233,7 @@ __device__ __forceinline__ void load_raster_record(
     rec.mx = rec.my = rec.a = rec.b = rec.c = rec.ha = rec.hb = rec.hc = 0;
     rec.i0 = 0;
     rec.i1 = -1;
+    rec.pd = true;
     return;
   }
   rec.mx = means2d[2 * g];
@@ -144,28 +245,64 @@ __device__ __forceinline__ void load_raster_record(
   rec.hb = static_cast<T>(kLog2e) * rec.b;
   rec.hc = static_cast<T>(0.5 * kLog2e) * rec.c;
   const Cull2<T> cu = cull2_setup(rec.a, rec.b, rec.c, fabs(rec.om), kThr2);
+  rec.pd = cu.ok;
   rec.i0 = oy;
   rec.i1 = y1;
   if (cu.ok && !index_range<T>(rec.my, -cu.hy, cu.hy, oy, y1, rec.i0, rec.i1)) rec.live = false;
 }
 
+// Moments of one tile row for one record: s0 = sum w, s1 = sum w dx,
+// s2 = sum w dx^2 over the row's passing pixels (w = v exp(-sigma)), and
+// px, py = sums of |w (P d)_x|, |w (P d)_y|.  vv holds the row's upstream
+// gradient (zero beyond the image).  kGuard: also exclude columns k >= nx
+// explicitly -- needed only for records whose sigma may be -inf or NaN, for
+// which v = 0 would not make w = 0.
+template <typename T, int R, bool kExact, bool kAbs, bool kGuard>
+__device__ __forceinline__ void raster_row(const RasterRecord<T> &rec, const T (&vv)[R], int k0,
+                                           T dx0, int nx, int nts, T B, T C, T bdy, T cdy,
+                                           T &s0, T &s1, T &s2, T &px, T &py) {
+  const T thr = static_cast<T>(kThr2);
+#pragma unroll
+  for (int kk = 0; kk < R; ++kk) {
+    const int k = k0 + kk;
+    if (!kExact && k >= nts) break;
+    const T dx = dx0 + static_cast<T>(k);
+    const T sl = (rec.ha * dx + B) * dx + C;
+    const T e = neg_exp2(sl);
+    bool skip = (sl < static_cast<T>(0)) || (fabs(rec.om * e) < thr);
+    if (kGuard) skip = skip || k >= nx;
+    const T w = skip ? static_cast<T>(0) : vv[kk] * e;
+    s0 += w;
+    const T wx = w * dx;
+    s1 += wx;
+    s2 += wx * dx;
+    if (kAbs) {
+      px += fabs(w * (rec.a * dx + bdy));
+      py += fabs(w * (rec.b * dx + cdy));
+    }
+  }
+}
+
 // Records in tile order (tile_offsets, flatten_ids; isect_ids optional), one
 // lane per record.  kRows = false: each record's nine partials go out
 // through global atomics.  kRows = true: they are stored as the row
-// isect_src[r] of `rows` (see r2s_rows.h), zeros included.
-template <typename T, int R, bool kAbs, bool kRows, bool kVec>
+// isect_src[r] of `rows` (see r2s_rows.h), zeros included.  kExact: the tile
+// size equals R (loops fully unrolled); otherwise ts <= R at run time.
+template <typename T, int R, bool kExact, bool kAbs, bool kRows>
 __global__ __launch_bounds__(kBwdThreads) void raster_bwd_kernel(
     const T *__restrict__ means2d, const T *__restrict__ conics, const T *__restrict__ opac,
     const T *__restrict__ mus, const int32_t *__restrict__ tile_offsets,
     const int64_t *__restrict__ isect_ids, const int32_t *__restrict__ flatten_ids,
     const int32_t *__restrict__ isect_src, int64_t n_isects, uint32_t n_keys, int64_t n_items,
     const T *__restrict__ v_image, uint32_t W, uint32_t H, uint32_t ts, uint32_t tw,
-    uint32_t th, T *__restrict__ v_xy_abs, T *__restrict__ v_xy, T *__restrict__ v_conic,
-    T *__restrict__ v_opac, T *__restrict__ v_mu, T *__restrict__ rows) {
+    uint32_t th, bool vec, T *__restrict__ v_xy_abs, T *__restrict__ v_xy,
+    T *__restrict__ v_conic, T *__restrict__ v_opac, T *__restrict__ v_mu,
+    T *__restrict__ rows) {
   const int64_t rb = static_cast<int64_t>(blockIdx.x) * kBwdThreads + 64 * wave_index();
   if (rb >= n_isects) return;  // uniform per wave
   const int64_t r = rb + lane_id();
   const bool in_list = r < n_isects;
+  const int nts = kExact ? R : static_cast<int>(ts);
   uint32_t key;
   bool key_ok = in_list;
   if (isect_ids != nullptr) {
@@ -179,20 +316,23 @@ __global__ __launch_bounds__(kBwdThreads) void raster_bwd_kernel(
   const uint32_t n_tiles = tw * th;
   const uint32_t cam = key / n_tiles, t = key - cam * n_tiles;
   const uint32_t ty = t / tw, tx = t - ty * tw;
-  const int ox = static_cast<int>(tx * ts), oy = static_cast<int>(ty * ts);
-  const int nx = static_cast<int>(min(ts, W - tx * ts));
-  const int ny = static_cast<int>(min(ts, H - ty * ts));
+  const int ox = static_cast<int>(tx) * nts, oy = static_cast<int>(ty) * nts;
+  const int nx = min(nts, static_cast<int>(W) - ox);
+  const int ny = min(nts, static_cast<int>(H) - oy);
   const T *__restrict__ vimg = v_image + static_cast<int64_t>(cam) * H * W;
   RasterRecord<T> rec;
   load_raster_record(means2d, conics, opac, mus, g, n_items, key_ok, oy, oy + ny - 1, rec);
-  const T thr = static_cast<T>(kThr2), half = static_cast<T>(0.5);
-  const T px0 = static_cast<T>(ox) + half;
-  // T_k = sum over rows of s_k = sum(w dx^k); Y0 = sum dy s0, Y1 = sum dy s1,
-  // YY = sum dy^2 s0; PX, PY = sums of |w (P d)_x|, |w (P d)_y|.
+  const T half = static_cast<T>(0.5);
+  const T dx0 = (static_cast<T>(ox) + half) - rec.mx;
+  // Columns past the image matter only for records whose sigma may be
+  // non-finite (uniform over the wave).
+  const bool guard = ballot(rec.live && !rec.pd && nx < nts) != 0;
+  // T_k = sum over rows of s_k; Y0 = sum dy s0, Y1 = sum dy s1, YY = sum dy^2 s0;
+  // PX, PY = sums of the per-pixel absolute mean gradients.
   T T0 = 0, T1 = 0, T2 = 0, Y0 = 0, Y1 = 0, YY = 0, PX = 0, PY = 0;
   if (ballot(rec.live) != 0) {
     for (int ly = 0; ly < R; ++ly) {
-      if (ly >= static_cast<int>(ts)) break;
+      if (!kExact && ly >= nts) break;
       const int i = oy + ly;
       const bool in_row = rec.live && i >= rec.i0 && i <= rec.i1;
       if (ballot(in_row) == 0) continue;
@@ -200,27 +340,22 @@ __global__ __launch_bounds__(kBwdThreads) void raster_bwd_kernel(
       const T B = rec.hb * dy, C = rec.hc * dy * dy;
       const T bdy = rec.b * dy, cdy = rec.c * dy;
       const T *__restrict__ vrow = vimg + static_cast<int64_t>(in_row ? i : 0) * W + ox;
-      T vv[R];
-      load_grad_row<T, R, kVec>(vrow, in_row, nx, static_cast<int>(ts), vv);
       T s0 = 0, s1 = 0, s2 = 0, px = 0, py = 0;
-#pragma unroll
-      for (int k = 0; k < R; ++k) {
-        if (k >= static_cast<int>(ts)) break;
-        const bool here = in_row && k < nx;
-        const T v = vv[k];
-        const T dx = (px0 + static_cast<T>(k)) - rec.mx;
-        const T sl = (rec.ha * dx + B) * dx + C;
-        const T e = neg_exp2(sl);
-        const bool skip = !here || (sl < static_cast<T>(0)) || (fabs(rec.om * e) < thr);
-        const T w = skip ? static_cast<T>(0) : v * e;
-        s0 += w;
-        const T wx = w * dx;
-        s1 += wx;
-        s2 += wx * dx;
-        if (kAbs) {
-          px += fabs(w * (rec.a * dx + bdy));
-          py += fabs(w * (rec.b * dx + cdy));
-        }
+      constexpr int CH = R < kChunk ? R : kChunk;
+#pragma unroll 1
+      for (int k0 = 0; k0 < R; k0 += CH) {
+        if (!kExact && k0 >= nts) break;
+        T vv[CH];
+        if (vec)
+          load_grad_row<T, CH, true>(vrow + k0, in_row, nx - k0, nts - k0, vv);
+        else
+          load_grad_row<T, CH, false>(vrow + k0, in_row, nx - k0, nts - k0, vv);
+        if (guard)
+          raster_row<T, CH, kExact, kAbs, true>(rec, vv, k0, dx0, nx, nts, B, C, bdy, cdy, s0,
+                                                s1, s2, px, py);
+        else
+          raster_row<T, CH, kExact, kAbs, false>(rec, vv, k0, dx0, nx, nts, B, C, bdy, cdy, s0,
+                                                 s1, s2, px, py);
       }
       T0 += s0;
       T1 += s1;
@@ -302,27 +437,42 @@ int raster_fwd_impl(const T *means2d, const T *conics, const T *opac, const T *m
   R2S_REQUIRE(means2d && conics && opac && mus && tile_offsets && flatten_ids,
               "%s: null pointer", name);
   const uint32_t n_keys = static_cast<uint32_t>(C) * tw * th;
-  const uint32_t bs = ts * ts;
-  const size_t smem = (bs + (bs & 1u)) * sizeof(typename Vec<T>::v2) + bs * sizeof(typename Vec<T>::v4);
-  raster_fwd_kernel<T><<<dim3(n_keys), dim3(bs), smem, stream>>>(
-      means2d, conics, opac, mus, tile_offsets, flatten_ids, n_isects, n_keys, W, H, ts, tw, th,
-      image);
+#define R2S_RASTER_FWD_ROWS(TS)                                                                  \
+  raster_fwd_rows_kernel<T, TS><<<dim3(n_keys), dim3(kFwdBatch), 0, stream>>>(                 \
+      means2d, conics, opac, mus, tile_offsets, flatten_ids, n_isects, n_keys, C * N, W, H, tw,  \
+      th, image)
+  if (ts == 16) {
+    R2S_RASTER_FWD_ROWS(16);
+  } else if (ts == 8) {
+    R2S_RASTER_FWD_ROWS(8);
+  } else if (ts == 32) {
+    R2S_RASTER_FWD_ROWS(32);
+  } else {
+    const uint32_t bs = ts * ts;
+    const size_t smem =
+        (bs + (bs & 1u)) * sizeof(typename Vec<T>::v2) + bs * sizeof(typename Vec<T>::v4);
+    raster_fwd_kernel<T><<<dim3(n_keys), dim3(bs), smem, stream>>>(
+        means2d, conics, opac, mus, tile_offsets, flatten_ids, n_isects, n_keys, W, H, ts, tw,
+        th, image);
+  }
+#undef R2S_RASTER_FWD_ROWS
   return check_launch(name);
 }
 
-template <typename T, int R, bool kVec>
+template <typename T, int R, bool kExact>
 void launch_raster_bwd(const T *means2d, const T *conics, const T *opac, const T *mus,
                        const int32_t *tile_offsets, const int64_t *isect_ids,
                        const int32_t *flatten_ids, const int32_t *isect_src, int64_t n_isects,
                        uint32_t n_keys, int64_t n_items, const T *v_image, uint32_t W,
-                       uint32_t H, uint32_t ts, uint32_t tw, uint32_t th, T *v_xy_abs, T *v_xy,
-                       T *v_conic, T *v_opac, T *v_mu, T *rows, hipStream_t stream) {
+                       uint32_t H, uint32_t ts, uint32_t tw, uint32_t th, bool vec, T *v_xy_abs,
+                       T *v_xy, T *v_conic, T *v_opac, T *v_mu, T *rows, hipStream_t stream) {
   const dim3 grid(static_cast<uint32_t>(ceil_div(n_isects, kBwdThreads)));
   const dim3 block(kBwdThreads);
 #define R2S_RASTER_BWD_LAUNCH(ABS, ROWS)                                                         \
-  raster_bwd_kernel<T, R, ABS, ROWS, kVec><<<grid, block, 0, stream>>>(                        \
+  raster_bwd_kernel<T, R, kExact, ABS, ROWS><<<grid, block, 0, stream>>>(                      \
       means2d, conics, opac, mus, tile_offsets, isect_ids, flatten_ids, isect_src, n_isects,     \
-      n_keys, n_items, v_image, W, H, ts, tw, th, v_xy_abs, v_xy, v_conic, v_opac, v_mu, rows)
+      n_keys, n_items, v_image, W, H, ts, tw, th, vec, v_xy_abs, v_xy, v_conic, v_opac, v_mu,    \
+      rows)
   if (v_xy_abs != nullptr) {
     if (rows != nullptr)
       R2S_RASTER_BWD_LAUNCH(true, true);
@@ -375,26 +525,21 @@ int raster_bwd_impl(const T *means2d, const T *conics, const T *opac, const T *m
   hipStream_t stream = as_stream(st);
   // 16-byte loads of gradient rows when every row segment starts aligned.
   const bool vec = vec_rows_ok<T>(v_image, W, ts);
-#define R2S_RASTER_BWD_R(RR, VEC)                                                                \
-  launch_raster_bwd<T, RR, VEC>(means2d, conics, opac, mus, tile_offsets, isect_ids,             \
-                                flatten_ids, isect_src, n_isects, n_keys, C * N, v_image, W, H,  \
-                                ts, tw, th, v_xy_abs, v_xy, v_conic, v_opac, v_mu, rows, stream)
-  if (ts <= 8) {
-    if (vec)
-      R2S_RASTER_BWD_R(8, true);
-    else
-      R2S_RASTER_BWD_R(8, false);
-  } else if (ts <= 16) {
-    if (vec)
-      R2S_RASTER_BWD_R(16, true);
-    else
-      R2S_RASTER_BWD_R(16, false);
-  } else {
-    if (vec)
-      R2S_RASTER_BWD_R(32, true);
-    else
-      R2S_RASTER_BWD_R(32, false);
-  }
+#define R2S_RASTER_BWD_R(RR, EXACT)                                                              \
+  launch_raster_bwd<T, RR, EXACT>(means2d, conics, opac, mus, tile_offsets, isect_ids,           \
+                                  flatten_ids, isect_src, n_isects, n_keys, C * N, v_image, W,   \
+                                  H, ts, tw, th, vec, v_xy_abs, v_xy, v_conic, v_opac, v_mu,     \
+                                  rows, stream)
+  if (ts == 16)
+    R2S_RASTER_BWD_R(16, true);
+  else if (ts == 8)
+    R2S_RASTER_BWD_R(8, true);
+  else if (ts < 8)
+    R2S_RASTER_BWD_R(8, false);
+  else if (ts < 16)
+    R2S_RASTER_BWD_R(16, false);
+  else
+    R2S_RASTER_BWD_R(32, false);
 #undef R2S_RASTER_BWD_R
   R2S_RETURN_IF(check_launch(name));
   if (!two_pass) return R2S_OK;

@@ -216,22 +216,50 @@ __device__ __forceinline__ void load_bwd_record(const T *__restrict__ means3d,
     rec.live = false;
 }
 
+// Moments of one brick row for one record: s0 = sum w, s1 = sum w dx,
+// s2 = sum w dx^2 over the row's passing voxels (w = v exp(-sigma)).  vv
+// holds the row's upstream gradient (zero beyond the volume).  kGuard: also
+// exclude columns k >= nk explicitly -- needed only for records whose sigma
+// may be -inf or NaN, for which v = 0 would not make w = 0.
+template <typename T, int R, bool kExact, bool kGuard>
+__device__ __forceinline__ void voxel_row(const BwdRecord<T> &rec, const T (&vv)[R], T dx0,
+                                          int nk, int nts, T B, T C, T &s0, T &s1, T &s2) {
+  const T thr = static_cast<T>(kThr3);
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    if (!kExact && k >= nts) break;
+    const T dx = dx0 + static_cast<T>(k);
+    const T sl = (rec.h[0] * dx + B) * dx + C;
+    const T e = neg_exp2(sl);
+    bool skip = (sl < static_cast<T>(0)) || (fabs(rec.o * e) < thr);
+    if (kGuard) skip = skip || k >= nk;
+    const T w = skip ? static_cast<T>(0) : vv[k] * e;
+    s0 += w;
+    const T wx = w * dx;
+    s1 += wx;
+    s2 += wx * dx;
+  }
+}
+
 // Records in brick order (tile_offsets, flatten_ids; isect_ids optional),
 // one lane per record.  kRows = false: each record's ten partials go out
 // through global atomics.  kRows = true: they are stored as the row
-// isect_src[r] of `rows` (see r2s_rows.h), zeros included.
-template <typename T, int R, bool kRows, bool kVec>
+// isect_src[r] of `rows` (see r2s_rows.h), zeros included.  kExact: the
+// brick size equals R (loops fully unrolled); otherwise ts <= R at run time.
+template <typename T, int R, bool kExact, bool kRows>
 __global__ __launch_bounds__(kBwdThreads) void voxel_bwd_kernel(
     const T *__restrict__ means3d, const T *__restrict__ conics, const T *__restrict__ opac,
     const int32_t *__restrict__ tile_offsets, const int64_t *__restrict__ isect_ids,
     const int32_t *__restrict__ flatten_ids, const int32_t *__restrict__ isect_src,
     int64_t n_isects, uint32_t n_keys, int64_t N, const T *__restrict__ v_vol, uint32_t D2,
-    uint32_t D1, uint32_t D0, uint32_t ts, uint32_t n2, uint32_t n1, T *__restrict__ v_means,
-    T *__restrict__ v_conics, T *__restrict__ v_opac, T *__restrict__ rows) {
+    uint32_t D1, uint32_t D0, uint32_t ts, uint32_t n2, uint32_t n1, bool vec,
+    T *__restrict__ v_means, T *__restrict__ v_conics, T *__restrict__ v_opac,
+    T *__restrict__ rows) {
   const int64_t rb = static_cast<int64_t>(blockIdx.x) * kBwdThreads + 64 * wave_index();
   if (rb >= n_isects) return;  // uniform per wave
   const int64_t r = rb + lane_id();
   const bool in_list = r < n_isects;
+  const int nts = kExact ? R : static_cast<int>(ts);
   uint32_t key;
   bool key_ok = in_list;
   if (isect_ids != nullptr) {
@@ -242,16 +270,19 @@ __global__ __launch_bounds__(kBwdThreads) void voxel_bwd_kernel(
     key = wave_record_key(tile_offsets, n_keys, n_isects, rb, r);
   }
   const int64_t g = key_ok ? static_cast<int64_t>(flatten_ids[r]) : -1;
-  const Brick b = brick_of(key, n2, n1, ts, D2, D1, D0);
+  const Brick b = brick_of(key, n2, n1, static_cast<uint32_t>(nts), D2, D1, D0);
   BwdRecord<T> rec;
   load_bwd_record(means3d, conics, opac, g, N, key_ok, b, rec);
-  const T thr = static_cast<T>(kThr3), half = static_cast<T>(0.5);
-  const T px0 = static_cast<T>(b.ok) + half;
+  const T half = static_cast<T>(0.5);
+  const T dx0 = (static_cast<T>(b.ok) + half) - rec.m[0];
   const int64_t plane = static_cast<int64_t>(D1) * D2;
+  // Columns past the volume matter only for records whose sigma may be
+  // non-finite (uniform over the wave).
+  const bool guard = ballot(rec.live && !rec.cu.ok && b.nk < nts) != 0;
   T T0 = 0, T1 = 0, T2 = 0, Y0 = 0, Z0 = 0, Y1 = 0, Z1 = 0, YY = 0, YZ = 0, ZZ = 0;
   if (ballot(rec.live) != 0) {
     for (int li = 0; li < R; ++li) {
-      if (li >= static_cast<int>(ts)) break;
+      if (!kExact && li >= nts) break;
       const int i = b.oi + li;
       const bool in_slice = rec.live && i >= rec.i0 && i <= rec.i1;
       if (ballot(in_slice) == 0) continue;
@@ -268,7 +299,7 @@ __global__ __launch_bounds__(kBwdThreads) void voxel_bwd_kernel(
       }
       const T h4dz = rec.h[4] * dz, h5dzz = rec.h[5] * dz * dz, Bz = rec.h[2] * dz;
       for (int lj = 0; lj < R; ++lj) {
-        if (lj >= static_cast<int>(ts)) break;
+        if (!kExact && lj >= nts) break;
         const int j = b.oj + lj;
         const bool in_row = j >= j0 && j <= j1;
         if (ballot(in_row) == 0) continue;
@@ -279,23 +310,15 @@ __global__ __launch_bounds__(kBwdThreads) void voxel_bwd_kernel(
             v_vol +
             (in_row ? static_cast<int64_t>(i) * plane + static_cast<int64_t>(j) * D2 : 0) + b.ok;
         T vv[R];
-        load_grad_row<T, R, kVec>(vrow, in_row, b.nk, static_cast<int>(ts), vv);
+        if (vec)
+          load_grad_row<T, R, true>(vrow, in_row, b.nk, nts, vv);
+        else
+          load_grad_row<T, R, false>(vrow, in_row, b.nk, nts, vv);
         T s0 = 0, s1 = 0, s2 = 0;
-#pragma unroll
-        for (int k = 0; k < R; ++k) {
-          if (k >= static_cast<int>(ts)) break;
-          const bool here = in_row && k < b.nk;
-          const T v = vv[k];
-          const T dx = (px0 + static_cast<T>(k)) - rec.m[0];
-          const T sl = (rec.h[0] * dx + B) * dx + C;
-          const T e = neg_exp2(sl);
-          const bool skip = !here || (sl < static_cast<T>(0)) || (fabs(rec.o * e) < thr);
-          const T w = skip ? static_cast<T>(0) : v * e;
-          s0 += w;
-          const T wx = w * dx;
-          s1 += wx;
-          s2 += wx * dx;
-        }
+        if (guard)
+          voxel_row<T, R, kExact, true>(rec, vv, dx0, b.nk, nts, B, C, s0, s1, s2);
+        else
+          voxel_row<T, R, kExact, false>(rec, vv, dx0, b.nk, nts, B, C, s0, s1, s2);
         T0 += s0;
         T1 += s1;
         T2 += s2;
@@ -399,22 +422,22 @@ int voxel_fwd_impl(const T *means3d, const T *conics, const T *opac,
   return check_launch(name);
 }
 
-template <typename T, int R, bool kVec>
+template <typename T, int R, bool kExact>
 void launch_voxel_bwd(const T *means3d, const T *conics, const T *opac,
                       const int32_t *tile_offsets, const int64_t *isect_ids,
                       const int32_t *flatten_ids, const int32_t *isect_src, int64_t n_isects,
                       uint32_t n_keys, int64_t N, const T *v_vol, uint32_t D2, uint32_t D1,
-                      uint32_t D0, uint32_t ts, uint32_t n2, uint32_t n1, T *v_means,
+                      uint32_t D0, uint32_t ts, uint32_t n2, uint32_t n1, bool vec, T *v_means,
                       T *v_conics, T *v_opac, T *rows, hipStream_t stream) {
   const dim3 grid(static_cast<uint32_t>(ceil_div(n_isects, kBwdThreads)));
   if (rows != nullptr)
-    voxel_bwd_kernel<T, R, true, kVec><<<grid, dim3(kBwdThreads), 0, stream>>>(
+    voxel_bwd_kernel<T, R, kExact, true><<<grid, dim3(kBwdThreads), 0, stream>>>(
         means3d, conics, opac, tile_offsets, isect_ids, flatten_ids, isect_src, n_isects, n_keys,
-        N, v_vol, D2, D1, D0, ts, n2, n1, v_means, v_conics, v_opac, rows);
+        N, v_vol, D2, D1, D0, ts, n2, n1, vec, v_means, v_conics, v_opac, rows);
   else
-    voxel_bwd_kernel<T, R, false, kVec><<<grid, dim3(kBwdThreads), 0, stream>>>(
+    voxel_bwd_kernel<T, R, kExact, false><<<grid, dim3(kBwdThreads), 0, stream>>>(
         means3d, conics, opac, tile_offsets, isect_ids, flatten_ids, isect_src, n_isects, n_keys,
-        N, v_vol, D2, D1, D0, ts, n2, n1, v_means, v_conics, v_opac, rows);
+        N, v_vol, D2, D1, D0, ts, n2, n1, vec, v_means, v_conics, v_opac, rows);
 }
 
 int64_t voxel_rows_bytes(int64_t n_isects, int dtype_bytes) {
@@ -457,26 +480,20 @@ int voxel_bwd_impl(const T *means3d, const T *conics, const T *opac,
   hipStream_t stream = as_stream(st);
   // 16-byte loads of gradient rows when every row segment starts aligned.
   const bool vec = vec_rows_ok<T>(v_vol, D2, ts);
-#define R2S_VOXEL_BWD_R(RR, VEC)                                                               \
-  launch_voxel_bwd<T, RR, VEC>(means3d, conics, opac, tile_offsets, isect_ids, flatten_ids,    \
-                               isect_src, n_isects, n_keys, N, v_vol, D2, D1, D0, ts, n2, n1,  \
-                               v_means, v_conics, v_opac, rows, stream)
-  if (ts <= 4) {
-    if (vec)
-      R2S_VOXEL_BWD_R(4, true);
-    else
-      R2S_VOXEL_BWD_R(4, false);
-  } else if (ts <= 8) {
-    if (vec)
-      R2S_VOXEL_BWD_R(8, true);
-    else
-      R2S_VOXEL_BWD_R(8, false);
-  } else {
-    if (vec)
-      R2S_VOXEL_BWD_R(16, true);
-    else
-      R2S_VOXEL_BWD_R(16, false);
-  }
+#define R2S_VOXEL_BWD_R(RR, EXACT)                                                             \
+  launch_voxel_bwd<T, RR, EXACT>(means3d, conics, opac, tile_offsets, isect_ids, flatten_ids,  \
+                                 isect_src, n_isects, n_keys, N, v_vol, D2, D1, D0, ts, n2, n1, \
+                                 vec, v_means, v_conics, v_opac, rows, stream)
+  if (ts == 8)
+    R2S_VOXEL_BWD_R(8, true);
+  else if (ts == 4)
+    R2S_VOXEL_BWD_R(4, true);
+  else if (ts < 4)
+    R2S_VOXEL_BWD_R(4, false);
+  else if (ts < 8)
+    R2S_VOXEL_BWD_R(8, false);
+  else
+    R2S_VOXEL_BWD_R(16, false);
 #undef R2S_VOXEL_BWD_R
   R2S_RETURN_IF(check_launch(name));
   if (!two_pass) return R2S_OK;

@@ -211,7 +211,8 @@ def _raster_case(n, seed, W_img, H_img, ts, n_views=1, dtype=torch.float32, log_
 
 @pytest.mark.parametrize("order", ["emission", "tile"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
-@pytest.mark.parametrize("shape", [(64, 64, 16), (70, 45, 16), (40, 40, 8)])
+@pytest.mark.parametrize("shape", [(64, 64, 16), (70, 45, 16), (40, 40, 8), (50, 38, 12),
+                                   (66, 40, 20)])
 def test_rasterize_fwd_bwd(dtype, shape, order):
     W_img, H_img, ts = shape
     d, m2, con, mu, op, ids, fl, off = _raster_case(3000, 7, W_img, H_img, ts, 2, dtype)
@@ -276,7 +277,8 @@ def _voxel_case(n, seed, dims, ts, dtype=torch.float32, log_mu=-3.2):
 
 @pytest.mark.parametrize("order", ["emission", "tile"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
-@pytest.mark.parametrize("dims,ts", [((32, 32, 32), 8), ((30, 20, 26), 8), ((24, 24, 24), 4)])
+@pytest.mark.parametrize("dims,ts", [((32, 32, 32), 8), ((30, 20, 26), 8), ((24, 24, 24), 4),
+                                     ((20, 18, 22), 6), ((21, 22, 20), 10)])
 def test_voxelize_fwd_bwd(dtype, dims, ts, order):
     d, m3, con, ids, fl, off = _voxel_case(2500, 8, dims, ts, dtype)
     d2, d1, d0 = dims
