@@ -234,6 +234,10 @@ __global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(const uint32_t
   hist[static_cast<int64_t>(threadIdx.x) * nblocks + blockIdx.x] = h[threadIdx.x];
 }
 
+// One block sorts its kSortTile items by digit in LDS (stable: waves in
+// order, rounds in order, lanes by ballot rank), then writes them out in
+// block-local digit order, so each digit's items leave as one contiguous run
+// of the destination (coalesced writes).
 template <bool kFinal>
 __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     const uint32_t *__restrict__ keys_in, const uint32_t *__restrict__ vals_in, int64_t n,
@@ -243,11 +247,17 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     const int32_t *__restrict__ emit_ids, int32_t *__restrict__ src_out) {
   __shared__ uint32_t cnt[4][kRadix];
   __shared__ uint32_t wbase[4][kRadix];
+  __shared__ uint32_t dbase[kRadix];   // block-local start of each digit
+  __shared__ uint32_t gbase[kRadix];   // global start of this block's run of each digit
+  __shared__ uint32_t wsum[4];
+  __shared__ uint32_t s_key[kSortTile];
+  __shared__ uint32_t s_val[kSortTile];
   const uint32_t w = threadIdx.x / 64, lane = threadIdx.x % 64;
   for (int k = threadIdx.x; k < 4 * kRadix; k += kSortThreads) (&cnt[0][0])[k] = 0;
   __syncthreads();
   const uint32_t mask = (1u << bits) - 1u;
-  const int64_t first = static_cast<int64_t>(blockIdx.x) * kSortTile + w * kSortWaveItems;
+  const int64_t block_first = static_cast<int64_t>(blockIdx.x) * kSortTile;
+  const int64_t first = block_first + w * kSortWaveItems;
   const uint64_t lt = lanemask_lt();
   uint32_t key[kSortRounds], val[kSortRounds], rank[kSortRounds];
 #pragma unroll
@@ -273,13 +283,22 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
   }
   __syncthreads();
   {
+    // Per digit: wave offsets, block total, then the exclusive scan of the
+    // totals over digits (one digit per thread, 4 waves of 64).
     const uint32_t d = threadIdx.x;
-    uint32_t s = 0;
+    uint32_t tot = 0;
 #pragma unroll
     for (int ww = 0; ww < 4; ++ww) {
-      wbase[ww][d] = s;
-      s += cnt[ww][d];
+      wbase[ww][d] = tot;
+      tot += cnt[ww][d];
     }
+    const uint32_t incl = wave_inclusive_scan(tot);
+    if (lane == 63) wsum[w] = incl;
+    __syncthreads();
+    uint32_t before = 0;
+    for (uint32_t ww = 0; ww < w; ++ww) before += wsum[ww];
+    dbase[d] = before + incl - tot;
+    gbase[d] = digit_offsets[static_cast<int64_t>(d) * nblocks + blockIdx.x];
   }
   __syncthreads();
 #pragma unroll
@@ -287,21 +306,28 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     const int64_t i = first + r * 64 + lane;
     if (i < n) {
       const uint32_t d = (key[r] >> shift) & mask;
-      const int64_t dest = static_cast<int64_t>(digit_offsets[static_cast<int64_t>(d) * nblocks +
-                                                              blockIdx.x]) +
-                           wbase[w][d] + rank[r];
-      if (kFinal) {
-        keys_out64[dest] = static_cast<int64_t>(key[r]);
-        if (emit_ids != nullptr) {  // val = emission index of the record
-          vals_out32[dest] = emit_ids[val[r]];
-          src_out[dest] = static_cast<int32_t>(val[r]);
-        } else {
-          vals_out32[dest] = static_cast<int32_t>(val[r]);
-        }
+      const uint32_t lp = dbase[d] + wbase[w][d] + rank[r];
+      s_key[lp] = key[r];
+      s_val[lp] = val[r];
+    }
+  }
+  __syncthreads();
+  const int count = static_cast<int>(min(static_cast<int64_t>(kSortTile), n - block_first));
+  for (int lp = threadIdx.x; lp < count; lp += kSortThreads) {
+    const uint32_t k = s_key[lp], v = s_val[lp];
+    const uint32_t d = (k >> shift) & mask;
+    const int64_t dest = static_cast<int64_t>(gbase[d]) + (lp - static_cast<int>(dbase[d]));
+    if (kFinal) {
+      keys_out64[dest] = static_cast<int64_t>(k);
+      if (emit_ids != nullptr) {  // v = emission index of the record
+        vals_out32[dest] = emit_ids[v];
+        src_out[dest] = static_cast<int32_t>(v);
       } else {
-        keys_out[dest] = key[r];
-        vals_out[dest] = val[r];
+        vals_out32[dest] = static_cast<int32_t>(v);
       }
+    } else {
+      keys_out[dest] = k;
+      vals_out[dest] = v;
     }
   }
 }
