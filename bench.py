@@ -12,6 +12,7 @@ Mvox/s and % of HBM peak), the training-step shape of config 4 (projection +
 timings, the roofline of the dominant kernel and the CPU oracle baseline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+                       [--no-voxel] [--no-train] [--kernel-reps R] [--copy-bytes B]
 """
 
 from __future__ import annotations
@@ -32,7 +33,9 @@ import numpy as np  # noqa: E402
 import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, AMD public spec
-FP32_VALU_PEAK_TFLOPS = 157.3
+# 157.3 TFLOPS fp32 vector = 2 (FMA) x 2 (packed) x 39.3 T lane instructions/s;
+# this build does not use packed fp32, so one lane instruction per lane-cycle.
+VALU_LANE_PEAK_T = 39.3
 SMIN, SMAX = 5e-4, 1.0
 EPS = 1e-8
 DET = 512
@@ -82,6 +85,49 @@ class Projection:
                                           tile_size=16, eps2d=EPS, radius_clip=3.0, absgrad=True)
         res.image.grad = self.v_images[k % 4]
         explicit.explicit_backward(state, means, quats, scales, opac)
+        return state
+
+
+class TrainStep:
+    """Config-4 training-step shape on the projection workload: projection
+    fwd+bwd of one view, plus a 128^3 voxelization over [-1, 1]^3 (the volume
+    regulariser's input; v_volume ~ N(0,1) stands in for its gradient) sharing
+    the same prepared state, plus the densify/prune compaction of a 1 % mask
+    every 100 steps."""
+
+    def __init__(self, proj: Projection, dim=128, seed=2):
+        g = torch.Generator().manual_seed(seed)
+        dev = proj.viewmats.device
+        self.proj = proj
+        self.dim = dim
+        self.v_volume = torch.randn(dim, dim, dim, generator=g).to(dev)
+        self.ranges = torch.full((3,), 2.0, device=dev)
+        self.centers = torch.zeros(3, device=dev)
+        self.masks = [torch.rand(N_PROJ, generator=g).to(dev) < 0.01 for _ in range(2)]
+        self.step_i = 0
+
+    def step(self):
+        from r2splat.ops import compact, explicit
+
+        p = self.proj
+        means, quats, scales, opac = p.params
+        for t in p.params:
+            t.grad = None
+        k = self.step_i % 360
+        state = explicit.prepare_explicit_gaussians(quats, scales, opac, scale_min=SMIN,
+                                                    scale_max=SMAX)
+        res = explicit.explicit_rasterize(state, means, p.viewmats[k:k + 1], p.Ks[k:k + 1],
+                                          img_w=p.det, img_h=p.det, tile_size=16, eps2d=EPS,
+                                          radius_clip=3.0, absgrad=True)
+        vox = explicit.explicit_voxelize(state, means, self.ranges, self.centers, dim2=self.dim,
+                                         dim1=self.dim, dim0=self.dim, tile_size=8, eps3d=EPS,
+                                         radius_clip=3.0)
+        res.image.grad = p.v_images[k % 4]
+        vox.volume.grad = self.v_volume
+        explicit.explicit_backward(state, means, quats, scales, opac)
+        if self.step_i % 100 == 0:
+            compact.split_indices(self.masks[(self.step_i // 100) % 2])
+        self.step_i += 1
         return state
 
 
@@ -147,9 +193,15 @@ def time_kernel(fn, reps):
 
 
 def kernel_breakdown(proj: Projection, reps):
-    """Event timings of each projection stage at the config-4 inputs of view 0."""
+    """Event timings of each projection stage at the config-4 inputs of view 0.
+
+    Entries other than ``binning_2d`` (count, scan, one host read, emit,
+    sort passes, offsets) are single kernel launches: the two backward passes
+    are timed apart through their C entry points."""
+    from r2splat.cuda import _backend, _ops
     from r2splat.cuda import _wrapper as W
 
+    lib = _backend.library()
     means, quats, scales, opac = proj.params
     vm, Ks, det = proj.viewmats[:1], proj.Ks[:1], proj.det
     cov, ms, op = W.prepare_gaussians(quats.detach(), scales.detach(), opac.detach(), SMIN, SMAX)
@@ -158,8 +210,30 @@ def kernel_breakdown(proj: Projection, reps):
     nt = -(-det // 16)
     _, ids, fl = W.isect_tiles(m2, r, 16, nt, nt)
     off = W.isect_offset_encode(ids, 1, nt, nt)
+    emit_ids, isect_src = _ops._emission_order(fl, nt * nt)
     v_img = proj.v_images[0]
-    out = {"n_isects_2d": int(fl.numel())}
+    n = int(fl.numel())
+    rows = torch.empty(lib.r2s_rasterize_bwd_workspace_bytes(n, 4), dtype=torch.uint8,
+                       device=m2.device)
+    outs = [torch.zeros_like(m2), torch.zeros_like(m2), torch.zeros_like(con),
+            torch.zeros_like(opc), torch.zeros_like(mu)]
+    P = _ops._ptr
+
+    def bwd_rows():
+        stream = torch.cuda.current_stream().cuda_stream
+        rc = lib.r2s_rasterize_bwd_rows_f32(P(m2), P(con), P(opc), P(mu), P(off), P(ids), P(fl),
+                                            P(isect_src), n, P(v_img), 1, N_PROJ, det, det, 16,
+                                            nt, nt, 1, P(rows), rows.numel(), stream)
+        assert rc == 0, lib.r2s_last_error()
+
+    def bwd_reduce():
+        stream = torch.cuda.current_stream().cuda_stream
+        rc = lib.r2s_rasterize_bwd_reduce_f32(P(rows), P(emit_ids), n, 1, N_PROJ, P(outs[0]),
+                                              P(outs[1]), P(outs[2]), P(outs[3]), P(outs[4]),
+                                              stream)
+        assert rc == 0, lib.r2s_last_error()
+
+    out = {"n_isects_2d": n}
     t = {}
     t["prepare"] = time_kernel(lambda: W.prepare_gaussians(quats.detach(), scales.detach(),
                                                            opac.detach(), SMIN, SMAX), reps)
@@ -168,10 +242,27 @@ def kernel_breakdown(proj: Projection, reps):
     t["binning_2d"] = time_kernel(lambda: W.isect_tiles(m2, r, 16, nt, nt), reps)
     t["rasterize_fwd"] = time_kernel(lambda: W.rasterize_to_pixels_fwd(
         m2, con, opc, mu, off, fl, det, det, 16), reps)
-    t["rasterize_bwd"] = time_kernel(lambda: W.rasterize_to_pixels_bwd_per_gaussian(
+    t["rasterize_bwd_rows"] = time_kernel(bwd_rows, reps)
+    t["rasterize_bwd_reduce"] = time_kernel(bwd_reduce, reps)
+    t["rasterize_bwd_op"] = time_kernel(lambda: W.rasterize_to_pixels_bwd_per_gaussian(
         m2, con, opc, mu, off, ids, fl, v_img, det, det, 16, True), reps)
     out["seconds"] = t
     return out
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 --pmc
+    summary (profiles/pmc_<kernel>.txt, line ``hbm_bytes_per_launch: N``), or
+    None when no such measurement is committed."""
+    path = os.path.join(ROOT, "profiles", f"pmc_{kernel}.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("hbm_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def proj_bytes(n, i2, p):
@@ -184,11 +275,12 @@ def vox_bytes(n, i3, v):
     return 144 * n + 156 * i3 + 8 * v
 
 
-def cpu_baseline(proj: Projection, stride=8):
+def cpu_baseline(proj: Projection, stride=1):
     """Oracle (numpy + sequential C, one core) projection fwd+bwd on a seeded
-    random 1/``stride`` subset of the config-4 Gaussians, 512^2, view 0; the
-    time is scaled by ``stride`` to the full set (work is linear in the
-    number of tile records).  Returns (calls/s, seconds, sample text)."""
+    random 1/``stride`` subset of the config-4 Gaussians (by default all of
+    them: about 15 s of CPU work), 512^2, view 0; the time is scaled by
+    ``stride`` to the full set (work is linear in the number of tile
+    records).  Returns (calls/s, seconds, sample text)."""
     from oracle import compose
 
     raw = proj.raw
@@ -207,9 +299,13 @@ def cpu_baseline(proj: Projection, stride=8):
     compose.explicit_backward(covars, fwd, None, means, quats, scales, opac, SMIN, SMAX, v_img)
     dt = time.perf_counter() - t0
     n_s = means.shape[0]
-    sample = (f"oracle projection fwd+bwd (numpy + sequential C, 1 core) on a seeded random "
-              f"{n_s} of the {raw.n} config-4 Gaussians, 512^2, view 0, "
-              f"{fwd['isect_ids'].size} tile records; time x{stride} to the full set")
+    if stride == 1:
+        sample = (f"oracle projection fwd+bwd (numpy + sequential C, 1 core) on all {raw.n} "
+                  f"config-4 Gaussians, 512^2, view 0, {fwd['isect_ids'].size} tile records")
+    else:
+        sample = (f"oracle projection fwd+bwd (numpy + sequential C, 1 core) on a seeded random "
+                  f"{n_s} of the {raw.n} config-4 Gaussians, 512^2, view 0, "
+                  f"{fwd['isect_ids'].size} tile records; time x{stride} to the full set")
     return 1.0 / (dt * stride), dt, sample
 
 
@@ -220,7 +316,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-voxel", action="store_true")
+    ap.add_argument("--no-train", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=10)
+    ap.add_argument("--copy-bytes", type=int, default=0,
+                    help="also run a plain device copy of this many bytes 3 times (the "
+                         "reference kernel for calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the r2splat path has no "
@@ -267,28 +367,51 @@ def main():
                       "hbm_frac": b_proj / t_proj / (HBM_PEAK_GBS * 1e9),
                       "kernel_ms": {k: v * 1e3 for k, v in kb["seconds"].items()}}
 
-    # Dominant kernel and its roofline.
+    # Dominant single kernel and its roofline (binning_2d and the backward op
+    # span several launches and are not candidates).
     secs = kb["seconds"]
-    dom = max(secs, key=secs.get)
+    single = {k: v for k, v in secs.items() if k not in ("binning_2d", "rasterize_bwd_op")}
+    dom = max(single, key=single.get)
     n_pix = DET * DET
     dom_bytes = {
-        "rasterize_bwd": 76 * i2 + 4 * n_pix,   # key 8 + id 4 + payload 28 + partials 36
+        # list (key 8 + id 4) + payload 28 + partials 36 per record; v_image read
+        "rasterize_bwd_rows": 76 * i2 + 4 * n_pix,
+        "rasterize_bwd_reduce": 64 * i2 + 4 * i2 + 36 * N_PROJ,
         "rasterize_fwd": 32 * i2 + 4 * n_pix,   # id 4 + payload 28; image write
-        "binning_2d": 16 * N_PROJ + 12 * i2,
         "project_fwd": 108 * N_PROJ,
         "prepare": 76 * N_PROJ,
     }[dom]
     evals = 256 * i2
-    flops_per_eval = {"rasterize_fwd": 16, "rasterize_bwd": 40}.get(dom, 0)
+    flops_per_eval = {"rasterize_fwd": 10, "rasterize_bwd_rows": 20}.get(dom, 0)
+    traffic = measured_traffic(dom)
     result["roofline"] = {
         "kernel": dom, "bound": "hbm",
         "achieved": dom_bytes / secs[dom] / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-        "frac": dom_bytes / secs[dom] / 1e9 / HBM_PEAK_GBS, "traffic": None,
+        "frac": dom_bytes / secs[dom] / 1e9 / HBM_PEAK_GBS, "traffic": traffic,
         "algorithmic_bytes": dom_bytes, "avg_launch_ms": secs[dom] * 1e3,
-        "valu": {"evaluations": evals, "flops_per_eval": flops_per_eval,
-                 "achieved_tflops": evals * flops_per_eval / secs[dom] / 1e12,
-                 "peak_tflops": FP32_VALU_PEAK_TFLOPS},
+        "valu": {"evaluations": evals, "vector_instructions_per_eval": flops_per_eval,
+                 "achieved_t_lane_instructions_per_s": evals * flops_per_eval / secs[dom] / 1e12,
+                 "peak_t_lane_instructions_per_s": VALU_LANE_PEAK_T},
     }
+
+    if args.copy_bytes > 0:
+        src = torch.ones(args.copy_bytes // 4, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.mul(src, 1.0, out=dst)  # reads and writes copy_bytes each
+        torch.cuda.synchronize()
+        result["copy_calibration_bytes"] = args.copy_bytes
+
+    if not args.no_train:
+        log("config-4 training-step shape (projection + 128^3 voxelization + compaction / 100)")
+        train = TrainStep(proj)
+        n_train = max(100, args.steps)
+        t_train = time_steps(train.step, n_train, args.warmup)
+        result["train_step"] = {
+            "workload": "config4 training-step shape: projection fwd+bwd + 128^3 voxelize "
+                        "fwd+bwd over [-1,1]^3 + compaction of a 1% mask every 100 steps",
+            "steps": n_train, "ms_per_step": t_train * 1e3, "steps_per_s": 1.0 / t_train}
+        log(f"training-step shape: {t_train * 1e3:.3f} ms/step")
 
     if not args.no_voxel:
         log("building config-3 voxelization workload (200k Gaussians, 256^3)")

@@ -465,7 +465,8 @@ void launch_raster_bwd(const T *means2d, const T *conics, const T *opac, const T
                        const int32_t *flatten_ids, const int32_t *isect_src, int64_t n_isects,
                        uint32_t n_keys, int64_t n_items, const T *v_image, uint32_t W,
                        uint32_t H, uint32_t ts, uint32_t tw, uint32_t th, bool vec, T *v_xy_abs,
-                       T *v_xy, T *v_conic, T *v_opac, T *v_mu, T *rows, hipStream_t stream) {
+                       T *v_xy, T *v_conic, T *v_opac, T *v_mu, T *rows, bool absgrad,
+                       hipStream_t stream) {
   const dim3 grid(static_cast<uint32_t>(ceil_div(n_isects, kBwdThreads)));
   const dim3 block(kBwdThreads);
 #define R2S_RASTER_BWD_LAUNCH(ABS, ROWS)                                                         \
@@ -473,7 +474,7 @@ void launch_raster_bwd(const T *means2d, const T *conics, const T *opac, const T
       means2d, conics, opac, mus, tile_offsets, isect_ids, flatten_ids, isect_src, n_isects,     \
       n_keys, n_items, v_image, W, H, ts, tw, th, vec, v_xy_abs, v_xy, v_conic, v_opac, v_mu,    \
       rows)
-  if (v_xy_abs != nullptr) {
+  if (v_xy_abs != nullptr || (rows != nullptr && absgrad)) {
     if (rows != nullptr)
       R2S_RASTER_BWD_LAUNCH(true, true);
     else
@@ -491,7 +492,33 @@ int64_t raster_rows_bytes(int64_t n_isects, int dtype_bytes) {
   return n_isects * kRowStride * static_cast<int64_t>(dtype_bytes);
 }
 
-// emit_ids / isect_src / ws non-null: the two-pass form (r2s_rows.h).
+// Second pass of the two-pass backward: per-Gaussian sums of the rows.
+template <typename T>
+int raster_reduce_impl(const T *rows, const int32_t *emit_ids, int64_t n_isects, int64_t C,
+                       int64_t N, T *v_xy_abs, T *v_xy, T *v_conic, T *v_opac, T *v_mu,
+                       r2s_stream_t st) {
+  const char *name = "rasterize_to_pixels_bwd (row reduction)";
+  R2S_REQUIRE(C >= 0 && N >= 0 && C * N <= kInt32Max && n_isects >= 0 && n_isects <= kInt32Max,
+              "%s: bad size", name);
+  if (C * N == 0 || n_isects == 0) return R2S_OK;
+  R2S_REQUIRE(rows && emit_ids && v_xy && v_conic && v_opac && v_mu, "%s: null pointer", name);
+  R2S_REQUIRE(reinterpret_cast<uintptr_t>(rows) % 16 == 0, "%s: rows not 16-byte aligned", name);
+  hipStream_t stream = as_stream(st);
+  if (v_xy_abs != nullptr) {
+    RowTargets<T, 9> tg = {{v_xy, v_xy + 1, v_conic, v_conic + 1, v_conic + 2, v_opac, v_mu,
+                            v_xy_abs, v_xy_abs + 1},
+                           {2, 2, 3, 3, 3, 1, 1, 2, 2}};
+    launch_row_reduce(rows, emit_ids, n_isects, C * N, tg, stream);
+  } else {
+    RowTargets<T, 7> tg = {{v_xy, v_xy + 1, v_conic, v_conic + 1, v_conic + 2, v_opac, v_mu},
+                           {2, 2, 3, 3, 3, 1, 1}};
+    launch_row_reduce(rows, emit_ids, n_isects, C * N, tg, stream);
+  }
+  return check_launch(name);
+}
+
+// two_pass: emit_ids / isect_src / ws give the two-pass form (r2s_rows.h);
+// rows_only stops after the first pass (the rows are left in ws).
 template <typename T>
 int raster_bwd_impl(const T *means2d, const T *conics, const T *opac, const T *mus,
                     const int32_t *tile_offsets, const int64_t *isect_ids,
@@ -499,7 +526,8 @@ int raster_bwd_impl(const T *means2d, const T *conics, const T *opac, const T *m
                     const int32_t *isect_src, int64_t n_isects, const T *v_image, int64_t C,
                     int64_t N, uint32_t W, uint32_t H, uint32_t ts, uint32_t tw, uint32_t th,
                     T *v_xy_abs, T *v_xy, T *v_conic, T *v_opac, T *v_mu, void *ws,
-                    size_t ws_bytes, bool two_pass, r2s_stream_t st) {
+                    size_t ws_bytes, bool two_pass, r2s_stream_t st, bool rows_only = false,
+                    bool absgrad = true) {
   clear_error();
   const char *name = two_pass   ? "rasterize_to_pixels_bwd (two-pass)"
                      : isect_ids ? "rasterize_to_pixels_bwd_per_gaussian"
@@ -507,11 +535,11 @@ int raster_bwd_impl(const T *means2d, const T *conics, const T *opac, const T *m
   R2S_RETURN_IF(check_raster_args(n_isects, C, N, W, H, ts, tw, th, name));
   if (C * N == 0 || n_isects == 0) return R2S_OK;
   R2S_REQUIRE(tile_offsets && flatten_ids, "%s: null tile lists", name);
-  R2S_REQUIRE(means2d && conics && opac && mus && v_image && v_xy && v_conic && v_opac && v_mu,
-              "%s: null pointer", name);
+  R2S_REQUIRE(means2d && conics && opac && mus && v_image, "%s: null pointer", name);
+  R2S_REQUIRE(rows_only || (v_xy && v_conic && v_opac && v_mu), "%s: null output", name);
   T *rows = nullptr;
   if (two_pass) {
-    R2S_REQUIRE(emit_ids && isect_src, "%s: null emit_ids / isect_src", name);
+    R2S_REQUIRE(isect_src && (rows_only || emit_ids), "%s: null emit_ids / isect_src", name);
     const int64_t need = raster_rows_bytes(n_isects, sizeof(T));
     if (ws == nullptr || static_cast<int64_t>(ws_bytes) < need) {
       set_error("%s: workspace of %zu bytes, %lld required", name, ws_bytes, (long long)need);
@@ -529,7 +557,7 @@ int raster_bwd_impl(const T *means2d, const T *conics, const T *opac, const T *m
   launch_raster_bwd<T, RR, EXACT>(means2d, conics, opac, mus, tile_offsets, isect_ids,           \
                                   flatten_ids, isect_src, n_isects, n_keys, C * N, v_image, W,   \
                                   H, ts, tw, th, vec, v_xy_abs, v_xy, v_conic, v_opac, v_mu,     \
-                                  rows, stream)
+                                  rows, absgrad, stream)
   if (ts == 16)
     R2S_RASTER_BWD_R(16, true);
   else if (ts == 8)
@@ -542,18 +570,9 @@ int raster_bwd_impl(const T *means2d, const T *conics, const T *opac, const T *m
     R2S_RASTER_BWD_R(32, false);
 #undef R2S_RASTER_BWD_R
   R2S_RETURN_IF(check_launch(name));
-  if (!two_pass) return R2S_OK;
-  if (v_xy_abs != nullptr) {
-    RowTargets<T, 9> tg = {{v_xy, v_xy + 1, v_conic, v_conic + 1, v_conic + 2, v_opac, v_mu,
-                            v_xy_abs, v_xy_abs + 1},
-                           {2, 2, 3, 3, 3, 1, 1, 2, 2}};
-    launch_row_reduce(rows, emit_ids, n_isects, C * N, tg, stream);
-  } else {
-    RowTargets<T, 7> tg = {{v_xy, v_xy + 1, v_conic, v_conic + 1, v_conic + 2, v_opac, v_mu},
-                           {2, 2, 3, 3, 3, 1, 1}};
-    launch_row_reduce(rows, emit_ids, n_isects, C * N, tg, stream);
-  }
-  return check_launch(name);
+  if (!two_pass || rows_only) return R2S_OK;
+  return raster_reduce_impl<T>(rows, emit_ids, n_isects, C, N, v_xy_abs, v_xy, v_conic, v_opac,
+                               v_mu, st);
 }
 
 }  // namespace
@@ -609,6 +628,31 @@ int64_t r2s_rasterize_workspace_bytes(int64_t n_keys, int64_t n_isects, uint32_t
                                    W, H, ts, tw, th, v_xy_abs, v_xy, v_conic, v_opac, v_mu,   \
                                    ws, ws_bytes, true, st);                                   \
   }
+
+#define R2S_RASTER_STAGE_API(SUF, T)                                                          \
+  int r2s_rasterize_bwd_rows_##SUF(                                                           \
+      const T *means2d, const T *conics, const T *opac, const T *mus,                         \
+      const int32_t *tile_offsets, const int64_t *isect_ids, const int32_t *flatten_ids,      \
+      const int32_t *isect_src, int64_t n_isects, const T *v_image, int64_t C, int64_t N,     \
+      uint32_t W, uint32_t H, uint32_t ts, uint32_t tw, uint32_t th, int absgrad, void *rows, \
+      size_t rows_bytes, r2s_stream_t st) {                                                   \
+    return r2s::raster_bwd_impl<T>(means2d, conics, opac, mus, tile_offsets, isect_ids,       \
+                                   flatten_ids, nullptr, isect_src, n_isects, v_image, C, N,  \
+                                   W, H, ts, tw, th, nullptr, nullptr, nullptr, nullptr,      \
+                                   nullptr, rows, rows_bytes, true, st, true, absgrad != 0);  \
+  }                                                                                           \
+  int r2s_rasterize_bwd_reduce_##SUF(const T *rows, const int32_t *emit_ids, int64_t n_isects, \
+                                     int64_t C, int64_t N, T *v_xy_abs, T *v_xy, T *v_conic,  \
+                                     T *v_opac, T *v_mu, r2s_stream_t st) {                   \
+    r2s::clear_error();                                                                       \
+    return r2s::raster_reduce_impl<T>(rows, emit_ids, n_isects, C, N, v_xy_abs, v_xy,         \
+                                      v_conic, v_opac, v_mu, st);                             \
+  }
+
+R2S_RASTER_STAGE_API(f32, float)
+R2S_RASTER_STAGE_API(f64, double)
+
+#undef R2S_RASTER_STAGE_API
 
 R2S_RASTER_API(f32, float)
 R2S_RASTER_API(f64, double)

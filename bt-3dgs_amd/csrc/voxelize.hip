@@ -444,7 +444,25 @@ int64_t voxel_rows_bytes(int64_t n_isects, int dtype_bytes) {
   return n_isects * kRowStride * static_cast<int64_t>(dtype_bytes);
 }
 
-// two_pass: emit_ids / isect_src / ws give the two-pass form (r2s_rows.h).
+// Second pass of the two-pass backward: per-Gaussian sums of the rows.
+template <typename T>
+int voxel_reduce_impl(const T *rows, const int32_t *emit_ids, int64_t n_isects, int64_t N,
+                      T *v_means, T *v_conics, T *v_opac, r2s_stream_t st) {
+  const char *name = "voxelize_to_voxels_bwd (row reduction)";
+  R2S_REQUIRE(N >= 0 && N <= kInt32Max && n_isects >= 0 && n_isects <= kInt32Max,
+              "%s: bad size", name);
+  if (N == 0 || n_isects == 0) return R2S_OK;
+  R2S_REQUIRE(rows && emit_ids && v_means && v_conics && v_opac, "%s: null pointer", name);
+  R2S_REQUIRE(reinterpret_cast<uintptr_t>(rows) % 16 == 0, "%s: rows not 16-byte aligned", name);
+  RowTargets<T, 10> tg = {{v_means, v_means + 1, v_means + 2, v_conics, v_conics + 1,
+                           v_conics + 2, v_conics + 3, v_conics + 4, v_conics + 5, v_opac},
+                          {3, 3, 3, 6, 6, 6, 6, 6, 6, 1}};
+  launch_row_reduce(rows, emit_ids, n_isects, N, tg, as_stream(st));
+  return check_launch(name);
+}
+
+// two_pass: emit_ids / isect_src / ws give the two-pass form (r2s_rows.h);
+// rows_only stops after the first pass (the rows are left in ws).
 template <typename T>
 int voxel_bwd_impl(const T *means3d, const T *conics, const T *opac,
                    const int32_t *tile_offsets, const int64_t *isect_ids,
@@ -452,7 +470,7 @@ int voxel_bwd_impl(const T *means3d, const T *conics, const T *opac,
                    const int32_t *isect_src, int64_t n_isects, const T *v_vol, int64_t N,
                    uint32_t D2, uint32_t D1, uint32_t D0, uint32_t ts, uint32_t n2, uint32_t n1,
                    uint32_t n0, T *v_means, T *v_conics, T *v_opac, void *ws, size_t ws_bytes,
-                   bool two_pass, r2s_stream_t st) {
+                   bool two_pass, r2s_stream_t st, bool rows_only = false) {
   clear_error();
   const char *name = two_pass   ? "voxelize_to_voxels_bwd (two-pass)"
                      : isect_ids ? "voxelize_to_voxels_bwd_per_gaussian"
@@ -462,11 +480,11 @@ int voxel_bwd_impl(const T *means3d, const T *conics, const T *opac,
   const int64_t n_vox = static_cast<int64_t>(D2) * D1 * D0;
   if (n_vox == 0) return R2S_OK;
   R2S_REQUIRE(tile_offsets && flatten_ids, "%s: null brick lists", name);
-  R2S_REQUIRE(means3d && conics && opac && v_vol && v_means && v_conics && v_opac,
-              "%s: null pointer", name);
+  R2S_REQUIRE(means3d && conics && opac && v_vol, "%s: null pointer", name);
+  R2S_REQUIRE(rows_only || (v_means && v_conics && v_opac), "%s: null output", name);
   T *rows = nullptr;
   if (two_pass) {
-    R2S_REQUIRE(emit_ids && isect_src, "%s: null emit_ids / isect_src", name);
+    R2S_REQUIRE(isect_src && (rows_only || emit_ids), "%s: null emit_ids / isect_src", name);
     const int64_t need = voxel_rows_bytes(n_isects, sizeof(T));
     if (ws == nullptr || static_cast<int64_t>(ws_bytes) < need) {
       set_error("%s: workspace of %zu bytes, %lld required", name, ws_bytes, (long long)need);
@@ -496,12 +514,8 @@ int voxel_bwd_impl(const T *means3d, const T *conics, const T *opac,
     R2S_VOXEL_BWD_R(16, false);
 #undef R2S_VOXEL_BWD_R
   R2S_RETURN_IF(check_launch(name));
-  if (!two_pass) return R2S_OK;
-  RowTargets<T, 10> tg = {{v_means, v_means + 1, v_means + 2, v_conics, v_conics + 1,
-                           v_conics + 2, v_conics + 3, v_conics + 4, v_conics + 5, v_opac},
-                          {3, 3, 3, 6, 6, 6, 6, 6, 6, 1}};
-  launch_row_reduce(rows, emit_ids, n_isects, N, tg, stream);
-  return check_launch(name);
+  if (!two_pass || rows_only) return R2S_OK;
+  return voxel_reduce_impl<T>(rows, emit_ids, n_isects, N, v_means, v_conics, v_opac, st);
 }
 
 }  // namespace
@@ -543,6 +557,31 @@ int64_t r2s_voxelize_bwd_workspace_bytes(int64_t n_isects, int dtype_bytes) {
                                   emit_ids, isect_src, n_isects, v_vol, N, D2, D1, D0, ts, n2, \
                                   n1, n0, v_means, v_conics, v_opac, ws, ws_bytes, true, st);  \
   }
+
+#define R2S_VOXEL_STAGE_API(SUF, T)                                                            \
+  int r2s_voxelize_bwd_rows_##SUF(                                                             \
+      const T *means3d, const T *conics, const T *opac, const int32_t *tile_offsets,           \
+      const int64_t *isect_ids, const int32_t *flatten_ids, const int32_t *isect_src,          \
+      int64_t n_isects, const T *v_vol, int64_t N, uint32_t D2, uint32_t D1, uint32_t D0,      \
+      uint32_t ts, uint32_t n2, uint32_t n1, uint32_t n0, void *rows, size_t rows_bytes,       \
+      r2s_stream_t st) {                                                                       \
+    return r2s::voxel_bwd_impl<T>(means3d, conics, opac, tile_offsets, isect_ids, flatten_ids, \
+                                  nullptr, isect_src, n_isects, v_vol, N, D2, D1, D0, ts, n2,  \
+                                  n1, n0, nullptr, nullptr, nullptr, rows, rows_bytes, true,   \
+                                  st, true);                                                   \
+  }                                                                                            \
+  int r2s_voxelize_bwd_reduce_##SUF(const T *rows, const int32_t *emit_ids, int64_t n_isects,  \
+                                    int64_t N, T *v_means, T *v_conics, T *v_opac,             \
+                                    r2s_stream_t st) {                                         \
+    r2s::clear_error();                                                                        \
+    return r2s::voxel_reduce_impl<T>(rows, emit_ids, n_isects, N, v_means, v_conics, v_opac,   \
+                                     st);                                                      \
+  }
+
+R2S_VOXEL_STAGE_API(f32, float)
+R2S_VOXEL_STAGE_API(f64, double)
+
+#undef R2S_VOXEL_STAGE_API
 
 R2S_VOXEL_API(f32, float)
 R2S_VOXEL_API(f64, double)

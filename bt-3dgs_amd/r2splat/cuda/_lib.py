@@ -45,6 +45,9 @@ _FLOAT_OPS = {
                       _u32, _p, _p, _p, _p, _p, _p],
     "rasterize_bwd_emit": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _u32, _u32,
                            _u32, _u32, _u32, _p, _p, _p, _p, _p, _p, _sz, _p],
+    "rasterize_bwd_rows": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _u32, _u32, _u32,
+                           _u32, _u32, _i32, _p, _sz, _p],
+    "rasterize_bwd_reduce": [_p, _p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p],
     "world_to_volume_mapping_fwd": [_p, _p, _p, _p, _u32, _u32, _u32, _f64, _f64, _p, _p, _p,
                                     _i64, _p],
     "world_to_volume_mapping_bwd": [_p, _p, _p, _p, _u32, _u32, _u32, _f64, _p, _p, _p, _p,
@@ -53,6 +56,9 @@ _FLOAT_OPS = {
                      _p, _p],
     "voxelize_bwd": [_p, _p, _p, _p, _p, _p, _i64, _p, _i64, _u32, _u32, _u32, _u32, _u32, _u32,
                      _u32, _p, _p, _p, _p],
+    "voxelize_bwd_rows": [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _u32, _u32, _u32, _u32, _u32,
+                          _u32, _u32, _p, _sz, _p],
+    "voxelize_bwd_reduce": [_p, _p, _i64, _i64, _p, _p, _p, _p],
     "voxelize_bwd_emit": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _u32, _u32, _u32, _u32,
                           _u32, _u32, _u32, _p, _p, _p, _p, _sz, _p],
 }

@@ -358,6 +358,38 @@ int r2s_rasterize_bwd_emit_f64(const double *means2d, const double *conics,
                                double *v_opacities, double *v_mus, void *workspace,
                                size_t workspace_bytes, r2s_stream_t stream);
 
+/* The two passes of r2s_rasterize_bwd_emit_* as separate calls (for callers
+ * that schedule or time them apart).  _rows: the first pass; writes the
+ * per-record rows (16 values, 9 used with absgrad != 0, else 7) at their
+ * emission index into `rows` (r2s_rasterize_bwd_workspace_bytes, 16-byte
+ * aligned).  _reduce: the second pass; stores each Gaussian's sums into the
+ * zeroed outputs (v_means2d_abs NULL exactly when the rows were written
+ * with absgrad == 0).  No reference counterpart. */
+int r2s_rasterize_bwd_rows_f32(const float *means2d, const float *conics,
+                               const float *opacities, const float *mus,
+                               const int32_t *tile_offsets, const int64_t *isect_ids,
+                               const int32_t *flatten_ids, const int32_t *isect_src,
+                               int64_t n_isects, const float *v_image, int64_t C, int64_t N,
+                               uint32_t width, uint32_t height, uint32_t tile_size,
+                               uint32_t n_tiles_w, uint32_t n_tiles_h, int absgrad,
+                               void *rows, size_t rows_bytes, r2s_stream_t stream);
+int r2s_rasterize_bwd_rows_f64(const double *means2d, const double *conics,
+                               const double *opacities, const double *mus,
+                               const int32_t *tile_offsets, const int64_t *isect_ids,
+                               const int32_t *flatten_ids, const int32_t *isect_src,
+                               int64_t n_isects, const double *v_image, int64_t C, int64_t N,
+                               uint32_t width, uint32_t height, uint32_t tile_size,
+                               uint32_t n_tiles_w, uint32_t n_tiles_h, int absgrad,
+                               void *rows, size_t rows_bytes, r2s_stream_t stream);
+int r2s_rasterize_bwd_reduce_f32(const float *rows, const int32_t *emit_ids, int64_t n_isects,
+                                 int64_t C, int64_t N, float *v_means2d_abs, float *v_means2d,
+                                 float *v_conics, float *v_opacities, float *v_mus,
+                                 r2s_stream_t stream);
+int r2s_rasterize_bwd_reduce_f64(const double *rows, const int32_t *emit_ids,
+                                 int64_t n_isects, int64_t C, int64_t N,
+                                 double *v_means2d_abs, double *v_means2d, double *v_conics,
+                                 double *v_opacities, double *v_mus, r2s_stream_t stream);
+
 /* ---------------------------------------------------------------------- */
 /* Volume mapping and voxelizer                                           */
 /* ---------------------------------------------------------------------- */
@@ -458,6 +490,31 @@ int r2s_voxelize_bwd_emit_f64(const double *means3d, const double *conics,
                               uint32_t n_tiles_d1, uint32_t n_tiles_d0, double *v_means3d,
                               double *v_conics, double *v_opacities, void *workspace,
                               size_t workspace_bytes, r2s_stream_t stream);
+
+/* The two passes of r2s_voxelize_bwd_emit_* as separate calls, as for the
+ * rasterizer (10 row values).  No reference counterpart. */
+int r2s_voxelize_bwd_rows_f32(const float *means3d, const float *conics,
+                              const float *opacities, const int32_t *tile_offsets,
+                              const int64_t *isect_ids, const int32_t *flatten_ids,
+                              const int32_t *isect_src, int64_t n_isects,
+                              const float *v_volume, int64_t N, uint32_t dim2, uint32_t dim1,
+                              uint32_t dim0, uint32_t tile_size, uint32_t n_tiles_d2,
+                              uint32_t n_tiles_d1, uint32_t n_tiles_d0, void *rows,
+                              size_t rows_bytes, r2s_stream_t stream);
+int r2s_voxelize_bwd_rows_f64(const double *means3d, const double *conics,
+                              const double *opacities, const int32_t *tile_offsets,
+                              const int64_t *isect_ids, const int32_t *flatten_ids,
+                              const int32_t *isect_src, int64_t n_isects,
+                              const double *v_volume, int64_t N, uint32_t dim2,
+                              uint32_t dim1, uint32_t dim0, uint32_t tile_size,
+                              uint32_t n_tiles_d2, uint32_t n_tiles_d1, uint32_t n_tiles_d0,
+                              void *rows, size_t rows_bytes, r2s_stream_t stream);
+int r2s_voxelize_bwd_reduce_f32(const float *rows, const int32_t *emit_ids, int64_t n_isects,
+                                int64_t N, float *v_means3d, float *v_conics,
+                                float *v_opacities, r2s_stream_t stream);
+int r2s_voxelize_bwd_reduce_f64(const double *rows, const int32_t *emit_ids,
+                                int64_t n_isects, int64_t N, double *v_means3d,
+                                double *v_conics, double *v_opacities, r2s_stream_t stream);
 
 /* ---------------------------------------------------------------------- */
 /* Densify / prune index compaction                                        */

@@ -336,3 +336,41 @@ def test_emission_order_backward_is_deterministic():
             for _ in range(2)]
     for a, b in zip(runs[0], runs[1]):
         assert torch.equal(a, b)
+
+
+def test_backward_stage_entry_points_match_the_two_pass_op():
+    from r2splat.cuda import _backend
+
+    lib, P = _backend.library(), _ops._ptr
+    st = torch.cuda.current_stream().cuda_stream
+    d, m2, con, mu, op, ids, fl, off = _raster_case(3000, 13, 64, 48, 16, 2, torch.float32)
+    v = torch.randn((2, 48, 64), generator=d["gen"]).to(DEV)
+    want = W.rasterize_to_pixels_bwd_per_gaussian(m2, con, op, mu, off, ids, fl, v, 64, 48, 16,
+                                                  True)
+    emit_ids, src = _ops._emission_order(fl, off.numel())
+    n, N = fl.numel(), m2.shape[1]
+    rows = torch.empty(lib.r2s_rasterize_bwd_workspace_bytes(n, 4), dtype=torch.uint8,
+                       device=DEV)
+    assert lib.r2s_rasterize_bwd_rows_f32(P(m2), P(con), P(op), P(mu), P(off), P(ids), P(fl),
+                                          P(src), n, P(v), 2, N, 64, 48, 16, 4, 3, 1, P(rows),
+                                          rows.numel(), st) == 0
+    got = [torch.zeros_like(t) for t in want]
+    assert lib.r2s_rasterize_bwd_reduce_f32(P(rows), P(emit_ids), n, 2, N, *[P(t) for t in got],
+                                            st) == 0
+    for a, b in zip(got, want):
+        assert torch.equal(a, b)
+    d3, m3, con3, ids3, fl3, off3 = _voxel_case(2500, 14, (32, 24, 16), 8)
+    v3 = torch.randn((16, 24, 32), generator=d3["gen"]).to(DEV)
+    want3 = W.voxelize_to_voxels_bwd(m3, con3, d3["opac"], off3, fl3, v3, 32, 24, 16, 8)
+    emit3, src3 = _ops._emission_order(fl3, off3.numel())
+    n3, N3 = fl3.numel(), m3.shape[0]
+    rows3 = torch.empty(lib.r2s_voxelize_bwd_workspace_bytes(n3, 4), dtype=torch.uint8,
+                        device=DEV)
+    assert lib.r2s_voxelize_bwd_rows_f32(P(m3), P(con3), P(d3["opac"]), P(off3), None, P(fl3),
+                                         P(src3), n3, P(v3), N3, 32, 24, 16, 8, 4, 3, 2,
+                                         P(rows3), rows3.numel(), st) == 0
+    got3 = [torch.zeros_like(t) for t in want3]
+    assert lib.r2s_voxelize_bwd_reduce_f32(P(rows3), P(emit3), n3, N3, *[P(t) for t in got3],
+                                           st) == 0
+    for a, b in zip(got3, want3):
+        assert torch.equal(a, b)
