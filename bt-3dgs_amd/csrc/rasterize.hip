@@ -213,6 +213,7 @@ struct RasterRecord {
   bool live;          // a valid record whose pixels can pass the alpha test
   T mx, my, a, b, c, o, mu, om;
   T ha, hb, hc;       // a/2, b, c/2 pre-scaled by log2(e)
+  T elo;              // 1e-5 / |o mu|: the alpha test |o mu e| >= 1e-5 as e >= elo
   int i0, i1;         // rows the alpha-test ellipse reaches (all rows when not PD)
   bool pd;            // conic positive definite and finite (sigma finite, >= 0 up to rounding)
 };
@@ -231,6 +232,7 @@ __device__ __forceinline__ void load_raster_record(
   if (!rec.live) {
     rec.o = rec.mu = rec.om = 0;
     rec.mx = rec.my = rec.a = rec.b = rec.c = rec.ha = rec.hb = rec.hc = 0;
+    rec.elo = static_cast<T>(INFINITY);
     rec.i0 = 0;
     rec.i1 = -1;
     rec.pd = true;
@@ -244,6 +246,7 @@ __device__ __forceinline__ void load_raster_record(
   rec.ha = static_cast<T>(0.5 * kLog2e) * rec.a;
   rec.hb = static_cast<T>(kLog2e) * rec.b;
   rec.hc = static_cast<T>(0.5 * kLog2e) * rec.c;
+  rec.elo = static_cast<T>(kThr2) / fabs(rec.om);
   const Cull2<T> cu = cull2_setup(rec.a, rec.b, rec.c, fabs(rec.om), kThr2);
   rec.pd = cu.ok;
   rec.i0 = oy;
@@ -261,7 +264,6 @@ template <typename T, int R, bool kExact, bool kAbs, bool kGuard>
 __device__ __forceinline__ void raster_row(const RasterRecord<T> &rec, const T (&vv)[R], int k0,
                                            T dx0, int nx, int nts, T B, T C, T bdy, T cdy,
                                            T &s0, T &s1, T &s2, T &px, T &py) {
-  const T thr = static_cast<T>(kThr2);
 #pragma unroll
   for (int kk = 0; kk < R; ++kk) {
     const int k = k0 + kk;
@@ -269,16 +271,18 @@ __device__ __forceinline__ void raster_row(const RasterRecord<T> &rec, const T (
     const T dx = dx0 + static_cast<T>(k);
     const T sl = (rec.ha * dx + B) * dx + C;
     const T e = neg_exp2(sl);
-    bool skip = (sl < static_cast<T>(0)) || (fabs(rec.om * e) < thr);
+    // |o mu e| < 1e-5 tested as e < 1e-5 / |o mu| (equal up to the rounding
+    // of the cut-off itself).
+    bool skip = (sl < static_cast<T>(0)) || (e < rec.elo);
     if (kGuard) skip = skip || k >= nx;
     const T w = skip ? static_cast<T>(0) : vv[kk] * e;
     s0 += w;
     const T wx = w * dx;
     s1 += wx;
     s2 += wx * dx;
-    if (kAbs) {
-      px += fabs(w * (rec.a * dx + bdy));
-      py += fabs(w * (rec.b * dx + cdy));
+    if (kAbs) {  // |w t| = |w| |t|: one FMA with source modifiers
+      px = fma(fabs(w), fabs(rec.a * dx + bdy), px);
+      py = fma(fabs(w), fabs(rec.b * dx + cdy), py);
     }
   }
 }
@@ -298,7 +302,9 @@ __global__ __launch_bounds__(kBwdThreads) void raster_bwd_kernel(
     uint32_t th, bool vec, T *__restrict__ v_xy_abs, T *__restrict__ v_xy,
     T *__restrict__ v_conic, T *__restrict__ v_opac, T *__restrict__ v_mu,
     T *__restrict__ rows) {
-  const int64_t rb = static_cast<int64_t>(blockIdx.x) * kBwdThreads + 64 * wave_index();
+  // Consecutive blocks (neighbouring tiles, which share Gaussians) on one XCD.
+  const int64_t rb =
+      static_cast<int64_t>(xcd_swizzle(blockIdx.x, gridDim.x)) * kBwdThreads + 64 * wave_index();
   if (rb >= n_isects) return;  // uniform per wave
   const int64_t r = rb + lane_id();
   const bool in_list = r < n_isects;

@@ -179,6 +179,7 @@ template <typename T>
 struct BwdRecord {
   bool live;     // a valid record whose voxels can pass the alpha test
   T m[3], q[6], h[6], o;
+  T elo;         // 1e-6 / |o|: the alpha test |o e| >= 1e-6 as e >= elo
   Cull3<T> cu;
   int i0, i1;    // slice range (all slices when !cu.ok)
 };
@@ -192,8 +193,10 @@ __device__ __forceinline__ void load_bwd_record(const T *__restrict__ means3d,
   rec.o = rec.live ? opac[g] : static_cast<T>(0);
   // |alpha| <= |o| for sigma >= 0: nothing passes (non-finite o stays live).
   if (fabs(rec.o) < static_cast<T>(kThr3)) rec.live = false;
+  rec.elo = static_cast<T>(kThr3) / fabs(rec.o);
   if (!rec.live) {
     rec.o = 0;
+    rec.elo = static_cast<T>(INFINITY);
 #pragma unroll
     for (int c = 0; c < 3; ++c) rec.m[c] = 0;
 #pragma unroll
@@ -224,14 +227,15 @@ __device__ __forceinline__ void load_bwd_record(const T *__restrict__ means3d,
 template <typename T, int R, bool kExact, bool kGuard>
 __device__ __forceinline__ void voxel_row(const BwdRecord<T> &rec, const T (&vv)[R], T dx0,
                                           int nk, int nts, T B, T C, T &s0, T &s1, T &s2) {
-  const T thr = static_cast<T>(kThr3);
 #pragma unroll
   for (int k = 0; k < R; ++k) {
     if (!kExact && k >= nts) break;
     const T dx = dx0 + static_cast<T>(k);
     const T sl = (rec.h[0] * dx + B) * dx + C;
     const T e = neg_exp2(sl);
-    bool skip = (sl < static_cast<T>(0)) || (fabs(rec.o * e) < thr);
+    // |o e| < 1e-6 tested as e < 1e-6 / |o| (equal up to the rounding of the
+    // cut-off itself).
+    bool skip = (sl < static_cast<T>(0)) || (e < rec.elo);
     if (kGuard) skip = skip || k >= nk;
     const T w = skip ? static_cast<T>(0) : vv[k] * e;
     s0 += w;
@@ -255,7 +259,9 @@ __global__ __launch_bounds__(kBwdThreads) void voxel_bwd_kernel(
     uint32_t D1, uint32_t D0, uint32_t ts, uint32_t n2, uint32_t n1, bool vec,
     T *__restrict__ v_means, T *__restrict__ v_conics, T *__restrict__ v_opac,
     T *__restrict__ rows) {
-  const int64_t rb = static_cast<int64_t>(blockIdx.x) * kBwdThreads + 64 * wave_index();
+  // Consecutive blocks (neighbouring tiles, which share Gaussians) on one XCD.
+  const int64_t rb =
+      static_cast<int64_t>(xcd_swizzle(blockIdx.x, gridDim.x)) * kBwdThreads + 64 * wave_index();
   if (rb >= n_isects) return;  // uniform per wave
   const int64_t r = rb + lane_id();
   const bool in_list = r < n_isects;
