@@ -21,6 +21,8 @@
 // reference's CUB sort of the same records.
 #pragma clang fp contract(off)
 
+#include <utility>
+
 #include "r2s_common.h"
 #include "r2s_scan.h"
 
@@ -129,7 +131,8 @@ template <typename T>
 __global__ __launch_bounds__(256) void emit_2d_kernel(
     const T *__restrict__ means2d, const int32_t *__restrict__ radii, int rect, int64_t M,
     int64_t N, uint32_t ts, uint32_t tw, uint32_t th, const int64_t *__restrict__ offsets,
-    uint32_t *__restrict__ keys, uint32_t *__restrict__ vals, int32_t *__restrict__ emit_ids) {
+    uint32_t *__restrict__ keys, uint32_t *__restrict__ vals, uint32_t *__restrict__ vals2,
+    int32_t *__restrict__ emit_ids) {
   const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + (threadIdx.x & ~63u);
   const int64_t idx = wave_first + lane_id();
   Rect r = {0, 0, 0, 0};
@@ -156,6 +159,7 @@ __global__ __launch_bounds__(256) void emit_2d_kernel(
       keys[base + k] = kbase + (y0 + row) * tw + (x0 + col);
       if (emit_ids != nullptr) {
         vals[base + k] = static_cast<uint32_t>(base + k);
+        vals2[base + k] = static_cast<uint32_t>(gid);
         emit_ids[base + k] = static_cast<int32_t>(gid);
       } else {
         vals[base + k] = static_cast<uint32_t>(gid);
@@ -168,7 +172,8 @@ template <typename T>
 __global__ __launch_bounds__(256) void emit_3d_kernel(
     const T *__restrict__ means3d, const int32_t *__restrict__ radii, int64_t N, uint32_t ts,
     uint32_t n2, uint32_t n1, uint32_t n0, const int64_t *__restrict__ offsets,
-    uint32_t *__restrict__ keys, uint32_t *__restrict__ vals, int32_t *__restrict__ emit_ids) {
+    uint32_t *__restrict__ keys, uint32_t *__restrict__ vals, uint32_t *__restrict__ vals2,
+    int32_t *__restrict__ emit_ids) {
   const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + (threadIdx.x & ~63u);
   const int64_t idx = wave_first + lane_id();
   const uint32_t n[3] = {n2, n1, n0};
@@ -200,6 +205,7 @@ __global__ __launch_bounds__(256) void emit_3d_kernel(
       keys[base + k] = (l0 + t0) * (n1 * n2) + (l1 + t1) * n2 + (l2 + t2);
       if (emit_ids != nullptr) {
         vals[base + k] = static_cast<uint32_t>(base + k);
+        vals2[base + k] = gid;
         emit_ids[base + k] = static_cast<int32_t>(gid);
       } else {
         vals[base + k] = gid;
@@ -237,14 +243,17 @@ __global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(const uint32_t
 // One block sorts its kSortTile items by digit in LDS (stable: waves in
 // order, rounds in order, lanes by ballot rank), then writes them out in
 // block-local digit order, so each digit's items leave as one contiguous run
-// of the destination (coalesced writes).
-template <bool kFinal>
+// of the destination (coalesced writes).  kTwo: a second payload (the flat
+// id while the first is the emission index) travels with the key; the final
+// pass then writes vals_out32 = second payload and src_out = first.
+template <bool kFinal, bool kTwo>
 __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
-    const uint32_t *__restrict__ keys_in, const uint32_t *__restrict__ vals_in, int64_t n,
-    uint32_t shift, uint32_t bits, const uint32_t *__restrict__ digit_offsets, uint32_t nblocks,
-    uint32_t *__restrict__ keys_out, uint32_t *__restrict__ vals_out,
+    const uint32_t *__restrict__ keys_in, const uint32_t *__restrict__ vals_in,
+    const uint32_t *__restrict__ vals2_in, int64_t n, uint32_t shift, uint32_t bits,
+    const uint32_t *__restrict__ digit_offsets, uint32_t nblocks, uint32_t *__restrict__ keys_out,
+    uint32_t *__restrict__ vals_out, uint32_t *__restrict__ vals2_out,
     int64_t *__restrict__ keys_out64, int32_t *__restrict__ vals_out32,
-    const int32_t *__restrict__ emit_ids, int32_t *__restrict__ src_out) {
+    int32_t *__restrict__ src_out) {
   __shared__ uint32_t cnt[4][kRadix];
   __shared__ uint32_t wbase[4][kRadix];
   __shared__ uint32_t dbase[kRadix];   // block-local start of each digit
@@ -252,6 +261,7 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
   __shared__ uint32_t wsum[4];
   __shared__ uint32_t s_key[kSortTile];
   __shared__ uint32_t s_val[kSortTile];
+  __shared__ uint32_t s_val2[kTwo ? kSortTile : 1];
   const uint32_t w = threadIdx.x / 64, lane = threadIdx.x % 64;
   for (int k = threadIdx.x; k < 4 * kRadix; k += kSortThreads) (&cnt[0][0])[k] = 0;
   __syncthreads();
@@ -259,13 +269,14 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
   const int64_t block_first = static_cast<int64_t>(blockIdx.x) * kSortTile;
   const int64_t first = block_first + w * kSortWaveItems;
   const uint64_t lt = lanemask_lt();
-  uint32_t key[kSortRounds], val[kSortRounds], rank[kSortRounds];
+  uint32_t key[kSortRounds], val[kSortRounds], val2[kSortRounds], rank[kSortRounds];
 #pragma unroll
   for (int r = 0; r < kSortRounds; ++r) {
     const int64_t i = first + r * 64 + lane;
     const bool valid = i < n;
     key[r] = valid ? keys_in[i] : 0u;
     val[r] = valid ? vals_in[i] : 0u;
+    val2[r] = (kTwo && valid) ? vals2_in[i] : 0u;
     const uint32_t d = (key[r] >> shift) & mask;
     // Lanes holding the same digit: intersect the ballots of every digit bit.
     uint64_t peers = ballot(valid);
@@ -309,6 +320,7 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
       const uint32_t lp = dbase[d] + wbase[w][d] + rank[r];
       s_key[lp] = key[r];
       s_val[lp] = val[r];
+      if (kTwo) s_val2[lp] = val2[r];
     }
   }
   __syncthreads();
@@ -319,8 +331,8 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     const int64_t dest = static_cast<int64_t>(gbase[d]) + (lp - static_cast<int>(dbase[d]));
     if (kFinal) {
       keys_out64[dest] = static_cast<int64_t>(k);
-      if (emit_ids != nullptr) {  // v = emission index of the record
-        vals_out32[dest] = emit_ids[v];
+      if (kTwo) {
+        vals_out32[dest] = static_cast<int32_t>(s_val2[lp]);
         src_out[dest] = static_cast<int32_t>(v);
       } else {
         vals_out32[dest] = static_cast<int32_t>(v);
@@ -328,6 +340,7 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     } else {
       keys_out[dest] = k;
       vals_out[dest] = v;
+      if (kTwo) vals2_out[dest] = s_val2[lp];
     }
   }
 }
@@ -353,7 +366,7 @@ __global__ __launch_bounds__(256) void offset_encode_kernel(const int64_t *__res
 // ----------------------------------------------------------- workspace ---
 
 struct SortSpace {
-  uint32_t *ka, *va, *kb, *vb, *hist, *hist_scan, *partials;
+  uint32_t *ka, *va, *wa, *kb, *vb, *wb, *hist, *hist_scan, *partials;
   int64_t nblocks, n_hist;
 };
 
@@ -363,8 +376,10 @@ SortSpace carve_sort(Carver &cv, int64_t n) {
   s.n_hist = s.nblocks * kRadix;
   s.ka = cv.take<uint32_t>(n);
   s.va = cv.take<uint32_t>(n);
+  s.wa = cv.take<uint32_t>(n);
   s.kb = cv.take<uint32_t>(n);
   s.vb = cv.take<uint32_t>(n);
+  s.wb = cv.take<uint32_t>(n);
   s.hist = cv.take<uint32_t>(s.n_hist);
   s.hist_scan = cv.take<uint32_t>(s.n_hist);
   s.partials = cv.take<uint32_t>(scan_partials_count(s.n_hist));
@@ -383,40 +398,45 @@ int64_t sort_space_bytes(int64_t n) {
   return static_cast<int64_t>(cv.used);
 }
 
-// Sorts the emitted (keys, vals) held in (kin0, vin0) into the final outputs;
-// intermediate passes ping-pong between s.kb/s.vb and s.ka/s.va.  With
-// emit_ids, vals are emission indices: the final pass writes
-// vals32[r] = emit_ids[val] and src[r] = val.
-int radix_sort(SortSpace &s, const uint32_t *kin0, const uint32_t *vin0, int64_t n,
-               uint32_t end_bit, int64_t *keys64, int32_t *vals32, const int32_t *emit_ids,
-               int32_t *src, hipStream_t stream) {
-  const int passes = static_cast<int>((end_bit + kRadixBits - 1) / kRadixBits);
-  const uint32_t *kin = kin0, *vin = vin0;
-  uint32_t *kout = s.kb, *vout = s.vb, *kalt = s.ka, *valt = s.va;
+// Sorts the emitted records held in s.ka / s.va (/ s.wa) into the final
+// outputs; passes ping-pong between the a and b buffers.  two: s.va holds
+// emission indices and s.wa flat ids; the final pass writes vals32 = flat id
+// and src = emission index.  The key bits are split evenly over the passes
+// (e.g. 6 + 5 for 11 bits): fewer digits per pass give longer runs per digit
+// and block, hence better coalesced writes.
+int radix_sort(SortSpace &s, int64_t n, uint32_t end_bit, int64_t *keys64, int32_t *vals32,
+               bool two, int32_t *src, hipStream_t stream) {
+  const uint32_t passes = (end_bit + kRadixBits - 1) / kRadixBits;
+  const uint32_t pbits = (end_bit + passes - 1) / passes;
+  uint32_t *kin = s.ka, *vin = s.va, *win = s.wa, *kout = s.kb, *vout = s.vb, *wout = s.wb;
   const uint32_t nb = static_cast<uint32_t>(s.nblocks);
-  for (int p = 0; p < passes; ++p) {
-    const uint32_t shift = static_cast<uint32_t>(p * kRadixBits);
-    const uint32_t bits = min(static_cast<uint32_t>(kRadixBits), end_bit - shift);
+  for (uint32_t p = 0; p < passes; ++p) {
+    const uint32_t shift = p * pbits;
+    const uint32_t bits = min(pbits, end_bit - shift);
     const uint32_t mask = (1u << bits) - 1u;
     radix_hist_kernel<<<dim3(nb), dim3(kSortThreads), 0, stream>>>(kin, n, shift, mask, s.hist, nb);
     R2S_RETURN_IF(device_exclusive_scan<uint32_t, uint32_t>(s.hist, s.n_hist, s.hist_scan,
                                                             nullptr, s.partials, stream,
                                                             "isect sort scan"));
-    if (p == passes - 1) {
-      radix_scatter_kernel<true><<<dim3(nb), dim3(kSortThreads), 0, stream>>>(
-          kin, vin, n, shift, bits, s.hist_scan, nb, nullptr, nullptr, keys64, vals32, emit_ids,
-          src);
+    const bool last = p == passes - 1;
+#define R2S_SCATTER(FINAL, TWO)                                                                 \
+  radix_scatter_kernel<FINAL, TWO><<<dim3(nb), dim3(kSortThreads), 0, stream>>>(               \
+      kin, vin, win, n, shift, bits, s.hist_scan, nb, kout, vout, wout, keys64, vals32, src)
+    if (last) {
+      if (two)
+        R2S_SCATTER(true, true);
+      else
+        R2S_SCATTER(true, false);
     } else {
-      radix_scatter_kernel<false><<<dim3(nb), dim3(kSortThreads), 0, stream>>>(
-          kin, vin, n, shift, bits, s.hist_scan, nb, kout, vout, nullptr, nullptr, nullptr,
-          nullptr);
-      kin = kout;
-      vin = vout;
-      kout = kalt;
-      vout = valt;
-      kalt = const_cast<uint32_t *>(kin);
-      valt = const_cast<uint32_t *>(vin);
+      if (two)
+        R2S_SCATTER(false, true);
+      else
+        R2S_SCATTER(false, false);
+      std::swap(kin, kout);
+      std::swap(vin, vout);
+      std::swap(win, wout);
     }
+#undef R2S_SCATTER
     R2S_RETURN_IF(check_launch("isect sort pass"));
   }
   return R2S_OK;
@@ -518,9 +538,9 @@ int emit_sort_2d_impl(const T *means2d, const int32_t *radii, int rect, int64_t 
               "%s: emit_ids and isect_src must be given together", name);
   const int64_t M = C * N;
   emit_2d_kernel<T><<<dim3(static_cast<uint32_t>(ceil_div(M, 256))), dim3(256), 0, stream>>>(
-      means2d, radii, rect, M, N, ts, tw, th, offsets, s.ka, s.va, emit_ids);
+      means2d, radii, rect, M, N, ts, tw, th, offsets, s.ka, s.va, s.wa, emit_ids);
   R2S_RETURN_IF(check_launch(name));
-  return radix_sort(s, s.ka, s.va, n_isects, end_bit, keys, vals, emit_ids, isect_src, stream);
+  return radix_sort(s, n_isects, end_bit, keys, vals, emit_ids != nullptr, isect_src, stream);
 }
 
 template <typename T>
@@ -543,9 +563,9 @@ int emit_sort_3d_impl(const T *means3d, const int32_t *radii, int64_t N, uint32_
   R2S_REQUIRE((emit_ids == nullptr) == (isect_src == nullptr),
               "%s: emit_ids and isect_src must be given together", name);
   emit_3d_kernel<T><<<dim3(static_cast<uint32_t>(ceil_div(N, 256))), dim3(256), 0, stream>>>(
-      means3d, radii, N, ts, n2, n1, n0, offsets, s.ka, s.va, emit_ids);
+      means3d, radii, N, ts, n2, n1, n0, offsets, s.ka, s.va, s.wa, emit_ids);
   R2S_RETURN_IF(check_launch(name));
-  return radix_sort(s, s.ka, s.va, n_isects, end_bit, keys, vals, emit_ids, isect_src, stream);
+  return radix_sort(s, n_isects, end_bit, keys, vals, emit_ids != nullptr, isect_src, stream);
 }
 
 }  // namespace
