@@ -127,44 +127,73 @@ __global__ __launch_bounds__(256) void count_3d_kernel(const T *__restrict__ mea
 
 // ---------------------------------------------------------------- emit ---
 
+// Lane (of the calling wave) owning output t of a wave whose lanes emit
+// excl[j] .. excl[j] + cnt[j] - 1: the largest j with excl[j] <= t (a lane
+// with cnt > 0, as zero-count lanes share the excl of the next lane).
+__device__ __forceinline__ uint32_t owner_lane(uint32_t excl, uint32_t t) {
+  uint32_t lo = 0;
+#pragma unroll
+  for (uint32_t step = 32; step > 0; step >>= 1) {
+    const uint32_t cand = lo + step;
+    const uint32_t e = static_cast<uint32_t>(__shfl(static_cast<int>(excl), static_cast<int>(cand & 63u), 64));
+    if (cand < 64u && e <= t) lo = cand;
+  }
+  return lo;
+}
+
+// Writes one record: key, payload(s) and, for the emission-order arrays,
+// the flat id.
+__device__ __forceinline__ void put_record(uint32_t *__restrict__ keys, uint32_t *__restrict__ vals,
+                                           uint32_t *__restrict__ vals2,
+                                           int32_t *__restrict__ emit_ids, int64_t e,
+                                           uint32_t key, uint32_t gid) {
+  keys[e] = key;
+  if (emit_ids != nullptr) {
+    vals[e] = static_cast<uint32_t>(e);
+    vals2[e] = gid;
+    emit_ids[e] = static_cast<int32_t>(gid);
+  } else {
+    vals[e] = gid;
+  }
+}
+
+// A wave's 64 consecutive items emit one contiguous range of records
+// (offsets is the exclusive scan of the counts); the range is spread over
+// the lanes 64 records at a time, so every store instruction writes 64
+// consecutive records.  Tiles of one item are row-major in its rectangle.
 template <typename T>
 __global__ __launch_bounds__(256) void emit_2d_kernel(
     const T *__restrict__ means2d, const int32_t *__restrict__ radii, int rect, int64_t M,
     int64_t N, uint32_t ts, uint32_t tw, uint32_t th, const int64_t *__restrict__ offsets,
     uint32_t *__restrict__ keys, uint32_t *__restrict__ vals, uint32_t *__restrict__ vals2,
     int32_t *__restrict__ emit_ids) {
-  const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + (threadIdx.x & ~63u);
+  const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + 64 * wave_index();
+  if (wave_first >= M) return;  // uniform per wave
   const int64_t idx = wave_first + lane_id();
   Rect r = {0, 0, 0, 0};
   uint32_t cnt = 0;
-  int64_t off = 0;
-  if (idx < M) {
-    cnt = rect_2d(means2d, radii, rect, idx, ts, tw, th, r);
-    off = offsets[idx];
-  }
-  const uint32_t n_tiles = tw * th;
+  if (idx < M) cnt = rect_2d(means2d, radii, rect, idx, ts, tw, th, r);
+  const uint32_t incl = wave_inclusive_scan(cnt);
+  const uint32_t excl = incl - cnt;
+  const uint32_t total = readlane_u32(incl, 63);
+  const int64_t base = offsets[wave_first];
   const uint32_t width = r.x1 - r.x0;
-  uint64_t todo = ballot(cnt > 0);
-  while (todo) {
-    const uint32_t j = static_cast<uint32_t>(__builtin_ctzll(todo));
-    todo &= todo - 1;
-    const uint32_t cj = readlane_u32(cnt, j);
-    const uint32_t wj = readlane_u32(width, j);
-    const uint32_t x0 = readlane_u32(r.x0, j), y0 = readlane_u32(r.y0, j);
-    const int64_t base = readlane_i64(off, j);
+  const uint32_t n_tiles = tw * th;
+  // Uniform loop: every lane takes part in the shuffles (a lane past the end
+  // works on the last record and stores nothing).
+  for (uint32_t t0 = 0; t0 < total; t0 += 64) {
+    const uint32_t t = min(t0 + lane_id(), total - 1);
+    const uint32_t j = owner_lane(excl, t);
+    const int jj = static_cast<int>(j);
+    const uint32_t k = t - static_cast<uint32_t>(__shfl(static_cast<int>(excl), jj, 64));
+    const uint32_t wj = static_cast<uint32_t>(__shfl(static_cast<int>(width), jj, 64));
+    const uint32_t x0 = static_cast<uint32_t>(__shfl(static_cast<int>(r.x0), jj, 64));
+    const uint32_t y0 = static_cast<uint32_t>(__shfl(static_cast<int>(r.y0), jj, 64));
+    const uint32_t row = k / wj, col = k - row * wj;
     const int64_t gid = wave_first + j;
-    const uint32_t kbase = static_cast<uint32_t>(gid / N) * n_tiles;
-    for (uint32_t k = lane_id(); k < cj; k += 64) {
-      const uint32_t row = k / wj, col = k - row * wj;
-      keys[base + k] = kbase + (y0 + row) * tw + (x0 + col);
-      if (emit_ids != nullptr) {
-        vals[base + k] = static_cast<uint32_t>(base + k);
-        vals2[base + k] = static_cast<uint32_t>(gid);
-        emit_ids[base + k] = static_cast<int32_t>(gid);
-      } else {
-        vals[base + k] = static_cast<uint32_t>(gid);
-      }
-    }
+    const uint32_t key = static_cast<uint32_t>(gid / N) * n_tiles + (y0 + row) * tw + (x0 + col);
+    if (t0 + lane_id() < total)
+      put_record(keys, vals, vals2, emit_ids, base + t, key, static_cast<uint32_t>(gid));
   }
 }
 
@@ -174,43 +203,41 @@ __global__ __launch_bounds__(256) void emit_3d_kernel(
     uint32_t n2, uint32_t n1, uint32_t n0, const int64_t *__restrict__ offsets,
     uint32_t *__restrict__ keys, uint32_t *__restrict__ vals, uint32_t *__restrict__ vals2,
     int32_t *__restrict__ emit_ids) {
-  const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + (threadIdx.x & ~63u);
+  const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + 64 * wave_index();
+  if (wave_first >= N) return;  // uniform per wave
   const int64_t idx = wave_first + lane_id();
   const uint32_t n[3] = {n2, n1, n0};
   Box b;
   uint32_t cnt = 0;
-  int64_t off = 0;
   if (idx < N) {
     cnt = box_3d(means3d, radii, idx, ts, n, b);
-    off = offsets[idx];
   } else {
 #pragma unroll
     for (int a = 0; a < 3; ++a) b.lo[a] = b.hi[a] = 0;
   }
+  const uint32_t incl = wave_inclusive_scan(cnt);
+  const uint32_t excl = incl - cnt;
+  const uint32_t total = readlane_u32(incl, 63);
+  const int64_t base = offsets[wave_first];
   const uint32_t e2 = b.hi[0] - b.lo[0], e1 = b.hi[1] - b.lo[1];
-  uint64_t todo = ballot(cnt > 0);
-  while (todo) {
-    const uint32_t j = static_cast<uint32_t>(__builtin_ctzll(todo));
-    todo &= todo - 1;
-    const uint32_t cj = readlane_u32(cnt, j);
-    const uint32_t e2j = readlane_u32(e2, j), e1j = readlane_u32(e1, j);
-    const uint32_t l2 = readlane_u32(b.lo[0], j), l1 = readlane_u32(b.lo[1], j),
-                   l0 = readlane_u32(b.lo[2], j);
-    const int64_t base = readlane_i64(off, j);
-    const uint32_t gid = static_cast<uint32_t>(wave_first + j);
+  // Uniform loop: every lane takes part in the shuffles (a lane past the end
+  // works on the last record and stores nothing).
+  for (uint32_t t0 = 0; t0 < total; t0 += 64) {
+    const uint32_t t = min(t0 + lane_id(), total - 1);
+    const uint32_t j = owner_lane(excl, t);
+    const int jj = static_cast<int>(j);
+    const uint32_t k = t - static_cast<uint32_t>(__shfl(static_cast<int>(excl), jj, 64));
+    const uint32_t e2j = static_cast<uint32_t>(__shfl(static_cast<int>(e2), jj, 64));
+    const uint32_t e1j = static_cast<uint32_t>(__shfl(static_cast<int>(e1), jj, 64));
+    const uint32_t l2 = static_cast<uint32_t>(__shfl(static_cast<int>(b.lo[0]), jj, 64));
+    const uint32_t l1 = static_cast<uint32_t>(__shfl(static_cast<int>(b.lo[1]), jj, 64));
+    const uint32_t l0 = static_cast<uint32_t>(__shfl(static_cast<int>(b.lo[2]), jj, 64));
     const uint32_t plane = e2j * e1j;
-    for (uint32_t k = lane_id(); k < cj; k += 64) {
-      const uint32_t t0 = k / plane, rem = k - t0 * plane;
-      const uint32_t t1 = rem / e2j, t2 = rem - t1 * e2j;
-      keys[base + k] = (l0 + t0) * (n1 * n2) + (l1 + t1) * n2 + (l2 + t2);
-      if (emit_ids != nullptr) {
-        vals[base + k] = static_cast<uint32_t>(base + k);
-        vals2[base + k] = gid;
-        emit_ids[base + k] = static_cast<int32_t>(gid);
-      } else {
-        vals[base + k] = gid;
-      }
-    }
+    const uint32_t tz = k / plane, rem = k - tz * plane;
+    const uint32_t ty = rem / e2j, tx = rem - ty * e2j;
+    const uint32_t key = (l0 + tz) * (n1 * n2) + (l1 + ty) * n2 + (l2 + tx);
+    if (t0 + lane_id() < total)
+      put_record(keys, vals, vals2, emit_ids, base + t, key, static_cast<uint32_t>(wave_first + j));
   }
 }
 
