@@ -31,6 +31,7 @@ SOURCES = [
     "mapping.hip",
     "voxelize.hip",
     "compact.hip",
+    "densify.hip",
 ]
 
 ARCH = os.environ.get("R2S_OFFLOAD_ARCH", "gfx950")

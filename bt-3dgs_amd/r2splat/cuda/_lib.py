@@ -5,7 +5,7 @@ from __future__ import annotations
 import ctypes
 import os
 
-__all__ = ["LIB_PATH", "load", "SYMBOLS"]
+__all__ = ["LIB_PATH", "load", "SYMBOLS", "Column", "SplitGeometry"]
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "lib",
                         "libr2splat_hip.so")
@@ -73,11 +73,35 @@ _PLAIN = {
     "r2s_voxelize_bwd_workspace_bytes": (_i64, [_i64, _i32]),
     "r2s_mask_workspace_bytes": (_i64, [_i64]),
     "r2s_mask_split": (_i32, [_p, _i64, _p, _p, _p, _sz, _p]),
+    "r2s_densify_split": (_i32, [_p, _i64, _p, _i64, _i64, _p, _p, _i32, _p]),
+    "r2s_densify_duplicate": (_i32, [_p, _i64, _p, _i64, _i64, _p, _i32, _p]),
+    "r2s_densify_remove": (_i32, [_p, _i64, _p, _i32, _p]),
 }
+
+
+
+class Column(ctypes.Structure):
+    """r2s_column_t: one column of the Gaussian table for the densify calls."""
+
+    _fields_ = [("src", _p), ("dst", _p), ("extra", _p), ("rows", _i64), ("width", _i32),
+                ("role", _i32)]
+
+
+class SplitGeometry(ctypes.Structure):
+    """r2s_split_geometry_t: live quats / raw scales and the scale activation."""
+
+    _fields_ = [("quats", _p), ("raw_scales", _p), ("scale_min", _f32 * 3),
+                ("scale_max", _f32 * 3), ("scale_eps", _f32), ("sigmoid_scales", _i32)]
+
+
+# Column roles (R2S_COL_* in include/r2splat_hip.h).
+COL_COPY, COL_ZERO_NEW, COL_MEANS, COL_RAW_SCALES, COL_RAW_OPACITIES, COL_PARENT, COL_LEVEL, \
+    COL_HISTORY = range(8)
+DENSIFY_MAX_WIDTH = 16
 
 SYMBOLS = sorted(list(_PLAIN) + [f"r2s_{n}_{s}" for n in _FLOAT_OPS for s in ("f32", "f64")])
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 def load(path: str = LIB_PATH) -> ctypes.CDLL:

@@ -10,6 +10,7 @@ no CPU fallback: without the library every call raises ``RuntimeError``.
 
 from __future__ import annotations
 
+import ctypes
 import math
 from typing import Optional, Tuple
 
@@ -819,3 +820,145 @@ def mask_split(mask: Tensor) -> Tuple[Tensor, int]:
               _ptr(count), _ptr(ws), ws.numel(), _stream(dev))
         n_true = int(count.item())
     return out, n_true
+
+
+# ------------------------------------------------------------- densify --
+#
+# One launch rebuilds every column of the Gaussian table (parameters, Adam
+# moments, tree buffers, strategy statistics, history archive) for the
+# binary-tree strategy's split / duplicate / remove
+# (src/strategies/binary_tree.py:17-171, src/utils/ops.py:61-103).
+# A column is given as (src, role, extra): `role` is one of the _lib.COL_*
+# values; `extra` is the live column appended to a history archive
+# (role COL_HISTORY) and None otherwise.
+
+def _densify_table(columns, n_rows: int, main_rows: int, hist_rows: int, n_sel: int, what: str):
+    from . import _lib as L
+
+    table = (L.Column * max(len(columns), 1))()
+    outs, used = [], 0
+    for i, col in enumerate(columns):
+        src, role, extra = col
+        _check_input(src, f"{what}: column {i}")
+        _check(src.dtype in (torch.float32, torch.int32),
+               f"{what}: column {i} must be float32 or int32, got {src.dtype}")
+        _check(src.dim() >= 1, f"{what}: column {i} must have a row dimension")
+        width = int(math.prod(src.shape[1:]))
+        _check(1 <= width <= L.DENSIFY_MAX_WIDTH,
+               f"{what}: column {i} has {width} values per row (1..{L.DENSIFY_MAX_WIDTH})")
+        if role in (L.COL_MEANS, L.COL_RAW_SCALES, L.COL_RAW_OPACITIES):
+            _check(src.dtype == torch.float32, f"{what}: column {i} (role {role}) must be float32")
+        if role in (L.COL_PARENT, L.COL_LEVEL):
+            _check(src.dtype == torch.int32 and width == 1,
+                   f"{what}: column {i} (parent / level) must be int32 [N]")
+        if role == L.COL_HISTORY:
+            _check(extra is not None, f"{what}: history column {i} needs its live column")
+            _check_input(extra, f"{what}: live column of history column {i}")
+            _check(extra.dtype == src.dtype and tuple(extra.shape[1:]) == tuple(src.shape[1:]),
+                   f"{what}: history column {i} and its live column differ in dtype or shape")
+            _check(extra.size(0) == n_rows,
+                   f"{what}: live column of history column {i} has {extra.size(0)} rows, "
+                   f"expected {n_rows}")
+            _check(src.size(0) == hist_rows,
+                   f"{what}: history column {i} has {src.size(0)} rows, expected {hist_rows}")
+            if n_sel == 0:
+                outs.append(src)  # nothing to archive: the archive is returned as is
+                continue
+            rows = hist_rows + n_sel
+        else:
+            _check(extra is None, f"{what}: column {i}: only history columns take a live column")
+            _check(src.size(0) == n_rows,
+                   f"{what}: column {i} has {src.size(0)} rows, expected {n_rows}")
+            rows = main_rows
+        dst = torch.empty((rows,) + tuple(src.shape[1:]), dtype=src.dtype, device=src.device)
+        table[used] = L.Column(src.data_ptr() if src.numel() else None,
+                               dst.data_ptr() if dst.numel() else None,
+                               extra.data_ptr() if extra is not None and extra.numel() else None,
+                               rows, width, role)
+        used += 1
+        outs.append(dst)
+    return table, used, outs
+
+
+def _densify_mask(mask: Tensor, n_rows: int, what: str):
+    _check(isinstance(mask, torch.Tensor) and mask.is_cuda, f"{what}: mask must be a CUDA tensor")
+    _check(mask.dim() == 1 and mask.size(0) == n_rows,
+           f"{what}: mask must be 1-D with {n_rows} entries")
+    m = mask if mask.dtype in (torch.bool, torch.uint8) else mask != 0
+    return m.contiguous().view(torch.uint8)
+
+
+def densify_split(mask: Tensor, columns, history_rows: int = 0, geometry=None):
+    """Split the rows where ``mask`` is true (binary_tree.py:93-148).
+
+    Each non-history column becomes ``cat(src[rest], child_plus, child_minus)``
+    (children of the selected rows, in ascending order); history columns
+    become ``cat(src, extra[sel])``.  ``geometry`` is ``(quats, raw_scales,
+    scale_min[3], scale_max[3], scale_eps, sigmoid_scales)`` of the live
+    table, required by the MEANS / RAW_SCALES roles.  Returns
+    ``(outputs, n_sel)`` with outputs in column order.
+    """
+    from . import _lib as L
+
+    n = int(mask.shape[0]) if isinstance(mask, torch.Tensor) and mask.dim() == 1 else -1
+    m = _densify_mask(mask, n, "densify_split")
+    idx, n_sel = mask_split(m)
+    n_rest = n - n_sel
+    dev = m.device
+    table, used, outs = _densify_table(columns, n, n_rest + 2 * n_sel, history_rows, n_sel,
+                                       "densify_split")
+    geo = None
+    if geometry is not None:
+        quats, raw_scales, smin, smax, eps, sigmoid = geometry
+        for t, name in ((quats, "quats"), (raw_scales, "raw_scales")):
+            _check_input(t, name)
+            _check(t.dtype == torch.float32, f"densify_split: {name} must be float32")
+        _check(tuple(quats.shape) == (n, 4) and tuple(raw_scales.shape) == (n, 3),
+               "densify_split: geometry must be quats [N,4] and raw_scales [N,3]")
+        smin = [float(v) for v in smin]
+        smax = [float(v) for v in smax]
+        _check(len(smin) == 3 and len(smax) == 3, "densify_split: three scale bounds per side")
+        geo = L.SplitGeometry(quats.data_ptr() if n else None, raw_scales.data_ptr() if n else None,
+                              (ctypes.c_float * 3)(*smin), (ctypes.c_float * 3)(*smax),
+                              float(eps), int(bool(sigmoid)))
+    with torch.cuda.device(dev):
+        _call("r2s_densify_split", idx.data_ptr() if n_sel else None, n_sel,
+              idx[n_sel:].data_ptr() if n_rest else None, n_rest, int(history_rows),
+              ctypes.byref(geo) if geo is not None else None, table, used, _stream(dev))
+    return outs, n_sel
+
+
+def densify_duplicate(mask: Tensor, columns, history_rows: int = 0):
+    """Duplicate the rows where ``mask`` is true (binary_tree.py:60-90).
+
+    Each non-history column becomes ``cat(src', src'[sel])`` where ``src'``
+    is ``src`` with the selected rows' parent / level updated (roles PARENT,
+    LEVEL) and the copies' Adam moments zero (role ZERO_NEW).  Returns
+    ``(outputs, n_sel)``.
+    """
+    n = int(mask.shape[0]) if isinstance(mask, torch.Tensor) and mask.dim() == 1 else -1
+    m = _densify_mask(mask, n, "densify_duplicate")
+    idx, n_sel = mask_split(m)
+    dev = m.device
+    table, used, outs = _densify_table(columns, n, n + n_sel, history_rows, n_sel,
+                                       "densify_duplicate")
+    with torch.cuda.device(dev):
+        _call("r2s_densify_duplicate", m.data_ptr() if n else None, n,
+              idx.data_ptr() if n_sel else None, n_sel, int(history_rows), table, used,
+              _stream(dev))
+    return outs, n_sel
+
+
+def densify_remove(mask: Tensor, columns):
+    """Keep the rows where ``mask`` is false (binary_tree.py:151-171).
+    Returns ``(outputs, n_removed)``."""
+    n = int(mask.shape[0]) if isinstance(mask, torch.Tensor) and mask.dim() == 1 else -1
+    m = _densify_mask(mask, n, "densify_remove")
+    idx, n_sel = mask_split(m)
+    n_keep = n - n_sel
+    dev = m.device
+    table, used, outs = _densify_table(columns, n, n_keep, 0, 0, "densify_remove")
+    with torch.cuda.device(dev):
+        _call("r2s_densify_remove", idx[n_sel:].data_ptr() if n_keep else None, n_keep, table,
+              used, _stream(dev))
+    return outs, n_sel

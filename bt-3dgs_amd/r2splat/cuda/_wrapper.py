@@ -44,6 +44,9 @@ project_gaussians_fwd = _make_cuda_func("project_gaussians_fwd")
 project_gaussians_bwd = _make_cuda_func("project_gaussians_bwd")
 opacity_bwd = _make_cuda_func("opacity_bwd")
 mask_split = _make_cuda_func("mask_split")
+densify_split = _make_cuda_func("densify_split")
+densify_duplicate = _make_cuda_func("densify_duplicate")
+densify_remove = _make_cuda_func("densify_remove")
 
 
 def is_cuda_extension_available() -> bool:

@@ -531,6 +531,82 @@ int r2s_mask_split(const uint8_t *mask, int64_t n, int64_t *out,
                    int64_t *n_true_dev, void *workspace,
                    size_t workspace_bytes, r2s_stream_t stream);
 
+/* ---------------------------------------------------------------------- */
+/* Densify / prune: fused table rewrite                                    */
+/* ---------------------------------------------------------------------- */
+
+/* The Gaussian table of the binary-tree model is a set of columns with one
+ * row per Gaussian: the trainable parameters, their Adam moments, the tree
+ * buffers (parent, level), the strategy's per-Gaussian statistics and the
+ * history archive.  split / duplicate / remove rebuild every column from the
+ * selected (sel) and kept (rest) index lists in one launch.  Each column is
+ * rows of `width` 4-byte words (float32 or int32); `dst` is a new array of
+ * `rows` rows that the call fills completely. */
+#define R2S_COL_COPY 0          /* new rows copy their source row              */
+#define R2S_COL_ZERO_NEW 1      /* new rows are zero (Adam exp_avg/exp_avg_sq) */
+#define R2S_COL_MEANS 2         /* split: mean +/- rotated longest axis        */
+#define R2S_COL_RAW_SCALES 3    /* split: longest axis / 1.6, re-inverted      */
+#define R2S_COL_RAW_OPACITIES 4 /* split: revised opacity 1 - sqrt(1 - o)      */
+#define R2S_COL_PARENT 5        /* int32 parent links                          */
+#define R2S_COL_LEVEL 6         /* int32 depths                                */
+#define R2S_COL_HISTORY 7       /* dst = cat(src[0:history_rows], extra[sel])  */
+
+#define R2S_DENSIFY_MAX_WIDTH 16
+
+typedef struct r2s_column {
+  const void *src;   /* [n_src, width]; for R2S_COL_HISTORY the archive     */
+  void *dst;         /* [rows, width], written completely                  */
+  const void *extra; /* R2S_COL_HISTORY: live column whose sel rows append */
+  int64_t rows;      /* rows of dst (checked against the operation)        */
+  int32_t width;     /* 4-byte words per row, 1..R2S_DENSIFY_MAX_WIDTH     */
+  int32_t role;      /* R2S_COL_*                                          */
+} r2s_column_t;
+
+/* Scale activation of the model (src/models/gaussian_model.py:258-274):
+ * bounded sigmoid min + (max - min) * sigmoid(raw) when sigmoid_scales != 0,
+ * else exp(raw).  Per-axis bounds; repeat a scalar bound three times. */
+typedef struct r2s_split_geometry {
+  const float *quats;      /* [n, 4] (w, x, y, z), as stored (not normalised) */
+  const float *raw_scales; /* [n, 3] */
+  float scale_min[3];
+  float scale_max[3];
+  float scale_eps;
+  int32_t sigmoid_scales;
+} r2s_split_geometry_t;
+
+/* src/strategies/binary_tree.py:93-148 split() together with
+ * _append_history (:17-57) and src/utils/ops.py:61-103
+ * _update_param_with_optimizer.  With rest = where(~mask) (n_rest rows) and
+ * sel = where(mask) (n_sel rows), every non-history column gets
+ * n_rest + 2 n_sel rows: the kept rows in `rest` order, then the children
+ * [all +offset; all -offset] of the `sel` rows.  Parent rows of children are
+ * history_rows + j (j = position in sel), levels level[sel] + 1.  History
+ * columns get history_rows + n_sel rows.  `geometry` describes the live
+ * (pre-split) quats and raw scales; it may be NULL when no column has role
+ * MEANS or RAW_SCALES. */
+int r2s_densify_split(const int64_t *sel, int64_t n_sel, const int64_t *rest,
+                      int64_t n_rest, int64_t history_rows,
+                      const r2s_split_geometry_t *geometry,
+                      const r2s_column_t *columns, int32_t n_columns,
+                      r2s_stream_t stream);
+
+/* src/strategies/binary_tree.py:60-90 duplicate(): every non-history column
+ * gets n + n_sel rows, the n old rows then copies of the sel rows.  Old rows
+ * with mask[i] != 0 get parent history_rows + j and level + 1 (as do their
+ * copies); Adam moments (R2S_COL_ZERO_NEW) of the copies are zero.  History
+ * columns get history_rows + n_sel rows. */
+int r2s_densify_duplicate(const uint8_t *mask, int64_t n, const int64_t *sel,
+                          int64_t n_sel, int64_t history_rows,
+                          const r2s_column_t *columns, int32_t n_columns,
+                          r2s_stream_t stream);
+
+/* src/strategies/binary_tree.py:151-171 remove(): every column gets the
+ * n_keep rows keep = where(~mask), in order.  History columns are not
+ * allowed (remove leaves the archive unchanged). */
+int r2s_densify_remove(const int64_t *keep, int64_t n_keep,
+                       const r2s_column_t *columns, int32_t n_columns,
+                       r2s_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

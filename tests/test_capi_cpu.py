@@ -68,3 +68,31 @@ def test_workspace_queries(lib):
     rc = lib.r2s_isect_emit_sort_2d_f32(None, None, 1, 1, 10, 16, 4, 4, None, 100, 5, buf, buf,
                                         None, None, buf, 16, None)
     assert rc in (1001, 1004)
+
+
+def test_densify_arguments_are_checked_without_a_device(lib):
+    C = _lib.Column
+    cols = (C * 1)()
+    cols[0] = C(None, None, None, 0, 0, _lib.COL_COPY)
+    assert lib.r2s_densify_remove(None, 0, cols, 1, None) == 1001
+    assert b"width 0" in lib.r2s_last_error()
+    assert lib.r2s_densify_remove(None, 5, cols, 1, None) == 1001
+    assert b"null keep" in lib.r2s_last_error()
+    cols[0] = C(None, None, None, 0, 1, _lib.COL_HISTORY)
+    assert lib.r2s_densify_remove(None, 0, cols, 1, None) == 1001
+    assert b"history" in lib.r2s_last_error()
+    cols[0] = C(None, None, None, 3, 1, _lib.COL_COPY)
+    assert lib.r2s_densify_remove(None, 0, cols, 1, None) == 1001
+    assert b"3 rows, the operation writes 0" in lib.r2s_last_error()
+    cols[0] = C(None, None, None, 0, 3, _lib.COL_PARENT)
+    assert lib.r2s_densify_split(None, 0, None, 0, 0, None, cols, 1, None) == 1001
+    assert b"width 1" in lib.r2s_last_error()
+    cols[0] = C(None, None, None, 0, 3, _lib.COL_MEANS)
+    assert lib.r2s_densify_split(None, 0, None, 0, 0, None, cols, 1, None) == 1001
+    assert b"geometry" in lib.r2s_last_error()
+    fake = ctypes.c_void_p(256)  # never dereferenced: the size check fails first
+    assert lib.r2s_densify_split(fake, 2, None, 0, (1 << 31) - 2, None, None, 0, None) == 1002
+    assert lib.r2s_densify_duplicate(None, 4, None, 0, 0, None, 0, None) == 1001  # null mask
+    # Nothing to write is a successful no-op.
+    assert lib.r2s_densify_remove(None, 0, None, 0, None) == 0
+    assert lib.r2s_densify_split(None, 0, None, 0, 0, None, None, 0, None) == 0
