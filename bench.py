@@ -33,9 +33,9 @@ import numpy as np  # noqa: E402
 import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, AMD public spec
-# 157.3 TFLOPS fp32 vector = 2 (FMA) x 2 (packed) x 39.3 T lane instructions/s;
-# this build does not use packed fp32, so one lane instruction per lane-cycle.
-VALU_LANE_PEAK_T = 39.3
+# MI355X fp32 vector peak, 157.3 TFLOP/s (AMD public spec), expressed as
+# wave64 FMA instructions: 157.3e12 / (2 flop x 64 lanes) = 1228.9 G/s.
+VALU_PEAK_G_WAVE_INSTR = 157.3e3 / 128
 SMIN, SMAX = 5e-4, 1.0
 EPS = 1e-8
 DET = 512
@@ -265,6 +265,26 @@ def measured_traffic(kernel: str):
     return None
 
 
+def measured_valu(kernel: str):
+    """VALU and transcendental wave64 instructions per launch of ``kernel``
+    from the committed rocprofv3 --pmc summary (profiles/pmc_valu_<kernel>.txt,
+    lines ``valu_wave_instructions_per_launch: N`` and
+    ``trans_wave_instructions_per_launch: N``), or (None, None)."""
+    path = os.path.join(ROOT, "profiles", f"pmc_valu_{kernel}.txt")
+    vals = {}
+    try:
+        with open(path) as f:
+            for line in f:
+                key, _, v = line.partition(":")
+                if key in ("valu_wave_instructions_per_launch",
+                           "trans_wave_instructions_per_launch"):
+                    vals[key] = float(v)
+    except OSError:
+        pass
+    return (vals.get("valu_wave_instructions_per_launch"),
+            vals.get("trans_wave_instructions_per_launch"))
+
+
 def proj_bytes(n, i2, p):
     """Algorithmic bytes of one projection fwd+bwd call (B_proj)."""
     return 164 * n + 128 * i2 + 8 * p
@@ -381,17 +401,23 @@ def main():
         "project_fwd": 108 * N_PROJ,
         "prepare": 76 * N_PROJ,
     }[dom]
-    evals = 256 * i2
-    flops_per_eval = {"rasterize_fwd": 10, "rasterize_bwd_rows": 20}.get(dom, 0)
     traffic = measured_traffic(dom)
+    valu, trans = measured_valu(dom)
+    valu_rate = None if valu is None else valu / secs[dom] / 1e9
     result["roofline"] = {
         "kernel": dom, "bound": "hbm",
         "achieved": dom_bytes / secs[dom] / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": dom_bytes / secs[dom] / 1e9 / HBM_PEAK_GBS, "traffic": traffic,
         "algorithmic_bytes": dom_bytes, "avg_launch_ms": secs[dom] * 1e3,
-        "valu": {"evaluations": evals, "vector_instructions_per_eval": flops_per_eval,
-                 "achieved_t_lane_instructions_per_s": evals * flops_per_eval / secs[dom] / 1e12,
-                 "peak_t_lane_instructions_per_s": VALU_LANE_PEAK_T},
+        # The raster kernels are bound by vector-ALU issue, not HBM: the
+        # instruction counts come from a rocprofv3 --pmc pass of this kernel.
+        "valu": {"reference_evaluations": 256 * i2,
+                 "executed_evaluations": None if trans is None else trans * 64,
+                 "wave_instructions_per_launch": valu,
+                 "achieved_g_wave_instructions_per_s": valu_rate,
+                 "peak_g_wave_instructions_per_s": VALU_PEAK_G_WAVE_INSTR,
+                 "frac": None if valu_rate is None else valu_rate / VALU_PEAK_G_WAVE_INSTR,
+                 "source": f"profiles/pmc_valu_{dom}.txt"},
     }
 
     if args.copy_bytes > 0:

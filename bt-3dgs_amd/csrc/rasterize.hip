@@ -287,6 +287,80 @@ __device__ __forceinline__ void raster_row(const RasterRecord<T> &rec, const T (
   }
 }
 
+// The whole tile of one record when every tile of the wave lies inside the
+// image (no column guard).  The column offsets dx_k are the same on every
+// row, so they are kept in registers, and the column sums W_k = sum over
+// rows of w accumulate per column: T0, T1, T2 then follow from W_k once per
+// record, which leaves three accumulations per pixel (W_k, s0, s1) instead
+// of four.  Rows outside the record's reach test against an infinite cut-off
+// (every pixel fails), so the upstream gradient is loaded without masks.
+template <typename T, int R, bool kAbs>
+__device__ __forceinline__ void raster_tile_full(const RasterRecord<T> &rec,
+                                                 const T *__restrict__ vimg, uint32_t W, int ox,
+                                                 int oy, T dx0, T &T0, T &T1, T &T2, T &Y0, T &Y1,
+                                                 T &YY, T &PX, T &PY) {
+  using Q = typename Quad<T>::type;
+  constexpr int kq = Quad<T>::n;
+  T dxk[R], wk[R];
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    dxk[k] = dx0 + static_cast<T>(k);
+    wk[k] = 0;
+  }
+  const T half = static_cast<T>(0.5);
+#pragma unroll 1
+  for (int ly = 0; ly < R; ++ly) {
+    const int i = oy + ly;
+    const bool in_row = rec.live && i >= rec.i0 && i <= rec.i1;
+    if (ballot(in_row) == 0) continue;
+    const T dy = (static_cast<T>(i) + half) - rec.my;
+    const T B = rec.hb * dy, C = rec.hc * dy * dy;
+    const T bdy = rec.b * dy, cdy = rec.c * dy;
+    const T elo = in_row ? rec.elo : static_cast<T>(INFINITY);
+    const T *__restrict__ vrow = vimg + static_cast<int64_t>(in_row ? i : oy) * W + ox;
+    T s0 = 0, s1 = 0, px = 0, py = 0;
+#pragma unroll
+    for (int h = 0; h < R; h += kChunk) {
+      T vv[kChunk];
+#pragma unroll
+      for (int q = 0; q < kChunk / kq; ++q)
+        *reinterpret_cast<Q *>(vv + q * kq) = *reinterpret_cast<const Q *>(vrow + h + q * kq);
+#pragma unroll
+      for (int kk = 0; kk < kChunk; ++kk) {
+        // Explicit FMAs: written as products plus sums, the products of the
+        // row-invariant dx_k would be hoisted out of the row loop into 48
+        // more registers for no saving.
+        const T dx = dxk[h + kk];
+        const T sl = fma(fma(rec.ha, dx, B), dx, C);
+        const T e = neg_exp2(sl);
+        const bool skip = (sl < static_cast<T>(0)) || (e < elo);
+        const T w = skip ? static_cast<T>(0) : vv[kk] * e;
+        wk[h + kk] += w;
+        s0 += w;
+        s1 = fma(w, dx, s1);
+        if (kAbs) {
+          px = fma(fabs(w), fabs(fma(rec.a, dx, bdy)), px);
+          py = fma(fabs(w), fabs(fma(rec.b, dx, cdy)), py);
+        }
+      }
+    }
+    Y0 += dy * s0;
+    YY += dy * (dy * s0);
+    Y1 += dy * s1;
+    if (kAbs) {
+      PX += px;
+      PY += py;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const T wx = wk[k] * dxk[k];
+    T0 += wk[k];
+    T1 += wx;
+    T2 += wx * dxk[k];
+  }
+}
+
 // Records in tile order (tile_offsets, flatten_ids; isect_ids optional), one
 // lane per record.  kRows = false: each record's nine partials go out
 // through global atomics.  kRows = true: they are stored as the row
@@ -336,7 +410,11 @@ __global__ __launch_bounds__(kBwdThreads) void raster_bwd_kernel(
   // T_k = sum over rows of s_k; Y0 = sum dy s0, Y1 = sum dy s1, YY = sum dy^2 s0;
   // PX, PY = sums of the per-pixel absolute mean gradients.
   T T0 = 0, T1 = 0, T2 = 0, Y0 = 0, Y1 = 0, YY = 0, PX = 0, PY = 0;
-  if (ballot(rec.live) != 0) {
+  bool full = false;
+  if constexpr (kExact && R <= 16 && R % kChunk == 0) full = vec && ballot(nx < nts) == 0;
+  if (full && ballot(rec.live) != 0) {
+    raster_tile_full<T, R, kAbs>(rec, vimg, W, ox, oy, dx0, T0, T1, T2, Y0, Y1, YY, PX, PY);
+  } else if (ballot(rec.live) != 0) {
     for (int ly = 0; ly < R; ++ly) {
       if (!kExact && ly >= nts) break;
       const int i = oy + ly;
