@@ -8,11 +8,13 @@ explicit_rasterize -> explicit_backward, the reference's training path.
 
 Also reported: the voxelizer at config 3 (200k Gaussians, 256^3, fwd + bwd,
 Mvox/s and % of HBM peak), the training-step shape of config 4 (projection +
-128^3 voxelization fwd/bwd + compaction every 100 steps), per-kernel event
+128^3 voxelization fwd/bwd + compaction every 100 steps), the fused
+densify / prune rewrite of the config-4 model table, per-kernel event
 timings, the roofline of the dominant kernel and the CPU oracle baseline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                       [--no-voxel] [--no-train] [--kernel-reps R] [--copy-bytes B]
+                       [--no-voxel] [--no-train] [--no-densify] [--kernel-reps R]
+                       [--copy-bytes B]
 """
 
 from __future__ import annotations
@@ -166,6 +168,74 @@ class Voxelization:
                                       EPS, vm3, vc3)
         self.last = (m3, con, off, ids, fl, vol)
         return vol
+
+
+class DensifyTable:
+    """Config-4 densify/prune workload: the binary-tree model table at
+    N = 500k (params, Adam moments, parent / level, three strategy
+    statistics) with the N - 1 archived ancestors, and 1 % masks."""
+
+    def __init__(self, proj: Projection, seed=3):
+        from r2splat.cuda import _lib as L
+
+        dev = proj.viewmats.device
+        g = torch.Generator().manual_seed(seed)
+        n = N_PROJ
+        means, quats, scales, opac = (t.detach() for t in proj.params)
+        f32 = lambda *shape: torch.randn(*shape, generator=g).to(dev)  # noqa: E731
+        i32 = lambda k: torch.randint(0, 20, (k,), generator=g, dtype=torch.int32).to(dev)  # noqa
+        params = [(means, L.COL_MEANS), (scales, L.COL_RAW_SCALES), (quats, L.COL_COPY),
+                  (opac, L.COL_RAW_OPACITIES)]
+        moments = [f32(*t.shape) for t, _ in params for _ in range(2)]
+        state = [f32(n) for _ in range(3)]
+        parent, level = i32(n), i32(n)
+        h = n - 1
+        hist_src = [means, scales, quats, opac, parent, level]
+        hist = [torch.zeros((h,) + tuple(t.shape[1:]), dtype=t.dtype, device=dev)
+                for t in hist_src]
+        self.history_rows = h
+        self.hist_cols = [(a, L.COL_HISTORY, b) for a, b in zip(hist, hist_src)]
+        self.tree = [(parent, L.COL_PARENT, None), (level, L.COL_LEVEL, None)]
+        self.params = params
+        self.moments = moments
+        self.state = state
+        self.geometry = (quats, scales, [SMIN] * 3, [SMAX] * 3, 1e-5, True)
+        self.masks = [torch.rand(n, generator=g).to(dev) < 0.01 for _ in range(3)]
+        self.words = sum(int(t[0].numel() // t[0].shape[0]) for t in self.tree)
+        self.words += sum(int(t.numel() // t.shape[0]) for t, _ in params)
+        self.words += sum(int(t.numel() // t.shape[0]) for t in moments + state)
+        self.hist_words = sum(int(t.numel() // t.shape[0]) for t in hist_src)
+
+    def columns(self, op):
+        from r2splat.cuda import _lib as L
+
+        cols = [] if op == "remove" else list(self.hist_cols)
+        cols += [(t, L.COL_COPY if op == "remove" else r, None) for t, r, _ in self.tree]
+        cols += [(t, r if op == "split" else L.COL_COPY, None) for t, r in self.params]
+        moment_role = L.COL_COPY if op == "remove" else L.COL_ZERO_NEW
+        cols += [(t, moment_role, None) for t in self.moments]
+        cols += [(t, L.COL_COPY, None) for t in self.state]
+        return cols
+
+    def run(self, op):
+        from r2splat.cuda import _wrapper as W
+
+        if op == "split":
+            return W.densify_split(self.masks[0], self.columns(op), self.history_rows,
+                                   self.geometry)
+        if op == "duplicate":
+            return W.densify_duplicate(self.masks[1], self.columns(op), self.history_rows)
+        return W.densify_remove(self.masks[2], self.columns(op))
+
+    def algorithmic_bytes(self, op, n_sel):
+        """Each source row read once, each destination row written once, the
+        8-byte index lists read once; the archive copied and appended."""
+        n, h, w, hw = N_PROJ, self.history_rows, self.words, self.hist_words
+        if op == "remove":
+            return 4 * w * (n + (n - n_sel)) + 8 * n
+        rows_out = n + n_sel
+        hist = 4 * hw * (2 * h + 2 * n_sel)
+        return 4 * w * (n + rows_out) + 8 * n + hist + (n if op == "duplicate" else 0)
 
 
 def time_steps(fn, steps, warmup):
@@ -337,6 +407,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-voxel", action="store_true")
     ap.add_argument("--no-train", action="store_true")
+    ap.add_argument("--no-densify", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=10)
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="also run a plain device copy of this many bytes 3 times (the "
@@ -461,6 +532,23 @@ def main():
             "voxelize_fwd_hbm_frac": (40 * i3 + 4 * n_vox) / t_vf / (HBM_PEAK_GBS * 1e9),
         }
         log(f"voxelization fwd+bwd: {t_vox * 1e3:.3f} ms/call, I3={i3}")
+
+    if not args.no_densify:
+        log("config-4 densify / prune table (500k rows + 500k archived, 1% masks)")
+        table = DensifyTable(proj)
+        dens = {"workload": "config4 densify/prune: fused rewrite of params, Adam moments, "
+                            "parent/level, strategy statistics and the history archive",
+                "n_rows": N_PROJ, "history_rows": table.history_rows,
+                "words_per_row": table.words, "history_words_per_row": table.hist_words}
+        for op in ("split", "duplicate", "remove"):
+            n_sel = table.run(op)[1]
+            t_op = time_kernel(lambda: table.run(op), args.kernel_reps)
+            b = table.algorithmic_bytes(op, n_sel)
+            dens[op] = {"n_selected": n_sel, "ms_per_call": t_op * 1e3, "algorithmic_bytes": b,
+                        "hbm_frac": b / t_op / (HBM_PEAK_GBS * 1e9)}
+        result["densify"] = dens
+        log("densify: " + ", ".join(f"{op} {dens[op]['ms_per_call']:.3f} ms"
+                                    for op in ("split", "duplicate", "remove")))
 
     if not args.no_cpu_baseline:
         log("timing the CPU oracle baseline")

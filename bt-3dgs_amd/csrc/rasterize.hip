@@ -116,12 +116,20 @@ __global__ __launch_bounds__(1024) void raster_fwd_kernel(
 // pixels of one row per lane, and taking every kFwdWaves-th record of each
 // LDS batch.  A record's row terms (dy, b dy, c dy^2) are shared by the R
 // pixels; sigma log2(e) = (h_a dx + h_b dy) dx + h_c dy^2 with pre-scaled
-// coefficients, so a pixel costs two FMAs, one v_exp_f32 and the alpha test.
-// The waves' partial images are summed in a fixed order at the end, so the
-// result is deterministic (the per-pixel order differs from a plain
-// list-order sum only by rounding).
+// coefficients, and the alpha test |o mu e| >= 1e-5 is e >= 1e-5 / |o mu|
+// with the bound staged per record, so a pixel costs two FMAs, one
+// v_exp_f32, two compares, a select and the accumulating FMA.  The waves'
+// partial images are summed in a fixed order at the end, so the result is
+// deterministic (the per-pixel order differs from a plain list-order sum
+// only by rounding).
 constexpr int kFwdWaves = 8;
 constexpr int kFwdBatch = 64 * kFwdWaves;
+
+// One staged forward record: {x, y, h_a, h_b} and {h_c, o mu, e bound, 0}.
+template <typename T>
+struct FwdRecord {
+  typename Vec<T>::v4 p, q;
+};
 
 template <typename T, int TS>
 __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
@@ -134,8 +142,7 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
   constexpr int R = TS * TS / 64;   // pixels per lane
   constexpr int LPR = TS / R;       // lanes per tile row
   static_assert(R * 64 == TS * TS && LPR * R == TS, "unsupported tile size");
-  __shared__ V4 s_p[kFwdBatch];     // {x, y, h_a, h_b}
-  __shared__ V2 s_q[kFwdBatch];     // {h_c, opacity * mu}
+  __shared__ FwdRecord<T> s_rec[kFwdBatch];
   __shared__ T s_part[kFwdWaves][TS * TS];
 
   const uint32_t key = xcd_swizzle(blockIdx.x, n_keys);
@@ -161,8 +168,8 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
     const int64_t idx = base + tid;
     if (idx < end) {
       const int64_t g = flatten_ids[idx];
-      V4 p;
-      V2 q;
+      FwdRecord<T> rec;
+      V4 &p = rec.p, &q = rec.q;
       if (g >= 0 && g < n_items) {
         const V2 xy = *reinterpret_cast<const V2 *>(means2d + 2 * g);
         p.x = xy.x;
@@ -171,26 +178,32 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
         p.w = l * conics[3 * g + 1];
         q.x = hl * conics[3 * g + 2];
         q.y = opac[g] * mus[g];
-      } else {  // never passes: alpha = 0
+        // |o mu e| < 1e-5 tested as e < 1e-5 / |o mu| (equal up to the
+        // rounding of the cut-off itself); NaN o mu gives a NaN bound, which
+        // no e is below, as no NaN alpha is below 1e-5.
+        q.z = thr / fabs(q.y);
+      } else {  // never passes
         p.x = p.y = p.z = p.w = 0;
         q.x = q.y = 0;
+        q.z = static_cast<T>(INFINITY);
       }
-      s_p[tid] = p;
-      s_q[tid] = q;
+      q.w = 0;
+      s_rec[tid] = rec;
     }
     __syncthreads();
     const int cnt = static_cast<int>(min(static_cast<int64_t>(kFwdBatch), end - base));
     for (int j = wave; j < cnt; j += kFwdWaves) {
-      const V4 p = s_p[j];
-      const V2 q = s_q[j];
+      const V4 p = s_rec[j].p;
+      const V4 q = s_rec[j].q;
       const T dy = py - p.y;
       const T B = p.w * dy, C = q.x * dy * dy;
 #pragma unroll
       for (int k = 0; k < R; ++k) {
         const T dx = (px0 + static_cast<T>(k)) - p.x;
         const T sl = (p.z * dx + B) * dx + C;
-        const T alpha = q.y * neg_exp2(sl);
-        acc[k] += ((sl < static_cast<T>(0)) || (fabs(alpha) < thr)) ? static_cast<T>(0) : alpha;
+        const T e = neg_exp2(sl);
+        const bool skip = (sl < static_cast<T>(0)) || (e < q.z);
+        acc[k] = fma(q.y, skip ? static_cast<T>(0) : e, acc[k]);
       }
     }
   }

@@ -245,6 +245,101 @@ __device__ __forceinline__ void voxel_row(const BwdRecord<T> &rec, const T (&vv)
   }
 }
 
+// Slice range of one record's brick rows: rows j0..j1 of slice dz that the
+// ellipsoid reaches (empty when the slice is not reached).
+template <typename T>
+__device__ __forceinline__ void slice_rows(const BwdRecord<T> &rec, const Brick &b, bool in_slice,
+                                           T dz, int &j0, int &j1) {
+  j0 = b.oj;
+  j1 = b.oj + b.nj - 1;
+  if (!in_slice) {
+    j1 = j0 - 1;
+  } else if (rec.cu.ok) {
+    const T bud_z = rec.cu.s - static_cast<T>(0.5) * rec.cu.c3 * dz * dz;
+    if (!budget_range<T>(rec.m[1], -rec.cu.ky * dz, bud_z, rec.cu.inv_a2, b.oj, b.oj + b.nj - 1,
+                         j0, j1))
+      j1 = j0 - 1;
+  }
+}
+
+// The whole brick of one record when every brick of the wave lies inside
+// the volume (no column guard).  The column offsets dx_k are the same on
+// every row and the column sums W_k = sum over rows of w accumulate per
+// column, so T0, T1, T2 follow from W_k once per record and each voxel adds
+// three sums (W_k, s0, s1) instead of four.  Rows the record does not reach
+// test against an infinite cut-off (every voxel fails), so the upstream
+// gradient is loaded without masks.
+template <typename T, int R>
+__device__ __forceinline__ void voxel_brick_full(const BwdRecord<T> &rec, const Brick &b,
+                                                 const T *__restrict__ v_vol, int64_t plane,
+                                                 uint32_t D2, T dx0, T &T0, T &T1, T &T2, T &Y0,
+                                                 T &Z0, T &Y1, T &Z1, T &YY, T &YZ, T &ZZ) {
+  using Q = typename Quad<T>::type;
+  constexpr int kq = Quad<T>::n;
+  T dxk[R], wk[R];
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    dxk[k] = dx0 + static_cast<T>(k);
+    wk[k] = 0;
+  }
+  const T half = static_cast<T>(0.5);
+#pragma unroll 1
+  for (int li = 0; li < R; ++li) {
+    const int i = b.oi + li;
+    const bool in_slice = rec.live && i >= rec.i0 && i <= rec.i1;
+    if (ballot(in_slice) == 0) continue;
+    const T dz = (static_cast<T>(i) + half) - rec.m[2];
+    int j0, j1;
+    slice_rows(rec, b, in_slice, dz, j0, j1);
+    const T h4dz = rec.h[4] * dz, h5dzz = rec.h[5] * dz * dz, Bz = rec.h[2] * dz;
+    const T *__restrict__ vslice = v_vol + static_cast<int64_t>(i) * plane + b.ok;
+#pragma unroll 1
+    for (int lj = 0; lj < R; ++lj) {
+      const int j = b.oj + lj;
+      const bool in_row = j >= j0 && j <= j1;
+      if (ballot(in_row) == 0) continue;
+      const T dy = (static_cast<T>(j) + half) - rec.m[1];
+      const T B = fma(rec.h[1], dy, Bz);
+      const T C = fma(fma(rec.h[3], dy, h4dz), dy, h5dzz);
+      const T elo = in_row ? rec.elo : static_cast<T>(INFINITY);
+      const T *__restrict__ vrow = vslice + static_cast<int64_t>(j) * D2;
+      T vv[R];
+#pragma unroll
+      for (int q = 0; q < R / kq; ++q)
+        *reinterpret_cast<Q *>(vv + q * kq) = *reinterpret_cast<const Q *>(vrow + q * kq);
+      T s0 = 0, s1 = 0;
+#pragma unroll
+      for (int k = 0; k < R; ++k) {
+        // Explicit FMAs keep the row-invariant products of dx_k from being
+        // hoisted into extra registers.
+        const T dx = dxk[k];
+        const T sl = fma(fma(rec.h[0], dx, B), dx, C);
+        const T e = neg_exp2(sl);
+        const bool skip = (sl < static_cast<T>(0)) || (e < elo);
+        const T w = skip ? static_cast<T>(0) : vv[k] * e;
+        wk[k] += w;
+        s0 += w;
+        s1 = fma(w, dx, s1);
+      }
+      const T dys0 = dy * s0, dzs0 = dz * s0;
+      Y0 += dys0;
+      Z0 += dzs0;
+      YY += dy * dys0;
+      YZ += dz * dys0;
+      ZZ += dz * dzs0;
+      Y1 += dy * s1;
+      Z1 += dz * s1;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const T wx = wk[k] * dxk[k];
+    T0 += wk[k];
+    T1 += wx;
+    T2 += wx * dxk[k];
+  }
+}
+
 // Records in brick order (tile_offsets, flatten_ids; isect_ids optional),
 // one lane per record.  kRows = false: each record's ten partials go out
 // through global atomics.  kRows = true: they are stored as the row
@@ -286,7 +381,12 @@ __global__ __launch_bounds__(kBwdThreads) void voxel_bwd_kernel(
   // non-finite (uniform over the wave).
   const bool guard = ballot(rec.live && !rec.cu.ok && b.nk < nts) != 0;
   T T0 = 0, T1 = 0, T2 = 0, Y0 = 0, Z0 = 0, Y1 = 0, Z1 = 0, YY = 0, YZ = 0, ZZ = 0;
-  if (ballot(rec.live) != 0) {
+  bool full = false;
+  if constexpr (kExact && R % Quad<T>::n == 0)
+    full = vec && ballot(b.ni < nts || b.nj < nts || b.nk < nts) == 0;
+  if (full && ballot(rec.live) != 0) {
+    voxel_brick_full<T, R>(rec, b, v_vol, plane, D2, dx0, T0, T1, T2, Y0, Z0, Y1, Z1, YY, YZ, ZZ);
+  } else if (ballot(rec.live) != 0) {
     for (int li = 0; li < R; ++li) {
       if (!kExact && li >= nts) break;
       const int i = b.oi + li;
@@ -294,15 +394,8 @@ __global__ __launch_bounds__(kBwdThreads) void voxel_bwd_kernel(
       if (ballot(in_slice) == 0) continue;
       const T dz = (static_cast<T>(i) + half) - rec.m[2];
       // Rows of this slice the lane's ellipsoid can reach.
-      int j0 = b.oj, j1 = b.oj + b.nj - 1;
-      if (!in_slice) {
-        j1 = j0 - 1;
-      } else if (rec.cu.ok) {
-        const T bud_z = rec.cu.s - half * rec.cu.c3 * dz * dz;
-        if (!budget_range<T>(rec.m[1], -rec.cu.ky * dz, bud_z, rec.cu.inv_a2, b.oj,
-                             b.oj + b.nj - 1, j0, j1))
-          j1 = j0 - 1;
-      }
+      int j0, j1;
+      slice_rows(rec, b, in_slice, dz, j0, j1);
       const T h4dz = rec.h[4] * dz, h5dzz = rec.h[5] * dz * dz, Bz = rec.h[2] * dz;
       for (int lj = 0; lj < R; ++lj) {
         if (!kExact && lj >= nts) break;
