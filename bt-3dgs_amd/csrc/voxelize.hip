@@ -89,14 +89,12 @@ __global__ __launch_bounds__(1024) void voxel_fwd_kernel(
     const int32_t *__restrict__ tile_offsets, const int32_t *__restrict__ flatten_ids,
     int64_t n_isects, uint32_t n_keys, int64_t N, uint32_t D2, uint32_t D1, uint32_t D0,
     uint32_t ts, uint32_t n2, uint32_t n1, T *__restrict__ volume) {
-  using V2 = typename Vec<T>::v2;
   using V4 = typename Vec<T>::v4;
   extern __shared__ double smem_raw[];
   const uint32_t nt = blockDim.x;
-  const uint32_t nb = min(nt, kFwdBatch);            // records staged per batch
-  V4 *s_mo = reinterpret_cast<V4 *>(smem_raw);  // {mx, my, mz, o}
-  V4 *s_h0 = s_mo + nb;                           // {h0, h1, h2, h3}
-  V2 *s_h1 = reinterpret_cast<V2 *>(s_h0 + nb);   // {h4, h5}
+  const uint32_t nb = min(nt, kFwdBatch);  // records staged per batch
+  // Per staged record: {mx, my, mz, o}, {h0, h1, h2, h3}, {h4, h5, e bound, 0}.
+  V4 *s_rec = reinterpret_cast<V4 *>(smem_raw);
 
   const uint32_t key = xcd_swizzle(blockIdx.x, n_keys);
   const Brick b = brick_of(key, n2, n1, ts, D2, D1, D0);
@@ -121,8 +119,7 @@ __global__ __launch_bounds__(1024) void voxel_fwd_kernel(
     const int64_t idx = base + tid;
     if (tid < nb && idx < end) {
       int64_t g = flatten_ids[idx];
-      V4 mo, h0;
-      V2 h1;
+      V4 mo, h0, h1;
       if (g >= 0 && g < N) {
         T q[6], h[6];
 #pragma unroll
@@ -138,21 +135,26 @@ __global__ __launch_bounds__(1024) void voxel_fwd_kernel(
         h0.w = h[3];
         h1.x = h[4];
         h1.y = h[5];
-      } else {  // never passes: alpha = 0
+        // |o e| < 1e-6 tested as e < 1e-6 / |o| (equal up to the rounding of
+        // the cut-off itself; a NaN o gives a NaN bound that no e is below).
+        h1.z = thr / fabs(mo.w);
+      } else {  // never passes
         mo.x = mo.y = mo.z = mo.w = 0;
         h0.x = h0.y = h0.z = h0.w = 0;
         h1.x = h1.y = 0;
+        h1.z = static_cast<T>(INFINITY);
       }
-      s_mo[tid] = mo;
-      s_h0[tid] = h0;
-      s_h1[tid] = h1;
+      h1.w = 0;
+      s_rec[3 * tid] = mo;
+      s_rec[3 * tid + 1] = h0;
+      s_rec[3 * tid + 2] = h1;
     }
     __syncthreads();
     const int cnt = static_cast<int>(min(static_cast<int64_t>(nb), end - base));
     for (int t = 0; t < cnt; ++t) {
-      const V4 mo = s_mo[t];
-      const V4 h0 = s_h0[t];
-      const V2 h1 = s_h1[t];
+      const V4 mo = s_rec[3 * t];
+      const V4 h0 = s_rec[3 * t + 1];
+      const V4 h1 = s_rec[3 * t + 2];
       const T dy = py - mo.y, dz = pz - mo.z;
       const T B = h0.y * dy + h0.z * dz;
       const T C = (h0.w * dy + h1.x * dz) * dy + h1.y * dz * dz;
@@ -160,8 +162,9 @@ __global__ __launch_bounds__(1024) void voxel_fwd_kernel(
       for (int r = 0; r < R; ++r) {
         const T dx = (px0 + static_cast<T>(r)) - mo.x;
         const T sl = (h0.x * dx + B) * dx + C;
-        const T alpha = mo.w * neg_exp2(sl);
-        acc[r] += ((sl < static_cast<T>(0)) || (fabs(alpha) < thr)) ? static_cast<T>(0) : alpha;
+        const T e = neg_exp2(sl);
+        const bool skip = (sl < static_cast<T>(0)) || (e < h1.z);
+        acc[r] = fma(mo.w, skip ? static_cast<T>(0) : e, acc[r]);
       }
     }
   }
@@ -488,7 +491,7 @@ void launch_voxel_fwd(const T *means3d, const T *conics, const T *opac,
                       uint32_t ts, uint32_t n2, uint32_t n1, T *volume, hipStream_t stream) {
   const uint32_t nt = ts * ts * (ts / R);
   const size_t smem =
-      min(nt, kFwdBatch) * (2 * sizeof(typename Vec<T>::v4) + sizeof(typename Vec<T>::v2));
+      min(nt, kFwdBatch) * (3 * sizeof(typename Vec<T>::v4));
   voxel_fwd_kernel<T, R><<<dim3(n_keys), dim3(nt), smem, stream>>>(
       means3d, conics, opac, tile_offsets, flatten_ids, n_isects, n_keys, N, D2, D1, D0, ts, n2,
       n1, volume);
