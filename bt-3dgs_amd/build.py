@@ -32,6 +32,7 @@ SOURCES = [
     "voxelize.hip",
     "compact.hip",
     "densify.hip",
+    "loss.hip",
 ]
 
 ARCH = os.environ.get("R2S_OFFLOAD_ARCH", "gfx950")

@@ -76,6 +76,14 @@ _PLAIN = {
     "r2s_densify_split": (_i32, [_p, _i64, _p, _i64, _i64, _p, _p, _i32, _p]),
     "r2s_densify_duplicate": (_i32, [_p, _i64, _p, _i64, _i64, _p, _i32, _p]),
     "r2s_densify_remove": (_i32, [_p, _i64, _p, _i32, _p]),
+    "r2s_projection_loss_workspace_bytes": (_i64, [_i64, _i32, _i32]),
+    "r2s_projection_loss_fwd_f32": (_i32, [_p, _p, _p, _p, _i64, _i32, _i32, _i32, _p, _p, _sz,
+                                           _p]),
+    "r2s_projection_loss_bwd_f32": (_i32, [_p, _p, _p, _p, _i64, _i32, _i32, _i32, _p, _p, _sz,
+                                           _p, _p]),
+    "r2s_tv_workspace_bytes": (_i64, []),
+    "r2s_tv_fwd_f32": (_i32, [_p, _i32, _i32, _i32, _i32, _p, _p, _sz, _p]),
+    "r2s_tv_bwd_f32": (_i32, [_p, _i32, _i32, _i32, _i32, _p, _p, _p]),
 }
 
 

@@ -962,3 +962,94 @@ def densify_remove(mask: Tensor, columns):
         _call("r2s_densify_remove", idx[n_sel:].data_ptr() if n_keep else None, n_keep, table,
               used, _stream(dev))
     return outs, n_sel
+
+
+# ---------------------------------------------------------- projection loss --
+
+def _loss_images(t: Tensor, name: str) -> Tensor:
+    _check(isinstance(t, torch.Tensor) and t.is_cuda, f"{name} must be a CUDA tensor")
+    _check(t.dtype == torch.float32, f"{name} must be float32, got {t.dtype}")
+    return t.contiguous()
+
+
+def projection_loss_fwd(render: Tensor, target: Tensor, edge_target: Optional[Tensor],
+                        edge_mask: Optional[Tensor], window_size: int = 11):
+    """Losses [3] = (mean |r - t|, 1 - mean SSIM(r, t), mean m |r - e|) over
+    images [n, H, W] (loss.py:135-172, metric.py:36-54), and the workspace the
+    backward needs."""
+    r = _loss_images(render, "render")
+    _check(r.dim() == 3, "render must be [n, H, W]")
+    t = _loss_images(target, "target")
+    _check(t.shape == r.shape, "target must have the render's shape")
+    if (edge_target is None) != (edge_mask is None):
+        raise RuntimeError("edge_target and edge_mask go together")
+    e = m = None
+    if edge_target is not None:
+        e = _loss_images(edge_target, "edge_target")
+        m = _loss_images(edge_mask, "edge_mask")
+        _check(e.shape == r.shape and m.shape == r.shape,
+               "edge_target and edge_mask must have the render's shape")
+    n, H, W = r.shape
+    dev = r.device
+    lib = _lib()
+    losses = torch.empty(3, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        ws = _workspace(lib.r2s_projection_loss_workspace_bytes(n, H, W), dev)
+        _call("r2s_projection_loss_fwd_f32", _ptr(r), _ptr(t), _ptr(e), _ptr(m), n, H, W,
+              int(window_size), _ptr(losses), _ptr(ws), ws.numel(), _stream(dev))
+    return losses, ws
+
+
+def projection_loss_bwd(render: Tensor, target: Tensor, edge_target: Optional[Tensor],
+                        edge_mask: Optional[Tensor], grad_losses: Tensor, workspace: Tensor,
+                        window_size: int = 11) -> Tensor:
+    """v_render [n, H, W] for upstream gradients grad_losses [3] of the three losses."""
+    r = _loss_images(render, "render")
+    t = _loss_images(target, "target")
+    e = None if edge_target is None else _loss_images(edge_target, "edge_target")
+    m = None if edge_mask is None else _loss_images(edge_mask, "edge_mask")
+    g = _loss_images(grad_losses, "grad_losses")
+    _check(g.numel() == 3, "grad_losses must hold three values")
+    n, H, W = r.shape
+    dev = r.device
+    out = torch.empty_like(r)
+    with torch.cuda.device(dev):
+        _call("r2s_projection_loss_bwd_f32", _ptr(r), _ptr(t), _ptr(e), _ptr(m), n, H, W,
+              int(window_size), _ptr(g), _ptr(workspace), workspace.numel(), _ptr(out),
+              _stream(dev))
+    return out
+
+
+# ---------------------------------------------------------------------- TV --
+
+def _tv_volume(vol: Tensor) -> Tensor:
+    v = _loss_images(vol, "volume")
+    _check(v.dim() == 3, "tv_3d_loss expects 3D volume")
+    _check(v.numel() < 2 ** 31 * 256, "volume too large")
+    return v
+
+
+def tv_fwd(volume: Tensor, mean: bool = True) -> Tensor:
+    """loss.py:10-21 compute_tv_loss of a [D0, D1, D2] volume (0-dim result)."""
+    v = _tv_volume(volume)
+    dev = v.device
+    lib = _lib()
+    out = torch.empty((), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        ws = _workspace(lib.r2s_tv_workspace_bytes(), dev)
+        _call("r2s_tv_fwd_f32", _ptr(v), *v.shape, int(bool(mean)), _ptr(out), _ptr(ws),
+              ws.numel(), _stream(dev))
+    return out
+
+
+def tv_bwd(volume: Tensor, grad_out: Tensor, mean: bool = True) -> Tensor:
+    """d tv / d volume scaled by the upstream gradient grad_out (0-dim)."""
+    v = _tv_volume(volume)
+    g = _loss_images(grad_out, "grad_out")
+    _check(g.numel() == 1, "grad_out must be a scalar")
+    dev = v.device
+    out = torch.empty_like(v)
+    with torch.cuda.device(dev):
+        _call("r2s_tv_bwd_f32", _ptr(v), *v.shape, int(bool(mean)), _ptr(g), _ptr(out),
+              _stream(dev))
+    return out

@@ -47,6 +47,10 @@ mask_split = _make_cuda_func("mask_split")
 densify_split = _make_cuda_func("densify_split")
 densify_duplicate = _make_cuda_func("densify_duplicate")
 densify_remove = _make_cuda_func("densify_remove")
+projection_loss_fwd = _make_cuda_func("projection_loss_fwd")
+projection_loss_bwd = _make_cuda_func("projection_loss_bwd")
+tv_fwd = _make_cuda_func("tv_fwd")
+tv_bwd = _make_cuda_func("tv_bwd")
 
 
 def is_cuda_extension_available() -> bool:

@@ -1,0 +1,189 @@
+"""Training losses that feed the Gaussian backward, as fused HIP kernels.
+
+Drop-in for the projection and volume terms of ``src/utils/loss.py`` and for
+``ssim2d`` of ``src/utils/metric.py``:
+
+* ``projection_losses`` returns the L1, 1 - SSIM and masked edge L1 terms of
+  ``BinaryTreeLossComputer`` (loss.py:135-172) from one forward launch (plus
+  a one-block reduction); autograd's backward is one launch that produces
+  ``v_image`` directly.  The reference runs five 2-D convolutions and a few
+  dozen element-wise kernels for the same values and as many again backward.
+* ``compute_tv_loss`` (loss.py:10-21) is one reduction launch forward and one
+  element-wise launch backward.
+* ``LossComputer`` / ``BinaryTreeLossComputer`` keep the reference's
+  constructor arguments and output dictionary (loss.py:74-172).
+
+Images and volumes are float32 CUDA tensors, as the trainer produces them;
+gradients flow to the renders / volume only (targets, masks and edge
+targets are data).
+"""
+
+from __future__ import annotations
+
+from typing import Dict, Optional, Tuple
+
+import torch
+from torch import Tensor
+
+from ..cuda import _wrapper as W
+
+__all__ = ["projection_losses", "ssim2d", "compute_tv_loss", "compute_edge_loss",
+           "LossComputer", "BinaryTreeLossComputer"]
+
+
+class _ProjectionLoss(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, render, target, edge_target, edge_mask, window_size):
+        losses, ws = W.projection_loss_fwd(render, target, edge_target, edge_mask, window_size)
+        ctx.save_for_backward(render, target, edge_target, edge_mask, ws)
+        ctx.window_size = window_size
+        return losses
+
+    @staticmethod
+    def backward(ctx, grad):
+        if any(ctx.needs_input_grad[1:4]):
+            raise NotImplementedError("gradients w.r.t. targets, edge targets or edge masks "
+                                      "are not provided")
+        render, target, edge_target, edge_mask, ws = ctx.saved_tensors
+        g = W.projection_loss_bwd(render, target, edge_target, edge_mask,
+                                  grad.to(torch.float32).contiguous(), ws, ctx.window_size)
+        return g, None, None, None, None
+
+
+def _planes(t: Tensor) -> Tensor:
+    """[N, H, W, K] (the trainer's renders layout) -> [N*K, H, W] images."""
+    if t.dim() != 4:
+        raise ValueError(f"expected [N, H, W, C] images, got shape {tuple(t.shape)}")
+    n, h, w, k = t.shape
+    return t.permute(0, 3, 1, 2).reshape(n * k, h, w).contiguous()
+
+
+def _as_float(t: Tensor) -> Tensor:
+    return t if t.dtype == torch.float32 else t.to(torch.float32)
+
+
+def projection_losses(renders: Tensor, targets: Tensor, edge_mask: Optional[Tensor] = None,
+                      edge_targets: Optional[Tensor] = None,
+                      ssim_window: int = 11) -> Tuple[Tensor, Tensor, Tensor]:
+    """(mean |r - t|, 1 - ssim2d(r, t), mean(edge_mask |r - edge_targets|)) of
+    renders / targets [N, H, W, C] (loss.py:143-158).  ``edge_targets``
+    defaults to ``targets``; without an edge mask the edge term is zero."""
+    if renders.shape != targets.shape:
+        raise AssertionError("Input shapes must match for SSIM")
+    if renders.dtype != torch.float32:
+        raise TypeError(f"renders must be float32, got {renders.dtype}")
+    r = _planes(renders)
+    t = _planes(_as_float(targets.detach()))
+    e = m = None
+    if edge_mask is not None:
+        et = targets if edge_targets is None else edge_targets
+        if torch.broadcast_shapes(edge_mask.shape, et.shape, renders.shape) != renders.shape:
+            raise ValueError("edge_mask and edge_targets must broadcast to the renders' shape")
+        e = _planes(_as_float(et.detach()).expand(renders.shape))
+        m = _planes(_as_float(edge_mask.detach()).expand(renders.shape))
+    losses = _ProjectionLoss.apply(r, t, e, m, int(ssim_window))
+    edge = losses[2] if edge_mask is not None else torch.zeros((), device=renders.device)
+    return losses[0], losses[1], edge
+
+
+def ssim2d(img1: Tensor, img2: Tensor, window_size: int = 11) -> Tensor:
+    """metric.py:36-54: mean SSIM of [N, C, H, W] images (differentiable in img1)."""
+    if img1.shape != img2.shape:
+        raise AssertionError("Input shapes must match for SSIM")
+    n, c, h, w = img1.shape
+    a = img1.reshape(n * c, h, w).contiguous()
+    b = _as_float(img2.detach()).reshape(n * c, h, w).contiguous()
+    return 1.0 - _ProjectionLoss.apply(a, b, None, None, int(window_size))[1]
+
+
+def compute_edge_loss(pred: Tensor, target: Tensor, edge_mask: Tensor) -> Tensor:
+    """loss.py:23-24: (edge_mask * |pred - target|).mean()."""
+    return projection_losses(pred, target, edge_mask, target)[2]
+
+
+class _TV(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, vol, mean):
+        ctx.save_for_backward(vol)
+        ctx.mean = mean
+        return W.tv_fwd(vol, mean)
+
+    @staticmethod
+    def backward(ctx, grad):
+        (vol,) = ctx.saved_tensors
+        return W.tv_bwd(vol, grad.to(torch.float32).reshape(1).contiguous(), ctx.mean), None
+
+
+def compute_tv_loss(vol: Tensor, reduction: str = "mean") -> Tensor:
+    """loss.py:10-21: anisotropic TV of a [D0, D1, D2] (or [1, D0, D1, D2]) volume."""
+    if vol.dim() == 4 and vol.size(0) == 1:
+        vol = vol[0]
+    assert vol.dim() == 3, "tv_3d_loss expects 3D volume"
+    return _TV.apply(vol.contiguous(), reduction == "mean")
+
+
+class LossComputer:
+    """loss.py:74-103: weighted projection L1 / SSIM and volume TV."""
+
+    def __init__(self, w_l1: float, w_ssim: float, w_tv: float, ssim_window: int = 11):
+        self.w_l1 = w_l1
+        self.w_ssim = w_ssim
+        self.w_tv = w_tv
+        self.ssim_window = ssim_window
+
+    def __call__(self, renders: Tensor, targets: Tensor,
+                 volume_pred: Optional[Tensor] = None) -> Dict[str, Tensor]:
+        out: Dict[str, Tensor] = {}
+        l1, ssim_loss, _ = projection_losses(renders, targets, ssim_window=self.ssim_window)
+        out["proj_l1"] = l1
+        out["proj_ssim"] = ssim_loss
+        out["vol_tv"] = _tv_term(self.w_tv, volume_pred, renders.device)
+        out["total"] = self.w_l1 * l1 + self.w_ssim * ssim_loss + self.w_tv * out["vol_tv"]
+        return out
+
+
+class BinaryTreeLossComputer:
+    """loss.py:105-172: projection L1 / SSIM, masked edge L1, volume TV and
+    the hierarchy term (computed by the caller)."""
+
+    def __init__(self, w_l1: float, w_ssim: float, w_tv: float, w_edge: float,
+                 w_hierarchy: float = 0.0, ssim_window: int = 11):
+        self.w_l1 = w_l1
+        self.w_ssim = w_ssim
+        self.w_tv = w_tv
+        self.w_edge = w_edge
+        self.w_hierarchy = w_hierarchy
+        self.ssim_window = ssim_window
+
+    def __call__(self, renders: Tensor, targets: Tensor, edge_mask: Optional[Tensor],
+                 volume_pred: Optional[Tensor] = None,
+                 hierarchy_loss: Optional[Tensor] = None,
+                 edge_targets: Optional[Tensor] = None,
+                 edge_weight_override: Optional[float] = None) -> Dict[str, Tensor]:
+        out: Dict[str, Tensor] = {}
+        if edge_targets is None:
+            edge_targets = targets
+        l1, ssim_loss, edge_loss = projection_losses(renders, targets, edge_mask, edge_targets,
+                                                     self.ssim_window)
+        out["proj_l1"] = l1
+        out["proj_ssim"] = ssim_loss
+        out["vol_tv"] = _tv_term(self.w_tv, volume_pred, renders.device)
+        out["edge"] = edge_loss
+        if hierarchy_loss is None:
+            hierarchy_loss = torch.zeros((), device=renders.device)
+        out["hierarchy"] = hierarchy_loss
+        edge_weight = self.w_edge if edge_weight_override is None else float(edge_weight_override)
+        out["edge_weight"] = torch.tensor(edge_weight, device=renders.device)
+        out["total"] = (self.w_l1 * l1 + self.w_ssim * ssim_loss + self.w_tv * out["vol_tv"]
+                        + edge_weight * edge_loss + self.w_hierarchy * hierarchy_loss)
+        return out
+
+
+def _tv_term(w_tv: float, volume_pred: Optional[Tensor], device) -> Tensor:
+    # loss.py:93-99 / 159-165: a volume that is not 3-D after squeezing gives 0.
+    if w_tv > 0 and volume_pred is not None:
+        try:
+            return compute_tv_loss(volume_pred.squeeze(), reduction="mean")
+        except Exception:
+            return torch.zeros((), device=device)
+    return torch.zeros((), device=device)

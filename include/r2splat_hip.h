@@ -607,6 +607,59 @@ int r2s_densify_remove(const int64_t *keep, int64_t n_keep,
                        const r2s_column_t *columns, int32_t n_columns,
                        r2s_stream_t stream);
 
+/* ---------------------------------------------------------------------- */
+/* Projection loss (L1 + SSIM + masked edge L1)                            */
+/* ---------------------------------------------------------------------- */
+
+/* Workspace of r2s_projection_loss_fwd/bwd: the SSIM partial-derivative
+ * maps (3 floats per pixel) and per-tile sums; the forward fills it, the
+ * backward reads it, so keep it between the two calls. */
+int64_t r2s_projection_loss_workspace_bytes(int64_t n_images, int32_t H, int32_t W);
+
+/* src/utils/loss.py:135-172 (BinaryTreeLossComputer.__call__, projection
+ * terms) with ssim2d of src/utils/metric.py:36-54: render, target,
+ * edge_target, edge_mask [n_images, H, W] float32 (one channel each; the
+ * edge pair may both be NULL) ->
+ * losses[3] (device) = { mean |render - target|,
+ *                        1 - mean SSIM(render, target),
+ *                        mean edge_mask |render - edge_target| }.
+ * Gaussian window of window_size (odd, <= 15) and sigma 1.5, zero padding. */
+int r2s_projection_loss_fwd_f32(const float *render, const float *target,
+                                const float *edge_target, const float *edge_mask,
+                                int64_t n_images, int32_t H, int32_t W,
+                                int32_t window_size, float *losses, void *workspace,
+                                size_t workspace_bytes, r2s_stream_t stream);
+
+/* The VJP of the three losses above (autograd's backward of loss.py:143-172):
+ * grad_scales[3] (device) = upstream gradients of the three losses ->
+ * v_render [n_images, H, W].  Reads the workspace the forward filled. */
+int r2s_projection_loss_bwd_f32(const float *render, const float *target,
+                                const float *edge_target, const float *edge_mask,
+                                int64_t n_images, int32_t H, int32_t W,
+                                int32_t window_size, const float *grad_scales,
+                                const void *workspace, size_t workspace_bytes,
+                                float *v_render, r2s_stream_t stream);
+
+/* ---------------------------------------------------------------------- */
+/* Volume TV regulariser                                                   */
+/* ---------------------------------------------------------------------- */
+
+/* Workspace of r2s_tv_fwd_f32 (per-block partial sums). */
+int64_t r2s_tv_workspace_bytes(void);
+
+/* src/utils/loss.py:10-21 compute_tv_loss: volume [D0, D1, D2] float32 ->
+ * out[0] (device) = sum over the three axes of |v[i+1] - v[i]|, divided by
+ * max(1, number of differences) when `mean` is nonzero (reduction "mean"). */
+int r2s_tv_fwd_f32(const float *volume, int32_t D0, int32_t D1, int32_t D2,
+                   int32_t mean, float *out, void *workspace, size_t workspace_bytes,
+                   r2s_stream_t stream);
+
+/* Its VJP (autograd's backward of loss.py:14-21): grad_out[0] (device) ->
+ * v_volume [D0, D1, D2], sign(0) = 0 as torch.abs. */
+int r2s_tv_bwd_f32(const float *volume, int32_t D0, int32_t D1, int32_t D2,
+                   int32_t mean, const float *grad_out, float *v_volume,
+                   r2s_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,120 @@
+"""Fused projection loss (L1 + SSIM + edge) and volume TV against the oracle.
+
+The oracle is float64 on the float32 inputs; the kernels are float32 with a
+separable window, so values agree to float32 rounding of the moment sums:
+losses within 1e-5 absolute, gradients within a small fraction of their
+largest magnitude.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import np32
+from oracle import loss as L
+from r2splat.ops import loss as LO
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _images(n, h, w, seed, edge=True):
+    rng = np.random.default_rng(seed)
+    x = rng.uniform(0, 1, (n, h, w)).astype(np.float32)
+    y = np.clip(x + rng.normal(0, 0.15, x.shape), 0, 1).astype(np.float32)
+    e = np.clip(x + rng.normal(0, 0.3, x.shape), 0, 1).astype(np.float32) if edge else None
+    m = (rng.uniform(size=x.shape) < 0.2).astype(np.float32) if edge else None
+    return x, y, e, m
+
+
+def _t(a):
+    return None if a is None else torch.from_numpy(a)[..., None].to(DEV)  # [n, H, W, 1]
+
+
+CASES = [(1, 64, 64, 11), (3, 50, 70, 11), (1, 512, 512, 11), (2, 33, 47, 7), (1, 40, 40, 1),
+         (1, 45, 38, 15)]
+
+
+@pytest.mark.parametrize("n,h,w,ws", CASES)
+@pytest.mark.parametrize("edge", [True, False])
+def test_projection_losses_and_gradient(n, h, w, ws, edge):
+    x, y, e, m = _images(n, h, w, 100 + h + ws, edge)
+    scales = (1.0, 0.25, 0.8)
+    r = _t(x).requires_grad_(True)
+    l1, sl, ed = LO.projection_losses(r, _t(y), _t(m), _t(e), ssim_window=ws)
+    el1, esl, eed = L.projection_losses(x, y, e, m, ws)
+    assert abs(l1.item() - el1) < 1e-6 * max(1, el1) + 1e-7
+    assert abs(sl.item() - esl) < 1e-5
+    assert abs(ed.item() - eed) < 1e-6 * max(1, eed) + 1e-7
+    (scales[0] * l1 + scales[1] * sl + scales[2] * ed).backward()
+    g = np32(r.grad)[..., 0]
+    expect = L.projection_loss_grad(x, y, e, m, scales, ws)
+    scale = np.abs(expect).max()
+    err = np.abs(g - expect)
+    assert err.max() < 2e-3 * scale, (err.max(), scale)
+    assert np.median(err) < 1e-5 * scale
+
+
+def test_projection_loss_is_deterministic():
+    x, y, e, m = _images(2, 96, 80, 7)
+    outs = []
+    for _ in range(2):
+        r = _t(x).requires_grad_(True)
+        l1, sl, ed = LO.projection_losses(r, _t(y), _t(m), _t(e))
+        (l1 + sl + ed).backward()
+        outs.append((l1.item(), sl.item(), ed.item(), r.grad.clone()))
+    assert outs[0][:3] == outs[1][:3]
+    assert torch.equal(outs[0][3], outs[1][3])
+
+
+def test_binary_tree_loss_computer_matches_the_oracle_total():
+    x, y, e, m = _images(1, 128, 96, 8)
+    rng = np.random.default_rng(9)
+    vol = rng.normal(size=(32, 32, 32)).astype(np.float32)
+    comp = LO.BinaryTreeLossComputer(w_l1=1.0, w_ssim=0.25, w_tv=0.05, w_edge=0.5,
+                                     w_hierarchy=0.05, ssim_window=11)
+    r = _t(x).requires_grad_(True)
+    v = torch.from_numpy(vol)[None].to(DEV).requires_grad_(True)
+    hier = torch.tensor(0.3, device=DEV)
+    out = comp(r, _t(y), _t(m), v, hierarchy_loss=hier, edge_targets=_t(e),
+               edge_weight_override=0.7)
+    assert set(out) == {"proj_l1", "proj_ssim", "vol_tv", "edge", "hierarchy", "edge_weight",
+                        "total"}
+    el1, esl, eed = L.projection_losses(x, y, e, m)
+    etv = L.tv(vol)
+    expect = 1.0 * el1 + 0.25 * esl + 0.05 * etv + 0.7 * eed + 0.05 * 0.3
+    assert abs(out["total"].item() - expect) < 2e-5
+    out["total"].backward()
+    gx = L.projection_loss_grad(x, y, e, m, (1.0, 0.25, 0.7))
+    assert np.abs(np32(r.grad)[..., 0] - gx).max() < 2e-3 * np.abs(gx).max()
+    np.testing.assert_allclose(np32(v.grad)[0], L.tv_grad(vol, 0.05), rtol=1e-6, atol=1e-12)
+    plain = LO.LossComputer(w_l1=1.0, w_ssim=0.25, w_tv=0.0)(_t(x), _t(y))
+    assert set(plain) == {"proj_l1", "proj_ssim", "vol_tv", "total"}
+    assert plain["vol_tv"].item() == 0.0
+
+
+def test_ssim2d_metric():
+    x, y, _, _ = _images(2, 70, 60, 10, edge=False)
+    a = torch.from_numpy(x)[:, None].to(DEV)
+    b = torch.from_numpy(y)[:, None].to(DEV)
+    assert abs(LO.ssim2d(a, b).item() - (1 - L.projection_losses(x, y)[1])) < 1e-5
+    assert abs(LO.ssim2d(a, a).item() - 1.0) < 1e-6
+
+
+@pytest.mark.parametrize("shape", [(32, 32, 32), (1, 40, 33, 17), (128, 128, 128), (1, 1, 5),
+                                   (1, 1, 1)])
+@pytest.mark.parametrize("reduction", ["mean", "sum"])
+def test_tv_loss_and_gradient(shape, reduction):
+    rng = np.random.default_rng(sum(shape))
+    vol = rng.normal(size=shape).astype(np.float32)
+    vol[..., :2] = 0.0  # exact zero differences: sign(0) = 0
+    v = torch.from_numpy(vol).to(DEV).requires_grad_(True)
+    tv = LO.compute_tv_loss(v, reduction)
+    base = vol[0] if vol.ndim == 4 else vol
+    expect = L.tv(base, reduction)
+    assert abs(tv.item() - expect) <= 1e-6 * abs(expect) + 1e-7
+    (tv * 3.0).backward()
+    g = np32(v.grad)
+    g = g[0] if g.ndim == 4 else g
+    np.testing.assert_allclose(g, L.tv_grad(base, 3.0, reduction), rtol=1e-6, atol=1e-12)
