@@ -91,21 +91,29 @@ class Projection:
 
 
 class TrainStep:
-    """Config-4 training-step shape on the projection workload: projection
-    fwd+bwd of one view, plus a 128^3 voxelization over [-1, 1]^3 (the volume
-    regulariser's input; v_volume ~ N(0,1) stands in for its gradient) sharing
-    the same prepared state, plus the densify/prune compaction of a 1 % mask
+    """Config-4 training-step shape on the projection workload: projection of
+    one view and a 128^3 voxelization over [-1, 1]^3 sharing the prepared
+    state; the trainer's loss (configs/trainer/binary_tree.yaml weights:
+    L1 1.0, SSIM 0.25 with an 11x11 window, TV 0.05, edge 1.0) against a
+    synthetic target and edge mask, its backward into v_image / v_volume,
+    the explicit backward; plus the densify/prune compaction of a 1 % mask
     every 100 steps."""
 
     def __init__(self, proj: Projection, dim=128, seed=2):
+        from r2splat.ops import loss
+
         g = torch.Generator().manual_seed(seed)
         dev = proj.viewmats.device
         self.proj = proj
         self.dim = dim
-        self.v_volume = torch.randn(dim, dim, dim, generator=g).to(dev)
         self.ranges = torch.full((3,), 2.0, device=dev)
         self.centers = torch.zeros(3, device=dev)
         self.masks = [torch.rand(N_PROJ, generator=g).to(dev) < 0.01 for _ in range(2)]
+        det = proj.det
+        self.targets = torch.rand(1, det, det, 1, generator=g).to(dev)
+        self.edge_mask = (torch.rand(1, det, det, 1, generator=g) < 0.1).float().to(dev)
+        self.loss = loss.BinaryTreeLossComputer(w_l1=1.0, w_ssim=0.25, w_tv=0.05, w_edge=1.0,
+                                                w_hierarchy=0.0, ssim_window=11)
         self.step_i = 0
 
     def step(self):
@@ -124,8 +132,8 @@ class TrainStep:
         vox = explicit.explicit_voxelize(state, means, self.ranges, self.centers, dim2=self.dim,
                                          dim1=self.dim, dim0=self.dim, tile_size=8, eps3d=EPS,
                                          radius_clip=3.0)
-        res.image.grad = p.v_images[k % 4]
-        vox.volume.grad = self.v_volume
+        out = self.loss(res.image.unsqueeze(-1), self.targets, self.edge_mask, vox.volume)
+        out["total"].backward()
         explicit.explicit_backward(state, means, quats, scales, opac)
         if self.step_i % 100 == 0:
             compact.split_indices(self.masks[(self.step_i // 100) % 2])
@@ -236,6 +244,75 @@ class DensifyTable:
         rows_out = n + n_sel
         hist = 4 * hw * (2 * h + 2 * n_sel)
         return 4 * w * (n + rows_out) + 8 * n + hist + (n if op == "duplicate" else 0)
+
+
+def torch_projection_loss(renders, targets, edge_mask, window):
+    """The reference's projection terms as plain torch ops (2-D conv2d SSIM of
+    metric.py:36-54, L1, masked edge L1), for timing beside the fused path."""
+    import torch.nn.functional as F
+
+    c1, c2 = 0.01 ** 2, 0.03 ** 2
+    r = renders.permute(0, 3, 1, 2).contiguous()
+    t = targets.permute(0, 3, 1, 2).contiguous()
+    pad = window.shape[-1] // 2
+    mu1, mu2 = F.conv2d(r, window, padding=pad), F.conv2d(t, window, padding=pad)
+    s11 = F.conv2d(r * r, window, padding=pad) - mu1 * mu1
+    s22 = F.conv2d(t * t, window, padding=pad) - mu2 * mu2
+    s12 = F.conv2d(r * t, window, padding=pad) - mu1 * mu2
+    ssim = (((2 * mu1 * mu2 + c1) * (2 * s12 + c2)) /
+            ((mu1 * mu1 + mu2 * mu2 + c1) * (s11 + s22 + c2))).mean()
+    l1 = (renders - targets).abs().mean()
+    edge = (edge_mask * (renders - targets).abs()).mean()
+    return l1 + 0.25 * (1 - ssim) + edge
+
+
+def torch_tv(vol):
+    """loss.py:10-21 as plain torch ops, for timing beside the fused path."""
+    dx = (vol[1:] - vol[:-1]).abs()
+    dy = (vol[:, 1:] - vol[:, :-1]).abs()
+    dz = (vol[:, :, 1:] - vol[:, :, :-1]).abs()
+    return (dx.sum() + dy.sum() + dz.sum()) / (dx.numel() + dy.numel() + dz.numel())
+
+
+def time_losses(dev, reps, det=DET):
+    """Loss forward + backward at the config-4 shapes, fused kernels beside
+    the same terms as plain torch ops: the 512^2 projection loss (L1, SSIM,
+    edge) and TV over 32^3 (the trainer's sampled volume) and 128^3."""
+    from r2splat.ops import loss
+
+    g = torch.Generator().manual_seed(5)
+    renders = torch.rand(1, det, det, 1, generator=g).to(dev).requires_grad_(True)
+    targets = torch.rand(1, det, det, 1, generator=g).to(dev)
+    edge_mask = (torch.rand(1, det, det, 1, generator=g) < 0.1).float().to(dev)
+    taps = torch.exp(-(torch.arange(11, dtype=torch.float32) - 5) ** 2 / 4.5)
+    taps = taps / taps.sum()
+    window = (taps[:, None] @ taps[None, :])[None, None].to(dev)
+
+    def fused():
+        renders.grad = None
+        l1, sl, ed = loss.projection_losses(renders, targets, edge_mask, targets)
+        (l1 + 0.25 * sl + ed).backward()
+
+    def composed():
+        renders.grad = None
+        torch_projection_loss(renders, targets, edge_mask, window).backward()
+
+    out = {"projection_loss_fused_ms": time_kernel(fused, reps) * 1e3,
+           "projection_loss_torch_ms": time_kernel(composed, reps) * 1e3}
+    for d in (32, 128):
+        vol = torch.randn(d, d, d, generator=g).to(dev).requires_grad_(True)
+
+        def tv_fused(vol=vol):
+            vol.grad = None
+            loss.compute_tv_loss(vol).backward()
+
+        def tv_composed(vol=vol):
+            vol.grad = None
+            torch_tv(vol).backward()
+
+        out[f"tv_{d}_fused_ms"] = time_kernel(tv_fused, reps) * 1e3
+        out[f"tv_{d}_torch_ms"] = time_kernel(tv_composed, reps) * 1e3
+    return out
 
 
 def time_steps(fn, steps, warmup):
@@ -505,8 +582,9 @@ def main():
         n_train = max(100, args.steps)
         t_train = time_steps(train.step, n_train, args.warmup)
         result["train_step"] = {
-            "workload": "config4 training-step shape: projection fwd+bwd + 128^3 voxelize "
-                        "fwd+bwd over [-1,1]^3 + compaction of a 1% mask every 100 steps",
+            "workload": "config4 training-step shape: projection fwd + 128^3 voxelize fwd over "
+                        "[-1,1]^3 + L1/SSIM/edge/TV loss fwd+bwd + explicit backward + "
+                        "compaction of a 1% mask every 100 steps",
             "steps": n_train, "ms_per_step": t_train * 1e3, "steps_per_s": 1.0 / t_train}
         log(f"training-step shape: {t_train * 1e3:.3f} ms/step")
 
@@ -532,6 +610,10 @@ def main():
             "voxelize_fwd_hbm_frac": (40 * i3 + 4 * n_vox) / t_vf / (HBM_PEAK_GBS * 1e9),
         }
         log(f"voxelization fwd+bwd: {t_vox * 1e3:.3f} ms/call, I3={i3}")
+
+    log("losses (fused vs torch ops)")
+    result["losses"] = time_losses(dev, args.kernel_reps)
+    log("losses: " + ", ".join(f"{k} {v:.3f}" for k, v in result["losses"].items()))
 
     if not args.no_densify:
         log("config-4 densify / prune table (500k rows + 500k archived, 1% masks)")
