@@ -33,6 +33,7 @@ SOURCES = [
     "compact.hip",
     "densify.hip",
     "loss.hip",
+    "adam.hip",
 ]
 
 ARCH = os.environ.get("R2S_OFFLOAD_ARCH", "gfx950")

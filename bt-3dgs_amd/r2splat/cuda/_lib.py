@@ -84,6 +84,7 @@ _PLAIN = {
     "r2s_tv_workspace_bytes": (_i64, []),
     "r2s_tv_fwd_f32": (_i32, [_p, _i32, _i32, _i32, _i32, _p, _p, _sz, _p]),
     "r2s_tv_bwd_f32": (_i32, [_p, _i32, _i32, _i32, _i32, _p, _p, _p]),
+    "r2s_adam_step_f32": (_i32, [_p, _i32, _p]),
 }
 
 
@@ -100,6 +101,15 @@ class SplitGeometry(ctypes.Structure):
 
     _fields_ = [("quats", _p), ("raw_scales", _p), ("scale_min", _f32 * 3),
                 ("scale_max", _f32 * 3), ("scale_eps", _f32), ("sigmoid_scales", _i32)]
+
+
+class AdamTensor(ctypes.Structure):
+    """r2s_adam_tensor_t: one parameter tensor of an Adam step."""
+
+    _fields_ = [("param", _p), ("grad", _p), ("exp_avg", _p), ("exp_avg_sq", _p), ("n", _i64),
+                ("lerp_weight", _f32), ("beta2", _f32), ("one_minus_beta2", _f32),
+                ("weight_decay", _f32), ("bias_correction2_sqrt", _f32), ("eps", _f32),
+                ("step_size", _f32)]
 
 
 # Column roles (R2S_COL_* in include/r2splat_hip.h).

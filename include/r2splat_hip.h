@@ -660,6 +660,40 @@ int r2s_tv_bwd_f32(const float *volume, int32_t D0, int32_t D1, int32_t D2,
                    int32_t mean, const float *grad_out, float *v_volume,
                    r2s_stream_t stream);
 
+/* ---------------------------------------------------------------------- */
+/* Adam step                                                               */
+/* ---------------------------------------------------------------------- */
+
+/* One parameter tensor of an Adam step: float32 device arrays of n elements
+ * and the step's scalars, computed by the caller in double as
+ * torch/optim/adam.py does and rounded to float:
+ *   lerp_weight = 1 - beta1, one_minus_beta2 = 1 - beta2,
+ *   bias_correction2_sqrt = (1 - beta2^t)^0.5,
+ *   step_size = -lr / (1 - beta1^t), t = the tensor's step count. */
+typedef struct r2s_adam_tensor {
+  float *param;
+  const float *grad;
+  float *exp_avg;
+  float *exp_avg_sq;
+  int64_t n;
+  float lerp_weight;
+  float beta2;
+  float one_minus_beta2;
+  float weight_decay;
+  float bias_correction2_sqrt;
+  float eps;
+  float step_size;
+} r2s_adam_tensor_t;
+
+/* torch.optim.Adam.step (torch/optim/adam.py _multi_tensor_adam, the
+ * non-capturable path) for every tensor of the list in one launch; the
+ * trainer's per-group optimizers are built by
+ * src/models/gaussian_model.py:514-530 and stepped by
+ * src/trainers/binary_tree.py:208-210.  Updates param, exp_avg and
+ * exp_avg_sq in place. */
+int r2s_adam_step_f32(const r2s_adam_tensor_t *tensors, int32_t n_tensors,
+                      r2s_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
