@@ -90,53 +90,108 @@ class Projection:
         return state
 
 
+# configs/optim/binary_tree.yaml initial learning rates.
+LRS = {"means": 6.0e-4, "scales": 4.0e-3, "quats": 3.0e-4, "opacities": 1.0e-2}
+
+
+class BenchTreeModel:
+    """The attributes of the reference's BinaryTreeGaussianModel that the
+    training step touches: the four parameters (cloned from the config-4
+    tree), parent / level, the archive of the N - 1 split ancestors and the
+    bounded-sigmoid scale activation."""
+
+    def __init__(self, proj: Projection):
+        dev = proj.viewmats.device
+        means, quats, scales, opac = (t.detach().clone() for t in proj.params)
+        self.means = torch.nn.Parameter(means)
+        self.quats = torch.nn.Parameter(quats)
+        self.scales = torch.nn.Parameter(scales)
+        self.opacities = torch.nn.Parameter(opac)
+        n = means.shape[0]
+        self.parent = torch.zeros(n, dtype=torch.int32, device=dev)
+        self.level = torch.full((n,), 19, dtype=torch.int32, device=dev)
+        h = n - 1
+        self.history_means = torch.zeros(h, 3, device=dev)
+        self.history_scales = torch.zeros(h, 3, device=dev)
+        self.history_quats = torch.zeros(h, 4, device=dev)
+        self.history_opacities = torch.zeros(h, device=dev)
+        self.history_parent = torch.zeros(h, dtype=torch.int32, device=dev)
+        self.history_level = torch.zeros(h, dtype=torch.int32, device=dev)
+        self._use_sigmoid_scale = True
+        self._scale_min = torch.tensor(SMIN)
+        self._scale_max = torch.tensor(SMAX)
+        self._scale_eps = 1e-5
+        self.trainable_param_keys = ["means", "scales", "quats", "opacities"]
+
+    def param_dict(self):
+        return {k: getattr(self, k) for k in self.trainable_param_keys}
+
+
 class TrainStep:
-    """Config-4 training-step shape on the projection workload: projection of
-    one view and a 128^3 voxelization over [-1, 1]^3 sharing the prepared
-    state; the trainer's loss (configs/trainer/binary_tree.yaml weights:
-    L1 1.0, SSIM 0.25 with an 11x11 window, TV 0.05, edge 1.0) against a
-    synthetic target and edge mask, its backward into v_image / v_volume,
-    the explicit backward; plus the densify/prune compaction of a 1 % mask
-    every 100 steps."""
+    """Config-4 training step: projection of one view and a 128^3
+    voxelization over [-1, 1]^3 sharing the prepared state; the trainer's
+    loss (configs/trainer/binary_tree.yaml weights: L1 1.0, SSIM 0.25 with an
+    11x11 window, TV 0.05, edge 1.0) against a synthetic target and edge
+    mask and its backward into v_image / v_volume; the explicit backward; the
+    Adam step of the four parameter groups (configs/optim/binary_tree.yaml
+    learning rates); and, every 100th step, a 1 % split and a 1 % prune of the
+    whole model table (parameters, Adam moments, tree buffers, statistics,
+    archive).  The model is a copy: the headline workload is not changed."""
 
     def __init__(self, proj: Projection, dim=128, seed=2):
+        from r2splat import optim
         from r2splat.ops import loss
 
         g = torch.Generator().manual_seed(seed)
         dev = proj.viewmats.device
         self.proj = proj
+        self.model = BenchTreeModel(proj)
+        self.opts = {k: optim.Adam([{"params": p, "name": k}], lr=LRS[k], eps=1e-15)
+                     for k, p in self.model.param_dict().items()}
+        n = self.model.means.shape[0]
+        self.state = {"grad2d": torch.zeros(n, device=dev), "count": torch.zeros(n, device=dev),
+                      "radii": torch.zeros(n, device=dev), "scene_scale": 1.0}
         self.dim = dim
         self.ranges = torch.full((3,), 2.0, device=dev)
         self.centers = torch.zeros(3, device=dev)
-        self.masks = [torch.rand(N_PROJ, generator=g).to(dev) < 0.01 for _ in range(2)]
         det = proj.det
         self.targets = torch.rand(1, det, det, 1, generator=g).to(dev)
         self.edge_mask = (torch.rand(1, det, det, 1, generator=g) < 0.1).float().to(dev)
         self.loss = loss.BinaryTreeLossComputer(w_l1=1.0, w_ssim=0.25, w_tv=0.05, w_edge=1.0,
                                                 w_hierarchy=0.0, ssim_window=11)
+        self.mask_gen = torch.Generator(device=dev).manual_seed(seed)
         self.step_i = 0
+        self.refines = 0
 
     def step(self):
-        from r2splat.ops import compact, explicit
+        from r2splat import optim
+        from r2splat.ops import densify, explicit
 
-        p = self.proj
-        means, quats, scales, opac = p.params
-        for t in p.params:
-            t.grad = None
+        p, m = self.proj, self.model
         k = self.step_i % 360
-        state = explicit.prepare_explicit_gaussians(quats, scales, opac, scale_min=SMIN,
-                                                    scale_max=SMAX)
-        res = explicit.explicit_rasterize(state, means, p.viewmats[k:k + 1], p.Ks[k:k + 1],
+        state = explicit.prepare_explicit_gaussians(m.quats, m.scales, m.opacities,
+                                                    scale_min=SMIN, scale_max=SMAX)
+        res = explicit.explicit_rasterize(state, m.means, p.viewmats[k:k + 1], p.Ks[k:k + 1],
                                           img_w=p.det, img_h=p.det, tile_size=16, eps2d=EPS,
                                           radius_clip=3.0, absgrad=True)
-        vox = explicit.explicit_voxelize(state, means, self.ranges, self.centers, dim2=self.dim,
-                                         dim1=self.dim, dim0=self.dim, tile_size=8, eps3d=EPS,
-                                         radius_clip=3.0)
+        vox = explicit.explicit_voxelize(state, m.means, self.ranges, self.centers,
+                                         dim2=self.dim, dim1=self.dim, dim0=self.dim,
+                                         tile_size=8, eps3d=EPS, radius_clip=3.0)
         out = self.loss(res.image.unsqueeze(-1), self.targets, self.edge_mask, vox.volume)
         out["total"].backward()
-        explicit.explicit_backward(state, means, quats, scales, opac)
-        if self.step_i % 100 == 0:
-            compact.split_indices(self.masks[(self.step_i // 100) % 2])
+        explicit.explicit_backward(state, m.means, m.quats, m.scales, m.opacities)
+        optim.step_all(self.opts)
+        for t in m.param_dict().values():
+            t.grad = None
+        if self.step_i % 100 == 99:
+            keys = m.trainable_param_keys
+            n = m.means.shape[0]
+            grow = torch.rand(n, device=m.means.device, generator=self.mask_gen) < 0.01
+            densify.split(m, self.opts, self.state, grow, keys)
+            n = m.means.shape[0]
+            prune = torch.rand(n, device=m.means.device, generator=self.mask_gen) < 0.01
+            densify.remove(m, self.opts, self.state, prune, keys)
+            self.refines += 1
         self.step_i += 1
         return state
 
@@ -312,6 +367,34 @@ def time_losses(dev, reps, det=DET):
 
         out[f"tv_{d}_fused_ms"] = time_kernel(tv_fused, reps) * 1e3
         out[f"tv_{d}_torch_ms"] = time_kernel(tv_composed, reps) * 1e3
+    return out
+
+
+def time_adam(proj: Projection, reps):
+    """The Adam step of the four config-4 parameter groups: one fused launch
+    (r2splat.optim.step_all) beside four torch.optim.Adam.step() calls."""
+    from r2splat import optim
+
+    out = {}
+    g = torch.Generator().manual_seed(6)
+    for name, cls in (("fused", optim.Adam), ("torch", torch.optim.Adam)):
+        params = {k: torch.nn.Parameter(t.detach().clone())
+                  for k, t in zip(("means", "quats", "scales", "opacities"), proj.params)}
+        opts = {k: cls([{"params": p, "name": k}], lr=LRS[k], eps=1e-15)
+                for k, p in params.items()}
+        for p in params.values():
+            p.grad = torch.randn(p.shape, generator=g).to(p.device)
+        if name == "fused":
+            fn = lambda: optim.step_all(opts)  # noqa: E731
+        else:
+            def fn():
+                for o in opts.values():
+                    o.step()
+        out[f"adam_{name}_ms"] = time_kernel(fn, reps) * 1e3
+    n_elem = sum(int(t.numel()) for t in proj.params)
+    out["adam_algorithmic_bytes"] = 4 * n_elem * 7  # read p, g, m, v; write p, m, v
+    out["adam_fused_hbm_frac"] = (out["adam_algorithmic_bytes"] / (out["adam_fused_ms"] * 1e-3)
+                                  / (HBM_PEAK_GBS * 1e9))
     return out
 
 
@@ -577,14 +660,16 @@ def main():
         result["copy_calibration_bytes"] = args.copy_bytes
 
     if not args.no_train:
-        log("config-4 training-step shape (projection + 128^3 voxelization + compaction / 100)")
+        log("config-4 training step (projection, voxelization, losses, Adam, densify / 100)")
         train = TrainStep(proj)
         n_train = max(100, args.steps)
         t_train = time_steps(train.step, n_train, args.warmup)
         result["train_step"] = {
-            "workload": "config4 training-step shape: projection fwd + 128^3 voxelize fwd over "
-                        "[-1,1]^3 + L1/SSIM/edge/TV loss fwd+bwd + explicit backward + "
-                        "compaction of a 1% mask every 100 steps",
+            "workload": "config4 training step: projection fwd + 128^3 voxelize fwd over "
+                        "[-1,1]^3 + L1/SSIM/edge/TV loss fwd+bwd + explicit backward + Adam "
+                        "step of the 4 parameter groups + a 1% split and 1% prune of the model "
+                        "table every 100 steps",
+            "refines": train.refines, "n_gaussians_after": int(train.model.means.shape[0]),
             "steps": n_train, "ms_per_step": t_train * 1e3, "steps_per_s": 1.0 / t_train}
         log(f"training-step shape: {t_train * 1e3:.3f} ms/step")
 
@@ -613,6 +698,7 @@ def main():
 
     log("losses (fused vs torch ops)")
     result["losses"] = time_losses(dev, args.kernel_reps)
+    result["losses"].update(time_adam(proj, args.kernel_reps))
     log("losses: " + ", ".join(f"{k} {v:.3f}" for k, v in result["losses"].items()))
 
     if not args.no_densify:
