@@ -312,6 +312,107 @@ int64_t tv_terms(int D0, int D1, int D2) {
          static_cast<int64_t>(D0) * D1 * (D2 - 1);
 }
 
+// ----------------------------------------------------------- hierarchy --
+// src/utils/loss.py:27-71 compute_hierarchy_loss: children whose parent
+// index is in the archive contribute relu(|diag(1/s) R^T (c - p)| - a)^2 / a^2
+// (R from the parent's normalised quaternion, s its activated scales
+// clamped at 1e-6, a = max(factor, 1e-6)); the loss is their mean.  The
+// forward also stores each child's gradient for a unit upstream gradient
+// and a count of 1, d/dc = 2 e / (a r) M^T M (c - p) with M = diag(1/s) R^T.
+__global__ __launch_bounds__(kLossThreads) void hierarchy_fwd_kernel(
+    const float *__restrict__ child_means, const int32_t *__restrict__ parent, int64_t n,
+    const float *__restrict__ hist_means, const float *__restrict__ hist_scales,
+    const float *__restrict__ hist_quats, int64_t hist_count, float allowed,
+    float *__restrict__ grad_unit, float *__restrict__ partials) {
+  __shared__ float s_red[2][kLossThreads / 64];
+  float acc = 0, cnt = 0;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kLossThreads + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * kLossThreads) {
+    const int32_t pid = parent[i];
+    float g0 = 0, g1 = 0, g2 = 0;
+    if (pid >= 0 && pid < hist_count) {
+      const float *q = hist_quats + 4 * static_cast<int64_t>(pid);
+      const float nq = sqrtf(q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3]);
+      const float den = fmaxf(nq, 1e-12f);
+      const float w = q[0] / den, x = q[1] / den, y = q[2] / den, z = q[3] / den;
+      // Rows of R^T are the columns of normalized_quat_to_rotmat (math.py:35-53).
+      const float r00 = 1 - 2 * (y * y + z * z), r01 = 2 * (x * y - w * z), r02 = 2 * (x * z + w * y);
+      const float r10 = 2 * (x * y + w * z), r11 = 1 - 2 * (x * x + z * z), r12 = 2 * (y * z - w * x);
+      const float r20 = 2 * (x * z - w * y), r21 = 2 * (y * z + w * x), r22 = 1 - 2 * (x * x + y * y);
+      const float *pm = hist_means + 3 * static_cast<int64_t>(pid);
+      const float *ps = hist_scales + 3 * static_cast<int64_t>(pid);
+      const float d0 = child_means[3 * i] - pm[0], d1 = child_means[3 * i + 1] - pm[1],
+                  d2 = child_means[3 * i + 2] - pm[2];
+      const float i0 = 1.0f / fmaxf(ps[0], 1e-6f), i1 = 1.0f / fmaxf(ps[1], 1e-6f),
+                  i2 = 1.0f / fmaxf(ps[2], 1e-6f);
+      // u = diag(1/s) R^T d
+      const float u0 = (r00 * d0 + r10 * d1 + r20 * d2) * i0;
+      const float u1 = (r01 * d0 + r11 * d1 + r21 * d2) * i1;
+      const float u2 = (r02 * d0 + r12 * d1 + r22 * d2) * i2;
+      const float rad = sqrtf(u0 * u0 + u1 * u1 + u2 * u2);
+      const float e = fmaxf(rad - allowed, 0.0f) / allowed;
+      acc += e * e;
+      cnt += 1.0f;
+      if (e > 0.0f) {
+        const float k = 2.0f * e / (allowed * rad);
+        const float v0 = k * u0 * i0, v1 = k * u1 * i1, v2 = k * u2 * i2;  // k diag(1/s) u
+        g0 = r00 * v0 + r01 * v1 + r02 * v2;  // R v
+        g1 = r10 * v0 + r11 * v1 + r12 * v2;
+        g2 = r20 * v0 + r21 * v1 + r22 * v2;
+      }
+    }
+    grad_unit[3 * i] = g0;
+    grad_unit[3 * i + 1] = g1;
+    grad_unit[3 * i + 2] = g2;
+  }
+  acc = wave_sum(acc);
+  cnt = wave_sum(cnt);
+  if (lane_id() == 0) {
+    s_red[0][threadIdx.x / 64] = acc;
+    s_red[1][threadIdx.x / 64] = cnt;
+  }
+  __syncthreads();
+  if (threadIdx.x < 2) {
+    float t = 0;
+    for (int k = 0; k < kLossThreads / 64; ++k) t += s_red[threadIdx.x][k];
+    partials[2 * blockIdx.x + threadIdx.x] = t;
+  }
+}
+
+// out[0] = sum / count (0 without valid children), out[1] = count.
+__global__ __launch_bounds__(kLossThreads) void hierarchy_reduce_kernel(
+    const float *__restrict__ partials, int64_t n_blocks, float *__restrict__ out) {
+  __shared__ double s_red[2][kLossThreads / 64];
+  double t[2] = {0, 0};
+  for (int64_t b = threadIdx.x; b < n_blocks; b += kLossThreads) {
+    t[0] += partials[2 * b];
+    t[1] += partials[2 * b + 1];
+  }
+  for (int k = 0; k < 2; ++k) {
+    const double v = wave_sum(t[k]);
+    if (lane_id() == 0) s_red[k][threadIdx.x / 64] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double s = 0, c = 0;
+    for (int k = 0; k < kLossThreads / 64; ++k) {
+      s += s_red[0][k];
+      c += s_red[1][k];
+    }
+    out[0] = c > 0 ? static_cast<float>(s / c) : 0.0f;
+    out[1] = static_cast<float>(c);
+  }
+}
+
+__global__ __launch_bounds__(kLossThreads) void hierarchy_bwd_kernel(
+    const float *__restrict__ grad_unit, int64_t n3, const float *__restrict__ grad_out,
+    const float *__restrict__ loss_count, float *__restrict__ v_means) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kLossThreads + threadIdx.x;
+  if (i >= n3) return;
+  const float c = loss_count[1];
+  v_means[i] = c > 0.0f ? grad_unit[i] * (grad_out[0] / c) : 0.0f;
+}
+
 struct LossSpace {
   float *A, *B, *C, *partials;
 };
@@ -362,6 +463,70 @@ int check_tv_args(int D0, int D1, int D2, const char *what) {
 }  // namespace r2s
 
 extern "C" {
+
+int64_t r2s_hierarchy_workspace_bytes(int64_t n) {
+  const int64_t blocks = std::max<int64_t>(
+      1, std::min<int64_t>(r2s::kTvBlocks, r2s::ceil_div(n > 0 ? n : 0, r2s::kLossThreads)));
+  r2s::Carver cv(nullptr);
+  cv.take<float>(3 * (n > 0 ? n : 0));
+  cv.take<float>(2 * blocks);
+  return static_cast<int64_t>(cv.used);
+}
+
+int r2s_hierarchy_loss_fwd_f32(const float *child_means, const int32_t *parent, int64_t n,
+                               const float *history_means, const float *parent_scales,
+                               const float *history_quats, int64_t history_count,
+                               float max_parent_distance_factor, float *out, void *workspace,
+                               size_t workspace_bytes, r2s_stream_t st) {
+  r2s::clear_error();
+  const char *what = "hierarchy_loss_fwd";
+  R2S_REQUIRE(n >= 0 && history_count >= 0, "%s: negative size", what);
+  R2S_REQUIRE(out != nullptr, "%s: null output", what);
+  R2S_REQUIRE(n == 0 || (child_means && parent), "%s: null child arrays", what);
+  R2S_REQUIRE(history_count == 0 || (history_means && parent_scales && history_quats),
+              "%s: null history arrays", what);
+  const int64_t need = r2s_hierarchy_workspace_bytes(n);
+  if (workspace == nullptr || static_cast<int64_t>(workspace_bytes) < need) {
+    r2s::set_error("%s: workspace of %zu bytes, %lld required", what, workspace_bytes,
+                   (long long)need);
+    return R2S_EWORKSPACE;
+  }
+  r2s::Carver cv(workspace);
+  float *grad_unit = cv.take<float>(3 * n);
+  const int64_t blocks =
+      std::max<int64_t>(1, std::min<int64_t>(r2s::kTvBlocks, r2s::ceil_div(n, r2s::kLossThreads)));
+  float *partials = cv.take<float>(2 * blocks);
+  hipStream_t stream = r2s::as_stream(st);
+  // loss.py:67: allowed = max(factor, 1e-6).
+  const float allowed = std::max(max_parent_distance_factor, 1e-6f);
+  r2s::hierarchy_fwd_kernel<<<dim3(static_cast<uint32_t>(blocks)), dim3(r2s::kLossThreads), 0,
+                              stream>>>(child_means, parent, n, history_means, parent_scales,
+                                        history_quats, history_count, allowed, grad_unit,
+                                        partials);
+  R2S_RETURN_IF(r2s::check_launch(what));
+  r2s::hierarchy_reduce_kernel<<<1, r2s::kLossThreads, 0, stream>>>(partials, blocks, out);
+  return r2s::check_launch(what);
+}
+
+int r2s_hierarchy_loss_bwd_f32(int64_t n, const float *grad_out, const float *loss_out,
+                               const void *workspace, size_t workspace_bytes, float *v_means,
+                               r2s_stream_t st) {
+  r2s::clear_error();
+  const char *what = "hierarchy_loss_bwd";
+  R2S_REQUIRE(n >= 0, "%s: negative size", what);
+  if (n == 0) return R2S_OK;
+  R2S_REQUIRE(grad_out && loss_out && v_means, "%s: null pointer", what);
+  if (workspace == nullptr ||
+      static_cast<int64_t>(workspace_bytes) < r2s_hierarchy_workspace_bytes(n)) {
+    r2s::set_error("%s: workspace smaller than the forward's", what);
+    return R2S_EWORKSPACE;
+  }
+  const float *grad_unit = static_cast<const float *>(workspace);
+  r2s::hierarchy_bwd_kernel<<<dim3(static_cast<uint32_t>(r2s::ceil_div(3 * n, r2s::kLossThreads))),
+                              dim3(r2s::kLossThreads), 0, r2s::as_stream(st)>>>(
+      grad_unit, 3 * n, grad_out, loss_out, v_means);
+  return r2s::check_launch(what);
+}
 
 int64_t r2s_tv_workspace_bytes(void) {
   return static_cast<int64_t>(r2s::kTvBlocks * sizeof(float));

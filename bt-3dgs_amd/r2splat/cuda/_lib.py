@@ -85,6 +85,9 @@ _PLAIN = {
     "r2s_tv_fwd_f32": (_i32, [_p, _i32, _i32, _i32, _i32, _p, _p, _sz, _p]),
     "r2s_tv_bwd_f32": (_i32, [_p, _i32, _i32, _i32, _i32, _p, _p, _p]),
     "r2s_adam_step_f32": (_i32, [_p, _i32, _p]),
+    "r2s_hierarchy_workspace_bytes": (_i64, [_i64]),
+    "r2s_hierarchy_loss_fwd_f32": (_i32, [_p, _p, _i64, _p, _p, _p, _i64, _f32, _p, _p, _sz, _p]),
+    "r2s_hierarchy_loss_bwd_f32": (_i32, [_i64, _p, _p, _p, _sz, _p, _p]),
 }
 
 

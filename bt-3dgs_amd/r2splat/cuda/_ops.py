@@ -1053,3 +1053,43 @@ def tv_bwd(volume: Tensor, grad_out: Tensor, mean: bool = True) -> Tensor:
         _call("r2s_tv_bwd_f32", _ptr(v), *v.shape, int(bool(mean)), _ptr(g), _ptr(out),
               _stream(dev))
     return out
+
+
+# --------------------------------------------------------- hierarchy loss --
+
+def hierarchy_loss_fwd(child_means: Tensor, parent: Tensor, history_means: Tensor,
+                       parent_scales: Tensor, history_quats: Tensor, history_count: int,
+                       max_parent_distance_factor: float = 1.0):
+    """loss.py:27-71 compute_hierarchy_loss with the archived scales already
+    activated: (out [2] = (loss, count), workspace for the backward)."""
+    c = _loss_images(child_means, "child_means")
+    _check(c.dim() == 2 and c.size(1) == 3, "child_means must be [N, 3]")
+    _check(isinstance(parent, torch.Tensor) and parent.is_cuda, "parent must be a CUDA tensor")
+    par = parent.to(torch.int32).contiguous()
+    _check(par.numel() == c.size(0), "parent must have one entry per child")
+    hm = _loss_images(history_means, "history_means")
+    hs = _loss_images(parent_scales, "parent_scales")
+    hq = _loss_images(history_quats, "history_quats")
+    _check(hm.size(0) >= history_count and hs.size(0) >= history_count and
+           hq.size(0) >= history_count, "history shorter than history_count")
+    n = c.size(0)
+    dev = c.device
+    lib = _lib()
+    out = torch.empty(2, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        ws = _workspace(lib.r2s_hierarchy_workspace_bytes(n), dev)
+        _call("r2s_hierarchy_loss_fwd_f32", _ptr(c), _ptr(par), n, _ptr(hm), _ptr(hs), _ptr(hq),
+              int(history_count), float(max_parent_distance_factor), _ptr(out), _ptr(ws),
+              ws.numel(), _stream(dev))
+    return out, ws
+
+
+def hierarchy_loss_bwd(n: int, grad_out: Tensor, out: Tensor, workspace: Tensor) -> Tensor:
+    """d loss / d child_means [N, 3] times the upstream gradient grad_out."""
+    g = _loss_images(grad_out, "grad_out")
+    dev = out.device
+    v = torch.empty((n, 3), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _call("r2s_hierarchy_loss_bwd_f32", n, _ptr(g), _ptr(out), _ptr(workspace),
+              workspace.numel(), _ptr(v), _stream(dev))
+    return v

@@ -51,6 +51,8 @@ projection_loss_fwd = _make_cuda_func("projection_loss_fwd")
 projection_loss_bwd = _make_cuda_func("projection_loss_bwd")
 tv_fwd = _make_cuda_func("tv_fwd")
 tv_bwd = _make_cuda_func("tv_bwd")
+hierarchy_loss_fwd = _make_cuda_func("hierarchy_loss_fwd")
+hierarchy_loss_bwd = _make_cuda_func("hierarchy_loss_bwd")
 
 
 def is_cuda_extension_available() -> bool:

@@ -10,6 +10,9 @@ Drop-in for the projection and volume terms of ``src/utils/loss.py`` and for
   dozen element-wise kernels for the same values and as many again backward.
 * ``compute_tv_loss`` (loss.py:10-21) is one reduction launch forward and one
   element-wise launch backward.
+* ``compute_hierarchy_loss`` (loss.py:27-71) gathers each child's archived
+  parent, measures it in the parent's scaled frame and stores its gradient
+  in one launch; the backward scales it.
 * ``LossComputer`` / ``BinaryTreeLossComputer`` keep the reference's
   constructor arguments and output dictionary (loss.py:74-172).
 
@@ -28,7 +31,7 @@ from torch import Tensor
 from ..cuda import _wrapper as W
 
 __all__ = ["projection_losses", "ssim2d", "compute_tv_loss", "compute_edge_loss",
-           "LossComputer", "BinaryTreeLossComputer"]
+           "compute_hierarchy_loss", "LossComputer", "BinaryTreeLossComputer"]
 
 
 class _ProjectionLoss(torch.autograd.Function):
@@ -120,6 +123,42 @@ def compute_tv_loss(vol: Tensor, reduction: str = "mean") -> Tensor:
         vol = vol[0]
     assert vol.dim() == 3, "tv_3d_loss expects 3D volume"
     return _TV.apply(vol.contiguous(), reduction == "mean")
+
+
+class _Hierarchy(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, child_means, parent, history_means, parent_scales, history_quats,
+                history_count, factor):
+        out, ws = W.hierarchy_loss_fwd(child_means, parent, history_means, parent_scales,
+                                       history_quats, history_count, factor)
+        ctx.save_for_backward(out, ws)
+        ctx.n = child_means.shape[0]
+        return out[0]
+
+    @staticmethod
+    def backward(ctx, grad):
+        out, ws = ctx.saved_tensors
+        v = W.hierarchy_loss_bwd(ctx.n, grad.to(torch.float32).reshape(1).contiguous(), out, ws)
+        return v, None, None, None, None, None, None
+
+
+def compute_hierarchy_loss(child_means: Tensor, parent_indices: Tensor, history_means: Tensor,
+                           history_scales: Tensor, history_quats: Tensor, scale_activation,
+                           max_parent_distance_factor: float = 1.0) -> Tensor:
+    """loss.py:27-71: mean squared excess of each child's distance from its
+    archived parent, in the parent's scaled frame, over the allowed radius.
+    The archive's scales go through ``scale_activation`` (the model's
+    activation) as one element-wise pass; the rest is one fused launch."""
+    if (child_means.numel() == 0 or parent_indices.numel() == 0 or history_means.numel() == 0
+            or history_scales.numel() == 0 or history_quats.numel() == 0):
+        return child_means.new_zeros(())
+    history_count = min(history_means.shape[0], history_scales.shape[0],
+                        history_quats.shape[0])
+    parent_scales = scale_activation(history_scales[:history_count].detach())
+    return _Hierarchy.apply(child_means, parent_indices, history_means.detach(),
+                            parent_scales.to(torch.float32).contiguous(),
+                            history_quats.detach(), int(history_count),
+                            float(max_parent_distance_factor))
 
 
 class LossComputer:

@@ -661,6 +661,33 @@ int r2s_tv_bwd_f32(const float *volume, int32_t D0, int32_t D1, int32_t D2,
                    r2s_stream_t stream);
 
 /* ---------------------------------------------------------------------- */
+/* Hierarchy loss                                                          */
+/* ---------------------------------------------------------------------- */
+
+/* Workspace of r2s_hierarchy_loss_fwd/bwd for n children. */
+int64_t r2s_hierarchy_workspace_bytes(int64_t n);
+
+/* src/utils/loss.py:27-71 compute_hierarchy_loss: child_means [n,3],
+ * parent [n] int32 (archive indices; out-of-range = no parent),
+ * history_means [h,3], parent_scales [h,3] (the archived scales already
+ * activated), history_quats [h,4] with h >= history_count ->
+ * out[0] (device) = mean over children with a parent of
+ * relu(|diag(1/max(s,1e-6)) R^T (c - p)| - a)^2 / a^2, a = max(factor, 1e-6)
+ * (0 when there is none), out[1] = that number of children.  Keep out and
+ * the workspace for the backward. */
+int r2s_hierarchy_loss_fwd_f32(const float *child_means, const int32_t *parent, int64_t n,
+                               const float *history_means, const float *parent_scales,
+                               const float *history_quats, int64_t history_count,
+                               float max_parent_distance_factor, float *out,
+                               void *workspace, size_t workspace_bytes,
+                               r2s_stream_t stream);
+
+/* Its VJP w.r.t. child_means: grad_out[0] (device) -> v_means [n,3]. */
+int r2s_hierarchy_loss_bwd_f32(int64_t n, const float *grad_out, const float *loss_out,
+                               const void *workspace, size_t workspace_bytes,
+                               float *v_means, r2s_stream_t stream);
+
+/* ---------------------------------------------------------------------- */
 /* Adam step                                                               */
 /* ---------------------------------------------------------------------- */
 

@@ -129,3 +129,33 @@ def tv_grad(vol, grad_out=1.0, reduction="mean"):
         g[tuple(hi)] += s
     scale = grad_out / max(1, count) if reduction == "mean" else grad_out
     return g * scale
+
+
+def hierarchy_loss(child_means, parent, hist_means, parent_scales, hist_quats, history_count,
+                   factor=1.0):
+    """loss.py:27-71 compute_hierarchy_loss (archived scales already activated),
+    float64: returns (loss, d loss / d child_means)."""
+    c = np.asarray(child_means, np.float64)
+    par = np.asarray(parent).astype(np.int64)
+    valid = (par >= 0) & (par < history_count)
+    grad = np.zeros_like(c)
+    if not valid.any():
+        return 0.0, grad
+    ids = par[valid]
+    q = np.asarray(hist_quats, np.float64)[ids]
+    q = q / np.maximum(np.linalg.norm(q, axis=1), 1e-12)[:, None]
+    w, x, y, z = q.T
+    R = np.stack([1 - 2 * (y * y + z * z), 2 * (x * y - w * z), 2 * (x * z + w * y),
+                  2 * (x * y + w * z), 1 - 2 * (x * x + z * z), 2 * (y * z - w * x),
+                  2 * (x * z - w * y), 2 * (y * z + w * x), 1 - 2 * (x * x + y * y)],
+                 -1).reshape(-1, 3, 3)
+    s = np.maximum(np.asarray(parent_scales, np.float64)[ids], 1e-6)
+    d = c[valid] - np.asarray(hist_means, np.float64)[ids]
+    u = np.einsum("nji,nj->ni", R, d) / s
+    r = np.linalg.norm(u, axis=1)
+    a = max(float(factor), 1e-6)
+    e = np.maximum(r - a, 0.0) / a
+    n = int(valid.sum())
+    k = np.where(e > 0, 2 * e / (a * np.where(r > 0, r, 1.0) * n), 0.0)
+    grad[valid] = np.einsum("nij,nj->ni", R, (k[:, None] * u / s))
+    return float((e * e).mean()), grad

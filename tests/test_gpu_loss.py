@@ -118,3 +118,32 @@ def test_tv_loss_and_gradient(shape, reduction):
     g = np32(v.grad)
     g = g[0] if g.ndim == 4 else g
     np.testing.assert_allclose(g, L.tv_grad(base, 3.0, reduction), rtol=1e-6, atol=1e-12)
+
+
+def _sigmoid_scales(raw):
+    return 5e-4 + (1.0 - 5e-4) * torch.sigmoid(raw)
+
+
+@pytest.mark.parametrize("n,h", [(5000, 3000), (20, 0), (64, 5)])
+def test_hierarchy_loss_and_gradient(n, h):
+    rng = np.random.default_rng(n + h)
+    hm = rng.normal(size=(max(h, 1), 3)).astype(np.float32)[:h]
+    hs = rng.normal(-1.5, 0.5, size=(h, 3)).astype(np.float32)
+    hq = rng.normal(size=(h, 4)).astype(np.float32)
+    par = rng.integers(-3, h + 3, n).astype(np.int32) if h else np.full(n, -1, np.int32)
+    base = hm[np.clip(par, 0, max(h - 1, 0))] if h else np.zeros((n, 3), np.float32)
+    cm = (base + rng.normal(0, 0.3, (n, 3))).astype(np.float32)
+    c = torch.from_numpy(cm).to(DEV).requires_grad_(True)
+    loss = LO.compute_hierarchy_loss(c, torch.from_numpy(par).to(DEV), torch.from_numpy(hm).to(DEV),
+                                     torch.from_numpy(hs).to(DEV), torch.from_numpy(hq).to(DEV),
+                                     _sigmoid_scales, 0.9)
+    if h == 0:
+        assert loss.item() == 0.0 and not loss.requires_grad
+        return
+    act = np32(_sigmoid_scales(torch.from_numpy(hs)))
+    exp_loss, exp_grad = L.hierarchy_loss(cm, par, hm, act, hq, h, 0.9)
+    assert abs(loss.item() - exp_loss) <= 1e-5 * max(1.0, exp_loss)
+    (loss * 2.0).backward()
+    g = np32(c.grad)
+    scale = np.abs(exp_grad).max() * 2.0 + 1e-30
+    assert np.abs(g - 2.0 * exp_grad).max() < 1e-4 * scale

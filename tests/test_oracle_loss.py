@@ -116,3 +116,35 @@ def test_tv_of_a_ramp_and_its_gradient():
     dz = (vt[:, :, 1:] - vt[:, :, :-1]).abs()
     ((dx.sum() + dy.sum() + dz.sum()) / (dx.numel() + dy.numel() + dz.numel()) * 2.5).backward()
     np.testing.assert_allclose(L.tv_grad(v, 2.5), vt.grad.numpy(), rtol=1e-12, atol=1e-15)
+
+
+def test_hierarchy_loss_closed_form_and_autograd():
+    # A child on the parent's second principal axis at 2.5 scales, factor 1.5:
+    # excess (2.5 - 1.5) / 1.5, squared.
+    q = np.array([[0.8, 0.2, -0.4, 0.4]])
+    qn = q / np.linalg.norm(q)
+    from scipy.spatial.transform import Rotation
+    R = Rotation.from_quat(qn[:, [1, 2, 3, 0]]).as_matrix()[0]
+    s = np.array([[0.3, 0.2, 0.5]])
+    p = np.array([[0.1, -0.2, 0.3]])
+    child = p + 2.5 * s[0, 1] * R[:, 1]
+    loss, _ = L.hierarchy_loss(child, np.array([0]), p, s, q, 1, 1.5)
+    assert abs(loss - ((2.5 - 1.5) / 1.5) ** 2) < 1e-12
+    # Random children: the gradient against autograd of a direct restatement.
+    rng = np.random.default_rng(5)
+    h, n = 20, 60
+    hm, hs, hq = rng.normal(size=(h, 3)), rng.uniform(0.05, 0.5, (h, 3)), rng.normal(size=(h, 4))
+    par = rng.integers(-2, h + 3, n)
+    cm = hm[np.clip(par, 0, h - 1)] + rng.normal(0, 0.4, (n, 3))
+    loss, grad = L.hierarchy_loss(cm, par, hm, hs, hq, h, 0.8)
+    ct = torch.tensor(cm, requires_grad=True)
+    valid = torch.tensor((par >= 0) & (par < h))
+    ids = torch.tensor(par)[valid]
+    qt = torch.nn.functional.normalize(torch.tensor(hq)[ids], dim=-1)
+    Rt = torch.tensor(Rotation.from_quat(qt.numpy()[:, [1, 2, 3, 0]]).as_matrix())
+    local = torch.einsum("nji,nj->ni", Rt, ct[valid] - torch.tensor(hm)[ids])
+    r = torch.linalg.norm(local / torch.tensor(hs)[ids].clamp_min(1e-6), dim=-1)
+    ref = (torch.relu(r - 0.8) / 0.8).square().mean()
+    ref.backward()
+    assert abs(loss - ref.item()) < 1e-12
+    np.testing.assert_allclose(grad, ct.grad.numpy(), rtol=1e-9, atol=1e-14)
