@@ -13,8 +13,8 @@ densify / prune rewrite of the config-4 model table, per-kernel event
 timings, the roofline of the dominant kernel and the CPU oracle baseline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                       [--no-voxel] [--no-train] [--no-densify] [--kernel-reps R]
-                       [--copy-bytes B]
+                       [--no-voxel] [--no-train] [--no-densify] [--no-losses]
+                       [--kernel-reps R] [--copy-bytes B]
 """
 
 from __future__ import annotations
@@ -108,15 +108,18 @@ class BenchTreeModel:
         self.scales = torch.nn.Parameter(scales)
         self.opacities = torch.nn.Parameter(opac)
         n = means.shape[0]
-        self.parent = torch.zeros(n, dtype=torch.int32, device=dev)
-        self.level = torch.full((n,), 19, dtype=torch.int32, device=dev)
         h = n - 1
-        self.history_means = torch.zeros(h, 3, device=dev)
-        self.history_scales = torch.zeros(h, 3, device=dev)
-        self.history_quats = torch.zeros(h, 4, device=dev)
-        self.history_opacities = torch.zeros(h, device=dev)
-        self.history_parent = torch.zeros(h, dtype=torch.int32, device=dev)
-        self.history_level = torch.zeros(h, dtype=torch.int32, device=dev)
+        # A stand-in archive of N - 1 ancestors: leaf i's parent is entry
+        # min(i, h - 1), holding that leaf's own parameters.
+        self.parent = torch.clamp(torch.arange(n, device=dev), max=h - 1).to(torch.int32)
+        self.level = torch.full((n,), 19, dtype=torch.int32, device=dev)
+        self.history_means = means[:h].clone()
+        self.history_scales = scales[:h].clone()
+        self.history_quats = quats[:h].clone()
+        self.history_opacities = opac[:h].clone()
+        self.history_parent = torch.clamp(torch.arange(h, device=dev) // 2 - 1, min=-1).to(
+            torch.int32)
+        self.history_level = torch.full((h,), 18, dtype=torch.int32, device=dev)
         self._use_sigmoid_scale = True
         self._scale_min = torch.tensor(SMIN)
         self._scale_max = torch.tensor(SMAX)
@@ -126,13 +129,18 @@ class BenchTreeModel:
     def param_dict(self):
         return {k: getattr(self, k) for k in self.trainable_param_keys}
 
+    @staticmethod
+    def activate_scale(raw):
+        return SMIN + (SMAX - SMIN) * torch.sigmoid(raw)
+
 
 class TrainStep:
     """Config-4 training step: projection of one view and a 128^3
     voxelization over [-1, 1]^3 sharing the prepared state; the trainer's
     loss (configs/trainer/binary_tree.yaml weights: L1 1.0, SSIM 0.25 with an
-    11x11 window, TV 0.05, edge 1.0) against a synthetic target and edge
-    mask and its backward into v_image / v_volume; the explicit backward; the
+    11x11 window, TV 0.05, edge 1.0, hierarchy 0.05) against a synthetic
+    target and edge mask and its backward into v_image / v_volume / means;
+    the explicit backward; the
     Adam step of the four parameter groups (configs/optim/binary_tree.yaml
     learning rates); and, every 100th step, a 1 % split and a 1 % prune of the
     whole model table (parameters, Adam moments, tree buffers, statistics,
@@ -158,14 +166,14 @@ class TrainStep:
         self.targets = torch.rand(1, det, det, 1, generator=g).to(dev)
         self.edge_mask = (torch.rand(1, det, det, 1, generator=g) < 0.1).float().to(dev)
         self.loss = loss.BinaryTreeLossComputer(w_l1=1.0, w_ssim=0.25, w_tv=0.05, w_edge=1.0,
-                                                w_hierarchy=0.0, ssim_window=11)
+                                                w_hierarchy=0.05, ssim_window=11)
         self.mask_gen = torch.Generator(device=dev).manual_seed(seed)
         self.step_i = 0
         self.refines = 0
 
     def step(self):
         from r2splat import optim
-        from r2splat.ops import densify, explicit
+        from r2splat.ops import densify, explicit, loss
 
         p, m = self.proj, self.model
         k = self.step_i % 360
@@ -177,7 +185,10 @@ class TrainStep:
         vox = explicit.explicit_voxelize(state, m.means, self.ranges, self.centers,
                                          dim2=self.dim, dim1=self.dim, dim0=self.dim,
                                          tile_size=8, eps3d=EPS, radius_clip=3.0)
-        out = self.loss(res.image.unsqueeze(-1), self.targets, self.edge_mask, vox.volume)
+        hier = loss.compute_hierarchy_loss(m.means, m.parent, m.history_means, m.history_scales,
+                                           m.history_quats, m.activate_scale, 1.0)
+        out = self.loss(res.image.unsqueeze(-1), self.targets, self.edge_mask, vox.volume,
+                        hierarchy_loss=hier)
         out["total"].backward()
         explicit.explicit_backward(state, m.means, m.quats, m.scales, m.opacities)
         optim.step_all(self.opts)
@@ -568,6 +579,7 @@ def main():
     ap.add_argument("--no-voxel", action="store_true")
     ap.add_argument("--no-train", action="store_true")
     ap.add_argument("--no-densify", action="store_true")
+    ap.add_argument("--no-losses", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=10)
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="also run a plain device copy of this many bytes 3 times (the "
@@ -666,7 +678,7 @@ def main():
         t_train = time_steps(train.step, n_train, args.warmup)
         result["train_step"] = {
             "workload": "config4 training step: projection fwd + 128^3 voxelize fwd over "
-                        "[-1,1]^3 + L1/SSIM/edge/TV loss fwd+bwd + explicit backward + Adam "
+                        "[-1,1]^3 + L1/SSIM/edge/TV/hierarchy loss fwd+bwd + explicit backward + Adam "
                         "step of the 4 parameter groups + a 1% split and 1% prune of the model "
                         "table every 100 steps",
             "refines": train.refines, "n_gaussians_after": int(train.model.means.shape[0]),
@@ -696,10 +708,11 @@ def main():
         }
         log(f"voxelization fwd+bwd: {t_vox * 1e3:.3f} ms/call, I3={i3}")
 
-    log("losses (fused vs torch ops)")
-    result["losses"] = time_losses(dev, args.kernel_reps)
-    result["losses"].update(time_adam(proj, args.kernel_reps))
-    log("losses: " + ", ".join(f"{k} {v:.3f}" for k, v in result["losses"].items()))
+    if not args.no_losses:
+        log("losses and Adam (fused vs torch ops)")
+        result["losses"] = time_losses(dev, args.kernel_reps)
+        result["losses"].update(time_adam(proj, args.kernel_reps))
+        log("losses: " + ", ".join(f"{k} {v:.3f}" for k, v in result["losses"].items()))
 
     if not args.no_densify:
         log("config-4 densify / prune table (500k rows + 500k archived, 1% masks)")
