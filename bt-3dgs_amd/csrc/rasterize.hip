@@ -131,12 +131,26 @@ struct FwdRecord {
   typename Vec<T>::v4 p, q;
 };
 
+// Blocks per (view, tile) of the forward: tiles carry different record counts
+// (max/mean 1.4 at config 4) and all of them are resident at once, so one
+// block per tile leaves the heaviest tiles running alone at the end.  With
+// `splits` blocks per tile, each sums an equal share of the tile's records
+// into its own partial tile, and fwd_combine_kernel adds the partials in a
+// fixed order (deterministic).
+inline uint32_t fwd_splits(int64_t n_keys, int64_t n_isects) {
+  if (n_keys <= 0) return 1;
+  const int64_t per_tile = n_isects / n_keys;
+  const int64_t s = per_tile / 1024;
+  return static_cast<uint32_t>(s < 1 ? 1 : (s > 8 ? 8 : s));
+}
+
 template <typename T, int TS>
 __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
     const T *__restrict__ means2d, const T *__restrict__ conics, const T *__restrict__ opac,
     const T *__restrict__ mus, const int32_t *__restrict__ tile_offsets,
     const int32_t *__restrict__ flatten_ids, int64_t n_isects, uint32_t n_keys, int64_t n_items,
-    uint32_t W, uint32_t H, uint32_t tw, uint32_t th, T *__restrict__ image) {
+    uint32_t W, uint32_t H, uint32_t tw, uint32_t th, uint32_t splits, T *__restrict__ image,
+    T *__restrict__ partial) {
   using V2 = typename Vec<T>::v2;
   using V4 = typename Vec<T>::v4;
   constexpr int R = TS * TS / 64;   // pixels per lane
@@ -145,7 +159,9 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
   __shared__ FwdRecord<T> s_rec[kFwdBatch];
   __shared__ T s_part[kFwdWaves][TS * TS];
 
-  const uint32_t key = xcd_swizzle(blockIdx.x, n_keys);
+  // The splits of one tile are consecutive logical blocks (same XCD).
+  const uint32_t lb = xcd_swizzle(blockIdx.x, gridDim.x);
+  const uint32_t key = lb / splits, split = lb - key * splits;
   const uint32_t n_tiles = tw * th;
   const uint32_t cam = key / n_tiles, t = key - cam * n_tiles;
   const uint32_t ty = t / tw, tx = t - ty * tw;
@@ -158,8 +174,10 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
   const T thr = static_cast<T>(kThr2);
   const T l = static_cast<T>(kLog2e), hl = static_cast<T>(0.5 * kLog2e);
 
-  const int64_t start = tile_offsets[key];
-  const int64_t end = (key == n_keys - 1) ? n_isects : static_cast<int64_t>(tile_offsets[key + 1]);
+  const int64_t t0 = tile_offsets[key];
+  const int64_t t1 = (key == n_keys - 1) ? n_isects : static_cast<int64_t>(tile_offsets[key + 1]);
+  const int64_t start = t0 + (t1 - t0) * split / splits;
+  const int64_t end = t0 + (t1 - t0) * (split + 1) / splits;
   T acc[R];
 #pragma unroll
   for (int q = 0; q < R; ++q) acc[q] = 0;
@@ -214,10 +232,31 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
     T sum = s_part[0][pix];
 #pragma unroll
     for (int w = 1; w < kFwdWaves; ++w) sum += s_part[w][pix];
+    if (splits > 1) {
+      partial[(static_cast<int64_t>(key) * splits + split) * (TS * TS) + pix] = sum;
+      continue;
+    }
     const int i = static_cast<int>(ty) * TS + pix / TS, j = static_cast<int>(tx) * TS + pix % TS;
     if (i < static_cast<int>(H) && j < static_cast<int>(W))
       image[static_cast<int64_t>(cam) * H * W + static_cast<int64_t>(i) * W + j] = sum;
   }
+}
+
+// image = sum over the splits of each tile's partial tiles, in split order.
+template <typename T, int TS>
+__global__ __launch_bounds__(TS * TS) void fwd_combine_kernel(const T *__restrict__ partial,
+                                                              uint32_t splits, uint32_t W,
+                                                              uint32_t H, uint32_t tw,
+                                                              uint32_t th, T *__restrict__ image) {
+  const uint32_t key = blockIdx.x, pix = threadIdx.x;
+  const uint32_t n_tiles = tw * th;
+  const uint32_t cam = key / n_tiles, t = key - cam * n_tiles;
+  const uint32_t ty = t / tw, tx = t - ty * tw;
+  const T *p = partial + static_cast<int64_t>(key) * splits * (TS * TS) + pix;
+  T sum = p[0];
+  for (uint32_t s = 1; s < splits; ++s) sum += p[s * (TS * TS)];
+  const uint32_t i = ty * TS + pix / TS, j = tx * TS + pix % TS;
+  if (i < H && j < W) image[static_cast<int64_t>(cam) * H * W + static_cast<int64_t>(i) * W + j] = sum;
 }
 
 // One backward record in registers.
@@ -522,7 +561,7 @@ template <typename T>
 int raster_fwd_impl(const T *means2d, const T *conics, const T *opac, const T *mus,
                     const int32_t *tile_offsets, const int32_t *flatten_ids, int64_t n_isects,
                     int64_t C, int64_t N, uint32_t W, uint32_t H, uint32_t ts, uint32_t tw,
-                    uint32_t th, T *image, r2s_stream_t st) {
+                    uint32_t th, T *image, void *ws, size_t ws_bytes, r2s_stream_t st) {
   clear_error();
   const char *name = "rasterize_to_pixels_fwd";
   R2S_RETURN_IF(check_raster_args(n_isects, C, N, W, H, ts, tw, th, name));
@@ -534,10 +573,28 @@ int raster_fwd_impl(const T *means2d, const T *conics, const T *opac, const T *m
   R2S_REQUIRE(means2d && conics && opac && mus && tile_offsets && flatten_ids,
               "%s: null pointer", name);
   const uint32_t n_keys = static_cast<uint32_t>(C) * tw * th;
+  uint32_t splits = 1;
+  T *partial = nullptr;
+  if (ts == 8 || ts == 16 || ts == 32) {
+    splits = fwd_splits(n_keys, n_isects);
+    if (splits > 1) {
+      const size_t need = static_cast<size_t>(n_keys) * splits * ts * ts * sizeof(T);
+      if (ws == nullptr || ws_bytes < need) {
+        set_error("%s: workspace of %zu bytes, %zu required", name, ws_bytes, need);
+        return R2S_EWORKSPACE;
+      }
+      partial = static_cast<T *>(ws);
+    }
+  }
+  R2S_REQUIRE(static_cast<uint64_t>(n_keys) * splits <= 0x7fffffffull, "%s: too many tiles",
+              name);
 #define R2S_RASTER_FWD_ROWS(TS)                                                                  \
-  raster_fwd_rows_kernel<T, TS><<<dim3(n_keys), dim3(kFwdBatch), 0, stream>>>(                 \
+  raster_fwd_rows_kernel<T, TS><<<dim3(n_keys * splits), dim3(kFwdBatch), 0, stream>>>(        \
       means2d, conics, opac, mus, tile_offsets, flatten_ids, n_isects, n_keys, C * N, W, H, tw,  \
-      th, image)
+      th, splits, image, partial);                                                               \
+  if (splits > 1)                                                                                \
+  fwd_combine_kernel<T, TS><<<dim3(n_keys), dim3(TS * TS), 0, stream>>>(partial, splits, W, H,   \
+                                                                        tw, th, image)
   if (ts == 16) {
     R2S_RASTER_FWD_ROWS(16);
   } else if (ts == 8) {
@@ -684,11 +741,10 @@ int64_t r2s_rasterize_bwd_workspace_bytes(int64_t n_isects, int dtype_bytes) {
 
 int64_t r2s_rasterize_workspace_bytes(int64_t n_keys, int64_t n_isects, uint32_t tile_size,
                                       int dtype_bytes) {
-  (void)n_keys;
-  (void)n_isects;
-  (void)tile_size;
-  (void)dtype_bytes;
-  return 0;
+  if (n_keys <= 0 || (tile_size != 8 && tile_size != 16 && tile_size != 32)) return 0;
+  const uint32_t splits = r2s::fwd_splits(n_keys, n_isects);
+  if (splits <= 1) return 0;
+  return n_keys * splits * static_cast<int64_t>(tile_size) * tile_size * dtype_bytes;
 }
 
 #define R2S_RASTER_API(SUF, T)                                                                \
@@ -697,10 +753,8 @@ int64_t r2s_rasterize_workspace_bytes(int64_t n_keys, int64_t n_isects, uint32_t
                               int64_t n_isects, int64_t C, int64_t N, uint32_t W, uint32_t H, \
                               uint32_t ts, uint32_t tw, uint32_t th, T *image, void *ws,      \
                               size_t ws_bytes, r2s_stream_t st) {                             \
-    (void)ws;                                                                                 \
-    (void)ws_bytes;                                                                           \
     return r2s::raster_fwd_impl<T>(means2d, conics, opac, mus, tile_offsets, flatten_ids,     \
-                                   n_isects, C, N, W, H, ts, tw, th, image, st);              \
+                                   n_isects, C, N, W, H, ts, tw, th, image, ws, ws_bytes, st);\
   }                                                                                           \
   int r2s_rasterize_bwd_##SUF(const T *means2d, const T *conics, const T *opac, const T *mus, \
                               const int32_t *tile_offsets, const int64_t *isect_ids,          \

@@ -542,10 +542,14 @@ def rasterize_to_pixels_fwd(means2d: Tensor, conics: Tensor, opacities: Tensor, 
     if C == 0 or N == 0 or n_isects == 0:
         return out.zero_()
     sfx = _suffix(means2d, "rasterize_to_pixels_fwd")
+    lib = _lib()
     with torch.cuda.device(dev):
+        nbytes = lib.r2s_rasterize_workspace_bytes(C * tw * th, n_isects, ts,
+                                                   means2d.element_size())
+        ws = _workspace(nbytes, dev) if nbytes > 0 else None
         _call(f"r2s_rasterize_fwd_{sfx}", _ptr(means2d), _ptr(conics), _ptr(opacities),
               _ptr(mus), _ptr(tile_offsets), _ptr(flatten_ids), n_isects, C, N, W, H, ts, tw, th,
-              _ptr(out), None, 0, _stream(dev))
+              _ptr(out), _ptr(ws), 0 if ws is None else ws.numel(), _stream(dev))
     return out
 
 

@@ -272,7 +272,9 @@ int r2s_isect_offset_encode(const int64_t *isect_ids, int64_t n_isects,
 /* Line-integral rasterizer                                               */
 /* ---------------------------------------------------------------------- */
 
-/* Workspace for r2s_rasterize_fwd_* / r2s_rasterize_bwd_*. */
+/* Workspace for r2s_rasterize_fwd_*: the partial tiles when heavy tiles are
+ * split across several blocks (tile sizes 8, 16, 32 with 2048 or more
+ * records per tile on average); 0 otherwise. */
 int64_t r2s_rasterize_workspace_bytes(int64_t n_keys, int64_t n_isects,
                                       uint32_t tile_size, int dtype_bytes);
 

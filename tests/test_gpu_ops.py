@@ -249,6 +249,31 @@ def test_rasterize_fwd_bwd(dtype, shape, order):
     assert no_abs[0] is None
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("shape", [(32, 32, 16), (48, 40, 8)])
+def test_rasterize_fwd_splits_heavy_tiles(dtype, shape):
+    """Many large Gaussians on a small detector: thousands of records per tile,
+    so each tile is summed by several blocks and their partials combined."""
+    from r2splat.cuda import _backend
+
+    W_img, H_img, ts = shape
+    d, m2, con, mu, op, ids, fl, off = _raster_case(6000, 11, W_img, H_img, ts, 2, dtype,
+                                                    log_mu=-2.0)
+    n_keys = off.numel()
+    lib = _backend.library()
+    assert lib.r2s_rasterize_workspace_bytes(n_keys, fl.numel(), ts, 4) > 0  # split path
+    img = W.rasterize_to_pixels_fwd(m2, con, op, mu, off, fl, W_img, H_img, ts)
+    img_o = native.raster_fwd(np32(m2), np32(con), np32(op), np32(mu), np32(off), np32(fl),
+                              W_img, H_img, ts)
+    f32 = dtype == torch.float32
+    scale = float(np.abs(img_o).max())
+    tol = dict(rtol=1e-4, atol=1e-6 * scale) if f32 else dict(rtol=1e-9, atol=1e-12 * scale)
+    assert_close(np32(img), img_o, "image", max_outliers=img_o.size // 1000 if f32 else 0,
+                 outlier_atol=3e-5 if f32 else None, **tol)
+    again = W.rasterize_to_pixels_fwd(m2, con, op, mu, off, fl, W_img, H_img, ts)
+    assert torch.equal(img, again)
+
+
 def test_rasterize_empty():
     m2 = torch.zeros(1, 3, 2, device=DEV)
     z3 = torch.zeros(1, 3, 3, device=DEV)
