@@ -5,7 +5,7 @@
 // Gaussian's gradient with device-scope float atomics runs at about 21 G
 // atomics/s on MI355X (measured for scattered fp32 adds), which dominates the
 // backward passes.  Instead a kernel stores each record's partials as one
-// 16-value row of a workspace at the record's emission index; in emission
+// 12-value row of a workspace at the record's emission index; in emission
 // order the records of one Gaussian are consecutive, so a streaming pass sums
 // each Gaussian's rows with a segmented wave reduction and writes the sums
 // once with plain stores.  The result does not depend on scheduling.
@@ -15,7 +15,9 @@
 
 namespace r2s {
 
-constexpr int kRowStride = 16;  // values per row: 64 bytes (float) / 128 (double)
+// Values per row: 48 bytes (float) / 96 (double), three 16-byte vectors; the
+// rasterizer stores 9 partials, the voxelizer 10.
+constexpr int kRowStride = 12;
 
 template <typename T>
 struct Quad;
@@ -30,7 +32,7 @@ struct Quad<double> {
   static constexpr int n = 2;
 };
 
-// Rows start at multiples of 64 (float) / 128 (double) bytes from a
+// Rows start at multiples of 48 (float) / 96 (double) bytes from a
 // 16-byte-aligned workspace, so they are written and read as 16-byte vectors.
 template <typename T, int NV>
 __device__ __forceinline__ void store_row(T *__restrict__ rows, int64_t e, const T (&v)[NV]) {
