@@ -69,6 +69,14 @@ def _workspace(nbytes: int, device: torch.device) -> Tensor:
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
 
+def _check_record_count(n_isects: int, op: str) -> None:
+    # The tile offsets are int32, as in the reference (IsectTiles.cpp:191); the
+    # sort would otherwise need tens of GB before the library rejects the size.
+    if n_isects > 2 ** 31 - 1:
+        raise RuntimeError(f"{op}: {n_isects} tile records exceed the int32 offset range "
+                           f"(2**31 - 1)")
+
+
 def _end_bit(n_keys: int) -> int:
     # IsectTiles.cpp:146-147
     return int(math.ceil(math.log2(float(n_keys + 1))))
@@ -415,6 +423,7 @@ def isect_tiles(means2d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim1: in
         n_isects = int(offsets[-1].item())  # the one host read-back (IsectTiles.cpp:100)
         if n_isects == 0:
             return (tiles_per_gauss,) + empty_ids
+        _check_record_count(n_isects, "isect_tiles")
         end_bit = _end_bit(C * tw * th)
         isect_ids = torch.empty((n_isects,), dtype=torch.int64, device=dev)
         flatten_ids = torch.empty((n_isects,), dtype=torch.int32, device=dev)
@@ -474,6 +483,7 @@ def isect_tiles_3d(means3d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim2:
         n_isects = int(offsets[-1].item())  # IsectTiles3D.cpp:96
         if n_isects == 0:
             return (tiles_per_gauss,) + empty_ids
+        _check_record_count(n_isects, "isect_tiles_3d")
         end_bit = _end_bit(n2 * n1 * n0)
         isect_ids = torch.empty((n_isects,), dtype=torch.int64, device=dev)
         flatten_ids = torch.empty((n_isects,), dtype=torch.int32, device=dev)
