@@ -14,7 +14,7 @@ timings, the roofline of the dominant kernel and the CPU oracle baseline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
                        [--no-voxel] [--no-train] [--no-densify] [--no-losses]
-                       [--kernel-reps R] [--copy-bytes B]
+                       [--no-stress] [--kernel-reps R] [--copy-bytes B]
 """
 
 from __future__ import annotations
@@ -56,11 +56,14 @@ def _events():
 class Projection:
     """Config-4 projection workload resident on the device."""
 
-    def __init__(self, dev, n=N_PROJ, det=DET, seed=0):
+    def __init__(self, dev, n=N_PROJ, det=DET, seed=0, stress=False):
         from r2splat import geometry, scenes
 
         g = torch.Generator().manual_seed(seed)
-        raw = scenes.binary_tree_gaussians(n, g, opacity="uniform")
+        if stress:  # config 5: log-scales N(-5, 1), 5 % needles
+            raw = scenes.stress_gaussians(n, g)
+        else:
+            raw = scenes.binary_tree_gaussians(n, g, opacity="uniform")
         self.raw = raw
         self.params = [torch.nn.Parameter(t.clone().to(dev)) for t in
                        (raw.means, raw.quats, raw.raw_scales, raw.raw_opacities)]
@@ -210,12 +213,15 @@ class TrainStep:
 class Voxelization:
     """Config-3 voxelization workload: the voxel branch at the op boundary."""
 
-    def __init__(self, dev, n=N_VOX, dim=VOX_DIM, seed=1):
+    def __init__(self, dev, n=N_VOX, dim=VOX_DIM, seed=1, needle_fraction=None):
         from r2splat import scenes
         from r2splat.cuda import _wrapper as W
 
         g = torch.Generator().manual_seed(seed)
-        raw = scenes.random_gaussians(n, g, -4.5, 0.6)
+        if needle_fraction is None:
+            raw = scenes.random_gaussians(n, g, -4.5, 0.6)
+        else:  # config 5 scales with a given share of needles
+            raw = scenes.stress_gaussians(n, g, needle_fraction=needle_fraction)
         means = raw.means.to(dev)
         covars, max_scales, opac = W.prepare_gaussians(raw.quats.to(dev), raw.raw_scales.to(dev),
                                                        raw.raw_opacities.to(dev), SMIN, SMAX)
@@ -580,6 +586,7 @@ def main():
     ap.add_argument("--no-train", action="store_true")
     ap.add_argument("--no-densify", action="store_true")
     ap.add_argument("--no-losses", action="store_true")
+    ap.add_argument("--no-stress", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=10)
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="also run a plain device copy of this many bytes 3 times (the "
@@ -730,6 +737,35 @@ def main():
         result["densify"] = dens
         log("densify: " + ", ".join(f"{op} {dens[op]['ms_per_call']:.3f} ms"
                                     for op in ("split", "duplicate", "remove")))
+
+    if not args.no_stress:
+        log("config-5 stress shapes (2M Gaussians: 1024^2 projection, 512^3 voxelization)")
+        sp = Projection(dev, n=2_000_000, det=1024, seed=5, stress=True)
+        t_sp = time_steps(sp.step, 3, 1)
+        with torch.no_grad():
+            from r2splat.cuda import _wrapper as W2
+
+            cov, _, op = W2.prepare_gaussians(sp.params[1].detach(), sp.params[2].detach(),
+                                              sp.params[3].detach(), SMIN, SMAX)
+            m2, _, rad, _, _, _ = W2.project_gaussians_fwd(sp.params[0].detach(), cov, op,
+                                                          sp.viewmats[:1], sp.Ks[:1], 1024, 1024,
+                                                          EPS, 3.0)
+            i2_stress = int(W2.isect_tiles(m2, rad, 16, 64, 64)[1].numel())
+        sv = Voxelization(dev, n=2_000_000, dim=512, seed=5, needle_fraction=0.0005)
+        t_sv = time_steps(sv.step, 3, 1)
+        result["stress"] = {
+            "projection": {"workload": "config5 projection fwd+bwd: 2M Gaussians (log-scale "
+                                       "N(-5,1), 5% needles), 1024^2, one view",
+                           "n_isects_view0": i2_stress, "ms_per_call": t_sp * 1e3},
+            "voxelization": {"workload": "config5 voxelization fwd+bwd at 512^3 with 0.05% "
+                                         "needles (5% needles need 7.46e9 brick records, beyond "
+                                         "the int32 offsets)",
+                             "n_isects": int(sv.last[4].numel()), "ms_per_call": t_sv * 1e3,
+                             "mvox_per_s": 512 ** 3 / t_sv / 1e6}}
+        log(f"stress: projection {t_sp * 1e3:.2f} ms, voxelization {t_sv * 1e3:.2f} ms "
+            f"({int(sv.last[4].numel())} records)")
+        del sp, sv
+        torch.cuda.empty_cache()
 
     if not args.no_cpu_baseline:
         log("timing the CPU oracle baseline")
