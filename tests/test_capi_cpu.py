@@ -96,3 +96,29 @@ def test_densify_arguments_are_checked_without_a_device(lib):
     # Nothing to write is a successful no-op.
     assert lib.r2s_densify_remove(None, 0, None, 0, None) == 0
     assert lib.r2s_densify_split(None, 0, None, 0, 0, None, None, 0, None) == 0
+
+
+def test_loss_and_optimizer_arguments_are_checked_without_a_device(lib):
+    out = ctypes.c_void_p(256)  # never dereferenced: the checks fail first
+    # Even windows are rejected (metric.py's padding would change the map size).
+    assert lib.r2s_projection_loss_fwd_f32(out, out, None, None, 1, 8, 8, 10, out, None, 0,
+                                           None) == 1001
+    assert b"window_size must be odd" in lib.r2s_last_error()
+    assert lib.r2s_projection_loss_fwd_f32(out, out, out, None, 1, 8, 8, 11, out, None, 0,
+                                           None) == 1001
+    assert b"go together" in lib.r2s_last_error()
+    assert lib.r2s_projection_loss_fwd_f32(out, out, None, None, 1, 8, 8, 11, out, None, 0,
+                                           None) == 1004
+    assert lib.r2s_projection_loss_workspace_bytes(2, 64, 64) >= 3 * 2 * 64 * 64 * 4
+    assert lib.r2s_tv_fwd_f32(None, 4, 4, 4, 1, out, None, 0, None) == 1001
+    assert lib.r2s_tv_workspace_bytes() > 0
+    assert lib.r2s_hierarchy_loss_fwd_f32(None, None, 5, None, None, None, 0, 1.0, out, None, 0,
+                                          None) == 1001
+    assert b"null child arrays" in lib.r2s_last_error()
+    A = _lib.AdamTensor
+    table = (A * 1)()
+    table[0] = A(None, None, None, None, 10, 0.1, 0.999, 0.001, 0.0, 1.0, 1e-8, -1e-3)
+    assert lib.r2s_adam_step_f32(ctypes.cast(table, ctypes.c_void_p), 1, None) == 1001
+    assert b"null pointer" in lib.r2s_last_error()
+    table[0] = A(None, None, None, None, 0, 0.1, 0.999, 0.001, 0.0, 1.0, 1e-8, -1e-3)
+    assert lib.r2s_adam_step_f32(ctypes.cast(table, ctypes.c_void_p), 1, None) == 0
