@@ -497,6 +497,90 @@ def kernel_breakdown(proj: Projection, reps):
     return out
 
 
+def op_table(proj: Projection, vox, reps):
+    """Every reference operator (r2splat/cuda/_wrapper.py:18-39) and the fused
+    passes, timed at the config-4 (2D) and config-3 (3D) inputs with HIP
+    events, with algorithmic bytes (inputs read once, outputs written once;
+    per tile record: 12 B list + 28 B payload (2D) / 40 B (3D) + partials) and
+    the resulting fraction of HBM peak.  The raster / voxel ops are
+    VALU-bound, so their HBM fraction is low by construction."""
+    from r2splat.cuda import _wrapper as W
+
+    means, quats, scales, opac = (t.detach() for t in proj.params)
+    vm, Ks, det = proj.viewmats[:1], proj.Ks[:1], proj.det
+    N = means.shape[0]
+    cov, ms, op = W.prepare_gaussians(quats, scales, opac, SMIN, SMAX)
+    m2, c2, r2 = W.world_to_image_projection_fwd(means, cov, vm, Ks, det, det, EPS, 3.0)
+    con, mu = W.conics_mu_fwd(c2, EPS)
+    opc = op[None].contiguous()
+    nt = -(-det // 16)
+    _, ids, fl = W.isect_tiles(m2, r2, 16, nt, nt)
+    off = W.isect_offset_encode(ids, 1, nt, nt)
+    i2, P = int(fl.numel()), det * det
+    v_img = proj.v_images[0]
+    g = torch.Generator().manual_seed(7)
+    rnd = lambda t: torch.randn(t.shape, generator=g).to(t.device)  # noqa: E731
+    v_m2, v_c2, v_cov, v_con, v_mu = rnd(m2), rnd(c2), rnd(cov), rnd(con), rnd(mu)
+    ops = {
+        "parameter_transform_fwd": (lambda: W.parameter_transform_fwd(quats, scales, SMIN, SMAX),
+                                    56 * N),
+        "parameter_transform_bwd": (lambda: W.parameter_transform_bwd(quats, scales, SMIN, SMAX,
+                                                                      v_cov), 80 * N),
+        "prepare_gaussians": (lambda: W.prepare_gaussians(quats, scales, opac, SMIN, SMAX),
+                              64 * N),
+        "world_to_image_projection_fwd": (lambda: W.world_to_image_projection_fwd(
+            means, cov, vm, Ks, det, det, EPS, 3.0), 76 * N),
+        "world_to_image_projection_bwd": (lambda: W.world_to_image_projection_bwd(
+            means, cov, vm, Ks, det, det, v_m2, v_c2), 104 * N),
+        "conics_mu_fwd": (lambda: W.conics_mu_fwd(c2, EPS), 40 * N),
+        "conics_mu_bwd": (lambda: W.conics_mu_bwd(c2, EPS, con, mu, v_con, v_mu), 80 * N),
+        "project_gaussians_fwd": (lambda: W.project_gaussians_fwd(means, cov, op, vm, Ks, det,
+                                                                  det, EPS, 3.0), 100 * N),
+        "isect_tiles": (lambda: W.isect_tiles(m2, r2, 16, nt, nt), 16 * N + 12 * i2),
+        "isect_offset_encode": (lambda: W.isect_offset_encode(ids, 1, nt, nt), 4 * nt * nt),
+        "rasterize_to_pixels_fwd": (lambda: W.rasterize_to_pixels_fwd(
+            m2, con, opc, mu, off, fl, det, det, 16), 32 * i2 + 4 * P),
+        "rasterize_to_pixels_bwd_per_gaussian": (lambda: W.rasterize_to_pixels_bwd_per_gaussian(
+            m2, con, opc, mu, off, ids, fl, v_img, det, det, 16, True), 76 * i2 + 4 * P + 36 * N),
+        "rasterize_to_pixels_bwd (pixel mode)": (lambda: W.rasterize_to_pixels_bwd(
+            m2, con, opc, mu, off, fl, v_img, det, det, 16, True), 76 * i2 + 4 * P + 36 * N),
+    }
+    if vox is not None:
+        d = vox.dim
+        nb3 = -(-d // 8)
+        m3, con3, off3, ids3, fl3, _ = vox.last
+        i3, V, N3 = int(fl3.numel()), d ** 3, vox.means.shape[0]
+        r3 = W.world_to_volume_mapping_fwd(vox.means, vox.covars, vox.max_scales, vox.ranges,
+                                           vox.centers, d, d, d, EPS, 3.0)[2]
+        v_m3, v_c3 = rnd(m3), rnd(con3)
+        ops.update({
+            "world_to_volume_mapping_fwd": (lambda: W.world_to_volume_mapping_fwd(
+                vox.means, vox.covars, vox.max_scales, vox.ranges, vox.centers, d, d, d, EPS, 3.0),
+                84 * N3),
+            "world_to_volume_mapping_bwd": (lambda: W.world_to_volume_mapping_bwd(
+                vox.means, vox.covars, vox.ranges, vox.centers, d, d, d, EPS, v_m3, v_c3),
+                108 * N3),
+            "isect_tiles_3d": (lambda: W.isect_tiles_3d(m3, r3, 8, nb3, nb3, nb3),
+                               24 * N3 + 12 * i3),
+            "isect_offset_encode_3d": (lambda: W.isect_offset_encode_3d(ids3, nb3, nb3, nb3),
+                                       4 * nb3 ** 3),
+            "voxelize_to_voxels_fwd": (lambda: W.voxelize_to_voxels_fwd(
+                m3, con3, vox.opac, off3, fl3, d, d, d, 8), 52 * i3 + 4 * V),
+            "voxelize_to_voxels_bwd_per_gaussian": (lambda: W.voxelize_to_voxels_bwd_per_gaussian(
+                m3, con3, vox.opac, off3, ids3, fl3, vox.v_volume, d, d, d, 8),
+                92 * i3 + 4 * V + 40 * N3),
+            "voxelize_to_voxels_bwd (pixel mode)": (lambda: W.voxelize_to_voxels_bwd(
+                m3, con3, vox.opac, off3, fl3, vox.v_volume, d, d, d, 8),
+                92 * i3 + 4 * V + 40 * N3),
+        })
+    table = {}
+    for name, (fn, nbytes) in ops.items():
+        sec = time_kernel(fn, reps)
+        table[name] = {"ms": sec * 1e3, "algorithmic_bytes": int(nbytes),
+                       "hbm_frac": nbytes / sec / (HBM_PEAK_GBS * 1e9)}
+    return table
+
+
 def measured_traffic(kernel: str):
     """HBM bytes per launch of ``kernel`` from the committed rocprofv3 --pmc
     summary (profiles/pmc_<kernel>.txt, line ``hbm_bytes_per_launch: N``), or
@@ -714,6 +798,9 @@ def main():
             "voxelize_fwd_hbm_frac": (40 * i3 + 4 * n_vox) / t_vf / (HBM_PEAK_GBS * 1e9),
         }
         log(f"voxelization fwd+bwd: {t_vox * 1e3:.3f} ms/call, I3={i3}")
+
+    log("per-operator table (config 4 / config 3 inputs)")
+    result["ops"] = op_table(proj, None if args.no_voxel else vox, args.kernel_reps)
 
     if not args.no_losses:
         log("losses and Adam (fused vs torch ops)")
