@@ -9,11 +9,14 @@
 //           tiles costs ceil(tiles/64) coalesced store rounds instead of a
 //           serial per-thread loop.  Emission order is the reference's
 //           (record id, then rows / z-y-x), keys are 32-bit.
-//   sort    stable LSD radix sort on bits [0, end_bit), 8-bit digits.  Per
-//           pass: LDS digit histogram per 4096-item tile, device scan of the
-//           digit-major histogram table, stable scatter with per-wave ranks
-//           from ballot-based digit matching (no per-item atomics).  The last
-//           pass widens keys to int64 on the way out.
+//   sort    stable LSD radix sort on the bits that hold every key below
+//           n_keys, in the fewest passes of at most 11-bit digits (one pass
+//           for up to 2048 tiles).  Per pass: LDS digit histogram per
+//           4096-item tile, device scan of the digit-major histogram table,
+//           stable scatter with per-wave ranks from ballot-based digit
+//           matching (no per-item atomics).  The first pass takes the
+//           emission index from the item's position; the last widens keys
+//           to int64 on the way out.
 //   offsets lower_bound of every key in the sorted list (binary search).
 //
 // Because emission is in ascending record id and every pass is stable, the
@@ -141,20 +144,12 @@ __device__ __forceinline__ uint32_t owner_lane(uint32_t excl, uint32_t t) {
   return lo;
 }
 
-// Writes one record: key, payload(s) and, for the emission-order arrays,
-// the flat id.
-__device__ __forceinline__ void put_record(uint32_t *__restrict__ keys, uint32_t *__restrict__ vals,
-                                           uint32_t *__restrict__ vals2,
-                                           int32_t *__restrict__ emit_ids, int64_t e,
-                                           uint32_t key, uint32_t gid) {
+// Writes emitted record e: its key and its flat id (the emission-order id
+// array the two-pass backward reads, or the sort's own copy).
+__device__ __forceinline__ void put_record(uint32_t *__restrict__ keys, uint32_t *__restrict__ gids,
+                                           int64_t e, uint32_t key, uint32_t gid) {
   keys[e] = key;
-  if (emit_ids != nullptr) {
-    vals[e] = static_cast<uint32_t>(e);
-    vals2[e] = gid;
-    emit_ids[e] = static_cast<int32_t>(gid);
-  } else {
-    vals[e] = gid;
-  }
+  gids[e] = gid;
 }
 
 // A wave's 64 consecutive items emit one contiguous range of records
@@ -165,8 +160,7 @@ template <typename T>
 __global__ __launch_bounds__(256) void emit_2d_kernel(
     const T *__restrict__ means2d, const int32_t *__restrict__ radii, int rect, int64_t M,
     int64_t N, uint32_t ts, uint32_t tw, uint32_t th, const int64_t *__restrict__ offsets,
-    uint32_t *__restrict__ keys, uint32_t *__restrict__ vals, uint32_t *__restrict__ vals2,
-    int32_t *__restrict__ emit_ids) {
+    uint32_t *__restrict__ keys, uint32_t *__restrict__ gids) {
   const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + 64 * wave_index();
   if (wave_first >= M) return;  // uniform per wave
   const int64_t idx = wave_first + lane_id();
@@ -193,7 +187,7 @@ __global__ __launch_bounds__(256) void emit_2d_kernel(
     const int64_t gid = wave_first + j;
     const uint32_t key = static_cast<uint32_t>(gid / N) * n_tiles + (y0 + row) * tw + (x0 + col);
     if (t0 + lane_id() < total)
-      put_record(keys, vals, vals2, emit_ids, base + t, key, static_cast<uint32_t>(gid));
+      put_record(keys, gids, base + t, key, static_cast<uint32_t>(gid));
   }
 }
 
@@ -201,8 +195,7 @@ template <typename T>
 __global__ __launch_bounds__(256) void emit_3d_kernel(
     const T *__restrict__ means3d, const int32_t *__restrict__ radii, int64_t N, uint32_t ts,
     uint32_t n2, uint32_t n1, uint32_t n0, const int64_t *__restrict__ offsets,
-    uint32_t *__restrict__ keys, uint32_t *__restrict__ vals, uint32_t *__restrict__ vals2,
-    int32_t *__restrict__ emit_ids) {
+    uint32_t *__restrict__ keys, uint32_t *__restrict__ gids) {
   const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + 64 * wave_index();
   if (wave_first >= N) return;  // uniform per wave
   const int64_t idx = wave_first + lane_id();
@@ -237,7 +230,7 @@ __global__ __launch_bounds__(256) void emit_3d_kernel(
     const uint32_t ty = rem / e2j, tx = rem - ty * e2j;
     const uint32_t key = (l0 + tz) * (n1 * n2) + (l1 + ty) * n2 + (l2 + tx);
     if (t0 + lane_id() < total)
-      put_record(keys, vals, vals2, emit_ids, base + t, key, static_cast<uint32_t>(wave_first + j));
+      put_record(keys, gids, base + t, key, static_cast<uint32_t>(wave_first + j));
   }
 }
 
@@ -247,63 +240,74 @@ constexpr int kSortThreads = 256;                       // 4 waves
 constexpr int kSortRounds = 16;                         // 64-item rounds per wave
 constexpr int kSortWaveItems = 64 * kSortRounds;        // 1024
 constexpr int kSortTile = 4 * kSortWaveItems;           // 4096 items per block
-constexpr int kRadixBits = 8;
-constexpr int kRadix = 1 << kRadixBits;
+constexpr int kMaxPassBits = 11;                        // up to 2048 digits per pass
+constexpr int kMaxDigits = 1 << kMaxPassBits;
+constexpr int kDigitsPerThread = kMaxDigits / kSortThreads;  // 8
 
+// Digit histogram of one 4096-item tile, written digit-major:
+// hist[d * nblocks + tile].  Tiles are XCD-contiguous (xcd_swizzle), so the
+// blocks writing neighbouring words of a digit's row share an L2.
 __global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(const uint32_t *__restrict__ keys,
                                                                   int64_t n, uint32_t shift,
-                                                                  uint32_t mask,
+                                                                  uint32_t digits,
                                                                   uint32_t *__restrict__ hist,
                                                                   uint32_t nblocks) {
-  __shared__ uint32_t h[kRadix];
-  h[threadIdx.x] = 0;
+  __shared__ uint32_t h[kMaxDigits];
+  const uint32_t tile = xcd_swizzle(blockIdx.x, nblocks);
+  for (uint32_t d = threadIdx.x; d < digits; d += kSortThreads) h[d] = 0;
   __syncthreads();
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kSortTile;
+  const uint32_t mask = digits - 1u;
+  const int64_t base = static_cast<int64_t>(tile) * kSortTile;
   for (int i = threadIdx.x; i < kSortTile; i += kSortThreads) {
     const int64_t k = base + i;
     if (k < n) atomicAdd(&h[(keys[k] >> shift) & mask], 1u);
   }
   __syncthreads();
-  hist[static_cast<int64_t>(threadIdx.x) * nblocks + blockIdx.x] = h[threadIdx.x];
+  for (uint32_t d = threadIdx.x; d < digits; d += kSortThreads)
+    hist[static_cast<int64_t>(d) * nblocks + tile] = h[d];
 }
 
 // One block sorts its kSortTile items by digit in LDS (stable: waves in
 // order, rounds in order, lanes by ballot rank), then writes them out in
 // block-local digit order, so each digit's items leave as one contiguous run
-// of the destination (coalesced writes).  kTwo: a second payload (the flat
-// id while the first is the emission index) travels with the key; the final
-// pass then writes vals_out32 = second payload and src_out = first.
-template <bool kFinal, bool kTwo>
+// of the destination.  Each item carries its key, its flat id (gid) and,
+// with kTwo, its emission index e.  kFirst: the input is the emission-order
+// array itself, so e is the input index and only keys and gids are read.
+// kFinal: writes keys_out64 / vals_out32 = gid / src_out = e.
+template <bool kFirst, bool kFinal, bool kTwo>
 __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
-    const uint32_t *__restrict__ keys_in, const uint32_t *__restrict__ vals_in,
-    const uint32_t *__restrict__ vals2_in, int64_t n, uint32_t shift, uint32_t bits,
+    const uint32_t *__restrict__ keys_in, const uint32_t *__restrict__ e_in,
+    const uint32_t *__restrict__ gid_in, int64_t n, uint32_t shift, uint32_t bits,
     const uint32_t *__restrict__ digit_offsets, uint32_t nblocks, uint32_t *__restrict__ keys_out,
-    uint32_t *__restrict__ vals_out, uint32_t *__restrict__ vals2_out,
+    uint32_t *__restrict__ e_out, uint32_t *__restrict__ gid_out,
     int64_t *__restrict__ keys_out64, int32_t *__restrict__ vals_out32,
     int32_t *__restrict__ src_out) {
-  __shared__ uint32_t cnt[4][kRadix];
-  __shared__ uint32_t wbase[4][kRadix];
-  __shared__ uint32_t dbase[kRadix];   // block-local start of each digit
-  __shared__ uint32_t gbase[kRadix];   // global start of this block's run of each digit
-  __shared__ uint32_t wsum[4];
+  // Per-wave digit counters, then (in place) each wave's start within the
+  // digit's block-local run; at most 1024 items per wave, so 16 bits hold them.
+  __shared__ uint16_t cnt[4][kMaxDigits];
+  __shared__ uint16_t dbase[kMaxDigits];  // block-local start of each digit (<= 4096)
+  __shared__ uint32_t gbase[kMaxDigits];  // global start of this block's run of each digit
+  __shared__ uint32_t wsum[kSortThreads / 64];
   __shared__ uint32_t s_key[kSortTile];
-  __shared__ uint32_t s_val[kSortTile];
-  __shared__ uint32_t s_val2[kTwo ? kSortTile : 1];
+  __shared__ uint32_t s_gid[kSortTile];
+  __shared__ uint32_t s_e[kTwo ? kSortTile : 1];
+  const uint32_t digits = 1u << bits, mask = digits - 1u;
+  const uint32_t tile = xcd_swizzle(blockIdx.x, nblocks);
   const uint32_t w = threadIdx.x / 64, lane = threadIdx.x % 64;
-  for (int k = threadIdx.x; k < 4 * kRadix; k += kSortThreads) (&cnt[0][0])[k] = 0;
+  for (uint32_t k = threadIdx.x; k < 4 * digits; k += kSortThreads)
+    cnt[k / digits][k % digits] = 0;
   __syncthreads();
-  const uint32_t mask = (1u << bits) - 1u;
-  const int64_t block_first = static_cast<int64_t>(blockIdx.x) * kSortTile;
+  const int64_t block_first = static_cast<int64_t>(tile) * kSortTile;
   const int64_t first = block_first + w * kSortWaveItems;
   const uint64_t lt = lanemask_lt();
-  uint32_t key[kSortRounds], val[kSortRounds], val2[kSortRounds], rank[kSortRounds];
+  uint32_t key[kSortRounds], gid[kSortRounds], ev[kSortRounds], rank[kSortRounds];
 #pragma unroll
   for (int r = 0; r < kSortRounds; ++r) {
     const int64_t i = first + r * 64 + lane;
     const bool valid = i < n;
     key[r] = valid ? keys_in[i] : 0u;
-    val[r] = valid ? vals_in[i] : 0u;
-    val2[r] = (kTwo && valid) ? vals2_in[i] : 0u;
+    gid[r] = valid ? gid_in[i] : 0u;
+    if (kTwo) ev[r] = kFirst ? static_cast<uint32_t>(i) : (valid ? e_in[i] : 0u);
     const uint32_t d = (key[r] >> shift) & mask;
     // Lanes holding the same digit: intersect the ballots of every digit bit.
     uint64_t peers = ballot(valid);
@@ -317,26 +321,43 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     rank[r] = c + static_cast<uint32_t>(__popcll(peers & lt));
     // The highest lane of each digit group advances that digit's counter.
     if (valid && lane == 63u - static_cast<uint32_t>(__clzll(peers)))
-      cnt[w][d] = c + static_cast<uint32_t>(__popcll(peers));
+      cnt[w][d] = static_cast<uint16_t>(c + static_cast<uint32_t>(__popcll(peers)));
   }
   __syncthreads();
   {
-    // Per digit: wave offsets, block total, then the exclusive scan of the
-    // totals over digits (one digit per thread, 4 waves of 64).
-    const uint32_t d = threadIdx.x;
-    uint32_t tot = 0;
+    // Thread t owns digits [t*k, t*k + k): per digit the waves' starts and
+    // the block total, then an exclusive scan of the totals over digits.
+    const uint32_t k = (digits + kSortThreads - 1) / kSortThreads;
+    const uint32_t d0 = threadIdx.x * k;
+    uint32_t tot[kDigitsPerThread];
+    uint32_t mine = 0;
 #pragma unroll
-    for (int ww = 0; ww < 4; ++ww) {
-      wbase[ww][d] = tot;
-      tot += cnt[ww][d];
+    for (uint32_t j = 0; j < kDigitsPerThread; ++j) {
+      tot[j] = 0;
+      const uint32_t d = d0 + j;
+      if (j < k && d < digits) {
+        uint32_t run = 0;
+#pragma unroll
+        for (int ww = 0; ww < 4; ++ww) {
+          const uint32_t c = cnt[ww][d];
+          cnt[ww][d] = static_cast<uint16_t>(run);
+          run += c;
+        }
+        tot[j] = run;
+        mine += run;
+      }
     }
-    const uint32_t incl = wave_inclusive_scan(tot);
-    if (lane == 63) wsum[w] = incl;
-    __syncthreads();
-    uint32_t before = 0;
-    for (uint32_t ww = 0; ww < w; ++ww) before += wsum[ww];
-    dbase[d] = before + incl - tot;
-    gbase[d] = digit_offsets[static_cast<int64_t>(d) * nblocks + blockIdx.x];
+    uint32_t block_total;
+    uint32_t run = block_exclusive_scan(mine, wsum, block_total);
+#pragma unroll
+    for (uint32_t j = 0; j < kDigitsPerThread; ++j) {
+      const uint32_t d = d0 + j;
+      if (j < k && d < digits) {
+        dbase[d] = static_cast<uint16_t>(run);
+        run += tot[j];
+        gbase[d] = digit_offsets[static_cast<int64_t>(d) * nblocks + tile];
+      }
+    }
   }
   __syncthreads();
 #pragma unroll
@@ -344,30 +365,26 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     const int64_t i = first + r * 64 + lane;
     if (i < n) {
       const uint32_t d = (key[r] >> shift) & mask;
-      const uint32_t lp = dbase[d] + wbase[w][d] + rank[r];
+      const uint32_t lp = dbase[d] + cnt[w][d] + rank[r];
       s_key[lp] = key[r];
-      s_val[lp] = val[r];
-      if (kTwo) s_val2[lp] = val2[r];
+      s_gid[lp] = gid[r];
+      if (kTwo) s_e[lp] = ev[r];
     }
   }
   __syncthreads();
   const int count = static_cast<int>(min(static_cast<int64_t>(kSortTile), n - block_first));
   for (int lp = threadIdx.x; lp < count; lp += kSortThreads) {
-    const uint32_t k = s_key[lp], v = s_val[lp];
+    const uint32_t k = s_key[lp];
     const uint32_t d = (k >> shift) & mask;
     const int64_t dest = static_cast<int64_t>(gbase[d]) + (lp - static_cast<int>(dbase[d]));
     if (kFinal) {
       keys_out64[dest] = static_cast<int64_t>(k);
-      if (kTwo) {
-        vals_out32[dest] = static_cast<int32_t>(s_val2[lp]);
-        src_out[dest] = static_cast<int32_t>(v);
-      } else {
-        vals_out32[dest] = static_cast<int32_t>(v);
-      }
+      vals_out32[dest] = static_cast<int32_t>(s_gid[lp]);
+      if (kTwo) src_out[dest] = static_cast<int32_t>(s_e[lp]);
     } else {
       keys_out[dest] = k;
-      vals_out[dest] = v;
-      if (kTwo) vals2_out[dest] = s_val2[lp];
+      gid_out[dest] = s_gid[lp];
+      if (kTwo) e_out[dest] = s_e[lp];
     }
   }
 }
@@ -392,21 +409,41 @@ __global__ __launch_bounds__(256) void offset_encode_kernel(const int64_t *__res
 
 // ----------------------------------------------------------- workspace ---
 
+// Workspace of the sort.  Emission writes keys to k0 and flat ids to gid0
+// (the caller's emit_ids array, or g0).  Pass p reads one set and writes the
+// other: (k0, gid0) -> (k1, e1, g1) -> (k0, e0, g0) -> ...; the final pass
+// writes the outputs instead.
 struct SortSpace {
-  uint32_t *ka, *va, *wa, *kb, *vb, *wb, *hist, *hist_scan, *partials;
+  uint32_t *k0, *e0, *g0, *k1, *e1, *g1, *hist, *hist_scan, *partials;
+  const uint32_t *gid0;
   int64_t nblocks, n_hist;
 };
 
-SortSpace carve_sort(Carver &cv, int64_t n) {
-  SortSpace s;
+// Passes and digit width for keys of `key_bits` bits: the fewest passes of
+// at most kMaxPassBits bits, split evenly (e.g. 8 + 7 for 15 bits).  Fewer
+// passes move the records fewer times; the scatter keeps each digit's items
+// of a block together, so even 1024 digits leave in short contiguous runs.
+inline uint32_t sort_passes(uint32_t key_bits) {
+  return key_bits == 0 ? 1u : (key_bits + kMaxPassBits - 1) / kMaxPassBits;
+}
+
+// Sized for any key width up to end_bit: the passes never exceed
+// sort_passes(end_bit), and a pass's digits never exceed
+// 2^min(end_bit, kMaxPassBits).
+SortSpace carve_sort(Carver &cv, int64_t n, uint32_t end_bit) {
+  SortSpace s{};
+  const uint32_t passes = sort_passes(end_bit);
+  const uint32_t max_digits = 1u << min(end_bit, static_cast<uint32_t>(kMaxPassBits));
   s.nblocks = ceil_div(n, kSortTile);
-  s.n_hist = s.nblocks * kRadix;
-  s.ka = cv.take<uint32_t>(n);
-  s.va = cv.take<uint32_t>(n);
-  s.wa = cv.take<uint32_t>(n);
-  s.kb = cv.take<uint32_t>(n);
-  s.vb = cv.take<uint32_t>(n);
-  s.wb = cv.take<uint32_t>(n);
+  s.n_hist = s.nblocks * max_digits;
+  s.k0 = cv.take<uint32_t>(n);
+  s.g0 = cv.take<uint32_t>(n);
+  if (passes > 1) {
+    s.k1 = cv.take<uint32_t>(n);
+    s.e1 = cv.take<uint32_t>(n);
+    s.g1 = cv.take<uint32_t>(n);
+    s.e0 = cv.take<uint32_t>(n);
+  }
   s.hist = cv.take<uint32_t>(s.n_hist);
   s.hist_scan = cv.take<uint32_t>(s.n_hist);
   s.partials = cv.take<uint32_t>(scan_partials_count(s.n_hist));
@@ -419,52 +456,65 @@ int64_t count_space_bytes(int64_t n_items) {
   return static_cast<int64_t>(cv.used);
 }
 
-int64_t sort_space_bytes(int64_t n) {
+int64_t sort_space_bytes(int64_t n, uint32_t end_bit) {
   Carver cv(nullptr);
-  carve_sort(cv, n);
+  carve_sort(cv, n, end_bit);
   return static_cast<int64_t>(cv.used);
 }
 
-// Sorts the emitted records held in s.ka / s.va (/ s.wa) into the final
-// outputs; passes ping-pong between the a and b buffers.  two: s.va holds
-// emission indices and s.wa flat ids; the final pass writes vals32 = flat id
-// and src = emission index.  The key bits are split evenly over the passes
-// (e.g. 6 + 5 for 11 bits): fewer digits per pass give longer runs per digit
-// and block, hence better coalesced writes.
-int radix_sort(SortSpace &s, int64_t n, uint32_t end_bit, int64_t *keys64, int32_t *vals32,
+// Number of bits that hold every key below n_keys.
+inline uint32_t key_bits_for(int64_t n_keys) {
+  uint32_t b = 0;
+  while (b < 32 && (1ll << b) < n_keys) ++b;
+  return b;
+}
+
+// Sorts the emitted records (s.k0, s.gid0) into the final outputs.  two:
+// the emission index travels too and the final pass writes it to src.
+int radix_sort(SortSpace &s, int64_t n, uint32_t key_bits, int64_t *keys64, int32_t *vals32,
                bool two, int32_t *src, hipStream_t stream) {
-  const uint32_t passes = (end_bit + kRadixBits - 1) / kRadixBits;
-  const uint32_t pbits = (end_bit + passes - 1) / passes;
-  uint32_t *kin = s.ka, *vin = s.va, *win = s.wa, *kout = s.kb, *vout = s.vb, *wout = s.wb;
+  const uint32_t passes = sort_passes(key_bits);
+  const uint32_t pbits = max(1u, (key_bits + passes - 1) / passes);
   const uint32_t nb = static_cast<uint32_t>(s.nblocks);
+  const uint32_t *kin = s.k0, *ein = nullptr, *gin = s.gid0;
   for (uint32_t p = 0; p < passes; ++p) {
     const uint32_t shift = p * pbits;
-    const uint32_t bits = min(pbits, end_bit - shift);
-    const uint32_t mask = (1u << bits) - 1u;
-    radix_hist_kernel<<<dim3(nb), dim3(kSortThreads), 0, stream>>>(kin, n, shift, mask, s.hist, nb);
-    R2S_RETURN_IF(device_exclusive_scan<uint32_t, uint32_t>(s.hist, s.n_hist, s.hist_scan,
-                                                            nullptr, s.partials, stream,
+    const uint32_t bits = key_bits == 0 ? 1u : min(pbits, key_bits - shift);
+    const uint32_t digits = 1u << bits;
+    const int64_t n_hist = static_cast<int64_t>(nb) * digits;
+    radix_hist_kernel<<<dim3(nb), dim3(kSortThreads), 0, stream>>>(kin, n, shift, digits, s.hist,
+                                                                   nb);
+    R2S_RETURN_IF(device_exclusive_scan<uint32_t, uint32_t>(s.hist, n_hist, s.hist_scan, nullptr,
+                                                            s.partials, stream,
                                                             "isect sort scan"));
-    const bool last = p == passes - 1;
-#define R2S_SCATTER(FINAL, TWO)                                                                 \
-  radix_scatter_kernel<FINAL, TWO><<<dim3(nb), dim3(kSortThreads), 0, stream>>>(               \
-      kin, vin, win, n, shift, bits, s.hist_scan, nb, kout, vout, wout, keys64, vals32, src)
-    if (last) {
-      if (two)
-        R2S_SCATTER(true, true);
-      else
-        R2S_SCATTER(true, false);
-    } else {
-      if (two)
-        R2S_SCATTER(false, true);
-      else
-        R2S_SCATTER(false, false);
-      std::swap(kin, kout);
-      std::swap(vin, vout);
-      std::swap(win, wout);
-    }
+    const bool first = p == 0, last = p == passes - 1;
+    uint32_t *kout = (p % 2 == 0) ? s.k1 : s.k0;
+    uint32_t *eout = (p % 2 == 0) ? s.e1 : s.e0;
+    uint32_t *gout = (p % 2 == 0) ? s.g1 : s.g0;
+#define R2S_SCATTER(FIRST, FINAL, TWO)                                                         \
+  radix_scatter_kernel<FIRST, FINAL, TWO><<<dim3(nb), dim3(kSortThreads), 0, stream>>>(       \
+      kin, ein, gin, n, shift, bits, s.hist_scan, nb, kout, eout, gout, keys64, vals32, src)
+#define R2S_SCATTER_TWO(FIRST, FINAL) \
+  do {                                \
+    if (two)                          \
+      R2S_SCATTER(FIRST, FINAL, true); \
+    else                              \
+      R2S_SCATTER(FIRST, FINAL, false); \
+  } while (0)
+    if (first && last)
+      R2S_SCATTER_TWO(true, true);
+    else if (first)
+      R2S_SCATTER_TWO(true, false);
+    else if (last)
+      R2S_SCATTER_TWO(false, true);
+    else
+      R2S_SCATTER_TWO(false, false);
+#undef R2S_SCATTER_TWO
 #undef R2S_SCATTER
     R2S_RETURN_IF(check_launch("isect sort pass"));
+    kin = kout;
+    ein = eout;
+    gin = gout;
   }
   return R2S_OK;
 }
@@ -542,7 +592,7 @@ int check_sort_args(int64_t n_isects, uint32_t end_bit, int64_t n_keys, void *ws
               end_bit, (long long)n_keys);
   if (n_isects == 0) return R2S_OK;
   R2S_REQUIRE(keys && vals, "%s: null output", name);
-  return check_workspace(ws, ws_bytes, sort_space_bytes(n_isects), name);
+  return check_workspace(ws, ws_bytes, sort_space_bytes(n_isects, end_bit), name);
 }
 
 template <typename T>
@@ -560,14 +610,17 @@ int emit_sort_2d_impl(const T *means2d, const int32_t *radii, int rect, int64_t 
   R2S_REQUIRE(means2d && radii && offsets, "%s: null pointer", name);
   hipStream_t stream = as_stream(st);
   Carver cv(ws);
-  SortSpace s = carve_sort(cv, n_isects);
+  SortSpace s = carve_sort(cv, n_isects, end_bit);
   R2S_REQUIRE((emit_ids == nullptr) == (isect_src == nullptr),
               "%s: emit_ids and isect_src must be given together", name);
+  uint32_t *gids = emit_ids != nullptr ? reinterpret_cast<uint32_t *>(emit_ids) : s.g0;
+  s.gid0 = gids;
   const int64_t M = C * N;
   emit_2d_kernel<T><<<dim3(static_cast<uint32_t>(ceil_div(M, 256))), dim3(256), 0, stream>>>(
-      means2d, radii, rect, M, N, ts, tw, th, offsets, s.ka, s.va, s.wa, emit_ids);
+      means2d, radii, rect, M, N, ts, tw, th, offsets, s.k0, gids);
   R2S_RETURN_IF(check_launch(name));
-  return radix_sort(s, n_isects, end_bit, keys, vals, emit_ids != nullptr, isect_src, stream);
+  return radix_sort(s, n_isects, key_bits_for(C * tw * th), keys, vals, emit_ids != nullptr,
+                    isect_src, stream);
 }
 
 template <typename T>
@@ -586,13 +639,16 @@ int emit_sort_3d_impl(const T *means3d, const int32_t *radii, int64_t N, uint32_
   R2S_REQUIRE(means3d && radii && offsets, "%s: null pointer", name);
   hipStream_t stream = as_stream(st);
   Carver cv(ws);
-  SortSpace s = carve_sort(cv, n_isects);
+  SortSpace s = carve_sort(cv, n_isects, end_bit);
   R2S_REQUIRE((emit_ids == nullptr) == (isect_src == nullptr),
               "%s: emit_ids and isect_src must be given together", name);
+  uint32_t *gids = emit_ids != nullptr ? reinterpret_cast<uint32_t *>(emit_ids) : s.g0;
+  s.gid0 = gids;
   emit_3d_kernel<T><<<dim3(static_cast<uint32_t>(ceil_div(N, 256))), dim3(256), 0, stream>>>(
-      means3d, radii, N, ts, n2, n1, n0, offsets, s.ka, s.va, s.wa, emit_ids);
+      means3d, radii, N, ts, n2, n1, n0, offsets, s.k0, gids);
   R2S_RETURN_IF(check_launch(name));
-  return radix_sort(s, n_isects, end_bit, keys, vals, emit_ids != nullptr, isect_src, stream);
+  return radix_sort(s, n_isects, key_bits_for(static_cast<int64_t>(n2) * n1 * n0), keys, vals,
+                    emit_ids != nullptr, isect_src, stream);
 }
 
 }  // namespace
@@ -601,9 +657,8 @@ int emit_sort_3d_impl(const T *means3d, const int32_t *radii, int64_t N, uint32_
 extern "C" {
 
 int64_t r2s_isect_workspace_bytes(int64_t n_items, int64_t n_isects, uint32_t end_bit) {
-  (void)end_bit;
   const int64_t a = n_items > 0 ? r2s::count_space_bytes(n_items) : 0;
-  const int64_t b = n_isects > 0 ? r2s::sort_space_bytes(n_isects) : 0;
+  const int64_t b = n_isects > 0 ? r2s::sort_space_bytes(n_isects, end_bit) : 0;
   return a > b ? a : b;
 }
 

@@ -61,7 +61,11 @@ def test_workspace_queries(lib):
     assert lib.r2s_isect_workspace_bytes(0, 0, 11) == 0
     small = lib.r2s_isect_workspace_bytes(0, 1000, 11)
     big = lib.r2s_isect_workspace_bytes(0, 10_000_000, 11)
-    assert 16 * 1000 <= small < big and big >= 16 * 10_000_000
+    # Keys up to 11 bits sort in one pass: keys + ids (8 B per record) plus
+    # two 2048-digit tables per 4096 records.
+    assert 8 * 1000 <= small < big and big >= 10 * 10_000_000
+    # Wider keys take two or more passes and ping-pong (key, id, emission index).
+    assert lib.r2s_isect_workspace_bytes(0, 10_000_000, 15) >= 24 * 10_000_000
     assert lib.r2s_isect_workspace_bytes(500_000, 0, 0) > 0
     assert lib.r2s_mask_workspace_bytes(1_000_000) > 0
     buf = ctypes.create_string_buffer(16)

@@ -171,6 +171,42 @@ def test_isect_tiles_3d_bit_exact():
     assert_equal(np32(off), binning.isect_offset_encode_3d(ids_o, n2, n1, n0), "tile_offsets")
 
 
+@pytest.mark.parametrize("tiles,views", [((1, 1), 1), ((32, 32), 2), ((45, 46), 1)])
+def test_isect_tiles_sort_widths(tiles, views):
+    # Key widths 0 bits (one tile), 11 bits (2048 keys, the widest one-pass
+    # sort) and 12 bits (two passes).
+    tw, th = tiles
+    g = torch.Generator().manual_seed(11 + tw)
+    N = 4000
+    m2 = (torch.rand(views, N, 2, generator=g) * torch.tensor([16.0 * tw, 16.0 * th])).float()
+    r = torch.randint(0, 40, (views, N, 2), generator=g).int()
+    tpg, ids, fl = W.isect_tiles(m2.to(DEV), r.to(DEV), 16, tw, th)
+    tpg_o, ids_o, fl_o = binning.isect_tiles(m2.numpy(), r.numpy(), 16, tw, th)
+    assert ids_o.size > 3000
+    assert_equal(np32(tpg), tpg_o, "tiles_per_gauss")
+    assert_equal(np32(ids), ids_o, "isect_ids")
+    assert_equal(np32(fl), fl_o, "flatten_ids")
+    off = W.isect_offset_encode(ids, views, tw, th)
+    assert_equal(np32(off), binning.isect_offset_encode(ids_o, views, tw, th), "tile_offsets")
+
+
+@pytest.mark.parametrize("bricks", [(13, 13, 13), (256, 256, 160)])
+def test_isect_tiles_3d_sort_widths(bricks):
+    # 2197 bricks: two 6-bit passes; 10.5 M bricks (24-bit keys): three passes.
+    n2, n1, n0 = bricks
+    g = torch.Generator().manual_seed(n0)
+    N = 3000
+    ext = torch.tensor([8.0 * n2, 8.0 * n1, 8.0 * n0])
+    m3 = (torch.rand(N, 3, generator=g) * (ext + 40) - 20).float()
+    r3 = torch.randint(0, 20, (N, 3), generator=g).int()
+    tpg, ids, fl = W.isect_tiles_3d(m3.to(DEV), r3.to(DEV), 8, n2, n1, n0)
+    tpg_o, ids_o, fl_o = binning.isect_tiles_3d(m3.numpy(), r3.numpy(), 8, n2, n1, n0)
+    assert ids_o.size > 3000 and ids_o.max() >= n2 * n1 * n0 // 2
+    assert_equal(np32(tpg), tpg_o, "tiles_per_gauss")
+    assert_equal(np32(ids), ids_o, "isect_ids")
+    assert_equal(np32(fl), fl_o, "flatten_ids")
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
 def test_volume_mapping_bit_exact(dtype):
     d = _prepared(4000, 6, dtype, log_mu=-3.0)
