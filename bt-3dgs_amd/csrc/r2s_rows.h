@@ -102,74 +102,145 @@ struct RowTargets {
   int stride[NV];
 };
 
-// One wave per 64 consecutive rows (emission order).  Each Gaussian is
-// written by the wave holding its first row: a Gaussian continuing past the
-// wave's last lane has its remaining rows gathered by this wave (64 ids at a
-// time); a Gaussian that started in an earlier wave is skipped.  Plain
-// stores, no atomics: outputs must be zero on entry, and the per-Gaussian
-// summation order is fixed.
+// Zeroes ids [lo, hi) of every target: each lane its first kOwnZeros ids
+// itself (gaps are mostly short), the rest of long ranges one lane's range
+// after another, all 64 lanes storing consecutive ids.
+constexpr int kOwnZeros = 8;
+
+template <typename T, int NV>
+__device__ __forceinline__ void zero_id_ranges(int64_t lo, int64_t hi, const RowTargets<T, NV> &tg) {
+  const int64_t own = min(hi, lo + kOwnZeros);
+  for (int64_t k = lo; k < own; ++k) {
+#pragma unroll
+    for (int c = 0; c < NV; ++c) tg.ptr[c][k * tg.stride[c]] = static_cast<T>(0);
+  }
+  lo = own > lo ? own : lo;
+  uint64_t pending = ballot(hi > lo);
+  while (pending != 0) {
+    const uint32_t src = static_cast<uint32_t>(__builtin_ctzll(pending));
+    pending &= pending - 1;
+    const int64_t a = readlane_i64(lo, src), b = readlane_i64(hi, src);
+    for (int64_t k = a + lane_id(); k < b; k += 64) {
+#pragma unroll
+      for (int c = 0; c < NV; ++c) tg.ptr[c][k * tg.stride[c]] = static_cast<T>(0);
+    }
+  }
+}
+
+// Rounds of 64 rows per wave: the rows of all rounds are loaded up front,
+// and a Gaussian crossing from one round into the next carries its sum in
+// registers; only one crossing the wave's last row gathers rows of the next
+// wave.
+constexpr int kReduceRounds = 4;
+constexpr int kReduceWaveRows = 64 * kReduceRounds;
+
+// One wave per kReduceWaveRows consecutive rows (emission order).  Each
+// Gaussian is written by the wave holding its first row: a Gaussian
+// continuing past the wave's last row has its remaining rows gathered by
+// this wave (64 ids at a time); a Gaussian that started in an earlier wave
+// is skipped.  Plain stores, no atomics, and the per-Gaussian summation
+// order is fixed.  Emission order is ascending in the id, so the ids
+// strictly between two consecutive records' ids have no records: the first
+// row of each Gaussian zeroes the ids between it and the previous record,
+// and the wave holding the last record zeroes the ids after it.  Every
+// output is written; none needs zeroing beforehand.
 template <typename T, int NV>
 __global__ __launch_bounds__(256) void row_reduce_kernel(const T *__restrict__ rows,
                                                          const int32_t *__restrict__ emit_ids,
                                                          int64_t n, int64_t n_items,
                                                          RowTargets<T, NV> tg) {
-  const int64_t eb = static_cast<int64_t>(blockIdx.x) * 256 + 64 * wave_index();
+  constexpr int R = kReduceRounds;
+  const int64_t eb = (static_cast<int64_t>(blockIdx.x) * 4 + wave_index()) * kReduceWaveRows;
   if (eb >= n) return;  // uniform per wave
   const uint32_t lane = lane_id();
-  const int64_t e = eb + lane;
-  const bool in = e < n;
-  const int64_t g = in ? static_cast<int64_t>(emit_ids[e]) : -1;
-  const int32_t seg = (g >= 0 && g < n_items) ? static_cast<int32_t>(g)
-                                               : -1 - static_cast<int32_t>(lane);
-  const WaveSegments segs(seg);
-  const int32_t seg_prev = __shfl_up(seg, 1, 64);
-  const int32_t before = (eb > 0) ? emit_ids[eb - 1] : -1;
-  const int32_t seg_first = __shfl(seg, 0, 64);
-  const int32_t seg_last = __shfl(seg, 63, 64);
-  // First lane of each segment, unless the segment began in an earlier wave.
-  const bool head = seg >= 0 && (lane == 0 ? before != seg : seg_prev != seg);
-  T v[NV];
-  load_row(rows, in ? e : 0, v);
-  if (!in) {
+  // Segment id per row: the Gaussian, or a negative value unique to the row
+  // slot for rows past the end (or with an id out of range).
+  int32_t seg[R];
+  T v[R][NV];
 #pragma unroll
-    for (int c = 0; c < NV; ++c) v[c] = 0;
+  for (int r = 0; r < R; ++r) {
+    const int64_t e = eb + r * 64 + lane;
+    const bool in = e < n;
+    const int64_t g = in ? static_cast<int64_t>(emit_ids[e]) : -1;
+    seg[r] = (g >= 0 && g < n_items) ? static_cast<int32_t>(g)
+                                     : -1 - static_cast<int32_t>(r * 64 + lane);
+    load_row(rows, in ? e : 0, v[r]);
+    if (!in) {
+#pragma unroll
+      for (int c = 0; c < NV; ++c) v[r][c] = 0;
+    }
   }
-#pragma unroll
-  for (int c = 0; c < NV; ++c) v[c] = segs.suffix_sum(v[c]);
+  const int32_t before = (eb > 0) ? emit_ids[eb - 1] : -1;
+  const int32_t seg_first = __shfl(seg[0], 0, 64);
+  const int32_t seg_last = __shfl(seg[R - 1], 63, 64);
   // Rows of the last segment beyond this wave (uniform branch and loop).
-  const bool tail_owned = seg_last >= 0 && !(seg_first == seg_last && before == seg_last);
-  if (tail_owned && eb + 64 < n && emit_ids[eb + 64] == seg_last) {
-    T t[NV];
+  T carry[NV];
 #pragma unroll
-    for (int c = 0; c < NV; ++c) t[c] = 0;
-    for (int64_t base = eb + 64; base < n; base += 64) {
+  for (int c = 0; c < NV; ++c) carry[c] = 0;
+  int32_t carry_seg = -1 - kReduceWaveRows;  // matches no row slot
+  const bool tail_owned = seg_last >= 0 && !(seg_first == seg_last && before == seg_last);
+  const int64_t past = eb + kReduceWaveRows;
+  if (tail_owned && past < n && emit_ids[past] == seg_last) {
+    for (int64_t base = past; base < n; base += 64) {
       const int64_t e2 = base + lane;
       const bool take = e2 < n && emit_ids[e2] == seg_last;
       if (take) {
         T w[NV];
         load_row(rows, e2, w);
 #pragma unroll
-        for (int c = 0; c < NV; ++c) t[c] += w[c];
+        for (int c = 0; c < NV; ++c) carry[c] += w[c];
       }
       if (!(base + 63 < n && __shfl(static_cast<int>(take), 63, 64))) break;
     }
 #pragma unroll
-    for (int c = 0; c < NV; ++c) t[c] = wave_sum(t[c]);
-    if (seg == seg_last) {
+    for (int c = 0; c < NV; ++c) carry[c] = wave_sum(carry[c]);
+    carry_seg = seg_last;
+  }
+  // Rounds last to first: each round's suffix sums plus the carry of the
+  // segment continuing into the next round; the sum at lane 0 carries on.
+  const bool last_wave = past >= n;
 #pragma unroll
-      for (int c = 0; c < NV; ++c) v[c] += t[c];
+  for (int r = R - 1; r >= 0; --r) {
+    const WaveSegments segs(seg[r]);
+    T x[NV];
+#pragma unroll
+    for (int c = 0; c < NV; ++c) {
+      x[c] = segs.suffix_sum(v[r][c]);
+      if (seg[r] == carry_seg) x[c] += carry[c];
+    }
+    const int32_t seg_prev = __shfl_up(seg[r], 1, 64);
+    const int32_t prev_last = r > 0 ? __shfl(seg[r > 0 ? r - 1 : 0], 63, 64) : before;
+    const int32_t p = lane == 0 ? prev_last : seg_prev;
+    // First row of each Gaussian, unless it began in an earlier wave.
+    const bool head = seg[r] >= 0 && p != seg[r];
+#pragma unroll
+    for (int c = 0; c < NV; ++c) carry[c] = __shfl(x[c], 0, 64);
+    carry_seg = __shfl(seg[r], 0, 64);
+    // Ids without records before this Gaussian's id.
+    int64_t z_lo = 0, z_hi = 0;
+    if (head) {
+      z_lo = static_cast<int64_t>(p) + 1;
+      z_hi = seg[r];
+    }
+    zero_id_ranges(z_lo, z_hi, tg);
+    if (head) {
+      const int64_t g = seg[r];
+#pragma unroll
+      for (int c = 0; c < NV; ++c) tg.ptr[c][g * tg.stride[c]] = x[c];
     }
   }
-  if (!head) return;
-#pragma unroll
-  for (int c = 0; c < NV; ++c) tg.ptr[c][g * tg.stride[c]] = v[c];
+  if (last_wave) {  // uniform: this wave holds the last record
+    const int64_t last = emit_ids[n - 1];
+    const bool take = lane == 0 && last >= 0 && last < n_items;
+    zero_id_ranges<T, NV>(take ? last + 1 : 0, take ? n_items : 0, tg);
+  }
 }
 
 template <typename T, int NV>
 void launch_row_reduce(const T *rows, const int32_t *emit_ids, int64_t n, int64_t n_items,
                        const RowTargets<T, NV> &tg, hipStream_t stream) {
-  row_reduce_kernel<T, NV><<<dim3(static_cast<uint32_t>(ceil_div(n, 256))), dim3(256), 0,
-                             stream>>>(rows, emit_ids, n, n_items, tg);
+  row_reduce_kernel<T, NV><<<dim3(static_cast<uint32_t>(ceil_div(n, 4 * kReduceWaveRows))),
+                             dim3(256), 0, stream>>>(rows, emit_ids, n, n_items, tg);
 }
 
 }  // namespace r2s

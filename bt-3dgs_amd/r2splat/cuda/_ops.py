@@ -571,17 +571,21 @@ def _raster_bwd(means2d, conics, opacities, mus, tile_offsets, isect_ids, flatte
     _check(v_render.size(0) == C and v_render.size(1) == H and v_render.size(2) == W,
            "v_render_output shape must be [C, dim0, dim1]")
     th, tw = tile_offsets.size(1), tile_offsets.size(2)
-    v_means2d = torch.zeros_like(means2d)
-    v_abs = torch.zeros_like(means2d) if absgrad else None
-    v_conics = torch.zeros_like(conics)
-    v_opac = torch.zeros_like(opacities)
-    v_mus = torch.zeros_like(mus)
     n_isects = flatten_ids.numel()
-    if C == 0 or N == 0 or n_isects == 0:
+    empty = C == 0 or N == 0 or n_isects == 0
+    emit = None if empty else _emission_order(flatten_ids, C * tw * th)
+    # The two-pass form stores every output (zero for Gaussians without
+    # records); the one-pass form accumulates into zeros.
+    alloc = torch.empty_like if emit is not None else torch.zeros_like
+    v_means2d = alloc(means2d)
+    v_abs = alloc(means2d) if absgrad else None
+    v_conics = alloc(conics)
+    v_opac = alloc(opacities)
+    v_mus = alloc(mus)
+    if empty:
         return v_abs, v_means2d, v_conics, v_opac, v_mus
     sfx = _suffix(means2d, op)
     dev = means2d.device
-    emit = _emission_order(flatten_ids, C * tw * th)
     with torch.cuda.device(dev):
         if emit is not None:
             ws = _workspace(_lib().r2s_rasterize_bwd_workspace_bytes(n_isects,
@@ -752,16 +756,19 @@ def _voxel_bwd(means3d, conics, opacities, tile_offsets, isect_ids, flatten_ids,
     _check(v_render.dim() == 3, "v_render_output must be 3D [dim0, dim1, dim2]")
     d2, d1, d0, ts = int(dim2), int(dim1), int(dim0), int(tile_size)
     n0, n1, n2 = tile_offsets.size(0), tile_offsets.size(1), tile_offsets.size(2)
-    v_means3d = torch.zeros_like(means3d)
-    v_conics = torch.zeros_like(conics)
-    v_opac = torch.zeros_like(opacities)
     n_isects = flatten_ids.numel()
-    if N == 0 or n_isects == 0:
+    empty = N == 0 or n_isects == 0
+    emit = None if empty else _emission_order(flatten_ids, n2 * n1 * n0)
+    # As in _raster_bwd: the two-pass form stores every output.
+    alloc = torch.empty_like if emit is not None else torch.zeros_like
+    v_means3d = alloc(means3d)
+    v_conics = alloc(conics)
+    v_opac = alloc(opacities)
+    if empty:
         return v_means3d, v_conics, v_opac
     _check(tuple(v_render.shape) == (d0, d1, d2), "v_render_output shape must be [dim0, dim1, dim2]")
     sfx = _suffix(means3d, op)
     dev = means3d.device
-    emit = _emission_order(flatten_ids, n2 * n1 * n0)
     with torch.cuda.device(dev):
         if emit is not None:
             ws = _workspace(_lib().r2s_voxelize_bwd_workspace_bytes(n_isects,

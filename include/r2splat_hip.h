@@ -324,7 +324,7 @@ int r2s_rasterize_bwd_f64(const double *means2d, const double *conics,
                           double *v_conics, double *v_opacities, double *v_mus,
                           r2s_stream_t stream);
 
-/* Workspace of r2s_rasterize_bwd_emit_*: one row of 16 values of
+/* Workspace of r2s_rasterize_bwd_emit_*: one row of 12 values of
  * dtype_bytes per record. */
 int64_t r2s_rasterize_bwd_workspace_bytes(int64_t n_isects, int dtype_bytes);
 
@@ -335,8 +335,9 @@ int64_t r2s_rasterize_bwd_workspace_bytes(int64_t n_isects, int dtype_bytes);
  * walks the rows in emission order, where each Gaussian's records are
  * consecutive (emit_ids), sums them and stores each Gaussian's sums once.
  * Deterministic.  isect_ids may be NULL.  Outputs are stored, not
- * accumulated: the caller zeroes them (Gaussians without records are not
- * written). */
+ * accumulated, for every Gaussian: zero where it has no record, so they
+ * need no zeroing beforehand.  emit_ids must be as the emit-sort calls
+ * write it (ids ascending). */
 int r2s_rasterize_bwd_emit_f32(const float *means2d, const float *conics,
                                const float *opacities, const float *mus,
                                const int32_t *tile_offsets, const int64_t *isect_ids,
@@ -362,11 +363,11 @@ int r2s_rasterize_bwd_emit_f64(const double *means2d, const double *conics,
 
 /* The two passes of r2s_rasterize_bwd_emit_* as separate calls (for callers
  * that schedule or time them apart).  _rows: the first pass; writes the
- * per-record rows (16 values, 9 used with absgrad != 0, else 7) at their
+ * per-record rows (12 values, 9 used with absgrad != 0, else 7) at their
  * emission index into `rows` (r2s_rasterize_bwd_workspace_bytes, 16-byte
- * aligned).  _reduce: the second pass; stores each Gaussian's sums into the
- * zeroed outputs (v_means2d_abs NULL exactly when the rows were written
- * with absgrad == 0).  No reference counterpart. */
+ * aligned).  _reduce: the second pass; stores each Gaussian's sums, zero
+ * for Gaussians without records (v_means2d_abs NULL exactly when the rows
+ * were written with absgrad == 0).  No reference counterpart. */
 int r2s_rasterize_bwd_rows_f32(const float *means2d, const float *conics,
                                const float *opacities, const float *mus,
                                const int32_t *tile_offsets, const int64_t *isect_ids,
@@ -463,15 +464,15 @@ int r2s_voxelize_bwd_f64(const double *means3d, const double *conics,
                          double *v_means3d, double *v_conics,
                          double *v_opacities, r2s_stream_t stream);
 
-/* Workspace of r2s_voxelize_bwd_emit_*: one row of 16 values of
+/* Workspace of r2s_voxelize_bwd_emit_*: one row of 12 values of
  * dtype_bytes per record. */
 int64_t r2s_voxelize_bwd_workspace_bytes(int64_t n_isects, int dtype_bytes);
 
 /* The same VJP as r2s_voxelize_bwd_* (VoxelizeToVoxelsBwd.cu:71-441) in two
  * passes, as r2s_rasterize_bwd_emit_*: per-record rows stored at their
  * emission index, then summed per Gaussian and stored once.
- * Deterministic.  isect_ids may be NULL.  Outputs are stored, not
- * accumulated: the caller zeroes them. */
+ * Deterministic.  isect_ids may be NULL.  Outputs are stored for every
+ * Gaussian, zero where it has no record, as for the rasterizer. */
 int r2s_voxelize_bwd_emit_f32(const float *means3d, const float *conics,
                               const float *opacities, const int32_t *tile_offsets,
                               const int64_t *isect_ids, const int32_t *flatten_ids,

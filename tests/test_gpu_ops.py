@@ -399,6 +399,37 @@ def test_emission_order_backward_is_deterministic():
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("seed", [0, 1])
+def test_row_reduction_stores_every_id(seed):
+    # Hand-built emission orders: ids ascending, gaps before the first and
+    # after the last record and between records, segments longer than a
+    # wave; integer rows, so every summation order gives the same sums.
+    from r2splat.cuda import _backend
+
+    lib, P = _backend.library(), _ops._ptr
+    st = torch.cuda.current_stream().cuda_stream
+    g = torch.Generator().manual_seed(seed)
+    N = 700
+    ids = torch.sort(torch.randperm(N - 20, generator=g)[:300] + 7).values
+    ids = ids[(ids < 150) | (ids > 400)]  # one long run of ids without records
+    counts = torch.randint(1, 9, (ids.numel(),), generator=g)
+    counts[::25] = torch.randint(60, 200, (counts[::25].numel(),), generator=g)
+    emit_ids = torch.repeat_interleave(ids, counts).int()
+    n = emit_ids.numel()
+    rows = torch.randint(-8, 9, (n, 12), generator=g).float()
+    want = torch.zeros(N, 12).index_add_(0, emit_ids.long(), rows)
+    outs = [torch.full((1, N, k), float("nan"), device=DEV) for k in (2, 3)]
+    outs += [torch.full((1, N), float("nan"), device=DEV) for _ in range(2)]
+    outs.insert(0, torch.full((1, N, 2), float("nan"), device=DEV))  # absgrad
+    rows_d, emit_d = rows.to(DEV), emit_ids.to(DEV)
+    assert lib.r2s_rasterize_bwd_reduce_f32(P(rows_d), P(emit_d), n, 1, N,
+                                            *[P(t) for t in outs], st) == 0
+    v_abs, v_xy, v_con, v_op, v_mu = (t.cpu().reshape(N, -1) for t in outs)
+    got = torch.cat([v_xy, v_con, v_op, v_mu, v_abs], 1)
+    assert torch.equal(got, want[:, :9])
+    assert int(emit_ids[0]) > 0 and int(emit_ids[-1]) < N - 1
+
+
 def test_backward_stage_entry_points_match_the_two_pass_op():
     from r2splat.cuda import _backend
 
@@ -415,11 +446,16 @@ def test_backward_stage_entry_points_match_the_two_pass_op():
     assert lib.r2s_rasterize_bwd_rows_f32(P(m2), P(con), P(op), P(mu), P(off), P(ids), P(fl),
                                           P(src), n, P(v), 2, N, 64, 48, 16, 4, 3, 1, P(rows),
                                           rows.numel(), st) == 0
-    got = [torch.zeros_like(t) for t in want]
+    # NaN on entry: the reduction stores every output, zero without records.
+    got = [torch.full_like(t, float("nan")) for t in want]
     assert lib.r2s_rasterize_bwd_reduce_f32(P(rows), P(emit_ids), n, 2, N, *[P(t) for t in got],
                                             st) == 0
     for a, b in zip(got, want):
         assert torch.equal(a, b)
+    untouched = torch.ones(2 * N, dtype=torch.bool, device=DEV)
+    untouched[fl.long()] = False
+    assert int(untouched.sum()) > 0
+    assert int(got[1].reshape(2 * N, 2)[untouched].abs().sum()) == 0
     d3, m3, con3, ids3, fl3, off3 = _voxel_case(2500, 14, (32, 24, 16), 8)
     v3 = torch.randn((16, 24, 32), generator=d3["gen"]).to(DEV)
     want3 = W.voxelize_to_voxels_bwd(m3, con3, d3["opac"], off3, fl3, v3, 32, 24, 16, 8)
@@ -430,7 +466,7 @@ def test_backward_stage_entry_points_match_the_two_pass_op():
     assert lib.r2s_voxelize_bwd_rows_f32(P(m3), P(con3), P(d3["opac"]), P(off3), None, P(fl3),
                                          P(src3), n3, P(v3), N3, 32, 24, 16, 8, 4, 3, 2,
                                          P(rows3), rows3.numel(), st) == 0
-    got3 = [torch.zeros_like(t) for t in want3]
+    got3 = [torch.full_like(t, float("nan")) for t in want3]
     assert lib.r2s_voxelize_bwd_reduce_f32(P(rows3), P(emit3), n3, N3, *[P(t) for t in got3],
                                            st) == 0
     for a, b in zip(got3, want3):
