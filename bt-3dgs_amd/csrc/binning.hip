@@ -257,11 +257,14 @@ __global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(const uint32_t
   for (uint32_t d = threadIdx.x; d < digits; d += kSortThreads) h[d] = 0;
   __syncthreads();
   const uint32_t mask = digits - 1u;
-  const int64_t base = static_cast<int64_t>(tile) * kSortTile;
-  for (int i = threadIdx.x; i < kSortTile; i += kSortThreads) {
-    const int64_t k = base + i;
-    if (k < n) atomicAdd(&h[(keys[k] >> shift) & mask], 1u);
-  }
+  const int64_t base = static_cast<int64_t>(tile) * kSortTile + threadIdx.x;
+  // All loads first (clamped in bounds), then the LDS counts.
+  uint32_t key[kSortRounds];
+#pragma unroll
+  for (int r = 0; r < kSortRounds; ++r) key[r] = keys[min(base + r * kSortThreads, n - 1)];
+#pragma unroll
+  for (int r = 0; r < kSortRounds; ++r)
+    if (base + r * kSortThreads < n) atomicAdd(&h[(key[r] >> shift) & mask], 1u);
   __syncthreads();
   for (uint32_t d = threadIdx.x; d < digits; d += kSortThreads)
     hist[static_cast<int64_t>(d) * nblocks + tile] = h[d];
@@ -301,13 +304,20 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
   const int64_t first = block_first + w * kSortWaveItems;
   const uint64_t lt = lanemask_lt();
   uint32_t key[kSortRounds], gid[kSortRounds], ev[kSortRounds], rank[kSortRounds];
+  // All loads first (clamped in bounds: a block's last wave may run past n),
+  // so their latencies overlap; then the ranking rounds.
+#pragma unroll
+  for (int r = 0; r < kSortRounds; ++r) {
+    const int64_t i = first + r * 64 + lane;
+    const int64_t ic = min(i, n - 1);
+    key[r] = keys_in[ic];
+    gid[r] = gid_in[ic];
+    if (kTwo) ev[r] = kFirst ? static_cast<uint32_t>(i) : e_in[ic];
+  }
 #pragma unroll
   for (int r = 0; r < kSortRounds; ++r) {
     const int64_t i = first + r * 64 + lane;
     const bool valid = i < n;
-    key[r] = valid ? keys_in[i] : 0u;
-    gid[r] = valid ? gid_in[i] : 0u;
-    if (kTwo) ev[r] = kFirst ? static_cast<uint32_t>(i) : (valid ? e_in[i] : 0u);
     const uint32_t d = (key[r] >> shift) & mask;
     // Lanes holding the same digit: intersect the ballots of every digit bit.
     uint64_t peers = ballot(valid);
