@@ -160,9 +160,9 @@ template <typename T>
 __global__ __launch_bounds__(256) void emit_2d_kernel(
     const T *__restrict__ means2d, const int32_t *__restrict__ radii, int rect, int64_t M,
     int64_t N, uint32_t ts, uint32_t tw, uint32_t th, const int64_t *__restrict__ offsets,
-    uint32_t *__restrict__ keys, uint32_t *__restrict__ gids) {
+    int64_t cap, uint32_t *__restrict__ keys, uint32_t *__restrict__ gids) {
   const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + 64 * wave_index();
-  if (wave_first >= M) return;  // uniform per wave
+  if (wave_first >= M || offsets[M] > cap) return;  // uniform per wave
   const int64_t idx = wave_first + lane_id();
   Rect r = {0, 0, 0, 0};
   uint32_t cnt = 0;
@@ -194,10 +194,10 @@ __global__ __launch_bounds__(256) void emit_2d_kernel(
 template <typename T>
 __global__ __launch_bounds__(256) void emit_3d_kernel(
     const T *__restrict__ means3d, const int32_t *__restrict__ radii, int64_t N, uint32_t ts,
-    uint32_t n2, uint32_t n1, uint32_t n0, const int64_t *__restrict__ offsets,
+    uint32_t n2, uint32_t n1, uint32_t n0, const int64_t *__restrict__ offsets, int64_t cap,
     uint32_t *__restrict__ keys, uint32_t *__restrict__ gids) {
   const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + 64 * wave_index();
-  if (wave_first >= N) return;  // uniform per wave
+  if (wave_first >= N || offsets[N] > cap) return;  // uniform per wave
   const int64_t idx = wave_first + lane_id();
   const uint32_t n[3] = {n2, n1, n0};
   Box b;
@@ -244,15 +244,23 @@ constexpr int kMaxPassBits = 11;                        // up to 2048 digits per
 constexpr int kMaxDigits = 1 << kMaxPassBits;
 constexpr int kDigitsPerThread = kMaxDigits / kSortThreads;  // 8
 
+// The sort kernels are sized for `cap` items and read the actual count n
+// from the device (the emission scan's total); with n > cap they write
+// nothing, so a caller may launch them before it knows n.
+
 // Digit histogram of one 4096-item tile, written digit-major:
-// hist[d * nblocks + tile].  Tiles are XCD-contiguous (xcd_swizzle), so the
-// blocks writing neighbouring words of a digit's row share an L2.
+// hist[d * nblocks + tile] (zero rows for tiles past n).  Tiles are
+// XCD-contiguous (xcd_swizzle), so the blocks writing neighbouring words of
+// a digit's row share an L2.
 __global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(const uint32_t *__restrict__ keys,
-                                                                  int64_t n, uint32_t shift,
+                                                                  const int64_t *__restrict__ n_dev,
+                                                                  int64_t cap, uint32_t shift,
                                                                   uint32_t digits,
                                                                   uint32_t *__restrict__ hist,
                                                                   uint32_t nblocks) {
   __shared__ uint32_t h[kMaxDigits];
+  const int64_t n = *n_dev;
+  if (n <= 0 || n > cap) return;
   const uint32_t tile = xcd_swizzle(blockIdx.x, nblocks);
   for (uint32_t d = threadIdx.x; d < digits; d += kSortThreads) h[d] = 0;
   __syncthreads();
@@ -280,7 +288,8 @@ __global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(const uint32_t
 template <bool kFirst, bool kFinal, bool kTwo>
 __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     const uint32_t *__restrict__ keys_in, const uint32_t *__restrict__ e_in,
-    const uint32_t *__restrict__ gid_in, int64_t n, uint32_t shift, uint32_t bits,
+    const uint32_t *__restrict__ gid_in, const int64_t *__restrict__ n_dev, int64_t cap,
+    uint32_t shift, uint32_t bits,
     const uint32_t *__restrict__ digit_offsets, uint32_t nblocks, uint32_t *__restrict__ keys_out,
     uint32_t *__restrict__ e_out, uint32_t *__restrict__ gid_out,
     int64_t *__restrict__ keys_out64, int32_t *__restrict__ vals_out32,
@@ -296,11 +305,13 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
   __shared__ uint32_t s_e[kTwo ? kSortTile : 1];
   const uint32_t digits = 1u << bits, mask = digits - 1u;
   const uint32_t tile = xcd_swizzle(blockIdx.x, nblocks);
+  const int64_t n = *n_dev;
+  const int64_t block_first = static_cast<int64_t>(tile) * kSortTile;
+  if (n > cap || block_first >= n) return;  // uniform per block
   const uint32_t w = threadIdx.x / 64, lane = threadIdx.x % 64;
   for (uint32_t k = threadIdx.x; k < 4 * digits; k += kSortThreads)
     cnt[k / digits][k % digits] = 0;
   __syncthreads();
-  const int64_t block_first = static_cast<int64_t>(tile) * kSortTile;
   const int64_t first = block_first + w * kSortWaveItems;
   const uint64_t lt = lanemask_lt();
   uint32_t key[kSortRounds], gid[kSortRounds], ev[kSortRounds], rank[kSortRounds];
@@ -479,10 +490,11 @@ inline uint32_t key_bits_for(int64_t n_keys) {
   return b;
 }
 
-// Sorts the emitted records (s.k0, s.gid0) into the final outputs.  two:
-// the emission index travels too and the final pass writes it to src.
-int radix_sort(SortSpace &s, int64_t n, uint32_t key_bits, int64_t *keys64, int32_t *vals32,
-               bool two, int32_t *src, hipStream_t stream) {
+// Sorts the emitted records (s.k0, s.gid0) into the final outputs: *n_dev
+// records, at most cap (the size s was carved for).  two: the emission
+// index travels too and the final pass writes it to src.
+int radix_sort(SortSpace &s, const int64_t *n_dev, int64_t cap, uint32_t key_bits,
+               int64_t *keys64, int32_t *vals32, bool two, int32_t *src, hipStream_t stream) {
   const uint32_t passes = sort_passes(key_bits);
   const uint32_t pbits = max(1u, (key_bits + passes - 1) / passes);
   const uint32_t nb = static_cast<uint32_t>(s.nblocks);
@@ -492,8 +504,8 @@ int radix_sort(SortSpace &s, int64_t n, uint32_t key_bits, int64_t *keys64, int3
     const uint32_t bits = key_bits == 0 ? 1u : min(pbits, key_bits - shift);
     const uint32_t digits = 1u << bits;
     const int64_t n_hist = static_cast<int64_t>(nb) * digits;
-    radix_hist_kernel<<<dim3(nb), dim3(kSortThreads), 0, stream>>>(kin, n, shift, digits, s.hist,
-                                                                   nb);
+    radix_hist_kernel<<<dim3(nb), dim3(kSortThreads), 0, stream>>>(kin, n_dev, cap, shift,
+                                                                   digits, s.hist, nb);
     R2S_RETURN_IF(device_exclusive_scan<uint32_t, uint32_t>(s.hist, n_hist, s.hist_scan, nullptr,
                                                             s.partials, stream,
                                                             "isect sort scan"));
@@ -503,7 +515,8 @@ int radix_sort(SortSpace &s, int64_t n, uint32_t key_bits, int64_t *keys64, int3
     uint32_t *gout = (p % 2 == 0) ? s.g1 : s.g0;
 #define R2S_SCATTER(FIRST, FINAL, TWO)                                                         \
   radix_scatter_kernel<FIRST, FINAL, TWO><<<dim3(nb), dim3(kSortThreads), 0, stream>>>(       \
-      kin, ein, gin, n, shift, bits, s.hist_scan, nb, kout, eout, gout, keys64, vals32, src)
+      kin, ein, gin, n_dev, cap, shift, bits, s.hist_scan, nb, kout, eout, gout, keys64, vals32, \
+      src)
 #define R2S_SCATTER_TWO(FIRST, FINAL) \
   do {                                \
     if (two)                          \
@@ -627,10 +640,10 @@ int emit_sort_2d_impl(const T *means2d, const int32_t *radii, int rect, int64_t 
   s.gid0 = gids;
   const int64_t M = C * N;
   emit_2d_kernel<T><<<dim3(static_cast<uint32_t>(ceil_div(M, 256))), dim3(256), 0, stream>>>(
-      means2d, radii, rect, M, N, ts, tw, th, offsets, s.k0, gids);
+      means2d, radii, rect, M, N, ts, tw, th, offsets, n_isects, s.k0, gids);
   R2S_RETURN_IF(check_launch(name));
-  return radix_sort(s, n_isects, key_bits_for(C * tw * th), keys, vals, emit_ids != nullptr,
-                    isect_src, stream);
+  return radix_sort(s, offsets + M, n_isects, key_bits_for(C * tw * th), keys, vals,
+                    emit_ids != nullptr, isect_src, stream);
 }
 
 template <typename T>
@@ -655,10 +668,10 @@ int emit_sort_3d_impl(const T *means3d, const int32_t *radii, int64_t N, uint32_
   uint32_t *gids = emit_ids != nullptr ? reinterpret_cast<uint32_t *>(emit_ids) : s.g0;
   s.gid0 = gids;
   emit_3d_kernel<T><<<dim3(static_cast<uint32_t>(ceil_div(N, 256))), dim3(256), 0, stream>>>(
-      means3d, radii, N, ts, n2, n1, n0, offsets, s.k0, gids);
+      means3d, radii, N, ts, n2, n1, n0, offsets, n_isects, s.k0, gids);
   R2S_RETURN_IF(check_launch(name));
-  return radix_sort(s, n_isects, key_bits_for(static_cast<int64_t>(n2) * n1 * n0), keys, vals,
-                    emit_ids != nullptr, isect_src, stream);
+  return radix_sort(s, offsets + N, n_isects, key_bits_for(static_cast<int64_t>(n2) * n1 * n0),
+                    keys, vals, emit_ids != nullptr, isect_src, stream);
 }
 
 }  // namespace

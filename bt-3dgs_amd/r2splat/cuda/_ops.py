@@ -82,6 +82,69 @@ def _end_bit(n_keys: int) -> int:
     return int(math.ceil(math.log2(float(n_keys + 1))))
 
 
+# Record counts of recent binning calls, per (device, kind, items, keys).
+# The next call with the same sizes allocates its outputs for the largest
+# of them plus a margin and launches the emit + sort before reading its own
+# count back (the kernels read the count on the device and write nothing if
+# it exceeds the capacity), so the device does not sit idle while the host
+# waits for the count, allocates and launches.  The outputs are then the
+# leading n records of the larger buffers.  A short guess costs one exact
+# relaunch.
+_COUNT_HISTORY = {}
+_COUNT_HISTORY_LEN = 8
+_PINNED_COUNT = {}
+
+
+def _note_count(key, n: int) -> None:
+    hist = _COUNT_HISTORY.setdefault(key, [])
+    hist.append(n)
+    del hist[:-_COUNT_HISTORY_LEN]
+
+
+def _emit_and_sort(launch, offsets: Tensor, n_items: int, n_keys: int, op: str,
+                   dev: torch.device, kind: str):
+    """The emit + sort half of a binning op (IsectTiles.cpp:100-169): returns
+    (isect_ids, flatten_ids, emit_ids, isect_src), or None without records.
+    launch(capacity, end_bit, outputs, workspace) enqueues the library call."""
+    lib = _lib()
+    end_bit = _end_bit(n_keys)
+    key = (dev.index, kind, n_items, n_keys)
+
+    def alloc(cap):
+        outs = (torch.empty((cap,), dtype=torch.int64, device=dev),
+                torch.empty((cap,), dtype=torch.int32, device=dev),
+                torch.empty((cap,), dtype=torch.int32, device=dev),
+                torch.empty((cap,), dtype=torch.int32, device=dev))
+        return outs, _workspace(lib.r2s_isect_workspace_bytes(0, cap, end_bit), dev)
+
+    recent = _COUNT_HISTORY.get(key)
+    if recent:
+        guess = max(recent)
+        cap = min(guess + guess // 8 + 4096, 2 ** 31 - 1)
+        outs, ws = alloc(cap)
+        host = _PINNED_COUNT.get(dev.index)
+        if host is None:
+            host = _PINNED_COUNT[dev.index] = torch.empty(1, dtype=torch.int64, pin_memory=True)
+        host.copy_(offsets[n_items:n_items + 1], non_blocking=True)
+        ready = torch.cuda.Event()
+        ready.record()
+        launch(cap, end_bit, outs, ws)
+        ready.synchronize()
+        n = int(host[0])
+        _note_count(key, n)
+        if n <= cap:
+            return None if n == 0 else tuple(t[:n] for t in outs)
+    else:
+        n = int(offsets[n_items].item())  # the one host read-back (IsectTiles.cpp:100)
+        _note_count(key, n)
+    if n == 0:
+        return None
+    _check_record_count(n, op)
+    outs, ws = alloc(n)
+    launch(n, end_bit, outs, ws)
+    return outs
+
+
 # The binning ops also describe their records in emission order (id-major,
 # before the sort by tile) on the flatten_ids tensor they return: emit_ids[e]
 # is the id of emitted record e, isect_src[r] the emission index of sorted
@@ -420,19 +483,16 @@ def isect_tiles(means2d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim1: in
         ws = _workspace(lib.r2s_isect_workspace_bytes(C * N, 0, 0), dev)
         _call(f"r2s_isect_count_2d_{sfx}", _ptr(means2d), _ptr(radii), rect, C, N, ts, tw, th,
               _ptr(tiles_per_gauss), _ptr(offsets), _ptr(ws), ws.numel(), st)
-        n_isects = int(offsets[-1].item())  # the one host read-back (IsectTiles.cpp:100)
-        if n_isects == 0:
-            return (tiles_per_gauss,) + empty_ids
-        _check_record_count(n_isects, "isect_tiles")
-        end_bit = _end_bit(C * tw * th)
-        isect_ids = torch.empty((n_isects,), dtype=torch.int64, device=dev)
-        flatten_ids = torch.empty((n_isects,), dtype=torch.int32, device=dev)
-        emit_ids = torch.empty((n_isects,), dtype=torch.int32, device=dev)
-        isect_src = torch.empty((n_isects,), dtype=torch.int32, device=dev)
-        ws = _workspace(lib.r2s_isect_workspace_bytes(0, n_isects, end_bit), dev)
-        _call(f"r2s_isect_emit_sort_2d_{sfx}", _ptr(means2d), _ptr(radii), rect, C, N, ts, tw,
-              th, _ptr(offsets), n_isects, end_bit, _ptr(isect_ids), _ptr(flatten_ids),
-              _ptr(emit_ids), _ptr(isect_src), _ptr(ws), ws.numel(), st)
+
+        def launch(cap, end_bit, outs, ws):
+            _call(f"r2s_isect_emit_sort_2d_{sfx}", _ptr(means2d), _ptr(radii), rect, C, N, ts,
+                  tw, th, _ptr(offsets), cap, end_bit, *[_ptr(t) for t in outs], _ptr(ws),
+                  ws.numel(), st)
+
+        res = _emit_and_sort(launch, offsets, C * N, C * tw * th, "isect_tiles", dev, "2d")
+    if res is None:
+        return (tiles_per_gauss,) + empty_ids
+    isect_ids, flatten_ids, emit_ids, isect_src = res
     _keep_emission_order(flatten_ids, emit_ids, isect_src, C * tw * th)
     return tiles_per_gauss, isect_ids, flatten_ids
 
@@ -480,19 +540,17 @@ def isect_tiles_3d(means3d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim2:
         ws = _workspace(lib.r2s_isect_workspace_bytes(N, 0, 0), dev)
         _call(f"r2s_isect_count_3d_{sfx}", _ptr(means3d), _ptr(radii), N, ts, n2, n1, n0,
               _ptr(tiles_per_gauss), _ptr(offsets), _ptr(ws), ws.numel(), st)
-        n_isects = int(offsets[-1].item())  # IsectTiles3D.cpp:96
-        if n_isects == 0:
-            return (tiles_per_gauss,) + empty_ids
-        _check_record_count(n_isects, "isect_tiles_3d")
-        end_bit = _end_bit(n2 * n1 * n0)
-        isect_ids = torch.empty((n_isects,), dtype=torch.int64, device=dev)
-        flatten_ids = torch.empty((n_isects,), dtype=torch.int32, device=dev)
-        emit_ids = torch.empty((n_isects,), dtype=torch.int32, device=dev)
-        isect_src = torch.empty((n_isects,), dtype=torch.int32, device=dev)
-        ws = _workspace(lib.r2s_isect_workspace_bytes(0, n_isects, end_bit), dev)
-        _call(f"r2s_isect_emit_sort_3d_{sfx}", _ptr(means3d), _ptr(radii), N, ts, n2, n1, n0,
-              _ptr(offsets), n_isects, end_bit, _ptr(isect_ids), _ptr(flatten_ids),
-              _ptr(emit_ids), _ptr(isect_src), _ptr(ws), ws.numel(), st)
+
+        def launch(cap, end_bit, outs, ws):
+            _call(f"r2s_isect_emit_sort_3d_{sfx}", _ptr(means3d), _ptr(radii), N, ts, n2, n1,
+                  n0, _ptr(offsets), cap, end_bit, *[_ptr(t) for t in outs], _ptr(ws),
+                  ws.numel(), st)
+
+        # IsectTiles3D.cpp:96 reads the count back here.
+        res = _emit_and_sort(launch, offsets, N, n2 * n1 * n0, "isect_tiles_3d", dev, "3d")
+    if res is None:
+        return (tiles_per_gauss,) + empty_ids
+    isect_ids, flatten_ids, emit_ids, isect_src = res
     _keep_emission_order(flatten_ids, emit_ids, isect_src, n2 * n1 * n0)
     return tiles_per_gauss, isect_ids, flatten_ids
 

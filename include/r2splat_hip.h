@@ -205,7 +205,12 @@ int r2s_isect_count_2d_f64(const double *means2d, const int32_t *radii,
  * consecutive -- which the reference does not output: emit_ids[e] is the id
  * of emitted record e and isect_src[r] the emission index of sorted record
  * r.  The two-pass backward kernels (r2s_rasterize_bwd_emit_*,
- * r2s_voxelize_bwd_emit_*) take them. */
+ * r2s_voxelize_bwd_emit_*) take them.
+ * n_isects is the capacity of the outputs and the size the workspace is
+ * queried for; the kernels read the record count from offsets[C*N] on the
+ * device and write nothing when it exceeds n_isects.  A caller may thus
+ * launch this before reading the count back, with a guessed capacity, and
+ * call again with the exact count if the guess was short. */
 int r2s_isect_emit_sort_2d_f32(const float *means2d, const int32_t *radii,
                                int radii_is_rect, int64_t C, int64_t N,
                                uint32_t tile_size, uint32_t n_tiles_w,

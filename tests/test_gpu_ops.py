@@ -190,6 +190,42 @@ def test_isect_tiles_sort_widths(tiles, views):
     assert_equal(np32(off), binning.isect_offset_encode(ids_o, views, tw, th), "tile_offsets")
 
 
+def test_isect_tiles_capacity_guess():
+    # Later calls with the same sizes allocate from the recent record counts
+    # and launch the emit + sort before reading their count back; a count
+    # above the guess relaunches with exact sizes.  Every result equals the
+    # oracle's, and the backward reads the leading-record views correctly.
+    _ops._COUNT_HISTORY.clear()
+    g = torch.Generator().manual_seed(21)
+    N = 3000
+    m2 = (torch.rand(1, N, 2, generator=g) * 512).float()
+    con = torch.tensor([0.02, 0.003, 0.03]).repeat(1, N, 1)
+    op = torch.rand(1, N, generator=g) + 0.1
+    mu = torch.rand(1, N, generator=g)
+    v = torch.randn(1, 512, 512, generator=g).to(DEV)
+    guessed = []
+    for scale in (20, 10, 60, 60, 5):
+        r = torch.randint(0, scale, (1, N, 2), generator=g).int()
+        tpg, ids, fl = W.isect_tiles(m2.to(DEV), r.to(DEV), 16, 32, 32)
+        tpg_o, ids_o, fl_o = binning.isect_tiles(m2.numpy(), r.numpy(), 16, 32, 32)
+        assert_equal(np32(tpg), tpg_o, "tiles_per_gauss")
+        assert_equal(np32(ids), ids_o, "isect_ids")
+        assert_equal(np32(fl), fl_o, "flatten_ids")
+        guessed.append(ids.untyped_storage().nbytes() > 8 * ids.numel())
+        off = W.isect_offset_encode(ids, 1, 32, 32)
+        args = (m2.to(DEV), con.to(DEV), op.to(DEV), mu.to(DEV), off)
+        got = W.rasterize_to_pixels_bwd_per_gaussian(*args, ids, fl, v, 512, 512, 16, True)
+        # The same records in exact-size tensors, with the same emission order.
+        emit_ids, src = _ops._emission_order(fl, 1024)
+        ids2, fl2 = ids.clone(), fl.clone()
+        _ops._keep_emission_order(fl2, emit_ids.clone(), src.clone(), 1024)
+        want = W.rasterize_to_pixels_bwd_per_gaussian(*args, ids2, fl2, v, 512, 512, 16, True)
+        for a, b in zip(got, want):
+            assert torch.equal(a, b)
+    # First call exact; the third (60 > the guess from 20 and 10) relaunched.
+    assert guessed == [False, True, False, True, True]
+
+
 @pytest.mark.parametrize("bricks", [(13, 13, 13), (256, 256, 160)])
 def test_isect_tiles_3d_sort_widths(bricks):
     # 2197 bricks: two 6-bit passes; 10.5 M bricks (24-bit keys): three passes.
