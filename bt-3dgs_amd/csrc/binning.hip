@@ -316,7 +316,17 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
   const uint64_t lt = lanemask_lt();
   uint32_t key[kSortRounds], gid[kSortRounds], ev[kSortRounds], rank[kSortRounds];
   // All loads first (clamped in bounds: a block's last wave may run past n),
-  // so their latencies overlap; then the ranking rounds.
+  // so their latencies overlap; then the ranking rounds.  Thread t owns
+  // digits [t*dk, t*dk + dk) in the scan below; their global run starts do
+  // not depend on the ranking, so they load here too.
+  const uint32_t dk = (digits + kSortThreads - 1) / kSortThreads;
+  const uint32_t d0 = threadIdx.x * dk;
+  uint32_t gb[kDigitsPerThread];
+#pragma unroll
+  for (uint32_t j = 0; j < kDigitsPerThread; ++j) {
+    const uint32_t d = min(d0 + j, digits - 1u);
+    gb[j] = digit_offsets[static_cast<int64_t>(d) * nblocks + tile];
+  }
 #pragma unroll
   for (int r = 0; r < kSortRounds; ++r) {
     const int64_t i = first + r * 64 + lane;
@@ -346,10 +356,9 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
   }
   __syncthreads();
   {
-    // Thread t owns digits [t*k, t*k + k): per digit the waves' starts and
-    // the block total, then an exclusive scan of the totals over digits.
-    const uint32_t k = (digits + kSortThreads - 1) / kSortThreads;
-    const uint32_t d0 = threadIdx.x * k;
+    // Per owned digit the waves' starts and the block total, then an
+    // exclusive scan of the totals over digits.
+    const uint32_t k = dk;
     uint32_t tot[kDigitsPerThread];
     uint32_t mine = 0;
 #pragma unroll
@@ -376,7 +385,7 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
       if (j < k && d < digits) {
         dbase[d] = static_cast<uint16_t>(run);
         run += tot[j];
-        gbase[d] = digit_offsets[static_cast<int64_t>(d) * nblocks + tile];
+        gbase[d] = gb[j];
       }
     }
   }

@@ -1,9 +1,11 @@
 // Device-wide exclusive prefix sum (reduce -> scan partials -> downsweep).
 //
-// 256-thread blocks, 16 consecutive items per thread (4096 per block).  The
-// partial sums of all blocks are scanned by one 1024-thread block, so a scan
-// of n items needs ceil(n / 4096) partials of workspace.  Deterministic: the
-// same input always produces the same output.
+// 256-thread blocks, 4096 items per block taken as 16 chunks of 256: item
+// k * 256 + t of a block belongs to thread t, so every load and store of a
+// wave covers 64 consecutive items.  The partial sums of all blocks are
+// scanned by one 1024-thread block, so a scan of n items needs
+// ceil(n / 4096) partials of workspace.  Deterministic: the same input always
+// produces the same output.
 #pragma once
 
 #include "r2s_common.h"
@@ -40,11 +42,15 @@ __global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(const Tin *__
                                                                    int64_t n,
                                                                    Tout *__restrict__ partials) {
   __shared__ Tout lds[kScanThreads / 64];
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile + threadIdx.x * kScanItems;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile + threadIdx.x;
+  // Loads clamped in bounds and masked after, so all of them issue at once.
+  Tin v[kScanItems];
+#pragma unroll
+  for (int k = 0; k < kScanItems; ++k) v[k] = in[min(base + k * kScanThreads, n - 1)];
   Tout s = 0;
 #pragma unroll
   for (int k = 0; k < kScanItems; ++k)
-    if (base + k < n) s += static_cast<Tout>(in[base + k]);
+    if (base + k * kScanThreads < n) s += static_cast<Tout>(v[k]);
   Tout total;
   block_exclusive_scan(s, lds, total);
   if (threadIdx.x == 0) partials[blockIdx.x] = total;
@@ -69,26 +75,40 @@ __global__ __launch_bounds__(1024) void scan_partials_kernel(Tout *__restrict__ 
   if (threadIdx.x == 0 && total != nullptr) *total = running;
 }
 
+// Per chunk: a wave scan; then one scan over the 64 (chunk, wave) totals in
+// item order gives each chunk-wave its offset within the block.
 template <typename Tin, typename Tout>
 __global__ __launch_bounds__(kScanThreads) void scan_down_kernel(const Tin *__restrict__ in,
                                                                  int64_t n,
                                                                  const Tout *__restrict__ partials,
                                                                  Tout *__restrict__ out) {
-  __shared__ Tout lds[kScanThreads / 64];
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile + threadIdx.x * kScanItems;
-  Tout vals[kScanItems];
-  Tout s = 0;
+  static_assert(kScanItems * (kScanThreads / 64) == 64, "one wave scans the chunk totals");
+  __shared__ Tout s_tot[64];
+  const uint32_t w = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile + threadIdx.x;
+  Tout v[kScanItems], incl[kScanItems];
 #pragma unroll
   for (int k = 0; k < kScanItems; ++k) {
-    vals[k] = (base + k < n) ? static_cast<Tout>(in[base + k]) : static_cast<Tout>(0);
-    s += vals[k];
+    const int64_t i = base + k * kScanThreads;
+    const Tin x = in[min(i, n - 1)];
+    v[k] = i < n ? static_cast<Tout>(x) : static_cast<Tout>(0);
   }
-  Tout total;
-  Tout run = partials[blockIdx.x] + block_exclusive_scan(s, lds, total);
 #pragma unroll
   for (int k = 0; k < kScanItems; ++k) {
-    if (base + k < n) out[base + k] = run;
-    run += vals[k];
+    incl[k] = wave_inclusive_scan(v[k]);
+    if (lane == 63) s_tot[k * (kScanThreads / 64) + w] = incl[k];
+  }
+  __syncthreads();
+  if (w == 0) {  // each lane reads, then overwrites, its own entry
+    const Tout t = s_tot[lane];
+    s_tot[lane] = wave_inclusive_scan(t) - t;
+  }
+  __syncthreads();
+  const Tout p = partials[blockIdx.x];
+#pragma unroll
+  for (int k = 0; k < kScanItems; ++k) {
+    const int64_t i = base + k * kScanThreads;
+    if (i < n) out[i] = p + s_tot[k * (kScanThreads / 64) + w] + incl[k] - v[k];
   }
 }
 
