@@ -30,6 +30,59 @@ constexpr double kLog2e = 1.4426950408889634074;
 __device__ __forceinline__ float neg_exp2(float x) { return __builtin_amdgcn_exp2f(-x); }
 __device__ __forceinline__ double neg_exp2(double x) { return exp2(-x); }
 
+// The per-element alpha test -- sigma >= 0 and |w| exp(-sigma) >= thr, with
+// sl = sigma log2(e) -- as one unsigned compare of sl's bit pattern.
+// Non-negative values order like their patterns, and every negative value
+// (and -0, -inf, a negative NaN) has a larger pattern than any non-negative
+// one, so with sl* = log2(|w| / thr) >= 0:
+//   sl in [+0, sl*]  <=>  bits(sl) < bits(sl*) + 1.
+// Limits by record:
+//   * |w| < thr: 0, nothing passes (|alpha| <= |w| for sigma >= 0);
+//   * non-finite geometry or a NaN w: the sign bit, so every sl >= +0, +inf
+//     and a positive NaN pass -- their alpha is 0 or non-finite, which the
+//     reference does not skip either -- and sl < 0 fails, as there.
+// It differs from testing exp(-sigma) against thr / |w| only for elements
+// whose alpha is within a few ulp of thr.
+template <typename T>
+struct Bits;
+template <>
+struct Bits<float> {
+  using type = uint32_t;
+  static constexpr uint32_t kSign = 0x80000000u;
+};
+template <>
+struct Bits<double> {
+  using type = uint64_t;
+  static constexpr uint64_t kSign = 0x8000000000000000ull;
+};
+
+__device__ __forceinline__ uint32_t bits_of(float x) { return __float_as_uint(x); }
+__device__ __forceinline__ uint64_t bits_of(double x) {
+  return static_cast<uint64_t>(__double_as_longlong(x));
+}
+
+template <typename T>
+__device__ __forceinline__ typename Bits<T>::type alpha_limit(T w, bool finite_geometry,
+                                                              double thr) {
+  const T aw = fabs(w);
+  if (aw != aw || !finite_geometry) return Bits<T>::kSign;
+  if (!(aw >= static_cast<T>(thr))) return 0;
+  // log2(|w| / thr) >= 0 (+inf for an infinite w).
+  const T sl_max = fmax(log2(aw) - static_cast<T>(log2(thr)), static_cast<T>(0));
+  return bits_of(sl_max) + 1;
+}
+
+template <typename T>
+__device__ __forceinline__ bool alpha_pass(T sl, typename Bits<T>::type limit) {
+  return bits_of(sl) < limit;
+}
+
+// Bits of a limit kept in a T slot (forward records stage it in LDS).
+__device__ __forceinline__ float limit_as_value(uint32_t b) { return __uint_as_float(b); }
+__device__ __forceinline__ double limit_as_value(uint64_t b) {
+  return __longlong_as_double(static_cast<long long>(b));
+}
+
 // Keys of the records of a wave: `rb` is the wave's first record (uniform),
 // `r` the lane's; the key of record r is the last k with offsets[k] <= r
 // (offsets[0] = 0, non-decreasing).  One uniform binary search for rb, then a

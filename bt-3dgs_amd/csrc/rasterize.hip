@@ -116,16 +116,17 @@ __global__ __launch_bounds__(1024) void raster_fwd_kernel(
 // pixels of one row per lane, and taking every kFwdWaves-th record of each
 // LDS batch.  A record's row terms (dy, b dy, c dy^2) are shared by the R
 // pixels; sigma log2(e) = (h_a dx + h_b dy) dx + h_c dy^2 with pre-scaled
-// coefficients, and the alpha test |o mu e| >= 1e-5 is e >= 1e-5 / |o mu|
-// with the bound staged per record, so a pixel costs two FMAs, one
-// v_exp_f32, two compares, a select and the accumulating FMA.  The waves'
+// coefficients, and the alpha test (sigma >= 0, |o mu e| >= 1e-5) is one
+// unsigned compare of sl's bits against a limit staged per record
+// (alpha_limit), so a pixel costs two FMAs, one v_exp_f32, one compare, a
+// select and the accumulating FMA.  The waves'
 // partial images are summed in a fixed order at the end, so the result is
 // deterministic (the per-pixel order differs from a plain list-order sum
 // only by rounding).
 constexpr int kFwdWaves = 8;
 constexpr int kFwdBatch = 64 * kFwdWaves;
 
-// One staged forward record: {x, y, h_a, h_b} and {h_c, o mu, e bound, 0}.
+// One staged forward record: {x, y, h_a, h_b} and {h_c, o mu, limit bits, 0}.
 template <typename T>
 struct FwdRecord {
   typename Vec<T>::v4 p, q;
@@ -171,7 +172,6 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
   const T half = static_cast<T>(0.5);
   const T py = static_cast<T>(static_cast<int>(ty) * TS + ly) + half;
   const T px0 = static_cast<T>(static_cast<int>(tx) * TS + lx0) + half;
-  const T thr = static_cast<T>(kThr2);
   const T l = static_cast<T>(kLog2e), hl = static_cast<T>(0.5 * kLog2e);
 
   const int64_t t0 = tile_offsets[key];
@@ -196,14 +196,14 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
         p.w = l * conics[3 * g + 1];
         q.x = hl * conics[3 * g + 2];
         q.y = opac[g] * mus[g];
-        // |o mu e| < 1e-5 tested as e < 1e-5 / |o mu| (equal up to the
-        // rounding of the cut-off itself); NaN o mu gives a NaN bound, which
-        // no e is below, as no NaN alpha is below 1e-5.
-        q.z = thr / fabs(q.y);
+        // The alpha test's limit on the bits of sl (alpha_limit), kept in q.z.
+        const bool fin = isfinite(p.x) && isfinite(p.y) && isfinite(p.z) && isfinite(p.w) &&
+                         isfinite(q.x);
+        q.z = limit_as_value(alpha_limit(q.y, fin, kThr2));
       } else {  // never passes
         p.x = p.y = p.z = p.w = 0;
         q.x = q.y = 0;
-        q.z = static_cast<T>(INFINITY);
+        q.z = limit_as_value(static_cast<typename Bits<T>::type>(0));
       }
       q.w = 0;
       s_rec[tid] = rec;
@@ -213,6 +213,7 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
     for (int j = wave; j < cnt; j += kFwdWaves) {
       const V4 p = s_rec[j].p;
       const V4 q = s_rec[j].q;
+      const typename Bits<T>::type lim = bits_of(q.z);
       const T dy = py - p.y;
       const T B = p.w * dy, C = q.x * dy * dy;
 #pragma unroll
@@ -220,8 +221,7 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
         const T dx = (px0 + static_cast<T>(k)) - p.x;
         const T sl = (p.z * dx + B) * dx + C;
         const T e = neg_exp2(sl);
-        const bool skip = (sl < static_cast<T>(0)) || (e < q.z);
-        acc[k] = fma(q.y, skip ? static_cast<T>(0) : e, acc[k]);
+        acc[k] = fma(q.y, alpha_pass(sl, lim) ? e : static_cast<T>(0), acc[k]);
       }
     }
   }
@@ -265,7 +265,7 @@ struct RasterRecord {
   bool live;          // a valid record whose pixels can pass the alpha test
   T mx, my, a, b, c, o, mu, om;
   T ha, hb, hc;       // a/2, b, c/2 pre-scaled by log2(e)
-  T elo;              // 1e-5 / |o mu|: the alpha test |o mu e| >= 1e-5 as e >= elo
+  typename Bits<T>::type lim;  // the alpha test on the bits of sl (alpha_limit)
   int i0, i1;         // rows the alpha-test ellipse reaches (all rows when not PD)
   bool pd;            // conic positive definite and finite (sigma finite, >= 0 up to rounding)
 };
@@ -284,7 +284,7 @@ __device__ __forceinline__ void load_raster_record(
   if (!rec.live) {
     rec.o = rec.mu = rec.om = 0;
     rec.mx = rec.my = rec.a = rec.b = rec.c = rec.ha = rec.hb = rec.hc = 0;
-    rec.elo = static_cast<T>(INFINITY);
+    rec.lim = 0;
     rec.i0 = 0;
     rec.i1 = -1;
     rec.pd = true;
@@ -298,7 +298,9 @@ __device__ __forceinline__ void load_raster_record(
   rec.ha = static_cast<T>(0.5 * kLog2e) * rec.a;
   rec.hb = static_cast<T>(kLog2e) * rec.b;
   rec.hc = static_cast<T>(0.5 * kLog2e) * rec.c;
-  rec.elo = static_cast<T>(kThr2) / fabs(rec.om);
+  rec.lim = alpha_limit(rec.om, isfinite(rec.mx) && isfinite(rec.my) && isfinite(rec.a) &&
+                                   isfinite(rec.b) && isfinite(rec.c),
+                        kThr2);
   const Cull2<T> cu = cull2_setup(rec.a, rec.b, rec.c, fabs(rec.om), kThr2);
   rec.pd = cu.ok;
   rec.i0 = oy;
@@ -310,8 +312,9 @@ __device__ __forceinline__ void load_raster_record(
 // s2 = sum w dx^2 over the row's passing pixels (w = v exp(-sigma)), and
 // px, py = sums of |w (P d)_x|, |w (P d)_y|.  vv holds the row's upstream
 // gradient (zero beyond the image).  kGuard: also exclude columns k >= nx
-// explicitly -- needed only for records whose sigma may be -inf or NaN, for
-// which v = 0 would not make w = 0.
+// explicitly -- needed only for records whose sigma may be NaN (non-finite
+// geometry passes the alpha test there), for which v = 0 would not make
+// w = 0.
 template <typename T, int R, bool kExact, bool kAbs, bool kGuard>
 __device__ __forceinline__ void raster_row(const RasterRecord<T> &rec, const T (&vv)[R], int k0,
                                            T dx0, int nx, int nts, T B, T C, T bdy, T cdy,
@@ -323,9 +326,7 @@ __device__ __forceinline__ void raster_row(const RasterRecord<T> &rec, const T (
     const T dx = dx0 + static_cast<T>(k);
     const T sl = (rec.ha * dx + B) * dx + C;
     const T e = neg_exp2(sl);
-    // |o mu e| < 1e-5 tested as e < 1e-5 / |o mu| (equal up to the rounding
-    // of the cut-off itself).
-    bool skip = (sl < static_cast<T>(0)) || (e < rec.elo);
+    bool skip = !alpha_pass(sl, rec.lim);
     if (kGuard) skip = skip || k >= nx;
     const T w = skip ? static_cast<T>(0) : vv[kk] * e;
     s0 += w;
@@ -344,7 +345,7 @@ __device__ __forceinline__ void raster_row(const RasterRecord<T> &rec, const T (
 // row, so they are kept in registers, and the column sums W_k = sum over
 // rows of w accumulate per column: T0, T1, T2 then follow from W_k once per
 // record, which leaves three accumulations per pixel (W_k, s0, s1) instead
-// of four.  Rows outside the record's reach test against an infinite cut-off
+// of four.  Rows outside the record's reach test against a zero limit
 // (every pixel fails), so the upstream gradient is loaded without masks.
 template <typename T, int R, bool kAbs>
 __device__ __forceinline__ void raster_tile_full(const RasterRecord<T> &rec,
@@ -368,7 +369,7 @@ __device__ __forceinline__ void raster_tile_full(const RasterRecord<T> &rec,
     const T dy = (static_cast<T>(i) + half) - rec.my;
     const T B = rec.hb * dy, C = rec.hc * dy * dy;
     const T bdy = rec.b * dy, cdy = rec.c * dy;
-    const T elo = in_row ? rec.elo : static_cast<T>(INFINITY);
+    const typename Bits<T>::type lim = in_row ? rec.lim : 0;
     const T *__restrict__ vrow = vimg + static_cast<int64_t>(in_row ? i : oy) * W + ox;
     T s0 = 0, s1 = 0, px = 0, py = 0;
 #pragma unroll
@@ -385,8 +386,7 @@ __device__ __forceinline__ void raster_tile_full(const RasterRecord<T> &rec,
         const T dx = dxk[h + kk];
         const T sl = fma(fma(rec.ha, dx, B), dx, C);
         const T e = neg_exp2(sl);
-        const bool skip = (sl < static_cast<T>(0)) || (e < elo);
-        const T w = skip ? static_cast<T>(0) : vv[kk] * e;
+        const T w = alpha_pass(sl, lim) ? vv[kk] * e : static_cast<T>(0);
         wk[h + kk] += w;
         s0 += w;
         s1 = fma(w, dx, s1);

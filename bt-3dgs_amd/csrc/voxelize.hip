@@ -93,7 +93,7 @@ __global__ __launch_bounds__(1024) void voxel_fwd_kernel(
   extern __shared__ double smem_raw[];
   const uint32_t nt = blockDim.x;
   const uint32_t nb = min(nt, kFwdBatch);  // records staged per batch
-  // Per staged record: {mx, my, mz, o}, {h0, h1, h2, h3}, {h4, h5, e bound, 0}.
+  // Per staged record: {mx, my, mz, o}, {h0, h1, h2, h3}, {h4, h5, limit bits, 0}.
   V4 *s_rec = reinterpret_cast<V4 *>(smem_raw);
 
   const uint32_t key = xcd_swizzle(blockIdx.x, n_keys);
@@ -110,7 +110,6 @@ __global__ __launch_bounds__(1024) void voxel_fwd_kernel(
 
   const int64_t start = tile_offsets[key];
   const int64_t end = (key == n_keys - 1) ? n_isects : static_cast<int64_t>(tile_offsets[key + 1]);
-  const T thr = static_cast<T>(kThr3);
   T acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0;
@@ -135,14 +134,16 @@ __global__ __launch_bounds__(1024) void voxel_fwd_kernel(
         h0.w = h[3];
         h1.x = h[4];
         h1.y = h[5];
-        // |o e| < 1e-6 tested as e < 1e-6 / |o| (equal up to the rounding of
-        // the cut-off itself; a NaN o gives a NaN bound that no e is below).
-        h1.z = thr / fabs(mo.w);
+        // The alpha test's limit on the bits of sl (alpha_limit), kept in h1.z.
+        bool fin = isfinite(mo.x) && isfinite(mo.y) && isfinite(mo.z);
+#pragma unroll
+        for (int c = 0; c < 6; ++c) fin = fin && isfinite(h[c]);
+        h1.z = limit_as_value(alpha_limit(mo.w, fin, kThr3));
       } else {  // never passes
         mo.x = mo.y = mo.z = mo.w = 0;
         h0.x = h0.y = h0.z = h0.w = 0;
         h1.x = h1.y = 0;
-        h1.z = static_cast<T>(INFINITY);
+        h1.z = limit_as_value(static_cast<typename Bits<T>::type>(0));
       }
       h1.w = 0;
       s_rec[3 * tid] = mo;
@@ -155,6 +156,7 @@ __global__ __launch_bounds__(1024) void voxel_fwd_kernel(
       const V4 mo = s_rec[3 * t];
       const V4 h0 = s_rec[3 * t + 1];
       const V4 h1 = s_rec[3 * t + 2];
+      const typename Bits<T>::type lim = bits_of(h1.z);
       const T dy = py - mo.y, dz = pz - mo.z;
       const T B = h0.y * dy + h0.z * dz;
       const T C = (h0.w * dy + h1.x * dz) * dy + h1.y * dz * dz;
@@ -163,8 +165,7 @@ __global__ __launch_bounds__(1024) void voxel_fwd_kernel(
         const T dx = (px0 + static_cast<T>(r)) - mo.x;
         const T sl = (h0.x * dx + B) * dx + C;
         const T e = neg_exp2(sl);
-        const bool skip = (sl < static_cast<T>(0)) || (e < h1.z);
-        acc[r] = fma(mo.w, skip ? static_cast<T>(0) : e, acc[r]);
+        acc[r] = fma(mo.w, alpha_pass(sl, lim) ? e : static_cast<T>(0), acc[r]);
       }
     }
   }
@@ -182,7 +183,7 @@ template <typename T>
 struct BwdRecord {
   bool live;     // a valid record whose voxels can pass the alpha test
   T m[3], q[6], h[6], o;
-  T elo;         // 1e-6 / |o|: the alpha test |o e| >= 1e-6 as e >= elo
+  typename Bits<T>::type lim;  // the alpha test on the bits of sl (alpha_limit)
   Cull3<T> cu;
   int i0, i1;    // slice range (all slices when !cu.ok)
 };
@@ -196,10 +197,9 @@ __device__ __forceinline__ void load_bwd_record(const T *__restrict__ means3d,
   rec.o = rec.live ? opac[g] : static_cast<T>(0);
   // |alpha| <= |o| for sigma >= 0: nothing passes (non-finite o stays live).
   if (fabs(rec.o) < static_cast<T>(kThr3)) rec.live = false;
-  rec.elo = static_cast<T>(kThr3) / fabs(rec.o);
   if (!rec.live) {
     rec.o = 0;
-    rec.elo = static_cast<T>(INFINITY);
+    rec.lim = 0;
 #pragma unroll
     for (int c = 0; c < 3; ++c) rec.m[c] = 0;
 #pragma unroll
@@ -214,6 +214,12 @@ __device__ __forceinline__ void load_bwd_record(const T *__restrict__ means3d,
 #pragma unroll
   for (int c = 0; c < 6; ++c) rec.q[c] = conics[6 * g + c];
   scaled_conic(rec.q, rec.h);
+  bool fin = true;
+#pragma unroll
+  for (int c = 0; c < 3; ++c) fin = fin && isfinite(rec.m[c]);
+#pragma unroll
+  for (int c = 0; c < 6; ++c) fin = fin && isfinite(rec.h[c]);
+  rec.lim = alpha_limit(rec.o, fin, kThr3);
   rec.cu = cull3_setup(rec.q, fabs(rec.o), kThr3);
   rec.i0 = b.oi;
   rec.i1 = b.oi + b.ni - 1;
@@ -226,7 +232,8 @@ __device__ __forceinline__ void load_bwd_record(const T *__restrict__ means3d,
 // s2 = sum w dx^2 over the row's passing voxels (w = v exp(-sigma)).  vv
 // holds the row's upstream gradient (zero beyond the volume).  kGuard: also
 // exclude columns k >= nk explicitly -- needed only for records whose sigma
-// may be -inf or NaN, for which v = 0 would not make w = 0.
+// may be NaN (non-finite geometry passes the alpha test there), for which
+// v = 0 would not make w = 0.
 template <typename T, int R, bool kExact, bool kGuard>
 __device__ __forceinline__ void voxel_row(const BwdRecord<T> &rec, const T (&vv)[R], T dx0,
                                           int nk, int nts, T B, T C, T &s0, T &s1, T &s2) {
@@ -236,9 +243,7 @@ __device__ __forceinline__ void voxel_row(const BwdRecord<T> &rec, const T (&vv)
     const T dx = dx0 + static_cast<T>(k);
     const T sl = (rec.h[0] * dx + B) * dx + C;
     const T e = neg_exp2(sl);
-    // |o e| < 1e-6 tested as e < 1e-6 / |o| (equal up to the rounding of the
-    // cut-off itself).
-    bool skip = (sl < static_cast<T>(0)) || (e < rec.elo);
+    bool skip = !alpha_pass(sl, rec.lim);
     if (kGuard) skip = skip || k >= nk;
     const T w = skip ? static_cast<T>(0) : vv[k] * e;
     s0 += w;
@@ -270,7 +275,7 @@ __device__ __forceinline__ void slice_rows(const BwdRecord<T> &rec, const Brick 
 // every row and the column sums W_k = sum over rows of w accumulate per
 // column, so T0, T1, T2 follow from W_k once per record and each voxel adds
 // three sums (W_k, s0, s1) instead of four.  Rows the record does not reach
-// test against an infinite cut-off (every voxel fails), so the upstream
+// test against a zero limit (every voxel fails), so the upstream
 // gradient is loaded without masks.
 template <typename T, int R>
 __device__ __forceinline__ void voxel_brick_full(const BwdRecord<T> &rec, const Brick &b,
@@ -304,7 +309,7 @@ __device__ __forceinline__ void voxel_brick_full(const BwdRecord<T> &rec, const 
       const T dy = (static_cast<T>(j) + half) - rec.m[1];
       const T B = fma(rec.h[1], dy, Bz);
       const T C = fma(fma(rec.h[3], dy, h4dz), dy, h5dzz);
-      const T elo = in_row ? rec.elo : static_cast<T>(INFINITY);
+      const typename Bits<T>::type lim = in_row ? rec.lim : 0;
       const T *__restrict__ vrow = vslice + static_cast<int64_t>(j) * D2;
       T vv[R];
 #pragma unroll
@@ -318,8 +323,7 @@ __device__ __forceinline__ void voxel_brick_full(const BwdRecord<T> &rec, const 
         const T dx = dxk[k];
         const T sl = fma(fma(rec.h[0], dx, B), dx, C);
         const T e = neg_exp2(sl);
-        const bool skip = (sl < static_cast<T>(0)) || (e < elo);
-        const T w = skip ? static_cast<T>(0) : vv[k] * e;
+        const T w = alpha_pass(sl, lim) ? vv[k] * e : static_cast<T>(0);
         wk[k] += w;
         s0 += w;
         s1 = fma(w, dx, s1);
@@ -390,6 +394,8 @@ __global__ __launch_bounds__(kBwdThreads) void voxel_bwd_kernel(
   if (full && ballot(rec.live) != 0) {
     voxel_brick_full<T, R>(rec, b, v_vol, plane, D2, dx0, T0, T1, T2, Y0, Z0, Y1, Z1, YY, YZ, ZZ);
   } else if (ballot(rec.live) != 0) {
+    // Rolled loops: unrolled, the slices and rows multiply the registers.
+#pragma unroll 1
     for (int li = 0; li < R; ++li) {
       if (!kExact && li >= nts) break;
       const int i = b.oi + li;
@@ -400,6 +406,7 @@ __global__ __launch_bounds__(kBwdThreads) void voxel_bwd_kernel(
       int j0, j1;
       slice_rows(rec, b, in_slice, dz, j0, j1);
       const T h4dz = rec.h[4] * dz, h5dzz = rec.h[5] * dz * dz, Bz = rec.h[2] * dz;
+#pragma unroll 1
       for (int lj = 0; lj < R; ++lj) {
         if (!kExact && lj >= nts) break;
         const int j = b.oj + lj;
