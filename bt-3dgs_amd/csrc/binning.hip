@@ -340,13 +340,17 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     const int64_t i = first + r * 64 + lane;
     const bool valid = i < n;
     const uint32_t d = (key[r] >> shift) & mask;
-    // Lanes holding the same digit: intersect the ballots of every digit bit.
-    uint64_t peers = ballot(valid);
+    // Lanes holding the same digit: those whose bits agree with the lane's in
+    // every ballot.  Per bit, ballot ^ (the lane's bit copied to all 64)
+    // marks the lanes that differ there; the union over the bits is the
+    // complement of the peers.
+    uint64_t differ = 0;
     for (uint32_t b = 0; b < bits; ++b) {
-      const bool bit = (d >> b) & 1u;
-      const uint64_t bal = ballot(bit);
-      peers &= bit ? bal : ~bal;
+      const uint32_t x = static_cast<uint32_t>(__builtin_amdgcn_sbfe(static_cast<int32_t>(d), b, 1));
+      const uint64_t m = ballot(x != 0u);  // x: 0 or all ones
+      differ |= m ^ ((static_cast<uint64_t>(x) << 32) | x);
     }
+    const uint64_t peers = ballot(valid) & ~differ;
     uint32_t c = 0;
     if (valid) c = cnt[w][d];
     rank[r] = c + static_cast<uint32_t>(__popcll(peers & lt));
