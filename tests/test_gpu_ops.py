@@ -321,6 +321,57 @@ def test_rasterize_fwd_bwd(dtype, shape, order):
     assert no_abs[0] is None
 
 
+@pytest.mark.parametrize("order", ["emission", "tile"])
+def test_nan_opacity_propagates_as_in_the_reference(order):
+    # A NaN alpha is not below the cut-off, so the reference does not skip it:
+    # the pixels / voxels of a NaN-opacity Gaussian's tiles turn NaN, and so do
+    # that Gaussian's gradients that carry its opacity.  The NaN patterns must
+    # match the oracle's exactly, the finite values within tolerance.
+    d, m2, con, mu, op, ids, fl, off = _raster_case(3000, 17, 64, 64, 16, 1, torch.float32)
+    g = int(fl[fl.numel() // 2])
+    op = op.clone()
+    op[0, g] = float("nan")
+    img = W.rasterize_to_pixels_fwd(m2, con, op, mu, off, fl, 64, 64, 16)
+    img_o = native.raster_fwd(np32(m2), np32(con), np32(op), np32(mu), np32(off), np32(fl),
+                              64, 64, 16)
+    assert np.isnan(img_o).any() and not np.isnan(img_o).all()
+    assert_close(np32(img), img_o, "image", max_outliers=img_o.size // 1000,
+                 outlier_atol=3e-5)
+    v = torch.randn(img.shape, generator=d["gen"])
+    ref = native.raster_bwd(np32(m2), np32(con), np32(op), np32(mu), np32(off), np32(fl),
+                            v.numpy(), 64, 64, 16, True)
+    fl_run = fl if order == "emission" else fl.clone()
+    got = W.rasterize_to_pixels_bwd_per_gaussian(m2, con, op, mu, off, ids, fl_run, v.to(DEV),
+                                                 64, 64, 16, True)
+    for a, e, n in zip(got, ref, ("v_means2d_abs", "v_means2d", "v_conics", "v_opacities",
+                                  "v_mus")):
+        fin = e[np.isfinite(e)]
+        scale = float(np.abs(fin).max()) + 1e-30
+        assert_close(np32(a), e, n, atol=max(1e-5, 3e-6 * scale), max_outliers=e.size // 500,
+                     outlier_atol=2e-4 * scale)
+    assert np.isnan(ref[1]).any()
+    d3, m3, con3, ids3, fl3, off3 = _voxel_case(2500, 18, (32, 32, 32), 8)
+    g3 = int(fl3[fl3.numel() // 2])
+    op3 = d3["opac"].clone()
+    op3[g3] = float("nan")
+    vol = W.voxelize_to_voxels_fwd(m3, con3, op3, off3, fl3, 32, 32, 32, 8)
+    vol_o = native.voxel_fwd(np32(m3), np32(con3), np32(op3), np32(off3), np32(fl3), 32, 32, 32, 8)
+    assert np.isnan(vol_o).any() and not np.isnan(vol_o).all()
+    assert_close(np32(vol), vol_o, "volume", max_outliers=vol_o.size // 1000, outlier_atol=3e-6)
+    v3 = torch.randn(vol.shape, generator=d3["gen"])
+    ref3 = native.voxel_bwd(np32(m3), np32(con3), np32(op3), np32(off3), np32(fl3), v3.numpy(),
+                            32, 32, 32, 8)
+    fl3_run = fl3 if order == "emission" else fl3.clone()
+    got3 = W.voxelize_to_voxels_bwd_per_gaussian(m3, con3, op3, off3, ids3, fl3_run, v3.to(DEV),
+                                                 32, 32, 32, 8)
+    for a, e, n in zip(got3, ref3, ("v_means3d", "v_conics", "v_opacities")):
+        fin = e[np.isfinite(e)]
+        scale = float(np.abs(fin).max()) + 1e-30
+        assert_close(np32(a), e, n, atol=max(1e-5, 3e-6 * scale), max_outliers=e.size // 500,
+                     outlier_atol=2e-4 * scale)
+    assert np.isnan(ref3[0]).any()
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
 @pytest.mark.parametrize("shape", [(32, 32, 16), (48, 40, 8)])
 def test_rasterize_fwd_splits_heavy_tiles(dtype, shape):
