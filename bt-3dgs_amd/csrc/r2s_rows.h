@@ -127,14 +127,23 @@ __device__ __forceinline__ void zero_id_ranges(int64_t lo, int64_t hi, const Row
   }
 }
 
-// Rounds of 64 rows per wave: the rows of all rounds are loaded up front,
-// and a Gaussian crossing from one round into the next carries its sum in
-// registers; only one crossing the wave's last row gathers rows of the next
-// wave.
-constexpr int kReduceRounds = 4;
-constexpr int kReduceWaveRows = 64 * kReduceRounds;
+// Rows per wave of the reduction: 64 lanes x 4 consecutive rows.
+constexpr int kReduceRowsPerLane = 4;
+constexpr int kReduceWaveRows = 64 * kReduceRowsPerLane;
 
-// One wave per kReduceWaveRows consecutive rows (emission order).  Each
+// LDS slot of wave-row q (0..255) in the transposed staging: lane l reads
+// rows 4l .. 4l+3 from slots k*64 + ((l + 8k) mod 64), and lane l of load
+// round r writes row 64r + l; with the rotation by 8k both the writes and
+// the reads of each half-wave hit 32 different banks.
+__device__ __forceinline__ uint32_t reduce_slot(uint32_t q) {
+  return (q & 3u) * 64u + (((q >> 2) + 8u * (q & 3u)) & 63u);
+}
+
+// One wave per kReduceWaveRows consecutive rows (emission order), read with
+// coalesced loads and transposed through LDS so that each lane holds four
+// consecutive rows.  A lane sums the runs of equal ids among its rows in
+// registers; one segmented suffix sum over the lanes (keyed by the id of
+// each lane's first row) then completes the runs that cross lanes.  Each
 // Gaussian is written by the wave holding its first row: a Gaussian
 // continuing past the wave's last row has its remaining rows gathered by
 // this wave (64 ids at a time); a Gaussian that started in an earlier wave
@@ -149,87 +158,136 @@ __global__ __launch_bounds__(256) void row_reduce_kernel(const T *__restrict__ r
                                                          const int32_t *__restrict__ emit_ids,
                                                          int64_t n, int64_t n_items,
                                                          RowTargets<T, NV> tg) {
-  constexpr int R = kReduceRounds;
-  const int64_t eb = (static_cast<int64_t>(blockIdx.x) * 4 + wave_index()) * kReduceWaveRows;
-  if (eb >= n) return;  // uniform per wave
-  const uint32_t lane = lane_id();
+  constexpr int K = kReduceRowsPerLane;
+  __shared__ T s_val[4][NV][kReduceWaveRows];
+  __shared__ int32_t s_seg[4][kReduceWaveRows];
+  const uint32_t w = wave_index(), lane = lane_id();
+  const int64_t eb = (static_cast<int64_t>(blockIdx.x) * 4 + w) * kReduceWaveRows;
+  if (eb >= n) return;  // uniform per wave; the waves share no barrier below
   // Segment id per row: the Gaussian, or a negative value unique to the row
   // slot for rows past the end (or with an id out of range).
-  int32_t seg[R];
-  T v[R][NV];
+  {
+    int32_t sr[K];
+    T vr[K][NV];
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int64_t e = eb + r * 64 + lane;
-    const bool in = e < n;
-    const int64_t g = in ? static_cast<int64_t>(emit_ids[e]) : -1;
-    seg[r] = (g >= 0 && g < n_items) ? static_cast<int32_t>(g)
-                                     : -1 - static_cast<int32_t>(r * 64 + lane);
-    load_row(rows, in ? e : 0, v[r]);
-    if (!in) {
+    for (int r = 0; r < K; ++r) {
+      const uint32_t q = 64u * r + lane;
+      const int64_t e = eb + q;
+      const bool in = e < n;
+      const int64_t g = in ? static_cast<int64_t>(emit_ids[e]) : -1;
+      sr[r] = (g >= 0 && g < n_items) ? static_cast<int32_t>(g) : -1 - static_cast<int32_t>(q);
+      load_row(rows, in ? e : 0, vr[r]);
+      if (!in) {
 #pragma unroll
-      for (int c = 0; c < NV; ++c) v[r][c] = 0;
+        for (int c = 0; c < NV; ++c) vr[r][c] = 0;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < K; ++r) {
+      const uint32_t slot = reduce_slot(64u * r + lane);
+      s_seg[w][slot] = sr[r];
+#pragma unroll
+      for (int c = 0; c < NV; ++c) s_val[w][c][slot] = vr[r][c];
     }
   }
-  const int32_t before = (eb > 0) ? emit_ids[eb - 1] : -1;
-  const int32_t seg_first = __shfl(seg[0], 0, 64);
-  const int32_t seg_last = __shfl(seg[R - 1], 63, 64);
-  // Rows of the last segment beyond this wave (uniform branch and loop).
-  T carry[NV];
+  // The wave's LDS operations complete in order, so its own lanes' writes
+  // are visible to the reads below; keep the compiler from moving them.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  int32_t g[K];
+  T v[K][NV];
 #pragma unroll
-  for (int c = 0; c < NV; ++c) carry[c] = 0;
-  int32_t carry_seg = -1 - kReduceWaveRows;  // matches no row slot
+  for (int k = 0; k < K; ++k) {
+    const uint32_t slot = reduce_slot(K * lane + k);
+    g[k] = s_seg[w][slot];
+#pragma unroll
+    for (int c = 0; c < NV; ++c) v[k][c] = s_val[w][c][slot];
+  }
+  const int32_t before = (eb > 0) ? emit_ids[eb - 1] : -1;
+  const int32_t seg_first = __shfl(g[0], 0, 64);
+  const int32_t seg_last = __shfl(g[K - 1], 63, 64);
+  // In-lane run sums, last row first: acc[k] = rows k .. the end of k's run
+  // among the lane's rows.
+  T acc[K][NV];
+#pragma unroll
+  for (int c = 0; c < NV; ++c) acc[K - 1][c] = v[K - 1][c];
+#pragma unroll
+  for (int k = K - 2; k >= 0; --k) {
+    const bool same = g[k + 1] == g[k];
+#pragma unroll
+    for (int c = 0; c < NV; ++c) acc[k][c] = v[k][c] + (same ? acc[k + 1][c] : static_cast<T>(0));
+  }
+  // Rows of the last segment beyond this wave (uniform branch and loop),
+  // added to that segment's runs in lane 63.
   const bool tail_owned = seg_last >= 0 && !(seg_first == seg_last && before == seg_last);
   const int64_t past = eb + kReduceWaveRows;
   if (tail_owned && past < n && emit_ids[past] == seg_last) {
+    T carry[NV];
+#pragma unroll
+    for (int c = 0; c < NV; ++c) carry[c] = 0;
     for (int64_t base = past; base < n; base += 64) {
       const int64_t e2 = base + lane;
       const bool take = e2 < n && emit_ids[e2] == seg_last;
       if (take) {
-        T w[NV];
-        load_row(rows, e2, w);
+        T wv[NV];
+        load_row(rows, e2, wv);
 #pragma unroll
-        for (int c = 0; c < NV; ++c) carry[c] += w[c];
+        for (int c = 0; c < NV; ++c) carry[c] += wv[c];
       }
       if (!(base + 63 < n && __shfl(static_cast<int>(take), 63, 64))) break;
     }
 #pragma unroll
     for (int c = 0; c < NV; ++c) carry[c] = wave_sum(carry[c]);
-    carry_seg = seg_last;
-  }
-  // Rounds last to first: each round's suffix sums plus the carry of the
-  // segment continuing into the next round; the sum at lane 0 carries on.
-  const bool last_wave = past >= n;
+    if (lane == 63) {
 #pragma unroll
-  for (int r = R - 1; r >= 0; --r) {
-    const WaveSegments segs(seg[r]);
-    T x[NV];
+      for (int k = 0; k < K; ++k) {
+        if (g[k] == seg_last) {
 #pragma unroll
-    for (int c = 0; c < NV; ++c) {
-      x[c] = segs.suffix_sum(v[r][c]);
-      if (seg[r] == carry_seg) x[c] += carry[c];
+          for (int c = 0; c < NV; ++c) acc[k][c] += carry[c];
+        }
+      }
     }
-    const int32_t seg_prev = __shfl_up(seg[r], 1, 64);
-    const int32_t prev_last = r > 0 ? __shfl(seg[r > 0 ? r - 1 : 0], 63, 64) : before;
-    const int32_t p = lane == 0 ? prev_last : seg_prev;
-    // First row of each Gaussian, unless it began in an earlier wave.
-    const bool head = seg[r] >= 0 && p != seg[r];
+  }
+  // Runs crossing lanes: the suffix sums of each lane's first run over the
+  // following lanes with the same first id (a lane whose first run does not
+  // fill it ends the segment there, as ids ascend).
+  const WaveSegments segs(g[0]);
+  T lead[NV], next[NV];
 #pragma unroll
-    for (int c = 0; c < NV; ++c) carry[c] = __shfl(x[c], 0, 64);
-    carry_seg = __shfl(seg[r], 0, 64);
+  for (int c = 0; c < NV; ++c) {
+    lead[c] = segs.suffix_sum(acc[0][c]);
+    next[c] = __shfl_down(lead[c], 1, 64);
+  }
+  // Shuffles with every lane active (a source lane must take part).
+  const int32_t next_first_all = __shfl_down(g[0], 1, 64);
+  const int32_t next_first = lane < 63 ? next_first_all : -1;
+  const int32_t prev_last = __shfl_up(g[K - 1], 1, 64);
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int32_t p = k > 0 ? g[k - 1] : (lane == 0 ? before : prev_last);
+    const bool head = g[k] >= 0 && p != g[k];
+    // The Gaussian's total: its run in this lane, and, when that run reaches
+    // the lane's end, the following lanes' share.
+    T tot[NV];
+    const bool onward = g[K - 1] == g[k] && next_first == g[k];
+#pragma unroll
+    for (int c = 0; c < NV; ++c)
+      tot[c] = k == 0 ? lead[c] : acc[k][c] + (onward ? next[c] : static_cast<T>(0));
     // Ids without records before this Gaussian's id.
     int64_t z_lo = 0, z_hi = 0;
     if (head) {
       z_lo = static_cast<int64_t>(p) + 1;
-      z_hi = seg[r];
+      z_hi = g[k];
     }
     zero_id_ranges(z_lo, z_hi, tg);
     if (head) {
-      const int64_t g = seg[r];
+      const int64_t gi = g[k];
 #pragma unroll
-      for (int c = 0; c < NV; ++c) tg.ptr[c][g * tg.stride[c]] = x[c];
+      for (int c = 0; c < NV; ++c) tg.ptr[c][gi * tg.stride[c]] = tot[c];
     }
   }
-  if (last_wave) {  // uniform: this wave holds the last record
+  if (past >= n) {  // uniform: this wave holds the last record
     const int64_t last = emit_ids[n - 1];
     const bool take = lane == 0 && last >= 0 && last < n_items;
     zero_id_ranges<T, NV>(take ? last + 1 : 0, take ? n_items : 0, tg);
