@@ -102,29 +102,11 @@ struct RowTargets {
   int stride[NV];
 };
 
-// Zeroes ids [lo, hi) of every target: each lane its first kOwnZeros ids
-// itself (gaps are mostly short), the rest of long ranges one lane's range
-// after another, all 64 lanes storing consecutive ids.
-constexpr int kOwnZeros = 8;
-
+// Zeroes every target over ids [0, n_items): blockIdx.y is the column.
 template <typename T, int NV>
-__device__ __forceinline__ void zero_id_ranges(int64_t lo, int64_t hi, const RowTargets<T, NV> &tg) {
-  const int64_t own = min(hi, lo + kOwnZeros);
-  for (int64_t k = lo; k < own; ++k) {
-#pragma unroll
-    for (int c = 0; c < NV; ++c) tg.ptr[c][k * tg.stride[c]] = static_cast<T>(0);
-  }
-  lo = own > lo ? own : lo;
-  uint64_t pending = ballot(hi > lo);
-  while (pending != 0) {
-    const uint32_t src = static_cast<uint32_t>(__builtin_ctzll(pending));
-    pending &= pending - 1;
-    const int64_t a = readlane_i64(lo, src), b = readlane_i64(hi, src);
-    for (int64_t k = a + lane_id(); k < b; k += 64) {
-#pragma unroll
-      for (int c = 0; c < NV; ++c) tg.ptr[c][k * tg.stride[c]] = static_cast<T>(0);
-    }
-  }
+__global__ __launch_bounds__(256) void zero_targets_kernel(RowTargets<T, NV> tg, int64_t n_items) {
+  const int64_t k = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (k < n_items) tg.ptr[blockIdx.y][k * tg.stride[blockIdx.y]] = static_cast<T>(0);
 }
 
 // Rows per wave of the reduction: 64 lanes x 4 consecutive rows.
@@ -148,11 +130,9 @@ __device__ __forceinline__ uint32_t reduce_slot(uint32_t q) {
 // continuing past the wave's last row has its remaining rows gathered by
 // this wave (64 ids at a time); a Gaussian that started in an earlier wave
 // is skipped.  Plain stores, no atomics, and the per-Gaussian summation
-// order is fixed.  Emission order is ascending in the id, so the ids
-// strictly between two consecutive records' ids have no records: the first
-// row of each Gaussian zeroes the ids between it and the previous record,
-// and the wave holding the last record zeroes the ids after it.  Every
-// output is written; none needs zeroing beforehand.
+// order is fixed.  launch_row_reduce zeroes the targets first, so ids
+// without records (more than half of them at a heavily culled view) read
+// zero.
 template <typename T, int NV>
 __global__ __launch_bounds__(256) void row_reduce_kernel(const T *__restrict__ rows,
                                                          const int32_t *__restrict__ emit_ids,
@@ -274,29 +254,22 @@ __global__ __launch_bounds__(256) void row_reduce_kernel(const T *__restrict__ r
 #pragma unroll
     for (int c = 0; c < NV; ++c)
       tot[c] = k == 0 ? lead[c] : acc[k][c] + (onward ? next[c] : static_cast<T>(0));
-    // Ids without records before this Gaussian's id.
-    int64_t z_lo = 0, z_hi = 0;
-    if (head) {
-      z_lo = static_cast<int64_t>(p) + 1;
-      z_hi = g[k];
-    }
-    zero_id_ranges(z_lo, z_hi, tg);
     if (head) {
       const int64_t gi = g[k];
 #pragma unroll
       for (int c = 0; c < NV; ++c) tg.ptr[c][gi * tg.stride[c]] = tot[c];
     }
   }
-  if (past >= n) {  // uniform: this wave holds the last record
-    const int64_t last = emit_ids[n - 1];
-    const bool take = lane == 0 && last >= 0 && last < n_items;
-    zero_id_ranges<T, NV>(take ? last + 1 : 0, take ? n_items : 0, tg);
-  }
 }
 
+// Stores every target: zeros, then each Gaussian's sum over its rows.
 template <typename T, int NV>
 void launch_row_reduce(const T *rows, const int32_t *emit_ids, int64_t n, int64_t n_items,
                        const RowTargets<T, NV> &tg, hipStream_t stream) {
+  if (n_items <= 0) return;
+  zero_targets_kernel<T, NV><<<dim3(static_cast<uint32_t>(ceil_div(n_items, 256)), NV), dim3(256),
+                               0, stream>>>(tg, n_items);
+  if (n <= 0) return;
   row_reduce_kernel<T, NV><<<dim3(static_cast<uint32_t>(ceil_div(n, 4 * kReduceWaveRows))),
                              dim3(256), 0, stream>>>(rows, emit_ids, n, n_items, tg);
 }

@@ -654,8 +654,9 @@ int raster_reduce_impl(const T *rows, const int32_t *emit_ids, int64_t n_isects,
   const char *name = "rasterize_to_pixels_bwd (row reduction)";
   R2S_REQUIRE(C >= 0 && N >= 0 && C * N <= kInt32Max && n_isects >= 0 && n_isects <= kInt32Max,
               "%s: bad size", name);
-  if (C * N == 0 || n_isects == 0) return R2S_OK;
-  R2S_REQUIRE(rows && emit_ids && v_xy && v_conic && v_opac && v_mu, "%s: null pointer", name);
+  if (C * N == 0) return R2S_OK;
+  R2S_REQUIRE(v_xy && v_conic && v_opac && v_mu, "%s: null output", name);
+  R2S_REQUIRE(n_isects == 0 || (rows && emit_ids), "%s: null pointer", name);
   R2S_REQUIRE(reinterpret_cast<uintptr_t>(rows) % 16 == 0, "%s: rows not 16-byte aligned", name);
   hipStream_t stream = as_stream(st);
   if (v_xy_abs != nullptr) {
@@ -687,7 +688,12 @@ int raster_bwd_impl(const T *means2d, const T *conics, const T *opac, const T *m
                      : isect_ids ? "rasterize_to_pixels_bwd_per_gaussian"
                                  : "rasterize_to_pixels_bwd";
   R2S_RETURN_IF(check_raster_args(n_isects, C, N, W, H, ts, tw, th, name));
-  if (C * N == 0 || n_isects == 0) return R2S_OK;
+  if (C * N == 0) return R2S_OK;
+  if (n_isects == 0) {  // the two-pass form still stores its (zero) outputs
+    if (!two_pass || rows_only) return R2S_OK;
+    return raster_reduce_impl<T>(nullptr, nullptr, 0, C, N, v_xy_abs, v_xy, v_conic, v_opac,
+                                 v_mu, st);
+  }
   R2S_REQUIRE(tile_offsets && flatten_ids, "%s: null tile lists", name);
   R2S_REQUIRE(means2d && conics && opac && mus && v_image, "%s: null pointer", name);
   R2S_REQUIRE(rows_only || (v_xy && v_conic && v_opac && v_mu), "%s: null output", name);

@@ -560,8 +560,9 @@ int voxel_reduce_impl(const T *rows, const int32_t *emit_ids, int64_t n_isects, 
   const char *name = "voxelize_to_voxels_bwd (row reduction)";
   R2S_REQUIRE(N >= 0 && N <= kInt32Max && n_isects >= 0 && n_isects <= kInt32Max,
               "%s: bad size", name);
-  if (N == 0 || n_isects == 0) return R2S_OK;
-  R2S_REQUIRE(rows && emit_ids && v_means && v_conics && v_opac, "%s: null pointer", name);
+  if (N == 0) return R2S_OK;
+  R2S_REQUIRE(v_means && v_conics && v_opac, "%s: null output", name);
+  R2S_REQUIRE(n_isects == 0 || (rows && emit_ids), "%s: null pointer", name);
   R2S_REQUIRE(reinterpret_cast<uintptr_t>(rows) % 16 == 0, "%s: rows not 16-byte aligned", name);
   RowTargets<T, 10> tg = {{v_means, v_means + 1, v_means + 2, v_conics, v_conics + 1,
                            v_conics + 2, v_conics + 3, v_conics + 4, v_conics + 5, v_opac},
@@ -585,9 +586,12 @@ int voxel_bwd_impl(const T *means3d, const T *conics, const T *opac,
                      : isect_ids ? "voxelize_to_voxels_bwd_per_gaussian"
                                  : "voxelize_to_voxels_bwd";
   R2S_RETURN_IF(check_voxel_args(n_isects, N, D2, D1, D0, ts, n2, n1, n0, name));
-  if (N == 0 || n_isects == 0) return R2S_OK;
+  if (N == 0) return R2S_OK;
   const int64_t n_vox = static_cast<int64_t>(D2) * D1 * D0;
-  if (n_vox == 0) return R2S_OK;
+  if (n_isects == 0 || n_vox == 0) {  // the two-pass form still stores its (zero) outputs
+    if (!two_pass || rows_only) return R2S_OK;
+    return voxel_reduce_impl<T>(nullptr, nullptr, 0, N, v_means, v_conics, v_opac, st);
+  }
   R2S_REQUIRE(tile_offsets && flatten_ids, "%s: null brick lists", name);
   R2S_REQUIRE(means3d && conics && opac && v_vol, "%s: null pointer", name);
   R2S_REQUIRE(rows_only || (v_means && v_conics && v_opac), "%s: null output", name);

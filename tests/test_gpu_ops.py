@@ -515,6 +515,11 @@ def test_row_reduction_stores_every_id(seed):
     got = torch.cat([v_xy, v_con, v_op, v_mu, v_abs], 1)
     assert torch.equal(got, want[:, :9])
     assert int(emit_ids[0]) > 0 and int(emit_ids[-1]) < N - 1
+    # No records at all: every output is still stored (zeros).
+    for t in outs:
+        t.fill_(float("nan"))
+    assert lib.r2s_rasterize_bwd_reduce_f32(None, None, 0, 1, N, *[P(t) for t in outs], st) == 0
+    assert all(int(torch.count_nonzero(t)) == 0 for t in outs)
 
 
 def test_backward_stage_entry_points_match_the_two_pass_op():
