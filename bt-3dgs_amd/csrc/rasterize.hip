@@ -111,16 +111,17 @@ __global__ __launch_bounds__(1024) void raster_fwd_kernel(
   if (inside) image[static_cast<int64_t>(cam) * H * W + static_cast<int64_t>(i) * W + j] = acc;
 }
 
-// Forward for tile sizes 8, 16 and 32: kFwdWaves waves per (view, tile),
-// each covering all TS^2 pixels of the tile with R = TS^2 / 64 consecutive
-// pixels of one row per lane, and taking every kFwdWaves-th record of each
-// LDS batch.  A record's row terms (dy, b dy, c dy^2) are shared by the R
-// pixels; sigma log2(e) = (h_a dx + h_b dy) dx + h_c dy^2 with pre-scaled
-// coefficients, and the alpha test (sigma >= 0, |o mu e| >= 1e-5) is one
-// unsigned compare of sl's bits against a limit staged per record
-// (alpha_limit), so a pixel costs two FMAs, one v_exp_f32, one compare, a
-// select and the accumulating FMA.  The waves'
-// partial images are summed in a fixed order at the end, so the result is
+// Forward for tile sizes 8, 16 and 32: kFwdWaves waves per (view, tile).
+// A lane covers R = min(TS, 16) consecutive pixels of one tile row, so a
+// record's row terms (dy, b dy, c dy^2) are computed once for R pixels; the
+// TS^2 / R lanes covering the tile for one record form a group, and the
+// 64 / (TS^2 / R) groups of a wave take different records of each LDS batch
+// (4 per wave at TS = 16).  sigma log2(e) = (h_a dx + h_b dy) dx + h_c dy^2
+// with pre-scaled coefficients, and the alpha test (sigma >= 0,
+// |o mu e| >= 1e-5) is one unsigned compare of sl's bits against a limit
+// staged per record (alpha_limit), so a pixel costs two FMAs, one
+// v_exp_f32, one compare, a select and the accumulating FMA.  The groups'
+// partial tiles are summed in a fixed order at the end, so the result is
 // deterministic (the per-pixel order differs from a plain list-order sum
 // only by rounding).
 constexpr int kFwdWaves = 8;
@@ -154,11 +155,14 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
     T *__restrict__ partial) {
   using V2 = typename Vec<T>::v2;
   using V4 = typename Vec<T>::v4;
-  constexpr int R = TS * TS / 64;   // pixels per lane
-  constexpr int LPR = TS / R;       // lanes per tile row
-  static_assert(R * 64 == TS * TS && LPR * R == TS, "unsupported tile size");
+  constexpr int R = TS < 16 ? TS : 16;  // pixels per lane (a tile row, at most 16)
+  constexpr int NL = TS * TS / R;        // lanes covering the tile for one record
+  constexpr int G = 64 / NL;             // records in flight per wave
+  constexpr int LPR = TS / R;            // lanes per tile row
+  constexpr int NP = kFwdWaves * G;      // partial tiles per block
+  static_assert(G * NL == 64 && LPR * R == TS, "unsupported tile size");
   __shared__ FwdRecord<T> s_rec[kFwdBatch];
-  __shared__ T s_part[kFwdWaves][TS * TS];
+  __shared__ T s_part[NP][TS * TS];
 
   // The splits of one tile are consecutive logical blocks (same XCD).
   const uint32_t lb = xcd_swizzle(blockIdx.x, gridDim.x);
@@ -168,7 +172,8 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
   const uint32_t ty = t / tw, tx = t - ty * tw;
   const int tid = static_cast<int>(threadIdx.x);
   const int wave = static_cast<int>(wave_index()), lane = static_cast<int>(lane_id());
-  const int ly = lane / LPR, lx0 = (lane % LPR) * R;
+  const int slot = wave * G + lane / NL, gl = lane % NL;
+  const int ly = gl / LPR, lx0 = (gl % LPR) * R;
   const T half = static_cast<T>(0.5);
   const T py = static_cast<T>(static_cast<int>(ty) * TS + ly) + half;
   const T px0 = static_cast<T>(static_cast<int>(tx) * TS + lx0) + half;
@@ -210,7 +215,7 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
     }
     __syncthreads();
     const int cnt = static_cast<int>(min(static_cast<int64_t>(kFwdBatch), end - base));
-    for (int j = wave; j < cnt; j += kFwdWaves) {
+    for (int j = slot; j < cnt; j += NP) {
       const V4 p = s_rec[j].p;
       const V4 q = s_rec[j].q;
       const typename Bits<T>::type lim = bits_of(q.z);
@@ -226,12 +231,12 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
     }
   }
 #pragma unroll
-  for (int k = 0; k < R; ++k) s_part[wave][ly * TS + lx0 + k] = acc[k];
+  for (int k = 0; k < R; ++k) s_part[slot][ly * TS + lx0 + k] = acc[k];
   __syncthreads();
   for (int pix = tid; pix < TS * TS; pix += kFwdBatch) {
     T sum = s_part[0][pix];
 #pragma unroll
-    for (int w = 1; w < kFwdWaves; ++w) sum += s_part[w][pix];
+    for (int w = 1; w < NP; ++w) sum += s_part[w][pix];
     if (splits > 1) {
       partial[(static_cast<int64_t>(key) * splits + split) * (TS * TS) + pix] = sum;
       continue;

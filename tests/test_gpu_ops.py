@@ -284,7 +284,7 @@ def _raster_case(n, seed, W_img, H_img, ts, n_views=1, dtype=torch.float32, log_
 @pytest.mark.parametrize("order", ["emission", "tile"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
 @pytest.mark.parametrize("shape", [(64, 64, 16), (70, 45, 16), (40, 40, 8), (50, 38, 12),
-                                   (66, 40, 20)])
+                                   (66, 40, 20), (96, 72, 32)])
 def test_rasterize_fwd_bwd(dtype, shape, order):
     W_img, H_img, ts = shape
     d, m2, con, mu, op, ids, fl, off = _raster_case(3000, 7, W_img, H_img, ts, 2, dtype)
