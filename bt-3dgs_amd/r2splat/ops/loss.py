@@ -34,23 +34,77 @@ __all__ = ["projection_losses", "ssim2d", "compute_tv_loss", "compute_edge_loss"
            "compute_hierarchy_loss", "LossComputer", "BinaryTreeLossComputer"]
 
 
+_ZERO = {}
+
+
+def _zero(device) -> Tensor:
+    """A cached float32 zero scalar (never returned to callers)."""
+    z = _ZERO.get(device)
+    if z is None:
+        z = _ZERO[device] = torch.zeros((), dtype=torch.float32, device=device)
+    return z
+
+
+def _grad_vector(grads, device) -> Tensor:
+    """The upstream gradients of several scalar outputs as one float32 vector
+    (zero for outputs that received none): one launch."""
+    return torch.stack([_zero(device) if g is None else g.reshape(()).to(torch.float32)
+                        for g in grads])
+
+
 class _ProjectionLoss(torch.autograd.Function):
+    """(l1, 1 - ssim, edge) as three outputs of one launch; the backward is
+    one launch for any combination of their upstream gradients."""
+
     @staticmethod
     def forward(ctx, render, target, edge_target, edge_mask, window_size):
         losses, ws = W.projection_loss_fwd(render, target, edge_target, edge_mask, window_size)
         ctx.save_for_backward(render, target, edge_target, edge_mask, ws)
         ctx.window_size = window_size
-        return losses
+        return losses[0], losses[1], losses[2]
 
     @staticmethod
-    def backward(ctx, grad):
+    def backward(ctx, g_l1, g_ssim, g_edge):
         if any(ctx.needs_input_grad[1:4]):
             raise NotImplementedError("gradients w.r.t. targets, edge targets or edge masks "
                                       "are not provided")
         render, target, edge_target, edge_mask, ws = ctx.saved_tensors
-        g = W.projection_loss_bwd(render, target, edge_target, edge_mask,
-                                  grad.to(torch.float32).contiguous(), ws, ctx.window_size)
+        scales = _grad_vector((g_l1, g_ssim, g_edge), render.device)
+        g = W.projection_loss_bwd(render, target, edge_target, edge_mask, scales, ws,
+                                  ctx.window_size)
         return g, None, None, None, None
+
+
+_WEIGHTS = {}
+
+
+class _WeightedTotal(torch.autograd.Function):
+    """sum_i w_i t_i over scalar terms in two launches; the backward hands
+    each term w_i g from one launch (the weighted sums of loss.py:90-101 and
+    166-171, without a graph node per product and sum)."""
+
+    @staticmethod
+    def forward(ctx, weights, *terms):
+        ctx.save_for_backward(weights)
+        ctx.dtypes = [t.dtype for t in terms]
+        return torch.dot(_grad_vector(terms, weights.device), weights)
+
+    @staticmethod
+    def backward(ctx, grad):
+        (weights,) = ctx.saved_tensors
+        parts = (weights * grad.to(torch.float32)).unbind(0)
+        return (None,) + tuple(p.to(dt) for p, dt in zip(parts, ctx.dtypes))
+
+
+def _weighted_total(pairs, device) -> Tensor:
+    """Weighted sum of (weight, scalar term) pairs, in one graph node."""
+    key = (device, tuple(float(w) for w, _ in pairs))
+    w = _WEIGHTS.get(key)
+    if w is None:
+        w = _WEIGHTS[key] = torch.tensor(key[1], dtype=torch.float32, device=device)
+    terms = [t if isinstance(t, Tensor) else torch.as_tensor(t, dtype=torch.float32,
+                                                             device=device) for _, t in pairs]
+    return _WeightedTotal.apply(w, *terms)
 
 
 def _planes(t: Tensor) -> Tensor:
@@ -84,9 +138,10 @@ def projection_losses(renders: Tensor, targets: Tensor, edge_mask: Optional[Tens
             raise ValueError("edge_mask and edge_targets must broadcast to the renders' shape")
         e = _planes(_as_float(et.detach()).expand(renders.shape))
         m = _planes(_as_float(edge_mask.detach()).expand(renders.shape))
-    losses = _ProjectionLoss.apply(r, t, e, m, int(ssim_window))
-    edge = losses[2] if edge_mask is not None else torch.zeros((), device=renders.device)
-    return losses[0], losses[1], edge
+    l1, ssim_loss, edge = _ProjectionLoss.apply(r, t, e, m, int(ssim_window))
+    if edge_mask is None:
+        edge = torch.zeros((), device=renders.device)
+    return l1, ssim_loss, edge
 
 
 def ssim2d(img1: Tensor, img2: Tensor, window_size: int = 11) -> Tensor:
@@ -177,7 +232,8 @@ class LossComputer:
         out["proj_l1"] = l1
         out["proj_ssim"] = ssim_loss
         out["vol_tv"] = _tv_term(self.w_tv, volume_pred, renders.device)
-        out["total"] = self.w_l1 * l1 + self.w_ssim * ssim_loss + self.w_tv * out["vol_tv"]
+        out["total"] = _weighted_total(((self.w_l1, l1), (self.w_ssim, ssim_loss),
+                                        (self.w_tv, out["vol_tv"])), renders.device)
         return out
 
 
@@ -212,9 +268,10 @@ class BinaryTreeLossComputer:
             hierarchy_loss = torch.zeros((), device=renders.device)
         out["hierarchy"] = hierarchy_loss
         edge_weight = self.w_edge if edge_weight_override is None else float(edge_weight_override)
-        out["edge_weight"] = torch.tensor(edge_weight, device=renders.device)
-        out["total"] = (self.w_l1 * l1 + self.w_ssim * ssim_loss + self.w_tv * out["vol_tv"]
-                        + edge_weight * edge_loss + self.w_hierarchy * hierarchy_loss)
+        out["edge_weight"] = torch.full((), edge_weight, device=renders.device)
+        out["total"] = _weighted_total(((self.w_l1, l1), (self.w_ssim, ssim_loss),
+                                        (self.w_tv, out["vol_tv"]), (edge_weight, edge_loss),
+                                        (self.w_hierarchy, hierarchy_loss)), renders.device)
         return out
 
 

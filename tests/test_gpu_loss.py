@@ -76,7 +76,7 @@ def test_binary_tree_loss_computer_matches_the_oracle_total():
                                      w_hierarchy=0.05, ssim_window=11)
     r = _t(x).requires_grad_(True)
     v = torch.from_numpy(vol)[None].to(DEV).requires_grad_(True)
-    hier = torch.tensor(0.3, device=DEV)
+    hier = torch.tensor(0.3, device=DEV, requires_grad=True)
     out = comp(r, _t(y), _t(m), v, hierarchy_loss=hier, edge_targets=_t(e),
                edge_weight_override=0.7)
     assert set(out) == {"proj_l1", "proj_ssim", "vol_tv", "edge", "hierarchy", "edge_weight",
@@ -89,6 +89,16 @@ def test_binary_tree_loss_computer_matches_the_oracle_total():
     gx = L.projection_loss_grad(x, y, e, m, (1.0, 0.25, 0.7))
     assert np.abs(np32(r.grad)[..., 0] - gx).max() < 2e-3 * np.abs(gx).max()
     np.testing.assert_allclose(np32(v.grad)[0], L.tv_grad(vol, 0.05), rtol=1e-6, atol=1e-12)
+    assert abs(hier.grad.item() - 0.05) < 1e-8
+    assert out["edge_weight"].item() == np.float32(0.7)
+    # Each term stays differentiable on its own (the SSIM term alone here).
+    r2 = _t(x).requires_grad_(True)
+    comp(r2, _t(y), _t(m), None, edge_targets=_t(e))["proj_ssim"].backward()
+    gs = L.projection_loss_grad(x, y, e, m, (0.0, 1.0, 0.0))
+    assert np.abs(np32(r2.grad)[..., 0] - gs).max() < 2e-3 * np.abs(gs).max()
+    # A plain-number hierarchy term, as the reference's arithmetic accepts.
+    num = comp(_t(x), _t(y), _t(m), None, hierarchy_loss=0.3, edge_targets=_t(e))
+    assert abs(num["total"].item() - (el1 + 0.25 * esl + 0.5 * eed + 0.05 * 0.3)) < 2e-5
     plain = LO.LossComputer(w_l1=1.0, w_ssim=0.25, w_tv=0.0)(_t(x), _t(y))
     assert set(plain) == {"proj_l1", "proj_ssim", "vol_tv", "total"}
     assert plain["vol_tv"].item() == 0.0
