@@ -626,6 +626,173 @@ def vox_bytes(n, i3, v):
     return 144 * n + 156 * i3 + 8 * v
 
 
+def _tile_bound(v, upper):
+    # IsectTilesKernel.cu:30-40: non-finite or <= 0 -> 0, >= upper -> upper, else truncate.
+    v = torch.where(torch.isfinite(v) & (v > 0), v, torch.zeros_like(v))
+    return torch.clamp(v, max=float(upper)).floor()
+
+
+def dense_cover_2d(means2d, radii, ts, h, w):
+    """[N, H, W] mask of the pixels in the tiles the binning lists for each
+    Gaussian (IsectTilesKernel.cu:57-113), for the dense formulation."""
+    tw, th = -(-w // ts), -(-h // ts)
+    rx, ry = radii[:, 0].float(), radii[:, 1].float()
+    mx, my = means2d[:, 0], means2d[:, 1]
+    ok = (rx > 0) & (ry > 0) & torch.isfinite(mx) & torch.isfinite(my)
+    x0 = _tile_bound(torch.floor(mx / ts - rx / ts), tw)
+    x1 = _tile_bound(torch.ceil(mx / ts + rx / ts), tw)
+    y0 = _tile_bound(torch.floor(my / ts - ry / ts), th)
+    y1 = _tile_bound(torch.ceil(my / ts + ry / ts), th)
+    tj = (torch.arange(w) // ts).float()
+    ti = (torch.arange(h) // ts).float()
+    cx = (tj[None] >= x0[:, None]) & (tj[None] < x1[:, None])
+    cy = (ti[None] >= y0[:, None]) & (ti[None] < y1[:, None])
+    return ok[:, None, None] & cy[:, :, None] & cx[:, None, :]
+
+
+def dense_cover_3d(means3d, radii, ts, d):
+    """[N, D, D, D] mask of the voxels in the bricks the 3D binning lists
+    (IsectTiles3DKernel.cu:49-104)."""
+    n = -(-d // ts)
+    ok = (radii > 0).all(-1)
+    lo, hi = [], []
+    for a in range(3):
+        c, r = means3d[:, a] / ts, radii[:, a].float() / ts
+        lo.append(_tile_bound(torch.floor(c - r), n))
+        hi.append(_tile_bound(torch.ceil(c + r), n))
+    t = (torch.arange(d) // ts).float()
+    cx = (t[None] >= lo[0][:, None]) & (t[None] < hi[0][:, None])
+    cy = (t[None] >= lo[1][:, None]) & (t[None] < hi[1][:, None])
+    cz = (t[None] >= lo[2][:, None]) & (t[None] < hi[2][:, None])
+    return ok[:, None, None, None] & cz[:, :, None, None] & cy[:, None, :, None] & \
+        cx[:, None, None, :]
+
+
+def dense_raster(means2d, conics, om, cover):
+    """The reference's dense line-integral image (tests/test_cuda_gaussian_ops.py:200-215
+    semantics), masked by the tile cover: [N] Gaussians -> [H, W]."""
+    h, w = cover.shape[1:]
+    py, px = torch.meshgrid(torch.arange(h, dtype=means2d.dtype) + 0.5,
+                            torch.arange(w, dtype=means2d.dtype) + 0.5, indexing="ij")
+    dx = px[None] - means2d[:, 0, None, None]
+    dy = py[None] - means2d[:, 1, None, None]
+    sigma = (0.5 * conics[:, 0, None, None] * dx.square() + conics[:, 1, None, None] * dx * dy
+             + 0.5 * conics[:, 2, None, None] * dy.square())
+    alpha = om[:, None, None] * torch.exp(-sigma)
+    keep = cover & (sigma >= 0) & (alpha.abs() >= 1e-5)
+    return torch.where(keep, alpha, torch.zeros_like(alpha)).sum(0)
+
+
+def dense_voxel(means3d, conics, opac, cover):
+    """The reference's dense volume (tests/test_cuda_gaussian_ops.py:218-238 semantics),
+    masked by the brick cover: [N] Gaussians -> [D, D, D]."""
+    d = cover.shape[1]
+    pz, py, px = torch.meshgrid(*(torch.arange(d, dtype=means3d.dtype) + 0.5,) * 3,
+                                indexing="ij")
+    dx = px[None] - means3d[:, 0, None, None, None]
+    dy = py[None] - means3d[:, 1, None, None, None]
+    dz = pz[None] - means3d[:, 2, None, None, None]
+    q = [conics[:, i, None, None, None] for i in range(6)]
+    sigma = (0.5 * q[0] * dx.square() + q[1] * dx * dy + q[2] * dx * dz
+             + 0.5 * q[3] * dy.square() + q[4] * dy * dz + 0.5 * q[5] * dz.square())
+    alpha = opac[:, None, None, None] * torch.exp(-sigma)
+    keep = cover & (sigma >= 0) & (alpha.abs() >= 1e-6)
+    return torch.where(keep, alpha, torch.zeros_like(alpha)).sum(0)
+
+
+def config1(dev, steps, warmup, chunk=256):
+    """Config 1 like for like: 4,096 Gaussians (means U[-1,1]^3, log-scales
+    N(-4, 0.5), densities U[0,1]), one cone-beam view at an angle drawn from
+    the same generator, a 64^2 detector and a 64^3 voxelization over
+    [-1,1]^3, fwd+bwd against N(0,1) upstream gradients.  The GPU runs the
+    whole path (prepare, projection, binning, rasterize, voxelize, explicit
+    backward).  The CPU runs the reference's dense PyTorch formulation of the
+    rasterize and voxelize sums (masked by the tile / brick cover, as the
+    kernels evaluate) with torch autograd for their backward, on the host's
+    torch threads; the O(N) preprocessing is taken from the GPU run, so the
+    CPU figure covers the O(N P) part only.  Both results are compared."""
+    from r2splat import geometry, scenes
+    from r2splat.ops import explicit
+
+    g = torch.Generator().manual_seed(0)
+    raw = scenes.random_gaussians(4096, g, -4.0, 0.5)
+    angle = float(torch.rand(1, generator=g)) * 2.0 * math.pi
+    vm, Ks = geometry.cone_beam_views([angle], 64)
+    v_image = torch.randn(1, 64, 64, generator=g)
+    v_volume = torch.randn(64, 64, 64, generator=g)
+    params = [t.clone().to(dev).requires_grad_(True) for t in
+              (raw.means, raw.quats, raw.raw_scales, raw.raw_opacities)]
+    vm, Ks, vi, vv = vm.to(dev), Ks.to(dev), v_image.to(dev), v_volume.to(dev)
+    ranges = torch.full((3,), 2.0, device=dev)
+    centers = torch.zeros(3, device=dev)
+
+    def gpu_call():
+        means, quats, scales, opac = params
+        for p in params:
+            p.grad = None
+        st = explicit.prepare_explicit_gaussians(quats, scales, opac, scale_min=SMIN,
+                                                 scale_max=SMAX)
+        res = explicit.explicit_rasterize(st, means, vm, Ks, img_w=64, img_h=64, tile_size=16,
+                                          eps2d=EPS, radius_clip=3.0, absgrad=True)
+        vox = explicit.explicit_voxelize(st, means, ranges, centers, dim2=64, dim1=64, dim0=64,
+                                         tile_size=8, eps3d=EPS, radius_clip=3.0)
+        res.image.grad = vi
+        vox.volume.grad = vv
+        explicit.explicit_backward(st, means, quats, scales, opac)
+        return st, res, vox
+
+    t_gpu = time_steps(gpu_call, steps, warmup)
+    st, res, vox = gpu_call()
+    torch.cuda.synchronize()
+    pr, vx = st.projection, st.voxel
+    m2 = pr.means2d[0].detach().cpu()
+    con = pr.conics[0].detach().cpu()
+    om = (pr.opacity * pr.mus)[0].detach().cpu()
+    r2 = pr.radii[0].cpu()
+    m3, con3 = vx.means3d.detach().cpu(), vx.conics.detach().cpu()
+    op3, r3 = vx.opacity.detach().cpu(), vox.radii.cpu()
+
+    def cpu_raster():
+        a, b, c = (t.clone().requires_grad_(True) for t in (m2, con, om))
+        image = dense_raster(a, b, c, dense_cover_2d(a.detach(), r2, 16, 64, 64))
+        (image * v_image[0]).sum().backward()
+        return image.detach()
+
+    def cpu_voxel():
+        vol = torch.zeros(64, 64, 64)
+        for s0 in range(0, m3.shape[0], chunk):
+            x, y, z = (t[s0:s0 + chunk].clone().requires_grad_(True) for t in (m3, con3, op3))
+            part = dense_voxel(x, y, z, dense_cover_3d(x.detach(), r3[s0:s0 + chunk], 8, 64))
+            (part * v_volume).sum().backward()
+            vol += part.detach()
+        return vol
+
+    cpu_raster()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        image_cpu = cpu_raster()
+        times.append(time.perf_counter() - t0)
+    t_raster = sorted(times)[1]
+    t0 = time.perf_counter()
+    vol_cpu = cpu_voxel()  # one pass: about half a minute of CPU work
+    t_voxel = time.perf_counter() - t0
+    t_cpu = t_raster + t_voxel
+    d_img = float((image_cpu - res.image.detach()[0].cpu()).abs().max())
+    d_vol = float((vol_cpu - vox.volume.detach().cpu()).abs().max())
+    return {"workload": "config1: 4096 Gaussians, one view on 64^2 + 64^3 voxelization, "
+                        "fwd+bwd",
+            "gpu_ms_per_call": t_gpu * 1e3,
+            "cpu_dense_torch_ms_per_call": t_cpu * 1e3,
+            "cpu_threads": torch.get_num_threads(),
+            "cpu_raster_ms": t_raster * 1e3, "cpu_voxel_ms": t_voxel * 1e3,
+            "cpu_sample": "the rasterize sums with autograd backward (median of 3 after a "
+                          "warm-up) plus one pass of the voxelize sums (all 4096 Gaussians, "
+                          "in chunks of 256); preprocessing from the GPU run",
+            "gpu_speedup": t_cpu / t_gpu,
+            "image_max_abs_diff": d_img, "volume_max_abs_diff": d_vol}
+
+
 def cpu_baseline(proj: Projection, stride=1):
     """Oracle (numpy + sequential C, one core) projection fwd+bwd on a seeded
     random 1/``stride`` subset of the config-4 Gaussians (by default all of
@@ -855,6 +1022,13 @@ def main():
         torch.cuda.empty_cache()
 
     if not args.no_cpu_baseline:
+        log("config 1 like for like (GPU path vs the dense torch formulation on the host)")
+        result["config1"] = config1(dev, 20, 3)
+        c1 = result["config1"]
+        log(f"config1: GPU {c1['gpu_ms_per_call']:.3f} ms, CPU dense torch "
+            f"{c1['cpu_dense_torch_ms_per_call']:.1f} ms on {c1['cpu_threads']} threads, "
+            f"max |diff| image {c1['image_max_abs_diff']:.2e} volume "
+            f"{c1['volume_max_abs_diff']:.2e}")
         log("timing the CPU oracle baseline")
         cps, dt, sample = cpu_baseline(proj)
         result["cpu_baseline"] = {"value": cps, "unit": "proj fwd+bwd calls/s", "cores": 1,
