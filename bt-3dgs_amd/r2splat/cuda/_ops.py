@@ -12,6 +12,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import threading
 from typing import Optional, Tuple
 
 import torch
@@ -92,7 +93,7 @@ def _end_bit(n_keys: int) -> int:
 # relaunch.
 _COUNT_HISTORY = {}
 _COUNT_HISTORY_LEN = 8
-_PINNED_COUNT = {}
+_PINNED_COUNT = threading.local()  # per host thread: a count read back by one call at a time
 
 
 def _note_count(key, n: int) -> None:
@@ -122,9 +123,12 @@ def _emit_and_sort(launch, offsets: Tensor, n_items: int, n_keys: int, op: str,
         guess = max(recent)
         cap = min(guess + guess // 8 + 4096, 2 ** 31 - 1)
         outs, ws = alloc(cap)
-        host = _PINNED_COUNT.get(dev.index)
+        pinned = getattr(_PINNED_COUNT, "by_device", None)
+        if pinned is None:
+            pinned = _PINNED_COUNT.by_device = {}
+        host = pinned.get(dev.index)
         if host is None:
-            host = _PINNED_COUNT[dev.index] = torch.empty(1, dtype=torch.int64, pin_memory=True)
+            host = pinned[dev.index] = torch.empty(1, dtype=torch.int64, pin_memory=True)
         host.copy_(offsets[n_items:n_items + 1], non_blocking=True)
         ready = torch.cuda.Event()
         ready.record()
