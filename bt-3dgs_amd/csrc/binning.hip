@@ -24,6 +24,7 @@
 // reference's CUB sort of the same records.
 #pragma clang fp contract(off)
 
+#include <type_traits>
 #include <utility>
 
 #include "r2s_common.h"
@@ -242,7 +243,6 @@ constexpr int kSortWaveItems = 64 * kSortRounds;        // 1024
 constexpr int kSortTile = 4 * kSortWaveItems;           // 4096 items per block
 constexpr int kMaxPassBits = 11;                        // up to 2048 digits per pass
 constexpr int kMaxDigits = 1 << kMaxPassBits;
-constexpr int kDigitsPerThread = kMaxDigits / kSortThreads;  // 8
 
 // The sort kernels are sized for `cap` items and read the actual count n
 // from the device (the emission scan's total); with n > cap they write
@@ -285,7 +285,12 @@ __global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(const uint32_t
 // with kTwo, its emission index e.  kFirst: the input is the emission-order
 // array itself, so e is the input index and only keys and gids are read.
 // kFinal: writes keys_out64 / vals_out32 = gid / src_out = e.
-template <bool kFirst, bool kFinal, bool kTwo>
+// The LDS footprint follows the sort: digit tables for 2^kDBits digits,
+// keys staged as 16 bits when every key fits (kKey16), and in a single-pass
+// sort the emission index staged as its 16-bit block-local position.  At
+// config 4 (one 10-bit pass) and config 3 (two passes of 8 and 7 bits over
+// 15-bit keys) that leaves room for three blocks per CU instead of two.
+template <bool kFirst, bool kFinal, bool kTwo, int kDBits, bool kKey16>
 __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     const uint32_t *__restrict__ keys_in, const uint32_t *__restrict__ e_in,
     const uint32_t *__restrict__ gid_in, const int64_t *__restrict__ n_dev, int64_t cap,
@@ -294,15 +299,21 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     uint32_t *__restrict__ e_out, uint32_t *__restrict__ gid_out,
     int64_t *__restrict__ keys_out64, int32_t *__restrict__ vals_out32,
     int32_t *__restrict__ src_out) {
+  static_assert(kDBits >= 8 && kDBits <= kMaxPassBits, "digit tables of 256 to 2048");
+  constexpr int kD = 1 << kDBits;
+  constexpr int kDPT = kD / kSortThreads;  // digits per thread in the scan
+  constexpr bool kLocalE = kFirst && kFinal;
+  using KeyS = typename std::conditional<kKey16, uint16_t, uint32_t>::type;
+  using ES = typename std::conditional<kLocalE, uint16_t, uint32_t>::type;
   // Per-wave digit counters, then (in place) each wave's start within the
   // digit's block-local run; at most 1024 items per wave, so 16 bits hold them.
-  __shared__ uint16_t cnt[4][kMaxDigits];
-  __shared__ uint16_t dbase[kMaxDigits];  // block-local start of each digit (<= 4096)
-  __shared__ uint32_t gbase[kMaxDigits];  // global start of this block's run of each digit
+  __shared__ uint16_t cnt[4][kD];
+  __shared__ uint16_t dbase[kD];  // block-local start of each digit (<= 4096)
+  __shared__ uint32_t gbase[kD];  // global start of this block's run of each digit
   __shared__ uint32_t wsum[kSortThreads / 64];
-  __shared__ uint32_t s_key[kSortTile];
+  __shared__ KeyS s_key[kSortTile];
   __shared__ uint32_t s_gid[kSortTile];
-  __shared__ uint32_t s_e[kTwo ? kSortTile : 1];
+  __shared__ ES s_e[kTwo ? kSortTile : 1];
   const uint32_t digits = 1u << bits, mask = digits - 1u;
   const uint32_t tile = xcd_swizzle(blockIdx.x, nblocks);
   const int64_t n = *n_dev;
@@ -321,9 +332,9 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
   // not depend on the ranking, so they load here too.
   const uint32_t dk = (digits + kSortThreads - 1) / kSortThreads;
   const uint32_t d0 = threadIdx.x * dk;
-  uint32_t gb[kDigitsPerThread];
+  uint32_t gb[kDPT];
 #pragma unroll
-  for (uint32_t j = 0; j < kDigitsPerThread; ++j) {
+  for (uint32_t j = 0; j < kDPT; ++j) {
     const uint32_t d = min(d0 + j, digits - 1u);
     gb[j] = digit_offsets[static_cast<int64_t>(d) * nblocks + tile];
   }
@@ -363,10 +374,10 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     // Per owned digit the waves' starts and the block total, then an
     // exclusive scan of the totals over digits.
     const uint32_t k = dk;
-    uint32_t tot[kDigitsPerThread];
+    uint32_t tot[kDPT];
     uint32_t mine = 0;
 #pragma unroll
-    for (uint32_t j = 0; j < kDigitsPerThread; ++j) {
+    for (uint32_t j = 0; j < kDPT; ++j) {
       tot[j] = 0;
       const uint32_t d = d0 + j;
       if (j < k && d < digits) {
@@ -384,7 +395,7 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     uint32_t block_total;
     uint32_t run = block_exclusive_scan(mine, wsum, block_total);
 #pragma unroll
-    for (uint32_t j = 0; j < kDigitsPerThread; ++j) {
+    for (uint32_t j = 0; j < kDPT; ++j) {
       const uint32_t d = d0 + j;
       if (j < k && d < digits) {
         dbase[d] = static_cast<uint16_t>(run);
@@ -400,9 +411,9 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     if (i < n) {
       const uint32_t d = (key[r] >> shift) & mask;
       const uint32_t lp = dbase[d] + cnt[w][d] + rank[r];
-      s_key[lp] = key[r];
+      s_key[lp] = static_cast<KeyS>(key[r]);
       s_gid[lp] = gid[r];
-      if (kTwo) s_e[lp] = ev[r];
+      if (kTwo) s_e[lp] = static_cast<ES>(kLocalE ? ev[r] - block_first : ev[r]);
     }
   }
   __syncthreads();
@@ -414,7 +425,8 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     if (kFinal) {
       keys_out64[dest] = static_cast<int64_t>(k);
       vals_out32[dest] = static_cast<int32_t>(s_gid[lp]);
-      if (kTwo) src_out[dest] = static_cast<int32_t>(s_e[lp]);
+      if (kTwo)
+        src_out[dest] = static_cast<int32_t>(kLocalE ? block_first + s_e[lp] : s_e[lp]);
     } else {
       keys_out[dest] = k;
       gid_out[dest] = s_gid[lp];
@@ -503,6 +515,56 @@ inline uint32_t key_bits_for(int64_t n_keys) {
   return b;
 }
 
+// Launches the scatter instantiation for one pass: digit tables of 256,
+// 1024 (a single pass) or 2048 digits, 16-bit key staging when the keys fit.
+template <bool kFirst, bool kFinal, bool kTwo>
+int launch_scatter_sized(uint32_t bits, bool key16, const uint32_t *kin, const uint32_t *ein,
+                         const uint32_t *gin, const int64_t *n_dev, int64_t cap, uint32_t shift,
+                         const uint32_t *digit_offsets, uint32_t nb, uint32_t *kout,
+                         uint32_t *eout, uint32_t *gout, int64_t *keys64, int32_t *vals32,
+                         int32_t *src, hipStream_t stream) {
+#define R2S_SCATTER_SIZED(DB, K16)                                                              \
+  radix_scatter_kernel<kFirst, kFinal, kTwo, DB, K16><<<dim3(nb), dim3(kSortThreads), 0,      \
+                                                       stream>>>(                             \
+      kin, ein, gin, n_dev, cap, shift, bits, digit_offsets, nb, kout, eout, gout, keys64,     \
+      vals32, src)
+  if (bits <= 8 && key16)
+    R2S_SCATTER_SIZED(8, true);
+  else if (kFirst && kFinal && bits <= 10 && key16)
+    R2S_SCATTER_SIZED(10, true);
+  else
+    R2S_SCATTER_SIZED(kMaxPassBits, false);
+#undef R2S_SCATTER_SIZED
+  return check_launch("isect sort pass");
+}
+
+int launch_scatter(bool first, bool last, bool two, uint32_t bits, bool key16,
+                   const uint32_t *kin, const uint32_t *ein, const uint32_t *gin,
+                   const int64_t *n_dev, int64_t cap, uint32_t shift,
+                   const uint32_t *digit_offsets, uint32_t nb, uint32_t *kout, uint32_t *eout,
+                   uint32_t *gout, int64_t *keys64, int32_t *vals32, int32_t *src,
+                   hipStream_t stream) {
+#define R2S_SCATTER_PASS(F, L, T)                                                                \
+  return launch_scatter_sized<F, L, T>(bits, key16, kin, ein, gin, n_dev, cap, shift,           \
+                                       digit_offsets, nb, kout, eout, gout, keys64, vals32, src, \
+                                       stream)
+  if (first && last) {
+    if (two) R2S_SCATTER_PASS(true, true, true);
+    R2S_SCATTER_PASS(true, true, false);
+  }
+  if (first) {
+    if (two) R2S_SCATTER_PASS(true, false, true);
+    R2S_SCATTER_PASS(true, false, false);
+  }
+  if (last) {
+    if (two) R2S_SCATTER_PASS(false, true, true);
+    R2S_SCATTER_PASS(false, true, false);
+  }
+  if (two) R2S_SCATTER_PASS(false, false, true);
+  R2S_SCATTER_PASS(false, false, false);
+#undef R2S_SCATTER_PASS
+}
+
 // Sorts the emitted records (s.k0, s.gid0) into the final outputs: *n_dev
 // records, at most cap (the size s was carved for).  two: the emission
 // index travels too and the final pass writes it to src.
@@ -526,28 +588,9 @@ int radix_sort(SortSpace &s, const int64_t *n_dev, int64_t cap, uint32_t key_bit
     uint32_t *kout = (p % 2 == 0) ? s.k1 : s.k0;
     uint32_t *eout = (p % 2 == 0) ? s.e1 : s.e0;
     uint32_t *gout = (p % 2 == 0) ? s.g1 : s.g0;
-#define R2S_SCATTER(FIRST, FINAL, TWO)                                                         \
-  radix_scatter_kernel<FIRST, FINAL, TWO><<<dim3(nb), dim3(kSortThreads), 0, stream>>>(       \
-      kin, ein, gin, n_dev, cap, shift, bits, s.hist_scan, nb, kout, eout, gout, keys64, vals32, \
-      src)
-#define R2S_SCATTER_TWO(FIRST, FINAL) \
-  do {                                \
-    if (two)                          \
-      R2S_SCATTER(FIRST, FINAL, true); \
-    else                              \
-      R2S_SCATTER(FIRST, FINAL, false); \
-  } while (0)
-    if (first && last)
-      R2S_SCATTER_TWO(true, true);
-    else if (first)
-      R2S_SCATTER_TWO(true, false);
-    else if (last)
-      R2S_SCATTER_TWO(false, true);
-    else
-      R2S_SCATTER_TWO(false, false);
-#undef R2S_SCATTER_TWO
-#undef R2S_SCATTER
-    R2S_RETURN_IF(check_launch("isect sort pass"));
+    R2S_RETURN_IF(launch_scatter(first, last, two, bits, key_bits <= 16, kin, ein, gin, n_dev,
+                                 cap, shift, s.hist_scan, nb, kout, eout, gout, keys64, vals32,
+                                 src, stream));
     kin = kout;
     ein = eout;
     gin = gout;
