@@ -424,6 +424,96 @@ __device__ __forceinline__ void raster_tile_full(const RasterRecord<T> &rec,
   }
 }
 
+// Sums over one record's tile: T_k = sum w dx^k (k = 0, 1, 2), Y0 = sum w dy,
+// Y1 = sum w dx dy, YY = sum w dy^2; PX, PY = sums of the per-pixel absolute
+// mean gradients |w (P d)_x|, |w (P d)_y|.
+template <typename T>
+struct TileSums {
+  T T0, T1, T2, Y0, Y1, YY, PX, PY;
+};
+
+// The sums of one record (one lane) over its tile: the whole-tile form when
+// every tile of the wave lies inside the image, else row by row with masked
+// loads.  Wave-uniform branches only.
+template <typename T, int R, bool kExact, bool kAbs>
+__device__ __forceinline__ TileSums<T> raster_record_sums(const RasterRecord<T> &rec,
+                                                          const T *__restrict__ vimg, uint32_t W,
+                                                          int ox, int oy, int nx, int nts,
+                                                          bool vec, T dx0) {
+  const T half = static_cast<T>(0.5);
+  TileSums<T> s = {0, 0, 0, 0, 0, 0, 0, 0};
+  // Columns past the image matter only for records whose sigma may be
+  // non-finite (uniform over the wave).
+  const bool guard = ballot(rec.live && !rec.pd && nx < nts) != 0;
+  bool full = false;
+  if constexpr (kExact && R <= 16 && R % kChunk == 0) full = vec && ballot(nx < nts) == 0;
+  if (full && ballot(rec.live) != 0) {
+    raster_tile_full<T, R, kAbs>(rec, vimg, W, ox, oy, dx0, s.T0, s.T1, s.T2, s.Y0, s.Y1, s.YY,
+                                 s.PX, s.PY);
+  } else if (ballot(rec.live) != 0) {
+    for (int ly = 0; ly < R; ++ly) {
+      if (!kExact && ly >= nts) break;
+      const int i = oy + ly;
+      const bool in_row = rec.live && i >= rec.i0 && i <= rec.i1;
+      if (ballot(in_row) == 0) continue;
+      const T dy = (static_cast<T>(i) + half) - rec.my;
+      const T B = rec.hb * dy, C = rec.hc * dy * dy;
+      const T bdy = rec.b * dy, cdy = rec.c * dy;
+      const T *__restrict__ vrow = vimg + static_cast<int64_t>(in_row ? i : 0) * W + ox;
+      T s0 = 0, s1 = 0, s2 = 0, px = 0, py = 0;
+      constexpr int CH = R < kChunk ? R : kChunk;
+#pragma unroll 1
+      for (int k0 = 0; k0 < R; k0 += CH) {
+        if (!kExact && k0 >= nts) break;
+        T vv[CH];
+        if (vec)
+          load_grad_row<T, CH, true>(vrow + k0, in_row, nx - k0, nts - k0, vv);
+        else
+          load_grad_row<T, CH, false>(vrow + k0, in_row, nx - k0, nts - k0, vv);
+        if (guard)
+          raster_row<T, CH, kExact, kAbs, true>(rec, vv, k0, dx0, nx, nts, B, C, bdy, cdy, s0,
+                                                s1, s2, px, py);
+        else
+          raster_row<T, CH, kExact, kAbs, false>(rec, vv, k0, dx0, nx, nts, B, C, bdy, cdy, s0,
+                                                 s1, s2, px, py);
+      }
+      s.T0 += s0;
+      s.T1 += s1;
+      s.T2 += s2;
+      const T dys0 = dy * s0;
+      s.Y0 += dys0;
+      s.YY += dy * dys0;
+      s.Y1 += dy * s1;
+      if (kAbs) {
+        s.PX += px;
+        s.PY += py;
+      }
+    }
+  }
+  return s;
+}
+
+// Per-pixel terms of RasterizeToPixelsBwd.cu summed over the tile, with
+// v_sigma = -v alpha, d sigma / d mean = -(P d) and
+// d sigma / d conic = (dx^2 / 2, dx dy, dy^2 / 2): the nine partials of one
+// record (zero for dead records), in row order
+// {v_xy.x, v_xy.y, v_conic.a, v_conic.b, v_conic.c, v_opac, v_mu, v_xy_abs.x, v_xy_abs.y}.
+template <typename T, bool kAbs>
+__device__ __forceinline__ void raster_partials(const RasterRecord<T> &rec, const TileSums<T> &s,
+                                                T (&v)[9]) {
+  const T half = static_cast<T>(0.5);
+  const T om = rec.om;
+  v[0] = om * (rec.a * s.T1 + rec.b * s.Y0);
+  v[1] = om * (rec.c * s.Y0 + rec.b * s.T1);
+  v[2] = -half * om * s.T2;
+  v[3] = -om * s.Y1;
+  v[4] = -half * om * s.YY;
+  v[5] = rec.mu * s.T0;
+  v[6] = rec.o * s.T0;
+  v[7] = kAbs ? fabs(om) * s.PX : static_cast<T>(0);
+  v[8] = kAbs ? fabs(om) * s.PY : static_cast<T>(0);
+}
+
 // Records in tile order (tile_offsets, flatten_ids; isect_ids optional), one
 // lane per record.  kRows = false: each record's nine partials go out
 // through global atomics.  kRows = true: they are stored as the row
@@ -465,93 +555,224 @@ __global__ __launch_bounds__(kBwdThreads) void raster_bwd_kernel(
   const T *__restrict__ vimg = v_image + static_cast<int64_t>(cam) * H * W;
   RasterRecord<T> rec;
   load_raster_record(means2d, conics, opac, mus, g, n_items, key_ok, oy, oy + ny - 1, rec);
-  const T half = static_cast<T>(0.5);
-  const T dx0 = (static_cast<T>(ox) + half) - rec.mx;
-  // Columns past the image matter only for records whose sigma may be
-  // non-finite (uniform over the wave).
-  const bool guard = ballot(rec.live && !rec.pd && nx < nts) != 0;
-  // T_k = sum over rows of s_k; Y0 = sum dy s0, Y1 = sum dy s1, YY = sum dy^2 s0;
-  // PX, PY = sums of the per-pixel absolute mean gradients.
-  T T0 = 0, T1 = 0, T2 = 0, Y0 = 0, Y1 = 0, YY = 0, PX = 0, PY = 0;
-  bool full = false;
-  if constexpr (kExact && R <= 16 && R % kChunk == 0) full = vec && ballot(nx < nts) == 0;
-  if (full && ballot(rec.live) != 0) {
-    raster_tile_full<T, R, kAbs>(rec, vimg, W, ox, oy, dx0, T0, T1, T2, Y0, Y1, YY, PX, PY);
-  } else if (ballot(rec.live) != 0) {
-    for (int ly = 0; ly < R; ++ly) {
-      if (!kExact && ly >= nts) break;
-      const int i = oy + ly;
-      const bool in_row = rec.live && i >= rec.i0 && i <= rec.i1;
-      if (ballot(in_row) == 0) continue;
-      const T dy = (static_cast<T>(i) + half) - rec.my;
-      const T B = rec.hb * dy, C = rec.hc * dy * dy;
-      const T bdy = rec.b * dy, cdy = rec.c * dy;
-      const T *__restrict__ vrow = vimg + static_cast<int64_t>(in_row ? i : 0) * W + ox;
-      T s0 = 0, s1 = 0, s2 = 0, px = 0, py = 0;
-      constexpr int CH = R < kChunk ? R : kChunk;
-#pragma unroll 1
-      for (int k0 = 0; k0 < R; k0 += CH) {
-        if (!kExact && k0 >= nts) break;
-        T vv[CH];
-        if (vec)
-          load_grad_row<T, CH, true>(vrow + k0, in_row, nx - k0, nts - k0, vv);
-        else
-          load_grad_row<T, CH, false>(vrow + k0, in_row, nx - k0, nts - k0, vv);
-        if (guard)
-          raster_row<T, CH, kExact, kAbs, true>(rec, vv, k0, dx0, nx, nts, B, C, bdy, cdy, s0,
-                                                s1, s2, px, py);
-        else
-          raster_row<T, CH, kExact, kAbs, false>(rec, vv, k0, dx0, nx, nts, B, C, bdy, cdy, s0,
-                                                 s1, s2, px, py);
-      }
-      T0 += s0;
-      T1 += s1;
-      T2 += s2;
-      const T dys0 = dy * s0;
-      Y0 += dys0;
-      YY += dy * dys0;
-      Y1 += dy * s1;
-      if (kAbs) {
-        PX += px;
-        PY += py;
-      }
-    }
-  }
+  const T dx0 = (static_cast<T>(ox) + static_cast<T>(0.5)) - rec.mx;
+  const TileSums<T> s =
+      raster_record_sums<T, R, kExact, kAbs>(rec, vimg, W, ox, oy, nx, nts, vec, dx0);
   if (!key_ok) return;
-  // Per-pixel terms of RasterizeToPixelsBwd.cu summed over the tile, with
-  // v_sigma = -v alpha, d sigma / d mean = -(P d) and
-  // d sigma / d conic = (dx^2 / 2, dx dy, dy^2 / 2).  Zero for dead records.
-  const T om = rec.om;
-  const T ax = om * (rec.a * T1 + rec.b * Y0);
-  const T ay = om * (rec.c * Y0 + rec.b * T1);
-  const T ca = -half * om * T2, cb = -om * Y1, cc = -half * om * YY;
-  const T ao = rec.mu * T0, am = rec.o * T0;
-  const T aax = fabs(om) * PX, aay = fabs(om) * PY;
+  T v[9];
+  raster_partials<T, kAbs>(rec, s, v);
   if (kRows) {
     if (kAbs) {
-      const T v[9] = {ax, ay, ca, cb, cc, ao, am, aax, aay};
       store_row(rows, isect_src[r], v);
     } else {
-      const T v[7] = {ax, ay, ca, cb, cc, ao, am};
-      store_row(rows, isect_src[r], v);
+      const T v7[7] = {v[0], v[1], v[2], v[3], v[4], v[5], v[6]};
+      store_row(rows, isect_src[r], v7);
     }
     return;
   }
   if (!rec.live) return;
-  if (ax == 0 && ay == 0 && aax == 0 && aay == 0 && ca == 0 && cb == 0 && cc == 0 && ao == 0 &&
-      am == 0)
-    return;  // nothing to add
-  atomic_add(v_xy + 2 * g, ax);
-  atomic_add(v_xy + 2 * g + 1, ay);
+  bool any = false;
+#pragma unroll
+  for (int c = 0; c < 9; ++c) any = any || v[c] != 0;
+  if (!any) return;  // nothing to add
+  atomic_add(v_xy + 2 * g, v[0]);
+  atomic_add(v_xy + 2 * g + 1, v[1]);
   if (kAbs) {
-    atomic_add(v_xy_abs + 2 * g, aax);
-    atomic_add(v_xy_abs + 2 * g + 1, aay);
+    atomic_add(v_xy_abs + 2 * g, v[7]);
+    atomic_add(v_xy_abs + 2 * g + 1, v[8]);
   }
-  atomic_add(v_conic + 3 * g, ca);
-  atomic_add(v_conic + 3 * g + 1, cb);
-  atomic_add(v_conic + 3 * g + 2, cc);
-  atomic_add(v_opac + g, ao);
-  atomic_add(v_mu + g, am);
+  atomic_add(v_conic + 3 * g, v[2]);
+  atomic_add(v_conic + 3 * g + 1, v[3]);
+  atomic_add(v_conic + 3 * g + 2, v[4]);
+  atomic_add(v_opac + g, v[5]);
+  atomic_add(v_mu + g, v[6]);
+}
+
+// ------------------------------------------- sign-split backward (rows) ---
+//
+// When (P d)_x = a dx + b dy keeps one sign over a record's tile,
+// sum |w| |(P d)_x| = |a sum |w| dx + b sum |w| dy|: the absolute mean
+// gradient costs two accumulations per pixel (|w| and |w| dx per row) instead
+// of two FMAs and two absolute-value FMAs; likewise (P d)_y = b dx + c dy.
+// Waves are SIMD, so the cheaper form pays only where all 64 records of a
+// wave qualify: each block of kSplitThreads records is partitioned in LDS
+// (stable), qualifying whole-tile records first, and the waves then take
+// the records of their new slots.  Each record's row goes to isect_src[r]
+// whichever lane computed it, so the partition does not change the output.
+
+constexpr int kSplitThreads = 256;
+// A tile qualifies when min |p dx + q dy| over its pixel centres is at least
+// this fraction of max(|p| |dx|) + max(|q| |dy|), which bounds the
+// cancellation in |p sum |w| dx + q sum |w| dy| to a factor of 64.
+constexpr double kSignMargin = 1.0 / 64.0;
+
+template <typename T>
+__device__ __forceinline__ bool one_sign(T p, T q, T dxa, T dxb, T dya, T dyb) {
+  const T t0 = fma(p, dxa, q * dya), t1 = fma(p, dxb, q * dya);
+  const T t2 = fma(p, dxa, q * dyb), t3 = fma(p, dxb, q * dyb);
+  const T lo = fmin(fmin(t0, t1), fmin(t2, t3)), hi = fmax(fmax(t0, t1), fmax(t2, t3));
+  const T scale = fabs(p) * fmax(fabs(dxa), fabs(dxb)) + fabs(q) * fmax(fabs(dya), fabs(dyb));
+  const T m = static_cast<T>(kSignMargin) * scale;
+  return lo >= m || hi <= -m;  // false for NaN
+}
+
+// raster_tile_full for a record whose (P d)_x and (P d)_y keep one sign over
+// the tile: per row s0 = sum w, s1 = sum w dx, a0 = sum |w|, a1 = sum |w| dx,
+// column sums W_k of w; then PX = |a A1 + b AY|, PY = |b A1 + c AY| with
+// A1 = sum |w| dx and AY = sum |w| dy over the tile.
+template <typename T, int R>
+__device__ __forceinline__ TileSums<T> raster_tile_signed(const RasterRecord<T> &rec,
+                                                          const T *__restrict__ vimg, uint32_t W,
+                                                          int ox, int oy, T dx0) {
+  using Q = typename Quad<T>::type;
+  constexpr int kq = Quad<T>::n;
+  TileSums<T> s = {0, 0, 0, 0, 0, 0, 0, 0};
+  T dxk[R], wk[R];
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    dxk[k] = dx0 + static_cast<T>(k);
+    wk[k] = 0;
+  }
+  T A1 = 0, AY = 0;
+  const T half = static_cast<T>(0.5);
+#pragma unroll 1
+  for (int ly = 0; ly < R; ++ly) {
+    const int i = oy + ly;
+    const bool in_row = rec.live && i >= rec.i0 && i <= rec.i1;
+    if (ballot(in_row) == 0) continue;
+    const T dy = (static_cast<T>(i) + half) - rec.my;
+    const T B = rec.hb * dy, C = rec.hc * dy * dy;
+    const typename Bits<T>::type lim = in_row ? rec.lim : 0;
+    const T *__restrict__ vrow = vimg + static_cast<int64_t>(i) * W + ox;
+    T s0 = 0, s1 = 0, a0 = 0, a1 = 0;
+#pragma unroll
+    for (int h = 0; h < R; h += kChunk) {
+      T vv[kChunk];
+#pragma unroll
+      for (int q = 0; q < kChunk / kq; ++q)
+        *reinterpret_cast<Q *>(vv + q * kq) = *reinterpret_cast<const Q *>(vrow + h + q * kq);
+#pragma unroll
+      for (int kk = 0; kk < kChunk; ++kk) {
+        const T dx = dxk[h + kk];
+        const T sl = fma(fma(rec.ha, dx, B), dx, C);
+        const T e = neg_exp2(sl);
+        const T w = alpha_pass(sl, lim) ? vv[kk] * e : static_cast<T>(0);
+        wk[h + kk] += w;
+        s0 += w;
+        s1 = fma(w, dx, s1);
+        a0 += fabs(w);
+        a1 = fma(fabs(w), dx, a1);
+      }
+    }
+    s.Y0 += dy * s0;
+    s.YY += dy * (dy * s0);
+    s.Y1 += dy * s1;
+    AY = fma(dy, a0, AY);
+    A1 += a1;
+  }
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const T wx = wk[k] * dxk[k];
+    s.T0 += wk[k];
+    s.T1 += wx;
+    s.T2 += wx * dxk[k];
+  }
+  s.PX = fabs(fma(rec.a, A1, rec.b * AY));
+  s.PY = fabs(fma(rec.b, A1, rec.c * AY));
+  return s;
+}
+
+// The two-pass (rows) backward with absolute gradients at tile size 16 over
+// an image whose rows allow 16-byte loads.
+template <typename T>
+__global__ __launch_bounds__(kSplitThreads) void raster_bwd_split_kernel(
+    const T *__restrict__ means2d, const T *__restrict__ conics, const T *__restrict__ opac,
+    const T *__restrict__ mus, const int32_t *__restrict__ tile_offsets,
+    const int64_t *__restrict__ isect_ids, const int32_t *__restrict__ flatten_ids,
+    const int32_t *__restrict__ isect_src, int64_t n_isects, uint32_t n_keys, int64_t n_items,
+    const T *__restrict__ v_image, uint32_t W, uint32_t H, uint32_t tw, uint32_t th,
+    T *__restrict__ rows) {
+  constexpr int R = 16;
+  constexpr int kWaves = kSplitThreads / 64;
+  __shared__ RasterRecord<T> s_rec[kSplitThreads];
+  __shared__ int32_t s_r[kSplitThreads];
+  __shared__ uint32_t s_key[kSplitThreads];
+  __shared__ uint32_t s_count[kWaves];
+  const uint32_t wave = wave_index(), lane = lane_id();
+  const int64_t rb = static_cast<int64_t>(xcd_swizzle(blockIdx.x, gridDim.x)) * kSplitThreads +
+                     64 * static_cast<int64_t>(wave);
+  const int64_t r = rb + lane;
+  bool in_list = r < n_isects;
+  const uint32_t n_tiles = tw * th;
+  const T half = static_cast<T>(0.5);
+  // Load and classify each record in list order.  A record whose key is out
+  // of range gets no row, as in raster_bwd_kernel.
+  uint32_t key = 0;
+  if (rb < n_isects) {  // uniform per wave
+    if (isect_ids != nullptr) {
+      const int64_t k = in_list ? isect_ids[r] : 0;
+      in_list = in_list && k >= 0 && k < static_cast<int64_t>(n_keys);
+      key = in_list ? static_cast<uint32_t>(k) : 0u;
+    } else {
+      key = wave_record_key(tile_offsets, n_keys, n_isects, rb, r);
+    }
+  }
+  const int64_t g = in_list ? static_cast<int64_t>(flatten_ids[r]) : -1;
+  bool fast = false;
+  RasterRecord<T> rec;
+  {
+    const uint32_t cam = key / n_tiles, t = key - cam * n_tiles;
+    const uint32_t ty = t / tw, tx = t - ty * tw;
+    const int ox = static_cast<int>(tx) * R, oy = static_cast<int>(ty) * R;
+    const int ny = min(R, static_cast<int>(H) - oy);
+    load_raster_record(means2d, conics, opac, mus, g, n_items, in_list, oy, oy + ny - 1, rec);
+    if (in_list && ox + R <= static_cast<int>(W) && ny == R) {
+      const T dxa = (static_cast<T>(ox) + half) - rec.mx;
+      const T dya = (static_cast<T>(oy) + half) - rec.my;
+      const T dxb = dxa + static_cast<T>(R - 1), dyb = dya + static_cast<T>(R - 1);
+      fast = one_sign(rec.a, rec.b, dxa, dxb, dya, dyb) &&
+             one_sign(rec.b, rec.c, dxa, dxb, dya, dyb);
+    }
+  }
+  // Stable partition of the block, qualifying records first; each record
+  // moves with its loaded state.
+  const uint64_t fm = ballot(fast);
+  if (lane == 0) s_count[wave] = static_cast<uint32_t>(__popcll(fm));
+  __syncthreads();
+  uint32_t before = 0, n_fast = 0;
+#pragma unroll
+  for (uint32_t w = 0; w < kWaves; ++w) {
+    const uint32_t c = s_count[w];
+    before += w < wave ? c : 0u;
+    n_fast += c;
+  }
+  const uint32_t fast_lt = before + static_cast<uint32_t>(__popcll(fm & lanemask_lt()));
+  const uint32_t slot = fast ? fast_lt : n_fast + (threadIdx.x - fast_lt);
+  s_r[slot] = in_list ? static_cast<int32_t>(r) : -1;
+  s_key[slot] = key;
+  s_rec[slot] = rec;
+  __syncthreads();
+  const int32_t rr = s_r[threadIdx.x];
+  const bool valid = rr >= 0;
+  if (ballot(valid) == 0) return;  // uniform per wave; no barrier follows
+  key = s_key[threadIdx.x];
+  rec = s_rec[threadIdx.x];
+  const bool wave_fast = (wave + 1) * 64 <= n_fast;
+  const uint32_t cam = key / n_tiles, t = key - cam * n_tiles;
+  const uint32_t ty = t / tw, tx = t - ty * tw;
+  const int ox = static_cast<int>(tx) * R, oy = static_cast<int>(ty) * R;
+  const int nx = min(R, static_cast<int>(W) - ox);
+  const T *__restrict__ vimg = v_image + static_cast<int64_t>(cam) * H * W;
+  const T dx0 = (static_cast<T>(ox) + half) - rec.mx;
+  TileSums<T> s;
+  if (wave_fast)
+    s = raster_tile_signed<T, R>(rec, vimg, W, ox, oy, dx0);
+  else
+    s = raster_record_sums<T, R, true, true>(rec, vimg, W, ox, oy, nx, R, true, dx0);
+  if (!valid) return;
+  T v[9];
+  raster_partials<T, true>(rec, s, v);
+  store_row(rows, isect_src[rr], v);
 }
 
 int check_raster_args(int64_t n_isects, int64_t C, int64_t N, uint32_t W, uint32_t H,
@@ -729,7 +950,13 @@ int raster_bwd_impl(const T *means2d, const T *conics, const T *opac, const T *m
                                   flatten_ids, isect_src, n_isects, n_keys, C * N, v_image, W,   \
                                   H, ts, tw, th, vec, v_xy_abs, v_xy, v_conic, v_opac, v_mu,     \
                                   rows, absgrad, stream)
-  if (ts == 16)
+  const bool with_abs = v_xy_abs != nullptr || (rows != nullptr && absgrad);
+  if (ts == 16 && vec && rows != nullptr && with_abs)
+    raster_bwd_split_kernel<T>
+        <<<dim3(static_cast<uint32_t>(ceil_div(n_isects, kSplitThreads))), dim3(kSplitThreads),
+           0, stream>>>(means2d, conics, opac, mus, tile_offsets, isect_ids, flatten_ids,
+                        isect_src, n_isects, n_keys, C * N, v_image, W, H, tw, th, rows);
+  else if (ts == 16)
     R2S_RASTER_BWD_R(16, true);
   else if (ts == 8)
     R2S_RASTER_BWD_R(8, true);

@@ -321,6 +321,50 @@ def test_rasterize_fwd_bwd(dtype, shape, order):
     assert no_abs[0] is None
 
 
+def _one_sign(p, q, dxa, dya, span=15.0, margin=1.0 / 64):
+    """(p, q) . d keeps one sign over a tile's pixel centres, with margin."""
+    t = np.stack([p * (dxa + i) + q * (dya + j) for i in (0.0, span) for j in (0.0, span)], 1)
+    scale = (np.abs(p) * np.maximum(np.abs(dxa), np.abs(dxa + span))
+             + np.abs(q) * np.maximum(np.abs(dya), np.abs(dya + span)))
+    return (t.min(1) >= margin * scale) | (t.max(1) <= -margin * scale)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_absgrad_sign_split_backward(dtype):
+    """The tile-size-16 absolute-gradient backward partitions each block's
+    records: waves whose records keep one sign of (P d)_x and (P d)_y over
+    their tile sum |w| moments instead of per-pixel absolute values.  The
+    scene has large Gaussians so that both kinds of waves run; every output
+    is checked against the oracle."""
+    W_img = H_img = 128
+    d, m2, con, mu, op, ids, fl, off = _raster_case(1500, 11, W_img, H_img, 16, 1, dtype,
+                                                     log_mu=-2.0)
+    keys, g = np32(ids).astype(np.int64), np32(fl).astype(np.int64)
+    t = keys % 64
+    ox, oy = (t % 8) * 16.0, (t // 8) * 16.0
+    m2n, cn = np32(m2).reshape(-1, 2).astype(np.float64), np32(con).reshape(-1, 3)
+    a, b, c = cn[g, 0], cn[g, 1], cn[g, 2]
+    dxa, dya = ox + 0.5 - m2n[g, 0], oy + 0.5 - m2n[g, 1]
+    fast = _one_sign(a, b, dxa, dya) & _one_sign(b, c, dxa, dya)
+    n_blk = fast.size // 256
+    per_block = fast[:n_blk * 256].reshape(n_blk, 256).sum(1)
+    assert (per_block >= 64).any() and (per_block < 256).any(), per_block
+    img = W.rasterize_to_pixels_fwd(m2, con, op, mu, off, fl, W_img, H_img, 16)
+    v = torch.randn(img.shape, generator=d["gen"], dtype=dtype)
+    ref = native.raster_bwd(np32(m2), np32(con), np32(op), np32(mu), np32(off), np32(fl),
+                            v.numpy(), W_img, H_img, 16, True)
+    got = W.rasterize_to_pixels_bwd_per_gaussian(m2, con, op, mu, off, ids, fl, v.to(DEV),
+                                                 W_img, H_img, 16, True)
+    f32 = dtype == torch.float32
+    names = ("v_means2d_abs", "v_means2d", "v_conics", "v_opacities", "v_mus")
+    for x, e, n in zip(got, ref, names):
+        scale = float(np.abs(e).max()) + 1e-30
+        assert_close(np32(x), e, n, rtol=1e-4 if f32 else 1e-9,
+                     atol=(3e-6 if f32 else 1e-12) * scale,
+                     max_outliers=e.size // 500 if f32 else 0,
+                     outlier_atol=2e-4 * scale if f32 else None)
+
+
 @pytest.mark.parametrize("order", ["emission", "tile"])
 def test_nan_opacity_propagates_as_in_the_reference(order):
     # A NaN alpha is not below the cut-off, so the reference does not skip it:
