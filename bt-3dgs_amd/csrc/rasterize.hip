@@ -3,24 +3,25 @@
 // and |alpha| < 1e-5 (r2splat/cuda/csrc/RasterizeToPixelsFwd.cu:57-186), and
 // its VJP (RasterizeToPixelsBwd.cu:77-480).
 //
-// Forward: one workgroup per (camera, tile), one pixel per thread; the
-// tile's list is staged through LDS in batches of ts^2 Gaussians
-// ({mean} and {conic, opacity*mu} as 8- and 16-byte vectors, read by every
-// lane as an LDS broadcast).  Each pixel sums in list order, as the
-// reference does.  Workgroups are XCD-swizzled so neighbouring tiles, which
-// share most of their Gaussians, run on the same L2.
+// Forward (raster_fwd_rows_kernel, tile sizes 8/16/32): blocks of eight
+// waves per (view, tile), or per share of a heavy tile's list; the list is
+// staged through LDS in batches of 512 pre-scaled records, and a lane sums a
+// whole tile row of up to 16 pixels for the records of its group.  Partial
+// tiles are added in a fixed order.  Other tile sizes use raster_fwd_kernel
+// (one pixel per thread).
 //
-// Backward: one workgroup per (camera, tile) with the tile's upstream
-// gradient staged in LDS, one lane per record of the tile's list.  A lane
-// visits only the pixels that can pass the alpha test -- the rows of the
-// ellipse sigma <= ln(|o mu| / 1e-5) and the x-segment of each row
-// (r2s_cull.h) -- and accumulates, per row, the moments sum(w), sum(w dx),
-// sum(w dx^2) of w = v exp(-sigma) over passing pixels (plus the per-pixel
-// absolute mean gradients), folded into the nine partials once per row.
-// Then one hardware float atomic per partial.  Along a row sigma is
-// evaluated as (a dx / 2 + b dy) dx + c dy^2 / 2.  The two reference
+// Backward (raster_bwd_kernel): one lane per record in list order.  A lane
+// walks its tile row by row (rows no lane of the wave can reach are skipped)
+// and accumulates the moments sum(w), sum(w dx), sum(w dx^2), sum(w dy),
+// sum(w dx dy), sum(w dy^2) of w = v exp(-sigma) over passing pixels, plus
+// the per-pixel absolute mean gradients; the nine partials follow once per
+// record.  They go out through float atomics (one-pass form) or as the
+// record's row of a table that r2s_rows.h reduces per Gaussian (two-pass
+// form).  With absolute gradients at tile size 16, raster_bwd_split_kernel
+// partitions each block's records so that records whose (P d) keeps one
+// sign over the tile run the cheaper |w|-moment form.  The two reference
 // backward variants (per pixel, per Gaussian) compute the same sums and
-// share this kernel.
+// share these kernels.
 #include "r2s_common.h"
 #include "r2s_cull.h"
 #include "r2s_rows.h"
