@@ -23,9 +23,10 @@
 // voxels, and per record the ten sums
 //   T_k = sum s_k,  Y0 = sum dy s0, Z0 = sum dz s0, Y1 = sum dy s1,
 //   Z1 = sum dz s1, YY = sum dy^2 s0, YZ = sum dy dz s0, ZZ = sum dz^2 s0,
-// from which the ten partials follow; then ten hardware float atomics.
-// The two reference backward variants (per voxel, per Gaussian) compute the
-// same sums and share this kernel.
+// from which the ten partials follow.  They go out through float atomics
+// (one-pass form) or as the record's row of a table that r2s_rows.h reduces
+// per Gaussian (two-pass form).  The two reference backward variants (per
+// voxel, per Gaussian) compute the same sums and share this kernel.
 #include "r2s_common.h"
 #include "r2s_cull.h"
 #include "r2s_rows.h"
