@@ -222,16 +222,14 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
       const typename Bits<T>::type lim = bits_of(q.z);
       const T dy = py - p.y;
       const T B = p.w * dy, C = q.x * dy * dy;
-      // sl as a quadratic in the column k of the lane's row: with
-      // dx = dx0 + k, sl = h_a k^2 + (2 h_a dx0 + B) k + sl(dx0), so each
-      // pixel costs two FMAs on the constant k and no offset.
-      const T dx0 = px0 - p.x;
-      const T B1 = fma(p.z + p.z, dx0, B);
-      const T C1 = fma(fma(p.z, dx0, B), dx0, C);
+      // dx as the reference forms it (pixel centre minus mean, one rounding):
+      // a quadratic in the column offset instead would cancel badly where
+      // sigma is small but the offset's terms are large (sub-pixel
+      // footprints far along the row).
 #pragma unroll
       for (int k = 0; k < R; ++k) {
-        const T kk = static_cast<T>(k);
-        const T sl = fma(fma(p.z, kk, B1), kk, C1);
+        const T dx = (px0 + static_cast<T>(k)) - p.x;
+        const T sl = (p.z * dx + B) * dx + C;
         const T e = neg_exp2(sl);
         acc[k] = fma(q.y, alpha_pass(sl, lim) ? e : static_cast<T>(0), acc[k]);
       }

@@ -161,15 +161,10 @@ __global__ __launch_bounds__(1024) void voxel_fwd_kernel(
       const T dy = py - mo.y, dz = pz - mo.z;
       const T B = h0.y * dy + h0.z * dz;
       const T C = (h0.w * dy + h1.x * dz) * dy + h1.y * dz * dz;
-      // sl as a quadratic in the voxel offset r along the row: with
-      // dx = dx0 + r, sl = h_0 r^2 + (2 h_0 dx0 + B) r + sl(dx0).
-      const T dx0 = px0 - mo.x;
-      const T B1 = fma(h0.x + h0.x, dx0, B);
-      const T C1 = fma(fma(h0.x, dx0, B), dx0, C);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const T rr = static_cast<T>(r);
-        const T sl = fma(fma(h0.x, rr, B1), rr, C1);
+        const T dx = (px0 + static_cast<T>(r)) - mo.x;
+        const T sl = (h0.x * dx + B) * dx + C;
         const T e = neg_exp2(sl);
         acc[r] = fma(mo.w, alpha_pass(sl, lim) ? e : static_cast<T>(0), acc[r]);
       }

@@ -321,6 +321,47 @@ def test_rasterize_fwd_bwd(dtype, shape, order):
     assert no_abs[0] is None
 
 
+@pytest.mark.parametrize("ts", [8, 16, 32])
+def test_rasterize_fwd_small_gaussians(ts):
+    """Sub-pixel footprints (conic entries 20..80) anywhere along a lane's row
+    of pixels: where sigma is small the exponent's terms in dx are large, so
+    an evaluation that loses that cancellation (e.g. a quadratic in the
+    column offset from the row start) errs by 1e-4..1e-3 relative."""
+    g = torch.Generator().manual_seed(31)
+    N, W_img, H_img = 4000, 64, 64
+    m2 = torch.rand(1, N, 2, generator=g) * torch.tensor([W_img, H_img])
+    a = 20 + 60 * torch.rand(1, N, generator=g)
+    c = 20 + 60 * torch.rand(1, N, generator=g)
+    b = (torch.rand(1, N, generator=g) - 0.5) * (a * c).sqrt()
+    con = torch.stack([a, b, c], -1)
+    op = 0.2 + 0.8 * torch.rand(1, N, generator=g)
+    mu = torch.ones(1, N)
+    r = torch.full((1, N, 2), 2, dtype=torch.int32)
+    m2, con, op, mu, r = (t.to(DEV) for t in (m2, con, op, mu, r))
+    tw, th = -(-W_img // ts), -(-H_img // ts)
+    _, ids, fl = W.isect_tiles(m2, r, ts, tw, th)
+    off = W.isect_offset_encode(ids, 1, tw, th)
+    img = W.rasterize_to_pixels_fwd(m2, con, op, mu, off, fl, W_img, H_img, ts)
+    img_o = native.raster_fwd(np32(m2), np32(con), np32(op), np32(mu), np32(off), np32(fl),
+                              W_img, H_img, ts)
+    assert_close(np32(img), img_o, "image", rtol=1e-4, atol=1e-5,
+                 max_outliers=img_o.size // 1000, outlier_atol=3e-5)
+
+
+@pytest.mark.parametrize("dims,ts", [((32, 32, 32), 8), ((30, 20, 40), 10)])
+def test_voxelize_fwd_small_gaussians(dims, ts):
+    """Sub-voxel footprints anywhere along a thread's x-row (see
+    test_rasterize_fwd_small_gaussians)."""
+    d, m3, con, ids, fl, off = _voxel_case(6000, 22, dims, ts, log_mu=-5.0)
+    assert float(con[..., 0].max()) > 10.0
+    d2, d1, d0 = dims
+    vol = W.voxelize_to_voxels_fwd(m3, con, d["opac"], off, fl, d2, d1, d0, ts)
+    vol_o = native.voxel_fwd(np32(m3), np32(con), np32(d["opac"]), np32(off), np32(fl), d2, d1,
+                             d0, ts)
+    assert_close(np32(vol), vol_o, "volume", rtol=1e-4, atol=1e-5,
+                 max_outliers=vol_o.size // 1000, outlier_atol=3e-6)
+
+
 def _one_sign(p, q, dxa, dya, span=15.0, margin=1.0 / 64):
     """(p, q) . d keeps one sign over a tile's pixel centres, with margin."""
     t = np.stack([p * (dxa + i) + q * (dya + j) for i in (0.0, span) for j in (0.0, span)], 1)
