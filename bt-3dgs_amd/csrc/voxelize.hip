@@ -475,6 +475,245 @@ __global__ __launch_bounds__(kBwdThreads) void voxel_bwd_kernel(
   atomic_add(v_opac + g, go);
 }
 
+// ------------------------------------------- chunked backward (rows) ---
+//
+// A wave of 64 records walks the union of its lanes' reached rows, which is
+// nearly always every row of the brick, while one record's culled
+// ellipsoid reaches about 57 % of them at config 3.  This form lists, per
+// wave, the (record, slice, row) items the records reach -- slice by slice,
+// row by row, as slice_rows gives them -- and hands them out in chunks of up
+// to kChunkRows consecutive items of one record, one chunk per lane and
+// round, so lanes spend their steps on reached rows.  Chunks are ordered by
+// (chunk index within the record, record): within a round each record
+// appears at most once per chunk index, and the chunk sums are added to the
+// record's LDS accumulators one chunk index at a time in increasing order,
+// so the result does not depend on scheduling.  Every brick must lie inside
+// the volume with 16-byte gradient rows (the caller checks).
+
+constexpr int kChunkRows = 8;
+constexpr int kChunkWaves = 4;
+
+template <typename T>
+struct ChunkRecord {
+  T m[3], h[6];
+  typename Bits<T>::type lim;  // 0 for dead records
+  int ok, oj, oi, n_items;
+};
+
+template <typename T>
+__global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
+    const T *__restrict__ means3d, const T *__restrict__ conics, const T *__restrict__ opac,
+    const int32_t *__restrict__ tile_offsets, const int64_t *__restrict__ isect_ids,
+    const int32_t *__restrict__ flatten_ids, const int32_t *__restrict__ isect_src,
+    int64_t n_isects, uint32_t n_keys, int64_t N, const T *__restrict__ v_vol, uint32_t D2,
+    uint32_t D1, uint32_t D0, uint32_t n2, uint32_t n1, T *__restrict__ rows) {
+  constexpr int R = kChunkRows;
+  using Q = typename Quad<T>::type;
+  constexpr int kq = Quad<T>::n;
+  __shared__ ChunkRecord<T> s_rec[kChunkWaves][64];
+  __shared__ uint64_t s_slices[kChunkWaves][64];  // per slice: row offset (3 bits), count (4)
+  __shared__ T s_acc[kChunkWaves][10][64];
+  __shared__ uint16_t s_chunk[kChunkWaves][64 * R];
+  const uint32_t w = wave_index(), lane = lane_id();
+  const int64_t rb = static_cast<int64_t>(xcd_swizzle(blockIdx.x, gridDim.x)) *
+                         (64 * kChunkWaves) + 64 * static_cast<int64_t>(w);
+  if (rb >= n_isects) return;  // uniform per wave; the waves share no barrier
+  const int64_t r = rb + lane;
+  const bool in_list = r < n_isects;
+  uint32_t key;
+  bool key_ok = in_list;
+  if (isect_ids != nullptr) {
+    const int64_t k = in_list ? isect_ids[r] : 0;
+    key_ok = key_ok && k >= 0 && k < static_cast<int64_t>(n_keys);
+    key = key_ok ? static_cast<uint32_t>(k) : 0u;
+  } else {
+    key = wave_record_key(tile_offsets, n_keys, n_isects, rb, r);
+  }
+  const int64_t g = key_ok ? static_cast<int64_t>(flatten_ids[r]) : -1;
+  const Brick b = brick_of(key, n2, n1, R, D2, D1, D0);
+  BwdRecord<T> rec;
+  load_bwd_record(means3d, conics, opac, g, N, key_ok, b, rec);
+  const T half = static_cast<T>(0.5);
+  const uint32_t plane = D1 * D2;  // the caller checks D2 D1 D0 < 2^31
+
+  // The record's reached rows, slice by slice.
+  uint64_t slices = 0;
+  int n_items = 0;
+#pragma unroll 1
+  for (int li = 0; li < R; ++li) {
+    const int i = b.oi + li;
+    const bool in_slice = rec.live && i >= rec.i0 && i <= rec.i1;
+    const T dz = (static_cast<T>(i) + half) - rec.m[2];
+    int j0, j1;
+    slice_rows(rec, b, in_slice, dz, j0, j1);
+    const int c = j1 >= j0 ? j1 - j0 + 1 : 0;
+    slices |= static_cast<uint64_t>(((j0 - b.oj) & 7) | (c << 3)) << (8 * li);
+    n_items += c;
+  }
+  {
+    ChunkRecord<T> cr;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) cr.m[c] = rec.m[c];
+#pragma unroll
+    for (int c = 0; c < 6; ++c) cr.h[c] = rec.h[c];
+    cr.lim = rec.live ? rec.lim : 0;
+    cr.ok = b.ok;
+    cr.oj = b.oj;
+    cr.oi = b.oi;
+    cr.n_items = n_items;
+    s_rec[w][lane] = cr;
+    s_slices[w][lane] = slices;
+#pragma unroll
+    for (int c = 0; c < 10; ++c) s_acc[w][c][lane] = 0;
+  }
+  // Chunk list in (chunk index, record) order.
+  const int n_chunks = (n_items + R - 1) / R;
+  uint32_t n_list = 0;
+  const uint64_t lt = lanemask_lt();
+#pragma unroll
+  for (int q = 0; q < R; ++q) {
+    const bool has = n_chunks > q;
+    const uint64_t m = ballot(has);
+    if (has)
+      s_chunk[w][n_list + static_cast<uint32_t>(__popcll(m & lt))] =
+          static_cast<uint16_t>(lane | (static_cast<uint32_t>(q) << 6));
+    n_list += static_cast<uint32_t>(__popcll(m));
+  }
+  // The wave's LDS operations complete in order, so its own lanes' writes
+  // are visible to the reads below; keep the compiler from moving them.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+#pragma unroll 1
+  for (uint32_t cb = 0; cb < n_list; cb += 64) {
+    const uint32_t ci = cb + lane;
+    const bool act = ci < n_list;
+    const uint32_t ent = act ? static_cast<uint32_t>(s_chunk[w][ci]) : 0u;
+    const uint32_t rl = ent & 63u, q = ent >> 6;
+    const ChunkRecord<T> cr = s_rec[w][rl];
+    const uint64_t sl = s_slices[w][rl];
+    // Slices with reached rows, and the chunk's first item.
+    uint32_t nz = 0;
+    int cur_li = R, cur_r = 0, rem = static_cast<int>(q) * R;
+#pragma unroll
+    for (int li = 0; li < R; ++li) {
+      const int c = static_cast<int>((sl >> (8 * li + 3)) & 15u);
+      nz |= (c != 0 ? 1u : 0u) << li;
+      if (cur_li == R) {
+        if (rem < c) {
+          cur_li = li;
+          cur_r = rem;
+        } else {
+          rem -= c;
+        }
+      }
+    }
+    const int n_here = act ? min(R, cr.n_items - static_cast<int>(q) * R) : 0;
+    const T dx0 = (static_cast<T>(cr.ok) + half) - cr.m[0];
+    T dxk[R], wk[R];
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      dxk[k] = dx0 + static_cast<T>(k);
+      wk[k] = 0;
+    }
+    T Y0 = 0, Z0 = 0, Y1 = 0, Z1 = 0, YY = 0, YZ = 0, ZZ = 0;
+#pragma unroll 1
+    for (int st = 0; st < R; ++st) {
+      const bool item = st < n_here;
+      const int li = cur_li & 7;
+      const int i = cr.oi + li;
+      const int j = cr.oj + static_cast<int>((sl >> (8 * li)) & 7u) + cur_r;
+      const T dz = (static_cast<T>(i) + half) - cr.m[2];
+      const T dy = (static_cast<T>(j) + half) - cr.m[1];
+      const T B = fma(cr.h[1], dy, cr.h[2] * dz);
+      const T C = fma(fma(cr.h[3], dy, cr.h[4] * dz), dy, cr.h[5] * dz * dz);
+      const typename Bits<T>::type lim = item ? cr.lim : 0;
+      // 32-bit offsets; a step without an item reads the volume's first row.
+      const uint32_t off = item ? static_cast<uint32_t>(i) * plane +
+                                      static_cast<uint32_t>(j) * D2 + static_cast<uint32_t>(cr.ok)
+                                : 0u;
+      const T *__restrict__ vrow = v_vol + off;
+      T vv[R];
+#pragma unroll
+      for (int c = 0; c < R / kq; ++c)
+        *reinterpret_cast<Q *>(vv + c * kq) = *reinterpret_cast<const Q *>(vrow + c * kq);
+      T s0 = 0, s1 = 0;
+#pragma unroll
+      for (int k = 0; k < R; ++k) {
+        const T dx = dxk[k];
+        const T slv = fma(fma(cr.h[0], dx, B), dx, C);
+        // The select on e (not on the product) keeps every gradient load
+        // unconditional.
+        const T e = alpha_pass(slv, lim) ? neg_exp2(slv) : static_cast<T>(0);
+        const T wv = vv[k] * e;
+        wk[k] += wv;
+        s0 += wv;
+        s1 = fma(wv, dx, s1);
+      }
+      const T dys0 = dy * s0, dzs0 = dz * s0;
+      Y0 += dys0;
+      Z0 += dzs0;
+      YY = fma(dy, dys0, YY);
+      YZ = fma(dz, dys0, YZ);
+      ZZ = fma(dz, dzs0, ZZ);
+      Y1 = fma(dy, s1, Y1);
+      Z1 = fma(dz, s1, Z1);
+      // Next reached row: the next row of this slice, else the first of the
+      // next slice with reached rows (R when there is none).
+      ++cur_r;
+      if (cur_r >= static_cast<int>((sl >> (8 * li + 3)) & 15u)) {
+        cur_r = 0;
+        const uint32_t rest = li + 1 < R ? nz >> (li + 1) : 0u;
+        cur_li = rest != 0u ? li + 1 + __builtin_ctz(rest) : R;
+      }
+    }
+    T t0 = 0, t1 = 0, t2 = 0;
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      const T wx = wk[k] * dxk[k];
+      t0 += wk[k];
+      t1 += wx;
+      t2 += wx * dxk[k];
+    }
+    const T sums[10] = {t0, t1, t2, Y0, Z0, Y1, Z1, YY, YZ, ZZ};
+    // One chunk index at a time: the records of one index are distinct.
+    const uint32_t q_lo = static_cast<uint32_t>(s_chunk[w][cb]) >> 6;
+    const uint32_t q_hi = static_cast<uint32_t>(s_chunk[w][min(cb + 63u, n_list - 1u)]) >> 6;
+#pragma unroll 1
+    for (uint32_t qq = q_lo; qq <= q_hi; ++qq) {
+      if (act && q == qq) {
+#pragma unroll
+        for (int c = 0; c < 10; ++c) s_acc[w][c][rl] += sums[c];
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+  }
+  if (!key_ok) return;
+  T a[10];
+#pragma unroll
+  for (int c = 0; c < 10; ++c) a[c] = s_acc[w][c][lane];
+  const T T0 = a[0], T1 = a[1], T2 = a[2], Y0 = a[3], Z0 = a[4], Y1 = a[5], Z1 = a[6],
+          YY = a[7], YZ = a[8], ZZ = a[9];
+  // Per-voxel terms of VoxelizeToVoxelsBwd.cu:409-421 summed over the brick,
+  // as in voxel_bwd_kernel.
+  const T o = rec.o;
+  const T *qc = rec.q;
+  const T v[10] = {o * (qc[0] * T1 + qc[1] * Y0 + qc[2] * Z0),
+                   o * (qc[3] * Y0 + qc[4] * Z0 + qc[1] * T1),
+                   o * (qc[5] * Z0 + qc[4] * Y0 + qc[2] * T1),
+                   -half * o * T2,
+                   -o * Y1,
+                   -o * Z1,
+                   -half * o * YY,
+                   -o * YZ,
+                   -half * o * ZZ,
+                   T0};
+  store_row(rows, isect_src[r], v);
+}
+
 int check_voxel_args(int64_t n_isects, int64_t N, uint32_t D2, uint32_t D1, uint32_t D0,
                      uint32_t ts, uint32_t n2, uint32_t n1, uint32_t n0, const char *name) {
   R2S_REQUIRE(N >= 0 && N <= kInt32Max, "%s: bad size N=%lld", name, (long long)N);
@@ -616,7 +855,14 @@ int voxel_bwd_impl(const T *means3d, const T *conics, const T *opac,
   launch_voxel_bwd<T, RR, EXACT>(means3d, conics, opac, tile_offsets, isect_ids, flatten_ids,  \
                                  isect_src, n_isects, n_keys, N, v_vol, D2, D1, D0, ts, n2, n1, \
                                  vec, v_means, v_conics, v_opac, rows, stream)
-  if (ts == 8)
+  if (ts == 8 && rows != nullptr && vec && D2 % 8 == 0 && D1 % 8 == 0 && D0 % 8 == 0 &&
+      n_vox < (int64_t{1} << 31))
+    voxel_bwd_chunk_kernel<T>
+        <<<dim3(static_cast<uint32_t>(ceil_div(n_isects, 64 * kChunkWaves))),
+           dim3(64 * kChunkWaves), 0, stream>>>(means3d, conics, opac, tile_offsets, isect_ids,
+                                                flatten_ids, isect_src, n_isects, n_keys, N, v_vol,
+                                                D2, D1, D0, n2, n1, rows);
+  else if (ts == 8)
     R2S_VOXEL_BWD_R(8, true);
   else if (ts == 4)
     R2S_VOXEL_BWD_R(4, true);
