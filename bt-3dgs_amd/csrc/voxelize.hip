@@ -511,7 +511,7 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
   using Q = typename Quad<T>::type;
   constexpr int kq = Quad<T>::n;
   __shared__ ChunkRecord<T> s_rec[kChunkWaves][64];
-  __shared__ uint64_t s_slices[kChunkWaves][64];  // per slice: row offset (3 bits), count (4)
+  __shared__ uint64_t s_rows[kChunkWaves][64];  // reached rows: bit 8 * slice + row
   __shared__ T s_acc[kChunkWaves][10][64];
   __shared__ uint16_t s_chunk[kChunkWaves][64 * R];
   const uint32_t w = wave_index(), lane = lane_id();
@@ -536,9 +536,9 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
   const T half = static_cast<T>(0.5);
   const uint32_t plane = D1 * D2;  // the caller checks D2 D1 D0 < 2^31
 
-  // The record's reached rows, slice by slice.
-  uint64_t slices = 0;
-  int n_items = 0;
+  // The record's reached rows as a 64-bit mask, bit 8 * slice + row; the
+  // items are its set bits in increasing order.
+  uint64_t reach = 0;
 #pragma unroll 1
   for (int li = 0; li < R; ++li) {
     const int i = b.oi + li;
@@ -546,10 +546,11 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
     const T dz = (static_cast<T>(i) + half) - rec.m[2];
     int j0, j1;
     slice_rows(rec, b, in_slice, dz, j0, j1);
-    const int c = j1 >= j0 ? j1 - j0 + 1 : 0;
-    slices |= static_cast<uint64_t>(((j0 - b.oj) & 7) | (c << 3)) << (8 * li);
-    n_items += c;
+    const uint32_t c = j1 >= j0 ? static_cast<uint32_t>(j1 - j0 + 1) : 0u;  // rows j0 - oj ..
+    const uint32_t run = c >= 8u ? 0xFFu : ((1u << c) - 1u);
+    reach |= static_cast<uint64_t>((run << ((j0 - b.oj) & 7)) & 0xFFu) << (8 * li);
   }
+  const int n_items = __popcll(reach);
   {
     ChunkRecord<T> cr;
 #pragma unroll
@@ -562,7 +563,7 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
     cr.oi = b.oi;
     cr.n_items = n_items;
     s_rec[w][lane] = cr;
-    s_slices[w][lane] = slices;
+    s_rows[w][lane] = reach;
 #pragma unroll
     for (int c = 0; c < 10; ++c) s_acc[w][c][lane] = 0;
   }
@@ -592,22 +593,18 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
     const uint32_t ent = act ? static_cast<uint32_t>(s_chunk[w][ci]) : 0u;
     const uint32_t rl = ent & 63u, q = ent >> 6;
     const ChunkRecord<T> cr = s_rec[w][rl];
-    const uint64_t sl = s_slices[w][rl];
-    // Slices with reached rows, and the chunk's first item.
-    uint32_t nz = 0;
-    int cur_li = R, cur_r = 0, rem = static_cast<int>(q) * R;
+    const uint64_t rows_m = s_rows[w][rl];
+    // The chunk's first item, the (8 q)-th set bit: its slice by the
+    // running bit counts of the slice bytes; within a slice the reached rows
+    // are contiguous.
+    int pos = 64, rem = static_cast<int>(q) * R;
 #pragma unroll
     for (int li = 0; li < R; ++li) {
-      const int c = static_cast<int>((sl >> (8 * li + 3)) & 15u);
-      nz |= (c != 0 ? 1u : 0u) << li;
-      if (cur_li == R) {
-        if (rem < c) {
-          cur_li = li;
-          cur_r = rem;
-        } else {
-          rem -= c;
-        }
-      }
+      const uint32_t byte = static_cast<uint32_t>(rows_m >> (8 * li)) & 0xFFu;
+      const int c = __popc(byte);
+      const bool here = pos == 64 && rem < c;
+      pos = here ? 8 * li + static_cast<int>(__builtin_ctz(byte | 0x100u)) + rem : pos;
+      rem -= (pos == 64) ? c : 0;
     }
     const int n_here = act ? min(R, cr.n_items - static_cast<int>(q) * R) : 0;
     const T dx0 = (static_cast<T>(cr.ok) + half) - cr.m[0];
@@ -621,9 +618,8 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
 #pragma unroll 1
     for (int st = 0; st < R; ++st) {
       const bool item = st < n_here;
-      const int li = cur_li & 7;
-      const int i = cr.oi + li;
-      const int j = cr.oj + static_cast<int>((sl >> (8 * li)) & 7u) + cur_r;
+      const int i = cr.oi + ((pos >> 3) & 7);
+      const int j = cr.oj + (pos & 7);
       const T dz = (static_cast<T>(i) + half) - cr.m[2];
       const T dy = (static_cast<T>(j) + half) - cr.m[1];
       const T B = fma(cr.h[1], dy, cr.h[2] * dz);
@@ -659,14 +655,9 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
       ZZ = fma(dz, dzs0, ZZ);
       Y1 = fma(dy, s1, Y1);
       Z1 = fma(dz, s1, Z1);
-      // Next reached row: the next row of this slice, else the first of the
-      // next slice with reached rows (R when there is none).
-      ++cur_r;
-      if (cur_r >= static_cast<int>((sl >> (8 * li + 3)) & 15u)) {
-        cur_r = 0;
-        const uint32_t rest = li + 1 < R ? nz >> (li + 1) : 0u;
-        cur_li = rest != 0u ? li + 1 + __builtin_ctz(rest) : R;
-      }
+      // The next reached row (64 when there is none).
+      const uint64_t rest = pos < 63 ? rows_m >> (pos + 1) : 0ull;
+      pos = rest != 0ull ? pos + 1 + static_cast<int>(__builtin_ctzll(rest)) : 64;
     }
     T t0 = 0, t1 = 0, t2 = 0;
 #pragma unroll
