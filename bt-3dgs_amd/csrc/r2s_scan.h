@@ -1,11 +1,13 @@
-// Device-wide exclusive prefix sum (reduce -> scan partials -> downsweep).
+// Device-wide exclusive prefix sum in two launches: block sums, then a
+// downsweep in which each block adds up the sums of the blocks before it.
 //
 // 256-thread blocks, 4096 items per block taken as 16 chunks of 256: item
 // k * 256 + t of a block belongs to thread t, so every load and store of a
-// wave covers 64 consecutive items.  The partial sums of all blocks are
-// scanned by one 1024-thread block, so a scan of n items needs
-// ceil(n / 4096) partials of workspace.  Deterministic: the same input always
-// produces the same output.
+// wave covers 64 consecutive items.  A scan of n items needs
+// ceil(n / 4096) partials of workspace; block b of the downsweep reads the
+// b partials before it (a few hundred at the sizes here, from L2), which
+// costs less than a third launch that scans them.  Deterministic: the same
+// input always produces the same output.
 #pragma once
 
 #include "r2s_common.h"
@@ -56,34 +58,20 @@ __global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(const Tin *__
   if (threadIdx.x == 0) partials[blockIdx.x] = total;
 }
 
-// Single block of 1024 threads: exclusive scan of the partials in place and
-// the grand total (if `total` is not null).
-template <typename Tout>
-__global__ __launch_bounds__(1024) void scan_partials_kernel(Tout *__restrict__ partials,
-                                                             int64_t nb,
-                                                             Tout *__restrict__ total) {
-  __shared__ Tout lds[16];
-  Tout running = 0;
-  for (int64_t start = 0; start < nb; start += 1024) {
-    const int64_t i = start + threadIdx.x;
-    const Tout v = (i < nb) ? partials[i] : static_cast<Tout>(0);
-    Tout chunk;
-    const Tout ex = block_exclusive_scan(v, lds, chunk);
-    if (i < nb) partials[i] = running + ex;
-    running += chunk;
-  }
-  if (threadIdx.x == 0 && total != nullptr) *total = running;
-}
-
 // Per chunk: a wave scan; then one scan over the 64 (chunk, wave) totals in
-// item order gives each chunk-wave its offset within the block.
+// item order gives each chunk-wave its offset within the block.  The block's
+// own offset is the sum of the partials of the blocks before it; the last
+// block also writes the grand total (if `total` is not null).
 template <typename Tin, typename Tout>
 __global__ __launch_bounds__(kScanThreads) void scan_down_kernel(const Tin *__restrict__ in,
                                                                  int64_t n,
                                                                  const Tout *__restrict__ partials,
-                                                                 Tout *__restrict__ out) {
+                                                                 Tout *__restrict__ out,
+                                                                 Tout *__restrict__ total) {
   static_assert(kScanItems * (kScanThreads / 64) == 64, "one wave scans the chunk totals");
   __shared__ Tout s_tot[64];
+  __shared__ Tout s_pre[kScanThreads / 64];
+  __shared__ Tout s_block;
   const uint32_t w = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile + threadIdx.x;
   Tout v[kScanItems], incl[kScanItems];
@@ -101,33 +89,26 @@ __global__ __launch_bounds__(kScanThreads) void scan_down_kernel(const Tin *__re
   __syncthreads();
   if (w == 0) {  // each lane reads, then overwrites, its own entry
     const Tout t = s_tot[lane];
-    s_tot[lane] = wave_inclusive_scan(t) - t;
+    const Tout it = wave_inclusive_scan(t);
+    s_tot[lane] = it - t;
+    if (lane == 63) s_block = it;
   }
+  // Sum of the earlier blocks' partials: strided over the threads, then
+  // wave sums and one fixed-order pass over the waves.
+  Tout pre = 0;
+  for (uint32_t b = threadIdx.x; b < blockIdx.x; b += kScanThreads) pre += partials[b];
+  pre = wave_sum(pre);
+  if (lane == 0) s_pre[w] = pre;
   __syncthreads();
-  const Tout p = partials[blockIdx.x];
+  Tout p = 0;
+#pragma unroll
+  for (int k = 0; k < kScanThreads / 64; ++k) p += s_pre[k];
+  if (threadIdx.x == 0 && total != nullptr && blockIdx.x == gridDim.x - 1) *total = p + s_block;
 #pragma unroll
   for (int k = 0; k < kScanItems; ++k) {
     const int64_t i = base + k * kScanThreads;
     if (i < n) out[i] = p + s_tot[k * (kScanThreads / 64) + w] + incl[k] - v[k];
   }
-}
-
-// out[i] = sum_{j<i} in[j] for i < n; *total = sum of all (if not null).
-// `partials` must hold scan_partials_count(n) elements.
-template <typename Tin, typename Tout>
-int device_exclusive_scan(const Tin *in, int64_t n, Tout *out, Tout *total, Tout *partials,
-                          hipStream_t stream, const char *what) {
-  const int64_t nb = scan_partials_count(n);
-  if (nb > 0) {
-    scan_reduce_kernel<Tin, Tout><<<dim3(static_cast<uint32_t>(nb)), dim3(kScanThreads), 0, stream>>>(
-        in, n, partials);
-  }
-  scan_partials_kernel<Tout><<<dim3(1), dim3(1024), 0, stream>>>(partials, nb, total);
-  if (nb > 0) {
-    scan_down_kernel<Tin, Tout><<<dim3(static_cast<uint32_t>(nb)), dim3(kScanThreads), 0, stream>>>(
-        in, n, partials, out);
-  }
-  return check_launch(what);
 }
 
 template <typename T>
@@ -140,6 +121,23 @@ template <typename T>
 int device_fill(T *p, int64_t n, T v, hipStream_t stream, const char *what) {
   if (n <= 0) return R2S_OK;
   fill_kernel<T><<<dim3(static_cast<uint32_t>(ceil_div(n, 256))), dim3(256), 0, stream>>>(p, n, v);
+  return check_launch(what);
+}
+
+// out[i] = sum_{j<i} in[j] for i < n; *total = sum of all (if not null).
+// `partials` must hold scan_partials_count(n) elements.
+template <typename Tin, typename Tout>
+int device_exclusive_scan(const Tin *in, int64_t n, Tout *out, Tout *total, Tout *partials,
+                          hipStream_t stream, const char *what) {
+  const int64_t nb = scan_partials_count(n);
+  if (nb == 0) {
+    if (total != nullptr) return device_fill<Tout>(total, 1, static_cast<Tout>(0), stream, what);
+    return R2S_OK;
+  }
+  scan_reduce_kernel<Tin, Tout><<<dim3(static_cast<uint32_t>(nb)), dim3(kScanThreads), 0, stream>>>(
+      in, n, partials);
+  scan_down_kernel<Tin, Tout><<<dim3(static_cast<uint32_t>(nb)), dim3(kScanThreads), 0, stream>>>(
+      in, n, partials, out, total);
   return check_launch(what);
 }
 
