@@ -278,11 +278,15 @@ __device__ __forceinline__ void slice_rows(const BwdRecord<T> &rec, const Brick 
 // three sums (W_k, s0, s1) instead of four.  Rows the record does not reach
 // test against a zero limit (every voxel fails), so the upstream
 // gradient is loaded without masks.
-template <typename T, int R>
+// kReach: the slices' row ranges come from `reach` (bit 8 * slice + row of
+// the reached rows, as voxel_bwd_chunk_kernel computes them) instead of
+// slice_rows.
+template <typename T, int R, bool kReach = false>
 __device__ __forceinline__ void voxel_brick_full(const BwdRecord<T> &rec, const Brick &b,
                                                  const T *__restrict__ v_vol, int64_t plane,
                                                  uint32_t D2, T dx0, T &T0, T &T1, T &T2, T &Y0,
-                                                 T &Z0, T &Y1, T &Z1, T &YY, T &YZ, T &ZZ) {
+                                                 T &Z0, T &Y1, T &Z1, T &YY, T &YZ, T &ZZ,
+                                                 uint64_t reach = 0) {
   using Q = typename Quad<T>::type;
   constexpr int kq = Quad<T>::n;
   T dxk[R], wk[R];
@@ -299,7 +303,13 @@ __device__ __forceinline__ void voxel_brick_full(const BwdRecord<T> &rec, const 
     if (ballot(in_slice) == 0) continue;
     const T dz = (static_cast<T>(i) + half) - rec.m[2];
     int j0, j1;
-    slice_rows(rec, b, in_slice, dz, j0, j1);
+    if constexpr (kReach) {
+      const uint32_t byte = static_cast<uint32_t>(reach >> (8 * li)) & 0xFFu;
+      j0 = b.oj + static_cast<int>(__builtin_ctz(byte | 0x100u));
+      j1 = j0 + __popc(byte) - 1;
+    } else {
+      slice_rows(rec, b, in_slice, dz, j0, j1);
+    }
     const T h4dz = rec.h[4] * dz, h5dzz = rec.h[5] * dz * dz, Bz = rec.h[2] * dz;
     const T *__restrict__ vslice = v_vol + static_cast<int64_t>(i) * plane + b.ok;
 #pragma unroll 1
@@ -492,6 +502,11 @@ __global__ __launch_bounds__(kBwdThreads) void voxel_bwd_kernel(
 
 constexpr int kChunkRows = 8;
 constexpr int kChunkWaves = 4;
+// A chunked item costs about 1.3 times a row of the dense walk (indexing,
+// the walk, the chunk sums), so a wave whose records reach more than this
+// many of their 64 x 64 (record, row) pairs takes the dense walk instead
+// (large footprints, e.g. the binary-tree model on a 128^3 volume).
+constexpr int kDenseItems = 3072;
 
 template <typename T>
 struct ChunkRecord {
@@ -551,6 +566,28 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
     reach |= static_cast<uint64_t>((run << ((j0 - b.oj) & 7)) & 0xFFu) << (8 * li);
   }
   const int n_items = __popcll(reach);
+  if (wave_sum(n_items) > kDenseItems) {  // uniform per wave
+    T T0 = 0, T1 = 0, T2 = 0, Y0 = 0, Z0 = 0, Y1 = 0, Z1 = 0, YY = 0, YZ = 0, ZZ = 0;
+    if (ballot(rec.live) != 0)
+      voxel_brick_full<T, R, true>(rec, b, v_vol, static_cast<int64_t>(plane), D2,
+                                   (static_cast<T>(b.ok) + half) - rec.m[0], T0, T1, T2, Y0, Z0,
+                                   Y1, Z1, YY, YZ, ZZ, reach);
+    if (!key_ok) return;
+    const T o = rec.o;
+    const T *qc = rec.q;
+    const T v[10] = {o * (qc[0] * T1 + qc[1] * Y0 + qc[2] * Z0),
+                     o * (qc[3] * Y0 + qc[4] * Z0 + qc[1] * T1),
+                     o * (qc[5] * Z0 + qc[4] * Y0 + qc[2] * T1),
+                     -half * o * T2,
+                     -o * Y1,
+                     -o * Z1,
+                     -half * o * YY,
+                     -o * YZ,
+                     -half * o * ZZ,
+                     T0};
+    store_row(rows, isect_src[r], v);
+    return;
+  }
   {
     ChunkRecord<T> cr;
 #pragma unroll
