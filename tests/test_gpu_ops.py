@@ -543,6 +543,64 @@ def test_voxelize_fwd_bwd(dtype, dims, ts, order):
                          outlier_atol=2e-4 * scale if f32 else None)
 
 
+def _voxel_row_reach(m3, con, op, ids, fl, dims, ts):
+    """Rows (of 64) of its brick that each record's alpha-test ellipsoid reaches."""
+    d2, d1, d0 = dims
+    n2, n1 = -(-d2 // ts), -(-d1 // ts)
+    g = fl.astype(np.int64)
+    k = ids.astype(np.int64)
+    bi, rem = k // (n1 * n2), k % (n1 * n2)
+    bj, bk = rem // n2, rem % n2
+    q = con.reshape(-1, 6).astype(np.float64)[g]
+    p00, p01, p02, p11, p12, p22 = q.T
+    # Schur complement of the x block: sigma_min(y, z) = 1/2 [y z] S [y z]^T.
+    s11, s12, s22 = p11 - p01 * p01 / p00, p12 - p01 * p02 / p00, p22 - p02 * p02 / p00
+    s_max = np.log(np.maximum(np.abs(op.astype(np.float64)[g]), 1e-300) / 1e-6)
+    m = m3.reshape(-1, 3).astype(np.float64)[g]
+    out = np.zeros(g.size)
+    for li in range(ts):
+        dz = bi * ts + li + 0.5 - m[:, 2]
+        for lj in range(ts):
+            dy = bj * ts + lj + 0.5 - m[:, 1]
+            sig = 0.5 * (s11 * dy * dy + 2 * s12 * dy * dz + s22 * dz * dz)
+            out += (sig <= s_max)
+    return out
+
+
+@pytest.mark.parametrize("log_mu,dense", [(-3.2, False), (-1.6, True)])
+def test_voxelize_bwd_chunked_and_dense_waves(log_mu, dense):
+    """Brick size 8 with every brick inside the volume runs the chunked
+    backward: small footprints take the chunked walk over the reached rows,
+    large ones (most rows of every brick reached) the dense walk.  Both
+    against the oracle, in both backward modes."""
+    dims = (32, 32, 40)
+    d, m3, con, ids, fl, off = _voxel_case(1500, 13, dims, 8, log_mu=log_mu)
+    d2, d1, d0 = dims
+    op = d["opac"]
+    # Share of the kernel's waves (64 records in list order) whose records
+    # reach more than 3072 of their 64 x 64 (record, row) pairs: a row is
+    # reached when the smallest sigma over x on its centre line is within
+    # ln(|o| / 1e-6).
+    reach = _voxel_row_reach(np32(m3), np32(con), np32(op), np32(ids), np32(fl), dims, 8)
+    n_w = reach.size // 64
+    dense_waves = (reach[:n_w * 64].reshape(n_w, 64).sum(1) > 3072).mean()
+    assert (dense_waves > 0.5) == dense, dense_waves
+    vol = W.voxelize_to_voxels_fwd(m3, con, op, off, fl, d2, d1, d0, 8)
+    v = torch.randn(vol.shape, generator=d["gen"])
+    ref = native.voxel_bwd(np32(m3), np32(con), np32(op), np32(off), np32(fl), v.numpy(), d2, d1,
+                           d0, 8)
+    for mode in ("primitive", "pixel"):
+        if mode == "primitive":
+            got = W.voxelize_to_voxels_bwd_per_gaussian(m3, con, op, off, ids, fl, v.to(DEV), d2,
+                                                        d1, d0, 8)
+        else:
+            got = W.voxelize_to_voxels_bwd(m3, con, op, off, fl, v.to(DEV), d2, d1, d0, 8)
+        for a, e, n in zip(got, ref, ("v_means3d", "v_conics", "v_opacities")):
+            scale = float(np.abs(e).max()) + 1e-30
+            assert_close(np32(a), e, f"{mode} {n}", atol=max(1e-5, 3e-6 * scale),
+                         max_outliers=e.size // 500, outlier_atol=2e-4 * scale)
+
+
 @pytest.mark.parametrize("n", [0, 1, 63, 64, 65, 4095, 4096, 4097, 100_003, 2_000_000])
 def test_mask_split_matches_torch_where(n):
     g = torch.Generator().manual_seed(n)
