@@ -370,23 +370,28 @@ def _one_sign(p, q, dxa, dya, span=15.0, margin=1.0 / 64):
     return (t.min(1) >= margin * scale) | (t.max(1) <= -margin * scale)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
-def test_absgrad_sign_split_backward(dtype):
+@pytest.mark.parametrize("dtype,shape", [(torch.float32, (128, 128)),
+                                         (torch.float64, (128, 128)),
+                                         (torch.float32, (96, 72))])
+def test_absgrad_sign_split_backward(dtype, shape):
     """The tile-size-16 absolute-gradient backward partitions each block's
     records: waves whose records keep one sign of (P d)_x and (P d)_y over
     their tile sum |w| moments instead of per-pixel absolute values.  The
-    scene has large Gaussians so that both kinds of waves run; every output
-    is checked against the oracle."""
-    W_img = H_img = 128
+    scene has large Gaussians so that both kinds of waves run (and, at 96 x
+    72, records of tiles cut by the image edge, which never qualify); every
+    output is checked against the oracle."""
+    W_img, H_img = shape
     d, m2, con, mu, op, ids, fl, off = _raster_case(1500, 11, W_img, H_img, 16, 1, dtype,
                                                      log_mu=-2.0)
+    tw, th = -(-W_img // 16), -(-H_img // 16)
     keys, g = np32(ids).astype(np.int64), np32(fl).astype(np.int64)
-    t = keys % 64
-    ox, oy = (t % 8) * 16.0, (t // 8) * 16.0
+    t = keys % (tw * th)
+    ox, oy = (t % tw) * 16.0, (t // tw) * 16.0
     m2n, cn = np32(m2).reshape(-1, 2).astype(np.float64), np32(con).reshape(-1, 3)
     a, b, c = cn[g, 0], cn[g, 1], cn[g, 2]
     dxa, dya = ox + 0.5 - m2n[g, 0], oy + 0.5 - m2n[g, 1]
     fast = _one_sign(a, b, dxa, dya) & _one_sign(b, c, dxa, dya)
+    fast &= (ox + 16 <= W_img) & (oy + 16 <= H_img)
     n_blk = fast.size // 256
     per_block = fast[:n_blk * 256].reshape(n_blk, 256).sum(1)
     assert (per_block >= 64).any() and (per_block < 256).any(), per_block
