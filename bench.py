@@ -457,7 +457,7 @@ def kernel_breakdown(proj: Projection, reps):
     nt = -(-det // 16)
     _, ids, fl = W.isect_tiles(m2, r, 16, nt, nt)
     off = W.isect_offset_encode(ids, 1, nt, nt)
-    emit_ids, isect_src = _ops._emission_order(fl, nt * nt)
+    emit_ids, isect_src = _ops.emission_order(fl, nt * nt)
     v_img = proj.v_images[0]
     n = int(fl.numel())
     rows = torch.empty(lib.r2s_rasterize_bwd_workspace_bytes(n, 4), dtype=torch.uint8,
@@ -747,10 +747,10 @@ def config1(dev, steps, warmup, chunk=256):
     pr, vx = st.projection, st.voxel
     m2 = pr.means2d[0].detach().cpu()
     con = pr.conics[0].detach().cpu()
-    om = (pr.opacity * pr.mus)[0].detach().cpu()
+    om = (pr.weights * pr.mus)[0].detach().cpu()
     r2 = pr.radii[0].cpu()
     m3, con3 = vx.means3d.detach().cpu(), vx.conics.detach().cpu()
-    op3, r3 = vx.opacity.detach().cpu(), vox.radii.cpu()
+    op3, r3 = vx.weights.detach().cpu(), vox.radii.cpu()
 
     def cpu_raster():
         a, b, c = (t.clone().requires_grad_(True) for t in (m2, con, om))
