@@ -81,10 +81,13 @@ struct Box {
   uint32_t lo[3], hi[3];  // (dim2, dim1, dim0)
 };
 
+// Brick box of Gaussian idx, restricted to the brick layers z0 <= b0 < z1
+// (dim0; the whole grid is z0 = 0, z1 = n0).
 template <typename T>
 __device__ __forceinline__ uint32_t box_3d(const T *__restrict__ means3d,
                                            const int32_t *__restrict__ radii, int64_t idx,
-                                           uint32_t ts, const uint32_t n[3], Box &b) {
+                                           uint32_t ts, const uint32_t n[3], uint32_t z0,
+                                           uint32_t z1, Box &b) {
 #pragma unroll
   for (int a = 0; a < 3; ++a) b.lo[a] = b.hi[a] = 0;
   const T r0 = static_cast<T>(radii[3 * idx]), r1 = static_cast<T>(radii[3 * idx + 1]),
@@ -98,6 +101,12 @@ __device__ __forceinline__ uint32_t box_3d(const T *__restrict__ means3d,
     const T rt = rr[a] / tsf;
     b.lo[a] = min(sat_u32(floor(c - rt)), n[a]);
     b.hi[a] = min(sat_u32(ceil(c + rt)), n[a]);
+  }
+  b.lo[2] = max(b.lo[2], z0);
+  b.hi[2] = min(b.hi[2], z1);
+  if (b.hi[2] <= b.lo[2]) {
+    b.lo[2] = b.hi[2] = z0;
+    return 0;
   }
   return (b.hi[2] - b.lo[2]) * (b.hi[1] - b.lo[1]) * (b.hi[0] - b.lo[0]);
 }
@@ -120,13 +129,62 @@ template <typename T>
 __global__ __launch_bounds__(256) void count_3d_kernel(const T *__restrict__ means3d,
                                                        const int32_t *__restrict__ radii,
                                                        int64_t N, uint32_t ts, uint32_t n2,
-                                                       uint32_t n1, uint32_t n0,
+                                                       uint32_t n1, uint32_t n0, uint32_t z0,
+                                                       uint32_t z1,
                                                        int32_t *__restrict__ counts) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (idx >= N) return;
   const uint32_t n[3] = {n2, n1, n0};
   Box b;
-  counts[idx] = static_cast<int32_t>(box_3d(means3d, radii, idx, ts, n, b));
+  counts[idx] = static_cast<int32_t>(box_3d(means3d, radii, idx, ts, n, z0, z1, b));
+}
+
+// Records per brick layer: each Gaussian's box adds its (dim2, dim1) area to
+// the layers [lo2, hi2) of a difference array diff[0..n0] (diff[lo2] += a,
+// diff[hi2] -= a), summed in LDS per block when n0 < kLayerBins.
+constexpr uint32_t kLayerBins = 1024;
+
+template <typename T>
+__global__ __launch_bounds__(256) void layer_diff_3d_kernel(const T *__restrict__ means3d,
+                                                            const int32_t *__restrict__ radii,
+                                                            int64_t N, uint32_t ts, uint32_t n2,
+                                                            uint32_t n1, uint32_t n0,
+                                                            unsigned long long *__restrict__ diff) {
+  __shared__ unsigned long long s_bins[kLayerBins];
+  const bool lds = n0 < kLayerBins;
+  if (lds) {
+    for (uint32_t k = threadIdx.x; k <= n0; k += 256) s_bins[k] = 0ull;
+    __syncthreads();
+  }
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx < N) {
+    const uint32_t n[3] = {n2, n1, n0};
+    Box b;
+    if (box_3d(means3d, radii, idx, ts, n, 0u, n0, b) > 0) {
+      const unsigned long long area =
+          static_cast<unsigned long long>(b.hi[1] - b.lo[1]) * (b.hi[0] - b.lo[0]);
+      unsigned long long *bins = lds ? s_bins : diff;
+      atomicAdd(bins + b.lo[2], area);
+      atomicAdd(bins + b.hi[2], ~area + 1ull);  // two's complement: -area
+    }
+  }
+  if (lds) {
+    __syncthreads();
+    for (uint32_t k = threadIdx.x; k <= n0; k += 256)
+      if (s_bins[k] != 0ull) atomicAdd(diff + k, s_bins[k]);
+  }
+}
+
+// counts[z] = diff[0] + ... + diff[z] for z < n0 (one thread: n0 is the
+// number of brick layers).
+__global__ void layer_prefix_kernel(const unsigned long long *__restrict__ diff, uint32_t n0,
+                                    int64_t *__restrict__ counts) {
+  if (blockIdx.x != 0 || threadIdx.x != 0) return;
+  unsigned long long run = 0ull;
+  for (uint32_t z = 0; z < n0; ++z) {
+    run += diff[z];
+    counts[z] = static_cast<int64_t>(run);
+  }
 }
 
 // ---------------------------------------------------------------- emit ---
@@ -192,11 +250,13 @@ __global__ __launch_bounds__(256) void emit_2d_kernel(
   }
 }
 
+// Keys are relative to the window's first layer: (b0 - z0) n1 n2 + b1 n2 + b2.
 template <typename T>
 __global__ __launch_bounds__(256) void emit_3d_kernel(
     const T *__restrict__ means3d, const int32_t *__restrict__ radii, int64_t N, uint32_t ts,
-    uint32_t n2, uint32_t n1, uint32_t n0, const int64_t *__restrict__ offsets, int64_t cap,
-    uint32_t *__restrict__ keys, uint32_t *__restrict__ gids) {
+    uint32_t n2, uint32_t n1, uint32_t n0, uint32_t z0, uint32_t z1,
+    const int64_t *__restrict__ offsets, int64_t cap, uint32_t *__restrict__ keys,
+    uint32_t *__restrict__ gids) {
   const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + 64 * wave_index();
   if (wave_first >= N || offsets[N] > cap) return;  // uniform per wave
   const int64_t idx = wave_first + lane_id();
@@ -204,7 +264,7 @@ __global__ __launch_bounds__(256) void emit_3d_kernel(
   Box b;
   uint32_t cnt = 0;
   if (idx < N) {
-    cnt = box_3d(means3d, radii, idx, ts, n, b);
+    cnt = box_3d(means3d, radii, idx, ts, n, z0, z1, b);
   } else {
 #pragma unroll
     for (int a = 0; a < 3; ++a) b.lo[a] = b.hi[a] = 0;
@@ -229,7 +289,7 @@ __global__ __launch_bounds__(256) void emit_3d_kernel(
     const uint32_t plane = e2j * e1j;
     const uint32_t tz = k / plane, rem = k - tz * plane;
     const uint32_t ty = rem / e2j, tx = rem - ty * e2j;
-    const uint32_t key = (l0 + tz) * (n1 * n2) + (l1 + ty) * n2 + (l2 + tx);
+    const uint32_t key = (l0 - z0 + tz) * (n1 * n2) + (l1 + ty) * n2 + (l2 + tx);
     if (t0 + lane_id() < total)
       put_record(keys, gids, base + t, key, static_cast<uint32_t>(wave_first + j));
   }
@@ -636,14 +696,16 @@ int count_2d_impl(const T *means2d, const int32_t *radii, int rect, int64_t C, i
 
 template <typename T>
 int count_3d_impl(const T *means3d, const int32_t *radii, int64_t N, uint32_t ts, uint32_t n2,
-                  uint32_t n1, uint32_t n0, int32_t *counts, int64_t *offsets, void *ws,
-                  size_t ws_bytes, r2s_stream_t st) {
+                  uint32_t n1, uint32_t n0, uint32_t z0, uint32_t z1, int32_t *counts,
+                  int64_t *offsets, void *ws, size_t ws_bytes, r2s_stream_t st) {
   clear_error();
   const char *name = "isect_tiles_3d";
   R2S_REQUIRE(N >= 0 && N <= kInt32Max, "%s: bad size N=%lld", name, (long long)N);
   R2S_REQUIRE(ts > 0, "%s: tile_size must be positive", name);
   R2S_REQUIRE(static_cast<uint64_t>(n2) * n1 * n0 <= 0xffffffffull,
               "%s: n_tiles exceeds 32 bits", name);
+  R2S_REQUIRE(z0 <= z1 && z1 <= n0, "%s: brick layers [%u, %u) outside [0, %u)", name, z0,
+              z1, n0);
   R2S_REQUIRE(offsets != nullptr, "%s: null offsets", name);
   hipStream_t stream = as_stream(st);
   if (N == 0) return device_fill<int64_t>(offsets, 1, 0, stream, name);
@@ -652,7 +714,7 @@ int count_3d_impl(const T *means3d, const int32_t *radii, int64_t N, uint32_t ts
   Carver cv(ws);
   int64_t *partials = cv.take<int64_t>(scan_partials_count(N));
   count_3d_kernel<T><<<dim3(static_cast<uint32_t>(ceil_div(N, 256))), dim3(256), 0, stream>>>(
-      means3d, radii, N, ts, n2, n1, n0, counts);
+      means3d, radii, N, ts, n2, n1, n0, z0, z1, counts);
   R2S_RETURN_IF(check_launch(name));
   return device_exclusive_scan<int32_t, int64_t>(counts, N, offsets, offsets + N, partials,
                                                  stream, name);
@@ -704,16 +766,18 @@ int emit_sort_2d_impl(const T *means2d, const int32_t *radii, int rect, int64_t 
 
 template <typename T>
 int emit_sort_3d_impl(const T *means3d, const int32_t *radii, int64_t N, uint32_t ts,
-                      uint32_t n2, uint32_t n1, uint32_t n0, const int64_t *offsets,
-                      int64_t n_isects, uint32_t end_bit, int64_t *keys, int32_t *vals,
-                      int32_t *emit_ids, int32_t *isect_src, void *ws, size_t ws_bytes,
-                      r2s_stream_t st) {
+                      uint32_t n2, uint32_t n1, uint32_t n0, uint32_t z0, uint32_t z1,
+                      const int64_t *offsets, int64_t n_isects, uint32_t end_bit, int64_t *keys,
+                      int32_t *vals, int32_t *emit_ids, int32_t *isect_src, void *ws,
+                      size_t ws_bytes, r2s_stream_t st) {
   clear_error();
   const char *name = "isect_tiles_3d";
   R2S_REQUIRE(N >= 0 && N <= kInt32Max, "%s: bad size", name);
   R2S_REQUIRE(ts > 0, "%s: tile_size must be positive", name);
-  R2S_RETURN_IF(check_sort_args(n_isects, end_bit, static_cast<int64_t>(n2) * n1 * n0, ws,
-                                ws_bytes, keys, vals, name));
+  R2S_REQUIRE(z0 <= z1 && z1 <= n0, "%s: brick layers [%u, %u) outside [0, %u)", name, z0,
+              z1, n0);
+  const int64_t n_keys = static_cast<int64_t>(n2) * n1 * (z1 - z0);
+  R2S_RETURN_IF(check_sort_args(n_isects, end_bit, n_keys, ws, ws_bytes, keys, vals, name));
   if (n_isects == 0) return R2S_OK;
   R2S_REQUIRE(means3d && radii && offsets, "%s: null pointer", name);
   hipStream_t stream = as_stream(st);
@@ -724,10 +788,35 @@ int emit_sort_3d_impl(const T *means3d, const int32_t *radii, int64_t N, uint32_
   uint32_t *gids = emit_ids != nullptr ? reinterpret_cast<uint32_t *>(emit_ids) : s.g0;
   s.gid0 = gids;
   emit_3d_kernel<T><<<dim3(static_cast<uint32_t>(ceil_div(N, 256))), dim3(256), 0, stream>>>(
-      means3d, radii, N, ts, n2, n1, n0, offsets, n_isects, s.k0, gids);
+      means3d, radii, N, ts, n2, n1, n0, z0, z1, offsets, n_isects, s.k0, gids);
   R2S_RETURN_IF(check_launch(name));
-  return radix_sort(s, offsets + N, n_isects, key_bits_for(static_cast<int64_t>(n2) * n1 * n0),
-                    keys, vals, emit_ids != nullptr, isect_src, stream);
+  return radix_sort(s, offsets + N, n_isects, key_bits_for(n_keys), keys, vals,
+                    emit_ids != nullptr, isect_src, stream);
+}
+
+template <typename T>
+int layer_counts_3d_impl(const T *means3d, const int32_t *radii, int64_t N, uint32_t ts,
+                         uint32_t n2, uint32_t n1, uint32_t n0, int64_t *counts, void *ws,
+                         size_t ws_bytes, r2s_stream_t st) {
+  clear_error();
+  const char *name = "isect_tiles_3d (layer counts)";
+  R2S_REQUIRE(N >= 0 && N <= kInt32Max, "%s: bad size N=%lld", name, (long long)N);
+  R2S_REQUIRE(ts > 0, "%s: tile_size must be positive", name);
+  R2S_REQUIRE(n0 >= 1 && static_cast<uint64_t>(n2) * n1 * n0 <= 0xffffffffull,
+              "%s: bad brick grid", name);
+  R2S_REQUIRE(counts != nullptr, "%s: null counts", name);
+  hipStream_t stream = as_stream(st);
+  if (N == 0) return device_fill<int64_t>(counts, n0, 0, stream, name);
+  R2S_REQUIRE(means3d && radii, "%s: null pointer", name);
+  R2S_RETURN_IF(check_workspace(ws, ws_bytes, (static_cast<int64_t>(n0) + 1) * 8, name));
+  auto *diff = static_cast<unsigned long long *>(ws);
+  R2S_RETURN_IF(device_fill<int64_t>(reinterpret_cast<int64_t *>(diff), n0 + 1, 0, stream,
+                                     name));
+  layer_diff_3d_kernel<T><<<dim3(static_cast<uint32_t>(ceil_div(N, 256))), dim3(256), 0,
+                            stream>>>(means3d, radii, N, ts, n2, n1, n0, diff);
+  R2S_RETURN_IF(check_launch(name));
+  layer_prefix_kernel<<<dim3(1), dim3(1), 0, stream>>>(diff, n0, counts);
+  return check_launch(name);
 }
 
 }  // namespace
@@ -763,8 +852,8 @@ int64_t r2s_isect_workspace_bytes(int64_t n_items, int64_t n_isects, uint32_t en
                                uint32_t ts, uint32_t n2, uint32_t n1, uint32_t n0,            \
                                int32_t *counts, int64_t *offsets, void *ws, size_t ws_bytes,  \
                                r2s_stream_t st) {                                             \
-    return r2s::count_3d_impl<T>(means3d, radii, N, ts, n2, n1, n0, counts, offsets, ws,      \
-                                 ws_bytes, st);                                               \
+    return r2s::count_3d_impl<T>(means3d, radii, N, ts, n2, n1, n0, 0u, n0, counts, offsets,  \
+                                 ws, ws_bytes, st);                                           \
   }                                                                                           \
   int r2s_isect_emit_sort_3d_##SUF(const T *means3d, const int32_t *radii, int64_t N,        \
                                    uint32_t ts, uint32_t n2, uint32_t n1, uint32_t n0,        \
@@ -772,9 +861,33 @@ int64_t r2s_isect_workspace_bytes(int64_t n_items, int64_t n_isects, uint32_t en
                                    uint32_t end_bit, int64_t *keys, int32_t *vals,            \
                                    int32_t *emit_ids, int32_t *isect_src, void *ws,          \
                                    size_t ws_bytes, r2s_stream_t st) {                        \
-    return r2s::emit_sort_3d_impl<T>(means3d, radii, N, ts, n2, n1, n0, offsets, n_isects,    \
-                                     end_bit, keys, vals, emit_ids, isect_src, ws, ws_bytes,  \
-                                     st);                                                     \
+    return r2s::emit_sort_3d_impl<T>(means3d, radii, N, ts, n2, n1, n0, 0u, n0,               \
+                                     offsets, n_isects, end_bit, keys, vals, emit_ids,        \
+                                     isect_src, ws, ws_bytes, st);                            \
+  }                                                                                           \
+  int r2s_isect_layer_counts_3d_##SUF(const T *means3d, const int32_t *radii, int64_t N,     \
+                                      uint32_t ts, uint32_t n2, uint32_t n1, uint32_t n0,     \
+                                      int64_t *counts, void *ws, size_t ws_bytes,             \
+                                      r2s_stream_t st) {                                      \
+    return r2s::layer_counts_3d_impl<T>(means3d, radii, N, ts, n2, n1, n0, counts, ws,        \
+                                        ws_bytes, st);                                        \
+  }                                                                                           \
+  int r2s_isect_count_3d_slab_##SUF(const T *means3d, const int32_t *radii, int64_t N,       \
+                                    uint32_t ts, uint32_t n2, uint32_t n1, uint32_t n0,       \
+                                    uint32_t z0, uint32_t z1, int32_t *counts,                \
+                                    int64_t *offsets, void *ws, size_t ws_bytes,              \
+                                    r2s_stream_t st) {                                        \
+    return r2s::count_3d_impl<T>(means3d, radii, N, ts, n2, n1, n0, z0, z1, counts, offsets,  \
+                                 ws, ws_bytes, st);                                           \
+  }                                                                                           \
+  int r2s_isect_emit_sort_3d_slab_##SUF(                                                      \
+      const T *means3d, const int32_t *radii, int64_t N, uint32_t ts, uint32_t n2,            \
+      uint32_t n1, uint32_t n0, uint32_t z0, uint32_t z1, const int64_t *offsets,             \
+      int64_t n_isects, uint32_t end_bit, int64_t *keys, int32_t *vals, int32_t *emit_ids,    \
+      int32_t *isect_src, void *ws, size_t ws_bytes, r2s_stream_t st) {                       \
+    return r2s::emit_sort_3d_impl<T>(means3d, radii, N, ts, n2, n1, n0, z0, z1, offsets,      \
+                                     n_isects, end_bit, keys, vals, emit_ids, isect_src, ws,  \
+                                     ws_bytes, st);                                           \
   }
 
 R2S_BIN_API(f32, float)

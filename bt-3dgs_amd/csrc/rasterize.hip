@@ -778,8 +778,9 @@ int check_raster_args(int64_t n_isects, int64_t C, int64_t N, uint32_t W, uint32
                       uint32_t ts, uint32_t tw, uint32_t th, const char *name) {
   R2S_REQUIRE(C >= 0 && N >= 0 && C * N <= kInt32Max, "%s: bad size C=%lld N=%lld", name,
               (long long)C, (long long)N);
-  R2S_REQUIRE(ts > 0 && ts * ts <= 1024, "%s: tile_size must be positive with tile_size**2 <= 1024",
-              name);
+  // ts <= 32 first: ts * ts in 32 bits wraps for ts >= 65536.
+  R2S_REQUIRE(ts > 0 && ts <= 32 && ts * ts <= 1024,
+              "%s: tile_size must be positive with tile_size**2 <= 1024", name);
   R2S_REQUIRE(n_isects >= 0 && n_isects <= kInt32Max, "%s: bad n_isects %lld", name,
               (long long)n_isects);
   R2S_REQUIRE(static_cast<uint64_t>(tw) * ts >= W && static_cast<uint64_t>(th) * ts >= H,

@@ -88,8 +88,8 @@ template <typename T, int R>
 __global__ __launch_bounds__(1024) void voxel_fwd_kernel(
     const T *__restrict__ means3d, const T *__restrict__ conics, const T *__restrict__ opac,
     const int32_t *__restrict__ tile_offsets, const int32_t *__restrict__ flatten_ids,
-    int64_t n_isects, uint32_t n_keys, int64_t N, uint32_t D2, uint32_t D1, uint32_t D0,
-    uint32_t ts, uint32_t n2, uint32_t n1, T *__restrict__ volume) {
+    int64_t n_isects, uint32_t n_keys, uint32_t koff, int64_t N, uint32_t D2, uint32_t D1,
+    uint32_t D0, uint32_t ts, uint32_t n2, uint32_t n1, T *__restrict__ volume) {
   using V4 = typename Vec<T>::v4;
   extern __shared__ double smem_raw[];
   const uint32_t nt = blockDim.x;
@@ -97,8 +97,8 @@ __global__ __launch_bounds__(1024) void voxel_fwd_kernel(
   // Per staged record: {mx, my, mz, o}, {h0, h1, h2, h3}, {h4, h5, limit bits, 0}.
   V4 *s_rec = reinterpret_cast<V4 *>(smem_raw);
 
-  const uint32_t key = xcd_swizzle(blockIdx.x, n_keys);
-  const Brick b = brick_of(key, n2, n1, ts, D2, D1, D0);
+  const uint32_t key = xcd_swizzle(blockIdx.x, n_keys);  // in the lists (koff: the grid's)
+  const Brick b = brick_of(key + koff, n2, n1, ts, D2, D1, D0);
   const uint32_t tid = threadIdx.x;
   const uint32_t per_row = ts / R;
   const int lk0 = static_cast<int>((tid % per_row) * R);
@@ -368,8 +368,8 @@ __global__ __launch_bounds__(kBwdThreads) void voxel_bwd_kernel(
     const T *__restrict__ means3d, const T *__restrict__ conics, const T *__restrict__ opac,
     const int32_t *__restrict__ tile_offsets, const int64_t *__restrict__ isect_ids,
     const int32_t *__restrict__ flatten_ids, const int32_t *__restrict__ isect_src,
-    int64_t n_isects, uint32_t n_keys, int64_t N, const T *__restrict__ v_vol, uint32_t D2,
-    uint32_t D1, uint32_t D0, uint32_t ts, uint32_t n2, uint32_t n1, bool vec,
+    int64_t n_isects, uint32_t n_keys, uint32_t koff, int64_t N, const T *__restrict__ v_vol,
+    uint32_t D2, uint32_t D1, uint32_t D0, uint32_t ts, uint32_t n2, uint32_t n1, bool vec,
     T *__restrict__ v_means, T *__restrict__ v_conics, T *__restrict__ v_opac,
     T *__restrict__ rows) {
   // Consecutive blocks (neighbouring tiles, which share Gaussians) on one XCD.
@@ -389,7 +389,7 @@ __global__ __launch_bounds__(kBwdThreads) void voxel_bwd_kernel(
     key = wave_record_key(tile_offsets, n_keys, n_isects, rb, r);
   }
   const int64_t g = key_ok ? static_cast<int64_t>(flatten_ids[r]) : -1;
-  const Brick b = brick_of(key, n2, n1, static_cast<uint32_t>(nts), D2, D1, D0);
+  const Brick b = brick_of(key + koff, n2, n1, static_cast<uint32_t>(nts), D2, D1, D0);
   BwdRecord<T> rec;
   load_bwd_record(means3d, conics, opac, g, N, key_ok, b, rec);
   const T half = static_cast<T>(0.5);
@@ -520,8 +520,8 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
     const T *__restrict__ means3d, const T *__restrict__ conics, const T *__restrict__ opac,
     const int32_t *__restrict__ tile_offsets, const int64_t *__restrict__ isect_ids,
     const int32_t *__restrict__ flatten_ids, const int32_t *__restrict__ isect_src,
-    int64_t n_isects, uint32_t n_keys, int64_t N, const T *__restrict__ v_vol, uint32_t D2,
-    uint32_t D1, uint32_t D0, uint32_t n2, uint32_t n1, T *__restrict__ rows) {
+    int64_t n_isects, uint32_t n_keys, uint32_t koff, int64_t N, const T *__restrict__ v_vol,
+    uint32_t D2, uint32_t D1, uint32_t D0, uint32_t n2, uint32_t n1, T *__restrict__ rows) {
   constexpr int R = kChunkRows;
   using Q = typename Quad<T>::type;
   constexpr int kq = Quad<T>::n;
@@ -545,7 +545,7 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
     key = wave_record_key(tile_offsets, n_keys, n_isects, rb, r);
   }
   const int64_t g = key_ok ? static_cast<int64_t>(flatten_ids[r]) : -1;
-  const Brick b = brick_of(key, n2, n1, R, D2, D1, D0);
+  const Brick b = brick_of(key + koff, n2, n1, R, D2, D1, D0);
   BwdRecord<T> rec;
   load_bwd_record(means3d, conics, opac, g, N, key_ok, b, rec);
   const T half = static_cast<T>(0.5);
@@ -742,60 +742,77 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
   store_row(rows, isect_src[r], v);
 }
 
+// n0 brick layers of lists from layer z0 on (the whole grid: z0 = 0 and
+// n0 ts >= D0; a z-slab: z0 + n0 layers within the grid).
 int check_voxel_args(int64_t n_isects, int64_t N, uint32_t D2, uint32_t D1, uint32_t D0,
-                     uint32_t ts, uint32_t n2, uint32_t n1, uint32_t n0, const char *name) {
+                     uint32_t ts, uint32_t n2, uint32_t n1, uint32_t n0, const char *name,
+                     uint32_t z0 = 0, bool slab = false) {
   R2S_REQUIRE(N >= 0 && N <= kInt32Max, "%s: bad size N=%lld", name, (long long)N);
-  R2S_REQUIRE(ts > 0 && ts * ts * ts <= 1024,
+  // ts <= 10 first: ts^3 in 32 bits wraps for ts >= 1626.
+  R2S_REQUIRE(ts > 0 && ts <= 10 && ts * ts * ts <= 1024,
               "%s: tile_size must be positive with tile_size**3 <= 1024", name);
   R2S_REQUIRE(n_isects >= 0 && n_isects <= kInt32Max, "%s: bad n_isects", name);
   R2S_REQUIRE(static_cast<uint64_t>(n2) * ts >= D2 && static_cast<uint64_t>(n1) * ts >= D1 &&
-                  static_cast<uint64_t>(n0) * ts >= D0,
+                  (slab || static_cast<uint64_t>(n0) * ts >= D0),
               "%s: brick grid does not cover the volume", name);
+  R2S_REQUIRE(!slab || (static_cast<uint64_t>(z0) + n0) * ts < static_cast<uint64_t>(D0) + ts,
+              "%s: brick layers [%u, %u) outside the volume", name, z0, z0 + n0);
   R2S_REQUIRE(static_cast<uint64_t>(n2) * ts <= 0x7fffffffull &&
                   static_cast<uint64_t>(n1) * ts <= 0x7fffffffull &&
                   static_cast<uint64_t>(n0) * ts <= 0x7fffffffull,
               "%s: brick grid too large", name);
-  R2S_REQUIRE(static_cast<uint64_t>(n2) * n1 * n0 <= 0x7fffffffull, "%s: too many bricks", name);
+  R2S_REQUIRE(static_cast<uint64_t>(n2) * n1 * (static_cast<uint64_t>(z0) + n0) <=
+                  0x7fffffffull,
+              "%s: too many bricks", name);
   return R2S_OK;
 }
 
 template <typename T, int R>
 void launch_voxel_fwd(const T *means3d, const T *conics, const T *opac,
                       const int32_t *tile_offsets, const int32_t *flatten_ids, int64_t n_isects,
-                      uint32_t n_keys, int64_t N, uint32_t D2, uint32_t D1, uint32_t D0,
-                      uint32_t ts, uint32_t n2, uint32_t n1, T *volume, hipStream_t stream) {
+                      uint32_t n_keys, uint32_t koff, int64_t N, uint32_t D2, uint32_t D1,
+                      uint32_t D0, uint32_t ts, uint32_t n2, uint32_t n1, T *volume,
+                      hipStream_t stream) {
   const uint32_t nt = ts * ts * (ts / R);
   const size_t smem =
       min(nt, kFwdBatch) * (3 * sizeof(typename Vec<T>::v4));
   voxel_fwd_kernel<T, R><<<dim3(n_keys), dim3(nt), smem, stream>>>(
-      means3d, conics, opac, tile_offsets, flatten_ids, n_isects, n_keys, N, D2, D1, D0, ts, n2,
-      n1, volume);
+      means3d, conics, opac, tile_offsets, flatten_ids, n_isects, n_keys, koff, N, D2, D1, D0, ts,
+      n2, n1, volume);
 }
 
+// slab: the lists are those of brick layers [z0, z0 + n0) (keys relative to
+// layer z0) and only that z-range of the whole volume is written.
 template <typename T>
 int voxel_fwd_impl(const T *means3d, const T *conics, const T *opac,
                    const int32_t *tile_offsets, const int32_t *flatten_ids, int64_t n_isects,
                    int64_t N, uint32_t D2, uint32_t D1, uint32_t D0, uint32_t ts, uint32_t n2,
-                   uint32_t n1, uint32_t n0, T *volume, r2s_stream_t st) {
+                   uint32_t n1, uint32_t n0, T *volume, r2s_stream_t st, uint32_t z0 = 0,
+                   bool slab = false) {
   clear_error();
   const char *name = "voxelize_to_voxels_fwd";
-  R2S_RETURN_IF(check_voxel_args(n_isects, N, D2, D1, D0, ts, n2, n1, n0, name));
-  const int64_t n_vox = static_cast<int64_t>(D2) * D1 * D0;
-  if (n_vox == 0) return R2S_OK;
+  R2S_RETURN_IF(check_voxel_args(n_isects, N, D2, D1, D0, ts, n2, n1, n0, name, z0, slab));
+  // Voxel slices [i0, i1) of the layers' z-range.
+  const int64_t i0 = static_cast<int64_t>(z0) * ts;
+  const int64_t i1 = slab ? std::min<int64_t>(static_cast<int64_t>(z0 + n0) * ts, D0) : D0;
+  const int64_t plane = static_cast<int64_t>(D2) * D1;
+  const int64_t n_vox = plane * (i1 - i0);
+  if (n_vox <= 0) return R2S_OK;
   R2S_REQUIRE(volume != nullptr, "%s: null volume", name);
   hipStream_t stream = as_stream(st);
-  if (N == 0 || n_isects == 0) return device_fill<T>(volume, n_vox, static_cast<T>(0), stream, name);
+  if (N == 0 || n_isects == 0)
+    return device_fill<T>(volume + i0 * plane, n_vox, static_cast<T>(0), stream, name);
   R2S_REQUIRE(means3d && conics && opac && tile_offsets && flatten_ids, "%s: null pointer", name);
-  const uint32_t n_keys = n2 * n1 * n0;
+  const uint32_t n_keys = n2 * n1 * n0, koff = z0 * n1 * n2;
   if (ts == 8)
-    launch_voxel_fwd<T, 8>(means3d, conics, opac, tile_offsets, flatten_ids, n_isects, n_keys, N,
-                           D2, D1, D0, ts, n2, n1, volume, stream);
+    launch_voxel_fwd<T, 8>(means3d, conics, opac, tile_offsets, flatten_ids, n_isects, n_keys,
+                           koff, N, D2, D1, D0, ts, n2, n1, volume, stream);
   else if (ts == 16)
     launch_voxel_fwd<T, 16>(means3d, conics, opac, tile_offsets, flatten_ids, n_isects, n_keys,
-                            N, D2, D1, D0, ts, n2, n1, volume, stream);
+                            koff, N, D2, D1, D0, ts, n2, n1, volume, stream);
   else
-    launch_voxel_fwd<T, 1>(means3d, conics, opac, tile_offsets, flatten_ids, n_isects, n_keys, N,
-                           D2, D1, D0, ts, n2, n1, volume, stream);
+    launch_voxel_fwd<T, 1>(means3d, conics, opac, tile_offsets, flatten_ids, n_isects, n_keys,
+                           koff, N, D2, D1, D0, ts, n2, n1, volume, stream);
   return check_launch(name);
 }
 
@@ -803,18 +820,18 @@ template <typename T, int R, bool kExact>
 void launch_voxel_bwd(const T *means3d, const T *conics, const T *opac,
                       const int32_t *tile_offsets, const int64_t *isect_ids,
                       const int32_t *flatten_ids, const int32_t *isect_src, int64_t n_isects,
-                      uint32_t n_keys, int64_t N, const T *v_vol, uint32_t D2, uint32_t D1,
-                      uint32_t D0, uint32_t ts, uint32_t n2, uint32_t n1, bool vec, T *v_means,
-                      T *v_conics, T *v_opac, T *rows, hipStream_t stream) {
+                      uint32_t n_keys, uint32_t koff, int64_t N, const T *v_vol, uint32_t D2,
+                      uint32_t D1, uint32_t D0, uint32_t ts, uint32_t n2, uint32_t n1, bool vec,
+                      T *v_means, T *v_conics, T *v_opac, T *rows, hipStream_t stream) {
   const dim3 grid(static_cast<uint32_t>(ceil_div(n_isects, kBwdThreads)));
   if (rows != nullptr)
     voxel_bwd_kernel<T, R, kExact, true><<<grid, dim3(kBwdThreads), 0, stream>>>(
         means3d, conics, opac, tile_offsets, isect_ids, flatten_ids, isect_src, n_isects, n_keys,
-        N, v_vol, D2, D1, D0, ts, n2, n1, vec, v_means, v_conics, v_opac, rows);
+        koff, N, v_vol, D2, D1, D0, ts, n2, n1, vec, v_means, v_conics, v_opac, rows);
   else
     voxel_bwd_kernel<T, R, kExact, false><<<grid, dim3(kBwdThreads), 0, stream>>>(
         means3d, conics, opac, tile_offsets, isect_ids, flatten_ids, isect_src, n_isects, n_keys,
-        N, v_vol, D2, D1, D0, ts, n2, n1, vec, v_means, v_conics, v_opac, rows);
+        koff, N, v_vol, D2, D1, D0, ts, n2, n1, vec, v_means, v_conics, v_opac, rows);
 }
 
 int64_t voxel_rows_bytes(int64_t n_isects, int dtype_bytes) {
@@ -848,12 +865,13 @@ int voxel_bwd_impl(const T *means3d, const T *conics, const T *opac,
                    const int32_t *isect_src, int64_t n_isects, const T *v_vol, int64_t N,
                    uint32_t D2, uint32_t D1, uint32_t D0, uint32_t ts, uint32_t n2, uint32_t n1,
                    uint32_t n0, T *v_means, T *v_conics, T *v_opac, void *ws, size_t ws_bytes,
-                   bool two_pass, r2s_stream_t st, bool rows_only = false) {
+                   bool two_pass, r2s_stream_t st, bool rows_only = false, uint32_t z0 = 0,
+                   bool slab = false) {
   clear_error();
   const char *name = two_pass   ? "voxelize_to_voxels_bwd (two-pass)"
                      : isect_ids ? "voxelize_to_voxels_bwd_per_gaussian"
                                  : "voxelize_to_voxels_bwd";
-  R2S_RETURN_IF(check_voxel_args(n_isects, N, D2, D1, D0, ts, n2, n1, n0, name));
+  R2S_RETURN_IF(check_voxel_args(n_isects, N, D2, D1, D0, ts, n2, n1, n0, name, z0, slab));
   if (N == 0) return R2S_OK;
   const int64_t n_vox = static_cast<int64_t>(D2) * D1 * D0;
   if (n_isects == 0 || n_vox == 0) {  // the two-pass form still stores its (zero) outputs
@@ -875,21 +893,21 @@ int voxel_bwd_impl(const T *means3d, const T *conics, const T *opac,
                 name);
     rows = static_cast<T *>(ws);
   }
-  const uint32_t n_keys = n2 * n1 * n0;
+  const uint32_t n_keys = n2 * n1 * n0, koff = z0 * n1 * n2;
   hipStream_t stream = as_stream(st);
   // 16-byte loads of gradient rows when every row segment starts aligned.
   const bool vec = vec_rows_ok<T>(v_vol, D2, ts);
 #define R2S_VOXEL_BWD_R(RR, EXACT)                                                             \
   launch_voxel_bwd<T, RR, EXACT>(means3d, conics, opac, tile_offsets, isect_ids, flatten_ids,  \
-                                 isect_src, n_isects, n_keys, N, v_vol, D2, D1, D0, ts, n2, n1, \
-                                 vec, v_means, v_conics, v_opac, rows, stream)
+                                 isect_src, n_isects, n_keys, koff, N, v_vol, D2, D1, D0, ts,  \
+                                 n2, n1, vec, v_means, v_conics, v_opac, rows, stream)
   if (ts == 8 && rows != nullptr && vec && D2 % 8 == 0 && D1 % 8 == 0 && D0 % 8 == 0 &&
       n_vox < (int64_t{1} << 31))
     voxel_bwd_chunk_kernel<T>
         <<<dim3(static_cast<uint32_t>(ceil_div(n_isects, 64 * kChunkWaves))),
            dim3(64 * kChunkWaves), 0, stream>>>(means3d, conics, opac, tile_offsets, isect_ids,
-                                                flatten_ids, isect_src, n_isects, n_keys, N, v_vol,
-                                                D2, D1, D0, n2, n1, rows);
+                                                flatten_ids, isect_src, n_isects, n_keys, koff, N,
+                                                v_vol, D2, D1, D0, n2, n1, rows);
   else if (ts == 8)
     R2S_VOXEL_BWD_R(8, true);
   else if (ts == 4)
@@ -944,6 +962,26 @@ int64_t r2s_voxelize_bwd_workspace_bytes(int64_t n_isects, int dtype_bytes) {
     return r2s::voxel_bwd_impl<T>(means3d, conics, opac, tile_offsets, isect_ids, flatten_ids, \
                                   emit_ids, isect_src, n_isects, v_vol, N, D2, D1, D0, ts, n2, \
                                   n1, n0, v_means, v_conics, v_opac, ws, ws_bytes, true, st);  \
+  }                                                                                            \
+  int r2s_voxelize_fwd_slab_##SUF(const T *means3d, const T *conics, const T *opac,            \
+                                  const int32_t *tile_offsets, const int32_t *flatten_ids,     \
+                                  int64_t n_isects, int64_t N, uint32_t D2, uint32_t D1,       \
+                                  uint32_t D0, uint32_t ts, uint32_t n2, uint32_t n1,          \
+                                  uint32_t z0, uint32_t nz, T *volume, r2s_stream_t st) {      \
+    return r2s::voxel_fwd_impl<T>(means3d, conics, opac, tile_offsets, flatten_ids, n_isects,  \
+                                  N, D2, D1, D0, ts, n2, n1, nz, volume, st, z0, true);        \
+  }                                                                                            \
+  int r2s_voxelize_bwd_emit_slab_##SUF(                                                        \
+      const T *means3d, const T *conics, const T *opac, const int32_t *tile_offsets,           \
+      const int64_t *isect_ids, const int32_t *flatten_ids, const int32_t *emit_ids,           \
+      const int32_t *isect_src, int64_t n_isects, const T *v_vol, int64_t N, uint32_t D2,      \
+      uint32_t D1, uint32_t D0, uint32_t ts, uint32_t n2, uint32_t n1, uint32_t z0,            \
+      uint32_t nz, T *v_means, T *v_conics, T *v_opac, void *ws, size_t ws_bytes,              \
+      r2s_stream_t st) {                                                                       \
+    return r2s::voxel_bwd_impl<T>(means3d, conics, opac, tile_offsets, isect_ids, flatten_ids, \
+                                  emit_ids, isect_src, n_isects, v_vol, N, D2, D1, D0, ts, n2, \
+                                  n1, nz, v_means, v_conics, v_opac, ws, ws_bytes, true, st,   \
+                                  false, z0, true);                                            \
   }
 
 #define R2S_VOXEL_STAGE_API(SUF, T)                                                            \
@@ -957,6 +995,17 @@ int64_t r2s_voxelize_bwd_workspace_bytes(int64_t n_isects, int dtype_bytes) {
                                   nullptr, isect_src, n_isects, v_vol, N, D2, D1, D0, ts, n2,  \
                                   n1, n0, nullptr, nullptr, nullptr, rows, rows_bytes, true,   \
                                   st, true);                                                   \
+  }                                                                                            \
+  int r2s_voxelize_bwd_rows_slab_##SUF(                                                        \
+      const T *means3d, const T *conics, const T *opac, const int32_t *tile_offsets,           \
+      const int64_t *isect_ids, const int32_t *flatten_ids, const int32_t *isect_src,          \
+      int64_t n_isects, const T *v_vol, int64_t N, uint32_t D2, uint32_t D1, uint32_t D0,      \
+      uint32_t ts, uint32_t n2, uint32_t n1, uint32_t z0, uint32_t nz, void *rows,             \
+      size_t rows_bytes, r2s_stream_t st) {                                                    \
+    return r2s::voxel_bwd_impl<T>(means3d, conics, opac, tile_offsets, isect_ids, flatten_ids, \
+                                  nullptr, isect_src, n_isects, v_vol, N, D2, D1, D0, ts, n2,  \
+                                  n1, nz, nullptr, nullptr, nullptr, rows, rows_bytes, true,   \
+                                  st, true, z0, true);                                         \
   }                                                                                            \
   int r2s_voxelize_bwd_reduce_##SUF(const T *rows, const int32_t *emit_ids, int64_t n_isects,  \
                                     int64_t N, T *v_means, T *v_conics, T *v_opac,             \

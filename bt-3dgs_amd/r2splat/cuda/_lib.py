@@ -61,6 +61,17 @@ _FLOAT_OPS = {
     "voxelize_bwd_reduce": [_p, _p, _i64, _i64, _p, _p, _p, _p],
     "voxelize_bwd_emit": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _u32, _u32, _u32, _u32,
                           _u32, _u32, _u32, _p, _p, _p, _p, _sz, _p],
+    "isect_layer_counts_3d": [_p, _p, _i64, _u32, _u32, _u32, _u32, _p, _p, _sz, _p],
+    "isect_count_3d_slab": [_p, _p, _i64, _u32, _u32, _u32, _u32, _u32, _u32, _p, _p, _p, _sz,
+                            _p],
+    "isect_emit_sort_3d_slab": [_p, _p, _i64, _u32, _u32, _u32, _u32, _u32, _u32, _p, _i64, _u32,
+                                _p, _p, _p, _p, _p, _sz, _p],
+    "voxelize_fwd_slab": [_p, _p, _p, _p, _p, _i64, _i64, _u32, _u32, _u32, _u32, _u32, _u32,
+                          _u32, _u32, _p, _p],
+    "voxelize_bwd_rows_slab": [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _u32, _u32, _u32, _u32,
+                               _u32, _u32, _u32, _u32, _p, _sz, _p],
+    "voxelize_bwd_emit_slab": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _u32, _u32, _u32,
+                               _u32, _u32, _u32, _u32, _u32, _p, _p, _p, _p, _sz, _p],
 }
 
 _PLAIN = {

@@ -13,7 +13,8 @@ from __future__ import annotations
 import ctypes
 import math
 import threading
-from typing import Optional, Tuple
+import warnings
+from typing import NamedTuple, Optional, Tuple
 
 import torch
 
@@ -102,11 +103,16 @@ def _note_count(key, n: int) -> None:
     del hist[:-_COUNT_HISTORY_LEN]
 
 
+TOO_MANY = object()  # _emit_and_sort: the count exceeds max_records
+
+
 def _emit_and_sort(launch, offsets: Tensor, n_items: int, n_keys: int, op: str,
-                   dev: torch.device, kind: str):
+                   dev: torch.device, kind: str, max_records: Optional[int] = None):
     """The emit + sort half of a binning op (IsectTiles.cpp:100-169): returns
-    (isect_ids, flatten_ids, emit_ids, isect_src), or None without records.
-    launch(capacity, end_bit, outputs, workspace) enqueues the library call."""
+    (isect_ids, flatten_ids, emit_ids, isect_src), or None without records,
+    or TOO_MANY when there are more than max_records records (nothing
+    allocated for them).  launch(capacity, end_bit, outputs, workspace)
+    enqueues the library call."""
     lib = _lib()
     end_bit = _end_bit(n_keys)
     key = (dev.index, kind, n_items, n_keys)
@@ -141,6 +147,8 @@ def _emit_and_sort(launch, offsets: Tensor, n_items: int, n_keys: int, op: str,
     else:
         n = int(offsets[n_items].item())  # the one host read-back (IsectTiles.cpp:100)
         _note_count(key, n)
+    if max_records is not None and n > max_records:
+        return TOO_MANY
     if n == 0:
         return None
     _check_record_count(n, op)
@@ -149,26 +157,56 @@ def _emit_and_sort(launch, offsets: Tensor, n_items: int, n_keys: int, op: str,
     return outs
 
 
-# The binning ops also describe their records in emission order (id-major,
-# before the sort by tile) on the flatten_ids tensor they return: emit_ids[e]
-# is the id of emitted record e, isect_src[r] the emission index of sorted
-# record r.  The backward ops then run the two-pass kernels, which store each
-# record's partials at its emission index and sum them per Gaussian, instead
-# of one device-scope atomic per record and partial.  Any other flatten_ids
-# (built elsewhere, or modified in place since) takes the one-pass kernels.
-USE_EMISSION_ORDER = True
+# Binned records.  Besides the reference's sorted lists, the binning kernels
+# describe the records in emission order (Gaussian-major, before the sort by
+# tile): emit_ids[e] is the id of emitted record e and isect_src[r] the
+# emission index of sorted record r.  With them the backward ops run the
+# two-pass kernels, which store each record's partials at its emission index
+# and then sum them per Gaussian, instead of one device-scope atomic per
+# record and partial (about 3x slower at the headline shape).
+
+
+class TileLists(NamedTuple):
+    """Output of :func:`bin_tiles_2d` / :func:`bin_tiles_3d`."""
+
+    tiles_per_gauss: Tensor
+    isect_ids: Tensor   # int64 tile keys, sorted
+    flatten_ids: Tensor  # int32 ids in (key, emission) order
+    emit_ids: Optional[Tensor]   # None when there are no records
+    isect_src: Optional[Tensor]
+
+    @property
+    def emission(self) -> Optional[Tuple[Tensor, Tensor]]:
+        return None if self.emit_ids is None else (self.emit_ids, self.isect_src)
+
+
+# The reference's operator signatures (isect_tiles -> rasterize_to_pixels_bwd*)
+# pass only flatten_ids between the ops.  So that those callers still get the
+# two-pass backward, isect_tiles / isect_tiles_3d also attach the emission
+# arrays to the flatten_ids tensor they return (attribute _EMIT_ATTR, with
+# the tensor's version counter).  A flatten_ids that is not the returned
+# tensor itself, unmodified -- a clone, slice, .to() copy, or a list built
+# elsewhere -- is not in the table; the backward then runs the one-pass
+# kernels, counts the call in PATH_COUNTS["one_pass"] and warns once per
+# process.  r2splat.ops passes the arrays explicitly and never relies on it.
 _EMIT_ATTR = "_r2s_emission_order"
+PATH_COUNTS = {"two_pass": 0, "one_pass": 0}
+_WARNED_ONE_PASS = False
 
 
-def _keep_emission_order(flatten_ids: Tensor, emit_ids: Tensor, isect_src: Tensor,
-                         n_keys: int) -> None:
-    setattr(flatten_ids, _EMIT_ATTR, (emit_ids, isect_src, flatten_ids._version, int(n_keys)))
+class OnePassBackwardWarning(UserWarning):
+    """A backward op ran the one-pass atomic kernels for lack of emission order."""
 
 
-def _emission_order(flatten_ids: Tensor, n_keys: int):
-    """(emit_ids, isect_src) kept by the binning op for this flatten_ids, or None."""
-    if not USE_EMISSION_ORDER:
-        return None
+def _remember_emission(lists: TileLists, n_keys: int) -> None:
+    if lists.emit_ids is not None:
+        fl = lists.flatten_ids
+        setattr(fl, _EMIT_ATTR, (lists.emit_ids, lists.isect_src, fl._version, int(n_keys)))
+
+
+def emission_order(flatten_ids: Tensor, n_keys: int) -> Optional[Tuple[Tensor, Tensor]]:
+    """(emit_ids, isect_src) that isect_tiles* returned with this very
+    flatten_ids tensor for n_keys tile keys, if it is unmodified; else None."""
     rec = getattr(flatten_ids, _EMIT_ATTR, None)
     if rec is None:
         return None
@@ -176,6 +214,18 @@ def _emission_order(flatten_ids: Tensor, n_keys: int):
     if version != flatten_ids._version or nk != int(n_keys) or ids.numel() != flatten_ids.numel():
         return None
     return ids, src
+
+
+def _note_path(two_pass: bool, op: str) -> None:
+    global _WARNED_ONE_PASS
+    PATH_COUNTS["two_pass" if two_pass else "one_pass"] += 1
+    if not two_pass and not _WARNED_ONE_PASS:
+        _WARNED_ONE_PASS = True
+        warnings.warn(
+            f"{op}: flatten_ids carries no emission order (not the tensor isect_tiles* "
+            "returned, or modified since), so the one-pass atomic backward runs; pass the "
+            "emission arrays explicitly (r2splat.cuda._ops.TileLists) to keep the two-pass "
+            "form", OnePassBackwardWarning, stacklevel=4)
 
 
 # ------------------------------------------------------ parameter transform --
@@ -458,9 +508,10 @@ def project_gaussians_bwd(means: Tensor, covars: Tensor, viewmats: Tensor, Ks: T
 
 # ---------------------------------------------------------------- binning --
 
-def isect_tiles(means2d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim1: int,
-                n_tiles_dim0: int) -> Tuple[Tensor, Tensor, Tensor]:
-    """IsectTiles.cpp:31-170 -> (tiles_per_gauss [C,N], isect_ids i64, flatten_ids i32)."""
+def bin_tiles_2d(means2d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim1: int,
+                 n_tiles_dim0: int) -> TileLists:
+    """IsectTiles.cpp:31-170: the records of every (view, Gaussian, tile) overlap,
+    sorted by (tile key, emission index), with their emission order."""
     _check_input(means2d, "means2d")
     _check_input(radii, "radii")
     _check(means2d.dim() == 3, "means2d must be 3D [C, N, 2]")
@@ -474,10 +525,10 @@ def isect_tiles(means2d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim1: in
     dev = means2d.device
     tw, th, ts = int(n_tiles_dim1), int(n_tiles_dim0), int(tile_size)
     tiles_per_gauss = torch.empty((C, N), dtype=torch.int32, device=dev)
-    empty_ids = (torch.empty((0,), dtype=torch.int64, device=dev),
-                 torch.empty((0,), dtype=torch.int32, device=dev))
+    empty = TileLists(tiles_per_gauss, torch.empty((0,), dtype=torch.int64, device=dev),
+                      torch.empty((0,), dtype=torch.int32, device=dev), None, None)
     if C * N == 0:
-        return (tiles_per_gauss,) + empty_ids
+        return empty
     lib = _lib()
     sfx = _suffix(means2d, "isect_tiles")
     rect = 1 if radii.dim() == 3 else 0
@@ -495,10 +546,16 @@ def isect_tiles(means2d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim1: in
 
         res = _emit_and_sort(launch, offsets, C * N, C * tw * th, "isect_tiles", dev, "2d")
     if res is None:
-        return (tiles_per_gauss,) + empty_ids
-    isect_ids, flatten_ids, emit_ids, isect_src = res
-    _keep_emission_order(flatten_ids, emit_ids, isect_src, C * tw * th)
-    return tiles_per_gauss, isect_ids, flatten_ids
+        return empty
+    return TileLists(tiles_per_gauss, *res)
+
+
+def isect_tiles(means2d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim1: int,
+                n_tiles_dim0: int) -> Tuple[Tensor, Tensor, Tensor]:
+    """IsectTiles.cpp:31-170 -> (tiles_per_gauss [C,N], isect_ids i64, flatten_ids i32)."""
+    lists = bin_tiles_2d(means2d, radii, tile_size, n_tiles_dim1, n_tiles_dim0)
+    _remember_emission(lists, means2d.size(0) * int(n_tiles_dim1) * int(n_tiles_dim0))
+    return lists.tiles_per_gauss, lists.isect_ids, lists.flatten_ids
 
 
 def isect_offset_encode(isect_ids: Tensor, C: int, n_tiles_dim1: int,
@@ -517,9 +574,13 @@ def isect_offset_encode(isect_ids: Tensor, C: int, n_tiles_dim1: int,
     return offsets
 
 
-def isect_tiles_3d(means3d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim2: int,
-                   n_tiles_dim1: int, n_tiles_dim0: int) -> Tuple[Tensor, Tensor, Tensor]:
-    """IsectTiles3D.cpp:31-162 -> (tiles_per_gauss [N], isect_ids i64, flatten_ids i32)."""
+def bin_tiles_3d(means3d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim2: int,
+                 n_tiles_dim1: int, n_tiles_dim0: int,
+                 max_records: Optional[int] = None) -> Optional[TileLists]:
+    """IsectTiles3D.cpp:31-162: the (Gaussian, brick) records, sorted by
+    (brick key, emission index), with their emission order.  With
+    ``max_records``, None when there would be more records than that (the
+    caller then bins the volume in z-slabs, bin_tiles_3d_slab)."""
     _check_input(means3d, "means3d")
     _check_input(radii, "radii")
     _check(means3d.dim() == 2, "means3d must be 2D [N, 3]")
@@ -532,10 +593,10 @@ def isect_tiles_3d(means3d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim2:
     dev = means3d.device
     n2, n1, n0, ts = int(n_tiles_dim2), int(n_tiles_dim1), int(n_tiles_dim0), int(tile_size)
     tiles_per_gauss = torch.empty((N,), dtype=torch.int32, device=dev)
-    empty_ids = (torch.empty((0,), dtype=torch.int64, device=dev),
-                 torch.empty((0,), dtype=torch.int32, device=dev))
+    empty = TileLists(tiles_per_gauss, torch.empty((0,), dtype=torch.int64, device=dev),
+                      torch.empty((0,), dtype=torch.int32, device=dev), None, None)
     if N == 0:
-        return (tiles_per_gauss,) + empty_ids
+        return empty
     lib = _lib()
     sfx = _suffix(means3d, "isect_tiles_3d")
     with torch.cuda.device(dev):
@@ -551,12 +612,21 @@ def isect_tiles_3d(means3d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim2:
                   ws.numel(), st)
 
         # IsectTiles3D.cpp:96 reads the count back here.
-        res = _emit_and_sort(launch, offsets, N, n2 * n1 * n0, "isect_tiles_3d", dev, "3d")
+        res = _emit_and_sort(launch, offsets, N, n2 * n1 * n0, "isect_tiles_3d", dev, "3d",
+                             max_records)
+    if res is TOO_MANY:
+        return None
     if res is None:
-        return (tiles_per_gauss,) + empty_ids
-    isect_ids, flatten_ids, emit_ids, isect_src = res
-    _keep_emission_order(flatten_ids, emit_ids, isect_src, n2 * n1 * n0)
-    return tiles_per_gauss, isect_ids, flatten_ids
+        return empty
+    return TileLists(tiles_per_gauss, *res)
+
+
+def isect_tiles_3d(means3d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim2: int,
+                   n_tiles_dim1: int, n_tiles_dim0: int) -> Tuple[Tensor, Tensor, Tensor]:
+    """IsectTiles3D.cpp:31-162 -> (tiles_per_gauss [N], isect_ids i64, flatten_ids i32)."""
+    lists = bin_tiles_3d(means3d, radii, tile_size, n_tiles_dim2, n_tiles_dim1, n_tiles_dim0)
+    _remember_emission(lists, int(n_tiles_dim2) * int(n_tiles_dim1) * int(n_tiles_dim0))
+    return lists.tiles_per_gauss, lists.isect_ids, lists.flatten_ids
 
 
 def isect_offset_encode_3d(isect_ids: Tensor, n_tiles_dim2: int, n_tiles_dim1: int,
@@ -573,6 +643,144 @@ def isect_offset_encode_3d(isect_ids: Tensor, n_tiles_dim2: int, n_tiles_dim1: i
         _call("r2s_isect_offset_encode", _ptr(isect_ids), isect_ids.numel(), n0 * n1 * n2,
               _ptr(offsets), _stream(dev))
     return offsets
+
+
+# Z-slabs.  A volume whose brick list would exceed SLAB_RECORDS records (or
+# the int32 offsets of the reference's list, 2**31 - 1) is binned, voxelized
+# and back-propagated one slab of brick layers (dim0) at a time.  A slab's
+# list is the segment of the whole list whose bricks lie in its layers (keys
+# relative to its first layer), so the forward is the same per voxel and the
+# backward's per-Gaussian sums are added slab by slab.  SLAB_RECORDS bounds
+# the memory of one slab: about 70 bytes per record for the lists, the sort
+# and the backward rows, 19 GB at 2**28 records.
+SLAB_RECORDS = 1 << 28
+
+
+def layer_counts_3d(means3d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim2: int,
+                    n_tiles_dim1: int, n_tiles_dim0: int) -> list:
+    """Records of each brick layer (dim0) of the volume's list, on the host."""
+    _check_input(means3d, "means3d")
+    _check_input(radii, "radii")
+    N, n0 = means3d.size(0), int(n_tiles_dim0)
+    dev = means3d.device
+    counts = torch.empty((max(n0, 1),), dtype=torch.int64, device=dev)
+    ws = _workspace(8 * (n0 + 1), dev)
+    with torch.cuda.device(dev):
+        _call(f"r2s_isect_layer_counts_3d_{_suffix(means3d, 'isect_tiles_3d')}", _ptr(means3d),
+              _ptr(radii), N, int(tile_size), int(n_tiles_dim2), int(n_tiles_dim1), n0,
+              _ptr(counts), _ptr(ws), ws.numel(), _stream(dev))
+    return counts[:n0].tolist()
+
+
+def plan_slabs(layer_counts, limit: int = SLAB_RECORDS) -> list:
+    """Consecutive brick-layer ranges [z0, z1) of at most ``limit`` records
+    each (a layer above the limit on its own; one above the int32 offset
+    range raises RuntimeError)."""
+    slabs, z0, run = [], 0, 0
+    for z, c in enumerate(layer_counts):
+        _check_record_count(int(c), "isect_tiles_3d (one brick layer)")
+        if z > z0 and run + c > limit:
+            slabs.append((z0, z))
+            z0, run = z, 0
+        run += int(c)
+    if len(layer_counts) > z0:
+        slabs.append((z0, len(layer_counts)))
+    return slabs
+
+
+def bin_tiles_3d_slab(means3d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim2: int,
+                      n_tiles_dim1: int, n_tiles_dim0: int, z0: int,
+                      z1: int) -> Tuple[TileLists, Tensor]:
+    """(lists, tile_offsets [z1 - z0, n1, n2]) of the brick layers [z0, z1):
+    the records of the whole volume's list (bin_tiles_3d) whose brick lies in
+    those layers, in the same order, with keys relative to layer z0."""
+    _check_input(means3d, "means3d")
+    _check_input(radii, "radii")
+    _check(means3d.dim() == 2 and means3d.size(1) == 3, "means3d must be 2D [N, 3]")
+    _check(radii.dim() == 2 and radii.size(1) == 3 and radii.dtype == torch.int32,
+           "radii must be int32 [N, 3]")
+    N = means3d.size(0)
+    dev = means3d.device
+    n2, n1, n0, ts = int(n_tiles_dim2), int(n_tiles_dim1), int(n_tiles_dim0), int(tile_size)
+    z0, z1 = int(z0), int(z1)
+    _check(0 <= z0 <= z1 <= n0, f"brick layers [{z0}, {z1}) outside [0, {n0})")
+    n_keys = (z1 - z0) * n1 * n2
+    lib = _lib()
+    sfx = _suffix(means3d, "isect_tiles_3d")
+    tpg = torch.empty((N,), dtype=torch.int32, device=dev)
+    offs = torch.empty((z1 - z0, n1, n2), dtype=torch.int32, device=dev)
+    empty = TileLists(tpg, torch.empty((0,), dtype=torch.int64, device=dev),
+                      torch.empty((0,), dtype=torch.int32, device=dev), None, None)
+    with torch.cuda.device(dev):
+        st = _stream(dev)
+        offsets = torch.empty((N + 1,), dtype=torch.int64, device=dev)
+        ws = _workspace(lib.r2s_isect_workspace_bytes(N, 0, 0), dev)
+        _call(f"r2s_isect_count_3d_slab_{sfx}", _ptr(means3d), _ptr(radii), N, ts, n2, n1, n0,
+              z0, z1, _ptr(tpg), _ptr(offsets), _ptr(ws), ws.numel(), st)
+        n = int(offsets[N].item())
+        _check_record_count(n, "isect_tiles_3d (z-slab)")
+        if n == 0 or n_keys == 0:
+            offs.zero_()
+            return empty, offs
+        end_bit = _end_bit(n_keys)
+        outs = (torch.empty((n,), dtype=torch.int64, device=dev),
+                torch.empty((n,), dtype=torch.int32, device=dev),
+                torch.empty((n,), dtype=torch.int32, device=dev),
+                torch.empty((n,), dtype=torch.int32, device=dev))
+        ws = _workspace(lib.r2s_isect_workspace_bytes(0, n, end_bit), dev)
+        _call(f"r2s_isect_emit_sort_3d_slab_{sfx}", _ptr(means3d), _ptr(radii), N, ts, n2, n1, n0,
+              z0, z1, _ptr(offsets), n, end_bit, *[_ptr(t) for t in outs], _ptr(ws), ws.numel(),
+              st)
+        _call("r2s_isect_offset_encode", _ptr(outs[0]), n, n_keys, _ptr(offs), st)
+    return TileLists(tpg, *outs), offs
+
+
+def voxelize_slab(means3d: Tensor, conics: Tensor, opacities: Tensor, tile_offsets: Tensor,
+                  lists: TileLists, volume: Tensor, tile_size: int, z0: int) -> None:
+    """Writes the voxel slices of the brick layers [z0, z0 + nz) of ``volume``
+    [dim0, dim1, dim2] from their slab's lists (VoxelizeToVoxelsFwd.cu:69-221)."""
+    for t, n in ((means3d, "means3d"), (conics, "conics"), (opacities, "opacities"),
+                 (tile_offsets, "tile_offsets"), (volume, "volume")):
+        _check_input(t, n)
+    N = _check_voxel(means3d, conics, opacities, tile_offsets, lists.flatten_ids)
+    d0, d1, d2 = volume.shape
+    nz, n1, n2 = tile_offsets.shape
+    dev = means3d.device
+    with torch.cuda.device(dev):
+        _call(f"r2s_voxelize_fwd_slab_{_suffix(means3d, 'voxelize_to_voxels_fwd')}",
+              _ptr(means3d), _ptr(conics), _ptr(opacities), _ptr(tile_offsets),
+              _ptr(lists.flatten_ids) if lists.flatten_ids.numel() else None,
+              lists.flatten_ids.numel(), N, d2, d1, d0, int(tile_size), n2, n1, int(z0), nz,
+              _ptr(volume), _stream(dev))
+
+
+def voxel_backward_slab(means3d: Tensor, conics: Tensor, opacities: Tensor,
+                        tile_offsets: Tensor, lists: TileLists, v_volume: Tensor,
+                        tile_size: int, z0: int):
+    """The voxelizer's VJP over one slab's lists (VoxelizeToVoxelsBwd.cu:71-441,
+    two-pass): (v_means3d, v_conics, v_opacities) of that slab's records,
+    zero for Gaussians without records in it."""
+    for t, n in ((means3d, "means3d"), (conics, "conics"), (opacities, "opacities"),
+                 (tile_offsets, "tile_offsets"), (v_volume, "v_render_output")):
+        _check_input(t, n)
+    N = _check_voxel(means3d, conics, opacities, tile_offsets, lists.flatten_ids)
+    d0, d1, d2 = v_volume.shape
+    nz, n1, n2 = tile_offsets.shape
+    n = lists.flatten_ids.numel()
+    v_m, v_c, v_o = (torch.empty_like(t) for t in (means3d, conics, opacities))
+    dev = means3d.device
+    with torch.cuda.device(dev):
+        if n == 0:
+            for t in (v_m, v_c, v_o):
+                t.zero_()
+            return v_m, v_c, v_o
+        ws = _workspace(_lib().r2s_voxelize_bwd_workspace_bytes(n, means3d.element_size()), dev)
+        _call(f"r2s_voxelize_bwd_emit_slab_{_suffix(means3d, 'voxelize_to_voxels_bwd')}",
+              _ptr(means3d), _ptr(conics), _ptr(opacities), _ptr(tile_offsets),
+              _ptr(lists.isect_ids), _ptr(lists.flatten_ids), _ptr(lists.emit_ids),
+              _ptr(lists.isect_src), n, _ptr(v_volume), N, d2, d1, d0, int(tile_size), n2, n1,
+              int(z0), nz, _ptr(v_m), _ptr(v_c), _ptr(v_o), _ptr(ws), ws.numel(), _stream(dev))
+    return v_m, v_c, v_o
 
 
 # -------------------------------------------------------------- rasterizer --
@@ -625,8 +833,24 @@ def rasterize_to_pixels_fwd(means2d: Tensor, conics: Tensor, opacities: Tensor, 
     return out
 
 
+_LOOKUP = object()  # emission order: look it up on flatten_ids (the wrapper path)
+
+
+def _resolve_emission(emission, flatten_ids: Tensor, n_keys: int, op: str):
+    if emission is _LOOKUP:
+        emit = emission_order(flatten_ids, n_keys)
+    else:
+        emit = emission
+        if emit is not None:
+            _check(emit[0].numel() == flatten_ids.numel() and
+                   emit[1].numel() == flatten_ids.numel(),
+                   f"{op}: emission arrays must have one entry per record")
+    _note_path(emit is not None, op)
+    return emit
+
+
 def _raster_bwd(means2d, conics, opacities, mus, tile_offsets, isect_ids, flatten_ids,
-                v_render, dim1, dim0, tile_size, absgrad, op):
+                v_render, dim1, dim0, tile_size, absgrad, op, emission=_LOOKUP):
     C, N = _check_raster(means2d, conics, opacities, mus, tile_offsets, flatten_ids)
     _check(v_render.dim() == 3, "v_render_output must be 3D [C, dim0, dim1]")
     W, H, ts = int(dim1), int(dim0), int(tile_size)
@@ -635,7 +859,7 @@ def _raster_bwd(means2d, conics, opacities, mus, tile_offsets, isect_ids, flatte
     th, tw = tile_offsets.size(1), tile_offsets.size(2)
     n_isects = flatten_ids.numel()
     empty = C == 0 or N == 0 or n_isects == 0
-    emit = None if empty else _emission_order(flatten_ids, C * tw * th)
+    emit = None if empty else _resolve_emission(emission, flatten_ids, C * tw * th, op)
     # The two-pass form stores every output (zero for Gaussians without
     # records); the one-pass form accumulates into zeros.
     alloc = torch.empty_like if emit is not None else torch.zeros_like
@@ -695,6 +919,22 @@ def rasterize_to_pixels_bwd_per_gaussian(means2d: Tensor, conics: Tensor, opacit
     return _raster_bwd(means2d, conics, opacities, mus, tile_offsets, isect_ids, flatten_ids,
                        v_render_output, dim1, dim0, tile_size, bool(absgrad),
                        "rasterize_to_pixels_bwd_per_gaussian")
+
+
+def raster_backward(means2d: Tensor, conics: Tensor, opacities: Tensor, mus: Tensor,
+                    tile_offsets: Tensor, lists: TileLists, v_image: Tensor, img_w: int,
+                    img_h: int, tile_size: int, absgrad: bool):
+    """The rasterizer's VJP over lists returned by :func:`bin_tiles_2d`, with
+    their emission order passed explicitly (both reference modes compute the
+    same sums; RasterizeToPixels.cpp:122-317) ->
+    (v_means2d_abs or None, v_means2d, v_conics, v_opacities, v_mus)."""
+    for t, n in ((means2d, "means2d"), (conics, "conics"), (opacities, "opacities"),
+                 (mus, "mus"), (tile_offsets, "tile_offsets"), (lists.flatten_ids, "flatten_ids"),
+                 (v_image, "v_render_output")):
+        _check_input(t, n)
+    return _raster_bwd(means2d, conics, opacities, mus, tile_offsets, lists.isect_ids,
+                       lists.flatten_ids, v_image, img_w, img_h, tile_size, bool(absgrad),
+                       "raster_backward", emission=lists.emission)
 
 
 # ------------------------------------------------------------ voxelization --
@@ -813,14 +1053,14 @@ def voxelize_to_voxels_fwd(means3d: Tensor, conics: Tensor, opacities: Tensor,
 
 
 def _voxel_bwd(means3d, conics, opacities, tile_offsets, isect_ids, flatten_ids, v_render,
-               dim2, dim1, dim0, tile_size, op):
+               dim2, dim1, dim0, tile_size, op, emission=_LOOKUP):
     N = _check_voxel(means3d, conics, opacities, tile_offsets, flatten_ids)
     _check(v_render.dim() == 3, "v_render_output must be 3D [dim0, dim1, dim2]")
     d2, d1, d0, ts = int(dim2), int(dim1), int(dim0), int(tile_size)
     n0, n1, n2 = tile_offsets.size(0), tile_offsets.size(1), tile_offsets.size(2)
     n_isects = flatten_ids.numel()
     empty = N == 0 or n_isects == 0
-    emit = None if empty else _emission_order(flatten_ids, n2 * n1 * n0)
+    emit = None if empty else _resolve_emission(emission, flatten_ids, n2 * n1 * n0, op)
     # As in _raster_bwd: the two-pass form stores every output.
     alloc = torch.empty_like if emit is not None else torch.zeros_like
     v_means3d = alloc(means3d)
@@ -876,6 +1116,21 @@ def voxelize_to_voxels_bwd_per_gaussian(means3d: Tensor, conics: Tensor, opaciti
     return _voxel_bwd(means3d, conics, opacities, tile_offsets, isect_ids, flatten_ids,
                       v_render_output, dim2, dim1, dim0, tile_size,
                       "voxelize_to_voxels_bwd_per_gaussian")
+
+
+def voxel_backward(means3d: Tensor, conics: Tensor, opacities: Tensor, tile_offsets: Tensor,
+                   lists: TileLists, v_volume: Tensor, dim2: int, dim1: int, dim0: int,
+                   tile_size: int):
+    """The voxelizer's VJP over lists returned by :func:`bin_tiles_3d`, with
+    their emission order passed explicitly (VoxelizeToVoxels.cpp:115-278) ->
+    (v_means3d, v_conics, v_opacities)."""
+    for t, n in ((means3d, "means3d"), (conics, "conics"), (opacities, "opacities"),
+                 (tile_offsets, "tile_offsets"), (lists.flatten_ids, "flatten_ids"),
+                 (v_volume, "v_render_output")):
+        _check_input(t, n)
+    return _voxel_bwd(means3d, conics, opacities, tile_offsets, lists.isect_ids,
+                      lists.flatten_ids, v_volume, dim2, dim1, dim0, tile_size,
+                      "voxel_backward", emission=lists.emission)
 
 
 # -------------------------------------------------------------- compaction --

@@ -266,6 +266,54 @@ int r2s_isect_emit_sort_3d_f64(const double *means3d, const int32_t *radii,
                                void *workspace, size_t workspace_bytes,
                                r2s_stream_t stream);
 
+/* Z-slab binning of large volumes.  IsectTiles3D.cpp:96-161 sizes one list
+ * for the whole volume with int32 offsets (static_cast<int>(n_isects) at
+ * IsectTiles3DKernel.cu:383-402), so a volume with 2^31 or more brick
+ * records cannot be binned there.  These entries bin the brick layers
+ * [z0, z1) of the dim0 axis alone: the records are those of the whole list
+ * whose brick lies in the layers, in the same order, with keys relative to
+ * layer z0 ((b0 - z0) n1 n2 + b1 n2 + b2).  No reference counterpart.
+ *
+ * r2s_isect_layer_counts_3d_*: counts [n_tiles_d0] int64, the records of
+ * each brick layer (to plan slabs); workspace of (n_tiles_d0 + 1) * 8
+ * bytes. */
+int r2s_isect_layer_counts_3d_f32(const float *means3d, const int32_t *radii, int64_t N,
+                                  uint32_t tile_size, uint32_t n_tiles_d2,
+                                  uint32_t n_tiles_d1, uint32_t n_tiles_d0, int64_t *counts,
+                                  void *workspace, size_t workspace_bytes,
+                                  r2s_stream_t stream);
+int r2s_isect_layer_counts_3d_f64(const double *means3d, const int32_t *radii, int64_t N,
+                                  uint32_t tile_size, uint32_t n_tiles_d2,
+                                  uint32_t n_tiles_d1, uint32_t n_tiles_d0, int64_t *counts,
+                                  void *workspace, size_t workspace_bytes,
+                                  r2s_stream_t stream);
+/* As r2s_isect_count_3d_* / r2s_isect_emit_sort_3d_* for the layers
+ * [z0, z1) (n_tiles_d0 is the whole grid's; keys below (z1 - z0) n1 n2). */
+int r2s_isect_count_3d_slab_f32(const float *means3d, const int32_t *radii, int64_t N,
+                                uint32_t tile_size, uint32_t n_tiles_d2, uint32_t n_tiles_d1,
+                                uint32_t n_tiles_d0, uint32_t z0, uint32_t z1,
+                                int32_t *tiles_per_gauss, int64_t *offsets, void *workspace,
+                                size_t workspace_bytes, r2s_stream_t stream);
+int r2s_isect_count_3d_slab_f64(const double *means3d, const int32_t *radii, int64_t N,
+                                uint32_t tile_size, uint32_t n_tiles_d2, uint32_t n_tiles_d1,
+                                uint32_t n_tiles_d0, uint32_t z0, uint32_t z1,
+                                int32_t *tiles_per_gauss, int64_t *offsets, void *workspace,
+                                size_t workspace_bytes, r2s_stream_t stream);
+int r2s_isect_emit_sort_3d_slab_f32(const float *means3d, const int32_t *radii, int64_t N,
+                                    uint32_t tile_size, uint32_t n_tiles_d2,
+                                    uint32_t n_tiles_d1, uint32_t n_tiles_d0, uint32_t z0,
+                                    uint32_t z1, const int64_t *offsets, int64_t n_isects,
+                                    uint32_t end_bit, int64_t *isect_ids, int32_t *flatten_ids,
+                                    int32_t *emit_ids, int32_t *isect_src, void *workspace,
+                                    size_t workspace_bytes, r2s_stream_t stream);
+int r2s_isect_emit_sort_3d_slab_f64(const double *means3d, const int32_t *radii, int64_t N,
+                                    uint32_t tile_size, uint32_t n_tiles_d2,
+                                    uint32_t n_tiles_d1, uint32_t n_tiles_d0, uint32_t z0,
+                                    uint32_t z1, const int64_t *offsets, int64_t n_isects,
+                                    uint32_t end_bit, int64_t *isect_ids, int32_t *flatten_ids,
+                                    int32_t *emit_ids, int32_t *isect_src, void *workspace,
+                                    size_t workspace_bytes, r2s_stream_t stream);
+
 /* IsectTiles.cpp:176-215 isect_offset_encode_tensor and
  * IsectTiles3D.cpp:168-204 isect_offset_encode_3d_tensor:
  * tile_offsets[k] = lower_bound(isect_ids, k) for k in [0, n_keys). */
@@ -498,6 +546,70 @@ int r2s_voxelize_bwd_emit_f64(const double *means3d, const double *conics,
                               uint32_t n_tiles_d1, uint32_t n_tiles_d0, double *v_means3d,
                               double *v_conics, double *v_opacities, void *workspace,
                               size_t workspace_bytes, r2s_stream_t stream);
+
+/* One z-slab of a volume binned by r2s_isect_*_3d_slab_*: the lists of the
+ * nz brick layers from layer z0 on (tile_offsets [nz, n1, n2], keys
+ * relative to layer z0) against the whole volume [dim0, dim1, dim2] and its
+ * upstream gradient.  The forward writes only the slab's voxel slices
+ * [z0 ts, min((z0 + nz) ts, dim0)); the backward stores every Gaussian's
+ * output (zero without records in the slab), so a caller sums the slabs'
+ * outputs.  No reference counterpart (VoxelizeToVoxels.cpp:31-278 take one
+ * list of the whole volume). */
+int r2s_voxelize_fwd_slab_f32(const float *means3d, const float *conics,
+                              const float *opacities, const int32_t *tile_offsets,
+                              const int32_t *flatten_ids, int64_t n_isects, int64_t N,
+                              uint32_t dim2, uint32_t dim1, uint32_t dim0, uint32_t tile_size,
+                              uint32_t n_tiles_d2, uint32_t n_tiles_d1, uint32_t z0,
+                              uint32_t nz, float *volume, r2s_stream_t stream);
+int r2s_voxelize_fwd_slab_f64(const double *means3d, const double *conics,
+                              const double *opacities, const int32_t *tile_offsets,
+                              const int32_t *flatten_ids, int64_t n_isects, int64_t N,
+                              uint32_t dim2, uint32_t dim1, uint32_t dim0, uint32_t tile_size,
+                              uint32_t n_tiles_d2, uint32_t n_tiles_d1, uint32_t z0,
+                              uint32_t nz, double *volume, r2s_stream_t stream);
+int r2s_voxelize_bwd_emit_slab_f32(const float *means3d, const float *conics,
+                                   const float *opacities, const int32_t *tile_offsets,
+                                   const int64_t *isect_ids, const int32_t *flatten_ids,
+                                   const int32_t *emit_ids, const int32_t *isect_src,
+                                   int64_t n_isects, const float *v_volume, int64_t N,
+                                   uint32_t dim2, uint32_t dim1, uint32_t dim0,
+                                   uint32_t tile_size, uint32_t n_tiles_d2,
+                                   uint32_t n_tiles_d1, uint32_t z0, uint32_t nz,
+                                   float *v_means3d, float *v_conics, float *v_opacities,
+                                   void *workspace, size_t workspace_bytes,
+                                   r2s_stream_t stream);
+int r2s_voxelize_bwd_emit_slab_f64(const double *means3d, const double *conics,
+                                   const double *opacities, const int32_t *tile_offsets,
+                                   const int64_t *isect_ids, const int32_t *flatten_ids,
+                                   const int32_t *emit_ids, const int32_t *isect_src,
+                                   int64_t n_isects, const double *v_volume, int64_t N,
+                                   uint32_t dim2, uint32_t dim1, uint32_t dim0,
+                                   uint32_t tile_size, uint32_t n_tiles_d2,
+                                   uint32_t n_tiles_d1, uint32_t z0, uint32_t nz,
+                                   double *v_means3d, double *v_conics, double *v_opacities,
+                                   void *workspace, size_t workspace_bytes,
+                                   r2s_stream_t stream);
+
+/* The first pass of r2s_voxelize_bwd_emit_slab_* alone (the rows of one
+ * slab's records, as r2s_voxelize_bwd_rows_*). */
+int r2s_voxelize_bwd_rows_slab_f32(const float *means3d, const float *conics,
+                                   const float *opacities, const int32_t *tile_offsets,
+                                   const int64_t *isect_ids, const int32_t *flatten_ids,
+                                   const int32_t *isect_src, int64_t n_isects,
+                                   const float *v_volume, int64_t N, uint32_t dim2,
+                                   uint32_t dim1, uint32_t dim0, uint32_t tile_size,
+                                   uint32_t n_tiles_d2, uint32_t n_tiles_d1, uint32_t z0,
+                                   uint32_t nz, void *rows, size_t rows_bytes,
+                                   r2s_stream_t stream);
+int r2s_voxelize_bwd_rows_slab_f64(const double *means3d, const double *conics,
+                                   const double *opacities, const int32_t *tile_offsets,
+                                   const int64_t *isect_ids, const int32_t *flatten_ids,
+                                   const int32_t *isect_src, int64_t n_isects,
+                                   const double *v_volume, int64_t N, uint32_t dim2,
+                                   uint32_t dim1, uint32_t dim0, uint32_t tile_size,
+                                   uint32_t n_tiles_d2, uint32_t n_tiles_d1, uint32_t z0,
+                                   uint32_t nz, void *rows, size_t rows_bytes,
+                                   r2s_stream_t stream);
 
 /* The two passes of r2s_voxelize_bwd_emit_* as separate calls, as for the
  * rasterizer (10 row values).  No reference counterpart. */

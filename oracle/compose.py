@@ -56,31 +56,70 @@ def voxelize_forward(means, covars, opacities, ranges, centers, dim2, dim1, dim0
                 tile_size=tile_size, eps3d=eps3d)
 
 
+def _cast(x, dt):
+    if dt is None or not isinstance(x, np.ndarray) or x.dtype.kind != "f":
+        return x
+    return x.astype(dt)
+
+
 def explicit_backward(covars, proj, vox, means, quats, raw_scales, raw_opacities, scale_min,
-                      scale_max, v_image, v_volume=None, absgrad=True):
+                      scale_max, v_image, v_volume=None, absgrad=True, dtype=None, eta=0.0,
+                      raster_grads=None, voxel_grads=None):
     """explicit.py:233-385 -> dict of gradients (means, quats, raw_scales,
-    raw_opacities, means2d, means2d_abs)."""
-    dt = means.dtype
+    raw_opacities, means2d, means2d_abs).
+
+    ``dtype`` evaluates the whole backward in that precision on the given
+    values (e.g. float64 over a float32 forward: the forward's geometry and
+    tile lists stay those of the float32 run).  ``eta`` > 0 adds
+    ``flagged``: a bool [N] marking the Gaussians whose raster or voxel sums
+    hold a term within the flip bracket of an alpha cut-off (see
+    r2s_oracle.c).  ``raster_grads`` / ``voxel_grads`` replace the raster /
+    voxel VJPs by given values (the 5-tuple / 3-tuple of the ops), so that
+    only the chain after them is evaluated."""
+    dt = np.dtype(dtype) if dtype is not None else means.dtype
+    P = {k: _cast(v, dt) for k, v in proj.items()}
+    V = None if vox is None else {k: _cast(v, dt) for k, v in vox.items()}
+    covars, means, quats, raw_scales, raw_opacities = (
+        _cast(x, dt) for x in (covars, means, quats, raw_scales, raw_opacities))
+    N = means.shape[0]
+    flagged = np.zeros(N, bool)
     v_means = np.zeros_like(means)
     v_covars = np.zeros_like(covars)
-    v_opacity = np.zeros(means.shape[0], dt)
-    v_abs, v_means2d, v_conics, v_opac_cn, v_mus = native.raster_bwd(
-        proj["means2d"], proj["conics"], proj["opacity"], proj["mus"], proj["tile_offsets"],
-        proj["flatten_ids"], v_image, proj["img_w"], proj["img_h"], proj["tile_size"], absgrad)
-    v_cov2d = ops.conics_mu_bwd(proj["cov2d"], proj["eps2d"], proj["conics"], proj["mus"],
-                                v_conics, v_mus)
-    vm, vc = ops.world_to_image_projection_bwd(means, covars, proj["viewmats"], proj["Ks"],
-                                               proj["img_w"], proj["img_h"], v_means2d, v_cov2d)
+    v_opacity = np.zeros(N, dt)
+    if raster_grads is None:
+        res = native.raster_bwd(P["means2d"], P["conics"], P["opacity"], P["mus"],
+                                P["tile_offsets"], P["flatten_ids"], _cast(v_image, dt),
+                                P["img_w"], P["img_h"], P["tile_size"], absgrad, eta=eta,
+                                band=eta > 0)
+        if eta > 0:
+            res, bands = res
+            for b in bands:
+                if b is not None:
+                    flagged |= (b.reshape(b.shape[0], N, -1) > 0).any(-1).any(0)
+    else:
+        res = tuple(None if g is None else _cast(np.asarray(g), dt) for g in raster_grads)
+    v_abs, v_means2d, v_conics, v_opac_cn, v_mus = res
+    v_cov2d = ops.conics_mu_bwd(P["cov2d"], P["eps2d"], P["conics"], P["mus"], v_conics, v_mus)
+    vm, vc = ops.world_to_image_projection_bwd(means, covars, P["viewmats"], P["Ks"],
+                                               P["img_w"], P["img_h"], v_means2d, v_cov2d)
     v_means = v_means + vm
     v_covars = v_covars + vc
     v_opacity = v_opacity + v_opac_cn.sum(axis=0)
-    if vox is not None and v_volume is not None:
-        vm3, vc3, vo3 = native.voxel_bwd(vox["means3d"], vox["conics"], vox["opacity"],
-                                         vox["tile_offsets"], vox["flatten_ids"], v_volume,
-                                         vox["dim2"], vox["dim1"], vox["dim0"], vox["tile_size"])
-        vm, vc = ops.world_to_volume_mapping_bwd(means, covars, vox["ranges"], vox["centers"],
-                                                 vox["dim2"], vox["dim1"], vox["dim0"],
-                                                 vox["eps3d"], vm3, vc3)
+    if V is not None and (v_volume is not None or voxel_grads is not None):
+        if voxel_grads is None:
+            r3 = native.voxel_bwd(V["means3d"], V["conics"], V["opacity"], V["tile_offsets"],
+                                  V["flatten_ids"], _cast(v_volume, dt), V["dim2"], V["dim1"],
+                                  V["dim0"], V["tile_size"], eta=eta, band=eta > 0)
+            if eta > 0:
+                r3, b3 = r3
+                for b in b3:
+                    flagged |= (b.reshape(N, -1) > 0).any(-1)
+        else:
+            r3 = tuple(_cast(np.asarray(g), dt) for g in voxel_grads)
+        vm3, vc3, vo3 = r3
+        vm, vc = ops.world_to_volume_mapping_bwd(means, covars, V["ranges"], V["centers"],
+                                                 V["dim2"], V["dim1"], V["dim0"],
+                                                 V["eps3d"], vm3, vc3)
         v_means = v_means + vm
         v_covars = v_covars + vc
         v_opacity = v_opacity + vo3
@@ -88,6 +127,9 @@ def explicit_backward(covars, proj, vox, means, quats, raw_scales, raw_opacities
                                                         v_covars)
     k = dt.type
     sig = k(1) / (k(1) + np.exp(-raw_opacities))
-    return dict(means=v_means, quats=v_quats, raw_scales=v_raw_scales,
-                raw_opacities=(v_opacity * sig).astype(dt), means2d=v_means2d,
-                means2d_abs=v_abs)
+    out = dict(means=v_means, quats=v_quats, raw_scales=v_raw_scales,
+               raw_opacities=(v_opacity * sig).astype(dt), means2d=v_means2d,
+               means2d_abs=v_abs)
+    if eta > 0:
+        out["flagged"] = flagged
+    return out

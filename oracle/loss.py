@@ -103,6 +103,38 @@ def projection_loss_grad(x, y, e=None, m=None, scales=(1.0, 1.0, 1.0), window_si
     return g
 
 
+def projection_loss_grad_magnitude(x, y, e=None, m=None, scales=(1.0, 1.0, 1.0),
+                                   window_size=11):
+    """Sum of the absolute values of the terms of projection_loss_grad, per
+    pixel: sign terms |s| / n, and s_ssim (G*|A| + 2|x| G*|B| + |y| G*|C|) / n
+    with |A| the sum of the absolute values of A's four terms.  Where the
+    window's variances vanish (window size 1, flat regions), 2 x G*B and the
+    -2 mu_x S / d2 term of G*A are of size 2 x S / c2 ~ 1e3 and cancel: any
+    float32 evaluation then differs from the exact gradient by about u times
+    this magnitude, not u times the gradient."""
+    _, win = gaussian_window(window_size)
+    x, y = np.asarray(x, np.float64), np.asarray(y, np.float64)
+    n = x.size
+    g = np.full(x.shape, abs(scales[0]) / n)
+    for i in range(x.shape[0]):
+        mu1, mu2 = filter2d(x[i], win), filter2d(y[i], win)
+        m11, m22, m12 = filter2d(x[i] * x[i], win), filter2d(y[i] * y[i], win), filter2d(
+            x[i] * y[i], win)
+        s11, s22, s12 = m11 - mu1 ** 2, m22 - mu2 ** 2, m12 - mu1 * mu2
+        n1, n2 = 2 * mu1 * mu2 + C1, 2 * s12 + C2
+        d1, d2 = mu1 ** 2 + mu2 ** 2 + C1, s11 + s22 + C2
+        S = n1 * n2 / (d1 * d2)
+        a_abs = (np.abs(2 * mu2 * n2 / (d1 * d2)) + np.abs(2 * mu2 * n1 / (d1 * d2))
+                 + np.abs(2 * mu1 * S / d1) + np.abs(2 * mu1 * S / d2))
+        B, C = -S / d2, 2 * n1 / (d1 * d2)
+        t = (filter2d(a_abs, win) + 2 * np.abs(x[i]) * filter2d(np.abs(B), win)
+             + np.abs(y[i]) * filter2d(np.abs(C), win))
+        g[i] += abs(scales[1]) * t / n
+    if e is not None:
+        g += abs(scales[2]) * np.abs(np.asarray(m, np.float64)) / n
+    return g
+
+
 def tv(vol, reduction="mean"):
     """loss.py:10-21 compute_tv_loss in float64."""
     v = np.asarray(vol, np.float64)
@@ -159,3 +191,44 @@ def hierarchy_loss(child_means, parent, hist_means, parent_scales, hist_quats, h
     k = np.where(e > 0, 2 * e / (a * np.where(r > 0, r, 1.0) * n), 0.0)
     grad[valid] = np.einsum("nij,nj->ni", R, (k[:, None] * u / s))
     return float((e * e).mean()), grad
+
+
+def hierarchy_grad_magnitude(child_means, parent, hist_means, parent_scales, hist_quats,
+                             history_count, factor=1.0):
+    """Per child and component, a first-order bound (in units of the unit
+    roundoff) on the error of evaluating d loss / d child_means in another
+    order: the gradient is R v with v = k u / s, so component i sums
+    |R_ij v_j| (which cancel when the child lies along a principal axis),
+    each carrying the relative error of v: the difference d = c - p cancels
+    when the child is near the parent (|c| + |p|) / |d|, and the excess
+    r - a when it is near the parent's ellipsoid (r + a) / |r - a|."""
+    c = np.asarray(child_means, np.float64)
+    par = np.asarray(parent).astype(np.int64)
+    valid = (par >= 0) & (par < history_count)
+    out = np.zeros_like(c)
+    if not valid.any():
+        return out
+    ids = par[valid]
+    q = np.asarray(hist_quats, np.float64)[ids]
+    q = q / np.maximum(np.linalg.norm(q, axis=1), 1e-12)[:, None]
+    w, x, y, z = q.T
+    R = np.stack([1 - 2 * (y * y + z * z), 2 * (x * y - w * z), 2 * (x * z + w * y),
+                  2 * (x * y + w * z), 1 - 2 * (x * x + z * z), 2 * (y * z - w * x),
+                  2 * (x * z - w * y), 2 * (y * z + w * x), 1 - 2 * (x * x + y * y)],
+                 -1).reshape(-1, 3, 3)
+    s = np.maximum(np.asarray(parent_scales, np.float64)[ids], 1e-6)
+    pm = np.asarray(hist_means, np.float64)[ids]
+    d = c[valid] - pm
+    u = np.einsum("nji,nj->ni", R, d) / s
+    r = np.linalg.norm(u, axis=1)
+    a = max(float(factor), 1e-6)
+    e = np.maximum(r - a, 0.0) / a
+    n = int(valid.sum())
+    k = np.where(e > 0, 2 * e / (a * np.where(r > 0, r, 1.0) * n), 0.0)
+    v = k[:, None] * u / s
+    excess = (r + a) / np.maximum(np.abs(r - a), 1e-300)
+    near = (np.abs(c[valid]).sum(1) + np.abs(pm).sum(1)) / np.maximum(
+        np.linalg.norm(d, axis=1), 1e-300)
+    rel = 1 + excess + near * (1 + r / np.maximum(np.abs(r - a), 1e-300))
+    out[valid] = np.einsum("nij,nj->ni", np.abs(R), np.abs(v)) * rel[:, None]
+    return out

@@ -57,6 +57,28 @@ def test_invalid_arguments_are_rejected_without_a_device(lib):
     assert rc == 1001 and b"tile_size" in lib.r2s_last_error()
 
 
+def test_tile_sizes_whose_products_wrap_are_rejected(lib):
+    # 65536^2 and 2048^3 wrap to 0 in 32 bits; both must fail the tile-size
+    # check before any launch (the backward would otherwise pick a kernel for
+    # the first 32 rows only and report success).
+    rc = lib.r2s_rasterize_fwd_f32(None, None, None, None, None, None, 0, 1, 1, 64, 64, 65536, 1,
+                                   1, None, None, 0, None)
+    assert rc == 1001 and b"tile_size" in lib.r2s_last_error()
+    rc = lib.r2s_rasterize_bwd_f32(None, None, None, None, None, None, None, 5, None, 1, 1, 64,
+                                   64, 65536, 1, 1, None, None, None, None, None, None)
+    assert rc == 1001 and b"tile_size" in lib.r2s_last_error()
+    rc = lib.r2s_rasterize_bwd_emit_f32(None, None, None, None, None, None, None, None, None, 5,
+                                        None, 1, 1, 64, 64, 65536, 1, 1, None, None, None, None,
+                                        None, None, 0, None)
+    assert rc == 1001 and b"tile_size" in lib.r2s_last_error()
+    rc = lib.r2s_voxelize_fwd_f32(None, None, None, None, None, 0, 1, 8, 8, 8, 2048, 1, 1, 1,
+                                  None, None)
+    assert rc == 1001 and b"tile_size" in lib.r2s_last_error()
+    rc = lib.r2s_voxelize_bwd_f32(None, None, None, None, None, None, 5, None, 1, 8, 8, 8, 2048,
+                                  1, 1, 1, None, None, None, None)
+    assert rc == 1001 and b"tile_size" in lib.r2s_last_error()
+
+
 def test_workspace_queries(lib):
     assert lib.r2s_isect_workspace_bytes(0, 0, 11) == 0
     small = lib.r2s_isect_workspace_bytes(0, 1000, 11)

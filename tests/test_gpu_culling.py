@@ -13,8 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_close, np32
-from oracle import native
+from helpers import check_raster, check_voxel, np32, raster_references, voxel_references
 from r2splat.cuda import _ops
 from r2splat.cuda import _wrapper as W
 
@@ -78,19 +77,13 @@ def test_rasterize_hard_footprints(dtype, W_img, H_img, ts, order):
     off = W.isect_offset_encode(ids, 1, tw, th)
     assert fl.numel() > 1000
     img = W.rasterize_to_pixels_fwd(m2, con, op, mu, off, fl, W_img, H_img, ts)
-    img_o = native.raster_fwd(np32(m2), np32(con), np32(op), np32(mu), np32(off), np32(fl),
-                              W_img, H_img, ts)
-    f32 = dtype == torch.float32
-    tol = dict(rtol=1e-4, atol=1e-5) if f32 else dict(rtol=1e-9, atol=1e-12)
-    assert_close(np32(img), img_o, "image", max_outliers=img_o.size // 1000 if f32 else 0,
-                 outlier_atol=3e-5 if f32 else None, **tol)
     v = torch.randn(img.shape, generator=torch.Generator().manual_seed(3), dtype=dtype)
-    ref = native.raster_bwd(np32(m2), np32(con), np32(op), np32(mu), np32(off), np32(fl),
-                            v.numpy(), W_img, H_img, ts, True)
-    names = ("v_means2d_abs", "v_means2d", "v_conics", "v_opacities", "v_mus")
+    refs = raster_references(np32(m2), np32(con), np32(op), np32(mu), np32(off), np32(fl),
+                             W_img, H_img, ts, v_image=v.numpy())
+    print("image", check_raster(refs, image=np32(img)))
     if order == "tile":
         fl = fl.clone()  # no emission-order records: the tile-order kernels run
-    assert (_ops._emission_order(fl, fl_keys(off)) is not None) == (order == "emission")
+    assert (_ops.emission_order(fl, fl_keys(off)) is not None) == (order == "emission")
     for mode in ("primitive", "pixel"):
         if mode == "primitive":
             got = W.rasterize_to_pixels_bwd_per_gaussian(m2, con, op, mu, off, ids, fl,
@@ -98,12 +91,8 @@ def test_rasterize_hard_footprints(dtype, W_img, H_img, ts, order):
         else:
             got = W.rasterize_to_pixels_bwd(m2, con, op, mu, off, fl, v.to(DEV), W_img, H_img,
                                             ts, True)
-        for a, e, n in zip(got, ref, names):
-            scale = float(np.abs(e).max()) + 1e-30
-            assert_close(np32(a), e, f"{mode} {n}", rtol=tol["rtol"],
-                         atol=max(tol["atol"], (3e-6 if f32 else 1e-12) * scale),
-                         max_outliers=e.size // 500 if f32 else 0,
-                         outlier_atol=2e-4 * scale if f32 else None)
+        for n, r in check_raster(refs, grads=[np32(t) for t in got], tag=f"{mode} ").items():
+            print(mode, n, r)
 
 
 def _voxel_case(seed, n, dims, dtype):
@@ -132,26 +121,18 @@ def test_voxelize_hard_footprints(dtype, dims, ts, order):
     off = W.isect_offset_encode_3d(ids, n2, n1, n0)
     assert fl.numel() > 1000
     vol = W.voxelize_to_voxels_fwd(m3, con, op, off, fl, d2, d1, d0, ts)
-    vol_o = native.voxel_fwd(np32(m3), np32(con), np32(op), np32(off), np32(fl), d2, d1, d0, ts)
-    f32 = dtype == torch.float32
-    tol = dict(rtol=1e-4, atol=1e-5) if f32 else dict(rtol=1e-9, atol=1e-12)
-    assert_close(np32(vol), vol_o, "volume", max_outliers=vol_o.size // 1000 if f32 else 0,
-                 outlier_atol=3e-6 if f32 else None, **tol)
     v = torch.randn(vol.shape, generator=torch.Generator().manual_seed(4), dtype=dtype)
-    ref = native.voxel_bwd(np32(m3), np32(con), np32(op), np32(off), np32(fl), v.numpy(), d2, d1,
-                           d0, ts)
+    refs = voxel_references(np32(m3), np32(con), np32(op), np32(off), np32(fl), d2, d1, d0, ts,
+                            v_volume=v.numpy())
+    print("volume", check_voxel(refs, volume=np32(vol)))
     if order == "tile":
         fl = fl.clone()  # no emission-order records: the tile-order kernels run
-    assert (_ops._emission_order(fl, fl_keys(off)) is not None) == (order == "emission")
+    assert (_ops.emission_order(fl, fl_keys(off)) is not None) == (order == "emission")
     for mode in ("primitive", "pixel"):
         if mode == "primitive":
             got = W.voxelize_to_voxels_bwd_per_gaussian(m3, con, op, off, ids, fl, v.to(DEV), d2,
                                                         d1, d0, ts)
         else:
             got = W.voxelize_to_voxels_bwd(m3, con, op, off, fl, v.to(DEV), d2, d1, d0, ts)
-        for a, e, n in zip(got, ref, ("v_means3d", "v_conics", "v_opacities")):
-            scale = float(np.abs(e).max()) + 1e-30
-            assert_close(np32(a), e, f"{mode} {n}", rtol=tol["rtol"],
-                         atol=max(tol["atol"], (3e-6 if f32 else 1e-12) * scale),
-                         max_outliers=e.size // 500 if f32 else 0,
-                         outlier_atol=2e-4 * scale if f32 else None)
+        for n, r in check_voxel(refs, grads=[np32(t) for t in got], tag=f"{mode} ").items():
+            print(mode, n, r)

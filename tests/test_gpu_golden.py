@@ -3,9 +3,9 @@
 Given the fixture's covariances, the projection, conics/mu, volume mapping,
 tile lists, offsets and the compaction must equal the fixture bit for bit.
 Operators that evaluate exp (the sigmoid / softplus of the parameter
-transform, the rasterizer, the voxelizer) and the composed gradients match
-within rel 1e-4 / abs 1e-5 (fp32), with the alpha cut-off allowance of
-tests/helpers.py.
+transform, the rasterizer, the voxelizer) and the composed gradients meet the
+parity bar of helpers.assert_parity with the fixture as the reference-order
+float32 result and the oracle one precision up as the anchor.
 """
 
 import os
@@ -14,7 +14,10 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_close, assert_equal, np32
+from helpers import (assert_equal, assert_parity, check_parameter_gradients, check_raster,
+                     check_voxel, np32, raster_references, voxel_references)
+from oracle import compose, ops
+from r2splat.cuda import _ops
 from r2splat.cuda import _wrapper as W
 from r2splat.ops import compact, explicit
 
@@ -49,7 +52,10 @@ def test_projection_ops_fixture():
     assert_equal(np32(fl), f["flatten_ids"], "flatten_ids")
     assert_equal(np32(off), f["tile_offsets"], "tile_offsets")
     img = W.rasterize_to_pixels_fwd(m2, conics, op, mus, off, fl, 48, 48, 16)
-    assert_close(np32(img), f["image"], "image", max_outliers=2, outlier_atol=3e-5)
+    refs = raster_references(f["means2d"], f["conics"], np32(op), f["mus"], f["tile_offsets"],
+                             f["flatten_ids"], 48, 48, 16)
+    assert_equal(refs["fwd"][1], f["image"], "oracle image = fixture")
+    check_raster(refs, image=np32(img))
 
 
 def test_projection_pipeline_fixture():
@@ -59,24 +65,47 @@ def test_projection_pipeline_fixture():
     means, quats, scales, opac = params
     state = explicit.prepare_explicit_gaussians(quats, scales, opac, scale_min=5e-4,
                                                 scale_max=1.0)
-    assert_close(np32(state.covars), f["covars"], "covars", atol=1e-9)
-    assert_close(np32(state.opacities), f["opacities"], "opacities")
+    hi = lambda k: f[k].astype(np.float64)  # noqa: E731
+    cov64, _ = ops.parameter_transform_fwd(hi("quats"), hi("raw_scales"), 5e-4, 1.0)
+    assert_parity(np32(state.covars), cov64, f["covars"], None, "covars")
+    assert_parity(np32(state.opacities), ops.softplus(hi("raw_opacities")), f["opacities"], None,
+                  "opacities")
     res = explicit.explicit_rasterize(state, means, _t(f["viewmats"]), _t(f["Ks"]), img_w=48,
                                       img_h=48, tile_size=16, eps2d=1e-8, radius_clip=3.0,
                                       absgrad=True)
-    assert_close(np32(res.image), f["image"], "image", max_outliers=2, outlier_atol=3e-5)
     res.image.backward(_t(f["v_image"]))
     explicit.explicit_backward(state, means, quats, scales, opac)
-    for name, got in (("means", means.grad), ("quats", quats.grad), ("raw_scales", scales.grad),
-                      ("raw_opacities", opac.grad), ("means2d", res.means2d.grad),
-                      ("means2d_abs", res.means2d.absgrad)):
-        e = f[f"grad_{name}"]
-        scale = float(np.abs(e).max())
-        # The covariances enter through exp (sigmoid), so the composed
-        # gradients carry their ulp-level differences: same allowance as the
-        # end-to-end pipeline test.
-        assert_close(np32(got), e, f"grad {name}", atol=max(1e-5, 1e-5 * scale),
-                     max_outliers=e.size // 200, outlier_atol=1e-3 * scale)
+    # The fixture's chain ran on its own covariances; the GPU's differ in the
+    # last ulp (exp), so the composition is re-evaluated on the GPU's forward
+    # (bit-exact geometry and lists) and the fixture pins the oracle itself.
+    gc, go = np32(state.covars), np32(state.opacities)
+    proj = compose.rasterize_forward(f["means"], gc, go, f["viewmats"], f["Ks"], 48, 48, 16,
+                                     1e-8, 3.0)
+    assert_equal(np32(state.projection.lists.flatten_ids), proj["flatten_ids"], "flatten_ids")
+    refs = raster_references(proj["means2d"], proj["conics"], proj["opacity"], proj["mus"],
+                             proj["tile_offsets"], proj["flatten_ids"], 48, 48, 16,
+                             v_image=f["v_image"])
+    check_raster(refs, image=np32(res.image))
+    p = state.projection
+    rg = [np32(t) for t in _ops.raster_backward(p.means2d.detach(), p.conics, p.weights, p.mus,
+                                                p.tile_offsets, p.lists, p.image.grad, 48, 48,
+                                                16, True)]
+    check_raster(refs, grads=rg)
+    assert np.array_equal(rg[1], np32(res.means2d.grad))
+    assert np.array_equal(rg[0], np32(res.means2d.absgrad))
+    args = (gc, proj, None, f["means"], f["quats"], f["raw_scales"], f["raw_opacities"], 5e-4,
+            1.0, f["v_image"])
+    got = dict(means=np32(means.grad), quats=np32(quats.grad), raw_scales=np32(scales.grad),
+               raw_opacities=np32(opac.grad))
+    reps, plain = check_parameter_gradients(got, args, rg)
+    print(reps, plain)
+    # The fixture's gradients are the oracle's on the fixture's covariances.
+    fix = compose.explicit_backward(f["covars"], compose.rasterize_forward(
+        f["means"], f["covars"], f["opacities"], f["viewmats"], f["Ks"], 48, 48, 16, 1e-8, 3.0),
+        None, f["means"], f["quats"], f["raw_scales"], f["raw_opacities"], 5e-4, 1.0,
+        f["v_image"])
+    for name in ("means", "quats", "raw_scales", "raw_opacities", "means2d", "means2d_abs"):
+        assert_equal(fix[name], f[f"grad_{name}"], f"oracle grad {name} = fixture")
 
 
 def test_voxel_fixture():
@@ -94,14 +123,16 @@ def test_voxel_fixture():
     assert_equal(np32(fl), f["vox_flatten_ids"], "flatten_ids3d")
     assert_equal(np32(off), f["vox_tile_offsets"], "tile_offsets3d")
     vol = W.voxelize_to_voxels_fwd(m3, con, opac, off, fl, 16, 12, 20, 8)
-    assert_close(np32(vol), f["volume"], "volume", max_outliers=2, outlier_atol=3e-6)
     vm3, vc3, vo3 = W.voxelize_to_voxels_bwd_per_gaussian(m3, con, opac, off, ids, fl,
                                                           _t(f["v_volume"]), 16, 12, 20, 8)
-    for name, got in (("vox_v_means3d", vm3), ("vox_v_conics", vc3), ("vox_v_opacities", vo3)):
-        e = f[name]
-        scale = float(np.abs(e).max())
-        assert_close(np32(got), e, name, atol=max(1e-5, 3e-6 * scale), max_outliers=2,
-                     outlier_atol=2e-4 * scale)
+    refs = voxel_references(f["vox_means3d"], f["vox_conics"], f["opacities"],
+                            f["vox_tile_offsets"], f["vox_flatten_ids"], 16, 12, 20, 8,
+                            v_volume=f["v_volume"])
+    assert_equal(refs["fwd"][1], f["volume"], "oracle volume = fixture")
+    for (_, lo, _, _), name in zip(refs["bwd"], ("vox_v_means3d", "vox_v_conics",
+                                              "vox_v_opacities")):
+        assert_equal(lo, f[name], f"oracle {name} = fixture")
+    print(check_voxel(refs, volume=np32(vol), grads=[np32(t) for t in (vm3, vc3, vo3)]))
     vm, vc = W.world_to_volume_mapping_bwd(means, covars, _t(f["ranges"]), _t(f["centers"]),
                                            16, 12, 20, 1e-8, _t(f["vox_v_means3d"]),
                                            _t(f["vox_v_conics"]))

@@ -1,16 +1,21 @@
-"""Fused projection loss (L1 + SSIM + edge) and volume TV against the oracle.
+"""Fused projection loss (L1 + SSIM + edge), volume TV and hierarchy loss
+against the oracle.
 
-The oracle is float64 on the float32 inputs; the kernels are float32 with a
-separable window, so values agree to float32 rounding of the moment sums:
-losses within 1e-5 absolute, gradients within a small fraction of their
-largest magnitude.
+The oracle is float64 on the float32 inputs.  Losses agree within 1e-5
+absolute.  Gradients meet helpers.assert_parity (rel 1e-4 / abs 1e-5, or
+within twice the error of the reference's own float32 formulation -- the
+torch restatement of src/utils/loss.py / metric.py below -- against the
+float64 oracle, or within 8 u times the sum of |terms| of the gradient's
+formula where it cancels: oracle/loss.py *_magnitude), compared as gradients
+of the summed loss, i.e. scaled by the mean's element count, so that the
+absolute term means the same at every image size.
 """
 
 import numpy as np
 import pytest
 import torch
 
-from helpers import np32
+from helpers import assert_parity, np32
 from oracle import loss as L
 from r2splat.ops import loss as LO
 
@@ -48,12 +53,35 @@ def test_projection_losses_and_gradient(n, h, w, ws, edge):
     assert abs(sl.item() - esl) < 1e-5
     assert abs(ed.item() - eed) < 1e-6 * max(1, eed) + 1e-7
     (scales[0] * l1 + scales[1] * sl + scales[2] * ed).backward()
-    g = np32(r.grad)[..., 0]
-    expect = L.projection_loss_grad(x, y, e, m, scales, ws)
-    scale = np.abs(expect).max()
-    err = np.abs(g - expect)
-    assert err.max() < 2e-3 * scale, (err.max(), scale)
-    assert np.median(err) < 1e-5 * scale
+    n_el = x.size
+    g = np32(r.grad)[..., 0].astype(np.float64) * n_el
+    expect = L.projection_loss_grad(x, y, e, m, scales, ws) * n_el
+    lowp = _torch_f32_grad(x, y, e, m, scales, ws).astype(np.float64) * n_el
+    mag = L.projection_loss_grad_magnitude(x, y, e, m, scales, ws) * n_el
+    print(assert_parity(g.astype(np.float32), expect, lowp, None, "n * d loss / d render",
+                        mag=mag))
+
+
+def _torch_f32_grad(x, y, e, m, scales, ws):
+    """d(scales . losses)/dx of the reference's float32 formulation
+    (src/utils/metric.py:36-54 ssim with a conv2d of the float32 window,
+    src/utils/loss.py:135-172 l1 / edge means), by torch autograd on the CPU."""
+    _, win = L.gaussian_window(ws)
+    w = torch.tensor(win, dtype=torch.float32)[None, None]
+    xt = torch.tensor(x, requires_grad=True)
+    yt = torch.tensor(y)
+    conv = lambda t: torch.nn.functional.conv2d(t[:, None], w, padding=ws // 2)  # noqa: E731
+    mu1, mu2 = conv(xt), conv(yt)
+    s11 = conv(xt * xt) - mu1 * mu1
+    s22 = conv(yt * yt) - mu2 * mu2
+    s12 = conv(xt * yt) - mu1 * mu2
+    S = ((2 * mu1 * mu2 + L.C1) * (2 * s12 + L.C2)) / ((mu1 * mu1 + mu2 * mu2 + L.C1) *
+                                                        (s11 + s22 + L.C2))
+    total = scales[0] * (xt - yt).abs().mean() + scales[1] * (1 - S.mean())
+    if e is not None:
+        total = total + scales[2] * (torch.tensor(m) * (xt - torch.tensor(e)).abs()).mean()
+    total.backward()
+    return xt.grad.numpy()
 
 
 def test_projection_loss_is_deterministic():
@@ -154,6 +182,30 @@ def test_hierarchy_loss_and_gradient(n, h):
     exp_loss, exp_grad = L.hierarchy_loss(cm, par, hm, act, hq, h, 0.9)
     assert abs(loss.item() - exp_loss) <= 1e-5 * max(1.0, exp_loss)
     (loss * 2.0).backward()
-    g = np32(c.grad)
-    scale = np.abs(exp_grad).max() * 2.0 + 1e-30
-    assert np.abs(g - 2.0 * exp_grad).max() < 1e-4 * scale
+    k = int(((par >= 0) & (par < h)).sum())  # the mean's count
+    g = np32(c.grad).astype(np.float64) * k
+    lowp = _torch_f32_hierarchy_grad(cm, par, hm, act, hq, h, 0.9) * 2.0 * k
+    mag = L.hierarchy_grad_magnitude(cm, par, hm, act, hq, h, 0.9) * 2.0 * k
+    print(assert_parity(g.astype(np.float32), 2.0 * exp_grad * k, lowp, None,
+                        "count * d loss / d child_means", mag=mag))
+
+
+def _torch_f32_hierarchy_grad(cm, par, hm, act, hq, h, factor):
+    """src/utils/loss.py:27-71 in float32 torch on the CPU (autograd)."""
+    c = torch.tensor(cm, requires_grad=True)
+    p = torch.tensor(par).long()
+    valid = (p >= 0) & (p < h)
+    ids = p[valid]
+    q = torch.nn.functional.normalize(torch.tensor(hq)[ids], dim=-1)
+    w, x, y, z = q.unbind(-1)
+    R = torch.stack([1 - 2 * (y * y + z * z), 2 * (x * y - w * z), 2 * (x * z + w * y),
+                     2 * (x * y + w * z), 1 - 2 * (x * x + z * z), 2 * (y * z - w * x),
+                     2 * (x * z - w * y), 2 * (y * z + w * x), 1 - 2 * (x * x + y * y)],
+                    -1).reshape(-1, 3, 3)
+    s = torch.tensor(act)[ids].clamp_min(1e-6)
+    d = c[valid] - torch.tensor(hm)[ids]
+    u = (R.transpose(1, 2) @ d[..., None])[..., 0] / s
+    a = max(float(factor), 1e-6)
+    e = torch.relu(u.norm(dim=-1) - a) / a
+    (e * e).mean().backward()
+    return c.grad.numpy().astype(np.float64)

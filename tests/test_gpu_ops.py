@@ -1,16 +1,20 @@
 """HIP operators vs the CPU oracle on seeded inputs (op level).
 
 Bit-exact where the kernel has no transcendental function (projection,
-conics/mu, volume mapping, their VJPs, binning, offsets, compaction);
-rel 1e-4 / abs 1e-5 otherwise.  Every call goes through the C ABI via
-r2splat.cuda._wrapper.
+conics/mu, volume mapping, their VJPs, binning, offsets, compaction).
+Otherwise every output is checked against the oracle one precision up with
+helpers.assert_parity: rel 1e-4 / abs 1e-5 in float32 (rel 1e-9 / abs
+1e-12 in float64), or within twice the reference order's own error, plus
+the flip band of terms at an alpha cut-off (flips are counted).  Every call
+goes through the C ABI via r2splat.cuda._wrapper or r2splat.cuda._ops.
 """
 
 import numpy as np
 import pytest
 import torch
 
-from helpers import assert_close, assert_equal, make_scene, np32
+from helpers import (assert_close, assert_equal, assert_parity, check_raster, check_voxel,
+                     make_scene, np32, raster_references, voxel_references)
 from oracle import binning, native, ops
 from r2splat.cuda import _ops
 from r2splat.cuda import _wrapper as W
@@ -46,18 +50,24 @@ def test_parameter_transform(dtype):
     o = raw.raw_opacities.to(dtype)
     qd, sd, od = q.to(DEV), s.to(DEV), o.to(DEV)
     cov, ms = W.parameter_transform_fwd(qd, sd, 5e-4, 1.0)
+    hi = np.float64 if dtype == torch.float32 else np.longdouble
     cov_o, ms_o = ops.parameter_transform_fwd(q.numpy(), s.numpy(), 5e-4, 1.0)
-    assert_close(np32(cov), cov_o, "covars")
-    assert_close(np32(ms), ms_o, "max_scales")
+    cov_a, ms_a = ops.parameter_transform_fwd(q.numpy().astype(hi), s.numpy().astype(hi), 5e-4,
+                                              1.0)
+    assert_parity(np32(cov), cov_a, cov_o, None, "covars")
+    assert_parity(np32(ms), ms_a, ms_o, None, "max_scales")
     cov2, ms2, op2 = W.prepare_gaussians(qd, sd, od, 5e-4, 1.0)
     assert_equal(np32(cov2), np32(cov), "fused covars")
     assert_equal(np32(ms2), np32(ms), "fused max_scales")
-    assert_close(np32(op2), np32(torch.nn.functional.softplus(od)), "softplus")
+    assert_parity(np32(op2), ops.softplus(o.numpy().astype(hi)), ops.softplus(o.numpy()), None,
+                  "softplus")
     v = torch.randn(3000, 6, generator=g, dtype=dtype)
     vq, vs = W.parameter_transform_bwd(qd, sd, 5e-4, 1.0, v.to(DEV))
     vq_o, vs_o = ops.parameter_transform_bwd(q.numpy(), s.numpy(), 5e-4, 1.0, v.numpy())
-    assert_close(np32(vq), vq_o, "v_quats", atol=1e-4 if dtype == torch.float32 else 1e-9)
-    assert_close(np32(vs), vs_o, "v_raw_scales", atol=1e-4 if dtype == torch.float32 else 1e-9)
+    vq_a, vs_a = ops.parameter_transform_bwd(q.numpy().astype(hi), s.numpy().astype(hi), 5e-4,
+                                             1.0, v.numpy().astype(hi))
+    assert_parity(np32(vq), vq_a, vq_o, None, "v_quats")
+    assert_parity(np32(vs), vs_a, vs_o, None, "v_raw_scales")
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
@@ -216,10 +226,9 @@ def test_isect_tiles_capacity_guess():
         args = (m2.to(DEV), con.to(DEV), op.to(DEV), mu.to(DEV), off)
         got = W.rasterize_to_pixels_bwd_per_gaussian(*args, ids, fl, v, 512, 512, 16, True)
         # The same records in exact-size tensors, with the same emission order.
-        emit_ids, src = _ops._emission_order(fl, 1024)
-        ids2, fl2 = ids.clone(), fl.clone()
-        _ops._keep_emission_order(fl2, emit_ids.clone(), src.clone(), 1024)
-        want = W.rasterize_to_pixels_bwd_per_gaussian(*args, ids2, fl2, v, 512, 512, 16, True)
+        emit_ids, src = _ops.emission_order(fl, 1024)
+        lists = _ops.TileLists(tpg, ids.clone(), fl.clone(), emit_ids.clone(), src.clone())
+        want = _ops.raster_backward(*args, lists, v, 512, 512, 16, True)
         for a, b in zip(got, want):
             assert torch.equal(a, b)
     # First call exact; the third (60 > the guess from 20 and 10) relaunched.
@@ -290,19 +299,13 @@ def test_rasterize_fwd_bwd(dtype, shape, order):
     d, m2, con, mu, op, ids, fl, off = _raster_case(3000, 7, W_img, H_img, ts, 2, dtype)
     assert fl.numel() > 500
     img = W.rasterize_to_pixels_fwd(m2, con, op, mu, off, fl, W_img, H_img, ts)
-    img_o = native.raster_fwd(np32(m2), np32(con), np32(op), np32(mu), np32(off), np32(fl),
-                              W_img, H_img, ts)
-    f32 = dtype == torch.float32
-    tol = dict(rtol=1e-4, atol=1e-5) if f32 else dict(rtol=1e-9, atol=1e-12)
-    assert_close(np32(img), img_o, "image", max_outliers=img_o.size // 1000 if f32 else 0,
-                 outlier_atol=3e-5 if f32 else None, **tol)
     v = torch.randn(img.shape, generator=d["gen"], dtype=dtype)
-    ref = native.raster_bwd(np32(m2), np32(con), np32(op), np32(mu), np32(off), np32(fl),
-                            v.numpy(), W_img, H_img, ts, True)
-    names = ("v_means2d_abs", "v_means2d", "v_conics", "v_opacities", "v_mus")
+    refs = raster_references(np32(m2), np32(con), np32(op), np32(mu), np32(off), np32(fl),
+                             W_img, H_img, ts, v_image=v.numpy())
+    print("image", check_raster(refs, image=np32(img)))
     if order == "tile":
         fl = fl.clone()  # no emission-order records: the tile-order kernels run
-    assert (_ops._emission_order(fl, fl_keys(off)) is not None) == (order == "emission")
+    assert (_ops.emission_order(fl, fl_keys(off)) is not None) == (order == "emission")
     for mode in ("primitive", "pixel"):
         if mode == "primitive":
             got = W.rasterize_to_pixels_bwd_per_gaussian(m2, con, op, mu, off, ids, fl,
@@ -310,12 +313,8 @@ def test_rasterize_fwd_bwd(dtype, shape, order):
         else:
             got = W.rasterize_to_pixels_bwd(m2, con, op, mu, off, fl, v.to(DEV), W_img, H_img,
                                             ts, True)
-        for a, e, n in zip(got, ref, names):
-            scale = float(np.abs(e).max()) + 1e-30
-            assert_close(np32(a), e, f"{mode} {n}", rtol=tol["rtol"],
-                         atol=max(tol["atol"], (3e-6 if f32 else 1e-12) * scale),
-                         max_outliers=e.size // 500 if f32 else 0,
-                         outlier_atol=2e-4 * scale if f32 else None)
+        for n, r in check_raster(refs, grads=[np32(t) for t in got], tag=f"{mode} ").items():
+            print(mode, n, r)
     no_abs = W.rasterize_to_pixels_bwd_per_gaussian(m2, con, op, mu, off, ids, fl, v.to(DEV),
                                                     W_img, H_img, ts, False)
     assert no_abs[0] is None
@@ -342,10 +341,9 @@ def test_rasterize_fwd_small_gaussians(ts):
     _, ids, fl = W.isect_tiles(m2, r, ts, tw, th)
     off = W.isect_offset_encode(ids, 1, tw, th)
     img = W.rasterize_to_pixels_fwd(m2, con, op, mu, off, fl, W_img, H_img, ts)
-    img_o = native.raster_fwd(np32(m2), np32(con), np32(op), np32(mu), np32(off), np32(fl),
-                              W_img, H_img, ts)
-    assert_close(np32(img), img_o, "image", rtol=1e-4, atol=1e-5,
-                 max_outliers=img_o.size // 1000, outlier_atol=3e-5)
+    refs = raster_references(np32(m2), np32(con), np32(op), np32(mu), np32(off), np32(fl),
+                             W_img, H_img, ts)
+    print(check_raster(refs, image=np32(img)))
 
 
 @pytest.mark.parametrize("dims,ts", [((32, 32, 32), 8), ((30, 20, 40), 10)])
@@ -356,10 +354,9 @@ def test_voxelize_fwd_small_gaussians(dims, ts):
     assert float(con[..., 0].max()) > 10.0
     d2, d1, d0 = dims
     vol = W.voxelize_to_voxels_fwd(m3, con, d["opac"], off, fl, d2, d1, d0, ts)
-    vol_o = native.voxel_fwd(np32(m3), np32(con), np32(d["opac"]), np32(off), np32(fl), d2, d1,
-                             d0, ts)
-    assert_close(np32(vol), vol_o, "volume", rtol=1e-4, atol=1e-5,
-                 max_outliers=vol_o.size // 1000, outlier_atol=3e-6)
+    refs = voxel_references(np32(m3), np32(con), np32(d["opac"]), np32(off), np32(fl), d2, d1,
+                            d0, ts)
+    print(check_voxel(refs, volume=np32(vol)))
 
 
 def _one_sign(p, q, dxa, dya, span=15.0, margin=1.0 / 64):
@@ -397,18 +394,12 @@ def test_absgrad_sign_split_backward(dtype, shape):
     assert (per_block >= 64).any() and (per_block < 256).any(), per_block
     img = W.rasterize_to_pixels_fwd(m2, con, op, mu, off, fl, W_img, H_img, 16)
     v = torch.randn(img.shape, generator=d["gen"], dtype=dtype)
-    ref = native.raster_bwd(np32(m2), np32(con), np32(op), np32(mu), np32(off), np32(fl),
-                            v.numpy(), W_img, H_img, 16, True)
+    refs = raster_references(np32(m2), np32(con), np32(op), np32(mu), np32(off), np32(fl),
+                             W_img, H_img, 16, v_image=v.numpy())
     got = W.rasterize_to_pixels_bwd_per_gaussian(m2, con, op, mu, off, ids, fl, v.to(DEV),
                                                  W_img, H_img, 16, True)
-    f32 = dtype == torch.float32
-    names = ("v_means2d_abs", "v_means2d", "v_conics", "v_opacities", "v_mus")
-    for x, e, n in zip(got, ref, names):
-        scale = float(np.abs(e).max()) + 1e-30
-        assert_close(np32(x), e, n, rtol=1e-4 if f32 else 1e-9,
-                     atol=(3e-6 if f32 else 1e-12) * scale,
-                     max_outliers=e.size // 500 if f32 else 0,
-                     outlier_atol=2e-4 * scale if f32 else None)
+    for n, r in check_raster(refs, grads=[np32(t) for t in got]).items():
+        print(n, r)
 
 
 @pytest.mark.parametrize("order", ["emission", "tile"])
@@ -416,50 +407,37 @@ def test_nan_opacity_propagates_as_in_the_reference(order):
     # A NaN alpha is not below the cut-off, so the reference does not skip it:
     # the pixels / voxels of a NaN-opacity Gaussian's tiles turn NaN, and so do
     # that Gaussian's gradients that carry its opacity.  The NaN patterns must
-    # match the oracle's exactly, the finite values within tolerance.
+    # match the oracle's exactly, the finite values the parity bar.
     d, m2, con, mu, op, ids, fl, off = _raster_case(3000, 17, 64, 64, 16, 1, torch.float32)
     g = int(fl[fl.numel() // 2])
     op = op.clone()
     op[0, g] = float("nan")
     img = W.rasterize_to_pixels_fwd(m2, con, op, mu, off, fl, 64, 64, 16)
-    img_o = native.raster_fwd(np32(m2), np32(con), np32(op), np32(mu), np32(off), np32(fl),
-                              64, 64, 16)
-    assert np.isnan(img_o).any() and not np.isnan(img_o).all()
-    assert_close(np32(img), img_o, "image", max_outliers=img_o.size // 1000,
-                 outlier_atol=3e-5)
     v = torch.randn(img.shape, generator=d["gen"])
-    ref = native.raster_bwd(np32(m2), np32(con), np32(op), np32(mu), np32(off), np32(fl),
-                            v.numpy(), 64, 64, 16, True)
+    refs = raster_references(np32(m2), np32(con), np32(op), np32(mu), np32(off), np32(fl), 64,
+                             64, 16, v_image=v.numpy())
+    assert np.isnan(refs["fwd"][0]).any() and not np.isnan(refs["fwd"][0]).all()
+    check_raster(refs, image=np32(img))
     fl_run = fl if order == "emission" else fl.clone()
     got = W.rasterize_to_pixels_bwd_per_gaussian(m2, con, op, mu, off, ids, fl_run, v.to(DEV),
                                                  64, 64, 16, True)
-    for a, e, n in zip(got, ref, ("v_means2d_abs", "v_means2d", "v_conics", "v_opacities",
-                                  "v_mus")):
-        fin = e[np.isfinite(e)]
-        scale = float(np.abs(fin).max()) + 1e-30
-        assert_close(np32(a), e, n, atol=max(1e-5, 3e-6 * scale), max_outliers=e.size // 500,
-                     outlier_atol=2e-4 * scale)
-    assert np.isnan(ref[1]).any()
+    check_raster(refs, grads=[np32(t) for t in got])
+    assert np.isnan(refs["bwd"][1][0]).any()
     d3, m3, con3, ids3, fl3, off3 = _voxel_case(2500, 18, (32, 32, 32), 8)
     g3 = int(fl3[fl3.numel() // 2])
     op3 = d3["opac"].clone()
     op3[g3] = float("nan")
     vol = W.voxelize_to_voxels_fwd(m3, con3, op3, off3, fl3, 32, 32, 32, 8)
-    vol_o = native.voxel_fwd(np32(m3), np32(con3), np32(op3), np32(off3), np32(fl3), 32, 32, 32, 8)
-    assert np.isnan(vol_o).any() and not np.isnan(vol_o).all()
-    assert_close(np32(vol), vol_o, "volume", max_outliers=vol_o.size // 1000, outlier_atol=3e-6)
     v3 = torch.randn(vol.shape, generator=d3["gen"])
-    ref3 = native.voxel_bwd(np32(m3), np32(con3), np32(op3), np32(off3), np32(fl3), v3.numpy(),
-                            32, 32, 32, 8)
+    refs3 = voxel_references(np32(m3), np32(con3), np32(op3), np32(off3), np32(fl3), 32, 32, 32,
+                             8, v_volume=v3.numpy())
+    assert np.isnan(refs3["fwd"][0]).any() and not np.isnan(refs3["fwd"][0]).all()
+    check_voxel(refs3, volume=np32(vol))
     fl3_run = fl3 if order == "emission" else fl3.clone()
     got3 = W.voxelize_to_voxels_bwd_per_gaussian(m3, con3, op3, off3, ids3, fl3_run, v3.to(DEV),
                                                  32, 32, 32, 8)
-    for a, e, n in zip(got3, ref3, ("v_means3d", "v_conics", "v_opacities")):
-        fin = e[np.isfinite(e)]
-        scale = float(np.abs(fin).max()) + 1e-30
-        assert_close(np32(a), e, n, atol=max(1e-5, 3e-6 * scale), max_outliers=e.size // 500,
-                     outlier_atol=2e-4 * scale)
-    assert np.isnan(ref3[0]).any()
+    check_voxel(refs3, grads=[np32(t) for t in got3])
+    assert np.isnan(refs3["bwd"][0][0]).any()
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
@@ -476,13 +454,9 @@ def test_rasterize_fwd_splits_heavy_tiles(dtype, shape):
     lib = _backend.library()
     assert lib.r2s_rasterize_workspace_bytes(n_keys, fl.numel(), ts, 4) > 0  # split path
     img = W.rasterize_to_pixels_fwd(m2, con, op, mu, off, fl, W_img, H_img, ts)
-    img_o = native.raster_fwd(np32(m2), np32(con), np32(op), np32(mu), np32(off), np32(fl),
-                              W_img, H_img, ts)
-    f32 = dtype == torch.float32
-    scale = float(np.abs(img_o).max())
-    tol = dict(rtol=1e-4, atol=1e-6 * scale) if f32 else dict(rtol=1e-9, atol=1e-12 * scale)
-    assert_close(np32(img), img_o, "image", max_outliers=img_o.size // 1000 if f32 else 0,
-                 outlier_atol=3e-5 if f32 else None, **tol)
+    refs = raster_references(np32(m2), np32(con), np32(op), np32(mu), np32(off), np32(fl),
+                             W_img, H_img, ts)
+    print(check_raster(refs, image=np32(img)))
     again = W.rasterize_to_pixels_fwd(m2, con, op, mu, off, fl, W_img, H_img, ts)
     assert torch.equal(img, again)
 
@@ -523,29 +497,21 @@ def test_voxelize_fwd_bwd(dtype, dims, ts, order):
     assert fl.numel() > 500
     op = d["opac"]
     vol = W.voxelize_to_voxels_fwd(m3, con, op, off, fl, d2, d1, d0, ts)
-    vol_o = native.voxel_fwd(np32(m3), np32(con), np32(op), np32(off), np32(fl), d2, d1, d0, ts)
-    f32 = dtype == torch.float32
-    tol = dict(rtol=1e-4, atol=1e-5) if f32 else dict(rtol=1e-9, atol=1e-12)
-    assert_close(np32(vol), vol_o, "volume", max_outliers=vol_o.size // 1000 if f32 else 0,
-                 outlier_atol=3e-6 if f32 else None, **tol)
     v = torch.randn(vol.shape, generator=d["gen"], dtype=dtype)
-    ref = native.voxel_bwd(np32(m3), np32(con), np32(op), np32(off), np32(fl), v.numpy(), d2, d1,
-                           d0, ts)
+    refs = voxel_references(np32(m3), np32(con), np32(op), np32(off), np32(fl), d2, d1, d0, ts,
+                            v_volume=v.numpy())
+    print("volume", check_voxel(refs, volume=np32(vol)))
     if order == "tile":
         fl = fl.clone()  # no emission-order records: the tile-order kernels run
-    assert (_ops._emission_order(fl, fl_keys(off)) is not None) == (order == "emission")
+    assert (_ops.emission_order(fl, fl_keys(off)) is not None) == (order == "emission")
     for mode in ("primitive", "pixel"):
         if mode == "primitive":
             got = W.voxelize_to_voxels_bwd_per_gaussian(m3, con, op, off, ids, fl, v.to(DEV), d2,
                                                         d1, d0, ts)
         else:
             got = W.voxelize_to_voxels_bwd(m3, con, op, off, fl, v.to(DEV), d2, d1, d0, ts)
-        for a, e, n in zip(got, ref, ("v_means3d", "v_conics", "v_opacities")):
-            scale = float(np.abs(e).max()) + 1e-30
-            assert_close(np32(a), e, f"{mode} {n}", rtol=tol["rtol"],
-                         atol=max(tol["atol"], (3e-6 if f32 else 1e-12) * scale),
-                         max_outliers=e.size // 500 if f32 else 0,
-                         outlier_atol=2e-4 * scale if f32 else None)
+        for n, r in check_voxel(refs, grads=[np32(t) for t in got], tag=f"{mode} ").items():
+            print(mode, n, r)
 
 
 def _voxel_row_reach(m3, con, op, ids, fl, dims, ts):
@@ -592,18 +558,17 @@ def test_voxelize_bwd_chunked_and_dense_waves(log_mu, dense):
     assert (dense_waves > 0.5) == dense, dense_waves
     vol = W.voxelize_to_voxels_fwd(m3, con, op, off, fl, d2, d1, d0, 8)
     v = torch.randn(vol.shape, generator=d["gen"])
-    ref = native.voxel_bwd(np32(m3), np32(con), np32(op), np32(off), np32(fl), v.numpy(), d2, d1,
-                           d0, 8)
+    refs = voxel_references(np32(m3), np32(con), np32(op), np32(off), np32(fl), d2, d1, d0, 8,
+                            v_volume=v.numpy())
+    check_voxel(refs, volume=np32(vol))
     for mode in ("primitive", "pixel"):
         if mode == "primitive":
             got = W.voxelize_to_voxels_bwd_per_gaussian(m3, con, op, off, ids, fl, v.to(DEV), d2,
                                                         d1, d0, 8)
         else:
             got = W.voxelize_to_voxels_bwd(m3, con, op, off, fl, v.to(DEV), d2, d1, d0, 8)
-        for a, e, n in zip(got, ref, ("v_means3d", "v_conics", "v_opacities")):
-            scale = float(np.abs(e).max()) + 1e-30
-            assert_close(np32(a), e, f"{mode} {n}", atol=max(1e-5, 3e-6 * scale),
-                         max_outliers=e.size // 500, outlier_atol=2e-4 * scale)
+        for n, r in check_voxel(refs, grads=[np32(t) for t in got], tag=f"{mode} ").items():
+            print(mode, n, r)
 
 
 @pytest.mark.parametrize("n", [0, 1, 63, 64, 65, 4095, 4096, 4097, 100_003, 2_000_000])
@@ -679,7 +644,7 @@ def test_backward_stage_entry_points_match_the_two_pass_op():
     v = torch.randn((2, 48, 64), generator=d["gen"]).to(DEV)
     want = W.rasterize_to_pixels_bwd_per_gaussian(m2, con, op, mu, off, ids, fl, v, 64, 48, 16,
                                                   True)
-    emit_ids, src = _ops._emission_order(fl, off.numel())
+    emit_ids, src = _ops.emission_order(fl, off.numel())
     n, N = fl.numel(), m2.shape[1]
     rows = torch.empty(lib.r2s_rasterize_bwd_workspace_bytes(n, 4), dtype=torch.uint8,
                        device=DEV)
@@ -699,7 +664,7 @@ def test_backward_stage_entry_points_match_the_two_pass_op():
     d3, m3, con3, ids3, fl3, off3 = _voxel_case(2500, 14, (32, 24, 16), 8)
     v3 = torch.randn((16, 24, 32), generator=d3["gen"]).to(DEV)
     want3 = W.voxelize_to_voxels_bwd(m3, con3, d3["opac"], off3, fl3, v3, 32, 24, 16, 8)
-    emit3, src3 = _ops._emission_order(fl3, off3.numel())
+    emit3, src3 = _ops.emission_order(fl3, off3.numel())
     n3, N3 = fl3.numel(), m3.shape[0]
     rows3 = torch.empty(lib.r2s_voxelize_bwd_workspace_bytes(n3, 4), dtype=torch.uint8,
                         device=DEV)
@@ -711,3 +676,38 @@ def test_backward_stage_entry_points_match_the_two_pass_op():
                                            st) == 0
     for a, b in zip(got3, want3):
         assert torch.equal(a, b)
+
+
+def test_one_pass_fallback_is_counted_and_warned():
+    """The wrapper-level backward finds the emission order only on the very
+    flatten_ids tensor isect_tiles returned; any other tensor runs the
+    one-pass kernels, which is counted and warned about (once per process).
+    The explicit TileLists path needs no lookup."""
+    d, m2, con, mu, op, ids, fl, off = _raster_case(2000, 19, 64, 64, 16, 1, torch.float32)
+    v = torch.randn(1, 64, 64, generator=d["gen"]).to(DEV)
+    args = (m2, con, op, mu, off)
+    _ops._WARNED_ONE_PASS = False
+    c0 = dict(_ops.PATH_COUNTS)
+    fast = W.rasterize_to_pixels_bwd_per_gaussian(*args, ids, fl, v, 64, 64, 16, True)
+    assert _ops.PATH_COUNTS["two_pass"] == c0["two_pass"] + 1
+    with pytest.warns(_ops.OnePassBackwardWarning, match="one-pass"):
+        slow = W.rasterize_to_pixels_bwd_per_gaussian(*args, ids, fl.clone(), v, 64, 64, 16, True)
+    assert _ops.PATH_COUNTS["one_pass"] == c0["one_pass"] + 1
+    fl.add_(0)  # an in-place change invalidates the attached order
+    assert _ops.emission_order(fl, off.numel()) is None
+    lists = _ops.bin_tiles_2d(m2, _raster_radii(m2, d), 16, 4, 4)
+    assert lists.emission is not None and torch.equal(lists.flatten_ids, fl)
+    c1 = dict(_ops.PATH_COUNTS)
+    explicit = _ops.raster_backward(*args, lists, v, 64, 64, 16, True)
+    assert _ops.PATH_COUNTS == dict(c1, two_pass=c1["two_pass"] + 1)
+    for a, b, c in zip(fast, slow, explicit):
+        assert torch.equal(a, c)
+        assert_close(np32(b), np32(a), "one-pass vs two-pass", rtol=1e-4, atol=1e-5)
+
+
+def _raster_radii(m2, d):
+    Ks = d["Ks"].clone()
+    Ks[:, 0, 2] = 32
+    Ks[:, 1, 2] = 32
+    return W.project_gaussians_fwd(d["means"], d["covars"], d["opac"], d["viewmats"], Ks, 64, 64,
+                                   1e-8, 3.0)[2]

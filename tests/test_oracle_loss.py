@@ -148,3 +148,32 @@ def test_hierarchy_loss_closed_form_and_autograd():
     ref.backward()
     assert abs(loss - ref.item()) < 1e-12
     np.testing.assert_allclose(grad, ct.grad.numpy(), rtol=1e-9, atol=1e-14)
+
+
+@pytest.mark.parametrize("ws", [1, 11])
+def test_gradient_magnitude_bounds_the_gradient(ws):
+    rng = np.random.default_rng(3)
+    x = rng.uniform(size=(2, 19, 23))
+    y = np.clip(x + rng.normal(0, 0.2, size=x.shape), 0, 1)
+    e = rng.uniform(size=x.shape)
+    m = (rng.uniform(size=x.shape) < 0.3).astype(np.float64)
+    scales = (1.0, 0.25, 0.7)
+    g = L.projection_loss_grad(x, y, e, m, scales, ws)
+    mag = L.projection_loss_grad_magnitude(x, y, e, m, scales, ws)
+    assert (mag >= np.abs(g) * (1 - 1e-12)).all()
+    if ws == 1:  # the cancelling terms are ~1e3 times the gradient
+        assert np.median(mag / np.maximum(np.abs(g), 1e-300)) > 10
+
+
+def test_hierarchy_magnitude_bounds_the_gradient():
+    rng = np.random.default_rng(4)
+    h, n = 50, 400
+    hm = rng.normal(size=(h, 3))
+    hs = np.exp(rng.normal(-1.5, 0.5, size=(h, 3)))
+    hq = rng.normal(size=(h, 4))
+    par = rng.integers(-2, h + 2, n)
+    cm = hm[np.clip(par, 0, h - 1)] + rng.normal(0, 0.3, (n, 3))
+    _, g = L.hierarchy_loss(cm, par, hm, hs, hq, h, 0.9)
+    mag = L.hierarchy_grad_magnitude(cm, par, hm, hs, hq, h, 0.9)
+    assert (mag >= np.abs(g) * (1 - 1e-12)).all()
+    assert (mag[np.abs(g) > 0] > 2 * np.abs(g[np.abs(g) > 0])).all()
