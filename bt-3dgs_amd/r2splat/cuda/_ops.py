@@ -128,6 +128,10 @@ def _emit_and_sort(launch, offsets: Tensor, n_items: int, n_keys: int, op: str,
     if recent:
         guess = max(recent)
         cap = min(guess + guess // 8 + 4096, 2 ** 31 - 1)
+        if max_records is not None:
+            # A list that fits the speculative capacity must also fit the
+            # caller's limit; a longer one falls through to the check below.
+            cap = min(cap, max_records)
         outs, ws = alloc(cap)
         pinned = getattr(_PINNED_COUNT, "by_device", None)
         if pinned is None:

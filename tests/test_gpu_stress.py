@@ -12,7 +12,8 @@ deterministic.
 With 5 % needles the 512^3 volume needs 7.46e9 brick records (the needles'
 bounding boxes span the volume), beyond the int32 tile offsets of the
 reference and of its operator signature: isect_tiles_3d must fail cleanly
-before allocating.  The volume with 0.05 % needles (2.5e8 records) runs as
+before allocating (r2splat.ops voxelizes that volume in z-slabs, checked in
+test_gpu_slabs.py).  The volume with 0.05 % needles (2.5e8 records) runs as
 one list.
 """
 

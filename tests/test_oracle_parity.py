@@ -288,3 +288,27 @@ def test_sampled_tiles_and_records_reproduce_the_whole_oracle():
     for r in range(vrec.size):
         vs[v["fl"][r]] += vval[r]
     assert np.array_equal(vs, np.concatenate([vg[0], vg[1], vg[2][:, None]], 1))
+
+
+def test_voxel_oracle_on_slab_segments_with_a_key_offset():
+    v = _voxel_scene(N=300)
+    d2, d1, d0 = v["dims"]
+    n0, n1, n2 = v["off"].shape
+    # The whole list's segment of brick layers [1, 3) as a slab: keys
+    # relative to layer 1, offsets of its 2 layers.
+    keys_full = np.repeat(np.arange(v["off"].size), np.diff(np.append(v["off"].reshape(-1),
+                                                                      v["fl"].size)))
+    plane = n1 * n2
+    seg = (keys_full >= plane) & (keys_full < 3 * plane)
+    rel = keys_full[seg] - plane
+    off = np.searchsorted(rel, np.arange(2 * plane), "left").astype(np.int32).reshape(2, n1, n2)
+    fl_seg = v["fl"][seg]
+    vargs = (v["m3"], v["con"], v["op"])
+    full = native.voxel_fwd(*vargs, v["off"], v["fl"], d2, d1, d0, v["ts"])
+    slab = native.voxel_fwd(*vargs, off, fl_seg, d2, d1, d0, v["ts"], key_offset=plane)
+    assert np.array_equal(slab[8:24], full[8:24]) and not slab[:8].any()
+    rec_f, val_f, _, _ = native.voxel_records(*vargs, v["off"], v["fl"], v["v"], d2, d1, d0,
+                                              v["ts"], np.arange(plane, 3 * plane))
+    rec_s, val_s, _, _ = native.voxel_records(*vargs, off, fl_seg, v["v"], d2, d1, d0, v["ts"],
+                                              np.arange(2 * plane), key_offset=plane)
+    assert np.array_equal(val_s, val_f) and rec_s.size == seg.sum()
