@@ -676,10 +676,12 @@ def layer_counts_3d(means3d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim2
     return counts[:n0].tolist()
 
 
-def plan_slabs(layer_counts, limit: int = SLAB_RECORDS) -> list:
+def plan_slabs(layer_counts, limit: Optional[int] = None) -> list:
     """Consecutive brick-layer ranges [z0, z1) of at most ``limit`` records
-    each (a layer above the limit on its own; one above the int32 offset
-    range raises RuntimeError)."""
+    each (default: SLAB_RECORDS as it is at the call; a layer above the limit
+    on its own; one above the int32 offset range raises RuntimeError)."""
+    if limit is None:
+        limit = SLAB_RECORDS
     slabs, z0, run = [], 0, 0
     for z, c in enumerate(layer_counts):
         _check_record_count(int(c), "isect_tiles_3d (one brick layer)")

@@ -182,7 +182,8 @@ class VolumePass:
         weights = opacities.contiguous()
         lists = ops.bin_tiles_3d(means3d, radii, ts, n2, n1, n0, max_records=ops.SLAB_RECORDS)
         if lists is None:
-            slabs = tuple(ops.plan_slabs(ops.layer_counts_3d(means3d, radii, ts, n2, n1, n0)))
+            slabs = tuple(ops.plan_slabs(ops.layer_counts_3d(means3d, radii, ts, n2, n1, n0),
+                                         ops.SLAB_RECORDS))
             volume = torch.empty((d0, d1, d2), dtype=means3d.dtype, device=means3d.device)
             for z0, z1 in slabs:
                 slab_lists, slab_offsets = ops.bin_tiles_3d_slab(means3d, radii, ts, n2, n1, n0,
