@@ -27,6 +27,15 @@
 #include "r2s_rows.h"
 #include "r2s_scan.h"
 
+#include <mutex>
+
+// Partial tiles of r2s_rasterize_fwd_noalloc_*: a device array that each GPU
+// holds from the library's load to the end of the process.  Host code never
+// passes its name to a kernel (on the host it is a stand-in, not a device
+// address): it uses the address hipGetSymbolAddress returns for the current
+// device.
+static __device__ __align__(256) unsigned char scratch[R2S_RASTER_SCRATCH_BYTES];
+
 namespace r2s {
 namespace {
 
@@ -973,10 +982,99 @@ int raster_bwd_impl(const T *means2d, const T *conics, const T *opac, const T *m
                                v_mu, st);
 }
 
+// Device address of `scratch` on the current device, looked up once per
+// device and cached (each GPU holds its own copy at its own address).
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_lock;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_address(void **out, hipStream_t stream, const char *name) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) {
+    set_error("%s: hipGetDevice failed: %s", name, hipGetErrorString(err));
+    return R2S_EHIP;
+  }
+  R2S_REQUIRE(dev >= 0 && dev < kMaxDevices, "%s: device %d beyond %d", name, dev, kMaxDevices);
+  if (stream != nullptr) {
+    // The kernels run on the stream's device; the address must be that one's.
+    hipDevice_t sdev = -1;
+    err = hipStreamGetDevice(stream, &sdev);
+    if (err != hipSuccess) {
+      set_error("%s: hipStreamGetDevice failed: %s", name, hipGetErrorString(err));
+      return R2S_EHIP;
+    }
+    R2S_REQUIRE(sdev == dev, "%s: the stream belongs to device %d, the current device is %d",
+                name, static_cast<int>(sdev), dev);
+  }
+  std::lock_guard<std::mutex> hold(g_scratch_lock);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void *ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || ptr == nullptr) {
+      set_error("%s: hipGetSymbolAddress(scratch) failed on device %d: %s", name, dev,
+                hipGetErrorString(err));
+      return R2S_EHIP;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return R2S_OK;
+}
+
+// raster_fwd_impl with the split partial tiles in `scratch` instead of a
+// caller's workspace.  Every partial tile is written in full before
+// fwd_combine_kernel reads it, so nothing needs clearing between calls.
+template <typename T>
+int raster_fwd_noalloc_impl(const T *means2d, const T *conics, const T *opac, const T *mus,
+                            const int32_t *tile_offsets, const int32_t *flatten_ids,
+                            int64_t n_isects, int64_t C, int64_t N, uint32_t W, uint32_t H,
+                            uint32_t ts, uint32_t tw, uint32_t th, T *image, r2s_stream_t st) {
+  clear_error();
+  const char *name = "rasterize_to_pixels_fwd_noalloc";
+  R2S_RETURN_IF(check_raster_args(n_isects, C, N, W, H, ts, tw, th, name));
+  void *ws = nullptr;
+  size_t need = 0;
+  if (C * static_cast<int64_t>(W) * H > 0 && N > 0 && n_isects > 0 &&
+      (ts == 8 || ts == 16 || ts == 32)) {
+    const int64_t n_keys = C * static_cast<int64_t>(tw) * th;
+    const uint32_t splits = fwd_splits(n_keys, n_isects);
+    if (splits > 1) {
+      need = static_cast<size_t>(n_keys) * splits * ts * ts * sizeof(T);
+      if (need > static_cast<size_t>(R2S_RASTER_SCRATCH_BYTES)) {
+        set_error("%s: %lld tiles split %u ways need %zu bytes of partial tiles; the static "
+                  "scratch holds %zu (use r2s_rasterize_fwd_* with a workspace)",
+                  name, (long long)n_keys, splits, need,
+                  static_cast<size_t>(R2S_RASTER_SCRATCH_BYTES));
+        return R2S_ERANGE;
+      }
+      R2S_RETURN_IF(scratch_address(&ws, as_stream(st), name));
+    }
+  }
+  return raster_fwd_impl<T>(means2d, conics, opac, mus, tile_offsets, flatten_ids, n_isects, C,
+                            N, W, H, ts, tw, th, image, ws, need, st);
+}
+
 }  // namespace
 }  // namespace r2s
 
 extern "C" {
+
+#define R2S_RASTER_NOALLOC_API(SUF, T)                                                        \
+  int r2s_rasterize_fwd_noalloc_##SUF(const T *means2d, const T *conics, const T *opac,        \
+                                      const T *mus, const int32_t *tile_offsets,               \
+                                      const int32_t *flatten_ids, int64_t n_isects, int64_t C, \
+                                      int64_t N, uint32_t W, uint32_t H, uint32_t ts,          \
+                                      uint32_t tw, uint32_t th, T *image, r2s_stream_t st) {   \
+    return r2s::raster_fwd_noalloc_impl<T>(means2d, conics, opac, mus, tile_offsets,          \
+                                           flatten_ids, n_isects, C, N, W, H, ts, tw, th,     \
+                                           image, st);                                        \
+  }
+
+R2S_RASTER_NOALLOC_API(f32, float)
+R2S_RASTER_NOALLOC_API(f64, double)
+
+#undef R2S_RASTER_NOALLOC_API
 
 int64_t r2s_rasterize_bwd_workspace_bytes(int64_t n_isects, int dtype_bytes) {
   if (n_isects <= 0 || (dtype_bytes != 4 && dtype_bytes != 8)) return 0;

@@ -41,6 +41,8 @@ _FLOAT_OPS = {
                            _p, _p, _sz, _p],
     "rasterize_fwd": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _u32, _u32, _u32, _u32, _u32,
                       _p, _p, _sz, _p],
+    "rasterize_fwd_noalloc": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _u32, _u32, _u32, _u32,
+                              _u32, _p, _p],
     "rasterize_bwd": [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _u32, _u32, _u32, _u32,
                       _u32, _p, _p, _p, _p, _p, _p],
     "rasterize_bwd_emit": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _u32, _u32,

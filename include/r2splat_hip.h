@@ -5,7 +5,8 @@
  * and scalars, and a hipStream_t passed as `void*`.  Work is enqueued on that
  * stream; nothing here allocates or frees device memory: scratch space is a
  * caller-provided workspace whose size is returned by the *_workspace_bytes
- * queries.  Every function returns R2S_OK (0) on success, otherwise a status
+ * queries (r2s_rasterize_fwd_noalloc_* instead uses a fixed device array that
+ * the library holds on each GPU until the process ends).  Every function returns R2S_OK (0) on success, otherwise a status
  * code; r2s_last_error() then holds a message for the calling thread.
  *
  * Layouts follow the reference operators (row-major, contiguous):
@@ -350,6 +351,34 @@ int r2s_rasterize_fwd_f64(const double *means2d, const double *conics,
                           uint32_t tile_size, uint32_t n_tiles_w,
                           uint32_t n_tiles_h, double *image, void *workspace,
                           size_t workspace_bytes, r2s_stream_t stream);
+
+/* No counterpart in the reference: r2s_rasterize_fwd_* for callers that
+ * cannot allocate or pass a workspace (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  The split partial tiles
+ * live in a static device array of R2S_RASTER_SCRATCH_BYTES per GPU, held
+ * until the process ends; a call whose partial tiles
+ * (r2s_rasterize_workspace_bytes) exceed it fails with R2S_ERANGE.  The
+ * array's address is looked up on the first call on each device, which must
+ * be the current device and the stream's.  All calls on one GPU share the
+ * array: calls that overlap on one GPU (concurrent streams) race; calls on
+ * one stream do not.  The image equals r2s_rasterize_fwd_*'s bit for bit. */
+#define R2S_RASTER_SCRATCH_BYTES (32u << 20)
+int r2s_rasterize_fwd_noalloc_f32(const float *means2d, const float *conics,
+                                  const float *opacities, const float *mus,
+                                  const int32_t *tile_offsets,
+                                  const int32_t *flatten_ids, int64_t n_isects,
+                                  int64_t C, int64_t N, uint32_t width,
+                                  uint32_t height, uint32_t tile_size,
+                                  uint32_t n_tiles_w, uint32_t n_tiles_h,
+                                  float *image, r2s_stream_t stream);
+int r2s_rasterize_fwd_noalloc_f64(const double *means2d, const double *conics,
+                                  const double *opacities, const double *mus,
+                                  const int32_t *tile_offsets,
+                                  const int32_t *flatten_ids, int64_t n_isects,
+                                  int64_t C, int64_t N, uint32_t width,
+                                  uint32_t height, uint32_t tile_size,
+                                  uint32_t n_tiles_w, uint32_t n_tiles_h,
+                                  double *image, r2s_stream_t stream);
 
 /* RasterizeToPixels.cpp:226-317 rasterize_to_pixels_bwd_per_gaussian_tensor
  * (isect_ids != NULL) and RasterizeToPixels.cpp:122-222

@@ -96,6 +96,24 @@ def test_workspace_queries(lib):
     assert rc in (1001, 1004)
 
 
+def test_noalloc_forward_rejects_partial_tiles_beyond_its_array(lib):
+    # 64x64 tiles of 16 with 8192 records each split 8 ways: 4096 * 8 * 256
+    # pixels, 32 MiB in float32 (fits) and 64 MiB in float64 (does not).  The
+    # size check comes before any pointer is read or any HIP call is made.
+    n_keys, n = 64 * 64, 64 * 64 * 8192
+    assert lib.r2s_rasterize_workspace_bytes(n_keys, n, 16, 4) == 32 << 20
+    rc = lib.r2s_rasterize_fwd_noalloc_f64(None, None, None, None, None, None, n, 1, 1, 1024, 1024,
+                                           16, 64, 64, None, None)
+    assert rc == 1002 and b"static scratch holds 33554432" in lib.r2s_last_error()
+    rc = lib.r2s_rasterize_fwd_noalloc_f32(None, None, None, None, None, None, 2 * n, 2, 1, 1024,
+                                           1024, 16, 64, 64, None, None)
+    assert rc == 1002
+    # Argument checks still come first.
+    rc = lib.r2s_rasterize_fwd_noalloc_f32(None, None, None, None, None, None, n, 1, 1, 1024, 1024,
+                                           0, 64, 64, None, None)
+    assert rc == 1001
+
+
 def test_densify_arguments_are_checked_without_a_device(lib):
     C = _lib.Column
     cols = (C * 1)()
