@@ -20,6 +20,9 @@ Modules
              rasterizer and voxelizer (forward and both backward modes).
 ``compose``  the ``r2splat.ops`` forward/backward composition on top of the
              above (explicit.py / direct.py restated).
+``dense``    the reference's dense PyTorch formulation (every Gaussian at
+             every pixel / voxel, torch autograd backward): the CPU
+             baseline's workload, checked against the modules above.
 
 Seeded synthetic inputs come from ``r2splat.scenes`` / ``r2splat.geometry``
 (host-side generators, no device code).  How each function is pinned (the
