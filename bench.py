@@ -2,15 +2,19 @@
 
 Headline (``value``): projection forward + backward calls per second at the
 BASELINE config-4 shape -- 500,000 Gaussians grown as a binary tree from one
-root, 512x512 cone-beam detector, one view per call (angles k * 1 degree),
+root, 512x512 cone-beam detector, one view per call (call i projects view
+(18 i) mod 360 degrees, so 20 consecutive calls cover the orbit once),
 upstream image gradient N(0,1).  One call = prepare_explicit_gaussians ->
 explicit_rasterize -> explicit_backward, the reference's training path.
 
 Also reported: the voxelizer at config 3 (200k Gaussians, 256^3, fwd + bwd,
 Mvox/s and % of HBM peak), the training-step shape of config 4 (projection +
 128^3 voxelization fwd/bwd + compaction every 100 steps), the fused
-densify / prune rewrite of the config-4 model table, per-kernel event
-timings, the roofline of the dominant kernel and the CPU oracle baseline.
+densify / prune rewrite of the config-4 model table, the config-5 stress
+shapes (the 512^3 volume with 5 % needles in z-slabs), per-kernel event
+timings over the orbit views, the rooflines of the dominant raster and voxel
+kernels, the CPU baseline (the reference's dense torch formulation of
+config 1 on the host's threads) and the CPU oracle on the headline workload.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
                        [--no-voxel] [--no-train] [--no-densify] [--no-losses]
@@ -37,7 +41,8 @@ import torch  # noqa: E402
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, AMD public spec
 # MI355X fp32 vector peak, 157.3 TFLOP/s (AMD public spec), expressed as
 # wave64 FMA instructions: 157.3e12 / (2 flop x 64 lanes) = 1228.9 G/s.
-VALU_PEAK_G_WAVE_INSTR = 157.3e3 / 128
+VALU_PEAK_TFLOPS = 157.3
+VALU_PEAK_G_WAVE_INSTR = VALU_PEAK_TFLOPS * 1e3 / 128
 SMIN, SMAX = 5e-4, 1.0
 EPS = 1e-8
 DET = 512
@@ -47,6 +52,16 @@ N_VOX, VOX_DIM = 200_000, 256
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
+
+
+# The headline's call i projects view (18 i) mod 360 degrees: any 20
+# consecutive calls cover the orbit once, 18 degrees apart.
+ORBIT_STRIDE = 18
+ORBIT_VIEWS = 360 // ORBIT_STRIDE
+
+
+def orbit_view(i):
+    return (i * ORBIT_STRIDE) % 360
 
 
 def _events():
@@ -81,14 +96,15 @@ class Projection:
         means, quats, scales, opac = self.params
         for p in self.params:
             p.grad = None
-        k = self.step_i % 360
+        i = self.step_i
+        k = orbit_view(i)
         self.step_i += 1
         state = explicit.prepare_explicit_gaussians(quats, scales, opac, scale_min=SMIN,
                                                     scale_max=SMAX)
         res = explicit.explicit_rasterize(state, means, self.viewmats[k:k + 1],
                                           self.Ks[k:k + 1], img_w=self.det, img_h=self.det,
                                           tile_size=16, eps2d=EPS, radius_clip=3.0, absgrad=True)
-        res.image.grad = self.v_images[k % 4]
+        res.image.grad = self.v_images[i % 4]
         explicit.explicit_backward(state, means, quats, scales, opac)
         return state
 
@@ -248,6 +264,42 @@ class Voxelization:
                                       EPS, vm3, vc3)
         self.last = (m3, con, off, ids, fl, vol)
         return vol
+
+
+class SlabVoxelization:
+    """Config-5 volume at the stated 5 % needles: 2M Gaussians whose brick
+    list (7.46e9 records at 512^3) exceeds one list's int32 offsets, so
+    r2splat.ops voxelizes it in z-slabs (forward) and re-bins each slab for
+    the backward.  One step = VolumePass.run + vjp."""
+
+    def __init__(self, dev, seed=5):
+        from r2splat import scenes
+        from r2splat.cuda import _ops
+        from r2splat.cuda import _wrapper as W
+
+        g = torch.Generator().manual_seed(seed)
+        raw = scenes.stress_gaussians(2_000_000, g, needle_fraction=0.05)
+        self.means = raw.means.to(dev)
+        self.covars, self.max_scales, self.opac = W.prepare_gaussians(
+            raw.quats.to(dev), raw.raw_scales.to(dev), raw.raw_opacities.to(dev), SMIN, SMAX)
+        self.ranges = torch.full((3,), 2.0, device=dev)
+        self.centers = torch.zeros(3, device=dev)
+        self.v_volume = torch.randn(512, 512, 512, generator=g).to(dev)
+        self.limit = _ops.SLAB_RECORDS
+        self.slabs, self.records = (), 0
+
+    def step(self):
+        from r2splat.cuda import _ops
+        from r2splat.ops import _passes
+
+        p = _passes.VolumePass.run(self.means, self.covars, self.max_scales, self.opac,
+                                   self.ranges, self.centers, dim2=512, dim1=512, dim0=512,
+                                   tile_size=8, eps3d=EPS, radius_clip=3.0)
+        p.vjp(self.v_volume, self.means, self.covars)
+        if not self.records:
+            self.slabs = p.slabs
+            self.records = sum(_ops.layer_counts_3d(p.means3d, p.radii, 8, 64, 64, 64))
+        return p
 
 
 class DensifyTable:
@@ -440,60 +492,149 @@ def time_kernel(fn, reps):
 
 
 def kernel_breakdown(proj: Projection, reps):
-    """Event timings of each projection stage at the config-4 inputs of view 0.
+    """Event timings of each projection stage at the config-4 inputs of the
+    headline's 20 orbit views (each stage timed ``reps`` times per view, on
+    the stream its kernels run on), averaged over the views.
 
     Entries other than ``binning_2d`` (count, scan, one host read, emit,
-    sort passes, offsets) are single kernel launches: the two backward passes
-    are timed apart through their C entry points."""
+    sort passes, offsets) and ``rasterize_bwd_op`` (both passes) are single
+    kernel launches: the two backward passes are timed apart through their
+    C entry points.  Returns per-stage mean seconds, the per-view times of
+    the raster kernels, and the record count of each view."""
     from r2splat.cuda import _backend, _ops
     from r2splat.cuda import _wrapper as W
 
     lib = _backend.library()
-    means, quats, scales, opac = proj.params
-    vm, Ks, det = proj.viewmats[:1], proj.Ks[:1], proj.det
-    cov, ms, op = W.prepare_gaussians(quats.detach(), scales.detach(), opac.detach(), SMIN, SMAX)
-    m2, c2, r, con, mu, opc = W.project_gaussians_fwd(means.detach(), cov, op, vm, Ks, det, det,
-                                                      EPS, 3.0)
+    means, quats, scales, opac = (t.detach() for t in proj.params)
+    det = proj.det
     nt = -(-det // 16)
-    _, ids, fl = W.isect_tiles(m2, r, 16, nt, nt)
-    off = W.isect_offset_encode(ids, 1, nt, nt)
-    emit_ids, isect_src = _ops.emission_order(fl, nt * nt)
-    v_img = proj.v_images[0]
-    n = int(fl.numel())
-    rows = torch.empty(lib.r2s_rasterize_bwd_workspace_bytes(n, 4), dtype=torch.uint8,
-                       device=m2.device)
-    outs = [torch.zeros_like(m2), torch.zeros_like(m2), torch.zeros_like(con),
-            torch.zeros_like(opc), torch.zeros_like(mu)]
     P = _ops._ptr
+    cov, ms, op = W.prepare_gaussians(quats, scales, opac, SMIN, SMAX)
+    per_view = {}
+    counts = []
+    for v in range(ORBIT_VIEWS):
+        k = orbit_view(v)
+        vm, Ks = proj.viewmats[k:k + 1], proj.Ks[k:k + 1]
+        m2, c2, r, con, mu, opc = W.project_gaussians_fwd(means, cov, op, vm, Ks, det, det, EPS,
+                                                          3.0)
+        _, ids, fl = W.isect_tiles(m2, r, 16, nt, nt)
+        off = W.isect_offset_encode(ids, 1, nt, nt)
+        emit_ids, isect_src = _ops.emission_order(fl, nt * nt)
+        v_img = proj.v_images[v % 4]
+        n = int(fl.numel())
+        counts.append(n)
+        rows = torch.empty(lib.r2s_rasterize_bwd_workspace_bytes(n, 4), dtype=torch.uint8,
+                           device=m2.device)
+        outs = [torch.zeros_like(m2), torch.zeros_like(m2), torch.zeros_like(con),
+                torch.zeros_like(opc), torch.zeros_like(mu)]
+
+        def bwd_rows():
+            stream = torch.cuda.current_stream().cuda_stream
+            rc = lib.r2s_rasterize_bwd_rows_f32(P(m2), P(con), P(opc), P(mu), P(off), P(ids),
+                                                P(fl), P(isect_src), n, P(v_img), 1, N_PROJ, det,
+                                                det, 16, nt, nt, 1, P(rows), rows.numel(), stream)
+            assert rc == 0, lib.r2s_last_error()
+
+        def bwd_reduce():
+            stream = torch.cuda.current_stream().cuda_stream
+            rc = lib.r2s_rasterize_bwd_reduce_f32(P(rows), P(emit_ids), n, 1, N_PROJ, P(outs[0]),
+                                                  P(outs[1]), P(outs[2]), P(outs[3]), P(outs[4]),
+                                                  stream)
+            assert rc == 0, lib.r2s_last_error()
+
+        stages = {
+            "prepare": lambda: W.prepare_gaussians(quats, scales, opac, SMIN, SMAX),
+            "project_fwd": lambda: W.project_gaussians_fwd(means, cov, op, vm, Ks, det, det,
+                                                           EPS, 3.0),
+            "binning_2d": lambda: W.isect_tiles(m2, r, 16, nt, nt),
+            "rasterize_fwd": lambda: W.rasterize_to_pixels_fwd(m2, con, opc, mu, off, fl, det,
+                                                               det, 16),
+            "rasterize_bwd_rows": bwd_rows,
+            "rasterize_bwd_reduce": bwd_reduce,
+            "rasterize_bwd_op": lambda: W.rasterize_to_pixels_bwd_per_gaussian(
+                m2, con, opc, mu, off, ids, fl, v_img, det, det, 16, True),
+        }
+        for name, fn in stages.items():
+            per_view.setdefault(name, []).append(time_kernel(fn, reps))
+        del rows, outs
+    mean = {k: sum(v) / len(v) for k, v in per_view.items()}
+    return {"n_isects_2d": counts[0], "n_isects_per_view": counts, "seconds": mean,
+            "per_view_seconds": {k: per_view[k] for k in ("rasterize_fwd", "rasterize_bwd_rows")}}
+
+
+def voxel_breakdown(vox, reps):
+    """Event timings of the voxelizer's kernels at the config-3 inputs,
+    through their C entry points on the current stream: the forward
+    (voxel_fwd_kernel), the backward's rows pass (voxel_bwd_chunk_kernel)
+    and its per-Gaussian reduce (row_reduce_kernel<10>)."""
+    from r2splat.cuda import _backend, _ops
+
+    lib = _backend.library()
+    P = _ops._ptr
+    m3, con, off, ids, fl, _ = vox.last
+    d = vox.dim
+    nb = -(-d // 8)
+    n, N = int(fl.numel()), int(m3.shape[0])
+    emit_ids, isect_src = _ops.emission_order(fl, nb ** 3)
+    volume = torch.empty((d, d, d), device=m3.device)
+    rows = torch.empty(lib.r2s_voxelize_bwd_workspace_bytes(n, 4), dtype=torch.uint8,
+                       device=m3.device)
+    outs = [torch.zeros_like(m3), torch.zeros_like(con), torch.zeros_like(vox.opac)]
+
+    def stream():
+        return torch.cuda.current_stream().cuda_stream
+
+    def fwd():
+        rc = lib.r2s_voxelize_fwd_f32(P(m3), P(con), P(vox.opac), P(off), P(fl), n, N, d, d, d,
+                                      8, nb, nb, nb, P(volume), stream())
+        assert rc == 0, lib.r2s_last_error()
 
     def bwd_rows():
-        stream = torch.cuda.current_stream().cuda_stream
-        rc = lib.r2s_rasterize_bwd_rows_f32(P(m2), P(con), P(opc), P(mu), P(off), P(ids), P(fl),
-                                            P(isect_src), n, P(v_img), 1, N_PROJ, det, det, 16,
-                                            nt, nt, 1, P(rows), rows.numel(), stream)
+        rc = lib.r2s_voxelize_bwd_rows_f32(P(m3), P(con), P(vox.opac), P(off), P(ids), P(fl),
+                                           P(isect_src), n, P(vox.v_volume), N, d, d, d, 8, nb,
+                                           nb, nb, P(rows), rows.numel(), stream())
         assert rc == 0, lib.r2s_last_error()
 
     def bwd_reduce():
-        stream = torch.cuda.current_stream().cuda_stream
-        rc = lib.r2s_rasterize_bwd_reduce_f32(P(rows), P(emit_ids), n, 1, N_PROJ, P(outs[0]),
-                                              P(outs[1]), P(outs[2]), P(outs[3]), P(outs[4]),
-                                              stream)
+        rc = lib.r2s_voxelize_bwd_reduce_f32(P(rows), P(emit_ids), n, N, P(outs[0]), P(outs[1]),
+                                             P(outs[2]), stream())
         assert rc == 0, lib.r2s_last_error()
 
-    out = {"n_isects_2d": n}
-    t = {}
-    t["prepare"] = time_kernel(lambda: W.prepare_gaussians(quats.detach(), scales.detach(),
-                                                           opac.detach(), SMIN, SMAX), reps)
-    t["project_fwd"] = time_kernel(lambda: W.project_gaussians_fwd(
-        means.detach(), cov, op, vm, Ks, det, det, EPS, 3.0), reps)
-    t["binning_2d"] = time_kernel(lambda: W.isect_tiles(m2, r, 16, nt, nt), reps)
-    t["rasterize_fwd"] = time_kernel(lambda: W.rasterize_to_pixels_fwd(
-        m2, con, opc, mu, off, fl, det, det, 16), reps)
-    t["rasterize_bwd_rows"] = time_kernel(bwd_rows, reps)
-    t["rasterize_bwd_reduce"] = time_kernel(bwd_reduce, reps)
-    t["rasterize_bwd_op"] = time_kernel(lambda: W.rasterize_to_pixels_bwd_per_gaussian(
-        m2, con, opc, mu, off, ids, fl, v_img, det, det, 16, True), reps)
-    out["seconds"] = t
+    t = {"voxelize_fwd": time_kernel(fwd, reps), "voxelize_bwd_rows": time_kernel(bwd_rows, reps),
+         "voxelize_bwd_reduce": time_kernel(bwd_reduce, reps)}
+    return {"n_isects_3d": n, "seconds": t}
+
+
+def kernel_roofline(kernel, seconds, algorithmic_bytes, evaluations=None):
+    """Roofline object of one kernel: average launch ``seconds`` (live), its
+    algorithmic bytes, and the counters of its committed rocprofv3 --pmc
+    summaries (HBM bytes, VALU / transcendental instructions per launch).
+    The raster and voxel kernels are bound by vector-ALU issue: when the VALU
+    counts are committed, ``bound`` is "valu" and ``achieved`` / ``peak``
+    are the issue rate in fp32 FMA-equivalent TFLOP/s (wave64 instructions
+    x 64 lanes x 2) against MI355X's 157.3; the HBM figures follow under
+    ``hbm``."""
+    gbs = algorithmic_bytes / seconds / 1e9
+    traffic = measured_traffic(kernel)
+    valu, trans = measured_valu(kernel)
+    hbm = {"achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
+           "source": f"profiles/pmc_{kernel}.txt"}
+    out = {"kernel": kernel, "algorithmic_bytes": int(algorithmic_bytes),
+           "avg_launch_ms": seconds * 1e3, "traffic": traffic}
+    if valu is None:
+        out.update({"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": gbs / HBM_PEAK_GBS})
+        return out
+    rate = valu / seconds / 1e9
+    tflops = rate * 128 / 1e3
+    out.update({"bound": "valu", "achieved": tflops, "peak": VALU_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": tflops / VALU_PEAK_TFLOPS, "hbm": hbm})
+    out["valu"] = {"reference_evaluations": evaluations,
+                   "executed_evaluations": None if trans is None else trans * 64,
+                   "wave_instructions_per_launch": valu,
+                   "achieved_g_wave_instructions_per_s": rate,
+                   "peak_g_wave_instructions_per_s": VALU_PEAK_G_WAVE_INSTR,
+                   "source": f"profiles/pmc_valu_{kernel}.txt"}
     return out
 
 
@@ -626,93 +767,12 @@ def vox_bytes(n, i3, v):
     return 144 * n + 156 * i3 + 8 * v
 
 
-def _tile_bound(v, upper):
-    # IsectTilesKernel.cu:30-40: non-finite or <= 0 -> 0, >= upper -> upper, else truncate.
-    v = torch.where(torch.isfinite(v) & (v > 0), v, torch.zeros_like(v))
-    return torch.clamp(v, max=float(upper)).floor()
-
-
-def dense_cover_2d(means2d, radii, ts, h, w):
-    """[N, H, W] mask of the pixels in the tiles the binning lists for each
-    Gaussian (IsectTilesKernel.cu:57-113), for the dense formulation."""
-    tw, th = -(-w // ts), -(-h // ts)
-    rx, ry = radii[:, 0].float(), radii[:, 1].float()
-    mx, my = means2d[:, 0], means2d[:, 1]
-    ok = (rx > 0) & (ry > 0) & torch.isfinite(mx) & torch.isfinite(my)
-    x0 = _tile_bound(torch.floor(mx / ts - rx / ts), tw)
-    x1 = _tile_bound(torch.ceil(mx / ts + rx / ts), tw)
-    y0 = _tile_bound(torch.floor(my / ts - ry / ts), th)
-    y1 = _tile_bound(torch.ceil(my / ts + ry / ts), th)
-    tj = (torch.arange(w) // ts).float()
-    ti = (torch.arange(h) // ts).float()
-    cx = (tj[None] >= x0[:, None]) & (tj[None] < x1[:, None])
-    cy = (ti[None] >= y0[:, None]) & (ti[None] < y1[:, None])
-    return ok[:, None, None] & cy[:, :, None] & cx[:, None, :]
-
-
-def dense_cover_3d(means3d, radii, ts, d):
-    """[N, D, D, D] mask of the voxels in the bricks the 3D binning lists
-    (IsectTiles3DKernel.cu:49-104)."""
-    n = -(-d // ts)
-    ok = (radii > 0).all(-1)
-    lo, hi = [], []
-    for a in range(3):
-        c, r = means3d[:, a] / ts, radii[:, a].float() / ts
-        lo.append(_tile_bound(torch.floor(c - r), n))
-        hi.append(_tile_bound(torch.ceil(c + r), n))
-    t = (torch.arange(d) // ts).float()
-    cx = (t[None] >= lo[0][:, None]) & (t[None] < hi[0][:, None])
-    cy = (t[None] >= lo[1][:, None]) & (t[None] < hi[1][:, None])
-    cz = (t[None] >= lo[2][:, None]) & (t[None] < hi[2][:, None])
-    return ok[:, None, None, None] & cz[:, :, None, None] & cy[:, None, :, None] & \
-        cx[:, None, None, :]
-
-
-def dense_raster(means2d, conics, om, cover):
-    """The reference's dense line-integral image (tests/test_cuda_gaussian_ops.py:200-215
-    semantics), masked by the tile cover: [N] Gaussians -> [H, W]."""
-    h, w = cover.shape[1:]
-    py, px = torch.meshgrid(torch.arange(h, dtype=means2d.dtype) + 0.5,
-                            torch.arange(w, dtype=means2d.dtype) + 0.5, indexing="ij")
-    dx = px[None] - means2d[:, 0, None, None]
-    dy = py[None] - means2d[:, 1, None, None]
-    sigma = (0.5 * conics[:, 0, None, None] * dx.square() + conics[:, 1, None, None] * dx * dy
-             + 0.5 * conics[:, 2, None, None] * dy.square())
-    alpha = om[:, None, None] * torch.exp(-sigma)
-    keep = cover & (sigma >= 0) & (alpha.abs() >= 1e-5)
-    return torch.where(keep, alpha, torch.zeros_like(alpha)).sum(0)
-
-
-def dense_voxel(means3d, conics, opac, cover):
-    """The reference's dense volume (tests/test_cuda_gaussian_ops.py:218-238 semantics),
-    masked by the brick cover: [N] Gaussians -> [D, D, D]."""
-    d = cover.shape[1]
-    pz, py, px = torch.meshgrid(*(torch.arange(d, dtype=means3d.dtype) + 0.5,) * 3,
-                                indexing="ij")
-    dx = px[None] - means3d[:, 0, None, None, None]
-    dy = py[None] - means3d[:, 1, None, None, None]
-    dz = pz[None] - means3d[:, 2, None, None, None]
-    q = [conics[:, i, None, None, None] for i in range(6)]
-    sigma = (0.5 * q[0] * dx.square() + q[1] * dx * dy + q[2] * dx * dz
-             + 0.5 * q[3] * dy.square() + q[4] * dy * dz + 0.5 * q[5] * dz.square())
-    alpha = opac[:, None, None, None] * torch.exp(-sigma)
-    keep = cover & (sigma >= 0) & (alpha.abs() >= 1e-6)
-    return torch.where(keep, alpha, torch.zeros_like(alpha)).sum(0)
-
-
-def config1(dev, steps, warmup, chunk=256):
-    """Config 1 like for like: 4,096 Gaussians (means U[-1,1]^3, log-scales
-    N(-4, 0.5), densities U[0,1]), one cone-beam view at an angle drawn from
-    the same generator, a 64^2 detector and a 64^3 voxelization over
-    [-1,1]^3, fwd+bwd against N(0,1) upstream gradients.  The GPU runs the
-    whole path (prepare, projection, binning, rasterize, voxelize, explicit
-    backward).  The CPU runs the reference's dense PyTorch formulation of the
-    rasterize and voxelize sums (masked by the tile / brick cover, as the
-    kernels evaluate) with torch autograd for their backward, on the host's
-    torch threads; the O(N) preprocessing is taken from the GPU run, so the
-    CPU figure covers the O(N P) part only.  Both results are compared."""
+def _config1_inputs():
+    """BASELINE config 1 (seed 0): 4,096 Gaussians (means U[-1,1]^3,
+    log-scales N(-4, 0.5), unit quaternions, densities U[0,1]), one
+    cone-beam view at an angle U[0, 2 pi) from the same generator, a 64^2
+    detector, a 64^3 volume over [-1,1]^3, N(0,1) upstream gradients."""
     from r2splat import geometry, scenes
-    from r2splat.ops import explicit
 
     g = torch.Generator().manual_seed(0)
     raw = scenes.random_gaussians(4096, g, -4.0, 0.5)
@@ -720,13 +780,22 @@ def config1(dev, steps, warmup, chunk=256):
     vm, Ks = geometry.cone_beam_views([angle], 64)
     v_image = torch.randn(1, 64, 64, generator=g)
     v_volume = torch.randn(64, 64, 64, generator=g)
+    return raw, vm, Ks, v_image, v_volume
+
+
+def config1_gpu(dev, steps, warmup):
+    """The whole config-1 call on the GPU (prepare, projection, binning,
+    rasterize, voxelize, explicit backward): (seconds per call, image, volume)."""
+    from r2splat.ops import explicit
+
+    raw, vm, Ks, v_image, v_volume = _config1_inputs()
     params = [t.clone().to(dev).requires_grad_(True) for t in
               (raw.means, raw.quats, raw.raw_scales, raw.raw_opacities)]
     vm, Ks, vi, vv = vm.to(dev), Ks.to(dev), v_image.to(dev), v_volume.to(dev)
     ranges = torch.full((3,), 2.0, device=dev)
     centers = torch.zeros(3, device=dev)
 
-    def gpu_call():
+    def call():
         means, quats, scales, opac = params
         for p in params:
             p.grad = None
@@ -739,75 +808,80 @@ def config1(dev, steps, warmup, chunk=256):
         res.image.grad = vi
         vox.volume.grad = vv
         explicit.explicit_backward(st, means, quats, scales, opac)
-        return st, res, vox
+        return res, vox
 
-    t_gpu = time_steps(gpu_call, steps, warmup)
-    st, res, vox = gpu_call()
+    t = time_steps(call, steps, warmup)
+    res, vox = call()
     torch.cuda.synchronize()
-    pr, vx = st.projection, st.voxel
-    m2 = pr.means2d[0].detach().cpu()
-    con = pr.conics[0].detach().cpu()
-    om = (pr.weights * pr.mus)[0].detach().cpu()
-    r2 = pr.radii[0].cpu()
-    m3, con3 = vx.means3d.detach().cpu(), vx.conics.detach().cpu()
-    op3, r3 = vx.weights.detach().cpu(), vox.radii.cpu()
+    grads = [p.grad.detach().cpu() for p in params]
+    return t, res.image.detach()[0].cpu(), vox.volume.detach().cpu(), grads
 
-    def cpu_raster():
-        a, b, c = (t.clone().requires_grad_(True) for t in (m2, con, om))
-        image = dense_raster(a, b, c, dense_cover_2d(a.detach(), r2, 16, 64, 64))
-        (image * v_image[0]).sum().backward()
-        return image.detach()
 
-    def cpu_voxel():
-        vol = torch.zeros(64, 64, 64)
-        for s0 in range(0, m3.shape[0], chunk):
-            x, y, z = (t[s0:s0 + chunk].clone().requires_grad_(True) for t in (m3, con3, op3))
-            part = dense_voxel(x, y, z, dense_cover_3d(x.detach(), r3[s0:s0 + chunk], 8, 64))
-            (part * v_volume).sum().backward()
-            vol += part.detach()
-        return vol
+def cpu_threads():
+    """Host threads for the CPU baseline: the process's CPU share (the
+    OMP_NUM_THREADS the box sets, else the CPUs this process may run on)."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        return int(env)
+    return len(os.sched_getaffinity(0))
 
-    cpu_raster()
+
+def config1_cpu(runs=5):
+    """The reference's dense PyTorch formulation of config 1 on the host
+    (oracle/dense.py: preprocessing from the raw parameters, the dense
+    alpha sums masked by the tile / brick cover, torch autograd for the
+    backward, the voxel sums in chunks of 256 Gaussians), on all of the
+    process's host threads: the median of ``runs`` calls after one warm-up.
+    Returns (median seconds, every time, image, volume, grads)."""
+    from oracle import dense
+
+    raw, vm, Ks, v_image, v_volume = _config1_inputs()
+    torch.set_num_threads(cpu_threads())
     times = []
-    for _ in range(3):
+    for i in range(runs + 1):
+        params = [t.clone().requires_grad_(True) for t in
+                  (raw.means, raw.quats, raw.raw_scales, raw.raw_opacities)]
         t0 = time.perf_counter()
-        image_cpu = cpu_raster()
-        times.append(time.perf_counter() - t0)
-    t_raster = sorted(times)[1]
-    t0 = time.perf_counter()
-    vol_cpu = cpu_voxel()  # one pass: about half a minute of CPU work
-    t_voxel = time.perf_counter() - t0
-    t_cpu = t_raster + t_voxel
-    d_img = float((image_cpu - res.image.detach()[0].cpu()).abs().max())
-    d_vol = float((vol_cpu - vox.volume.detach().cpu()).abs().max())
+        image, volume = dense.config1_call(params, vm[0], Ks[0], 64, 64, v_image[0],
+                                           (64, 64, 64), v_volume, scale_min=SMIN,
+                                           scale_max=SMAX, eps=EPS)
+        dt = time.perf_counter() - t0
+        if i > 0:
+            times.append(dt)
+        log(f"config1 dense torch call {i}{' (warm-up)' if i == 0 else ''}: {dt:.2f} s")
+    grads = [p.grad.detach() for p in params]
+    return sorted(times)[len(times) // 2], times, image, volume, grads
+
+
+def config1(dev, steps, warmup, runs=5):
+    """Config 1 like for like: the GPU path and the dense CPU formulation,
+    their times and how far their images, volumes and gradients differ."""
+    t_gpu, img_g, vol_g, grads_g = config1_gpu(dev, steps, warmup)
+    t_cpu, times, img_c, vol_c, grads_c = config1_cpu(runs)
+    rel = lambda a, b: float((a - b).abs().max() / b.abs().max().clamp_min(1e-30))  # noqa: E731
     return {"workload": "config1: 4096 Gaussians, one view on 64^2 + 64^3 voxelization, "
-                        "fwd+bwd",
+                        "fwd+bwd from the raw parameters",
             "gpu_ms_per_call": t_gpu * 1e3,
             "cpu_dense_torch_ms_per_call": t_cpu * 1e3,
+            "cpu_dense_torch_ms_runs": [round(x * 1e3, 1) for x in times],
             "cpu_threads": torch.get_num_threads(),
-            "cpu_raster_ms": t_raster * 1e3, "cpu_voxel_ms": t_voxel * 1e3,
-            "cpu_sample": "the rasterize sums with autograd backward (median of 3 after a "
-                          "warm-up) plus one pass of the voxelize sums (all 4096 Gaussians, "
-                          "in chunks of 256); preprocessing from the GPU run",
             "gpu_speedup": t_cpu / t_gpu,
-            "image_max_abs_diff": d_img, "volume_max_abs_diff": d_vol}
+            "image_max_abs_diff": float((img_c - img_g).abs().max()),
+            "volume_max_abs_diff": float((vol_c - vol_g).abs().max()),
+            "grad_max_rel_diff": {n: rel(a, b) for n, a, b in
+                                  zip(("means", "quats", "raw_scales", "raw_opacities"),
+                                      grads_g, grads_c)}}
 
 
-def cpu_baseline(proj: Projection, stride=1):
-    """Oracle (numpy + sequential C, one core) projection fwd+bwd on a seeded
-    random 1/``stride`` subset of the config-4 Gaussians (by default all of
-    them: about 15 s of CPU work), 512^2, view 0; the time is scaled by
-    ``stride`` to the full set (work is linear in the number of tile
-    records).  Returns (calls/s, seconds, sample text)."""
+def oracle_projection_baseline(proj: Projection):
+    """The CPU oracle (numpy, plus the C restatement over OpenMP threads) on
+    the headline's own workload: config-4 projection fwd+bwd of all 500k
+    Gaussians, 512^2, view 0.  Returns (calls/s, seconds, sample text)."""
     from oracle import compose
 
     raw = proj.raw
-    sel = torch.from_numpy(np.sort(np.random.default_rng(0).choice(raw.n, raw.n // stride,
-                                                                    replace=False)))
-    means = raw.means[sel].numpy()
-    quats = raw.quats[sel].numpy()
-    scales = raw.raw_scales[sel].numpy()
-    opac = raw.raw_opacities[sel].numpy()
+    means, quats = raw.means.numpy(), raw.quats.numpy()
+    scales, opac = raw.raw_scales.numpy(), raw.raw_opacities.numpy()
     vm = proj.viewmats[:1].cpu().numpy()
     Ks = proj.Ks[:1].cpu().numpy()
     v_img = proj.v_images[0].cpu().numpy()
@@ -816,15 +890,10 @@ def cpu_baseline(proj: Projection, stride=1):
     fwd = compose.rasterize_forward(means, covars, op, vm, Ks, DET, DET, 16, EPS, 3.0)
     compose.explicit_backward(covars, fwd, None, means, quats, scales, opac, SMIN, SMAX, v_img)
     dt = time.perf_counter() - t0
-    n_s = means.shape[0]
-    if stride == 1:
-        sample = (f"oracle projection fwd+bwd (numpy + sequential C, 1 core) on all {raw.n} "
-                  f"config-4 Gaussians, 512^2, view 0, {fwd['isect_ids'].size} tile records")
-    else:
-        sample = (f"oracle projection fwd+bwd (numpy + sequential C, 1 core) on a seeded random "
-                  f"{n_s} of the {raw.n} config-4 Gaussians, 512^2, view 0, "
-                  f"{fwd['isect_ids'].size} tile records; time x{stride} to the full set")
-    return 1.0 / (dt * stride), dt, sample
+    sample = (f"oracle projection fwd+bwd (numpy + C over {cpu_threads()} OpenMP threads) on "
+              f"all {raw.n} config-4 Gaussians, 512^2, view 0, {fwd['isect_ids'].size} tile "
+              "records")
+    return 1.0 / dt, dt, sample
 
 
 def main():
@@ -883,10 +952,17 @@ def main():
                    "dso": 1.0, "dsd": 1.5, "s_detector": 3.0, "eps2d": EPS,
                    "radius_clip": 3.0, "backward_mode": "primitive", "absgrad": True},
     }
-    b_proj = proj_bytes(N_PROJ, i2, DET * DET)
-    result["proj"] = {"n_isects": i2, "algorithmic_bytes": b_proj,
+    # Means over the orbit views the headline cycles through.
+    i2_mean = sum(kb["n_isects_per_view"]) / len(kb["n_isects_per_view"])
+    b_proj = proj_bytes(N_PROJ, i2_mean, DET * DET)
+    result["proj"] = {"n_isects_mean": i2_mean, "n_isects_per_view": kb["n_isects_per_view"],
+                      "views_deg": [orbit_view(v) for v in range(ORBIT_VIEWS)],
+                      "algorithmic_bytes": b_proj,
                       "hbm_frac": b_proj / t_proj / (HBM_PEAK_GBS * 1e9),
-                      "kernel_ms": {k: v * 1e3 for k, v in kb["seconds"].items()}}
+                      "kernel_ms": {k: v * 1e3 for k, v in kb["seconds"].items()},
+                      "raster_kernel_ms_per_view": {
+                          k: [round(x * 1e3, 4) for x in v]
+                          for k, v in kb["per_view_seconds"].items()}}
 
     # Dominant single kernel and its roofline (binning_2d and the backward op
     # span several launches and are not candidates).
@@ -896,30 +972,13 @@ def main():
     n_pix = DET * DET
     dom_bytes = {
         # list (key 8 + id 4) + payload 28 + partials 36 per record; v_image read
-        "rasterize_bwd_rows": 76 * i2 + 4 * n_pix,
-        "rasterize_bwd_reduce": 64 * i2 + 4 * i2 + 36 * N_PROJ,
-        "rasterize_fwd": 32 * i2 + 4 * n_pix,   # id 4 + payload 28; image write
+        "rasterize_bwd_rows": 76 * i2_mean + 4 * n_pix,
+        "rasterize_bwd_reduce": 64 * i2_mean + 4 * i2_mean + 36 * N_PROJ,
+        "rasterize_fwd": 32 * i2_mean + 4 * n_pix,   # id 4 + payload 28; image write
         "project_fwd": 108 * N_PROJ,
         "prepare": 76 * N_PROJ,
     }[dom]
-    traffic = measured_traffic(dom)
-    valu, trans = measured_valu(dom)
-    valu_rate = None if valu is None else valu / secs[dom] / 1e9
-    result["roofline"] = {
-        "kernel": dom, "bound": "hbm",
-        "achieved": dom_bytes / secs[dom] / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-        "frac": dom_bytes / secs[dom] / 1e9 / HBM_PEAK_GBS, "traffic": traffic,
-        "algorithmic_bytes": dom_bytes, "avg_launch_ms": secs[dom] * 1e3,
-        # The raster kernels are bound by vector-ALU issue, not HBM: the
-        # instruction counts come from a rocprofv3 --pmc pass of this kernel.
-        "valu": {"reference_evaluations": 256 * i2,
-                 "executed_evaluations": None if trans is None else trans * 64,
-                 "wave_instructions_per_launch": valu,
-                 "achieved_g_wave_instructions_per_s": valu_rate,
-                 "peak_g_wave_instructions_per_s": VALU_PEAK_G_WAVE_INSTR,
-                 "frac": None if valu_rate is None else valu_rate / VALU_PEAK_G_WAVE_INSTR,
-                 "source": f"profiles/pmc_valu_{dom}.txt"},
-    }
+    result["roofline"] = kernel_roofline(dom, secs[dom], dom_bytes, 256 * i2_mean)
 
     if args.copy_bytes > 0:
         src = torch.ones(args.copy_bytes // 4, device=dev)
@@ -951,18 +1010,24 @@ def main():
         i3 = int(fl.numel())
         n_vox = VOX_DIM ** 3
         b_vox = vox_bytes(N_VOX, i3, n_vox)
-        t_vf = time_kernel(lambda: W.voxelize_to_voxels_fwd(m3, con, vox.opac, off, fl, VOX_DIM,
-                                                            VOX_DIM, VOX_DIM, 8), args.kernel_reps)
-        t_vb = time_kernel(lambda: W.voxelize_to_voxels_bwd_per_gaussian(
-            m3, con, vox.opac, off, ids, fl, vox.v_volume, VOX_DIM, VOX_DIM, VOX_DIM, 8),
-            args.kernel_reps)
+        vb = voxel_breakdown(vox, args.kernel_reps)
+        vsec = vb["seconds"]
+        vbytes = {
+            # id 4 + offsets/keys 8 + payload 40 per record; volume write
+            "voxelize_fwd": 52 * i3 + 4 * n_vox,
+            # list 12 + payload 40 + row 40 per record; v_volume read
+            "voxelize_bwd_rows": 92 * i3 + 4 * n_vox,
+            # row 48 + emission id 4 per record; 40 B per Gaussian out
+            "voxelize_bwd_reduce": 52 * i3 + 40 * N_VOX,
+        }
+        vdom = max(vsec, key=vsec.get)
         result["voxelize"] = {
             "workload": "config3 voxelization fwd+bwd", "n_gaussians": N_VOX, "grid": VOX_DIM,
             "n_isects": i3, "ms_per_call": t_vox * 1e3,
             "mvox_per_s": n_vox / t_vox / 1e6, "algorithmic_bytes": b_vox,
             "hbm_frac": b_vox / t_vox / (HBM_PEAK_GBS * 1e9),
-            "kernel_ms": {"voxelize_fwd": t_vf * 1e3, "voxelize_bwd": t_vb * 1e3},
-            "voxelize_fwd_hbm_frac": (40 * i3 + 4 * n_vox) / t_vf / (HBM_PEAK_GBS * 1e9),
+            "kernel_ms": {k: v * 1e3 for k, v in vsec.items()},
+            "roofline": kernel_roofline(vdom, vsec[vdom], vbytes[vdom], 512 * i3),
         }
         log(f"voxelization fwd+bwd: {t_vox * 1e3:.3f} ms/call, I3={i3}")
 
@@ -1007,32 +1072,54 @@ def main():
             i2_stress = int(W2.isect_tiles(m2, rad, 16, 64, 64)[1].numel())
         sv = Voxelization(dev, n=2_000_000, dim=512, seed=5, needle_fraction=0.0005)
         t_sv = time_steps(sv.step, 3, 1)
+        n_sv = int(sv.last[4].numel())
+        del sv
+        torch.cuda.empty_cache()
+        slab = SlabVoxelization(dev)
+        t_slab = time_steps(slab.step, 1, 1)
         result["stress"] = {
             "projection": {"workload": "config5 projection fwd+bwd: 2M Gaussians (log-scale "
                                        "N(-5,1), 5% needles), 1024^2, one view",
                            "n_isects_view0": i2_stress, "ms_per_call": t_sp * 1e3},
             "voxelization": {"workload": "config5 voxelization fwd+bwd at 512^3 with 0.05% "
-                                         "needles (5% needles need 7.46e9 brick records, beyond "
-                                         "the int32 offsets)",
-                             "n_isects": int(sv.last[4].numel()), "ms_per_call": t_sv * 1e3,
-                             "mvox_per_s": 512 ** 3 / t_sv / 1e6}}
+                                         "needles, one brick list",
+                             "n_isects": n_sv, "ms_per_call": t_sv * 1e3,
+                             "mvox_per_s": 512 ** 3 / t_sv / 1e6},
+            "voxelization_5pct_needles": {
+                "workload": "config5 voxelization fwd+bwd at 512^3 with the stated 5% needles "
+                            "through r2splat.ops (VolumePass): z-slabs of at most "
+                            f"{slab.limit} brick records, re-binned for the backward",
+                "n_isects": slab.records, "slabs": len(slab.slabs),
+                "ms_per_call": t_slab * 1e3, "mvox_per_s": 512 ** 3 / t_slab / 1e6}}
         log(f"stress: projection {t_sp * 1e3:.2f} ms, voxelization {t_sv * 1e3:.2f} ms "
-            f"({int(sv.last[4].numel())} records)")
-        del sp, sv
+            f"({n_sv} records); 5% needles {t_slab * 1e3:.1f} ms ({slab.records} records in "
+            f"{len(slab.slabs)} slabs)")
+        del sp, slab
         torch.cuda.empty_cache()
 
     if not args.no_cpu_baseline:
         log("config 1 like for like (GPU path vs the dense torch formulation on the host)")
-        result["config1"] = config1(dev, 20, 3)
-        c1 = result["config1"]
+        c1 = config1(dev, 20, 3)
+        result["config1"] = c1
         log(f"config1: GPU {c1['gpu_ms_per_call']:.3f} ms, CPU dense torch "
             f"{c1['cpu_dense_torch_ms_per_call']:.1f} ms on {c1['cpu_threads']} threads, "
             f"max |diff| image {c1['image_max_abs_diff']:.2e} volume "
             f"{c1['volume_max_abs_diff']:.2e}")
-        log("timing the CPU oracle baseline")
-        cps, dt, sample = cpu_baseline(proj)
-        result["cpu_baseline"] = {"value": cps, "unit": "proj fwd+bwd calls/s", "cores": 1,
-                                  "kind": "port", "sample": sample, "sample_seconds": dt}
+        t_cpu = c1["cpu_dense_torch_ms_per_call"] * 1e-3
+        result["cpu_baseline"] = {
+            "value": 1.0 / t_cpu, "unit": "config-1 fwd+bwd calls/s (64^2 view + 64^3 volume)",
+            "cores": c1["cpu_threads"], "kind": "port",
+            "sample": "BASELINE config 1 in full: the reference's dense PyTorch formulation "
+                      "(oracle/dense.py) from the raw parameters, torch autograd backward, "
+                      f"median of 5 calls after 1 warm-up on {c1['cpu_threads']} host threads",
+            "projections_per_s": 1.0 / t_cpu, "mvox_per_s": 64 ** 3 / t_cpu / 1e6,
+            "seconds_per_call": t_cpu,
+            "gpu_same_config_calls_per_s": 1e3 / c1["gpu_ms_per_call"]}
+        log("timing the CPU oracle on the headline workload")
+        cps, dt, sample = oracle_projection_baseline(proj)
+        result["cpu_oracle"] = {"value": cps, "unit": "proj fwd+bwd calls/s",
+                                "cores": cpu_threads(),
+                                "kind": "port", "sample": sample, "sample_seconds": dt}
     print(json.dumps(result), flush=True)
 
 

@@ -16,8 +16,9 @@ Modules
              function is involved.
 ``binning``  integer tile binning (count, emit, stable sort, offsets), 2D and
              3D, plus the densify/prune index compaction.
-``native``   ctypes bindings of ``oracle/c/r2s_oracle.c``: the sequential
-             rasterizer and voxelizer (forward and both backward modes).
+``native``   ctypes bindings of ``oracle/c/r2s_oracle.c``: the rasterizer and
+             voxelizer (forward and both backward modes), over OpenMP
+             threads with results independent of the thread count.
 ``compose``  the ``r2splat.ops`` forward/backward composition on top of the
              above (explicit.py / direct.py restated).
 ``dense``    the reference's dense PyTorch formulation (every Gaussian at
