@@ -119,6 +119,30 @@ __device__ __forceinline__ T wave_sum(T v) {
 }
 
 // Hardware float atomics (no CAS loop; built with -munsafe-fp-atomics).
+// N records of type Rec staged in LDS word-major: word w of record i at
+// words[w][i].  Lanes that touch one word of consecutive records hit
+// consecutive banks; a record-major array whose record size is a multiple
+// of 64 bytes would put a whole wave on two of the 32 banks.
+template <typename Rec, int N>
+struct WordMajor {
+  static constexpr int kWords = static_cast<int>((sizeof(Rec) + 3) / 4);
+  uint32_t words[kWords][N];
+  __device__ __forceinline__ void store(int i, const Rec &r) {
+    uint32_t t[kWords];
+    __builtin_memcpy(t, &r, sizeof(Rec));
+#pragma unroll
+    for (int w = 0; w < kWords; ++w) words[w][i] = t[w];
+  }
+  __device__ __forceinline__ Rec load(int i) const {
+    uint32_t t[kWords];
+#pragma unroll
+    for (int w = 0; w < kWords; ++w) t[w] = words[w][i];
+    Rec r;
+    __builtin_memcpy(&r, t, sizeof(Rec));
+    return r;
+  }
+};
+
 __device__ __forceinline__ void atomic_add(float *p, float v) { unsafeAtomicAdd(p, v); }
 __device__ __forceinline__ void atomic_add(double *p, double v) { unsafeAtomicAdd(p, v); }
 

@@ -702,7 +702,7 @@ __global__ __launch_bounds__(kSplitThreads) void raster_bwd_split_kernel(
     T *__restrict__ rows) {
   constexpr int R = 16;
   constexpr int kWaves = kSplitThreads / 64;
-  __shared__ RasterRecord<T> s_rec[kSplitThreads];
+  __shared__ WordMajor<RasterRecord<T>, kSplitThreads> s_rec;
   __shared__ int32_t s_r[kSplitThreads];
   __shared__ uint32_t s_key[kSplitThreads];
   __shared__ uint32_t s_count[kWaves];
@@ -758,13 +758,13 @@ __global__ __launch_bounds__(kSplitThreads) void raster_bwd_split_kernel(
   const uint32_t slot = fast ? fast_lt : n_fast + (threadIdx.x - fast_lt);
   s_r[slot] = in_list ? static_cast<int32_t>(r) : -1;
   s_key[slot] = key;
-  s_rec[slot] = rec;
+  s_rec.store(static_cast<int>(slot), rec);
   __syncthreads();
   const int32_t rr = s_r[threadIdx.x];
   const bool valid = rr >= 0;
   if (ballot(valid) == 0) return;  // uniform per wave; no barrier follows
   key = s_key[threadIdx.x];
-  rec = s_rec[threadIdx.x];
+  rec = s_rec.load(static_cast<int>(threadIdx.x));
   const bool wave_fast = (wave + 1) * 64 <= n_fast;
   const uint32_t cam = key / n_tiles, t = key - cam * n_tiles;
   const uint32_t ty = t / tw, tx = t - ty * tw;

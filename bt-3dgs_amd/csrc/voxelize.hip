@@ -525,7 +525,7 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
   constexpr int R = kChunkRows;
   using Q = typename Quad<T>::type;
   constexpr int kq = Quad<T>::n;
-  __shared__ ChunkRecord<T> s_rec[kChunkWaves][64];
+  __shared__ WordMajor<ChunkRecord<T>, 64> s_rec[kChunkWaves];
   __shared__ uint64_t s_rows[kChunkWaves][64];  // reached rows: bit 8 * slice + row
   __shared__ T s_acc[kChunkWaves][10][64];
   __shared__ uint16_t s_chunk[kChunkWaves][64 * R];
@@ -599,7 +599,7 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
     cr.oj = b.oj;
     cr.oi = b.oi;
     cr.n_items = n_items;
-    s_rec[w][lane] = cr;
+    s_rec[w].store(static_cast<int>(lane), cr);
     s_rows[w][lane] = reach;
 #pragma unroll
     for (int c = 0; c < 10; ++c) s_acc[w][c][lane] = 0;
@@ -629,7 +629,7 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
     const bool act = ci < n_list;
     const uint32_t ent = act ? static_cast<uint32_t>(s_chunk[w][ci]) : 0u;
     const uint32_t rl = ent & 63u, q = ent >> 6;
-    const ChunkRecord<T> cr = s_rec[w][rl];
+    const ChunkRecord<T> cr = s_rec[w].load(static_cast<int>(rl));
     const uint64_t rows_m = s_rows[w][rl];
     // The chunk's first item, the (8 q)-th set bit: its slice by the
     // running bit counts of the slice bytes; within a slice the reached rows
