@@ -119,6 +119,27 @@ __device__ __forceinline__ T wave_sum(T v) {
 }
 
 // Hardware float atomics (no CAS loop; built with -munsafe-fp-atomics).
+// Transpose of a 64 x 64 bit matrix held one row per lane (bit j of lane
+// i's word is M[i][j]): returns column `lane` (bit i is M[i][lane]).  Six
+// butterfly stages swap blocks of 32, 16, ..., 1 bits between lanes i and
+// i ^ s, two lane shuffles and a few logic operations each.
+__device__ __forceinline__ uint64_t transpose_bits64(uint64_t row, uint32_t lane) {
+  constexpr uint64_t kKeep[6] = {0x00000000FFFFFFFFull, 0x0000FFFF0000FFFFull,
+                                 0x00FF00FF00FF00FFull, 0x0F0F0F0F0F0F0F0Full,
+                                 0x3333333333333333ull, 0x5555555555555555ull};
+#pragma unroll
+  for (int k = 0; k < 6; ++k) {
+    const int s = 32 >> k;
+    const uint64_t m = kKeep[k];
+    const uint32_t lo = static_cast<uint32_t>(__shfl_xor(static_cast<int>(row), s));
+    const uint32_t hi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(row >> 32), s));
+    const uint64_t other = (static_cast<uint64_t>(hi) << 32) | lo;
+    row = (lane & static_cast<uint32_t>(s)) ? (((other >> s) & m) | (row & ~m))
+                                            : ((row & m) | ((other & m) << s));
+  }
+  return row;
+}
+
 // N records of type Rec staged in LDS word-major: word w of record i at
 // words[w][i].  Lanes that touch one word of consecutive records hit
 // consecutive banks; a record-major array whose record size is a multiple

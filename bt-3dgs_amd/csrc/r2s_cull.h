@@ -108,6 +108,11 @@ __device__ __forceinline__ uint32_t wave_record_key(const int32_t *__restrict__ 
   return key;
 }
 
+// Square root for culling bounds: the hardware v_sqrt_f32 (about 1 ulp),
+// far inside the margins, instead of the correctly rounded expansion.
+__device__ __forceinline__ float cull_sqrt(float x) { return __builtin_amdgcn_sqrtf(x); }
+__device__ __forceinline__ double cull_sqrt(double x) { return sqrt(x); }
+
 // Enlarged ln(|w| / thr); the float log is ample against the 1e-3 slack.
 __device__ __forceinline__ float sigma_bound(float w_abs, double thr) {
   return (logf(w_abs) - static_cast<float>(log(thr))) * (1.0f + 1e-3f) + 1e-3f;
@@ -181,6 +186,13 @@ struct Cull3 {
   T a2, inv_a2;  // p11 - p01^2 / p00 and its inverse
   T ky;          // y centre per unit z: yc = -ky z
   T c3;          // det / (p00 a2): slice minimum 1/2 c3 z^2
+  // The slice ellipse 1/2 p00 (x - xc)^2 + 1/2 a2 (y - yc)^2 <= budget, with
+  // xc = -(kx y + kz z), as vertical chords: at x = xe + u (xe its centre)
+  //   1/2 p11 (y - ye + r11 u)^2 + 1/2 e11 u^2 <= budget.
+  T kx, kz;      // p01 / p00, p02 / p00
+  T r11;         // p01 / p11
+  T e11;         // (p00 p11 - p01^2) / p11
+  T inv_p11;     // 1 / p11
 };
 
 template <typename T>
@@ -193,17 +205,26 @@ __device__ __forceinline__ Cull3<T> cull3_setup(const T q[6], T w_abs, double th
   r.ok = (p00 > 0.0) && (m2 > 0.0) && (det > 0.0) && isfinite(det) && isfinite(m2) &&
          isfinite(static_cast<double>(w_abs));
   r.s = r.hz = r.inv_p = r.a2 = r.inv_a2 = r.ky = r.c3 = 0;
+  r.kx = r.kz = r.r11 = r.e11 = r.inv_p11 = 0;
   if (r.ok) {
+    // Four reciprocals serve every quotient (a few ulp of double, far
+    // inside the margins); the differences of products stay in double.
+    const double ip00 = 1.0 / p00, im2 = 1.0 / m2, ip11 = 1.0 / p11, idet = 1.0 / det;
     const double s = static_cast<double>(sigma_bound(w_abs, thr));
-    const double a2 = m2 / p00;
-    const double k1 = p12 - p01 * p02 / p00;
+    const double a2 = m2 * ip00;
+    const double k1 = p12 - p01 * p02 * ip00;
     r.s = static_cast<T>(s);
-    r.hz = static_cast<T>(s > 0.0 ? sqrt(2.0 * s * m2 / det) : 0.0);
-    r.inv_p = static_cast<T>(1.0 / p00);
+    r.hz = static_cast<T>(s > 0.0 ? sqrt(2.0 * s * m2 * idet) : 0.0);
+    r.inv_p = static_cast<T>(ip00);
     r.a2 = static_cast<T>(a2);
-    r.inv_a2 = static_cast<T>(1.0 / a2);
-    r.ky = static_cast<T>(k1 / a2);
-    r.c3 = static_cast<T>(det / m2);
+    r.inv_a2 = static_cast<T>(p00 * im2);
+    r.ky = static_cast<T>(k1 * p00 * im2);
+    r.c3 = static_cast<T>(det * im2);
+    r.kx = static_cast<T>(p01 * ip00);
+    r.kz = static_cast<T>(p02 * ip00);
+    r.r11 = static_cast<T>(p01 * ip11);  // p11 > 0 follows from m2 > 0, p00 > 0
+    r.e11 = static_cast<T>(m2 * ip11);
+    r.inv_p11 = static_cast<T>(ip11);
   }
   return r;
 }

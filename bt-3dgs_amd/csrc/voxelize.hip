@@ -254,20 +254,157 @@ __device__ __forceinline__ void voxel_row(const BwdRecord<T> &rec, const T (&vv)
   }
 }
 
-// Slice range of one record's brick rows: rows j0..j1 of slice dz that the
-// ellipsoid reaches (empty when the slice is not reached).
+// Slice range of one record's brick rows: rows j0..j1 of slice dz whose
+// voxels (columns dx0 .. dx0 + nk - 1 as offsets from the mean) the
+// ellipsoid reaches; empty (j1 < j0) when none.  In the slice, the reached
+// part of the ellipse is its intersection with the brick's x-band, a convex
+// set, so its rows are one range: the top is the top of the vertical chord
+// at the band point nearest the ellipse's topmost point (chord tops are a
+// concave function of x), the bottom likewise; every term is a completed
+// square, so nothing cancels.  The band is widened by kCullMargin and the
+// rows are taken with index_range's margin.
 template <typename T>
 __device__ __forceinline__ void slice_rows(const BwdRecord<T> &rec, const Brick &b, bool in_slice,
-                                           T dz, int &j0, int &j1) {
+                                           T dz, T dx0, int &j0, int &j1) {
   j0 = b.oj;
   j1 = b.oj + b.nj - 1;
   if (!in_slice) {
     j1 = j0 - 1;
-  } else if (rec.cu.ok) {
-    const T bud_z = rec.cu.s - static_cast<T>(0.5) * rec.cu.c3 * dz * dz;
-    if (!budget_range<T>(rec.m[1], -rec.cu.ky * dz, bud_z, rec.cu.inv_a2, b.oj, b.oj + b.nj - 1,
-                         j0, j1))
-      j1 = j0 - 1;
+    return;
+  }
+  if (!rec.cu.ok) return;  // every row
+  const Cull3<T> &c = rec.cu;
+  const T half = static_cast<T>(0.5), two = static_cast<T>(2);
+  const T m = static_cast<T>(kCullMargin);
+  const T bud = c.s - half * c.c3 * dz * dz;
+  const T ye = -c.ky * dz;
+  const T xe = -(c.kx * ye + c.kz * dz);
+  const T hy = cull_sqrt(fmax(two * bud * c.inv_a2, static_cast<T>(0)));
+  const T ulo = (dx0 - m) - xe;
+  const T uhi = (dx0 + static_cast<T>(b.nk - 1) + m) - xe;
+  // Topmost point of the ellipse at u = -kx hy, bottommost at +kx hy.
+  const T ut = fmin(fmax(-c.kx * hy, ulo), uhi);
+  const T ub = fmin(fmax(c.kx * hy, ulo), uhi);
+  const T rt = bud - half * c.e11 * ut * ut;
+  const T rb = bud - half * c.e11 * ub * ub;
+  if (!(bud >= static_cast<T>(0)) || !(rt >= static_cast<T>(0))) {
+    j1 = j0 - 1;  // the slice, or the band, misses the ellipse
+    return;
+  }
+  const T top = ye + (cull_sqrt(two * rt * c.inv_p11) - c.r11 * ut);
+  const T bot = ye - (cull_sqrt(fmax(two * rb * c.inv_p11, static_cast<T>(0))) + c.r11 * ub);
+  if (!index_range<T>(rec.m[1], bot, top, b.oj, b.oj + b.nj - 1, j0, j1)) j1 = j0 - 1;
+}
+
+// The rows of a brick of size 8 that one record reaches, as a 64-bit mask:
+// bit 8 * slice + row (brick-local).
+template <typename T>
+__device__ __forceinline__ uint64_t reach_mask(const BwdRecord<T> &rec, const Brick &b, T dx0) {
+  const T half = static_cast<T>(0.5);
+  uint64_t reach = 0;
+#pragma unroll 1
+  for (int li = 0; li < 8; ++li) {
+    const int i = b.oi + li;
+    const bool in_slice = rec.live && li < b.ni && i >= rec.i0 && i <= rec.i1;
+    const T dz = (static_cast<T>(i) + half) - rec.m[2];
+    int j0, j1;
+    slice_rows(rec, b, in_slice, dz, dx0, j0, j1);
+    const uint32_t c = j1 >= j0 ? static_cast<uint32_t>(j1 - j0 + 1) : 0u;  // rows j0 - oj ..
+    const uint32_t run = c >= 8u ? 0xFFu : ((1u << c) - 1u);
+    reach |= static_cast<uint64_t>((run << ((j0 - b.oj) & 7)) & 0xFFu) << (8 * li);
+  }
+  return reach;
+}
+
+// Forward at brick size 8 with culled rows.  One wave per brick; lane =
+// x-row (slice lane / 8, row lane % 8), its 8 voxels in registers.  Per
+// batch of 64 records of the brick's list, each lane loads one record and
+// the rows it reaches (reach_mask); 64 ballots hand each row's lane the set
+// of batch records that reach that row; each lane then walks its own set in
+// list order, so a record costs a row only where it can pass the alpha
+// test.  Every voxel still sums its records in list order, and the rows a
+// record does not reach would only add exact zeros, so the volume equals
+// voxel_fwd_kernel's bit for bit.
+template <typename T>
+__global__ __launch_bounds__(64) void voxel_fwd_reach_kernel(
+    const T *__restrict__ means3d, const T *__restrict__ conics, const T *__restrict__ opac,
+    const int32_t *__restrict__ tile_offsets, const int32_t *__restrict__ flatten_ids,
+    int64_t n_isects, uint32_t n_keys, uint32_t koff, int64_t N, uint32_t D2, uint32_t D1,
+    uint32_t D0, uint32_t n2, uint32_t n1, T *__restrict__ volume) {
+  constexpr int R = 8;
+  using V4 = typename Vec<T>::v4;
+  // Per staged record {mx, my, mz, o}, {h0, h1, h2, h3}, {h4, h5, limit bits,
+  // 0}: three vector reads per use; the 12-word stride spreads 8
+  // consecutive records over all banks.
+  __shared__ V4 s_rec[64][3];
+  const uint32_t key = xcd_swizzle(blockIdx.x, n_keys);  // in the lists (koff: the grid's)
+  const Brick b = brick_of(key + koff, n2, n1, R, D2, D1, D0);
+  const int lane = static_cast<int>(lane_id());
+  const int li = lane >> 3, lj = lane & 7;
+  const T half = static_cast<T>(0.5);
+  const T py = static_cast<T>(b.oj + lj) + half;
+  const T pz = static_cast<T>(b.oi + li) + half;
+  const T px0 = static_cast<T>(b.ok) + half;
+  const int64_t start = tile_offsets[key];
+  const int64_t end = (key == n_keys - 1) ? n_isects : static_cast<int64_t>(tile_offsets[key + 1]);
+  T acc[R];
+#pragma unroll
+  for (int k = 0; k < R; ++k) acc[k] = 0;
+  for (int64_t base = start; base < end; base += 64) {
+    const int64_t idx = base + lane;
+    const bool in = idx < end;
+    const int64_t g = in ? static_cast<int64_t>(flatten_ids[idx]) : -1;
+    BwdRecord<T> rec;
+    load_bwd_record(means3d, conics, opac, g, N, in, b, rec);
+    const uint64_t reach = rec.live ? reach_mask(rec, b, px0 - rec.m[0]) : 0ull;
+    V4 a, hq, hr;
+    a.x = rec.m[0];
+    a.y = rec.m[1];
+    a.z = rec.m[2];
+    a.w = rec.o;
+    hq.x = rec.h[0];
+    hq.y = rec.h[1];
+    hq.z = rec.h[2];
+    hq.w = rec.h[3];
+    hr.x = rec.h[4];
+    hr.y = rec.h[5];
+    hr.z = limit_as_value(rec.lim);
+    hr.w = 0;
+    __syncthreads();  // the previous batch's reads are done
+    s_rec[lane][0] = a;
+    s_rec[lane][1] = hq;
+    s_rec[lane][2] = hr;
+    // Bit t of lane r's set: batch record t reaches row r.
+    const uint64_t mine = transpose_bits64(reach, static_cast<uint32_t>(lane));
+    uint32_t mine_lo = static_cast<uint32_t>(mine), mine_hi = static_cast<uint32_t>(mine >> 32);
+    __syncthreads();
+    while ((mine_lo | mine_hi) != 0u) {
+      const bool low = mine_lo != 0u;
+      const uint32_t word = low ? mine_lo : mine_hi;
+      const int t = static_cast<int>(__builtin_ctz(word)) + (low ? 0 : 32);
+      const uint32_t rest = word & (word - 1u);
+      mine_lo = low ? rest : mine_lo;
+      mine_hi = low ? mine_hi : rest;
+      const V4 qa = s_rec[t][0], qh = s_rec[t][1], qr = s_rec[t][2];
+      const typename Bits<T>::type lim = bits_of(qr.z);
+      const T dy = py - qa.y, dz = pz - qa.z;
+      const T B = qh.y * dy + qh.z * dz;
+      const T C = (qh.w * dy + qr.x * dz) * dy + qr.y * dz * dz;
+#pragma unroll
+      for (int k = 0; k < R; ++k) {
+        const T dx = (px0 + static_cast<T>(k)) - qa.x;
+        const T sl = (qh.x * dx + B) * dx + C;
+        const T e = neg_exp2(sl);
+        acc[k] = fma(qa.w, alpha_pass(sl, lim) ? e : static_cast<T>(0), acc[k]);
+      }
+    }
+  }
+  if (li < b.ni && lj < b.nj) {
+    T *out = volume + static_cast<int64_t>(b.oi + li) * D1 * D2 +
+             static_cast<int64_t>(b.oj + lj) * D2 + b.ok;
+#pragma unroll
+    for (int k = 0; k < R; ++k)
+      if (k < b.nk) out[k] = acc[k];
   }
 }
 
@@ -308,7 +445,7 @@ __device__ __forceinline__ void voxel_brick_full(const BwdRecord<T> &rec, const 
       j0 = b.oj + static_cast<int>(__builtin_ctz(byte | 0x100u));
       j1 = j0 + __popc(byte) - 1;
     } else {
-      slice_rows(rec, b, in_slice, dz, j0, j1);
+      slice_rows(rec, b, in_slice, dz, dx0, j0, j1);
     }
     const T h4dz = rec.h[4] * dz, h5dzz = rec.h[5] * dz * dz, Bz = rec.h[2] * dz;
     const T *__restrict__ vslice = v_vol + static_cast<int64_t>(i) * plane + b.ok;
@@ -415,7 +552,7 @@ __global__ __launch_bounds__(kBwdThreads) void voxel_bwd_kernel(
       const T dz = (static_cast<T>(i) + half) - rec.m[2];
       // Rows of this slice the lane's ellipsoid can reach.
       int j0, j1;
-      slice_rows(rec, b, in_slice, dz, j0, j1);
+      slice_rows(rec, b, in_slice, dz, dx0, j0, j1);
       const T h4dz = rec.h[4] * dz, h5dzz = rec.h[5] * dz * dz, Bz = rec.h[2] * dz;
 #pragma unroll 1
       for (int lj = 0; lj < R; ++lj) {
@@ -550,28 +687,16 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
   load_bwd_record(means3d, conics, opac, g, N, key_ok, b, rec);
   const T half = static_cast<T>(0.5);
   const uint32_t plane = D1 * D2;  // the caller checks D2 D1 D0 < 2^31
+  const T dx0 = (static_cast<T>(b.ok) + half) - rec.m[0];
 
-  // The record's reached rows as a 64-bit mask, bit 8 * slice + row; the
-  // items are its set bits in increasing order.
-  uint64_t reach = 0;
-#pragma unroll 1
-  for (int li = 0; li < R; ++li) {
-    const int i = b.oi + li;
-    const bool in_slice = rec.live && i >= rec.i0 && i <= rec.i1;
-    const T dz = (static_cast<T>(i) + half) - rec.m[2];
-    int j0, j1;
-    slice_rows(rec, b, in_slice, dz, j0, j1);
-    const uint32_t c = j1 >= j0 ? static_cast<uint32_t>(j1 - j0 + 1) : 0u;  // rows j0 - oj ..
-    const uint32_t run = c >= 8u ? 0xFFu : ((1u << c) - 1u);
-    reach |= static_cast<uint64_t>((run << ((j0 - b.oj) & 7)) & 0xFFu) << (8 * li);
-  }
+  // The record's reached rows; the items are its set bits in increasing order.
+  const uint64_t reach = reach_mask(rec, b, dx0);
   const int n_items = __popcll(reach);
   if (wave_sum(n_items) > kDenseItems) {  // uniform per wave
     T T0 = 0, T1 = 0, T2 = 0, Y0 = 0, Z0 = 0, Y1 = 0, Z1 = 0, YY = 0, YZ = 0, ZZ = 0;
     if (ballot(rec.live) != 0)
-      voxel_brick_full<T, R, true>(rec, b, v_vol, static_cast<int64_t>(plane), D2,
-                                   (static_cast<T>(b.ok) + half) - rec.m[0], T0, T1, T2, Y0, Z0,
-                                   Y1, Z1, YY, YZ, ZZ, reach);
+      voxel_brick_full<T, R, true>(rec, b, v_vol, static_cast<int64_t>(plane), D2, dx0, T0, T1,
+                                   T2, Y0, Z0, Y1, Z1, YY, YZ, ZZ, reach);
     if (!key_ok) return;
     const T o = rec.o;
     const T *qc = rec.q;
@@ -644,11 +769,11 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
       rem -= (pos == 64) ? c : 0;
     }
     const int n_here = act ? min(R, cr.n_items - static_cast<int>(q) * R) : 0;
-    const T dx0 = (static_cast<T>(cr.ok) + half) - cr.m[0];
+    const T cdx0 = (static_cast<T>(cr.ok) + half) - cr.m[0];
     T dxk[R], wk[R];
 #pragma unroll
     for (int k = 0; k < R; ++k) {
-      dxk[k] = dx0 + static_cast<T>(k);
+      dxk[k] = cdx0 + static_cast<T>(k);
       wk[k] = 0;
     }
     T Y0 = 0, Z0 = 0, Y1 = 0, Z1 = 0, YY = 0, YZ = 0, ZZ = 0;
@@ -805,8 +930,9 @@ int voxel_fwd_impl(const T *means3d, const T *conics, const T *opac,
   R2S_REQUIRE(means3d && conics && opac && tile_offsets && flatten_ids, "%s: null pointer", name);
   const uint32_t n_keys = n2 * n1 * n0, koff = z0 * n1 * n2;
   if (ts == 8)
-    launch_voxel_fwd<T, 8>(means3d, conics, opac, tile_offsets, flatten_ids, n_isects, n_keys,
-                           koff, N, D2, D1, D0, ts, n2, n1, volume, stream);
+    voxel_fwd_reach_kernel<T><<<dim3(n_keys), dim3(64), 0, stream>>>(
+        means3d, conics, opac, tile_offsets, flatten_ids, n_isects, n_keys, koff, N, D2, D1, D0,
+        n2, n1, volume);
   else if (ts == 16)
     launch_voxel_fwd<T, 16>(means3d, conics, opac, tile_offsets, flatten_ids, n_isects, n_keys,
                             koff, N, D2, D1, D0, ts, n2, n1, volume, stream);
