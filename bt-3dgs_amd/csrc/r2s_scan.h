@@ -1,12 +1,13 @@
-// Device-wide exclusive prefix sum in two launches: block sums, then a
-// downsweep in which each block adds up the sums of the blocks before it.
+// Device-wide exclusive prefix sum: block sums, then a downsweep.
 //
 // 256-thread blocks, 4096 items per block taken as 16 chunks of 256: item
 // k * 256 + t of a block belongs to thread t, so every load and store of a
-// wave covers 64 consecutive items.  A scan of n items needs
-// ceil(n / 4096) partials of workspace; block b of the downsweep reads the
-// b partials before it (a few hundred at the sizes here, from L2), which
-// costs less than a third launch that scans them.  Deterministic: the same
+// wave covers 64 consecutive items.  Up to kScanDirectBlocks blocks, block b
+// of the downsweep adds up the b block sums before it itself (from L2; two
+// launches in all), which costs less than scanning them.  Above that the
+// per-block reads would grow as the square of the block count, so the
+// block sums are first scanned by the same routine (one level down, out of
+// place) and each block reads its own offset.  Deterministic: the same
 // input always produces the same output.
 #pragma once
 
@@ -18,7 +19,14 @@ constexpr int kScanThreads = 256;
 constexpr int kScanItems = 16;
 constexpr int kScanTile = kScanThreads * kScanItems;
 
-inline int64_t scan_partials_count(int64_t n) { return ceil_div(n, kScanTile); }
+constexpr int64_t kScanDirectBlocks = 1024;
+
+// Workspace elements of a scan of n items: the block sums, and above
+// kScanDirectBlocks blocks also their scan and its own workspace.
+inline int64_t scan_partials_count(int64_t n) {
+  const int64_t nb = ceil_div(n, kScanTile);
+  return nb > kScanDirectBlocks ? 2 * nb + scan_partials_count(nb) : nb;
+}
 
 // Exclusive scan across the block; `total` receives the block sum.
 // `lds` needs blockDim.x / 64 entries.
@@ -62,7 +70,9 @@ __global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(const Tin *__
 // item order gives each chunk-wave its offset within the block.  The block's
 // own offset is the sum of the partials of the blocks before it; the last
 // block also writes the grand total (if `total` is not null).
-template <typename Tin, typename Tout>
+// kScanned: partials[b] already holds block b's offset (the scanned block
+// sums); otherwise the block sums them.
+template <typename Tin, typename Tout, bool kScanned>
 __global__ __launch_bounds__(kScanThreads) void scan_down_kernel(const Tin *__restrict__ in,
                                                                  int64_t n,
                                                                  const Tout *__restrict__ partials,
@@ -93,16 +103,21 @@ __global__ __launch_bounds__(kScanThreads) void scan_down_kernel(const Tin *__re
     s_tot[lane] = it - t;
     if (lane == 63) s_block = it;
   }
-  // Sum of the earlier blocks' partials: strided over the threads, then
-  // wave sums and one fixed-order pass over the waves.
-  Tout pre = 0;
-  for (uint32_t b = threadIdx.x; b < blockIdx.x; b += kScanThreads) pre += partials[b];
-  pre = wave_sum(pre);
-  if (lane == 0) s_pre[w] = pre;
-  __syncthreads();
   Tout p = 0;
+  if constexpr (kScanned) {
+    p = partials[blockIdx.x];
+    __syncthreads();
+  } else {
+    // Sum of the earlier blocks' partials: strided over the threads, then
+    // wave sums and one fixed-order pass over the waves.
+    Tout pre = 0;
+    for (uint32_t b = threadIdx.x; b < blockIdx.x; b += kScanThreads) pre += partials[b];
+    pre = wave_sum(pre);
+    if (lane == 0) s_pre[w] = pre;
+    __syncthreads();
 #pragma unroll
-  for (int k = 0; k < kScanThreads / 64; ++k) p += s_pre[k];
+    for (int k = 0; k < kScanThreads / 64; ++k) p += s_pre[k];
+  }
   if (threadIdx.x == 0 && total != nullptr && blockIdx.x == gridDim.x - 1) *total = p + s_block;
 #pragma unroll
   for (int k = 0; k < kScanItems; ++k) {
@@ -129,15 +144,22 @@ int device_fill(T *p, int64_t n, T v, hipStream_t stream, const char *what) {
 template <typename Tin, typename Tout>
 int device_exclusive_scan(const Tin *in, int64_t n, Tout *out, Tout *total, Tout *partials,
                           hipStream_t stream, const char *what) {
-  const int64_t nb = scan_partials_count(n);
-  if (nb == 0) {
+  const int64_t nb = ceil_div(n, kScanTile);
+  if (nb <= 0) {
     if (total != nullptr) return device_fill<Tout>(total, 1, static_cast<Tout>(0), stream, what);
     return R2S_OK;
   }
-  scan_reduce_kernel<Tin, Tout><<<dim3(static_cast<uint32_t>(nb)), dim3(kScanThreads), 0, stream>>>(
-      in, n, partials);
-  scan_down_kernel<Tin, Tout><<<dim3(static_cast<uint32_t>(nb)), dim3(kScanThreads), 0, stream>>>(
-      in, n, partials, out, total);
+  const dim3 grid(static_cast<uint32_t>(nb)), block(kScanThreads);
+  scan_reduce_kernel<Tin, Tout><<<grid, block, 0, stream>>>(in, n, partials);
+  if (nb <= kScanDirectBlocks) {
+    scan_down_kernel<Tin, Tout, false><<<grid, block, 0, stream>>>(in, n, partials, out, total);
+    return check_launch(what);
+  }
+  // Block offsets: the scan of the nb block sums into partials[nb, 2 nb).
+  R2S_RETURN_IF(check_launch(what));
+  R2S_RETURN_IF((device_exclusive_scan<Tout, Tout>(partials, nb, partials + nb, nullptr,
+                                                   partials + 2 * nb, stream, what)));
+  scan_down_kernel<Tin, Tout, true><<<grid, block, 0, stream>>>(in, n, partials + nb, out, total);
   return check_launch(what);
 }
 

@@ -582,6 +582,28 @@ def test_mask_split_matches_torch_where(n):
         assert torch.equal(out[:n_true], sel) and torch.equal(out[n_true:], rest)
 
 
+@pytest.mark.parametrize("n", [4_194_304, 4_194_305, 9_000_001])
+def test_count_scan_beyond_one_level(n):
+    # More than 1024 scan blocks of 4096 items: the block sums are scanned
+    # one level down.  Offsets must equal the int64 cumsum of the counts.
+    from r2splat.cuda import _backend
+
+    lib, P = _backend.library(), _ops._ptr
+    g = torch.Generator().manual_seed(n)
+    m2 = (torch.rand((1, n, 2), generator=g) * 256).to(DEV)
+    radii = torch.randint(0, 24, (1, n, 2), generator=g, dtype=torch.int32).to(DEV)
+    counts = torch.empty(n, dtype=torch.int32, device=DEV)
+    offsets = torch.empty(n + 1, dtype=torch.int64, device=DEV)
+    ws = torch.empty(lib.r2s_isect_workspace_bytes(n, 0, 0), dtype=torch.uint8, device=DEV)
+    rc = lib.r2s_isect_count_2d_f32(P(m2), P(radii), 1, 1, n, 16, 16, 16, P(counts), P(offsets),
+                                    P(ws), ws.numel(), torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib.r2s_last_error()
+    c = counts.cpu().numpy().astype(np.int64)
+    assert c.sum() > n
+    want = np.concatenate([[0], np.cumsum(c)])
+    assert np.array_equal(offsets.cpu().numpy(), want)
+
+
 def test_emission_order_backward_is_deterministic():
     d, m2, con, mu, op, ids, fl, off = _raster_case(3000, 9, 64, 64, 16, 2, torch.float32)
     v = torch.randn((2, 64, 64), generator=d["gen"]).to(DEV)
