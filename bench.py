@@ -523,7 +523,7 @@ def kernel_breakdown(proj: Projection, reps):
         v_img = proj.v_images[v % 4]
         n = int(fl.numel())
         counts.append(n)
-        rows = torch.empty(lib.r2s_rasterize_bwd_workspace_bytes(n, 4), dtype=torch.uint8,
+        rows = torch.empty(lib.r2s_rasterize_bwd_workspace_bytes(n, N_PROJ, 4), dtype=torch.uint8,
                            device=m2.device)
         outs = [torch.zeros_like(m2), torch.zeros_like(m2), torch.zeros_like(con),
                 torch.zeros_like(opc), torch.zeros_like(mu)]
@@ -537,9 +537,9 @@ def kernel_breakdown(proj: Projection, reps):
 
         def bwd_reduce():
             stream = torch.cuda.current_stream().cuda_stream
-            rc = lib.r2s_rasterize_bwd_reduce_f32(P(rows), P(emit_ids), n, 1, N_PROJ, P(outs[0]),
-                                                  P(outs[1]), P(outs[2]), P(outs[3]), P(outs[4]),
-                                                  stream)
+            rc = lib.r2s_rasterize_bwd_reduce_f32(P(rows), P(emit_ids), n, 1, N_PROJ, P(opc),
+                                                  P(mu), P(outs[0]), P(outs[1]), P(outs[2]),
+                                                  P(outs[3]), P(outs[4]), stream)
             assert rc == 0, lib.r2s_last_error()
 
         stages = {
@@ -971,9 +971,10 @@ def main():
     dom = max(single, key=single.get)
     n_pix = DET * DET
     dom_bytes = {
-        # list (key 8 + id 4) + payload 28 + partials 36 per record; v_image read
-        "rasterize_bwd_rows": 76 * i2_mean + 4 * n_pix,
-        "rasterize_bwd_reduce": 64 * i2_mean + 4 * i2_mean + 36 * N_PROJ,
+        # list (key 8 + id 4) + payload 28 + partials 32 per record; v_image read
+        "rasterize_bwd_rows": 72 * i2_mean + 4 * n_pix,
+        # rows 32 + emission id 4 per record; o, mu in, 36 B out per Gaussian
+        "rasterize_bwd_reduce": 36 * i2_mean + 44 * N_PROJ,
         "rasterize_fwd": 32 * i2_mean + 4 * n_pix,   # id 4 + payload 28; image write
         "project_fwd": 108 * N_PROJ,
         "prepare": 76 * N_PROJ,

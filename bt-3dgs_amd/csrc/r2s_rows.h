@@ -15,9 +15,15 @@
 
 namespace r2s {
 
-// Values per row: 48 bytes (float) / 96 (double), three 16-byte vectors; the
-// rasterizer stores 9 partials, the voxelizer 10.
-constexpr int kRowStride = 12;
+// Values per row: a row of up to 8 values takes 8 slots (32 bytes in float,
+// one 32-byte sector, so a row written at a scattered index costs one
+// sector), a longer one 12 (48 bytes, three 16-byte vectors).  The
+// rasterizer stores 8 values (6 without absolute gradients), the voxelizer
+// 10.
+template <int NV>
+constexpr int row_stride() {
+  return NV <= 8 ? 8 : 12;
+}
 
 template <typename T>
 struct Quad;
@@ -32,17 +38,17 @@ struct Quad<double> {
   static constexpr int n = 2;
 };
 
-// Rows start at multiples of 48 (float) / 96 (double) bytes from a
-// 16-byte-aligned workspace, so they are written and read as 16-byte vectors.
+// Rows start at multiples of the row size from a 16-byte-aligned
+// workspace, so they are written and read as 16-byte vectors.
 template <typename T, int NV>
 __device__ __forceinline__ void store_row(T *__restrict__ rows, int64_t e, const T (&v)[NV]) {
-  static_assert(NV <= kRowStride, "row too long");
+  static_assert(NV <= 12, "row too long");
   using Q = typename Quad<T>::type;
   constexpr int kq = Quad<T>::n, nq = (NV + kq - 1) / kq;
   T pad[nq * kq];
 #pragma unroll
   for (int c = 0; c < nq * kq; ++c) pad[c] = c < NV ? v[c] : static_cast<T>(0);
-  Q *dst = reinterpret_cast<Q *>(rows + e * kRowStride);
+  Q *dst = reinterpret_cast<Q *>(rows + e * row_stride<NV>());
 #pragma unroll
   for (int q = 0; q < nq; ++q) dst[q] = *reinterpret_cast<const Q *>(pad + q * kq);
 }
@@ -52,7 +58,7 @@ __device__ __forceinline__ void load_row(const T *__restrict__ rows, int64_t e, 
   using Q = typename Quad<T>::type;
   constexpr int kq = Quad<T>::n, nq = (NV + kq - 1) / kq;
   T pad[nq * kq];
-  const Q *src = reinterpret_cast<const Q *>(rows + e * kRowStride);
+  const Q *src = reinterpret_cast<const Q *>(rows + e * row_stride<NV>());
 #pragma unroll
   for (int q = 0; q < nq; ++q) *reinterpret_cast<Q *>(pad + q * kq) = src[q];
 #pragma unroll
@@ -95,28 +101,58 @@ inline bool vec_rows_ok(const T *base, uint32_t width, uint32_t ts) {
   return reinterpret_cast<uintptr_t>(base) % 16 == 0 && width % kq == 0 && ts % kq == 0;
 }
 
-// Destination of row value c: ptr[c][g * stride[c]].
+// Destinations of row value c for Gaussian g: ptr[c][g * stride[c]], times
+// scale[c][g] when scale[c] is set; and, when ptr2[c] is set, also
+// ptr2[c][g] = value * scale2[c][g] (one sum feeding two gradients, as the
+// rasterizer's opacity and mu partials do).
 template <typename T, int NV>
 struct RowTargets {
   T *ptr[NV];
   int stride[NV];
+  const T *scale[NV];
+  T *ptr2[NV];
+  const T *scale2[NV];
 };
 
-// Zeroes every target over ids [0, n_items): blockIdx.y is the column.
+// Every output array of a RowTargets as (pointer, stride) entries: the
+// ptr[c] columns, then the ptr2[c] columns (stride 1).
 template <typename T, int NV>
-__global__ __launch_bounds__(256) void zero_targets_kernel(RowTargets<T, NV> tg, int64_t n_items) {
-  const int64_t k = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (k < n_items) tg.ptr[blockIdx.y][k * tg.stride[blockIdx.y]] = static_cast<T>(0);
+struct TargetList {
+  T *ptr[2 * NV];
+  int stride[2 * NV];
+  int n;
+};
+
+template <typename T, int NV>
+inline TargetList<T, NV> target_list(const RowTargets<T, NV> &tg) {
+  TargetList<T, NV> tl{};
+  for (int c = 0; c < NV; ++c) {
+    tl.ptr[tl.n] = tg.ptr[c];
+    tl.stride[tl.n++] = tg.stride[c];
+  }
+  for (int c = 0; c < NV; ++c)
+    if (tg.ptr2[c] != nullptr) {
+      tl.ptr[tl.n] = tg.ptr2[c];
+      tl.stride[tl.n++] = 1;
+    }
+  return tl;
 }
 
-// The arrays under a RowTargets: each is covered by `stride` columns at
+// Zeroes every target over ids [0, n_items): blockIdx.y is the entry.
+template <typename T, int NV>
+__global__ __launch_bounds__(256) void zero_targets_kernel(TargetList<T, NV> tl, int64_t n_items) {
+  const int64_t k = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (k < n_items) tl.ptr[blockIdx.y][k * tl.stride[blockIdx.y]] = static_cast<T>(0);
+}
+
+// The arrays under a target list: each is covered by `stride` entries at
 // base, base + 1, ..., so zeroing the arrays contiguously zeroes every
 // target.  Zeroing them with 16-byte stores instead of one strided 4-byte
 // store per target halves the fill's time.
 template <typename T, int NV>
 struct FillArrays {
-  T *ptr[NV];
-  int64_t len[NV];
+  T *ptr[2 * NV];
+  int64_t len[2 * NV];
 };
 
 template <typename T, int NV>
@@ -138,21 +174,21 @@ __global__ __launch_bounds__(256) void fill_arrays_kernel(FillArrays<T, NV> fa) 
   }
 }
 
-// Splits the targets into their arrays: a column starts an array unless a
-// column of the same stride sits one element before it.  False when an
-// array is not 16-byte aligned (then the strided zeroing is used).
+// Splits a target list into its arrays: an entry starts an array unless an
+// entry of the same stride sits one element before it.  False when an array
+// is not 16-byte aligned (then the strided zeroing is used).
 template <typename T, int NV>
-inline bool target_arrays(const RowTargets<T, NV> &tg, int64_t n_items, FillArrays<T, NV> &fa,
+inline bool target_arrays(const TargetList<T, NV> &tl, int64_t n_items, FillArrays<T, NV> &fa,
                           int &n_arrays) {
   n_arrays = 0;
-  for (int c = 0; c < NV; ++c) {
+  for (int c = 0; c < tl.n; ++c) {
     bool start = true;
-    for (int d = 0; d < NV; ++d)
-      if (tg.stride[d] == tg.stride[c] && tg.ptr[d] + 1 == tg.ptr[c]) start = false;
+    for (int d = 0; d < tl.n; ++d)
+      if (tl.stride[d] == tl.stride[c] && tl.ptr[d] + 1 == tl.ptr[c]) start = false;
     if (!start) continue;
-    if (reinterpret_cast<uintptr_t>(tg.ptr[c]) % 16 != 0) return false;
-    fa.ptr[n_arrays] = tg.ptr[c];
-    fa.len[n_arrays] = static_cast<int64_t>(tg.stride[c]) * n_items;
+    if (reinterpret_cast<uintptr_t>(tl.ptr[c]) % 16 != 0) return false;
+    fa.ptr[n_arrays] = tl.ptr[c];
+    fa.len[n_arrays] = static_cast<int64_t>(tl.stride[c]) * n_items;
     ++n_arrays;
   }
   return true;
@@ -306,7 +342,10 @@ __global__ __launch_bounds__(256) void row_reduce_kernel(const T *__restrict__ r
     if (head) {
       const int64_t gi = g[k];
 #pragma unroll
-      for (int c = 0; c < NV; ++c) tg.ptr[c][gi * tg.stride[c]] = tot[c];
+      for (int c = 0; c < NV; ++c) {
+        tg.ptr[c][gi * tg.stride[c]] = tg.scale[c] != nullptr ? tot[c] * tg.scale[c][gi] : tot[c];
+        if (tg.ptr2[c] != nullptr) tg.ptr2[c][gi] = tot[c] * tg.scale2[c][gi];
+      }
     }
   }
 }
@@ -316,9 +355,10 @@ template <typename T, int NV>
 void launch_row_reduce(const T *rows, const int32_t *emit_ids, int64_t n, int64_t n_items,
                        const RowTargets<T, NV> &tg, hipStream_t stream) {
   if (n_items <= 0) return;
+  const TargetList<T, NV> tl = target_list(tg);
   FillArrays<T, NV> fa;
   int n_arrays = 0;
-  if (target_arrays(tg, n_items, fa, n_arrays)) {
+  if (target_arrays(tl, n_items, fa, n_arrays)) {
     int64_t longest = 0;
     for (int a = 0; a < n_arrays; ++a) longest = fa.len[a] > longest ? fa.len[a] : longest;
     const int64_t threads = ceil_div(longest, Quad<T>::n) + Quad<T>::n;
@@ -326,8 +366,9 @@ void launch_row_reduce(const T *rows, const int32_t *emit_ids, int64_t n, int64_
                                      static_cast<uint32_t>(n_arrays)),
                                 dim3(256), 0, stream>>>(fa);
   } else {
-    zero_targets_kernel<T, NV><<<dim3(static_cast<uint32_t>(ceil_div(n_items, 256)), NV),
-                                 dim3(256), 0, stream>>>(tg, n_items);
+    zero_targets_kernel<T, NV><<<dim3(static_cast<uint32_t>(ceil_div(n_items, 256)),
+                                      static_cast<uint32_t>(tl.n)),
+                                 dim3(256), 0, stream>>>(tl, n_items);
   }
   if (n <= 0) return;
   row_reduce_kernel<T, NV><<<dim3(static_cast<uint32_t>(ceil_div(n, 4 * kReduceWaveRows))),

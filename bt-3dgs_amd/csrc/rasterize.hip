@@ -327,6 +327,83 @@ __device__ __forceinline__ void load_raster_record(
   if (cu.ok && !index_range<T>(rec.my, -cu.hy, cu.hy, oy, y1, rec.i0, rec.i1)) rec.live = false;
 }
 
+// Per-(view, Gaussian) payload of the two-pass backward: what its rows pass
+// needs, packed as 8 values of T (32 bytes in float) -- mean, conic, o mu,
+// the alpha limit's bits and the culling half-height hy (negative when the
+// conic is not positive definite) -- so that a record's gather touches one
+// sector instead of four arrays' lines, and the per-record culling setup
+// runs once per Gaussian.  The rows need no o or mu apart from o mu: the
+// reduction forms the opacity and mu partials from T0.
+constexpr int kPayloadValues = 8;
+
+template <typename T>
+__global__ __launch_bounds__(256) void raster_pack_kernel(
+    const T *__restrict__ means2d, const T *__restrict__ conics, const T *__restrict__ opac,
+    const T *__restrict__ mus, int64_t n_items, T *__restrict__ payload) {
+  using V4 = typename Vec<T>::v4;
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (g >= n_items) return;
+  V4 p0, p1;
+  p0.x = means2d[2 * g];
+  p0.y = means2d[2 * g + 1];
+  p0.z = conics[3 * g];
+  p0.w = conics[3 * g + 1];
+  p1.x = conics[3 * g + 2];
+  p1.y = opac[g] * mus[g];
+  const bool fin = isfinite(p0.x) && isfinite(p0.y) && isfinite(p0.z) && isfinite(p0.w) &&
+                   isfinite(p1.x);
+  p1.z = limit_as_value(alpha_limit(p1.y, fin, kThr2));
+  const Cull2<T> cu = cull2_setup(p0.z, p0.w, p1.x, fabs(p1.y), kThr2);
+  p1.w = cu.ok ? cu.hy : static_cast<T>(-1);
+  V4 *dst = reinterpret_cast<V4 *>(payload + kPayloadValues * g);
+  dst[0] = p0;
+  dst[1] = p1;
+}
+
+// load_raster_record from the packed payload (o and mu are left zero).
+template <typename T>
+__device__ __forceinline__ void load_raster_record_packed(const T *__restrict__ payload,
+                                                          int64_t g, int64_t n_items, bool in_list,
+                                                          int oy, int y1, RasterRecord<T> &rec) {
+  using V4 = typename Vec<T>::v4;
+  rec.live = in_list && g >= 0 && g < n_items;
+  V4 p0, p1;
+  if (rec.live) {
+    const V4 *src = reinterpret_cast<const V4 *>(payload + kPayloadValues * g);
+    p0 = src[0];
+    p1 = src[1];
+  } else {
+    p0.x = p0.y = p0.z = p0.w = 0;
+    p1.x = p1.y = p1.z = p1.w = 0;
+  }
+  rec.o = rec.mu = 0;
+  rec.om = p1.y;
+  // |alpha| <= |o mu| for sigma >= 0: nothing passes (non-finite stays live).
+  if (fabs(rec.om) < static_cast<T>(kThr2)) rec.live = false;
+  if (!rec.live) {
+    rec.om = 0;
+    rec.mx = rec.my = rec.a = rec.b = rec.c = rec.ha = rec.hb = rec.hc = 0;
+    rec.lim = 0;
+    rec.i0 = 0;
+    rec.i1 = -1;
+    rec.pd = true;
+    return;
+  }
+  rec.mx = p0.x;
+  rec.my = p0.y;
+  rec.a = p0.z;
+  rec.b = p0.w;
+  rec.c = p1.x;
+  rec.ha = static_cast<T>(0.5 * kLog2e) * rec.a;
+  rec.hb = static_cast<T>(kLog2e) * rec.b;
+  rec.hc = static_cast<T>(0.5 * kLog2e) * rec.c;
+  rec.lim = bits_of(p1.z);
+  rec.pd = p1.w >= static_cast<T>(0);
+  rec.i0 = oy;
+  rec.i1 = y1;
+  if (rec.pd && !index_range<T>(rec.my, -p1.w, p1.w, oy, y1, rec.i0, rec.i1)) rec.live = false;
+}
+
 // Moments of one tile row for one record: s0 = sum w, s1 = sum w dx,
 // s2 = sum w dx^2 over the row's passing pixels (w = v exp(-sigma)), and
 // px, py = sums of |w (P d)_x|, |w (P d)_y|.  vv holds the row's upstream
@@ -536,7 +613,7 @@ __global__ __launch_bounds__(kBwdThreads) void raster_bwd_kernel(
     const T *__restrict__ v_image, uint32_t W, uint32_t H, uint32_t ts, uint32_t tw,
     uint32_t th, bool vec, T *__restrict__ v_xy_abs, T *__restrict__ v_xy,
     T *__restrict__ v_conic, T *__restrict__ v_opac, T *__restrict__ v_mu,
-    T *__restrict__ rows) {
+    T *__restrict__ rows, const T *__restrict__ payload) {
   // Consecutive blocks (neighbouring tiles, which share Gaussians) on one XCD.
   const int64_t rb =
       static_cast<int64_t>(xcd_swizzle(blockIdx.x, gridDim.x)) * kBwdThreads + 64 * wave_index();
@@ -562,7 +639,10 @@ __global__ __launch_bounds__(kBwdThreads) void raster_bwd_kernel(
   const int ny = min(nts, static_cast<int>(H) - oy);
   const T *__restrict__ vimg = v_image + static_cast<int64_t>(cam) * H * W;
   RasterRecord<T> rec;
-  load_raster_record(means2d, conics, opac, mus, g, n_items, key_ok, oy, oy + ny - 1, rec);
+  if (kRows)
+    load_raster_record_packed(payload, g, n_items, key_ok, oy, oy + ny - 1, rec);
+  else
+    load_raster_record(means2d, conics, opac, mus, g, n_items, key_ok, oy, oy + ny - 1, rec);
   const T dx0 = (static_cast<T>(ox) + static_cast<T>(0.5)) - rec.mx;
   const TileSums<T> s =
       raster_record_sums<T, R, kExact, kAbs>(rec, vimg, W, ox, oy, nx, nts, vec, dx0);
@@ -570,11 +650,14 @@ __global__ __launch_bounds__(kBwdThreads) void raster_bwd_kernel(
   T v[9];
   raster_partials<T, kAbs>(rec, s, v);
   if (kRows) {
+    // The opacity and mu partials are mu T0 and o T0: the row keeps T0 and
+    // the reduction scales its sum.
     if (kAbs) {
-      store_row(rows, isect_src[r], v);
+      const T r8[8] = {v[0], v[1], v[2], v[3], v[4], s.T0, v[7], v[8]};
+      store_row(rows, isect_src[r], r8);
     } else {
-      const T v7[7] = {v[0], v[1], v[2], v[3], v[4], v[5], v[6]};
-      store_row(rows, isect_src[r], v7);
+      const T r6[6] = {v[0], v[1], v[2], v[3], v[4], s.T0};
+      store_row(rows, isect_src[r], r6);
     }
     return;
   }
@@ -694,8 +777,7 @@ __device__ __forceinline__ TileSums<T> raster_tile_signed(const RasterRecord<T> 
 // an image whose rows allow 16-byte loads.
 template <typename T>
 __global__ __launch_bounds__(kSplitThreads) void raster_bwd_split_kernel(
-    const T *__restrict__ means2d, const T *__restrict__ conics, const T *__restrict__ opac,
-    const T *__restrict__ mus, const int32_t *__restrict__ tile_offsets,
+    const T *__restrict__ payload, const int32_t *__restrict__ tile_offsets,
     const int64_t *__restrict__ isect_ids, const int32_t *__restrict__ flatten_ids,
     const int32_t *__restrict__ isect_src, int64_t n_isects, uint32_t n_keys, int64_t n_items,
     const T *__restrict__ v_image, uint32_t W, uint32_t H, uint32_t tw, uint32_t th,
@@ -733,7 +815,7 @@ __global__ __launch_bounds__(kSplitThreads) void raster_bwd_split_kernel(
     const uint32_t ty = t / tw, tx = t - ty * tw;
     const int ox = static_cast<int>(tx) * R, oy = static_cast<int>(ty) * R;
     const int ny = min(R, static_cast<int>(H) - oy);
-    load_raster_record(means2d, conics, opac, mus, g, n_items, in_list, oy, oy + ny - 1, rec);
+    load_raster_record_packed(payload, g, n_items, in_list, oy, oy + ny - 1, rec);
     if (in_list && ox + R <= static_cast<int>(W) && ny == R) {
       const T dxa = (static_cast<T>(ox) + half) - rec.mx;
       const T dya = (static_cast<T>(oy) + half) - rec.my;
@@ -780,7 +862,8 @@ __global__ __launch_bounds__(kSplitThreads) void raster_bwd_split_kernel(
   if (!valid) return;
   T v[9];
   raster_partials<T, true>(rec, s, v);
-  store_row(rows, isect_src[rr], v);
+  const T r8[8] = {v[0], v[1], v[2], v[3], v[4], s.T0, v[7], v[8]};
+  store_row(rows, isect_src[rr], r8);
 }
 
 int check_raster_args(int64_t n_isects, int64_t C, int64_t N, uint32_t W, uint32_t H,
@@ -860,15 +943,15 @@ void launch_raster_bwd(const T *means2d, const T *conics, const T *opac, const T
                        const int32_t *flatten_ids, const int32_t *isect_src, int64_t n_isects,
                        uint32_t n_keys, int64_t n_items, const T *v_image, uint32_t W,
                        uint32_t H, uint32_t ts, uint32_t tw, uint32_t th, bool vec, T *v_xy_abs,
-                       T *v_xy, T *v_conic, T *v_opac, T *v_mu, T *rows, bool absgrad,
-                       hipStream_t stream) {
+                       T *v_xy, T *v_conic, T *v_opac, T *v_mu, T *rows, const T *payload,
+                       bool absgrad, hipStream_t stream) {
   const dim3 grid(static_cast<uint32_t>(ceil_div(n_isects, kBwdThreads)));
   const dim3 block(kBwdThreads);
 #define R2S_RASTER_BWD_LAUNCH(ABS, ROWS)                                                         \
   raster_bwd_kernel<T, R, kExact, ABS, ROWS><<<grid, block, 0, stream>>>(                      \
       means2d, conics, opac, mus, tile_offsets, isect_ids, flatten_ids, isect_src, n_isects,     \
       n_keys, n_items, v_image, W, H, ts, tw, th, vec, v_xy_abs, v_xy, v_conic, v_opac, v_mu,    \
-      rows)
+      rows, payload)
   if (v_xy_abs != nullptr || (rows != nullptr && absgrad)) {
     if (rows != nullptr)
       R2S_RASTER_BWD_LAUNCH(true, true);
@@ -883,31 +966,49 @@ void launch_raster_bwd(const T *means2d, const T *conics, const T *opac, const T
 #undef R2S_RASTER_BWD_LAUNCH
 }
 
+// Rows of the raster backward: v_xy (2), v_conic (3), T0 = sum of v e^-sigma
+// over the passing pixels, and, with absolute gradients, v_xy_abs (2).
+constexpr int kRasterRowValues = 8;
+
 int64_t raster_rows_bytes(int64_t n_isects, int dtype_bytes) {
-  return n_isects * kRowStride * static_cast<int64_t>(dtype_bytes);
+  return n_isects * row_stride<kRasterRowValues>() * static_cast<int64_t>(dtype_bytes);
 }
 
-// Second pass of the two-pass backward: per-Gaussian sums of the rows.
+// Workspace of the two-pass backward: the rows, then the packed payload of
+// the n_items (view, Gaussian) pairs.
+int64_t raster_bwd_ws_bytes(int64_t n_isects, int64_t n_items, int dtype_bytes) {
+  return raster_rows_bytes(n_isects, dtype_bytes) +
+         n_items * kPayloadValues * static_cast<int64_t>(dtype_bytes);
+}
+
+// Second pass of the two-pass backward: per-Gaussian sums of the rows, with
+// v_opac = mu sum(T0) and v_mu = o sum(T0).
 template <typename T>
 int raster_reduce_impl(const T *rows, const int32_t *emit_ids, int64_t n_isects, int64_t C,
-                       int64_t N, T *v_xy_abs, T *v_xy, T *v_conic, T *v_opac, T *v_mu,
-                       r2s_stream_t st) {
+                       int64_t N, const T *opac, const T *mus, T *v_xy_abs, T *v_xy,
+                       T *v_conic, T *v_opac, T *v_mu, r2s_stream_t st) {
   const char *name = "rasterize_to_pixels_bwd (row reduction)";
   R2S_REQUIRE(C >= 0 && N >= 0 && C * N <= kInt32Max && n_isects >= 0 && n_isects <= kInt32Max,
               "%s: bad size", name);
   if (C * N == 0) return R2S_OK;
   R2S_REQUIRE(v_xy && v_conic && v_opac && v_mu, "%s: null output", name);
-  R2S_REQUIRE(n_isects == 0 || (rows && emit_ids), "%s: null pointer", name);
+  R2S_REQUIRE(n_isects == 0 || (rows && emit_ids && opac && mus), "%s: null pointer", name);
   R2S_REQUIRE(reinterpret_cast<uintptr_t>(rows) % 16 == 0, "%s: rows not 16-byte aligned", name);
   hipStream_t stream = as_stream(st);
   if (v_xy_abs != nullptr) {
-    RowTargets<T, 9> tg = {{v_xy, v_xy + 1, v_conic, v_conic + 1, v_conic + 2, v_opac, v_mu,
-                            v_xy_abs, v_xy_abs + 1},
-                           {2, 2, 3, 3, 3, 1, 1, 2, 2}};
+    RowTargets<T, 8> tg = {{v_xy, v_xy + 1, v_conic, v_conic + 1, v_conic + 2, v_opac, v_xy_abs,
+                            v_xy_abs + 1},
+                           {2, 2, 3, 3, 3, 1, 2, 2},
+                           {nullptr, nullptr, nullptr, nullptr, nullptr, mus, nullptr, nullptr},
+                           {nullptr, nullptr, nullptr, nullptr, nullptr, v_mu, nullptr, nullptr},
+                           {nullptr, nullptr, nullptr, nullptr, nullptr, opac, nullptr, nullptr}};
     launch_row_reduce(rows, emit_ids, n_isects, C * N, tg, stream);
   } else {
-    RowTargets<T, 7> tg = {{v_xy, v_xy + 1, v_conic, v_conic + 1, v_conic + 2, v_opac, v_mu},
-                           {2, 2, 3, 3, 3, 1, 1}};
+    RowTargets<T, 6> tg = {{v_xy, v_xy + 1, v_conic, v_conic + 1, v_conic + 2, v_opac},
+                           {2, 2, 3, 3, 3, 1},
+                           {nullptr, nullptr, nullptr, nullptr, nullptr, mus},
+                           {nullptr, nullptr, nullptr, nullptr, nullptr, v_mu},
+                           {nullptr, nullptr, nullptr, nullptr, nullptr, opac}};
     launch_row_reduce(rows, emit_ids, n_isects, C * N, tg, stream);
   }
   return check_launch(name);
@@ -932,16 +1033,16 @@ int raster_bwd_impl(const T *means2d, const T *conics, const T *opac, const T *m
   if (C * N == 0) return R2S_OK;
   if (n_isects == 0) {  // the two-pass form still stores its (zero) outputs
     if (!two_pass || rows_only) return R2S_OK;
-    return raster_reduce_impl<T>(nullptr, nullptr, 0, C, N, v_xy_abs, v_xy, v_conic, v_opac,
-                                 v_mu, st);
+    return raster_reduce_impl<T>(nullptr, nullptr, 0, C, N, opac, mus, v_xy_abs, v_xy,
+                                 v_conic, v_opac, v_mu, st);
   }
   R2S_REQUIRE(tile_offsets && flatten_ids, "%s: null tile lists", name);
   R2S_REQUIRE(means2d && conics && opac && mus && v_image, "%s: null pointer", name);
   R2S_REQUIRE(rows_only || (v_xy && v_conic && v_opac && v_mu), "%s: null output", name);
-  T *rows = nullptr;
+  T *rows = nullptr, *payload = nullptr;
   if (two_pass) {
     R2S_REQUIRE(isect_src && (rows_only || emit_ids), "%s: null emit_ids / isect_src", name);
-    const int64_t need = raster_rows_bytes(n_isects, sizeof(T));
+    const int64_t need = raster_bwd_ws_bytes(n_isects, C * N, sizeof(T));
     if (ws == nullptr || static_cast<int64_t>(ws_bytes) < need) {
       set_error("%s: workspace of %zu bytes, %lld required", name, ws_bytes, (long long)need);
       return R2S_EWORKSPACE;
@@ -949,22 +1050,26 @@ int raster_bwd_impl(const T *means2d, const T *conics, const T *opac, const T *m
     R2S_REQUIRE(reinterpret_cast<uintptr_t>(ws) % 16 == 0, "%s: workspace not 16-byte aligned",
                 name);
     rows = static_cast<T *>(ws);
+    payload = rows + n_isects * row_stride<kRasterRowValues>();
   }
   const uint32_t n_keys = static_cast<uint32_t>(C) * tw * th;
   hipStream_t stream = as_stream(st);
+  if (two_pass)
+    raster_pack_kernel<T><<<dim3(static_cast<uint32_t>(ceil_div(C * N, 256))), dim3(256), 0,
+                            stream>>>(means2d, conics, opac, mus, C * N, payload);
   // 16-byte loads of gradient rows when every row segment starts aligned.
   const bool vec = vec_rows_ok<T>(v_image, W, ts);
 #define R2S_RASTER_BWD_R(RR, EXACT)                                                              \
   launch_raster_bwd<T, RR, EXACT>(means2d, conics, opac, mus, tile_offsets, isect_ids,           \
                                   flatten_ids, isect_src, n_isects, n_keys, C * N, v_image, W,   \
                                   H, ts, tw, th, vec, v_xy_abs, v_xy, v_conic, v_opac, v_mu,     \
-                                  rows, absgrad, stream)
+                                  rows, payload, absgrad, stream)
   const bool with_abs = v_xy_abs != nullptr || (rows != nullptr && absgrad);
   if (ts == 16 && vec && rows != nullptr && with_abs)
     raster_bwd_split_kernel<T>
         <<<dim3(static_cast<uint32_t>(ceil_div(n_isects, kSplitThreads))), dim3(kSplitThreads),
-           0, stream>>>(means2d, conics, opac, mus, tile_offsets, isect_ids, flatten_ids,
-                        isect_src, n_isects, n_keys, C * N, v_image, W, H, tw, th, rows);
+           0, stream>>>(payload, tile_offsets, isect_ids, flatten_ids, isect_src, n_isects,
+                        n_keys, C * N, v_image, W, H, tw, th, rows);
   else if (ts == 16)
     R2S_RASTER_BWD_R(16, true);
   else if (ts == 8)
@@ -978,8 +1083,8 @@ int raster_bwd_impl(const T *means2d, const T *conics, const T *opac, const T *m
 #undef R2S_RASTER_BWD_R
   R2S_RETURN_IF(check_launch(name));
   if (!two_pass || rows_only) return R2S_OK;
-  return raster_reduce_impl<T>(rows, emit_ids, n_isects, C, N, v_xy_abs, v_xy, v_conic, v_opac,
-                               v_mu, st);
+  return raster_reduce_impl<T>(rows, emit_ids, n_isects, C, N, opac, mus, v_xy_abs, v_xy,
+                               v_conic, v_opac, v_mu, st);
 }
 
 // Device address of `scratch` on the current device, looked up once per
@@ -1076,9 +1181,9 @@ R2S_RASTER_NOALLOC_API(f64, double)
 
 #undef R2S_RASTER_NOALLOC_API
 
-int64_t r2s_rasterize_bwd_workspace_bytes(int64_t n_isects, int dtype_bytes) {
-  if (n_isects <= 0 || (dtype_bytes != 4 && dtype_bytes != 8)) return 0;
-  return r2s::raster_rows_bytes(n_isects, dtype_bytes);
+int64_t r2s_rasterize_bwd_workspace_bytes(int64_t n_isects, int64_t n_items, int dtype_bytes) {
+  if (n_isects <= 0 || n_items < 0 || (dtype_bytes != 4 && dtype_bytes != 8)) return 0;
+  return r2s::raster_bwd_ws_bytes(n_isects, n_items, dtype_bytes);
 }
 
 int64_t r2s_rasterize_workspace_bytes(int64_t n_keys, int64_t n_isects, uint32_t tile_size,
@@ -1135,11 +1240,12 @@ int64_t r2s_rasterize_workspace_bytes(int64_t n_keys, int64_t n_isects, uint32_t
                                    nullptr, rows, rows_bytes, true, st, true, absgrad != 0);  \
   }                                                                                           \
   int r2s_rasterize_bwd_reduce_##SUF(const T *rows, const int32_t *emit_ids, int64_t n_isects, \
-                                     int64_t C, int64_t N, T *v_xy_abs, T *v_xy, T *v_conic,  \
-                                     T *v_opac, T *v_mu, r2s_stream_t st) {                   \
+                                     int64_t C, int64_t N, const T *opac, const T *mus,       \
+                                     T *v_xy_abs, T *v_xy, T *v_conic, T *v_opac, T *v_mu,    \
+                                     r2s_stream_t st) {                                       \
     r2s::clear_error();                                                                       \
-    return r2s::raster_reduce_impl<T>(rows, emit_ids, n_isects, C, N, v_xy_abs, v_xy,         \
-                                      v_conic, v_opac, v_mu, st);                             \
+    return r2s::raster_reduce_impl<T>(rows, emit_ids, n_isects, C, N, opac, mus, v_xy_abs,    \
+                                      v_xy, v_conic, v_opac, v_mu, st);                       \
   }
 
 R2S_RASTER_STAGE_API(f32, float)

@@ -961,7 +961,7 @@ void launch_voxel_bwd(const T *means3d, const T *conics, const T *opac,
 }
 
 int64_t voxel_rows_bytes(int64_t n_isects, int dtype_bytes) {
-  return n_isects * kRowStride * static_cast<int64_t>(dtype_bytes);
+  return n_isects * row_stride<10>() * static_cast<int64_t>(dtype_bytes);
 }
 
 // Second pass of the two-pass backward: per-Gaussian sums of the rows.

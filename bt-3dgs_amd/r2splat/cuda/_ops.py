@@ -880,8 +880,8 @@ def _raster_bwd(means2d, conics, opacities, mus, tile_offsets, isect_ids, flatte
     dev = means2d.device
     with torch.cuda.device(dev):
         if emit is not None:
-            ws = _workspace(_lib().r2s_rasterize_bwd_workspace_bytes(n_isects,
-                                                                     means2d.element_size()), dev)
+            ws = _workspace(_lib().r2s_rasterize_bwd_workspace_bytes(
+                n_isects, C * N, means2d.element_size()), dev)
             _call(f"r2s_rasterize_bwd_emit_{sfx}", _ptr(means2d), _ptr(conics), _ptr(opacities),
                   _ptr(mus), _ptr(tile_offsets), _ptr(isect_ids), _ptr(flatten_ids),
                   _ptr(emit[0]), _ptr(emit[1]), n_isects, _ptr(v_render), C, N, W, H, ts, tw,

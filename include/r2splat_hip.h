@@ -6,8 +6,9 @@
  * stream; nothing here allocates or frees device memory: scratch space is a
  * caller-provided workspace whose size is returned by the *_workspace_bytes
  * queries (r2s_rasterize_fwd_noalloc_* instead uses a fixed device array that
- * the library holds on each GPU until the process ends).  Every function returns R2S_OK (0) on success, otherwise a status
- * code; r2s_last_error() then holds a message for the calling thread.
+ * the library holds on each GPU until the process ends).  Every function
+ * returns R2S_OK (0) on success, otherwise a status code; r2s_last_error()
+ * then holds a message for the calling thread.
  *
  * Layouts follow the reference operators (row-major, contiguous):
  *   covariances are packed upper-triangular (00, 01, 02, 11, 12, 22);
@@ -406,9 +407,12 @@ int r2s_rasterize_bwd_f64(const double *means2d, const double *conics,
                           double *v_conics, double *v_opacities, double *v_mus,
                           r2s_stream_t stream);
 
-/* Workspace of r2s_rasterize_bwd_emit_*: one row of 12 values of
- * dtype_bytes per record. */
-int64_t r2s_rasterize_bwd_workspace_bytes(int64_t n_isects, int dtype_bytes);
+/* Workspace of r2s_rasterize_bwd_emit_* / _rows_* over n_isects records of
+ * n_items = C*N (view, Gaussian) pairs: one row of 8 values of dtype_bytes
+ * per record (32 bytes in float), then a packed payload of 8 values per
+ * pair. */
+int64_t r2s_rasterize_bwd_workspace_bytes(int64_t n_isects, int64_t n_items,
+                                          int dtype_bytes);
 
 /* The same VJP as r2s_rasterize_bwd_* (RasterizeToPixelsBwd.cu:77-480) in
  * two passes, without one device-scope atomic per record and partial: the
@@ -445,11 +449,15 @@ int r2s_rasterize_bwd_emit_f64(const double *means2d, const double *conics,
 
 /* The two passes of r2s_rasterize_bwd_emit_* as separate calls (for callers
  * that schedule or time them apart).  _rows: the first pass; writes the
- * per-record rows (12 values, 9 used with absgrad != 0, else 7) at their
- * emission index into `rows` (r2s_rasterize_bwd_workspace_bytes, 16-byte
- * aligned).  _reduce: the second pass; stores each Gaussian's sums, zero
- * for Gaussians without records (v_means2d_abs NULL exactly when the rows
- * were written with absgrad == 0).  No reference counterpart. */
+ * per-record rows at their emission index into `rows`
+ * (r2s_rasterize_bwd_workspace_bytes, 16-byte aligned): 8 values
+ * v_means2d (2), v_conics (3), T0 = sum of v exp(-sigma) over the record's
+ * passing pixels, v_means2d_abs (2) -- the last two zero with absgrad == 0.
+ * _reduce: the second pass; stores each Gaussian's sums, v_opacities =
+ * mus sum(T0) and v_mus = opacities sum(T0) (the record partials mu T0 and
+ * o T0, summed), zero for Gaussians without records (v_means2d_abs NULL
+ * exactly when the rows were written with absgrad == 0).  No reference
+ * counterpart. */
 int r2s_rasterize_bwd_rows_f32(const float *means2d, const float *conics,
                                const float *opacities, const float *mus,
                                const int32_t *tile_offsets, const int64_t *isect_ids,
@@ -467,11 +475,13 @@ int r2s_rasterize_bwd_rows_f64(const double *means2d, const double *conics,
                                uint32_t n_tiles_w, uint32_t n_tiles_h, int absgrad,
                                void *rows, size_t rows_bytes, r2s_stream_t stream);
 int r2s_rasterize_bwd_reduce_f32(const float *rows, const int32_t *emit_ids, int64_t n_isects,
-                                 int64_t C, int64_t N, float *v_means2d_abs, float *v_means2d,
+                                 int64_t C, int64_t N, const float *opacities,
+                                 const float *mus, float *v_means2d_abs, float *v_means2d,
                                  float *v_conics, float *v_opacities, float *v_mus,
                                  r2s_stream_t stream);
 int r2s_rasterize_bwd_reduce_f64(const double *rows, const int32_t *emit_ids,
                                  int64_t n_isects, int64_t C, int64_t N,
+                                 const double *opacities, const double *mus,
                                  double *v_means2d_abs, double *v_means2d, double *v_conics,
                                  double *v_opacities, double *v_mus, r2s_stream_t stream);
 

@@ -297,8 +297,15 @@ def check_parameter_gradients(got, args, raster_grads, voxel_grads=None):
 # their records as the two-pass backward kernels store them (one row per
 # record at its emission index), against oracle/native.py's *_records.
 
-RASTER_ROW = (2, 3, 4, 5, 6, 7, 8, 0, 1)  # oracle value index of row slot k
+# Oracle value index of row slot k.  The oracle's raster record values are
+# (abs x, abs y, v_xy x, v_xy y, conic 0..2, opacity, mu); the kernels' raster
+# row is (v_xy x, v_xy y, conic 0..2, T0, abs x, abs y) in 8 slots, the
+# opacity and mu partials being mu T0 and o T0.  Voxel rows: 12 slots, the
+# oracle's 10 values in order.
+RASTER_ROW = (2, 3, 4, 5, 6, None, 0, 1)
+RASTER_ROW_SLOTS = 8
 VOXEL_ROW = tuple(range(10))
+VOXEL_ROW_SLOTS = 12
 
 
 def sample_keys(tile_offsets, n_isects, n_sample, seed=0):
@@ -311,19 +318,21 @@ def sample_keys(tile_offsets, n_isects, n_sample, seed=0):
     return np.unique(np.append(pick, int(np.argmax(cnt))))
 
 
-def _row_values(rows_f32, src, rec, order):
-    r = np.asarray(rows_f32).reshape(-1, 12)[np.asarray(src)[rec]]
-    out = np.zeros((rec.size, len(order)), np.float32)
+def _row_values(rows_f32, src, rec, order, slots, n_values):
+    r = np.asarray(rows_f32).reshape(-1, slots)[np.asarray(src)[rec]]
+    out = np.zeros((rec.size, n_values), np.float64)
     for slot, j in enumerate(order):
-        out[:, j] = r[:, slot]
-    return out
+        if j is not None:
+            out[:, j] = r[:, slot]
+    return out, r
 
 
 def check_raster_sampled(m2, con, op, mu, off, fl, v_image, W, H, ts, keys, image=None,
                          rows=None, isect_src=None, tag=""):
     """assert_parity over the sampled tiles' pixels of ``image`` and over
-    their records' rows (``rows`` [n_isects * 12] float32 at emission index
-    ``isect_src``), all numpy float32."""
+    their records' rows (``rows`` [n_isects * 8] float32 at emission index
+    ``isect_src``; the opacity and mu partials formed as mu T0 and o T0 from
+    the row's T0), all numpy float32."""
     from oracle import native
 
     eta = ETA[np.dtype(np.float32)]
@@ -348,9 +357,13 @@ def check_raster_sampled(m2, con, op, mu, off, fl, v_image, W, H, ts, keys, imag
                                                  W, H, ts, keys, eta=eta)
         _, lv, _, _ = native.raster_records(*lo, off, fl, np.asarray(v_image, np.float32), W, H,
                                             ts, keys)
-        got = _row_values(rows, isect_src, rec, RASTER_ROW)
-        reps["records"] = assert_parity(got, val, lv, bd, f"{tag}record partials (sampled)",
-                                        mag=mg)
+        got, r = _row_values(rows, isect_src, rec, RASTER_ROW, RASTER_ROW_SLOTS, 9)
+        # Opacity and mu partials from the row's T0 (products in float64).
+        g = np.asarray(fl).reshape(-1)[rec].astype(np.int64)
+        got[:, 7] = hi[3].reshape(-1)[g] * r[:, 5]
+        got[:, 8] = hi[2].reshape(-1)[g] * r[:, 5]
+        reps["records"] = assert_parity(got.astype(np.float32), val, lv, bd,
+                                        f"{tag}record partials (sampled)", mag=mg)
         reps["records"]["records"] = int(rec.size)
     return reps
 
@@ -384,8 +397,8 @@ def check_voxel_sampled(m3, con, op, off, fl, v_volume, d2, d1, d0, ts, keys, vo
                                                 key_offset=key_offset)
         _, lv, _, _ = native.voxel_records(*lo, off, fl, np.asarray(v_volume, np.float32), d2, d1,
                                            d0, ts, keys, key_offset=key_offset)
-        got = _row_values(rows, isect_src, rec, VOXEL_ROW)
-        reps["records"] = assert_parity(got, val, lv, bd, f"{tag}record partials (sampled)",
-                                        mag=mg)
+        got, _ = _row_values(rows, isect_src, rec, VOXEL_ROW, VOXEL_ROW_SLOTS, 10)
+        reps["records"] = assert_parity(got.astype(np.float32), val, lv, bd,
+                                        f"{tag}record partials (sampled)", mag=mg)
         reps["records"]["records"] = int(rec.size)
     return reps

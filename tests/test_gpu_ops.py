@@ -638,22 +638,30 @@ def test_row_reduction_stores_every_id(seed):
     counts[::25] = torch.randint(60, 200, (counts[::25].numel(),), generator=g)
     emit_ids = torch.repeat_interleave(ids, counts).int()
     n = emit_ids.numel()
-    rows = torch.randint(-8, 9, (n, 12), generator=g).float()
-    want = torch.zeros(N, 12).index_add_(0, emit_ids.long(), rows)
+    # Rows (v_xy 2, v_conic 3, T0, v_xy_abs 2); small integers and integer
+    # opacities / mus, so the sums and the T0 products are exact.
+    rows = torch.randint(-8, 9, (n, 8), generator=g).float()
+    sums = torch.zeros(N, 8).index_add_(0, emit_ids.long(), rows)
+    opac = torch.randint(1, 5, (1, N), generator=g).float()
+    mus = torch.randint(1, 5, (1, N), generator=g).float()
+    want = torch.cat([sums[:, :5], mus.reshape(N, 1) * sums[:, 5:6],
+                      opac.reshape(N, 1) * sums[:, 5:6], sums[:, 6:8]], 1)
     outs = [torch.full((1, N, k), float("nan"), device=DEV) for k in (2, 3)]
     outs += [torch.full((1, N), float("nan"), device=DEV) for _ in range(2)]
     outs.insert(0, torch.full((1, N, 2), float("nan"), device=DEV))  # absgrad
     rows_d, emit_d = rows.to(DEV), emit_ids.to(DEV)
-    assert lib.r2s_rasterize_bwd_reduce_f32(P(rows_d), P(emit_d), n, 1, N,
+    op_d, mu_d = opac.to(DEV), mus.to(DEV)
+    assert lib.r2s_rasterize_bwd_reduce_f32(P(rows_d), P(emit_d), n, 1, N, P(op_d), P(mu_d),
                                             *[P(t) for t in outs], st) == 0
     v_abs, v_xy, v_con, v_op, v_mu = (t.cpu().reshape(N, -1) for t in outs)
     got = torch.cat([v_xy, v_con, v_op, v_mu, v_abs], 1)
-    assert torch.equal(got, want[:, :9])
+    assert torch.equal(got, want)
     assert int(emit_ids[0]) > 0 and int(emit_ids[-1]) < N - 1
     # No records at all: every output is still stored (zeros).
     for t in outs:
         t.fill_(float("nan"))
-    assert lib.r2s_rasterize_bwd_reduce_f32(None, None, 0, 1, N, *[P(t) for t in outs], st) == 0
+    assert lib.r2s_rasterize_bwd_reduce_f32(None, None, 0, 1, N, None, None,
+                                            *[P(t) for t in outs], st) == 0
     assert all(int(torch.count_nonzero(t)) == 0 for t in outs)
 
 
@@ -668,15 +676,15 @@ def test_backward_stage_entry_points_match_the_two_pass_op():
                                                   True)
     emit_ids, src = _ops.emission_order(fl, off.numel())
     n, N = fl.numel(), m2.shape[1]
-    rows = torch.empty(lib.r2s_rasterize_bwd_workspace_bytes(n, 4), dtype=torch.uint8,
+    rows = torch.empty(lib.r2s_rasterize_bwd_workspace_bytes(n, 2 * N, 4), dtype=torch.uint8,
                        device=DEV)
     assert lib.r2s_rasterize_bwd_rows_f32(P(m2), P(con), P(op), P(mu), P(off), P(ids), P(fl),
                                           P(src), n, P(v), 2, N, 64, 48, 16, 4, 3, 1, P(rows),
                                           rows.numel(), st) == 0
     # NaN on entry: the reduction stores every output, zero without records.
     got = [torch.full_like(t, float("nan")) for t in want]
-    assert lib.r2s_rasterize_bwd_reduce_f32(P(rows), P(emit_ids), n, 2, N, *[P(t) for t in got],
-                                            st) == 0
+    assert lib.r2s_rasterize_bwd_reduce_f32(P(rows), P(emit_ids), n, 2, N, P(op), P(mu),
+                                            *[P(t) for t in got], st) == 0
     for a, b in zip(got, want):
         assert torch.equal(a, b)
     untouched = torch.ones(2 * N, dtype=torch.bool, device=DEV)

@@ -16,7 +16,8 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import (check_voxel, check_voxel_sampled, np32, sample_keys, voxel_references)
+from helpers import (VOXEL_ROW_SLOTS, check_voxel, check_voxel_sampled, np32, sample_keys,
+                     voxel_references)
 from oracle import binning
 from r2splat import scenes
 from r2splat.cuda import _backend, _ops
@@ -171,7 +172,7 @@ def test_config5_512_volume_with_needles_in_slabs():
         o = np32(off).reshape(-1).astype(np.int64)
         pos = np.concatenate([np.arange(o[k], o[k + 1] if k + 1 < o.size else n) for k in keys])
         src = lists.isect_src[torch.from_numpy(pos).to(DEV)].long()
-        sub = rows.view(-1, 12)[src].cpu().numpy()
+        sub = rows.view(-1, VOXEL_ROW_SLOTS)[src].cpu().numpy()
         del rows
         lookup = np.full(n, -1, np.int64)
         lookup[pos] = np.arange(pos.size)

@@ -23,7 +23,8 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import check_raster_sampled, check_voxel_sampled, np32, sample_keys
+from helpers import (RASTER_ROW_SLOTS, VOXEL_ROW_SLOTS, check_raster_sampled, check_voxel_sampled,
+                     np32, sample_keys)
 from oracle import binning
 from r2splat import geometry, scenes
 from r2splat.cuda import _backend, _ops
@@ -73,7 +74,7 @@ def _project(d):
 def _raster_rows(m2, con, op, mu, off, lists, v, W_, H_, ts):
     lib, P = _backend.library(), _ops._ptr
     n, C, N = lists.flatten_ids.numel(), m2.shape[0], m2.shape[1]
-    rows = torch.empty(lib.r2s_rasterize_bwd_workspace_bytes(n, 4), dtype=torch.uint8,
+    rows = torch.empty(lib.r2s_rasterize_bwd_workspace_bytes(n, C * N, 4), dtype=torch.uint8,
                        device=DEV)
     tw, th = off.shape[2], off.shape[1]
     rc = lib.r2s_rasterize_bwd_rows_f32(P(m2), P(con), P(op), P(mu), P(off), P(lists.isect_ids),
@@ -84,14 +85,14 @@ def _raster_rows(m2, con, op, mu, off, lists, v, W_, H_, ts):
     return rows.view(torch.float32)
 
 
-def _sampled_rows(rows, lists, keys, off):
+def _sampled_rows(rows, lists, keys, off, slots):
     """Rows of the sampled tiles' records only (the whole table is GBs):
-    (rows [n_sampled * 12], index of each list position's row in them)."""
+    (rows [n_sampled * slots], index of each list position's row in them)."""
     o = np32(off).reshape(-1).astype(np.int64)
     n = lists.flatten_ids.numel()
     pos = np.concatenate([np.arange(o[k], o[k + 1] if k + 1 < o.size else n) for k in keys])
     src = lists.isect_src[torch.from_numpy(pos).to(DEV)].long()
-    sub = rows.view(-1, 12)[src].cpu().numpy()
+    sub = rows.view(-1, slots)[src].cpu().numpy()
     lookup = np.full(n, -1, np.int64)
     lookup[pos] = np.arange(pos.size)
     return sub.reshape(-1), lookup
@@ -118,7 +119,7 @@ def test_config5_projection_lists_render_and_backward(config5):
     v = torch.randn((1, DET5, DET5), generator=config5["g"]).to(DEV)
     rows = _raster_rows(m2, con, op, mu, off, lists, v, DET5, DET5, 16)
     keys = sample_keys(np32(off), n, 24, seed=5)
-    table, lookup = _sampled_rows(rows, lists, keys, off)
+    table, lookup = _sampled_rows(rows, lists, keys, off, RASTER_ROW_SLOTS)
     del rows
     reps = check_raster_sampled(np32(m2), np32(con), np32(op), np32(mu), np32(off), np32(fl),
                                 np32(v), DET5, DET5, 16, keys, image=np32(img), rows=table,
@@ -167,7 +168,7 @@ def test_config5_voxel_lists_volume_and_backward():
     v = torch.randn((VOX5, VOX5, VOX5), generator=d["g"]).to(DEV)
     rows = _voxel_rows(m3, con, d["opac"], off, lists, v, nb)
     keys = sample_keys(np32(off), n, 24, seed=6)
-    table, lookup = _sampled_rows(rows, lists, keys, off)
+    table, lookup = _sampled_rows(rows, lists, keys, off, VOXEL_ROW_SLOTS)
     del rows
     reps = check_voxel_sampled(np32(m3), np32(con), np32(d["opac"]), np32(off), np32(fl),
                                np32(v), VOX5, VOX5, VOX5, 8, keys, volume=np32(vol), rows=table,
