@@ -189,18 +189,64 @@ __global__ void layer_prefix_kernel(const unsigned long long *__restrict__ diff,
 
 // ---------------------------------------------------------------- emit ---
 
-// Lane (of the calling wave) owning output t of a wave whose lanes emit
-// excl[j] .. excl[j] + cnt[j] - 1: the largest j with excl[j] <= t (a lane
-// with cnt > 0, as zero-count lanes share the excl of the next lane).
-__device__ __forceinline__ uint32_t owner_lane(uint32_t excl, uint32_t t) {
-  uint32_t lo = 0;
-#pragma unroll
-  for (uint32_t step = 32; step > 0; step >>= 1) {
-    const uint32_t cand = lo + step;
-    const uint32_t e = static_cast<uint32_t>(__shfl(static_cast<int>(excl), static_cast<int>(cand & 63u), 64));
-    if (cand < 64u && e <= t) lo = cand;
+// Inclusive prefix maximum over the lanes of a wave: DPP row shifts by 1,
+// 2, 4, 8 within each row of 16 lanes, then the row broadcasts of lanes 15
+// and 31 (VALU only, no LDS round trip).  -1 is the identity (every value
+// is >= -1).
+__device__ __forceinline__ int wave_prefix_max(int v) {
+  v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x111, 0xf, 0xf, false));  // row_shr:1
+  v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x112, 0xf, 0xf, false));  // row_shr:2
+  v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x114, 0xf, 0xf, false));  // row_shr:4
+  v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x118, 0xf, 0xf, false));  // row_shr:8
+  v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x142, 0xa, 0xf, false));  // row_bcast:15
+  v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x143, 0xc, 0xf, false));  // row_bcast:31
+  return v;
+}
+
+// Owners of one round of a wave's emission: the lanes emit excl[j] ..
+// excl[j] + cnt[j] - 1, and output t0 + lane belongs to the largest j with
+// cnt[j] > 0 and excl[j] <= t0 + lane.  Each lane whose run starts inside the
+// round (`starts`, at rel = excl - t0) marks its start in `own` (tagged with
+// the round, so older marks read as absent), a prefix maximum over the lanes
+// carries each mark forward, and `carry` (the owner of the previous round's
+// last output) covers outputs before the round's first start.  Returns the
+// owner and updates carry (uniform).
+__device__ __forceinline__ int round_owner(uint32_t *own, bool starts, uint32_t rel,
+                                           uint32_t round, int &carry) {
+  const uint32_t lane = lane_id();
+  if (starts) own[rel] = (round << 6) | lane;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const uint32_t m = own[lane];
+  const int mark = (m >> 6) == round ? static_cast<int>(m & 63u) : -1;
+  const int o = max(wave_prefix_max(mark), carry);
+  carry = __builtin_amdgcn_readlane(o, 63);
+  return max(o, 0);
+}
+
+// Lane 63's copy of v, in every lane.
+__device__ __forceinline__ uint32_t from_lane63(uint32_t v) { return readlane_u32(v, 63); }
+__device__ __forceinline__ double from_lane63(double v) {
+  return __longlong_as_double(readlane_i64(__double_as_longlong(v), 63));
+}
+
+// q = n / d and n - q d for d >= 1 from a double reciprocal of d: one
+// multiply instead of an integer division.  The product is within 2^-20 of
+// n / d for n < 2^32 (two roundings of 2^-53), so the truncated quotient is
+// at most one off, and the remainder corrects it.
+__device__ __forceinline__ uint32_t div_rcp(uint32_t n, uint32_t d, double rcp, uint32_t &rem) {
+  uint32_t q = static_cast<uint32_t>(static_cast<double>(n) * rcp);
+  int64_t r = static_cast<int64_t>(n) - static_cast<int64_t>(q) * d;
+  if (r < 0) {
+    --q;
+    r += d;
+  } else if (r >= static_cast<int64_t>(d)) {
+    ++q;
+    r -= d;
   }
-  return lo;
+  rem = static_cast<uint32_t>(r);
+  return q;
 }
 
 // Writes emitted record e: its key and its flat id (the emission-order id
@@ -220,9 +266,13 @@ __global__ __launch_bounds__(256) void emit_2d_kernel(
     const T *__restrict__ means2d, const int32_t *__restrict__ radii, int rect, int64_t M,
     int64_t N, uint32_t ts, uint32_t tw, uint32_t th, const int64_t *__restrict__ offsets,
     int64_t cap, uint32_t *__restrict__ keys, uint32_t *__restrict__ gids) {
-  const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + 64 * wave_index();
+  __shared__ uint32_t s_own[4][64];
+  __shared__ uint4 s_item[4][64];  // excl, width, first key
+  __shared__ double s_rcp[4][64];  // 1 / width
+  const uint32_t w = wave_index(), lane = lane_id();
+  const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + 64 * w;
   if (wave_first >= M || offsets[M] > cap) return;  // uniform per wave
-  const int64_t idx = wave_first + lane_id();
+  const int64_t idx = wave_first + lane;
   Rect r = {0, 0, 0, 0};
   uint32_t cnt = 0;
   if (idx < M) cnt = rect_2d(means2d, radii, rect, idx, ts, tw, th, r);
@@ -230,23 +280,35 @@ __global__ __launch_bounds__(256) void emit_2d_kernel(
   const uint32_t excl = incl - cnt;
   const uint32_t total = readlane_u32(incl, 63);
   const int64_t base = offsets[wave_first];
-  const uint32_t width = r.x1 - r.x0;
-  const uint32_t n_tiles = tw * th;
-  // Uniform loop: every lane takes part in the shuffles (a lane past the end
-  // works on the last record and stores nothing).
-  for (uint32_t t0 = 0; t0 < total; t0 += 64) {
-    const uint32_t t = min(t0 + lane_id(), total - 1);
-    const uint32_t j = owner_lane(excl, t);
-    const int jj = static_cast<int>(j);
-    const uint32_t k = t - static_cast<uint32_t>(__shfl(static_cast<int>(excl), jj, 64));
-    const uint32_t wj = static_cast<uint32_t>(__shfl(static_cast<int>(width), jj, 64));
-    const uint32_t x0 = static_cast<uint32_t>(__shfl(static_cast<int>(r.x0), jj, 64));
-    const uint32_t y0 = static_cast<uint32_t>(__shfl(static_cast<int>(r.y0), jj, 64));
-    const uint32_t row = k / wj, col = k - row * wj;
-    const int64_t gid = wave_first + j;
-    const uint32_t key = static_cast<uint32_t>(gid / N) * n_tiles + (y0 + row) * tw + (x0 + col);
-    if (t0 + lane_id() < total)
-      put_record(keys, gids, base + t, key, static_cast<uint32_t>(gid));
+  // Per item once: the key of its rectangle's first tile and 1 / width, so
+  // that a record costs a multiply instead of two integer divisions.
+  const uint32_t width = max(r.x1 - r.x0, 1u);
+  const uint32_t kb = idx < M ? static_cast<uint32_t>(idx / N) * (tw * th) + r.y0 * tw + r.x0 : 0u;
+  s_item[w][lane] = make_uint4(excl, width, kb, 0u);
+  s_rcp[w][lane] = 1.0 / static_cast<double>(width);
+  s_own[w][lane] = 0xffffffffu;  // no round's tag
+  int carry = -1, o = 0;
+  uint4 it = s_item[w][lane];
+  double rc = s_rcp[w][lane];
+  for (uint32_t t0 = 0, round = 0; t0 < total; t0 += 64, ++round) {
+    const uint32_t rel = excl - t0;  // wraps for runs starting before the round
+    const bool starts = cnt > 0u && rel < 64u;
+    if (ballot(starts) == 0ull) {
+      // The round lies inside the run holding the previous round's last
+      // output (never the first round: its first output starts a run).
+      o = carry;
+      it = make_uint4(from_lane63(it.x), from_lane63(it.y), from_lane63(it.z), 0u);
+      rc = from_lane63(rc);
+    } else {
+      o = round_owner(s_own[w], starts, rel, round, carry);
+      it = s_item[w][o];
+      rc = s_rcp[w][o];
+    }
+    const uint32_t t = t0 + lane;
+    uint32_t col;
+    const uint32_t row = div_rcp(t - it.x, it.y, rc, col);
+    if (t < total)
+      put_record(keys, gids, base + t, it.z + row * tw + col, static_cast<uint32_t>(wave_first + o));
   }
 }
 
@@ -257,9 +319,13 @@ __global__ __launch_bounds__(256) void emit_3d_kernel(
     uint32_t n2, uint32_t n1, uint32_t n0, uint32_t z0, uint32_t z1,
     const int64_t *__restrict__ offsets, int64_t cap, uint32_t *__restrict__ keys,
     uint32_t *__restrict__ gids) {
-  const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + 64 * wave_index();
+  __shared__ uint32_t s_own[4][64];
+  __shared__ uint4 s_item[4][64];     // excl, extent along dim2, plane, first key
+  __shared__ double2 s_rcp[4][64];    // 1 / plane, 1 / extent along dim2
+  const uint32_t w = wave_index(), lane = lane_id();
+  const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + 64 * w;
   if (wave_first >= N || offsets[N] > cap) return;  // uniform per wave
-  const int64_t idx = wave_first + lane_id();
+  const int64_t idx = wave_first + lane;
   const uint32_t n[3] = {n2, n1, n0};
   Box b;
   uint32_t cnt = 0;
@@ -273,25 +339,39 @@ __global__ __launch_bounds__(256) void emit_3d_kernel(
   const uint32_t excl = incl - cnt;
   const uint32_t total = readlane_u32(incl, 63);
   const int64_t base = offsets[wave_first];
-  const uint32_t e2 = b.hi[0] - b.lo[0], e1 = b.hi[1] - b.lo[1];
-  // Uniform loop: every lane takes part in the shuffles (a lane past the end
-  // works on the last record and stores nothing).
-  for (uint32_t t0 = 0; t0 < total; t0 += 64) {
-    const uint32_t t = min(t0 + lane_id(), total - 1);
-    const uint32_t j = owner_lane(excl, t);
-    const int jj = static_cast<int>(j);
-    const uint32_t k = t - static_cast<uint32_t>(__shfl(static_cast<int>(excl), jj, 64));
-    const uint32_t e2j = static_cast<uint32_t>(__shfl(static_cast<int>(e2), jj, 64));
-    const uint32_t e1j = static_cast<uint32_t>(__shfl(static_cast<int>(e1), jj, 64));
-    const uint32_t l2 = static_cast<uint32_t>(__shfl(static_cast<int>(b.lo[0]), jj, 64));
-    const uint32_t l1 = static_cast<uint32_t>(__shfl(static_cast<int>(b.lo[1]), jj, 64));
-    const uint32_t l0 = static_cast<uint32_t>(__shfl(static_cast<int>(b.lo[2]), jj, 64));
-    const uint32_t plane = e2j * e1j;
-    const uint32_t tz = k / plane, rem = k - tz * plane;
-    const uint32_t ty = rem / e2j, tx = rem - ty * e2j;
-    const uint32_t key = (l0 - z0 + tz) * (n1 * n2) + (l1 + ty) * n2 + (l2 + tx);
-    if (t0 + lane_id() < total)
-      put_record(keys, gids, base + t, key, static_cast<uint32_t>(wave_first + j));
+  // Per item once: the key of its box's first brick and the reciprocals of
+  // its extents, so that a record costs two multiplies instead of two
+  // integer divisions.
+  const uint32_t e2 = max(b.hi[0] - b.lo[0], 1u), e1 = max(b.hi[1] - b.lo[1], 1u);
+  const uint32_t plane = e2 * e1;
+  s_item[w][lane] = make_uint4(excl, e2, plane, (b.lo[2] - z0) * (n1 * n2) + b.lo[1] * n2 + b.lo[0]);
+  s_rcp[w][lane] = make_double2(1.0 / static_cast<double>(plane), 1.0 / static_cast<double>(e2));
+  s_own[w][lane] = 0xffffffffu;  // no round's tag
+  int carry = -1, o = 0;
+  uint4 it = s_item[w][lane];
+  double2 rc = s_rcp[w][lane];
+  for (uint32_t t0 = 0, round = 0; t0 < total; t0 += 64, ++round) {
+    const uint32_t rel = excl - t0;  // wraps for runs starting before the round
+    const bool starts = cnt > 0u && rel < 64u;
+    if (ballot(starts) == 0ull) {
+      // The round lies inside the run holding the previous round's last
+      // output (never the first round: its first output starts a run).
+      o = carry;
+      it = make_uint4(from_lane63(it.x), from_lane63(it.y), from_lane63(it.z),
+                      from_lane63(it.w));
+      rc = make_double2(from_lane63(rc.x), from_lane63(rc.y));
+    } else {
+      o = round_owner(s_own[w], starts, rel, round, carry);
+      it = s_item[w][o];
+      rc = s_rcp[w][o];
+    }
+    const uint32_t t = t0 + lane;
+    uint32_t rem, tx;
+    const uint32_t tz = div_rcp(t - it.x, it.z, rc.x, rem);
+    const uint32_t ty = div_rcp(rem, it.y, rc.y, tx);
+    if (t < total)
+      put_record(keys, gids, base + t, it.w + tz * (n1 * n2) + ty * n2 + tx,
+                 static_cast<uint32_t>(wave_first + o));
   }
 }
 
