@@ -198,12 +198,16 @@ inline bool target_arrays(const TargetList<T, NV> &tl, int64_t n_items, FillArra
 constexpr int kReduceRowsPerLane = 4;
 constexpr int kReduceWaveRows = 64 * kReduceRowsPerLane;
 
-// LDS slot of wave-row q (0..255) in the transposed staging: lane l reads
-// rows 4l .. 4l+3 from slots k*64 + ((l + 8k) mod 64), and lane l of load
-// round r writes row 64r + l; with the rotation by 8k both the writes and
-// the reads of each half-wave hit 32 different banks.
+// The transpose goes through LDS in two phases of 128 rows (load rounds 0-1
+// to lanes 0-31, then rounds 2-3 to lanes 32-63), which halves the staging
+// buffer: the kernel waits on memory, and the smaller buffer lets twice as
+// many waves be resident.  LDS slot of phase-row q (0..127): lane l of the
+// half reads rows 4l .. 4l+3 from slots k*32 + ((l + 8k) mod 32), and lane l
+// of load round r writes row 64r + l; with the rotation by 8k both the
+// writes and the reads of each half-wave hit 32 different banks.
+constexpr int kReduceStage = kReduceWaveRows / 2;
 __device__ __forceinline__ uint32_t reduce_slot(uint32_t q) {
-  return (q & 3u) * 64u + (((q >> 2) + 8u * (q & 3u)) & 63u);
+  return (q & 3u) * 32u + (((q >> 2) + 8u * (q & 3u)) & 31u);
 }
 
 // One wave per kReduceWaveRows consecutive rows (emission order), read with
@@ -224,50 +228,57 @@ __global__ __launch_bounds__(256) void row_reduce_kernel(const T *__restrict__ r
                                                          int64_t n, int64_t n_items,
                                                          RowTargets<T, NV> tg) {
   constexpr int K = kReduceRowsPerLane;
-  __shared__ T s_val[4][NV][kReduceWaveRows];
-  __shared__ int32_t s_seg[4][kReduceWaveRows];
+  __shared__ T s_val[4][NV][kReduceStage];
+  __shared__ int32_t s_seg[4][kReduceStage];
   const uint32_t w = wave_index(), lane = lane_id();
   const int64_t eb = (static_cast<int64_t>(blockIdx.x) * 4 + w) * kReduceWaveRows;
   if (eb >= n) return;  // uniform per wave; the waves share no barrier below
   // Segment id per row: the Gaussian, or a negative value unique to the row
   // slot for rows past the end (or with an id out of range).
-  {
-    int32_t sr[K];
-    T vr[K][NV];
+  int32_t sr[K];
+  T vr[K][NV];
 #pragma unroll
-    for (int r = 0; r < K; ++r) {
-      const uint32_t q = 64u * r + lane;
-      const int64_t e = eb + q;
-      const bool in = e < n;
-      const int64_t g = in ? static_cast<int64_t>(emit_ids[e]) : -1;
-      sr[r] = (g >= 0 && g < n_items) ? static_cast<int32_t>(g) : -1 - static_cast<int32_t>(q);
-      load_row(rows, in ? e : 0, vr[r]);
-      if (!in) {
+  for (int r = 0; r < K; ++r) {
+    const uint32_t q = 64u * r + lane;
+    const int64_t e = eb + q;
+    const bool in = e < n;
+    const int64_t g = in ? static_cast<int64_t>(emit_ids[e]) : -1;
+    sr[r] = (g >= 0 && g < n_items) ? static_cast<int32_t>(g) : -1 - static_cast<int32_t>(q);
+    load_row(rows, in ? e : 0, vr[r]);
+    if (!in) {
 #pragma unroll
-        for (int c = 0; c < NV; ++c) vr[r][c] = 0;
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < K; ++r) {
-      const uint32_t slot = reduce_slot(64u * r + lane);
-      s_seg[w][slot] = sr[r];
-#pragma unroll
-      for (int c = 0; c < NV; ++c) s_val[w][c][slot] = vr[r][c];
+      for (int c = 0; c < NV; ++c) vr[r][c] = 0;
     }
   }
-  // The wave's LDS operations complete in order, so its own lanes' writes
-  // are visible to the reads below; keep the compiler from moving them.
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   int32_t g[K];
   T v[K][NV];
 #pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const uint32_t slot = reduce_slot(K * lane + k);
-    g[k] = s_seg[w][slot];
+  for (int h = 0; h < 2; ++h) {
 #pragma unroll
-    for (int c = 0; c < NV; ++c) v[k][c] = s_val[w][c][slot];
+    for (int r = 0; r < 2; ++r) {
+      const uint32_t slot = reduce_slot(64u * r + lane);
+      s_seg[w][slot] = sr[2 * h + r];
+#pragma unroll
+      for (int c = 0; c < NV; ++c) s_val[w][c][slot] = vr[2 * h + r][c];
+    }
+    // The wave's LDS operations complete in order, so its own lanes' writes
+    // are visible to the reads below (and the reads precede the next
+    // phase's writes); keep the compiler from moving them.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if ((lane >> 5) == static_cast<uint32_t>(h)) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const uint32_t slot = reduce_slot(K * (lane & 31u) + k);
+        g[k] = s_seg[w][slot];
+#pragma unroll
+        for (int c = 0; c < NV; ++c) v[k][c] = s_val[w][c][slot];
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
   const int32_t before = (eb > 0) ? emit_ids[eb - 1] : -1;
   const int32_t seg_first = __shfl(g[0], 0, 64);
