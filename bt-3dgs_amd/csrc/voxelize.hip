@@ -347,9 +347,15 @@ __global__ __launch_bounds__(64) void voxel_fwd_reach_kernel(
   const T px0 = static_cast<T>(b.ok) + half;
   const int64_t start = tile_offsets[key];
   const int64_t end = (key == n_keys - 1) ? n_isects : static_cast<int64_t>(tile_offsets[key + 1]);
-  T acc[R];
+  T acc[R], px[R];
 #pragma unroll
-  for (int k = 0; k < R; ++k) acc[k] = 0;
+  for (int k = 0; k < R; ++k) {
+    acc[k] = 0;
+    // The voxel centres stay in registers (opaque to the compiler, which
+    // would otherwise recompute some of them at every walked record).
+    px[k] = px0 + static_cast<T>(k);
+    asm volatile("" : "+v"(px[k]));
+  }
   for (int64_t base = start; base < end; base += 64) {
     const int64_t idx = base + lane;
     const bool in = idx < end;
@@ -392,7 +398,7 @@ __global__ __launch_bounds__(64) void voxel_fwd_reach_kernel(
       const T C = (qh.w * dy + qr.x * dz) * dy + qr.y * dz * dz;
 #pragma unroll
       for (int k = 0; k < R; ++k) {
-        const T dx = (px0 + static_cast<T>(k)) - qa.x;
+        const T dx = px[k] - qa.x;
         const T sl = (qh.x * dx + B) * dx + C;
         const T e = neg_exp2(sl);
         acc[k] = fma(qa.w, alpha_pass(sl, lim) ? e : static_cast<T>(0), acc[k]);
