@@ -6,6 +6,8 @@
 // the reductions.
 #pragma once
 
+#include <type_traits>
+
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -99,15 +101,39 @@ __device__ __forceinline__ int64_t readlane_i64(int64_t v, uint32_t src) {
   return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
-// Wave64 inclusive prefix sum (Hillis-Steele over lane shuffles).
+// One DPP lane move of a 32- or 64-bit value (the halves moved
+// separately): lanes the move does not write (no source lane in the row, or
+// a row outside kRowMask) read 0.
+template <int kCtrl, int kRowMask, typename T>
+__device__ __forceinline__ T dpp_take(T v) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32- or 64-bit values");
+  if constexpr (sizeof(T) == 4) {
+    const int x = __builtin_bit_cast(int, v);
+    return __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, x, kCtrl, kRowMask, 0xf, false));
+  } else {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(u)), kCtrl,
+                                               kRowMask, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(u >> 32)),
+                                               kCtrl, kRowMask, 0xf, false);
+    return __builtin_bit_cast(T, (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
+                                     static_cast<uint32_t>(lo));
+  }
+}
+
+// Wave64 inclusive prefix sum of an integer, all lanes active: DPP row
+// shifts by 1, 2, 4, 8 within each row of 16 lanes (Hillis-Steele), then the
+// broadcasts of lane 15 into rows 1 and 3 and of lane 31 into rows 2 and 3.
+// VALU only: no LDS round trip per step.
 template <typename T>
 __device__ __forceinline__ T wave_inclusive_scan(T v) {
-  const uint32_t l = __lane_id();
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    T o = __shfl_up(v, off, 64);
-    if (l >= static_cast<uint32_t>(off)) v += o;
-  }
+  static_assert(std::is_integral<T>::value, "integer sums (the order is not the lane order)");
+  v += dpp_take<0x111, 0xf>(v);  // row_shr:1
+  v += dpp_take<0x112, 0xf>(v);  // row_shr:2
+  v += dpp_take<0x114, 0xf>(v);  // row_shr:4
+  v += dpp_take<0x118, 0xf>(v);  // row_shr:8
+  v += dpp_take<0x142, 0xa>(v);  // row_bcast:15
+  v += dpp_take<0x143, 0xc>(v);  // row_bcast:31
   return v;
 }
 
