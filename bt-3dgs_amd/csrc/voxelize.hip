@@ -316,17 +316,20 @@ __device__ __forceinline__ uint64_t reach_mask(const BwdRecord<T> &rec, const Br
   return reach;
 }
 
-// Forward at brick size 8 with culled rows.  One wave per brick; lane =
-// x-row (slice lane / 8, row lane % 8), its 8 voxels in registers.  Per
-// batch of 64 records of the brick's list, each lane loads one record and
-// the rows it reaches (reach_mask); 64 ballots hand each row's lane the set
-// of batch records that reach that row; each lane then walks its own set in
+// Forward at brick size 8 with culled rows.  S waves per brick; lane =
+// x-row (slice lane / 8, row lane % 8), its 8 voxels in registers.  Wave w
+// takes the batches of 64 records w, w + S, w + 2S, ... of the brick's list.
+// Per batch, each lane loads one record and the rows it reaches
+// (reach_mask); a 64 x 64 bit transpose hands each row's lane the set of
+// batch records that reach that row; each lane then walks its own set in
 // list order, so a record costs a row only where it can pass the alpha
-// test.  Every voxel still sums its records in list order, and the rows a
-// record does not reach would only add exact zeros, so the volume equals
-// voxel_fwd_kernel's bit for bit.
-template <typename T>
-__global__ __launch_bounds__(64) void voxel_fwd_reach_kernel(
+// test, and the rows a record does not reach would only add exact zeros.
+// With S = 1 every voxel sums its records in list order (the volume equals
+// voxel_fwd_kernel's bit for bit); with S > 1 (long lists: the host picks S
+// from the mean list length) the S partial bricks are added in wave order
+// through LDS, a fixed order.
+template <typename T, int S>
+__global__ __launch_bounds__(64 * S) void voxel_fwd_reach_kernel(
     const T *__restrict__ means3d, const T *__restrict__ conics, const T *__restrict__ opac,
     const int32_t *__restrict__ tile_offsets, const int32_t *__restrict__ flatten_ids,
     int64_t n_isects, uint32_t n_keys, uint32_t koff, int64_t N, uint32_t D2, uint32_t D1,
@@ -336,10 +339,12 @@ __global__ __launch_bounds__(64) void voxel_fwd_reach_kernel(
   // Per staged record {mx, my, mz, o}, {h0, h1, h2, h3}, {h4, h5, limit bits,
   // 0}: three vector reads per use; the 12-word stride spreads 8
   // consecutive records over all banks.
-  __shared__ V4 s_rec[64][3];
+  __shared__ V4 s_rec[S][64][3];
+  __shared__ T s_part[S > 1 ? S - 1 : 1][R][64];
   const uint32_t key = xcd_swizzle(blockIdx.x, n_keys);  // in the lists (koff: the grid's)
   const Brick b = brick_of(key + koff, n2, n1, R, D2, D1, D0);
   const int lane = static_cast<int>(lane_id());
+  const int w = S > 1 ? static_cast<int>(wave_index()) : 0;
   const int li = lane >> 3, lj = lane & 7;
   const T half = static_cast<T>(0.5);
   const T py = static_cast<T>(b.oj + lj) + half;
@@ -356,7 +361,7 @@ __global__ __launch_bounds__(64) void voxel_fwd_reach_kernel(
     px[k] = px0 + static_cast<T>(k);
     asm volatile("" : "+v"(px[k]));
   }
-  for (int64_t base = start; base < end; base += 64) {
+  for (int64_t base = start + 64 * w; base < end; base += 64 * S) {
     const int64_t idx = base + lane;
     const bool in = idx < end;
     const int64_t g = in ? static_cast<int64_t>(flatten_ids[idx]) : -1;
@@ -376,14 +381,21 @@ __global__ __launch_bounds__(64) void voxel_fwd_reach_kernel(
     hr.y = rec.h[5];
     hr.z = limit_as_value(rec.lim);
     hr.w = 0;
-    __syncthreads();  // the previous batch's reads are done
-    s_rec[lane][0] = a;
-    s_rec[lane][1] = hq;
-    s_rec[lane][2] = hr;
+    // The wave's LDS operations complete in order: the fences keep the
+    // compiler from moving this batch's writes above the previous batch's
+    // reads, or the reads below above the writes.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    s_rec[w][lane][0] = a;
+    s_rec[w][lane][1] = hq;
+    s_rec[w][lane][2] = hr;
     // Bit t of lane r's set: batch record t reaches row r.
     const uint64_t mine = transpose_bits64(reach, static_cast<uint32_t>(lane));
     uint32_t mine_lo = static_cast<uint32_t>(mine), mine_hi = static_cast<uint32_t>(mine >> 32);
-    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     while ((mine_lo | mine_hi) != 0u) {
       const bool low = mine_lo != 0u;
       const uint32_t word = low ? mine_lo : mine_hi;
@@ -391,7 +403,7 @@ __global__ __launch_bounds__(64) void voxel_fwd_reach_kernel(
       const uint32_t rest = word & (word - 1u);
       mine_lo = low ? rest : mine_lo;
       mine_hi = low ? mine_hi : rest;
-      const V4 qa = s_rec[t][0], qh = s_rec[t][1], qr = s_rec[t][2];
+      const V4 qa = s_rec[w][t][0], qh = s_rec[w][t][1], qr = s_rec[w][t][2];
       const typename Bits<T>::type lim = bits_of(qr.z);
       const T dy = py - qa.y, dz = pz - qa.z;
       const T B = qh.y * dy + qh.z * dz;
@@ -403,6 +415,21 @@ __global__ __launch_bounds__(64) void voxel_fwd_reach_kernel(
         const T e = neg_exp2(sl);
         acc[k] = fma(qa.w, alpha_pass(sl, lim) ? e : static_cast<T>(0), acc[k]);
       }
+    }
+  }
+  if constexpr (S > 1) {
+    // Waves 1 .. S-1 hand their partial bricks to wave 0, which adds them in
+    // wave order.
+    if (w > 0) {
+#pragma unroll
+      for (int k = 0; k < R; ++k) s_part[w - 1][k][lane] = acc[k];
+    }
+    __syncthreads();
+    if (w > 0) return;
+#pragma unroll
+    for (int ww = 0; ww < S - 1; ++ww) {
+#pragma unroll
+      for (int k = 0; k < R; ++k) acc[k] += s_part[ww][k][lane];
     }
   }
   if (li < b.ni && lj < b.nj) {
@@ -935,11 +962,24 @@ int voxel_fwd_impl(const T *means3d, const T *conics, const T *opac,
     return device_fill<T>(volume + i0 * plane, n_vox, static_cast<T>(0), stream, name);
   R2S_REQUIRE(means3d && conics && opac && tile_offsets && flatten_ids, "%s: null pointer", name);
   const uint32_t n_keys = n2 * n1 * n0, koff = z0 * n1 * n2;
-  if (ts == 8)
-    voxel_fwd_reach_kernel<T><<<dim3(n_keys), dim3(64), 0, stream>>>(
-        means3d, conics, opac, tile_offsets, flatten_ids, n_isects, n_keys, koff, N, D2, D1, D0,
-        n2, n1, volume);
-  else if (ts == 16)
+  if (ts == 8) {
+    // Waves per brick from the mean list length: one up to 192 records (3
+    // batches), then 2, then 4 from 384, so that long lists (large
+    // footprints, few bricks) are shared out.
+    const int64_t per_brick = n_isects / n_keys;
+    const dim3 grid(n_keys);
+#define R2S_VOXEL_FWD_REACH(S)                                                                  \
+  voxel_fwd_reach_kernel<T, S><<<grid, dim3(64 * S), 0, stream>>>(                              \
+      means3d, conics, opac, tile_offsets, flatten_ids, n_isects, n_keys, koff, N, D2, D1, D0,  \
+      n2, n1, volume)
+    if (per_brick < 192)
+      R2S_VOXEL_FWD_REACH(1);
+    else if (per_brick < 384)
+      R2S_VOXEL_FWD_REACH(2);
+    else
+      R2S_VOXEL_FWD_REACH(4);
+#undef R2S_VOXEL_FWD_REACH
+  } else if (ts == 16)
     launch_voxel_fwd<T, 16>(means3d, conics, opac, tile_offsets, flatten_ids, n_isects, n_keys,
                             koff, N, D2, D1, D0, ts, n2, n1, volume, stream);
   else
