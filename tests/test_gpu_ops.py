@@ -514,6 +514,21 @@ def test_voxelize_fwd_bwd(dtype, dims, ts, order):
             print(mode, n, r)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("n,band", [(4500, (192, 384)), (8000, (384, 10 ** 9))])
+def test_voxelize_fwd_long_lists(dtype, n, band):
+    """Brick lists long enough that the forward shares each brick between 2 (mean 192-383
+    records per brick) or 4 waves (384 and more) and adds their partial bricks in wave
+    order: the volume against the oracle at the usual bar."""
+    dims = (32, 32, 32)
+    d, m3, con, ids, fl, off = _voxel_case(n, 8, dims, 8, dtype)
+    mean = fl.numel() / 64
+    assert band[0] <= mean < band[1], mean
+    vol = W.voxelize_to_voxels_fwd(m3, con, d["opac"], off, fl, *dims, 8)
+    refs = voxel_references(np32(m3), np32(con), np32(d["opac"]), np32(off), np32(fl), *dims, 8)
+    print("volume", check_voxel(refs, volume=np32(vol)))
+
+
 def _voxel_row_reach(m3, con, op, ids, fl, dims, ts):
     """Rows (of 64) of its brick that each record's alpha-test ellipsoid reaches."""
     d2, d1, d0 = dims
