@@ -265,6 +265,18 @@ class Voxelization:
         self.last = (m3, con, off, ids, fl, vol)
         return vol
 
+    def step_ops(self):
+        """The same voxelization through r2splat.ops (VolumePass: mapping, binning, the
+        forward with its per-record reach masks, and the backward that reuses them)."""
+        from r2splat.ops import _passes
+
+        d = self.dim
+        p = _passes.VolumePass.run(self.means, self.covars, self.max_scales, self.opac,
+                                   self.ranges, self.centers, dim2=d, dim1=d, dim0=d,
+                                   tile_size=8, eps3d=EPS, radius_clip=3.0)
+        p.vjp(self.v_volume, self.means, self.covars)
+        return p.volume
+
 
 class SlabVoxelization:
     """Config-5 volume at the stated 5 % needles: 2M Gaussians whose brick
@@ -600,9 +612,27 @@ def voxel_breakdown(vox, reps):
                                              P(outs[2]), stream())
         assert rc == 0, lib.r2s_last_error()
 
+    reach = torch.empty(n, dtype=torch.int64, device=m3.device)
+
+    def fwd_reach():
+        rc = lib.r2s_voxelize_fwd_reach_f32(P(m3), P(con), P(vox.opac), P(off), P(fl), n, N, d,
+                                            d, d, 8, nb, nb, nb, P(volume), P(reach), stream())
+        assert rc == 0, lib.r2s_last_error()
+
+    def bwd_rows_reach():
+        rc = lib.r2s_voxelize_bwd_rows_reach_f32(P(m3), P(con), P(vox.opac), P(off), P(ids),
+                                                 P(fl), P(isect_src), n, P(vox.v_volume), N, d,
+                                                 d, d, 8, nb, nb, nb, P(reach), P(rows),
+                                                 rows.numel(), stream())
+        assert rc == 0, lib.r2s_last_error()
+
     t = {"voxelize_fwd": time_kernel(fwd, reps), "voxelize_bwd_rows": time_kernel(bwd_rows, reps),
          "voxelize_bwd_reduce": time_kernel(bwd_reduce, reps)}
-    return {"n_isects_3d": n, "seconds": t}
+    # The r2splat.ops pair: the forward also stores the reach masks, the rows
+    # pass takes them (the masks of the timed forward's last call).
+    given = {"voxelize_fwd_reach": time_kernel(fwd_reach, reps),
+             "voxelize_bwd_rows_given_reach": time_kernel(bwd_rows_reach, reps)}
+    return {"n_isects_3d": n, "seconds": t, "given_reach_seconds": given}
 
 
 def kernel_roofline(kernel, seconds, algorithmic_bytes, evaluations=None):
@@ -1007,6 +1037,7 @@ def main():
         log("building config-3 voxelization workload (200k Gaussians, 256^3)")
         vox = Voxelization(dev)
         t_vox = time_steps(vox.step, max(3, args.steps // 2), args.warmup)
+        t_vox_ops = time_steps(vox.step_ops, max(3, args.steps // 2), args.warmup)
         m3, con, off, ids, fl, vol = vox.last
         i3 = int(fl.numel())
         n_vox = VOX_DIM ** 3
@@ -1029,8 +1060,13 @@ def main():
             "hbm_frac": b_vox / t_vox / (HBM_PEAK_GBS * 1e9),
             "kernel_ms": {k: v * 1e3 for k, v in vsec.items()},
             "roofline": kernel_roofline(vdom, vsec[vdom], vbytes[vdom], 512 * i3),
+            # The same call through r2splat.ops (VolumePass), whose backward reuses the
+            # forward's reach masks; the reference-signature operators above recompute them.
+            "ms_per_call_ops": t_vox_ops * 1e3, "mvox_per_s_ops": n_vox / t_vox_ops / 1e6,
+            "kernel_ms_given_reach": {k: v * 1e3 for k, v in vb["given_reach_seconds"].items()},
         }
-        log(f"voxelization fwd+bwd: {t_vox * 1e3:.3f} ms/call, I3={i3}")
+        log(f"voxelization fwd+bwd: {t_vox * 1e3:.3f} ms/call (r2splat.ops: "
+            f"{t_vox_ops * 1e3:.3f} ms), I3={i3}")
 
     log("per-operator table (config 4 / config 3 inputs)")
     result["ops"] = op_table(proj, None if args.no_voxel else vox, args.kernel_reps)

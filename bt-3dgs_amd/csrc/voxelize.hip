@@ -189,15 +189,19 @@ struct BwdRecord {
   int i0, i1;    // slice range (all slices when !cu.ok)
 };
 
+// A record's geometry, opacity and alpha limit; every slice of the brick in
+// range (no culling).
 template <typename T>
-__device__ __forceinline__ void load_bwd_record(const T *__restrict__ means3d,
-                                                const T *__restrict__ conics,
-                                                const T *__restrict__ opac, int64_t g, int64_t N,
-                                                bool in_list, const Brick &b, BwdRecord<T> &rec) {
+__device__ __forceinline__ void load_bwd_record_plain(const T *__restrict__ means3d,
+                                                      const T *__restrict__ conics,
+                                                      const T *__restrict__ opac, int64_t g,
+                                                      int64_t N, bool in_list, const Brick &b,
+                                                      BwdRecord<T> &rec) {
   rec.live = in_list && g >= 0 && g < N;
   rec.o = rec.live ? opac[g] : static_cast<T>(0);
   // |alpha| <= |o| for sigma >= 0: nothing passes (non-finite o stays live).
   if (fabs(rec.o) < static_cast<T>(kThr3)) rec.live = false;
+  rec.cu.ok = false;
   if (!rec.live) {
     rec.o = 0;
     rec.lim = 0;
@@ -205,7 +209,6 @@ __device__ __forceinline__ void load_bwd_record(const T *__restrict__ means3d,
     for (int c = 0; c < 3; ++c) rec.m[c] = 0;
 #pragma unroll
     for (int c = 0; c < 6; ++c) rec.q[c] = rec.h[c] = 0;
-    rec.cu.ok = false;
     rec.i0 = 0;
     rec.i1 = -1;
     return;
@@ -221,9 +224,20 @@ __device__ __forceinline__ void load_bwd_record(const T *__restrict__ means3d,
 #pragma unroll
   for (int c = 0; c < 6; ++c) fin = fin && isfinite(rec.h[c]);
   rec.lim = alpha_limit(rec.o, fin, kThr3);
-  rec.cu = cull3_setup(rec.q, fabs(rec.o), kThr3);
   rec.i0 = b.oi;
   rec.i1 = b.oi + b.ni - 1;
+}
+
+// As load_bwd_record_plain, with the culling setup and the slice range of
+// the record's alpha-test ellipsoid (a record reaching no slice is dead).
+template <typename T>
+__device__ __forceinline__ void load_bwd_record(const T *__restrict__ means3d,
+                                                const T *__restrict__ conics,
+                                                const T *__restrict__ opac, int64_t g, int64_t N,
+                                                bool in_list, const Brick &b, BwdRecord<T> &rec) {
+  load_bwd_record_plain(means3d, conics, opac, g, N, in_list, b, rec);
+  if (!rec.live) return;
+  rec.cu = cull3_setup(rec.q, fabs(rec.o), kThr3);
   if (rec.cu.ok &&
       !index_range<T>(rec.m[2], -rec.cu.hz, rec.cu.hz, b.oi, b.oi + b.ni - 1, rec.i0, rec.i1))
     rec.live = false;
@@ -327,13 +341,15 @@ __device__ __forceinline__ uint64_t reach_mask(const BwdRecord<T> &rec, const Br
 // With S = 1 every voxel sums its records in list order (the volume equals
 // voxel_fwd_kernel's bit for bit); with S > 1 (long lists: the host picks S
 // from the mean list length) the S partial bricks are added in wave order
-// through LDS, a fixed order.
+// through LDS, a fixed order.  reach_out (optional): each record's reach
+// mask, stored at its list position for a backward over the same lists.
 template <typename T, int S>
 __global__ __launch_bounds__(64 * S) void voxel_fwd_reach_kernel(
     const T *__restrict__ means3d, const T *__restrict__ conics, const T *__restrict__ opac,
     const int32_t *__restrict__ tile_offsets, const int32_t *__restrict__ flatten_ids,
     int64_t n_isects, uint32_t n_keys, uint32_t koff, int64_t N, uint32_t D2, uint32_t D1,
-    uint32_t D0, uint32_t n2, uint32_t n1, T *__restrict__ volume) {
+    uint32_t D0, uint32_t n2, uint32_t n1, T *__restrict__ volume,
+    uint64_t *__restrict__ reach_out) {
   constexpr int R = 8;
   using V4 = typename Vec<T>::v4;
   // Per staged record {mx, my, mz, o}, {h0, h1, h2, h3}, {h4, h5, limit bits,
@@ -368,6 +384,7 @@ __global__ __launch_bounds__(64 * S) void voxel_fwd_reach_kernel(
     BwdRecord<T> rec;
     load_bwd_record(means3d, conics, opac, g, N, in, b, rec);
     const uint64_t reach = rec.live ? reach_mask(rec, b, px0 - rec.m[0]) : 0ull;
+    if (reach_out != nullptr && in) reach_out[idx] = reach;
     V4 a, hq, hr;
     a.x = rec.m[0];
     a.y = rec.m[1];
@@ -685,13 +702,17 @@ struct ChunkRecord {
   int ok, oj, oi, n_items;
 };
 
-template <typename T>
+// kGiven: each record's reach mask comes from `reach` (stored by the forward
+// over the same lists, voxel_fwd_reach_kernel) instead of the culling
+// setup and the per-slice row ranges.
+template <typename T, bool kGiven>
 __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
     const T *__restrict__ means3d, const T *__restrict__ conics, const T *__restrict__ opac,
     const int32_t *__restrict__ tile_offsets, const int64_t *__restrict__ isect_ids,
     const int32_t *__restrict__ flatten_ids, const int32_t *__restrict__ isect_src,
     int64_t n_isects, uint32_t n_keys, uint32_t koff, int64_t N, const T *__restrict__ v_vol,
-    uint32_t D2, uint32_t D1, uint32_t D0, uint32_t n2, uint32_t n1, T *__restrict__ rows) {
+    uint32_t D2, uint32_t D1, uint32_t D0, uint32_t n2, uint32_t n1, T *__restrict__ rows,
+    const uint64_t *__restrict__ reach) {
   constexpr int R = kChunkRows;
   using Q = typename Quad<T>::type;
   constexpr int kq = Quad<T>::n;
@@ -717,19 +738,26 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
   const int64_t g = key_ok ? static_cast<int64_t>(flatten_ids[r]) : -1;
   const Brick b = brick_of(key + koff, n2, n1, R, D2, D1, D0);
   BwdRecord<T> rec;
-  load_bwd_record(means3d, conics, opac, g, N, key_ok, b, rec);
+  if constexpr (kGiven)
+    load_bwd_record_plain(means3d, conics, opac, g, N, key_ok, b, rec);
+  else
+    load_bwd_record(means3d, conics, opac, g, N, key_ok, b, rec);
   const T half = static_cast<T>(0.5);
   const uint32_t plane = D1 * D2;  // the caller checks D2 D1 D0 < 2^31
   const T dx0 = (static_cast<T>(b.ok) + half) - rec.m[0];
 
   // The record's reached rows; the items are its set bits in increasing order.
-  const uint64_t reach = reach_mask(rec, b, dx0);
-  const int n_items = __popcll(reach);
+  uint64_t reached;
+  if constexpr (kGiven)
+    reached = key_ok && rec.live ? reach[r] : 0ull;
+  else
+    reached = reach_mask(rec, b, dx0);
+  const int n_items = __popcll(reached);
   if (wave_sum(n_items) > kDenseItems) {  // uniform per wave
     T T0 = 0, T1 = 0, T2 = 0, Y0 = 0, Z0 = 0, Y1 = 0, Z1 = 0, YY = 0, YZ = 0, ZZ = 0;
     if (ballot(rec.live) != 0)
       voxel_brick_full<T, R, true>(rec, b, v_vol, static_cast<int64_t>(plane), D2, dx0, T0, T1,
-                                   T2, Y0, Z0, Y1, Z1, YY, YZ, ZZ, reach);
+                                   T2, Y0, Z0, Y1, Z1, YY, YZ, ZZ, reached);
     if (!key_ok) return;
     const T o = rec.o;
     const T *qc = rec.q;
@@ -758,7 +786,7 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
     cr.oi = b.oi;
     cr.n_items = n_items;
     s_rec[w].store(static_cast<int>(lane), cr);
-    s_rows[w][lane] = reach;
+    s_rows[w][lane] = reached;
 #pragma unroll
     for (int c = 0; c < 10; ++c) s_acc[w][c][lane] = 0;
   }
@@ -946,10 +974,11 @@ int voxel_fwd_impl(const T *means3d, const T *conics, const T *opac,
                    const int32_t *tile_offsets, const int32_t *flatten_ids, int64_t n_isects,
                    int64_t N, uint32_t D2, uint32_t D1, uint32_t D0, uint32_t ts, uint32_t n2,
                    uint32_t n1, uint32_t n0, T *volume, r2s_stream_t st, uint32_t z0 = 0,
-                   bool slab = false) {
+                   bool slab = false, uint64_t *reach = nullptr) {
   clear_error();
   const char *name = "voxelize_to_voxels_fwd";
   R2S_RETURN_IF(check_voxel_args(n_isects, N, D2, D1, D0, ts, n2, n1, n0, name, z0, slab));
+  R2S_REQUIRE(reach == nullptr || ts == 8, "%s: reach masks need tile_size 8", name);
   // Voxel slices [i0, i1) of the layers' z-range.
   const int64_t i0 = static_cast<int64_t>(z0) * ts;
   const int64_t i1 = slab ? std::min<int64_t>(static_cast<int64_t>(z0 + n0) * ts, D0) : D0;
@@ -971,7 +1000,7 @@ int voxel_fwd_impl(const T *means3d, const T *conics, const T *opac,
 #define R2S_VOXEL_FWD_REACH(S)                                                                  \
   voxel_fwd_reach_kernel<T, S><<<grid, dim3(64 * S), 0, stream>>>(                              \
       means3d, conics, opac, tile_offsets, flatten_ids, n_isects, n_keys, koff, N, D2, D1, D0,  \
-      n2, n1, volume)
+      n2, n1, volume, reach)
     if (per_brick < 192)
       R2S_VOXEL_FWD_REACH(1);
     else if (per_brick < 384)
@@ -1038,7 +1067,7 @@ int voxel_bwd_impl(const T *means3d, const T *conics, const T *opac,
                    uint32_t D2, uint32_t D1, uint32_t D0, uint32_t ts, uint32_t n2, uint32_t n1,
                    uint32_t n0, T *v_means, T *v_conics, T *v_opac, void *ws, size_t ws_bytes,
                    bool two_pass, r2s_stream_t st, bool rows_only = false, uint32_t z0 = 0,
-                   bool slab = false) {
+                   bool slab = false, const uint64_t *reach = nullptr) {
   clear_error();
   const char *name = two_pass   ? "voxelize_to_voxels_bwd (two-pass)"
                      : isect_ids ? "voxelize_to_voxels_bwd_per_gaussian"
@@ -1074,13 +1103,17 @@ int voxel_bwd_impl(const T *means3d, const T *conics, const T *opac,
                                  isect_src, n_isects, n_keys, koff, N, v_vol, D2, D1, D0, ts,  \
                                  n2, n1, vec, v_means, v_conics, v_opac, rows, stream)
   if (ts == 8 && rows != nullptr && vec && D2 % 8 == 0 && D1 % 8 == 0 && D0 % 8 == 0 &&
-      n_vox < (int64_t{1} << 31))
-    voxel_bwd_chunk_kernel<T>
-        <<<dim3(static_cast<uint32_t>(ceil_div(n_isects, 64 * kChunkWaves))),
-           dim3(64 * kChunkWaves), 0, stream>>>(means3d, conics, opac, tile_offsets, isect_ids,
-                                                flatten_ids, isect_src, n_isects, n_keys, koff, N,
-                                                v_vol, D2, D1, D0, n2, n1, rows);
-  else if (ts == 8)
+      n_vox < (int64_t{1} << 31)) {
+    const dim3 grid(static_cast<uint32_t>(ceil_div(n_isects, 64 * kChunkWaves)));
+    if (reach != nullptr)
+      voxel_bwd_chunk_kernel<T, true><<<grid, dim3(64 * kChunkWaves), 0, stream>>>(
+          means3d, conics, opac, tile_offsets, isect_ids, flatten_ids, isect_src, n_isects,
+          n_keys, koff, N, v_vol, D2, D1, D0, n2, n1, rows, reach);
+    else
+      voxel_bwd_chunk_kernel<T, false><<<grid, dim3(64 * kChunkWaves), 0, stream>>>(
+          means3d, conics, opac, tile_offsets, isect_ids, flatten_ids, isect_src, n_isects,
+          n_keys, koff, N, v_vol, D2, D1, D0, n2, n1, rows, nullptr);
+  } else if (ts == 8)
     R2S_VOXEL_BWD_R(8, true);
   else if (ts == 4)
     R2S_VOXEL_BWD_R(4, true);
@@ -1135,6 +1168,31 @@ int64_t r2s_voxelize_bwd_workspace_bytes(int64_t n_isects, int dtype_bytes) {
                                   emit_ids, isect_src, n_isects, v_vol, N, D2, D1, D0, ts, n2, \
                                   n1, n0, v_means, v_conics, v_opac, ws, ws_bytes, true, st);  \
   }                                                                                            \
+  int r2s_voxelize_fwd_reach_##SUF(const T *means3d, const T *conics, const T *opac,           \
+                                   const int32_t *tile_offsets, const int32_t *flatten_ids,    \
+                                   int64_t n_isects, int64_t N, uint32_t D2, uint32_t D1,      \
+                                   uint32_t D0, uint32_t ts, uint32_t n2, uint32_t n1,         \
+                                   uint32_t n0, T *volume, uint64_t *reach, r2s_stream_t st) { \
+    return r2s::voxel_fwd_impl<T>(means3d, conics, opac, tile_offsets, flatten_ids, n_isects,  \
+                                  N, D2, D1, D0, ts, n2, n1, n0, volume, st, 0, false, reach); \
+  }                                                                                            \
+  int r2s_voxelize_bwd_emit_reach_##SUF(                                                       \
+      const T *means3d, const T *conics, const T *opac, const int32_t *tile_offsets,           \
+      const int64_t *isect_ids, const int32_t *flatten_ids, const int32_t *emit_ids,           \
+      const int32_t *isect_src, int64_t n_isects, const T *v_vol, int64_t N, uint32_t D2,      \
+      uint32_t D1, uint32_t D0, uint32_t ts, uint32_t n2, uint32_t n1, uint32_t n0,            \
+      const uint64_t *reach, T *v_means, T *v_conics, T *v_opac, void *ws, size_t ws_bytes,    \
+      r2s_stream_t st) {                                                                       \
+    if (reach == nullptr) {                                                                    \
+      r2s::clear_error();                                                                      \
+      r2s::set_error("voxelize_to_voxels_bwd (two-pass): null reach masks");                   \
+      return R2S_EINVAL;                                                                       \
+    }                                                                                          \
+    return r2s::voxel_bwd_impl<T>(means3d, conics, opac, tile_offsets, isect_ids, flatten_ids, \
+                                  emit_ids, isect_src, n_isects, v_vol, N, D2, D1, D0, ts, n2, \
+                                  n1, n0, v_means, v_conics, v_opac, ws, ws_bytes, true, st,   \
+                                  false, 0, false, reach);                                     \
+  }                                                                                            \
   int r2s_voxelize_fwd_slab_##SUF(const T *means3d, const T *conics, const T *opac,            \
                                   const int32_t *tile_offsets, const int32_t *flatten_ids,     \
                                   int64_t n_isects, int64_t N, uint32_t D2, uint32_t D1,       \
@@ -1167,6 +1225,22 @@ int64_t r2s_voxelize_bwd_workspace_bytes(int64_t n_isects, int dtype_bytes) {
                                   nullptr, isect_src, n_isects, v_vol, N, D2, D1, D0, ts, n2,  \
                                   n1, n0, nullptr, nullptr, nullptr, rows, rows_bytes, true,   \
                                   st, true);                                                   \
+  }                                                                                            \
+  int r2s_voxelize_bwd_rows_reach_##SUF(                                                       \
+      const T *means3d, const T *conics, const T *opac, const int32_t *tile_offsets,           \
+      const int64_t *isect_ids, const int32_t *flatten_ids, const int32_t *isect_src,          \
+      int64_t n_isects, const T *v_vol, int64_t N, uint32_t D2, uint32_t D1, uint32_t D0,      \
+      uint32_t ts, uint32_t n2, uint32_t n1, uint32_t n0, const uint64_t *reach, void *rows,   \
+      size_t rows_bytes, r2s_stream_t st) {                                                    \
+    if (reach == nullptr) {                                                                    \
+      r2s::clear_error();                                                                      \
+      r2s::set_error("voxelize_to_voxels_bwd (two-pass): null reach masks");                   \
+      return R2S_EINVAL;                                                                       \
+    }                                                                                          \
+    return r2s::voxel_bwd_impl<T>(means3d, conics, opac, tile_offsets, isect_ids, flatten_ids, \
+                                  nullptr, isect_src, n_isects, v_vol, N, D2, D1, D0, ts, n2,  \
+                                  n1, n0, nullptr, nullptr, nullptr, rows, rows_bytes, true,   \
+                                  st, true, 0, false, reach);                                  \
   }                                                                                            \
   int r2s_voxelize_bwd_rows_slab_##SUF(                                                        \
       const T *means3d, const T *conics, const T *opac, const int32_t *tile_offsets,           \

@@ -70,6 +70,12 @@ _FLOAT_OPS = {
                                 _p, _p, _p, _p, _p, _sz, _p],
     "voxelize_fwd_slab": [_p, _p, _p, _p, _p, _i64, _i64, _u32, _u32, _u32, _u32, _u32, _u32,
                           _u32, _u32, _p, _p],
+    "voxelize_fwd_reach": [_p, _p, _p, _p, _p, _i64, _i64, _u32, _u32, _u32, _u32, _u32, _u32,
+                           _u32, _p, _p, _p],
+    "voxelize_bwd_rows_reach": [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _u32, _u32, _u32,
+                                _u32, _u32, _u32, _u32, _p, _p, _sz, _p],
+    "voxelize_bwd_emit_reach": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _u32, _u32, _u32,
+                                _u32, _u32, _u32, _u32, _p, _p, _p, _p, _p, _sz, _p],
     "voxelize_bwd_rows_slab": [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _u32, _u32, _u32, _u32,
                                _u32, _u32, _u32, _u32, _p, _sz, _p],
     "voxelize_bwd_emit_slab": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _u32, _u32, _u32,
@@ -135,7 +141,7 @@ DENSIFY_MAX_WIDTH = 16
 
 SYMBOLS = sorted(list(_PLAIN) + [f"r2s_{n}_{s}" for n in _FLOAT_OPS for s in ("f32", "f64")])
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 def load(path: str = LIB_PATH) -> ctypes.CDLL:

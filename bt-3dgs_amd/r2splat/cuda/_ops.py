@@ -1058,8 +1058,35 @@ def voxelize_to_voxels_fwd(means3d: Tensor, conics: Tensor, opacities: Tensor,
     return out
 
 
+def voxelize_with_reach(means3d: Tensor, conics: Tensor, opacities: Tensor,
+                        tile_offsets: Tensor, flatten_ids: Tensor, dim2: int, dim1: int,
+                        dim0: int) -> Tuple[Tensor, Optional[Tensor]]:
+    """:func:`voxelize_to_voxels_fwd` at tile size 8 that also returns each
+    record's reach mask (the brick rows its alpha-test ellipsoid reaches, one
+    int64 per record at its list position) for :func:`voxel_backward` over the
+    same inputs and lists (None when there are no records)."""
+    for t, n in ((means3d, "means3d"), (conics, "conics"), (opacities, "opacities"),
+                 (tile_offsets, "tile_offsets"), (flatten_ids, "flatten_ids")):
+        _check_input(t, n)
+    N = _check_voxel(means3d, conics, opacities, tile_offsets, flatten_ids)
+    d2, d1, d0 = int(dim2), int(dim1), int(dim0)
+    n0, n1, n2 = tile_offsets.size(0), tile_offsets.size(1), tile_offsets.size(2)
+    dev = means3d.device
+    n_isects = flatten_ids.numel()
+    if N == 0 or n_isects == 0:
+        return torch.zeros((d0, d1, d2), dtype=means3d.dtype, device=dev), None
+    out = torch.empty((d0, d1, d2), dtype=means3d.dtype, device=dev)
+    reach = torch.empty(n_isects, dtype=torch.int64, device=dev)
+    sfx = _suffix(means3d, "voxelize_to_voxels_fwd")
+    with torch.cuda.device(dev):
+        _call(f"r2s_voxelize_fwd_reach_{sfx}", _ptr(means3d), _ptr(conics), _ptr(opacities),
+              _ptr(tile_offsets), _ptr(flatten_ids), n_isects, N, d2, d1, d0, 8, n2, n1, n0,
+              _ptr(out), _ptr(reach), _stream(dev))
+    return out, reach
+
+
 def _voxel_bwd(means3d, conics, opacities, tile_offsets, isect_ids, flatten_ids, v_render,
-               dim2, dim1, dim0, tile_size, op, emission=_LOOKUP):
+               dim2, dim1, dim0, tile_size, op, emission=_LOOKUP, reach=None):
     N = _check_voxel(means3d, conics, opacities, tile_offsets, flatten_ids)
     _check(v_render.dim() == 3, "v_render_output must be 3D [dim0, dim1, dim2]")
     d2, d1, d0, ts = int(dim2), int(dim1), int(dim0), int(tile_size)
@@ -1078,7 +1105,18 @@ def _voxel_bwd(means3d, conics, opacities, tile_offsets, isect_ids, flatten_ids,
     sfx = _suffix(means3d, op)
     dev = means3d.device
     with torch.cuda.device(dev):
-        if emit is not None:
+        if emit is not None and reach is not None:
+            _check(ts == 8 and reach.dtype == torch.int64 and reach.numel() == n_isects
+                   and reach.is_contiguous() and reach.device == dev,
+                   "reach masks must come from voxelize_with_reach over these lists")
+            ws = _workspace(_lib().r2s_voxelize_bwd_workspace_bytes(n_isects,
+                                                                    means3d.element_size()), dev)
+            _call(f"r2s_voxelize_bwd_emit_reach_{sfx}", _ptr(means3d), _ptr(conics),
+                  _ptr(opacities), _ptr(tile_offsets), _ptr(isect_ids), _ptr(flatten_ids),
+                  _ptr(emit[0]), _ptr(emit[1]), n_isects, _ptr(v_render), N, d2, d1, d0, ts,
+                  n2, n1, n0, _ptr(reach), _ptr(v_means3d), _ptr(v_conics), _ptr(v_opac),
+                  _ptr(ws), ws.numel(), _stream(dev))
+        elif emit is not None:
             ws = _workspace(_lib().r2s_voxelize_bwd_workspace_bytes(n_isects,
                                                                     means3d.element_size()), dev)
             _call(f"r2s_voxelize_bwd_emit_{sfx}", _ptr(means3d), _ptr(conics), _ptr(opacities),
@@ -1126,17 +1164,19 @@ def voxelize_to_voxels_bwd_per_gaussian(means3d: Tensor, conics: Tensor, opaciti
 
 def voxel_backward(means3d: Tensor, conics: Tensor, opacities: Tensor, tile_offsets: Tensor,
                    lists: TileLists, v_volume: Tensor, dim2: int, dim1: int, dim0: int,
-                   tile_size: int):
+                   tile_size: int, reach: Optional[Tensor] = None):
     """The voxelizer's VJP over lists returned by :func:`bin_tiles_3d`, with
     their emission order passed explicitly (VoxelizeToVoxels.cpp:115-278) ->
-    (v_means3d, v_conics, v_opacities)."""
+    (v_means3d, v_conics, v_opacities).  ``reach``: the masks
+    :func:`voxelize_with_reach` returned for the same inputs and lists (the
+    backward then skips the culling setup)."""
     for t, n in ((means3d, "means3d"), (conics, "conics"), (opacities, "opacities"),
                  (tile_offsets, "tile_offsets"), (lists.flatten_ids, "flatten_ids"),
                  (v_volume, "v_render_output")):
         _check_input(t, n)
     return _voxel_bwd(means3d, conics, opacities, tile_offsets, lists.isect_ids,
                       lists.flatten_ids, v_volume, dim2, dim1, dim0, tile_size,
-                      "voxel_backward", emission=lists.emission)
+                      "voxel_backward", emission=lists.emission, reach=reach)
 
 
 # -------------------------------------------------------------- compaction --

@@ -163,6 +163,7 @@ class VolumePass:
     lists: object  # r2splat.cuda._ops.TileLists, None for a slabbed volume
     volume: Tensor
     slabs: Tuple[Tuple[int, int], ...] = ()
+    reach: Optional[Tensor] = None  # per-record reach masks (tile size 8) for the backward
 
     @classmethod
     @torch.no_grad()
@@ -194,10 +195,15 @@ class VolumePass:
             return cls(d2, d1, d0, ts, float(eps3d), ranges, centers, means3d, conics, weights,
                        radii, None, None, volume, slabs)
         tile_offsets = ops.isect_offset_encode_3d(lists.isect_ids, n2, n1, n0)
-        volume = ops.voxelize_to_voxels_fwd(means3d, conics, weights, tile_offsets,
-                                            lists.flatten_ids, d2, d1, d0, ts)
+        reach = None
+        if ts == 8:  # the backward reuses the forward's culling
+            volume, reach = ops.voxelize_with_reach(means3d, conics, weights, tile_offsets,
+                                                    lists.flatten_ids, d2, d1, d0)
+        else:
+            volume = ops.voxelize_to_voxels_fwd(means3d, conics, weights, tile_offsets,
+                                                lists.flatten_ids, d2, d1, d0, ts)
         return cls(d2, d1, d0, ts, float(eps3d), ranges, centers, means3d, conics, weights,
-                   radii, tile_offsets, lists, volume)
+                   radii, tile_offsets, lists, volume, reach=reach)
 
     @torch.no_grad()
     def vjp(self, v_volume: Tensor, means: Tensor, covars: Tensor) -> VolumeVJP:
@@ -218,7 +224,7 @@ class VolumePass:
         else:
             v_means3d, v_conics, v_weights = ops.voxel_backward(
                 self.means3d, self.conics, self.weights, self.tile_offsets, self.lists,
-                v_volume, self.dim2, self.dim1, self.dim0, self.tile_size)
+                v_volume, self.dim2, self.dim1, self.dim0, self.tile_size, reach=self.reach)
         v_means, v_covars = ops.world_to_volume_mapping_bwd(
             means.contiguous(), covars, self.ranges, self.centers, self.dim2, self.dim1,
             self.dim0, self.eps3d, v_means3d, v_conics)

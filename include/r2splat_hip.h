@@ -629,6 +629,70 @@ int r2s_voxelize_bwd_emit_slab_f64(const double *means3d, const double *conics,
                                    void *workspace, size_t workspace_bytes,
                                    r2s_stream_t stream);
 
+/* The forward and the two-pass backward over the same brick lists (tile
+ * size 8), for a caller that keeps the lists between them: the forward
+ * also stores each record's reach mask (the brick rows its alpha-test
+ * ellipsoid reaches, bit 8 * slice + row; reach [n_isects] at the record's
+ * list position), and the backward takes them instead of recomputing them.
+ * The masks are valid only for the means3d, conics, opacities and lists
+ * the forward saw.  No reference counterpart (VoxelizeToVoxels.cpp:31-278
+ * recompute everything per call). */
+int r2s_voxelize_fwd_reach_f32(const float *means3d, const float *conics,
+                               const float *opacities, const int32_t *tile_offsets,
+                               const int32_t *flatten_ids, int64_t n_isects, int64_t N,
+                               uint32_t dim2, uint32_t dim1, uint32_t dim0, uint32_t tile_size,
+                               uint32_t n_tiles_d2, uint32_t n_tiles_d1, uint32_t n_tiles_d0,
+                               float *volume, uint64_t *reach, r2s_stream_t stream);
+int r2s_voxelize_fwd_reach_f64(const double *means3d, const double *conics,
+                               const double *opacities, const int32_t *tile_offsets,
+                               const int32_t *flatten_ids, int64_t n_isects, int64_t N,
+                               uint32_t dim2, uint32_t dim1, uint32_t dim0, uint32_t tile_size,
+                               uint32_t n_tiles_d2, uint32_t n_tiles_d1, uint32_t n_tiles_d0,
+                               double *volume, uint64_t *reach, r2s_stream_t stream);
+int r2s_voxelize_bwd_emit_reach_f32(const float *means3d, const float *conics,
+                                    const float *opacities, const int32_t *tile_offsets,
+                                    const int64_t *isect_ids, const int32_t *flatten_ids,
+                                    const int32_t *emit_ids, const int32_t *isect_src,
+                                    int64_t n_isects, const float *v_volume, int64_t N,
+                                    uint32_t dim2, uint32_t dim1, uint32_t dim0,
+                                    uint32_t tile_size, uint32_t n_tiles_d2,
+                                    uint32_t n_tiles_d1, uint32_t n_tiles_d0,
+                                    const uint64_t *reach, float *v_means3d, float *v_conics,
+                                    float *v_opacities, void *workspace, size_t workspace_bytes,
+                                    r2s_stream_t stream);
+int r2s_voxelize_bwd_emit_reach_f64(const double *means3d, const double *conics,
+                                    const double *opacities, const int32_t *tile_offsets,
+                                    const int64_t *isect_ids, const int32_t *flatten_ids,
+                                    const int32_t *emit_ids, const int32_t *isect_src,
+                                    int64_t n_isects, const double *v_volume, int64_t N,
+                                    uint32_t dim2, uint32_t dim1, uint32_t dim0,
+                                    uint32_t tile_size, uint32_t n_tiles_d2,
+                                    uint32_t n_tiles_d1, uint32_t n_tiles_d0,
+                                    const uint64_t *reach, double *v_means3d,
+                                    double *v_conics, double *v_opacities, void *workspace,
+                                    size_t workspace_bytes, r2s_stream_t stream);
+
+/* The first pass of r2s_voxelize_bwd_emit_reach_* alone (as
+ * r2s_voxelize_bwd_rows_*, with the forward's reach masks). */
+int r2s_voxelize_bwd_rows_reach_f32(const float *means3d, const float *conics,
+                                    const float *opacities, const int32_t *tile_offsets,
+                                    const int64_t *isect_ids, const int32_t *flatten_ids,
+                                    const int32_t *isect_src, int64_t n_isects,
+                                    const float *v_volume, int64_t N, uint32_t dim2,
+                                    uint32_t dim1, uint32_t dim0, uint32_t tile_size,
+                                    uint32_t n_tiles_d2, uint32_t n_tiles_d1,
+                                    uint32_t n_tiles_d0, const uint64_t *reach, void *rows,
+                                    size_t rows_bytes, r2s_stream_t stream);
+int r2s_voxelize_bwd_rows_reach_f64(const double *means3d, const double *conics,
+                                    const double *opacities, const int32_t *tile_offsets,
+                                    const int64_t *isect_ids, const int32_t *flatten_ids,
+                                    const int32_t *isect_src, int64_t n_isects,
+                                    const double *v_volume, int64_t N, uint32_t dim2,
+                                    uint32_t dim1, uint32_t dim0, uint32_t tile_size,
+                                    uint32_t n_tiles_d2, uint32_t n_tiles_d1,
+                                    uint32_t n_tiles_d0, const uint64_t *reach, void *rows,
+                                    size_t rows_bytes, r2s_stream_t stream);
+
 /* The first pass of r2s_voxelize_bwd_emit_slab_* alone (the rows of one
  * slab's records, as r2s_voxelize_bwd_rows_*). */
 int r2s_voxelize_bwd_rows_slab_f32(const float *means3d, const float *conics,

@@ -79,6 +79,18 @@ def test_tile_sizes_whose_products_wrap_are_rejected(lib):
     assert rc == 1001 and b"tile_size" in lib.r2s_last_error()
 
 
+def test_reach_mask_entries_check_their_arguments(lib):
+    # Reach masks exist for tile size 8 only; the backward needs them given.
+    buf = ctypes.create_string_buffer(64)
+    rc = lib.r2s_voxelize_fwd_reach_f32(None, None, None, None, None, 0, 1, 8, 8, 8, 4, 2, 2, 2,
+                                        buf, buf, None)
+    assert rc == 1001 and b"reach masks need tile_size 8" in lib.r2s_last_error()
+    rc = lib.r2s_voxelize_bwd_emit_reach_f32(None, None, None, None, None, None, None, None, 5,
+                                             None, 1, 8, 8, 8, 8, 1, 1, 1, None, None, None,
+                                             None, None, 0, None)
+    assert rc == 1001 and b"null reach masks" in lib.r2s_last_error()
+
+
 def test_workspace_queries(lib):
     assert lib.r2s_isect_workspace_bytes(0, 0, 11) == 0
     small = lib.r2s_isect_workspace_bytes(0, 1000, 11)

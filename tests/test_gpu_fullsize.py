@@ -146,6 +146,14 @@ def test_config4_volume_regulariser_voxelization(config4):
     _report("tree 128^3 fwd", check_voxel(refs, volume=np32(vol)))
     got = _ops.voxel_backward(m3, con, d["opac"], off, lists, v.to(DEV), 128, 128, 128, 8)
     _report("tree 128^3 bwd", check_voxel(refs, grads=_grads(got)))
+    # The forward's reach masks given to the backward: the same outputs.
+    vol_r, reach = _ops.voxelize_with_reach(m3, con, d["opac"], off, lists.flatten_ids, 128, 128,
+                                            128)
+    assert torch.equal(vol_r, vol)
+    given = _ops.voxel_backward(m3, con, d["opac"], off, lists, v.to(DEV), 128, 128, 128, 8,
+                                reach=reach)
+    for a, b in zip(got, given):
+        assert torch.equal(a, b)
 
 
 # ---------------------------------------------------------------- config 3 --
@@ -205,6 +213,13 @@ def test_config3_voxel_forward_and_backward(config3, config3_refs):
     again = _ops.voxel_backward(d["m3"], d["con"], d["op"], d["off"], d["lists"],
                                 d["v"].to(DEV), 256, 256, 256, 8)
     for a, b in zip(got, again):
+        assert torch.equal(a, b)
+    vol_r, reach = _ops.voxelize_with_reach(d["m3"], d["con"], d["op"], d["off"],
+                                            d["lists"].flatten_ids, 256, 256, 256)
+    assert torch.equal(vol_r, vol)
+    given = _ops.voxel_backward(d["m3"], d["con"], d["op"], d["off"], d["lists"],
+                                d["v"].to(DEV), 256, 256, 256, 8, reach=reach)
+    for a, b in zip(got, given):
         assert torch.equal(a, b)
 
 

@@ -529,6 +529,34 @@ def test_voxelize_fwd_long_lists(dtype, n, band):
     print("volume", check_voxel(refs, volume=np32(vol)))
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("n,log_mu,dims", [(1500, -3.2, (32, 32, 40)), (1500, -1.6, (32, 32, 40)),
+                                           (8000, -3.2, (32, 32, 32))])
+def test_voxel_backward_reuses_the_forward_reach_masks(dtype, n, log_mu, dims):
+    """voxelize_with_reach stores each record's reach mask; the two-pass backward given them
+    skips its own culling and returns exactly what it computes without them (chunked waves,
+    dense waves, and lists long enough for 4 forward waves per brick), and the volume equals
+    the plain forward's."""
+    d = _prepared(n, 13, dtype, log_mu=log_mu)
+    ranges = torch.full((3,), 2.0, dtype=dtype, device=DEV)
+    centers = torch.zeros(3, dtype=dtype, device=DEV)
+    m3, con, r3 = W.world_to_volume_mapping_fwd(d["means"], d["covars"], d["opac"], ranges,
+                                                centers, *dims, 1e-8, 3.0)
+    n2, n1, n0 = (-(-x // 8) for x in dims)
+    lists = _ops.bin_tiles_3d(m3, r3, 8, n2, n1, n0)
+    off = W.isect_offset_encode_3d(lists.isect_ids, n2, n1, n0)
+    op = d["opac"]
+    vol = W.voxelize_to_voxels_fwd(m3, con, op, off, lists.flatten_ids, *dims, 8)
+    vol_r, reach = _ops.voxelize_with_reach(m3, con, op, off, lists.flatten_ids, *dims)
+    assert reach.numel() == lists.flatten_ids.numel() and bool((reach != 0).any())
+    assert torch.equal(vol, vol_r)
+    v = torch.randn(vol.shape, generator=d["gen"], dtype=dtype).to(DEV)
+    plain = _ops.voxel_backward(m3, con, op, off, lists, v, *dims, 8)
+    given = _ops.voxel_backward(m3, con, op, off, lists, v, *dims, 8, reach=reach)
+    for a, b in zip(plain, given):
+        assert torch.equal(a, b)
+
+
 def _voxel_row_reach(m3, con, op, ids, fl, dims, ts):
     """Rows (of 64) of its brick that each record's alpha-test ellipsoid reaches."""
     d2, d1, d0 = dims
