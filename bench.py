@@ -577,7 +577,7 @@ def kernel_breakdown(proj: Projection, reps):
 def voxel_breakdown(vox, reps):
     """Event timings of the voxelizer's kernels at the config-3 inputs,
     through their C entry points on the current stream: the forward
-    (voxel_fwd_kernel), the backward's rows pass (voxel_bwd_chunk_kernel)
+    (voxel_fwd_reach_kernel), the backward's rows pass (voxel_bwd_chunk_kernel)
     and its per-Gaussian reduce (row_reduce_kernel<10>)."""
     from r2splat.cuda import _backend, _ops
 
