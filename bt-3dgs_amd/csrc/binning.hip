@@ -194,12 +194,12 @@ __global__ void layer_prefix_kernel(const unsigned long long *__restrict__ diff,
 // and 31 (VALU only, no LDS round trip).  -1 is the identity (every value
 // is >= -1).
 __device__ __forceinline__ int wave_prefix_max(int v) {
-  v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x111, 0xf, 0xf, false));  // row_shr:1
-  v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x112, 0xf, 0xf, false));  // row_shr:2
-  v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x114, 0xf, 0xf, false));  // row_shr:4
-  v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x118, 0xf, 0xf, false));  // row_shr:8
-  v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x142, 0xa, 0xf, false));  // row_bcast:15
-  v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x143, 0xc, 0xf, false));  // row_bcast:31
+  v = max(v, dpp_take<0x111, 0xf>(v, -1));  // row_shr:1
+  v = max(v, dpp_take<0x112, 0xf>(v, -1));  // row_shr:2
+  v = max(v, dpp_take<0x114, 0xf>(v, -1));  // row_shr:4
+  v = max(v, dpp_take<0x118, 0xf>(v, -1));  // row_shr:8
+  v = max(v, dpp_take<0x142, 0xa>(v, -1));  // row_bcast:15
+  v = max(v, dpp_take<0x143, 0xc>(v, -1));  // row_bcast:31
   return v;
 }
 

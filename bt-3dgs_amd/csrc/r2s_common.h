@@ -103,18 +103,20 @@ __device__ __forceinline__ int64_t readlane_i64(int64_t v, uint32_t src) {
 
 // One DPP lane move of a 32- or 64-bit value (the halves moved
 // separately): lanes the move does not write (no source lane in the row, or
-// a row outside kRowMask) read 0.
+// a row outside kRowMask) read `fill`.
 template <int kCtrl, int kRowMask, typename T>
-__device__ __forceinline__ T dpp_take(T v) {
+__device__ __forceinline__ T dpp_take(T v, T fill = T(0)) {
   static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32- or 64-bit values");
   if constexpr (sizeof(T) == 4) {
-    const int x = __builtin_bit_cast(int, v);
-    return __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, x, kCtrl, kRowMask, 0xf, false));
+    const int x = __builtin_bit_cast(int, v), f = __builtin_bit_cast(int, fill);
+    return __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(f, x, kCtrl, kRowMask, 0xf, false));
   } else {
-    const uint64_t u = __builtin_bit_cast(uint64_t, v);
-    const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(u)), kCtrl,
+    const uint64_t u = __builtin_bit_cast(uint64_t, v), uf = __builtin_bit_cast(uint64_t, fill);
+    const int lo = __builtin_amdgcn_update_dpp(static_cast<int>(static_cast<uint32_t>(uf)),
+                                               static_cast<int>(static_cast<uint32_t>(u)), kCtrl,
                                                kRowMask, 0xf, false);
-    const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(u >> 32)),
+    const int hi = __builtin_amdgcn_update_dpp(static_cast<int>(static_cast<uint32_t>(uf >> 32)),
+                                               static_cast<int>(static_cast<uint32_t>(u >> 32)),
                                                kCtrl, kRowMask, 0xf, false);
     return __builtin_bit_cast(T, (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
                                      static_cast<uint32_t>(lo));
