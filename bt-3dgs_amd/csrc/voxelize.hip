@@ -1073,6 +1073,7 @@ int voxel_bwd_impl(const T *means3d, const T *conics, const T *opac,
                      : isect_ids ? "voxelize_to_voxels_bwd_per_gaussian"
                                  : "voxelize_to_voxels_bwd";
   R2S_RETURN_IF(check_voxel_args(n_isects, N, D2, D1, D0, ts, n2, n1, n0, name, z0, slab));
+  R2S_REQUIRE(reach == nullptr || ts == 8, "%s: reach masks need tile_size 8", name);
   if (N == 0) return R2S_OK;
   const int64_t n_vox = static_cast<int64_t>(D2) * D1 * D0;
   if (n_isects == 0 || n_vox == 0) {  // the two-pass form still stores its (zero) outputs

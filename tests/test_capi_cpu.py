@@ -89,6 +89,10 @@ def test_reach_mask_entries_check_their_arguments(lib):
                                              None, 1, 8, 8, 8, 8, 1, 1, 1, None, None, None,
                                              None, None, 0, None)
     assert rc == 1001 and b"null reach masks" in lib.r2s_last_error()
+    rc = lib.r2s_voxelize_bwd_emit_reach_f32(None, None, None, None, None, None, None, None, 5,
+                                             None, 1, 8, 8, 8, 4, 2, 2, 2, buf, None, None, None,
+                                             None, 0, None)
+    assert rc == 1001 and b"reach masks need tile_size 8" in lib.r2s_last_error()
 
 
 def test_workspace_queries(lib):
