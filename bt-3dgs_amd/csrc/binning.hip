@@ -494,9 +494,12 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     // Lanes holding the same digit: those whose bits agree with the lane's in
     // every ballot.  Per bit, ballot ^ (the lane's bit copied to all 64)
     // marks the lanes that differ there; the union over the bits is the
-    // complement of the peers.
+    // complement of the peers.  The loop runs over the table's kDBits bits,
+    // unrolled: bits at or above `bits` are zero in every lane's digit, so
+    // they mark no lane.
     uint64_t differ = 0;
-    for (uint32_t b = 0; b < bits; ++b) {
+#pragma unroll
+    for (uint32_t b = 0; b < static_cast<uint32_t>(kDBits); ++b) {
       const uint32_t x = static_cast<uint32_t>(__builtin_amdgcn_sbfe(static_cast<int32_t>(d), b, 1));
       const uint64_t m = ballot(x != 0u);  // x: 0 or all ones
       differ |= m ^ ((static_cast<uint64_t>(x) << 32) | x);

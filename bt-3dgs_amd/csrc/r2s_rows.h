@@ -361,11 +361,18 @@ __global__ __launch_bounds__(256) void row_reduce_kernel(const T *__restrict__ r
   }
 }
 
-// Stores every target: zeros, then each Gaussian's sum over its rows.
+// Stores every target: zeros (unless the caller stored them already:
+// zeroed), then each Gaussian's sum over its rows.
 template <typename T, int NV>
 void launch_row_reduce(const T *rows, const int32_t *emit_ids, int64_t n, int64_t n_items,
-                       const RowTargets<T, NV> &tg, hipStream_t stream) {
+                       const RowTargets<T, NV> &tg, hipStream_t stream, bool zeroed = false) {
   if (n_items <= 0) return;
+  if (zeroed) {
+    if (n > 0)
+      row_reduce_kernel<T, NV><<<dim3(static_cast<uint32_t>(ceil_div(n, 4 * kReduceWaveRows))),
+                                 dim3(256), 0, stream>>>(rows, emit_ids, n, n_items, tg);
+    return;
+  }
   const TargetList<T, NV> tl = target_list(tg);
   FillArrays<T, NV> fa;
   int n_arrays = 0;

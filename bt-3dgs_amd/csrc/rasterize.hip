@@ -171,7 +171,10 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
   constexpr int LPR = TS / R;            // lanes per tile row
   constexpr int NP = kFwdWaves * G;      // partial tiles per block
   static_assert(G * NL == 64 && LPR * R == TS, "unsupported tile size");
-  __shared__ FwdRecord<T> s_rec[kFwdBatch];
+  // G - 1 records of padding after the batch: the record loop's last round
+  // reads up to G - 1 entries past the batch's end.  Entries past the end
+  // hold dead records (zero limit, which no pixel passes).
+  __shared__ FwdRecord<T> s_rec[kFwdBatch + G];
   __shared__ T s_part[NP][TS * TS];
 
   // The splits of one tile are consecutive logical blocks (same XCD).
@@ -193,14 +196,29 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
   const int64_t t1 = (key == n_keys - 1) ? n_isects : static_cast<int64_t>(tile_offsets[key + 1]);
   const int64_t start = t0 + (t1 - t0) * split / splits;
   const int64_t end = t0 + (t1 - t0) * (split + 1) / splits;
-  T acc[R];
+  T acc[R], pxk[R];
 #pragma unroll
-  for (int q = 0; q < R; ++q) acc[q] = 0;
+  for (int q = 0; q < R; ++q) {
+    acc[q] = 0;
+    // The lane's pixel centres, kept in registers across the record loop
+    // (otherwise some are recomputed per record).
+    pxk[q] = px0 + static_cast<T>(q);
+    asm volatile("" : "+v"(pxk[q]));
+  }
+  const int wave_first = wave * G;  // uniform: the record loop below is a scalar loop
+  const int group = lane / NL;
+  if (tid < G) {
+    FwdRecord<T> dead;
+    dead.p.x = dead.p.y = dead.p.z = dead.p.w = 0;
+    dead.q.x = dead.q.y = dead.q.w = 0;
+    dead.q.z = limit_as_value(static_cast<typename Bits<T>::type>(0));
+    s_rec[kFwdBatch + tid] = dead;
+  }
   for (int64_t base = start; base < end; base += kFwdBatch) {
     __syncthreads();
     const int64_t idx = base + tid;
-    if (idx < end) {
-      const int64_t g = flatten_ids[idx];
+    {
+      const int64_t g = idx < end ? static_cast<int64_t>(flatten_ids[idx]) : -1;
       FwdRecord<T> rec;
       V4 &p = rec.p, &q = rec.q;
       if (g >= 0 && g < n_items) {
@@ -225,9 +243,10 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
     }
     __syncthreads();
     const int cnt = static_cast<int>(min(static_cast<int64_t>(kFwdBatch), end - base));
-    for (int j = slot; j < cnt; j += NP) {
-      const V4 p = s_rec[j].p;
-      const V4 q = s_rec[j].q;
+    for (int jb = wave_first; jb < cnt; jb += NP) {
+      // A group past the batch's end reads a dead record.
+      const V4 p = s_rec[jb + group].p;
+      const V4 q = s_rec[jb + group].q;
       const typename Bits<T>::type lim = bits_of(q.z);
       const T dy = py - p.y;
       const T B = p.w * dy, C = q.x * dy * dy;
@@ -237,7 +256,7 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
       // footprints far along the row).
 #pragma unroll
       for (int k = 0; k < R; ++k) {
-        const T dx = (px0 + static_cast<T>(k)) - p.x;
+        const T dx = pxk[k] - p.x;
         const T sl = (p.z * dx + B) * dx + C;
         const T e = neg_exp2(sl);
         acc[k] = fma(q.y, alpha_pass(sl, lim) ? e : static_cast<T>(0), acc[k]);
@@ -336,13 +355,25 @@ __device__ __forceinline__ void load_raster_record(
 // reduction forms the opacity and mu partials from T0.
 constexpr int kPayloadValues = 8;
 
+// With z_xy non-null it also stores zeros into the backward's outputs
+// (v_xy_abs may be null), which the reduction then overwrites for every pair
+// with records -- one launch fewer than a separate fill.
 template <typename T>
 __global__ __launch_bounds__(256) void raster_pack_kernel(
     const T *__restrict__ means2d, const T *__restrict__ conics, const T *__restrict__ opac,
-    const T *__restrict__ mus, int64_t n_items, T *__restrict__ payload) {
+    const T *__restrict__ mus, int64_t n_items, T *__restrict__ payload, T *__restrict__ z_xy,
+    T *__restrict__ z_abs, T *__restrict__ z_conic, T *__restrict__ z_opac,
+    T *__restrict__ z_mu) {
   using V4 = typename Vec<T>::v4;
   const int64_t g = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (g >= n_items) return;
+  if (z_xy != nullptr) {
+    z_xy[2 * g] = z_xy[2 * g + 1] = static_cast<T>(0);
+    if (z_abs != nullptr) z_abs[2 * g] = z_abs[2 * g + 1] = static_cast<T>(0);
+    z_conic[3 * g] = z_conic[3 * g + 1] = z_conic[3 * g + 2] = static_cast<T>(0);
+    z_opac[g] = static_cast<T>(0);
+    z_mu[g] = static_cast<T>(0);
+  }
   V4 p0, p1;
   p0.x = means2d[2 * g];
   p0.y = means2d[2 * g + 1];
@@ -983,10 +1014,11 @@ int64_t raster_bwd_ws_bytes(int64_t n_isects, int64_t n_items, int dtype_bytes) 
 
 // Second pass of the two-pass backward: per-Gaussian sums of the rows, with
 // v_opac = mu sum(T0) and v_mu = o sum(T0).
+// zeroed: the outputs hold zeros already (raster_pack_kernel stored them).
 template <typename T>
 int raster_reduce_impl(const T *rows, const int32_t *emit_ids, int64_t n_isects, int64_t C,
                        int64_t N, const T *opac, const T *mus, T *v_xy_abs, T *v_xy,
-                       T *v_conic, T *v_opac, T *v_mu, r2s_stream_t st) {
+                       T *v_conic, T *v_opac, T *v_mu, r2s_stream_t st, bool zeroed = false) {
   const char *name = "rasterize_to_pixels_bwd (row reduction)";
   R2S_REQUIRE(C >= 0 && N >= 0 && C * N <= kInt32Max && n_isects >= 0 && n_isects <= kInt32Max,
               "%s: bad size", name);
@@ -1002,14 +1034,14 @@ int raster_reduce_impl(const T *rows, const int32_t *emit_ids, int64_t n_isects,
                            {nullptr, nullptr, nullptr, nullptr, nullptr, mus, nullptr, nullptr},
                            {nullptr, nullptr, nullptr, nullptr, nullptr, v_mu, nullptr, nullptr},
                            {nullptr, nullptr, nullptr, nullptr, nullptr, opac, nullptr, nullptr}};
-    launch_row_reduce(rows, emit_ids, n_isects, C * N, tg, stream);
+    launch_row_reduce(rows, emit_ids, n_isects, C * N, tg, stream, zeroed);
   } else {
     RowTargets<T, 6> tg = {{v_xy, v_xy + 1, v_conic, v_conic + 1, v_conic + 2, v_opac},
                            {2, 2, 3, 3, 3, 1},
                            {nullptr, nullptr, nullptr, nullptr, nullptr, mus},
                            {nullptr, nullptr, nullptr, nullptr, nullptr, v_mu},
                            {nullptr, nullptr, nullptr, nullptr, nullptr, opac}};
-    launch_row_reduce(rows, emit_ids, n_isects, C * N, tg, stream);
+    launch_row_reduce(rows, emit_ids, n_isects, C * N, tg, stream, zeroed);
   }
   return check_launch(name);
 }
@@ -1054,9 +1086,13 @@ int raster_bwd_impl(const T *means2d, const T *conics, const T *opac, const T *m
   }
   const uint32_t n_keys = static_cast<uint32_t>(C) * tw * th;
   hipStream_t stream = as_stream(st);
+  // The full two-pass call zeroes its outputs in the pack launch.
+  const bool zero_in_pack = two_pass && !rows_only;
   if (two_pass)
     raster_pack_kernel<T><<<dim3(static_cast<uint32_t>(ceil_div(C * N, 256))), dim3(256), 0,
-                            stream>>>(means2d, conics, opac, mus, C * N, payload);
+                            stream>>>(means2d, conics, opac, mus, C * N, payload,
+                                      zero_in_pack ? v_xy : nullptr, v_xy_abs, v_conic, v_opac,
+                                      v_mu);
   // 16-byte loads of gradient rows when every row segment starts aligned.
   const bool vec = vec_rows_ok<T>(v_image, W, ts);
 #define R2S_RASTER_BWD_R(RR, EXACT)                                                              \
@@ -1084,7 +1120,7 @@ int raster_bwd_impl(const T *means2d, const T *conics, const T *opac, const T *m
   R2S_RETURN_IF(check_launch(name));
   if (!two_pass || rows_only) return R2S_OK;
   return raster_reduce_impl<T>(rows, emit_ids, n_isects, C, N, opac, mus, v_xy_abs, v_xy,
-                               v_conic, v_opac, v_mu, st);
+                               v_conic, v_opac, v_mu, st, zero_in_pack);
 }
 
 // Device address of `scratch` on the current device, looked up once per

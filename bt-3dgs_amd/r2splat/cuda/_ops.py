@@ -95,6 +95,20 @@ def _end_bit(n_keys: int) -> int:
 _COUNT_HISTORY = {}
 _COUNT_HISTORY_LEN = 8
 _PINNED_COUNT = threading.local()  # per host thread: a count read back by one call at a time
+# The read-back copy runs on a second stream (default priority, one per host
+# thread and device) that waits for the count's scan, so the copy and its
+# completion signal sit beside the emit + sort instead of in front of them.
+_COPY_STREAM = threading.local()
+
+
+def _copy_stream(dev: torch.device) -> torch.cuda.Stream:
+    streams = getattr(_COPY_STREAM, "by_device", None)
+    if streams is None:
+        streams = _COPY_STREAM.by_device = {}
+    st = streams.get(dev.index)
+    if st is None:
+        st = streams[dev.index] = torch.cuda.Stream(device=dev)
+    return st
 
 
 def _note_count(key, n: int) -> None:
@@ -139,9 +153,14 @@ def _emit_and_sort(launch, offsets: Tensor, n_items: int, n_keys: int, op: str,
         host = pinned.get(dev.index)
         if host is None:
             host = pinned[dev.index] = torch.empty(1, dtype=torch.int64, pin_memory=True)
-        host.copy_(offsets[n_items:n_items + 1], non_blocking=True)
-        ready = torch.cuda.Event()
-        ready.record()
+        counted = torch.cuda.Event()
+        counted.record()
+        side = _copy_stream(dev)
+        with torch.cuda.stream(side):
+            side.wait_event(counted)
+            host.copy_(offsets[n_items:n_items + 1], non_blocking=True)
+            ready = torch.cuda.Event()
+            ready.record(side)
         launch(cap, end_bit, outs, ws)
         ready.synchronize()
         n = int(host[0])
