@@ -438,7 +438,7 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     const uint32_t *__restrict__ digit_offsets, uint32_t nblocks, uint32_t *__restrict__ keys_out,
     uint32_t *__restrict__ e_out, uint32_t *__restrict__ gid_out,
     int64_t *__restrict__ keys_out64, int32_t *__restrict__ vals_out32,
-    int32_t *__restrict__ src_out) {
+    int32_t *__restrict__ src_out, int32_t *__restrict__ tile_offsets, uint32_t n_keys) {
   static_assert(kDBits >= 8 && kDBits <= kMaxPassBits, "digit tables of 256 to 2048");
   constexpr int kD = 1 << kDBits;
   constexpr int kDPT = kD / kSortThreads;  // digits per thread in the scan
@@ -477,6 +477,16 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
   for (uint32_t j = 0; j < kDPT; ++j) {
     const uint32_t d = min(d0 + j, digits - 1u);
     gb[j] = digit_offsets[static_cast<int64_t>(d) * nblocks + tile];
+  }
+  // A single pass over the whole key (the caller passes tile_offsets only
+  // then): block 0's run starts are the numbers of records with a smaller
+  // key, i.e. each key's first index in the sorted list.
+  if (kFinal && tile_offsets != nullptr && tile == 0) {
+#pragma unroll
+    for (uint32_t j = 0; j < kDPT; ++j) {
+      const uint32_t d = d0 + j;
+      if (j < dk && d < n_keys) tile_offsets[d] = static_cast<int32_t>(gb[j]);
+    }
   }
 #pragma unroll
   for (int r = 0; r < kSortRounds; ++r) {
@@ -580,12 +590,17 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
 
 // ------------------------------------------------------------- offsets ---
 
+// n_dev: the record count on the device, at most n (else nothing is
+// written); null: n records.
 __global__ __launch_bounds__(256) void offset_encode_kernel(const int64_t *__restrict__ ids,
                                                             int64_t n, int64_t n_keys,
-                                                            int32_t *__restrict__ out) {
+                                                            int32_t *__restrict__ out,
+                                                            const int64_t *__restrict__ n_dev) {
   const int64_t k = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (k >= n_keys) return;
-  int64_t lo = 0, hi = n;
+  const int64_t nn = n_dev != nullptr ? *n_dev : n;
+  if (nn > n) return;
+  int64_t lo = 0, hi = nn;
   while (lo < hi) {
     const int64_t mid = (lo + hi) >> 1;
     if (ids[mid] < k)
@@ -665,12 +680,13 @@ int launch_scatter_sized(uint32_t bits, bool key16, const uint32_t *kin, const u
                          const uint32_t *gin, const int64_t *n_dev, int64_t cap, uint32_t shift,
                          const uint32_t *digit_offsets, uint32_t nb, uint32_t *kout,
                          uint32_t *eout, uint32_t *gout, int64_t *keys64, int32_t *vals32,
-                         int32_t *src, hipStream_t stream) {
+                         int32_t *src, int32_t *tile_offsets, uint32_t n_keys,
+                         hipStream_t stream) {
 #define R2S_SCATTER_SIZED(DB, K16)                                                              \
   radix_scatter_kernel<kFirst, kFinal, kTwo, DB, K16><<<dim3(nb), dim3(kSortThreads), 0,      \
                                                        stream>>>(                             \
       kin, ein, gin, n_dev, cap, shift, bits, digit_offsets, nb, kout, eout, gout, keys64,     \
-      vals32, src)
+      vals32, src, tile_offsets, n_keys)
   if (bits <= 8 && key16)
     R2S_SCATTER_SIZED(8, true);
   else if (kFirst && kFinal && bits <= 10 && key16)
@@ -686,11 +702,11 @@ int launch_scatter(bool first, bool last, bool two, uint32_t bits, bool key16,
                    const int64_t *n_dev, int64_t cap, uint32_t shift,
                    const uint32_t *digit_offsets, uint32_t nb, uint32_t *kout, uint32_t *eout,
                    uint32_t *gout, int64_t *keys64, int32_t *vals32, int32_t *src,
-                   hipStream_t stream) {
+                   int32_t *tile_offsets, uint32_t n_keys, hipStream_t stream) {
 #define R2S_SCATTER_PASS(F, L, T)                                                                \
   return launch_scatter_sized<F, L, T>(bits, key16, kin, ein, gin, n_dev, cap, shift,           \
                                        digit_offsets, nb, kout, eout, gout, keys64, vals32, src, \
-                                       stream)
+                                       tile_offsets, n_keys, stream)
   if (first && last) {
     if (two) R2S_SCATTER_PASS(true, true, true);
     R2S_SCATTER_PASS(true, true, false);
@@ -710,9 +726,13 @@ int launch_scatter(bool first, bool last, bool two, uint32_t bits, bool key16,
 
 // Sorts the emitted records (s.k0, s.gid0) into the final outputs: *n_dev
 // records, at most cap (the size s was carved for).  two: the emission
-// index travels too and the final pass writes it to src.
+// index travels too and the final pass writes it to src.  tile_offsets
+// (optional): each of the n_keys keys' first index in the sorted list, as
+// offset_encode_kernel computes it -- taken from a single pass's digit
+// offsets when one pass covers the key, else searched in the sorted keys.
 int radix_sort(SortSpace &s, const int64_t *n_dev, int64_t cap, uint32_t key_bits,
-               int64_t *keys64, int32_t *vals32, bool two, int32_t *src, hipStream_t stream) {
+               int64_t *keys64, int32_t *vals32, bool two, int32_t *src,
+               int32_t *tile_offsets, int64_t n_keys, hipStream_t stream) {
   const uint32_t passes = sort_passes(key_bits);
   const uint32_t pbits = max(1u, (key_bits + passes - 1) / passes);
   const uint32_t nb = static_cast<uint32_t>(s.nblocks);
@@ -733,10 +753,16 @@ int radix_sort(SortSpace &s, const int64_t *n_dev, int64_t cap, uint32_t key_bit
     uint32_t *gout = (p % 2 == 0) ? s.g1 : s.g0;
     R2S_RETURN_IF(launch_scatter(first, last, two, bits, key_bits <= 16, kin, ein, gin, n_dev,
                                  cap, shift, s.hist_scan, nb, kout, eout, gout, keys64, vals32,
-                                 src, stream));
+                                 src, passes == 1 ? tile_offsets : nullptr,
+                                 static_cast<uint32_t>(n_keys), stream));
     kin = kout;
     ein = eout;
     gin = gout;
+  }
+  if (tile_offsets != nullptr && passes > 1) {
+    offset_encode_kernel<<<dim3(static_cast<uint32_t>(ceil_div(n_keys, 256))), dim3(256), 0,
+                           stream>>>(keys64, cap, n_keys, tile_offsets, n_dev);
+    return check_launch("isect offsets");
   }
   return R2S_OK;
 }
@@ -823,14 +849,18 @@ template <typename T>
 int emit_sort_2d_impl(const T *means2d, const int32_t *radii, int rect, int64_t C, int64_t N,
                       uint32_t ts, uint32_t tw, uint32_t th, const int64_t *offsets,
                       int64_t n_isects, uint32_t end_bit, int64_t *keys, int32_t *vals,
-                      int32_t *emit_ids, int32_t *isect_src, void *ws, size_t ws_bytes,
-                      r2s_stream_t st) {
+                      int32_t *emit_ids, int32_t *isect_src, int32_t *tile_offsets, void *ws,
+                      size_t ws_bytes, r2s_stream_t st) {
   clear_error();
   const char *name = "isect_tiles";
   R2S_REQUIRE(C >= 0 && N >= 0 && C * N <= kInt32Max, "%s: bad size", name);
   R2S_REQUIRE(ts > 0, "%s: tile_size must be positive", name);
   R2S_RETURN_IF(check_sort_args(n_isects, end_bit, C * tw * th, ws, ws_bytes, keys, vals, name));
-  if (n_isects == 0) return R2S_OK;
+  const int64_t n_keys = C * tw * th;
+  if (n_isects == 0)
+    return tile_offsets == nullptr || n_keys == 0
+               ? R2S_OK
+               : device_fill<int32_t>(tile_offsets, n_keys, 0, as_stream(st), name);
   R2S_REQUIRE(means2d && radii && offsets, "%s: null pointer", name);
   hipStream_t stream = as_stream(st);
   Carver cv(ws);
@@ -843,16 +873,16 @@ int emit_sort_2d_impl(const T *means2d, const int32_t *radii, int rect, int64_t 
   emit_2d_kernel<T><<<dim3(static_cast<uint32_t>(ceil_div(M, 256))), dim3(256), 0, stream>>>(
       means2d, radii, rect, M, N, ts, tw, th, offsets, n_isects, s.k0, gids);
   R2S_RETURN_IF(check_launch(name));
-  return radix_sort(s, offsets + M, n_isects, key_bits_for(C * tw * th), keys, vals,
-                    emit_ids != nullptr, isect_src, stream);
+  return radix_sort(s, offsets + M, n_isects, key_bits_for(n_keys), keys, vals,
+                    emit_ids != nullptr, isect_src, tile_offsets, n_keys, stream);
 }
 
 template <typename T>
 int emit_sort_3d_impl(const T *means3d, const int32_t *radii, int64_t N, uint32_t ts,
                       uint32_t n2, uint32_t n1, uint32_t n0, uint32_t z0, uint32_t z1,
                       const int64_t *offsets, int64_t n_isects, uint32_t end_bit, int64_t *keys,
-                      int32_t *vals, int32_t *emit_ids, int32_t *isect_src, void *ws,
-                      size_t ws_bytes, r2s_stream_t st) {
+                      int32_t *vals, int32_t *emit_ids, int32_t *isect_src,
+                      int32_t *tile_offsets, void *ws, size_t ws_bytes, r2s_stream_t st) {
   clear_error();
   const char *name = "isect_tiles_3d";
   R2S_REQUIRE(N >= 0 && N <= kInt32Max, "%s: bad size", name);
@@ -861,7 +891,10 @@ int emit_sort_3d_impl(const T *means3d, const int32_t *radii, int64_t N, uint32_
               z1, n0);
   const int64_t n_keys = static_cast<int64_t>(n2) * n1 * (z1 - z0);
   R2S_RETURN_IF(check_sort_args(n_isects, end_bit, n_keys, ws, ws_bytes, keys, vals, name));
-  if (n_isects == 0) return R2S_OK;
+  if (n_isects == 0)
+    return tile_offsets == nullptr || n_keys == 0
+               ? R2S_OK
+               : device_fill<int32_t>(tile_offsets, n_keys, 0, as_stream(st), name);
   R2S_REQUIRE(means3d && radii && offsets, "%s: null pointer", name);
   hipStream_t stream = as_stream(st);
   Carver cv(ws);
@@ -874,7 +907,7 @@ int emit_sort_3d_impl(const T *means3d, const int32_t *radii, int64_t N, uint32_
       means3d, radii, N, ts, n2, n1, n0, z0, z1, offsets, n_isects, s.k0, gids);
   R2S_RETURN_IF(check_launch(name));
   return radix_sort(s, offsets + N, n_isects, key_bits_for(n_keys), keys, vals,
-                    emit_ids != nullptr, isect_src, stream);
+                    emit_ids != nullptr, isect_src, tile_offsets, n_keys, stream);
 }
 
 template <typename T>
@@ -925,11 +958,12 @@ int64_t r2s_isect_workspace_bytes(int64_t n_items, int64_t n_isects, uint32_t en
                                    int64_t C, int64_t N, uint32_t ts, uint32_t tw,            \
                                    uint32_t th, const int64_t *offsets, int64_t n_isects,     \
                                    uint32_t end_bit, int64_t *keys, int32_t *vals,            \
-                                   int32_t *emit_ids, int32_t *isect_src, void *ws,          \
-                                   size_t ws_bytes, r2s_stream_t st) {                        \
+                                   int32_t *emit_ids, int32_t *isect_src,                     \
+                                   int32_t *tile_offsets, void *ws, size_t ws_bytes,          \
+                                   r2s_stream_t st) {                                         \
     return r2s::emit_sort_2d_impl<T>(means2d, radii, rect, C, N, ts, tw, th, offsets,         \
-                                     n_isects, end_bit, keys, vals, emit_ids, isect_src, ws,  \
-                                     ws_bytes, st);                                           \
+                                     n_isects, end_bit, keys, vals, emit_ids, isect_src,      \
+                                     tile_offsets, ws, ws_bytes, st);                         \
   }                                                                                           \
   int r2s_isect_count_3d_##SUF(const T *means3d, const int32_t *radii, int64_t N,            \
                                uint32_t ts, uint32_t n2, uint32_t n1, uint32_t n0,            \
@@ -942,11 +976,12 @@ int64_t r2s_isect_workspace_bytes(int64_t n_items, int64_t n_isects, uint32_t en
                                    uint32_t ts, uint32_t n2, uint32_t n1, uint32_t n0,        \
                                    const int64_t *offsets, int64_t n_isects,                  \
                                    uint32_t end_bit, int64_t *keys, int32_t *vals,            \
-                                   int32_t *emit_ids, int32_t *isect_src, void *ws,          \
-                                   size_t ws_bytes, r2s_stream_t st) {                        \
+                                   int32_t *emit_ids, int32_t *isect_src,                     \
+                                   int32_t *tile_offsets, void *ws, size_t ws_bytes,          \
+                                   r2s_stream_t st) {                                         \
     return r2s::emit_sort_3d_impl<T>(means3d, radii, N, ts, n2, n1, n0, 0u, n0,               \
                                      offsets, n_isects, end_bit, keys, vals, emit_ids,        \
-                                     isect_src, ws, ws_bytes, st);                            \
+                                     isect_src, tile_offsets, ws, ws_bytes, st);              \
   }                                                                                           \
   int r2s_isect_layer_counts_3d_##SUF(const T *means3d, const int32_t *radii, int64_t N,     \
                                       uint32_t ts, uint32_t n2, uint32_t n1, uint32_t n0,     \
@@ -967,10 +1002,10 @@ int64_t r2s_isect_workspace_bytes(int64_t n_items, int64_t n_isects, uint32_t en
       const T *means3d, const int32_t *radii, int64_t N, uint32_t ts, uint32_t n2,            \
       uint32_t n1, uint32_t n0, uint32_t z0, uint32_t z1, const int64_t *offsets,             \
       int64_t n_isects, uint32_t end_bit, int64_t *keys, int32_t *vals, int32_t *emit_ids,    \
-      int32_t *isect_src, void *ws, size_t ws_bytes, r2s_stream_t st) {                       \
+      int32_t *isect_src, int32_t *tile_offsets, void *ws, size_t ws_bytes, r2s_stream_t st) { \
     return r2s::emit_sort_3d_impl<T>(means3d, radii, N, ts, n2, n1, n0, z0, z1, offsets,      \
-                                     n_isects, end_bit, keys, vals, emit_ids, isect_src, ws,  \
-                                     ws_bytes, st);                                           \
+                                     n_isects, end_bit, keys, vals, emit_ids, isect_src,      \
+                                     tile_offsets, ws, ws_bytes, st);                         \
   }
 
 R2S_BIN_API(f32, float)
@@ -988,7 +1023,7 @@ int r2s_isect_offset_encode(const int64_t *ids, int64_t n_isects, int64_t n_keys
   if (n_isects == 0) return r2s::device_fill<int32_t>(out, n_keys, 0, stream, "isect_offset_encode");
   R2S_REQUIRE(ids != nullptr, "isect_offset_encode: null isect_ids");
   r2s::offset_encode_kernel<<<dim3(static_cast<uint32_t>(r2s::ceil_div(n_keys, 256))), dim3(256), 0,
-                              stream>>>(ids, n_isects, n_keys, out);
+                              stream>>>(ids, n_isects, n_keys, out, nullptr);
   return r2s::check_launch("isect_offset_encode");
 }
 

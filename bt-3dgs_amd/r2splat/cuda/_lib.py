@@ -35,10 +35,10 @@ _FLOAT_OPS = {
                               _i64, _i64, _p],
     "isect_count_2d": [_p, _p, _i32, _i64, _i64, _u32, _u32, _u32, _p, _p, _p, _sz, _p],
     "isect_emit_sort_2d": [_p, _p, _i32, _i64, _i64, _u32, _u32, _u32, _p, _i64, _u32, _p, _p,
-                           _p, _p, _p, _sz, _p],
+                           _p, _p, _p, _p, _sz, _p],
     "isect_count_3d": [_p, _p, _i64, _u32, _u32, _u32, _u32, _p, _p, _p, _sz, _p],
     "isect_emit_sort_3d": [_p, _p, _i64, _u32, _u32, _u32, _u32, _p, _i64, _u32, _p, _p, _p,
-                           _p, _p, _sz, _p],
+                           _p, _p, _p, _sz, _p],
     "rasterize_fwd": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _u32, _u32, _u32, _u32, _u32,
                       _p, _p, _sz, _p],
     "rasterize_fwd_noalloc": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _u32, _u32, _u32, _u32,
@@ -67,7 +67,7 @@ _FLOAT_OPS = {
     "isect_count_3d_slab": [_p, _p, _i64, _u32, _u32, _u32, _u32, _u32, _u32, _p, _p, _p, _sz,
                             _p],
     "isect_emit_sort_3d_slab": [_p, _p, _i64, _u32, _u32, _u32, _u32, _u32, _u32, _p, _i64, _u32,
-                                _p, _p, _p, _p, _p, _sz, _p],
+                                _p, _p, _p, _p, _p, _p, _sz, _p],
     "voxelize_fwd_slab": [_p, _p, _p, _p, _p, _i64, _i64, _u32, _u32, _u32, _u32, _u32, _u32,
                           _u32, _u32, _p, _p],
     "voxelize_fwd_reach": [_p, _p, _p, _p, _p, _i64, _i64, _u32, _u32, _u32, _u32, _u32, _u32,
@@ -141,7 +141,7 @@ DENSIFY_MAX_WIDTH = 16
 
 SYMBOLS = sorted(list(_PLAIN) + [f"r2s_{n}_{s}" for n in _FLOAT_OPS for s in ("f32", "f64")])
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 
 def load(path: str = LIB_PATH) -> ctypes.CDLL:

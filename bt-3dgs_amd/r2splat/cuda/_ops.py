@@ -95,20 +95,6 @@ def _end_bit(n_keys: int) -> int:
 _COUNT_HISTORY = {}
 _COUNT_HISTORY_LEN = 8
 _PINNED_COUNT = threading.local()  # per host thread: a count read back by one call at a time
-# The read-back copy runs on a second stream (default priority, one per host
-# thread and device) that waits for the count's scan, so the copy and its
-# completion signal sit beside the emit + sort instead of in front of them.
-_COPY_STREAM = threading.local()
-
-
-def _copy_stream(dev: torch.device) -> torch.cuda.Stream:
-    streams = getattr(_COPY_STREAM, "by_device", None)
-    if streams is None:
-        streams = _COPY_STREAM.by_device = {}
-    st = streams.get(dev.index)
-    if st is None:
-        st = streams[dev.index] = torch.cuda.Stream(device=dev)
-    return st
 
 
 def _note_count(key, n: int) -> None:
@@ -153,14 +139,9 @@ def _emit_and_sort(launch, offsets: Tensor, n_items: int, n_keys: int, op: str,
         host = pinned.get(dev.index)
         if host is None:
             host = pinned[dev.index] = torch.empty(1, dtype=torch.int64, pin_memory=True)
-        counted = torch.cuda.Event()
-        counted.record()
-        side = _copy_stream(dev)
-        with torch.cuda.stream(side):
-            side.wait_event(counted)
-            host.copy_(offsets[n_items:n_items + 1], non_blocking=True)
-            ready = torch.cuda.Event()
-            ready.record(side)
+        host.copy_(offsets[n_items:n_items + 1], non_blocking=True)
+        ready = torch.cuda.Event()
+        ready.record()
         launch(cap, end_bit, outs, ws)
         ready.synchronize()
         n = int(host[0])
@@ -197,6 +178,10 @@ class TileLists(NamedTuple):
     flatten_ids: Tensor  # int32 ids in (key, emission) order
     emit_ids: Optional[Tensor]   # None when there are no records
     isect_src: Optional[Tensor]
+    # Each key's first index in the sorted list, as isect_offset_encode /
+    # isect_offset_encode_3d return it (written by the sort); None when
+    # there are no records.
+    tile_offsets: Optional[Tensor] = None
 
     @property
     def emission(self) -> Optional[Tuple[Tensor, Tensor]]:
@@ -562,15 +547,17 @@ def bin_tiles_2d(means2d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim1: i
         _call(f"r2s_isect_count_2d_{sfx}", _ptr(means2d), _ptr(radii), rect, C, N, ts, tw, th,
               _ptr(tiles_per_gauss), _ptr(offsets), _ptr(ws), ws.numel(), st)
 
+        tile_offsets = torch.empty((C, th, tw), dtype=torch.int32, device=dev)
+
         def launch(cap, end_bit, outs, ws):
             _call(f"r2s_isect_emit_sort_2d_{sfx}", _ptr(means2d), _ptr(radii), rect, C, N, ts,
-                  tw, th, _ptr(offsets), cap, end_bit, *[_ptr(t) for t in outs], _ptr(ws),
-                  ws.numel(), st)
+                  tw, th, _ptr(offsets), cap, end_bit, *[_ptr(t) for t in outs],
+                  _ptr(tile_offsets), _ptr(ws), ws.numel(), st)
 
         res = _emit_and_sort(launch, offsets, C * N, C * tw * th, "isect_tiles", dev, "2d")
     if res is None:
         return empty
-    return TileLists(tiles_per_gauss, *res)
+    return TileLists(tiles_per_gauss, *res, tile_offsets)
 
 
 def isect_tiles(means2d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim1: int,
@@ -629,10 +616,12 @@ def bin_tiles_3d(means3d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim2: i
         _call(f"r2s_isect_count_3d_{sfx}", _ptr(means3d), _ptr(radii), N, ts, n2, n1, n0,
               _ptr(tiles_per_gauss), _ptr(offsets), _ptr(ws), ws.numel(), st)
 
+        tile_offsets = torch.empty((n0, n1, n2), dtype=torch.int32, device=dev)
+
         def launch(cap, end_bit, outs, ws):
             _call(f"r2s_isect_emit_sort_3d_{sfx}", _ptr(means3d), _ptr(radii), N, ts, n2, n1,
-                  n0, _ptr(offsets), cap, end_bit, *[_ptr(t) for t in outs], _ptr(ws),
-                  ws.numel(), st)
+                  n0, _ptr(offsets), cap, end_bit, *[_ptr(t) for t in outs],
+                  _ptr(tile_offsets), _ptr(ws), ws.numel(), st)
 
         # IsectTiles3D.cpp:96 reads the count back here.
         res = _emit_and_sort(launch, offsets, N, n2 * n1 * n0, "isect_tiles_3d", dev, "3d",
@@ -641,7 +630,7 @@ def bin_tiles_3d(means3d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim2: i
         return None
     if res is None:
         return empty
-    return TileLists(tiles_per_gauss, *res)
+    return TileLists(tiles_per_gauss, *res, tile_offsets)
 
 
 def isect_tiles_3d(means3d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim2: int,
@@ -754,10 +743,9 @@ def bin_tiles_3d_slab(means3d: Tensor, radii: Tensor, tile_size: int, n_tiles_di
                 torch.empty((n,), dtype=torch.int32, device=dev))
         ws = _workspace(lib.r2s_isect_workspace_bytes(0, n, end_bit), dev)
         _call(f"r2s_isect_emit_sort_3d_slab_{sfx}", _ptr(means3d), _ptr(radii), N, ts, n2, n1, n0,
-              z0, z1, _ptr(offsets), n, end_bit, *[_ptr(t) for t in outs], _ptr(ws), ws.numel(),
-              st)
-        _call("r2s_isect_offset_encode", _ptr(outs[0]), n, n_keys, _ptr(offs), st)
-    return TileLists(tpg, *outs), offs
+              z0, z1, _ptr(offsets), n, end_bit, *[_ptr(t) for t in outs], _ptr(offs), _ptr(ws),
+              ws.numel(), st)
+    return TileLists(tpg, *outs, offs), offs
 
 
 def voxelize_slab(means3d: Tensor, conics: Tensor, opacities: Tensor, tile_offsets: Tensor,

@@ -116,8 +116,10 @@ class ImagePass:
             width, height, float(eps2d), float(radius_clip))
         across, down = _tiles_along(width, ts), _tiles_along(height, ts)
         lists = ops.bin_tiles_2d(means2d, radii, ts, across, down)
-        tile_offsets = ops.isect_offset_encode(lists.isect_ids, int(viewmats.shape[0]), across,
-                                               down)
+        tile_offsets = lists.tile_offsets
+        if tile_offsets is None:  # no records
+            tile_offsets = ops.isect_offset_encode(lists.isect_ids, int(viewmats.shape[0]),
+                                                   across, down)
         image = ops.rasterize_to_pixels_fwd(means2d, conics, weights, mus, tile_offsets,
                                             lists.flatten_ids, width, height, ts)
         return cls(width, height, ts, float(eps2d), viewmats, Ks, means2d, cov2d, conics, mus,
@@ -194,7 +196,9 @@ class VolumePass:
                 del slab_lists, slab_offsets
             return cls(d2, d1, d0, ts, float(eps3d), ranges, centers, means3d, conics, weights,
                        radii, None, None, volume, slabs)
-        tile_offsets = ops.isect_offset_encode_3d(lists.isect_ids, n2, n1, n0)
+        tile_offsets = lists.tile_offsets
+        if tile_offsets is None:  # no records
+            tile_offsets = ops.isect_offset_encode_3d(lists.isect_ids, n2, n1, n0)
         reach = None
         if ts == 8:  # the backward reuses the forward's culling
             volume, reach = ops.voxelize_with_reach(means3d, conics, weights, tile_offsets,

@@ -208,6 +208,12 @@ int r2s_isect_count_2d_f64(const double *means2d, const int32_t *radii,
  * of emitted record e and isect_src[r] the emission index of sorted record
  * r.  The two-pass backward kernels (r2s_rasterize_bwd_emit_*,
  * r2s_voxelize_bwd_emit_*) take them.
+ * tile_offsets (may be NULL; int32 [C*n_tiles_h*n_tiles_w]) receives what
+ * r2s_isect_offset_encode computes from the sorted isect_ids, in the same
+ * launch sequence: when one sort pass covers the key (at most 2048 keys) it
+ * is read off that pass's digit offsets at no extra cost, else searched in
+ * the sorted keys.  Not in the reference (whose isect_tiles returns no
+ * offsets); r2splat.ops uses it in place of a separate encode call.
  * n_isects is the capacity of the outputs and the size the workspace is
  * queried for; the kernels read the record count from offsets[C*N] on the
  * device and write nothing when it exceeds n_isects.  A caller may thus
@@ -220,7 +226,8 @@ int r2s_isect_emit_sort_2d_f32(const float *means2d, const int32_t *radii,
                                int64_t n_isects, uint32_t end_bit,
                                int64_t *isect_ids, int32_t *flatten_ids,
                                int32_t *emit_ids, int32_t *isect_src,
-                               void *workspace, size_t workspace_bytes,
+                               int32_t *tile_offsets, void *workspace,
+                               size_t workspace_bytes,
                                r2s_stream_t stream);
 int r2s_isect_emit_sort_2d_f64(const double *means2d, const int32_t *radii,
                                int radii_is_rect, int64_t C, int64_t N,
@@ -229,7 +236,8 @@ int r2s_isect_emit_sort_2d_f64(const double *means2d, const int32_t *radii,
                                int64_t n_isects, uint32_t end_bit,
                                int64_t *isect_ids, int32_t *flatten_ids,
                                int32_t *emit_ids, int32_t *isect_src,
-                               void *workspace, size_t workspace_bytes,
+                               int32_t *tile_offsets, void *workspace,
+                               size_t workspace_bytes,
                                r2s_stream_t stream);
 
 /* r2splat/cuda/csrc/IsectTiles3D.cpp:72-96 (3D count + cumsum):
@@ -256,7 +264,8 @@ int r2s_isect_emit_sort_3d_f32(const float *means3d, const int32_t *radii,
                                int64_t n_isects, uint32_t end_bit,
                                int64_t *isect_ids, int32_t *flatten_ids,
                                int32_t *emit_ids, int32_t *isect_src,
-                               void *workspace, size_t workspace_bytes,
+                               int32_t *tile_offsets, void *workspace,
+                               size_t workspace_bytes,
                                r2s_stream_t stream);
 int r2s_isect_emit_sort_3d_f64(const double *means3d, const int32_t *radii,
                                int64_t N, uint32_t tile_size,
@@ -265,7 +274,8 @@ int r2s_isect_emit_sort_3d_f64(const double *means3d, const int32_t *radii,
                                int64_t n_isects, uint32_t end_bit,
                                int64_t *isect_ids, int32_t *flatten_ids,
                                int32_t *emit_ids, int32_t *isect_src,
-                               void *workspace, size_t workspace_bytes,
+                               int32_t *tile_offsets, void *workspace,
+                               size_t workspace_bytes,
                                r2s_stream_t stream);
 
 /* Z-slab binning of large volumes.  IsectTiles3D.cpp:96-161 sizes one list
@@ -306,14 +316,16 @@ int r2s_isect_emit_sort_3d_slab_f32(const float *means3d, const int32_t *radii, 
                                     uint32_t n_tiles_d1, uint32_t n_tiles_d0, uint32_t z0,
                                     uint32_t z1, const int64_t *offsets, int64_t n_isects,
                                     uint32_t end_bit, int64_t *isect_ids, int32_t *flatten_ids,
-                                    int32_t *emit_ids, int32_t *isect_src, void *workspace,
+                                    int32_t *emit_ids, int32_t *isect_src,
+                                    int32_t *tile_offsets, void *workspace,
                                     size_t workspace_bytes, r2s_stream_t stream);
 int r2s_isect_emit_sort_3d_slab_f64(const double *means3d, const int32_t *radii, int64_t N,
                                     uint32_t tile_size, uint32_t n_tiles_d2,
                                     uint32_t n_tiles_d1, uint32_t n_tiles_d0, uint32_t z0,
                                     uint32_t z1, const int64_t *offsets, int64_t n_isects,
                                     uint32_t end_bit, int64_t *isect_ids, int32_t *flatten_ids,
-                                    int32_t *emit_ids, int32_t *isect_src, void *workspace,
+                                    int32_t *emit_ids, int32_t *isect_src,
+                                    int32_t *tile_offsets, void *workspace,
                                     size_t workspace_bytes, r2s_stream_t stream);
 
 /* IsectTiles.cpp:176-215 isect_offset_encode_tensor and

@@ -47,10 +47,10 @@ def test_invalid_arguments_are_rejected_without_a_device(lib):
                                    None, None, 0, None)
     assert rc == 1001 and b"tile_size" in lib.r2s_last_error()
     rc = lib.r2s_isect_emit_sort_2d_f32(None, None, 1, 1, 10, 16, 4, 4, None, 1 << 31, 5, None,
-                                        None, None, None, None, 0, None)
+                                        None, None, None, None, None, 0, None)
     assert rc == 1002  # beyond the int32 offset range
     rc = lib.r2s_isect_emit_sort_2d_f32(None, None, 1, 1, 10, 16, 4, 4, None, 100, 3, None, None,
-                                        None, None, None, 0, None)
+                                        None, None, None, None, 0, None)
     assert rc == 1001 and b"end_bit" in lib.r2s_last_error()
     rc = lib.r2s_voxelize_fwd_f32(None, None, None, None, None, 0, 1, 8, 8, 8, 11, 1, 1, 1, None,
                                   None)
@@ -108,7 +108,7 @@ def test_workspace_queries(lib):
     assert lib.r2s_mask_workspace_bytes(1_000_000) > 0
     buf = ctypes.create_string_buffer(16)
     rc = lib.r2s_isect_emit_sort_2d_f32(None, None, 1, 1, 10, 16, 4, 4, None, 100, 5, buf, buf,
-                                        None, None, buf, 16, None)
+                                        None, None, None, buf, 16, None)
     assert rc in (1001, 1004)
 
 

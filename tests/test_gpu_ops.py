@@ -132,6 +132,10 @@ def test_isect_tiles_bit_exact(rect, n_views):
     assert_equal(np32(fl), fl_o, "flatten_ids")
     off = W.isect_offset_encode(ids, n_views, tw, th)
     assert_equal(np32(off), binning.isect_offset_encode(ids_o, n_views, tw, th), "tile_offsets")
+    # The offsets the sort writes itself (r2splat.ops uses them).
+    lists = _ops.bin_tiles_2d(m2, radii, 16, tw, th)
+    assert_equal(np32(lists.tile_offsets), binning.isect_offset_encode(ids_o, n_views, tw, th),
+                 "sort tile_offsets")
 
 
 def test_isect_tiles_large_footprints_and_degenerate():
@@ -179,6 +183,9 @@ def test_isect_tiles_3d_bit_exact():
     assert_equal(np32(fl), fl_o, "flatten_ids")
     off = W.isect_offset_encode_3d(ids, n2, n1, n0)
     assert_equal(np32(off), binning.isect_offset_encode_3d(ids_o, n2, n1, n0), "tile_offsets")
+    lists = _ops.bin_tiles_3d(m3, r3, 8, n2, n1, n0)
+    assert_equal(np32(lists.tile_offsets), binning.isect_offset_encode_3d(ids_o, n2, n1, n0),
+                 "sort tile_offsets")
 
 
 @pytest.mark.parametrize("tiles,views", [((1, 1), 1), ((32, 32), 2), ((45, 46), 1)])
@@ -198,6 +205,11 @@ def test_isect_tiles_sort_widths(tiles, views):
     assert_equal(np32(fl), fl_o, "flatten_ids")
     off = W.isect_offset_encode(ids, views, tw, th)
     assert_equal(np32(off), binning.isect_offset_encode(ids_o, views, tw, th), "tile_offsets")
+    # From the one pass's digit offsets (1 and 2048 keys) or, with two
+    # passes, searched after the sort.
+    lists = _ops.bin_tiles_2d(m2.to(DEV), r.to(DEV), 16, tw, th)
+    assert_equal(np32(lists.tile_offsets), binning.isect_offset_encode(ids_o, views, tw, th),
+                 "sort tile_offsets")
 
 
 def test_isect_tiles_capacity_guess():
@@ -216,13 +228,17 @@ def test_isect_tiles_capacity_guess():
     guessed = []
     for scale in (20, 10, 60, 60, 5):
         r = torch.randint(0, scale, (1, N, 2), generator=g).int()
-        tpg, ids, fl = W.isect_tiles(m2.to(DEV), r.to(DEV), 16, 32, 32)
+        # isect_tiles' own steps, keeping the lists for their tile offsets.
+        binned = _ops.bin_tiles_2d(m2.to(DEV), r.to(DEV), 16, 32, 32)
+        _ops._remember_emission(binned, 1024)
+        tpg, ids, fl = binned.tiles_per_gauss, binned.isect_ids, binned.flatten_ids
         tpg_o, ids_o, fl_o = binning.isect_tiles(m2.numpy(), r.numpy(), 16, 32, 32)
         assert_equal(np32(tpg), tpg_o, "tiles_per_gauss")
         assert_equal(np32(ids), ids_o, "isect_ids")
         assert_equal(np32(fl), fl_o, "flatten_ids")
         guessed.append(ids.untyped_storage().nbytes() > 8 * ids.numel())
         off = W.isect_offset_encode(ids, 1, 32, 32)
+        assert torch.equal(binned.tile_offsets, off)
         args = (m2.to(DEV), con.to(DEV), op.to(DEV), mu.to(DEV), off)
         got = W.rasterize_to_pixels_bwd_per_gaussian(*args, ids, fl, v, 512, 512, 16, True)
         # The same records in exact-size tensors, with the same emission order.
@@ -250,6 +266,10 @@ def test_isect_tiles_3d_sort_widths(bricks):
     assert_equal(np32(tpg), tpg_o, "tiles_per_gauss")
     assert_equal(np32(ids), ids_o, "isect_ids")
     assert_equal(np32(fl), fl_o, "flatten_ids")
+    # Two or three passes: the sort searches its sorted keys for the offsets.
+    lists = _ops.bin_tiles_3d(m3.to(DEV), r3.to(DEV), 8, n2, n1, n0)
+    assert_equal(np32(lists.tile_offsets), binning.isect_offset_encode_3d(ids_o, n2, n1, n0),
+                 "sort tile_offsets")
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
