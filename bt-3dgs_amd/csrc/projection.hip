@@ -14,6 +14,7 @@
 #pragma clang fp contract(off)
 
 #include "r2s_common.h"
+#include "r2s_param.h"
 
 namespace r2s {
 namespace {
@@ -429,6 +430,69 @@ __global__ __launch_bounds__(256) void project_bwd_kernel(
   for (int k = 0; k < 6; ++k) v_covars[6 * g + k] = vs[k];
 }
 
+// The end of the explicit backward (r2splat.ops) in one pass per Gaussian:
+// the projection VJP summed over the views as project_bwd_kernel computes it
+// (conics / mu path), plus the volume pass's world-space gradients when
+// given (image + volume, the order in which a running sum of the two adds
+// them), stored as v_means; then the covariance gradient's
+// parameter-transform VJP (param_bwd_one, as param_bwd_kernel) and the
+// opacity VJP (as opacity_bwd_kernel) straight from registers.  The same
+// expressions in the same order, so the outputs are bit-identical to the
+// three kernels run in turn, without the v_covars round trip and two
+// launches.
+template <typename T>
+struct TailArgs {
+  const T *means, *covars, *viewmats, *Ks;
+  uint32_t width, height;
+  T eps;
+  const T *cov2d, *conics, *mus, *v_means2d, *v_conics, *v_mus;
+  const T *add_means, *add_covars;  // both or neither
+  const T *quats, *raw_scales;
+  T smin, smax;
+  const T *raw_opac, *v_opac_cn, *v_opac_3d;  // v_opac_3d may be null
+  T *v_means, *v_quats, *v_raw_scales, *v_raw_opac;
+  int64_t C, N;
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void explicit_tail_kernel(TailArgs<T> a) {
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (g >= a.N) return;
+  const T p[3] = {a.means[3 * g], a.means[3 * g + 1], a.means[3 * g + 2]};
+  T s[6];
+#pragma unroll
+  for (int k = 0; k < 6; ++k) s[k] = a.covars[6 * g + k];
+  T vp[3] = {0, 0, 0}, vs[6] = {0, 0, 0, 0, 0, 0};
+  for (int64_t cam = 0; cam < a.C; ++cam) {
+    const int64_t idx = cam * a.N + g;
+    const Camera<T> cm = load_camera(a.viewmats + 16 * cam, a.Ks + 9 * cam, a.width, a.height);
+    T cov[6], con[3], vcon[3], vcov[6];
+#pragma unroll
+    for (int k = 0; k < 6; ++k) cov[k] = a.cov2d[6 * idx + k];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      con[k] = a.conics[3 * idx + k];
+      vcon[k] = a.v_conics[3 * idx + k];
+    }
+    conic_mu_bwd_one(cov, a.eps, con, a.mus[idx], vcon, a.v_mus[idx], vcov);
+    project_bwd_one(cm, p, s, a.v_means2d[2 * idx], a.v_means2d[2 * idx + 1], vcov, vp, vs);
+  }
+  if (a.add_means != nullptr) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k) vp[k] = vp[k] + a.add_means[3 * g + k];
+#pragma unroll
+    for (int k = 0; k < 6; ++k) vs[k] = vs[k] + a.add_covars[6 * g + k];
+  }
+#pragma unroll
+  for (int k = 0; k < 3; ++k) a.v_means[3 * g + k] = vp[k];
+  param_bwd_one(a.quats + 4 * g, a.raw_scales + 3 * g, a.smin, a.smax, vs, a.v_quats + 4 * g,
+                a.v_raw_scales + 3 * g);
+  T v = 0;
+  for (int64_t c = 0; c < a.C; ++c) v += a.v_opac_cn[c * a.N + g];
+  if (a.v_opac_3d != nullptr) v += a.v_opac_3d[g];
+  a.v_raw_opac[g] = v * sigmoid(a.raw_opac[g]);
+}
+
 // ------------------------------------------------------------ host side --
 
 int check_sizes(int64_t C, int64_t N, const char *name) {
@@ -476,6 +540,32 @@ int project_bwd_impl(const T *means, const T *covars, const T *viewmats, const T
   project_bwd_kernel<T><<<dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, as_stream(stream)>>>(
       means, covars, viewmats, Ks, width, height, static_cast<T>(eps2d), cov2d, conics, mus,
       v_means2d, v_cov2d, v_conics, v_mus, v_means, v_covars, C, N);
+  return check_launch(name);
+}
+
+template <typename T>
+int explicit_tail_impl(TailArgs<T> a, double eps2d, double smin, double smax,
+                       r2s_stream_t stream) {
+  clear_error();
+  const char *name = "explicit_backward_tail";
+  R2S_RETURN_IF(check_sizes(a.C, a.N, name));
+  R2S_REQUIRE(a.C >= 1, "%s: needs at least one view", name);
+  if (a.N == 0) return R2S_OK;
+  R2S_REQUIRE(a.means && a.covars && a.viewmats && a.Ks && a.cov2d && a.conics && a.mus &&
+                  a.v_means2d && a.v_conics && a.v_mus,
+              "%s: null projection input", name);
+  R2S_REQUIRE((a.add_means == nullptr) == (a.add_covars == nullptr),
+              "%s: add_means and add_covars must be given together", name);
+  R2S_REQUIRE(a.quats && a.raw_scales && a.raw_opac && a.v_opac_cn, "%s: null parameter input",
+              name);
+  R2S_REQUIRE(a.v_means && a.v_quats && a.v_raw_scales && a.v_raw_opac, "%s: null output",
+              name);
+  a.eps = static_cast<T>(eps2d);
+  a.smin = static_cast<T>(smin);
+  a.smax = static_cast<T>(smax);
+  const int64_t blocks = ceil_div(a.N, 256);
+  explicit_tail_kernel<T><<<dim3(static_cast<uint32_t>(blocks)), dim3(256), 0,
+                            as_stream(stream)>>>(a);
   return check_launch(name);
 }
 
@@ -566,6 +656,20 @@ extern "C" {
                               r2s_stream_t st) {                                              \
     return r2s::conics_bwd_impl<T>(cov2d, eps, conics, mus, v_conics, v_mus, v_cov2d, total,  \
                                    st);                                                       \
+  }                                                                                           \
+  int r2s_explicit_backward_tail_##SUF(                                                       \
+      const T *means, const T *covars, const T *viewmats, const T *Ks, uint32_t width,        \
+      uint32_t height, double eps2d, const T *cov2d, const T *conics, const T *mus,           \
+      const T *v_means2d, const T *v_conics, const T *v_mus, const T *add_means,              \
+      const T *add_covars, const T *quats, const T *raw_scales, double smin, double smax,     \
+      const T *raw_opac, const T *v_opac_cn, const T *v_opac_3d, T *v_means, T *v_quats,      \
+      T *v_raw_scales, T *v_raw_opac, int64_t C, int64_t N, r2s_stream_t st) {                \
+    r2s::TailArgs<T> a{means,      covars,     viewmats,  Ks,        width,       height,      \
+                       T(0),       cov2d,      conics,    mus,       v_means2d,   v_conics,    \
+                       v_mus,      add_means,  add_covars, quats,    raw_scales,  T(0),        \
+                       T(0),       raw_opac,   v_opac_cn, v_opac_3d, v_means,     v_quats,     \
+                       v_raw_scales, v_raw_opac, C,       N};                                 \
+    return r2s::explicit_tail_impl<T>(a, eps2d, smin, smax, st);                              \
   }
 
 R2S_PROJ_API(f32, float)

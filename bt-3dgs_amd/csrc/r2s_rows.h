@@ -237,6 +237,11 @@ __global__ __launch_bounds__(256) void row_reduce_kernel(const T *__restrict__ r
   // slot for rows past the end (or with an id out of range).
   int32_t sr[K];
   T vr[K][NV];
+  // The ids just before and just after the wave's rows, loaded with the rows
+  // (each would otherwise be one more memory round trip of the wave).
+  const int64_t past = eb + kReduceWaveRows;
+  const int32_t before = (eb > 0) ? emit_ids[eb - 1] : -1;
+  const int32_t after = past < n ? emit_ids[past] : -1;
 #pragma unroll
   for (int r = 0; r < K; ++r) {
     const uint32_t q = 64u * r + lane;
@@ -280,7 +285,6 @@ __global__ __launch_bounds__(256) void row_reduce_kernel(const T *__restrict__ r
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
-  const int32_t before = (eb > 0) ? emit_ids[eb - 1] : -1;
   const int32_t seg_first = __shfl(g[0], 0, 64);
   const int32_t seg_last = __shfl(g[K - 1], 63, 64);
   // In-lane run sums, last row first: acc[k] = rows k .. the end of k's run
@@ -297,8 +301,7 @@ __global__ __launch_bounds__(256) void row_reduce_kernel(const T *__restrict__ r
   // Rows of the last segment beyond this wave (uniform branch and loop),
   // added to that segment's runs in lane 63.
   const bool tail_owned = seg_last >= 0 && !(seg_first == seg_last && before == seg_last);
-  const int64_t past = eb + kReduceWaveRows;
-  if (tail_owned && past < n && emit_ids[past] == seg_last) {
+  if (tail_owned && past < n && after == seg_last) {
     T carry[NV];
 #pragma unroll
     for (int c = 0; c < NV; ++c) carry[c] = 0;

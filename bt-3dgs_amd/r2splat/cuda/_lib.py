@@ -24,6 +24,8 @@ _FLOAT_OPS = {
     "parameter_transform_bwd": [_p, _p, _f64, _f64, _p, _p, _p, _i64, _p],
     "prepare_gaussians": [_p, _p, _p, _f64, _f64, _p, _p, _p, _i64, _p],
     "opacity_bwd": [_p, _p, _p, _p, _i64, _i64, _p],
+    "explicit_backward_tail": [_p, _p, _p, _p, _u32, _u32, _f64, _p, _p, _p, _p, _p, _p, _p, _p,
+                               _p, _p, _f64, _f64, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p],
     "world_to_image_projection_fwd": [_p, _p, _p, _p, _u32, _u32, _f32, _f32, _p, _p, _p,
                                       _i64, _i64, _p],
     "world_to_image_projection_bwd": [_p, _p, _p, _p, _u32, _u32, _p, _p, _p, _p, _i64, _i64, _p],
@@ -141,7 +143,7 @@ DENSIFY_MAX_WIDTH = 16
 
 SYMBOLS = sorted(list(_PLAIN) + [f"r2s_{n}_{s}" for n in _FLOAT_OPS for s in ("f32", "f64")])
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 
 def load(path: str = LIB_PATH) -> ctypes.CDLL:

@@ -514,6 +514,64 @@ def project_gaussians_bwd(means: Tensor, covars: Tensor, viewmats: Tensor, Ks: T
     return v_means, v_covars
 
 
+def explicit_backward_tail(means: Tensor, covars: Tensor, viewmats: Tensor, Ks: Tensor,
+                           img_w: int, img_h: int, eps2d: float, cov2d: Tensor, conics: Tensor,
+                           mus: Tensor, v_means2d: Tensor, v_conics: Tensor, v_mus: Tensor,
+                           add_means: Optional[Tensor], add_covars: Optional[Tensor],
+                           quats: Tensor, raw_scales: Tensor, scale_min: float,
+                           scale_max: float, raw_opacities: Tensor, v_opacity_cn: Tensor,
+                           v_opacity_3d: Optional[Tensor]
+                           ) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    """project_gaussians_bwd (plus add_means / add_covars), parameter_transform_bwd
+    of the summed covariance gradient and opacity_bwd in one pass:
+    (v_means [N,3], v_quats [N,4], v_raw_scales [N,3], v_raw_opacities [N]),
+    bit-identical to the three ops in turn (explicit.py:299-316,
+    ParameterTransformBwd.cu:66-245)."""
+    for t, n in ((means, "means"), (covars, "covars"), (viewmats, "viewmats"), (Ks, "Ks"),
+                 (cov2d, "cov2d_3x3"), (conics, "conics"), (mus, "mus"),
+                 (v_means2d, "v_means2d"), (v_conics, "v_conics"), (v_mus, "v_mus"),
+                 (quats, "quats"), (raw_scales, "raw_scales"),
+                 (raw_opacities, "raw_opacities"), (v_opacity_cn, "v_opacity_cn")):
+        _check_input(t, n)
+    C, N = _check_cameras(means, covars, viewmats, Ks)
+    _check(C >= 1, "explicit_backward_tail needs at least one view")
+    for t, shape, n in ((cov2d, (C, N, 6), "cov2d_3x3"), (conics, (C, N, 3), "conics"),
+                        (mus, (C, N), "mus"), (v_means2d, (C, N, 2), "v_means2d"),
+                        (v_conics, (C, N, 3), "v_conics"), (v_mus, (C, N), "v_mus"),
+                        (quats, (N, 4), "quats"), (raw_scales, (N, 3), "raw_scales"),
+                        (raw_opacities, (N,), "raw_opacities"),
+                        (v_opacity_cn, (C, N), "v_opacity_cn")):
+        _check(tuple(t.shape) == shape, f"{n} shape must be {list(shape)}")
+    _check((add_means is None) == (add_covars is None),
+           "add_means and add_covars must be given together")
+    for t, shape, n in ((add_means, (N, 3), "add_means"), (add_covars, (N, 6), "add_covars"),
+                        (v_opacity_3d, (N,), "v_opacity_3d")):
+        if t is not None:
+            _check_input(t, n)
+            _check(tuple(t.shape) == shape, f"{n} shape must be {list(shape)}")
+    dev, dt = means.device, means.dtype
+    for t in (covars, viewmats, Ks, cov2d, conics, mus, v_means2d, v_conics, v_mus, add_means,
+              add_covars, quats, raw_scales, raw_opacities, v_opacity_cn, v_opacity_3d):
+        _check(t is None or (t.dtype == dt and t.device == dev),
+               "explicit_backward_tail inputs must share one dtype and device")
+    v_means = torch.empty((N, 3), dtype=dt, device=dev)
+    v_quats = torch.empty((N, 4), dtype=dt, device=dev)
+    v_raw_scales = torch.empty((N, 3), dtype=dt, device=dev)
+    v_raw_opac = torch.empty((N,), dtype=dt, device=dev)
+    if N == 0:
+        return v_means, v_quats, v_raw_scales, v_raw_opac
+    sfx = _suffix(means, "explicit_backward_tail")
+    with torch.cuda.device(dev):
+        _call(f"r2s_explicit_backward_tail_{sfx}", _ptr(means), _ptr(covars), _ptr(viewmats),
+              _ptr(Ks), int(img_w), int(img_h), float(eps2d), _ptr(cov2d), _ptr(conics),
+              _ptr(mus), _ptr(v_means2d), _ptr(v_conics), _ptr(v_mus), _ptr(add_means),
+              _ptr(add_covars), _ptr(quats), _ptr(raw_scales), float(scale_min),
+              float(scale_max), _ptr(raw_opacities), _ptr(v_opacity_cn), _ptr(v_opacity_3d),
+              _ptr(v_means), _ptr(v_quats), _ptr(v_raw_scales), _ptr(v_raw_opac), C, N,
+              _stream(dev))
+    return v_means, v_quats, v_raw_scales, v_raw_opac
+
+
 # ---------------------------------------------------------------- binning --
 
 def bin_tiles_2d(means2d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim1: int,

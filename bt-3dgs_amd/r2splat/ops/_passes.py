@@ -72,6 +72,15 @@ class VolumeVJP(NamedTuple):
     v_weights: Tensor     # [N]
 
 
+class ParameterVJP(NamedTuple):
+    v_means: Tensor          # [N, 3], image + volume
+    v_quats: Tensor          # [N, 4]
+    v_raw_scales: Tensor     # [N, 3]
+    v_raw_opacities: Tensor  # [N]
+    v_means2d: Tensor        # [C, N, 2]
+    v_means2d_abs: Optional[Tensor]
+
+
 @dataclass(eq=False)
 class ImagePass:
     """Projection + rasterization of C views of N Gaussians.
@@ -135,6 +144,29 @@ class ImagePass:
             means.contiguous(), covars, self.viewmats, self.Ks, self.width, self.height,
             self.eps2d, self.cov2d, self.conics, self.mus, v_means2d, v_conics, v_mus)
         return ImageVJP(v_means, v_covars, v_weights, v_means2d, v_abs)
+
+    @torch.no_grad()
+    def vjp_to_parameters(self, v_image: Tensor, means: Tensor, covars: Tensor,
+                          volume: Optional["VolumeVJP"], quats: Tensor, raw_scales: Tensor,
+                          scale_min: float, scale_max: float,
+                          raw_opacities: Tensor) -> "ParameterVJP":
+        """The image's VJP carried through to the raw parameters, with the
+        volume pass's VJP (if any) added where the two meet: the raster
+        backward, then one kernel for the projection, parameter-transform
+        and opacity VJPs (bit-identical to vjp + parameter_transform_bwd +
+        opacity_bwd with the world-space gradients summed image + volume)."""
+        ops = _ops()
+        v_abs, v_means2d, v_conics, v_weights, v_mus = ops.raster_backward(
+            self.means2d, self.conics, self.weights, self.mus, self.tile_offsets, self.lists,
+            v_image.contiguous(), self.width, self.height, self.tile_size, self.absgrad)
+        v_means, v_quats, v_raw_scales, v_raw_opac = ops.explicit_backward_tail(
+            means.contiguous(), covars.contiguous(), self.viewmats, self.Ks, self.width,
+            self.height, self.eps2d, self.cov2d, self.conics, self.mus, v_means2d, v_conics,
+            v_mus, None if volume is None else volume.v_means.contiguous(),
+            None if volume is None else volume.v_covars.contiguous(), quats.contiguous(),
+            raw_scales.contiguous(), scale_min, scale_max, raw_opacities.contiguous(),
+            v_weights, None if volume is None else volume.v_weights.contiguous())
+        return ParameterVJP(v_means, v_quats, v_raw_scales, v_raw_opac, v_means2d, v_abs)
 
 
 @dataclass(eq=False)

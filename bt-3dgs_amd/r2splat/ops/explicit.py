@@ -175,38 +175,43 @@ def explicit_backward(
         raise RuntimeError("Explicit backward requires a projection forward pass.")
     from ..cuda._backend import _C
 
-    world_means = _Sum(means)
-    world_covars = _Sum(state.covars)
-    view_weights = volume_weights = None
+    volume_pass = state.voxel
+    g3 = None
+    if volume_pass is not None and volume_pass.volume.grad is not None:
+        g3 = volume_pass.vjp(volume_pass.volume.grad, means, state.covars)
 
-    if image_pass.image.grad is None:
+    if image_pass.image.grad is not None:
+        # The raster backward, then one kernel for the projection, parameter
+        # transform and opacity VJPs with the volume's gradients added where
+        # the world-space gradients meet (image + volume).
+        gp = image_pass.vjp_to_parameters(image_pass.image.grad, means, state.covars, g3,
+                                          quats, raw_scales, state.scale_min, state.scale_max,
+                                          raw_opacities)
+        image_pass.means2d.grad = gp.v_means2d
+        if image_pass.absgrad:
+            image_pass.means2d.absgrad = gp.v_means2d_abs
+        v_means, v_quats = gp.v_means, gp.v_quats
+        v_raw_scales, v_raw_opacities = gp.v_raw_scales, gp.v_raw_opacities
+    else:
         image_pass.means2d.grad = torch.zeros_like(image_pass.means2d)
         if image_pass.absgrad:
             image_pass.means2d.absgrad = torch.zeros_like(image_pass.means2d)
-    else:
-        g = image_pass.vjp(image_pass.image.grad, means, state.covars)
-        world_means.add(g.v_means)
-        world_covars.add(g.v_covars)
-        view_weights = g.v_weights
-        image_pass.means2d.grad = g.v_means2d
-        if image_pass.absgrad:
-            image_pass.means2d.absgrad = g.v_means2d_abs
+        world_means = _Sum(means)
+        world_covars = _Sum(state.covars)
+        volume_weights = None
+        if g3 is not None:
+            world_means.add(g3.v_means)
+            world_covars.add(g3.v_covars)
+            volume_weights = g3.v_weights
+        # Covariance -> (quaternion, raw scale) VJP; opacity: the volume's
+        # gradient times softplus' = sigmoid.
+        v_quats, v_raw_scales = _C.parameter_transform_bwd(
+            quats.contiguous(), raw_scales.contiguous(), state.scale_min, state.scale_max,
+            world_covars.get().contiguous())
+        v_raw_opacities = _C.opacity_bwd(raw_opacities.contiguous(), None, volume_weights)
+        v_means = world_means.get()
 
-    volume_pass = state.voxel
-    if volume_pass is not None and volume_pass.volume.grad is not None:
-        g3 = volume_pass.vjp(volume_pass.volume.grad, means, state.covars)
-        world_means.add(g3.v_means)
-        world_covars.add(g3.v_covars)
-        volume_weights = g3.v_weights
-
-    # Covariance -> (quaternion, raw scale) VJP; opacity: the views' and the
-    # volume's gradients summed, times softplus' = sigmoid (one kernel).
-    v_quats, v_raw_scales = _C.parameter_transform_bwd(
-        quats.contiguous(), raw_scales.contiguous(), state.scale_min, state.scale_max,
-        world_covars.get().contiguous())
-    v_raw_opacities = _C.opacity_bwd(raw_opacities.contiguous(), view_weights, volume_weights)
-
-    _add_to_grad(means, world_means.get())
+    _add_to_grad(means, v_means)
     _add_to_grad(quats, v_quats)
     _add_to_grad(raw_scales, v_raw_scales)
     _add_to_grad(raw_opacities, v_raw_opacities)

@@ -174,6 +174,35 @@ int r2s_project_gaussians_bwd_f64(
     double *v_means, double *v_covars, int64_t C, int64_t N,
     r2s_stream_t stream);
 
+/* The end of r2splat.ops' explicit backward in one pass per Gaussian, for
+ * C >= 1 views: r2s_project_gaussians_bwd_* (explicit.py:299-316), plus
+ * add_means [N,3] / add_covars [N,6] when given (the volume pass's
+ * world-space gradients; both or neither), stored as v_means [N,3]; then
+ * r2s_parameter_transform_bwd_* of that covariance gradient
+ * (ParameterTransformBwd.cu:66-245) -> v_quats [N,4], v_raw_scales [N,3];
+ * and r2s_opacity_bwd_* -> v_raw_opac [N] from v_opac_cn [C,N] and
+ * v_opac_3d [N] (may be NULL).  Bit-identical to those three calls in turn
+ * with v_covars = image + volume.  No reference counterpart (the reference
+ * runs them as separate autograd nodes). */
+int r2s_explicit_backward_tail_f32(
+    const float *means, const float *covars, const float *viewmats, const float *Ks,
+    uint32_t width, uint32_t height, double eps2d, const float *cov2d,
+    const float *conics, const float *mus, const float *v_means2d,
+    const float *v_conics, const float *v_mus, const float *add_means,
+    const float *add_covars, const float *quats, const float *raw_scales, double smin,
+    double smax, const float *raw_opac, const float *v_opac_cn, const float *v_opac_3d,
+    float *v_means, float *v_quats, float *v_raw_scales, float *v_raw_opac, int64_t C,
+    int64_t N, r2s_stream_t stream);
+int r2s_explicit_backward_tail_f64(
+    const double *means, const double *covars, const double *viewmats, const double *Ks,
+    uint32_t width, uint32_t height, double eps2d, const double *cov2d,
+    const double *conics, const double *mus, const double *v_means2d,
+    const double *v_conics, const double *v_mus, const double *add_means,
+    const double *add_covars, const double *quats, const double *raw_scales, double smin,
+    double smax, const double *raw_opac, const double *v_opac_cn, const double *v_opac_3d,
+    double *v_means, double *v_quats, double *v_raw_scales, double *v_raw_opac, int64_t C,
+    int64_t N, r2s_stream_t stream);
+
 /* ---------------------------------------------------------------------- */
 /* Tile binning                                                           */
 /* ---------------------------------------------------------------------- */

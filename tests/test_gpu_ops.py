@@ -116,6 +116,39 @@ def test_projection_bit_exact(dtype, n_views):
     assert_equal(np32(fvc), vcovaro, "fused v_covars")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("n_views", [1, 3])
+@pytest.mark.parametrize("with_volume", [False, True])
+def test_explicit_backward_tail_equals_the_three_ops(dtype, n_views, with_volume):
+    # One kernel for project_gaussians_bwd (+ the volume's world-space
+    # gradients), parameter_transform_bwd and opacity_bwd: bit-identical to
+    # the three ops in turn, with v_covars = image + volume.
+    d = _prepared(4000, 5, dtype, n_det=96, n_views=n_views)
+    raw = d["raw"]
+    quats = raw.quats.to(dtype).to(DEV).contiguous()
+    scales = raw.raw_scales.to(dtype).to(DEV).contiguous()
+    ropac = raw.raw_opacities.to(dtype).to(DEV).contiguous()
+    m2, c2, r, con, mu, op = W.project_gaussians_fwd(d["means"], d["covars"], d["opac"],
+                                                     d["viewmats"], d["Ks"], 96, 96, 1e-8, 3.0)
+    g = torch.Generator().manual_seed(17)
+    C, N = n_views, 4000
+    rnd = lambda *shape: torch.randn(*shape, generator=g, dtype=dtype).to(DEV)  # noqa: E731
+    vm2, vcon, vmu, vop = rnd(C, N, 2), rnd(C, N, 3), rnd(C, N), rnd(C, N)
+    add_m, add_c, vop3 = (rnd(N, 3), rnd(N, 6), rnd(N)) if with_volume else (None, None, None)
+    got = _ops.explicit_backward_tail(d["means"], d["covars"], d["viewmats"], d["Ks"], 96, 96,
+                                      1e-8, c2, con, mu, vm2, vcon, vmu, add_m, add_c, quats,
+                                      scales, 5e-4, 1.0, ropac, vop, vop3)
+    vm, vc = _ops.project_gaussians_bwd(d["means"], d["covars"], d["viewmats"], d["Ks"], 96, 96,
+                                        1e-8, c2, con, mu, vm2, vcon, vmu)
+    if with_volume:
+        vm, vc = vm + add_m, vc + add_c
+    vq, vs = _ops.parameter_transform_bwd(quats, scales, 5e-4, 1.0, vc)
+    vo = _ops.opacity_bwd(ropac, vop, vop3)
+    for a, b, n in zip(got, (vm, vq, vs, vo), ("v_means", "v_quats", "v_raw_scales", "v_raw_opac")):
+        assert torch.equal(a, b), n
+    assert float(vq.abs().max()) > 0 and float(vo.abs().max()) > 0
+
+
 @pytest.mark.parametrize("rect", [True, False])
 @pytest.mark.parametrize("n_views", [1, 2])
 def test_isect_tiles_bit_exact(rect, n_views):
