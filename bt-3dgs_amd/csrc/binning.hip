@@ -112,31 +112,60 @@ __device__ __forceinline__ uint32_t box_3d(const T *__restrict__ means3d,
 }
 
 // --------------------------------------------------------------- count ---
+//
+// The count kernels cover the scan's tiles (r2s_scan.h: kScanTile items per
+// block) and store each block's count sum into the scan's block sums, so the
+// exclusive scan of the counts needs only its downsweep (one launch fewer).
+// kCountThreads threads per block (item k kCountThreads + t to thread t):
+// enough waves in flight to hide the gathers' latency.
+constexpr int kCountThreads = 1024;
+constexpr int kCountItems = kScanTile / kCountThreads;
 
 template <typename T>
-__global__ __launch_bounds__(256) void count_2d_kernel(const T *__restrict__ means2d,
-                                                       const int32_t *__restrict__ radii,
-                                                       int rect, int64_t M, uint32_t ts,
-                                                       uint32_t tw, uint32_t th,
-                                                       int32_t *__restrict__ counts) {
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (idx >= M) return;
-  Rect r;
-  counts[idx] = static_cast<int32_t>(rect_2d(means2d, radii, rect, idx, ts, tw, th, r));
+__global__ __launch_bounds__(kCountThreads) void count_2d_kernel(
+    const T *__restrict__ means2d, const int32_t *__restrict__ radii, int rect, int64_t M,
+    uint32_t ts, uint32_t tw, uint32_t th, int32_t *__restrict__ counts,
+    int64_t *__restrict__ block_sums) {
+  __shared__ int64_t lds[kCountThreads / 64];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile + threadIdx.x;
+  int64_t s = 0;
+#pragma unroll
+  for (int k = 0; k < kCountItems; ++k) {
+    const int64_t idx = base + k * kCountThreads;
+    if (idx < M) {
+      Rect r;
+      const uint32_t c = rect_2d(means2d, radii, rect, idx, ts, tw, th, r);
+      counts[idx] = static_cast<int32_t>(c);
+      s += c;
+    }
+  }
+  int64_t total;
+  block_exclusive_scan(s, lds, total);
+  if (threadIdx.x == 0) block_sums[blockIdx.x] = total;
 }
 
 template <typename T>
-__global__ __launch_bounds__(256) void count_3d_kernel(const T *__restrict__ means3d,
-                                                       const int32_t *__restrict__ radii,
-                                                       int64_t N, uint32_t ts, uint32_t n2,
-                                                       uint32_t n1, uint32_t n0, uint32_t z0,
-                                                       uint32_t z1,
-                                                       int32_t *__restrict__ counts) {
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (idx >= N) return;
+__global__ __launch_bounds__(kCountThreads) void count_3d_kernel(
+    const T *__restrict__ means3d, const int32_t *__restrict__ radii, int64_t N, uint32_t ts,
+    uint32_t n2, uint32_t n1, uint32_t n0, uint32_t z0, uint32_t z1,
+    int32_t *__restrict__ counts, int64_t *__restrict__ block_sums) {
+  __shared__ int64_t lds[kCountThreads / 64];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile + threadIdx.x;
   const uint32_t n[3] = {n2, n1, n0};
-  Box b;
-  counts[idx] = static_cast<int32_t>(box_3d(means3d, radii, idx, ts, n, z0, z1, b));
+  int64_t s = 0;
+#pragma unroll
+  for (int k = 0; k < kCountItems; ++k) {
+    const int64_t idx = base + k * kCountThreads;
+    if (idx < N) {
+      Box b;
+      const uint32_t c = box_3d(means3d, radii, idx, ts, n, z0, z1, b);
+      counts[idx] = static_cast<int32_t>(c);
+      s += c;
+    }
+  }
+  int64_t total;
+  block_exclusive_scan(s, lds, total);
+  if (threadIdx.x == 0) block_sums[blockIdx.x] = total;
 }
 
 // Records per brick layer: each Gaussian's box adds its (dim2, dim1) area to
@@ -796,11 +825,11 @@ int count_2d_impl(const T *means2d, const int32_t *radii, int rect, int64_t C, i
   R2S_RETURN_IF(check_workspace(ws, ws_bytes, count_space_bytes(M), name));
   Carver cv(ws);
   int64_t *partials = cv.take<int64_t>(scan_partials_count(M));
-  count_2d_kernel<T><<<dim3(static_cast<uint32_t>(ceil_div(M, 256))), dim3(256), 0, stream>>>(
-      means2d, radii, rect, M, ts, tw, th, counts);
+  count_2d_kernel<T><<<dim3(static_cast<uint32_t>(ceil_div(M, kScanTile))), dim3(kCountThreads),
+                      0, stream>>>(means2d, radii, rect, M, ts, tw, th, counts, partials);
   R2S_RETURN_IF(check_launch(name));
-  return device_exclusive_scan<int32_t, int64_t>(counts, M, offsets, offsets + M, partials,
-                                                 stream, name);
+  return device_exclusive_scan_from_sums<int32_t, int64_t>(counts, M, offsets, offsets + M,
+                                                           partials, stream, name);
 }
 
 template <typename T>
@@ -822,11 +851,11 @@ int count_3d_impl(const T *means3d, const int32_t *radii, int64_t N, uint32_t ts
   R2S_RETURN_IF(check_workspace(ws, ws_bytes, count_space_bytes(N), name));
   Carver cv(ws);
   int64_t *partials = cv.take<int64_t>(scan_partials_count(N));
-  count_3d_kernel<T><<<dim3(static_cast<uint32_t>(ceil_div(N, 256))), dim3(256), 0, stream>>>(
-      means3d, radii, N, ts, n2, n1, n0, z0, z1, counts);
+  count_3d_kernel<T><<<dim3(static_cast<uint32_t>(ceil_div(N, kScanTile))), dim3(kCountThreads),
+                      0, stream>>>(means3d, radii, N, ts, n2, n1, n0, z0, z1, counts, partials);
   R2S_RETURN_IF(check_launch(name));
-  return device_exclusive_scan<int32_t, int64_t>(counts, N, offsets, offsets + N, partials,
-                                                 stream, name);
+  return device_exclusive_scan_from_sums<int32_t, int64_t>(counts, N, offsets, offsets + N,
+                                                           partials, stream, name);
 }
 
 int check_sort_args(int64_t n_isects, uint32_t end_bit, int64_t n_keys, void *ws,

@@ -139,18 +139,18 @@ int device_fill(T *p, int64_t n, T v, hipStream_t stream, const char *what) {
   return check_launch(what);
 }
 
-// out[i] = sum_{j<i} in[j] for i < n; *total = sum of all (if not null).
-// `partials` must hold scan_partials_count(n) elements.
 template <typename Tin, typename Tout>
 int device_exclusive_scan(const Tin *in, int64_t n, Tout *out, Tout *total, Tout *partials,
-                          hipStream_t stream, const char *what) {
+                          hipStream_t stream, const char *what);
+
+// The downsweep of device_exclusive_scan, for a caller whose kernel already
+// stored the block sums (partials[b] = the sum of items [b kScanTile,
+// (b + 1) kScanTile), as scan_reduce_kernel does).  n > 0.
+template <typename Tin, typename Tout>
+int device_exclusive_scan_from_sums(const Tin *in, int64_t n, Tout *out, Tout *total,
+                                    Tout *partials, hipStream_t stream, const char *what) {
   const int64_t nb = ceil_div(n, kScanTile);
-  if (nb <= 0) {
-    if (total != nullptr) return device_fill<Tout>(total, 1, static_cast<Tout>(0), stream, what);
-    return R2S_OK;
-  }
   const dim3 grid(static_cast<uint32_t>(nb)), block(kScanThreads);
-  scan_reduce_kernel<Tin, Tout><<<grid, block, 0, stream>>>(in, n, partials);
   if (nb <= kScanDirectBlocks) {
     scan_down_kernel<Tin, Tout, false><<<grid, block, 0, stream>>>(in, n, partials, out, total);
     return check_launch(what);
@@ -161,6 +161,22 @@ int device_exclusive_scan(const Tin *in, int64_t n, Tout *out, Tout *total, Tout
                                                    partials + 2 * nb, stream, what)));
   scan_down_kernel<Tin, Tout, true><<<grid, block, 0, stream>>>(in, n, partials + nb, out, total);
   return check_launch(what);
+}
+
+// out[i] = sum_{j<i} in[j] for i < n; *total = sum of all (if not null).
+// `partials` must hold scan_partials_count(n) elements.
+template <typename Tin, typename Tout>
+int device_exclusive_scan(const Tin *in, int64_t n, Tout *out, Tout *total, Tout *partials,
+                          hipStream_t stream, const char *what) {
+  const int64_t nb = ceil_div(n, kScanTile);
+  if (nb <= 0) {
+    if (total != nullptr) return device_fill<Tout>(total, 1, static_cast<Tout>(0), stream, what);
+    return R2S_OK;
+  }
+  scan_reduce_kernel<Tin, Tout><<<dim3(static_cast<uint32_t>(nb)), dim3(kScanThreads), 0,
+                                  stream>>>(in, n, partials);
+  R2S_RETURN_IF(check_launch(what));
+  return device_exclusive_scan_from_sums<Tin, Tout>(in, n, out, total, partials, stream, what);
 }
 
 }  // namespace r2s
