@@ -718,6 +718,8 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
   constexpr int kq = Quad<T>::n;
   __shared__ WordMajor<ChunkRecord<T>, 64> s_rec[kChunkWaves];
   __shared__ uint64_t s_rows[kChunkWaves][64];  // reached rows: bit 8 * slice + row
+  // Per record, byte li: the reached rows of the slices before li (0..56).
+  __shared__ uint64_t s_pref[kChunkWaves][64];
   __shared__ T s_acc[kChunkWaves][10][64];
   __shared__ uint16_t s_chunk[kChunkWaves][64 * R];
   const uint32_t w = wave_index(), lane = lane_id();
@@ -787,6 +789,14 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
     cr.n_items = n_items;
     s_rec[w].store(static_cast<int>(lane), cr);
     s_rows[w][lane] = reached;
+    uint64_t pref = 0;
+    uint32_t run = 0;
+#pragma unroll
+    for (int li = 0; li < R; ++li) {
+      pref |= static_cast<uint64_t>(run) << (8 * li);
+      run += static_cast<uint32_t>(__popc(static_cast<uint32_t>(reached >> (8 * li)) & 0xFFu));
+    }
+    s_pref[w][lane] = pref;
 #pragma unroll
     for (int c = 0; c < 10; ++c) s_acc[w][c][lane] = 0;
   }
@@ -817,17 +827,22 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
     const uint32_t rl = ent & 63u, q = ent >> 6;
     const ChunkRecord<T> cr = s_rec[w].load(static_cast<int>(rl));
     const uint64_t rows_m = s_rows[w][rl];
-    // The chunk's first item, the (8 q)-th set bit: its slice by the
-    // running bit counts of the slice bytes; within a slice the reached rows
+    // The chunk's first item, the t-th set bit (t = 8 q): its slice li is the
+    // last whose byte of s_pref (reached rows before it) is <= t, found for
+    // all eight bytes at once (each byte | 0x80, minus t + 1, keeps its high
+    // bit exactly when the byte exceeds t); within a slice the reached rows
     // are contiguous.
-    int pos = 64, rem = static_cast<int>(q) * R;
-#pragma unroll
-    for (int li = 0; li < R; ++li) {
+    int pos = 64;
+    {
+      const uint64_t pref = s_pref[w][rl];
+      const uint32_t t = q * static_cast<uint32_t>(R);
+      constexpr uint64_t kHigh = 0x8080808080808080ull, kOnes = 0x0101010101010101ull;
+      const uint64_t above = ((pref | kHigh) - static_cast<uint64_t>(t + 1u) * kOnes) & kHigh;
+      const int li = 7 - __popcll(above);
       const uint32_t byte = static_cast<uint32_t>(rows_m >> (8 * li)) & 0xFFu;
-      const int c = __popc(byte);
-      const bool here = pos == 64 && rem < c;
-      pos = here ? 8 * li + static_cast<int>(__builtin_ctz(byte | 0x100u)) + rem : pos;
-      rem -= (pos == 64) ? c : 0;
+      const uint32_t before = static_cast<uint32_t>(pref >> (8 * li)) & 0xFFu;
+      if (act) pos = 8 * li + static_cast<int>(__builtin_ctz(byte | 0x100u)) +
+                     static_cast<int>(t - before);
     }
     const int n_here = act ? min(R, cr.n_items - static_cast<int>(q) * R) : 0;
     const T cdx0 = (static_cast<T>(cr.ok) + half) - cr.m[0];
