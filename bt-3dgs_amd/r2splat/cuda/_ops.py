@@ -55,13 +55,27 @@ def _ptr(t: Optional[Tensor]):
     return None if t is None else t.data_ptr()
 
 
+# The current stream's handle without building a torch Stream object per call
+# (torch's raw accessor where this build has it).
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(device: torch.device):
+    if _RAW_STREAM is not None:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        return _RAW_STREAM(idx)
     return torch.cuda.current_stream(device).cuda_stream
+
+
+_FUNCS = {}  # entry point name -> (library, its ctypes function)
 
 
 def _call(name: str, *args) -> None:
     lib = _lib()
-    rc = getattr(lib, name)(*args)
+    hit = _FUNCS.get(name)
+    if hit is None or hit[0] is not lib:
+        hit = _FUNCS[name] = (lib, getattr(lib, name))
+    rc = hit[1](*args)
     if rc != 0:
         msg = lib.r2s_last_error().decode(errors="replace")
         raise RuntimeError(f"{name} failed ({rc}): {msg}")
