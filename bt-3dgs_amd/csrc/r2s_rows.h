@@ -237,11 +237,16 @@ __global__ __launch_bounds__(256) void row_reduce_kernel(const T *__restrict__ r
   // slot for rows past the end (or with an id out of range).
   int32_t sr[K];
   T vr[K][NV];
-  // The ids just before and just after the wave's rows, loaded with the rows
-  // (each would otherwise be one more memory round trip of the wave).
+  // The id just before the wave's rows, and the first 64 rows after them
+  // with their ids (the last Gaussian nearly always continues there, and
+  // the tail gather below starts from them), loaded with the wave's rows:
+  // each would otherwise be one more memory round trip of the wave.
   const int64_t past = eb + kReduceWaveRows;
   const int32_t before = (eb > 0) ? emit_ids[eb - 1] : -1;
-  const int32_t after = past < n ? emit_ids[past] : -1;
+  const int64_t t_e = past + lane;
+  const int32_t t_id = t_e < n ? emit_ids[t_e] : -1;
+  T t_row[NV];
+  load_row(rows, t_e < n ? t_e : eb, t_row);
 #pragma unroll
   for (int r = 0; r < K; ++r) {
     const uint32_t q = 64u * r + lane;
@@ -301,16 +306,24 @@ __global__ __launch_bounds__(256) void row_reduce_kernel(const T *__restrict__ r
   // Rows of the last segment beyond this wave (uniform branch and loop),
   // added to that segment's runs in lane 63.
   const bool tail_owned = seg_last >= 0 && !(seg_first == seg_last && before == seg_last);
+  const int32_t after = __shfl(t_id, 0, 64);
   if (tail_owned && past < n && after == seg_last) {
     T carry[NV];
 #pragma unroll
     for (int c = 0; c < NV; ++c) carry[c] = 0;
     for (int64_t base = past; base < n; base += 64) {
       const int64_t e2 = base + lane;
-      const bool take = e2 < n && emit_ids[e2] == seg_last;
+      const bool first = base == past;  // uniform: the prefetched rows
+      const int32_t id2 = first ? t_id : (e2 < n ? emit_ids[e2] : -1);
+      const bool take = e2 < n && id2 == seg_last;
       if (take) {
         T wv[NV];
-        load_row(rows, e2, wv);
+        if (first) {
+#pragma unroll
+          for (int c = 0; c < NV; ++c) wv[c] = t_row[c];
+        } else {
+          load_row(rows, e2, wv);
+        }
 #pragma unroll
         for (int c = 0; c < NV; ++c) carry[c] += wv[c];
       }
@@ -342,25 +355,57 @@ __global__ __launch_bounds__(256) void row_reduce_kernel(const T *__restrict__ r
   const int32_t next_first_all = __shfl_down(g[0], 1, 64);
   const int32_t next_first = lane < 63 ? next_first_all : -1;
   const int32_t prev_last = __shfl_up(g[K - 1], 1, 64);
+  bool head[K];
+  uint32_t n_heads = 0;
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     const int32_t p = k > 0 ? g[k - 1] : (lane == 0 ? before : prev_last);
-    const bool head = g[k] >= 0 && p != g[k];
-    // The Gaussian's total: its run in this lane, and, when that run reaches
-    // the lane's end, the following lanes' share.
-    T tot[NV];
+    head[k] = g[k] >= 0 && p != g[k];
+    n_heads += head[k] ? 1u : 0u;
+    // The Gaussian's total (kept in acc[k]): its run in this lane, and, when
+    // that run reaches the lane's end, the following lanes' share.
     const bool onward = g[K - 1] == g[k] && next_first == g[k];
 #pragma unroll
     for (int c = 0; c < NV; ++c)
-      tot[c] = k == 0 ? lead[c] : acc[k][c] + (onward ? next[c] : static_cast<T>(0));
-    if (head) {
-      const int64_t gi = g[k];
+      acc[k][c] = k == 0 ? lead[c] : acc[k][c] + (onward ? next[c] : static_cast<T>(0));
+  }
+  // Stored in place, the heads (scattered over the lanes and their four rows)
+  // would take 4 NV store instructions with a few active lanes each.  The
+  // wave numbers its heads in row order (= Gaussian order), stages each
+  // head's id and totals in the transpose buffers (free now), and stores
+  // them with consecutive heads on consecutive lanes, kReduceStage heads a
+  // round (one round unless the wave's 256 rows hold more Gaussians).
+  const uint32_t incl = wave_inclusive_scan(n_heads);
+  const uint32_t h_total = readlane_u32(incl, 63);
+#pragma unroll 1
+  for (uint32_t r0 = 0; r0 < h_total; r0 += kReduceStage) {  // uniform
+    uint32_t h = incl - n_heads;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      if (head[k] && h >= r0 && h < r0 + kReduceStage) {
+        const uint32_t slot = h - r0;
+        s_seg[w][slot] = g[k];
+#pragma unroll
+        for (int c = 0; c < NV; ++c) s_val[w][c][slot] = acc[k][c];
+      }
+      h += head[k] ? 1u : 0u;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const uint32_t cnt = min(h_total - r0, static_cast<uint32_t>(kReduceStage));
+    for (uint32_t q = lane; q < cnt; q += 64) {
+      const int64_t gi = s_seg[w][q];
 #pragma unroll
       for (int c = 0; c < NV; ++c) {
-        tg.ptr[c][gi * tg.stride[c]] = tg.scale[c] != nullptr ? tot[c] * tg.scale[c][gi] : tot[c];
-        if (tg.ptr2[c] != nullptr) tg.ptr2[c][gi] = tot[c] * tg.scale2[c][gi];
+        const T v = s_val[w][c][q];
+        tg.ptr[c][gi * tg.stride[c]] = tg.scale[c] != nullptr ? v * tg.scale[c][gi] : v;
+        if (tg.ptr2[c] != nullptr) tg.ptr2[c][gi] = v * tg.scale2[c][gi];
       }
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 }
 
