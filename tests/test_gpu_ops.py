@@ -399,6 +399,36 @@ def test_rasterize_fwd_small_gaussians(ts):
     print(check_raster(refs, image=np32(img)))
 
 
+def test_raster_backward_with_many_gaussians_per_reduce_wave():
+    # Footprints of one or two tiles: a 256-row wave of the row reduce holds
+    # well over 128 Gaussians, so it stages and stores its totals in more
+    # than one round.
+    g = torch.Generator().manual_seed(33)
+    N, W_img, H_img, ts = 6000, 128, 128, 16
+    m2 = torch.rand(1, N, 2, generator=g) * torch.tensor([W_img, H_img])
+    a = 0.5 + 0.5 * torch.rand(1, N, generator=g)
+    c = 0.5 + 0.5 * torch.rand(1, N, generator=g)
+    b = (torch.rand(1, N, generator=g) - 0.5) * 0.5 * (a * c).sqrt()
+    con = torch.stack([a, b, c], -1)
+    op = 0.2 + 0.8 * torch.rand(1, N, generator=g)
+    mu = 0.5 + torch.rand(1, N, generator=g)
+    r = torch.full((1, N, 2), 3, dtype=torch.int32)
+    m2, con, op, mu, r = (t.to(DEV) for t in (m2, con, op, mu, r))
+    tw, th = W_img // ts, H_img // ts
+    _, ids, fl = W.isect_tiles(m2, r, ts, tw, th)
+    off = W.isect_offset_encode(ids, 1, tw, th)
+    emit_ids, _ = _ops.emission_order(fl, tw * th)
+    e = np32(emit_ids)
+    heads = max(int(np.unique(e[i:i + 256]).size) for i in range(0, e.size, 256))
+    assert heads > 128, heads
+    v = torch.randn(1, H_img, W_img, generator=g)
+    refs = raster_references(np32(m2), np32(con), np32(op), np32(mu), np32(off), np32(fl),
+                             W_img, H_img, ts, v_image=v.numpy())
+    got = W.rasterize_to_pixels_bwd_per_gaussian(m2, con, op, mu, off, ids, fl, v.to(DEV),
+                                                 W_img, H_img, ts, True)
+    print(check_raster(refs, grads=[np32(t) for t in got]))
+
+
 @pytest.mark.parametrize("dims,ts", [((32, 32, 32), 8), ((30, 20, 40), 10)])
 def test_voxelize_fwd_small_gaussians(dims, ts):
     """Sub-voxel footprints anywhere along a thread's x-row (see
