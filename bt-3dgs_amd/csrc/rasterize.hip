@@ -804,6 +804,56 @@ __device__ __forceinline__ TileSums<T> raster_tile_signed(const RasterRecord<T> 
   return s;
 }
 
+// What the partition moves through LDS per record: the fields of a
+// RasterRecord loaded from the packed payload that the rows pass reads (o
+// and mu stay zero there; the log2(e)-scaled conic is recomputed), ten words
+// in float instead of sixteen, so more blocks fit a CU.
+template <typename T>
+struct SplitRecord {
+  T mx, my, a, b, c, om;
+  typename Bits<T>::type lim;
+  int i0, i1;
+  uint32_t flags;  // 1: live, 2: pd
+};
+
+template <typename T>
+__device__ __forceinline__ SplitRecord<T> split_record(const RasterRecord<T> &r) {
+  SplitRecord<T> s;
+  s.mx = r.mx;
+  s.my = r.my;
+  s.a = r.a;
+  s.b = r.b;
+  s.c = r.c;
+  s.om = r.om;
+  s.lim = r.lim;
+  s.i0 = r.i0;
+  s.i1 = r.i1;
+  s.flags = (r.live ? 1u : 0u) | (r.pd ? 2u : 0u);
+  return s;
+}
+
+// The record as load_raster_record_packed forms it (same expressions).
+template <typename T>
+__device__ __forceinline__ RasterRecord<T> raster_record(const SplitRecord<T> &s) {
+  RasterRecord<T> r;
+  r.live = (s.flags & 1u) != 0;
+  r.pd = (s.flags & 2u) != 0;
+  r.mx = s.mx;
+  r.my = s.my;
+  r.a = s.a;
+  r.b = s.b;
+  r.c = s.c;
+  r.o = r.mu = 0;
+  r.om = s.om;
+  r.ha = static_cast<T>(0.5 * kLog2e) * r.a;
+  r.hb = static_cast<T>(kLog2e) * r.b;
+  r.hc = static_cast<T>(0.5 * kLog2e) * r.c;
+  r.lim = s.lim;
+  r.i0 = s.i0;
+  r.i1 = s.i1;
+  return r;
+}
+
 // The two-pass (rows) backward with absolute gradients at tile size 16 over
 // an image whose rows allow 16-byte loads.
 template <typename T>
@@ -815,7 +865,7 @@ __global__ __launch_bounds__(kSplitThreads) void raster_bwd_split_kernel(
     T *__restrict__ rows) {
   constexpr int R = 16;
   constexpr int kWaves = kSplitThreads / 64;
-  __shared__ WordMajor<RasterRecord<T>, kSplitThreads> s_rec;
+  __shared__ WordMajor<SplitRecord<T>, kSplitThreads> s_rec;
   __shared__ int32_t s_r[kSplitThreads];
   __shared__ uint32_t s_key[kSplitThreads];
   __shared__ uint32_t s_count[kWaves];
@@ -871,13 +921,13 @@ __global__ __launch_bounds__(kSplitThreads) void raster_bwd_split_kernel(
   const uint32_t slot = fast ? fast_lt : n_fast + (threadIdx.x - fast_lt);
   s_r[slot] = in_list ? static_cast<int32_t>(r) : -1;
   s_key[slot] = key;
-  s_rec.store(static_cast<int>(slot), rec);
+  s_rec.store(static_cast<int>(slot), split_record(rec));
   __syncthreads();
   const int32_t rr = s_r[threadIdx.x];
   const bool valid = rr >= 0;
   if (ballot(valid) == 0) return;  // uniform per wave; no barrier follows
   key = s_key[threadIdx.x];
-  rec = s_rec.load(static_cast<int>(threadIdx.x));
+  rec = raster_record(s_rec.load(static_cast<int>(threadIdx.x)));
   const bool wave_fast = (wave + 1) * 64 <= n_fast;
   const uint32_t cam = key / n_tiles, t = key - cam * n_tiles;
   const uint32_t ty = t / tw, tx = t - ty * tw;
