@@ -130,10 +130,10 @@ __global__ __launch_bounds__(1024) void raster_fwd_kernel(
 // with pre-scaled coefficients, and the alpha test (sigma >= 0,
 // |o mu e| >= 1e-5) is one unsigned compare of sl's bits against a limit
 // staged per record (alpha_limit), so a pixel costs two FMAs, one
-// v_exp_f32, one compare, a select and the accumulating FMA.  The groups'
-// partial tiles are summed in a fixed order at the end, so the result is
-// deterministic (the per-pixel order differs from a plain list-order sum
-// only by rounding).
+// v_exp_f32, one compare, a select and the accumulating FMA.  At the end
+// each wave adds its groups' partial tiles across lanes and the block adds
+// its waves' in order: a fixed order, so the result is deterministic (the
+// per-pixel order differs from a plain list-order sum only by rounding).
 constexpr int kFwdWaves = 8;
 constexpr int kFwdBatch = 64 * kFwdWaves;
 
@@ -169,13 +169,13 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
   constexpr int NL = TS * TS / R;        // lanes covering the tile for one record
   constexpr int G = 64 / NL;             // records in flight per wave
   constexpr int LPR = TS / R;            // lanes per tile row
-  constexpr int NP = kFwdWaves * G;      // partial tiles per block
+  constexpr int NP = kFwdWaves * G;      // records in flight per block
   static_assert(G * NL == 64 && LPR * R == TS, "unsupported tile size");
   // G - 1 records of padding after the batch: the record loop's last round
   // reads up to G - 1 entries past the batch's end.  Entries past the end
   // hold dead records (zero limit, which no pixel passes).
   __shared__ FwdRecord<T> s_rec[kFwdBatch + G];
-  __shared__ T s_part[NP][TS * TS];
+  __shared__ T s_part[kFwdWaves][TS * TS];
 
   // The splits of one tile are consecutive logical blocks (same XCD).
   const uint32_t lb = xcd_swizzle(blockIdx.x, gridDim.x);
@@ -185,7 +185,7 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
   const uint32_t ty = t / tw, tx = t - ty * tw;
   const int tid = static_cast<int>(threadIdx.x);
   const int wave = static_cast<int>(wave_index()), lane = static_cast<int>(lane_id());
-  const int slot = wave * G + lane / NL, gl = lane % NL;
+  const int gl = lane % NL;
   const int ly = gl / LPR, lx0 = (gl % LPR) * R;
   const T half = static_cast<T>(0.5);
   const T py = static_cast<T>(static_cast<int>(ty) * TS + ly) + half;
@@ -263,13 +263,23 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
       }
     }
   }
+  // The wave's G groups cover the same pixels: their partial tiles are added
+  // across lanes first (group g + 1 onto g, pairs of groups, ...; a fixed
+  // order), so the block stages one partial tile per wave.
 #pragma unroll
-  for (int k = 0; k < R; ++k) s_part[slot][ly * TS + lx0 + k] = acc[k];
+  for (int off = NL; off < 64; off *= 2) {
+#pragma unroll
+    for (int k = 0; k < R; ++k) acc[k] += __shfl_xor(acc[k], off, 64);
+  }
+  if (lane < NL) {
+#pragma unroll
+    for (int k = 0; k < R; ++k) s_part[wave][ly * TS + lx0 + k] = acc[k];
+  }
   __syncthreads();
   for (int pix = tid; pix < TS * TS; pix += kFwdBatch) {
     T sum = s_part[0][pix];
 #pragma unroll
-    for (int w = 1; w < NP; ++w) sum += s_part[w][pix];
+    for (int w = 1; w < kFwdWaves; ++w) sum += s_part[w][pix];
     if (splits > 1) {
       partial[(static_cast<int64_t>(key) * splits + split) * (TS * TS) + pix] = sum;
       continue;
