@@ -800,30 +800,17 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
 #pragma unroll
     for (int c = 0; c < 10; ++c) s_acc[w][c][lane] = 0;
   }
-  // Chunk list: the full chunks in (chunk index, record) order, then each
-  // record's partial last chunk, longest first.  A batch of 64 entries then
-  // holds chunks of non-increasing length, and one made of short partial
-  // chunks runs only as many row steps as its longest.  Each record's chunks
-  // still come in increasing chunk index (its partial chunk is its last).
-  const int n_full = n_items / R, tail = n_items % R;
+  // Chunk list in (chunk index, record) order.
+  const int n_chunks = (n_items + R - 1) / R;
   uint32_t n_list = 0;
   const uint64_t lt = lanemask_lt();
 #pragma unroll
   for (int q = 0; q < R; ++q) {
-    const bool has = n_full > q;
+    const bool has = n_chunks > q;
     const uint64_t m = ballot(has);
     if (has)
       s_chunk[w][n_list + static_cast<uint32_t>(__popcll(m & lt))] =
           static_cast<uint16_t>(lane | (static_cast<uint32_t>(q) << 6));
-    n_list += static_cast<uint32_t>(__popcll(m));
-  }
-#pragma unroll
-  for (int len = R - 1; len > 0; --len) {
-    const bool has = tail == len;
-    const uint64_t m = ballot(has);
-    if (has)
-      s_chunk[w][n_list + static_cast<uint32_t>(__popcll(m & lt))] =
-          static_cast<uint16_t>(lane | (static_cast<uint32_t>(n_full) << 6));
     n_list += static_cast<uint32_t>(__popcll(m));
   }
   // The wave's LDS operations complete in order, so its own lanes' writes
@@ -858,13 +845,6 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
                      static_cast<int>(t - before);
     }
     const int n_here = act ? min(R, cr.n_items - static_cast<int>(q) * R) : 0;
-    // Over the batch: bit n of the low half, some chunk holds n items; bit
-    // 16 + q, some chunk has index q.
-    uint32_t seen = act ? ((1u << n_here) | (1u << (16u + q))) : 1u;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) seen |= static_cast<uint32_t>(__shfl_xor(seen, off, 64));
-    seen = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(seen)));
-    const int n_steps = 31 - static_cast<int>(__builtin_clz(seen & 0xFFFFu));
     const T cdx0 = (static_cast<T>(cr.ok) + half) - cr.m[0];
     T dxk[R], wk[R];
 #pragma unroll
@@ -874,7 +854,7 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
     }
     T Y0 = 0, Z0 = 0, Y1 = 0, Z1 = 0, YY = 0, YZ = 0, ZZ = 0;
 #pragma unroll 1
-    for (int st = 0; st < n_steps; ++st) {
+    for (int st = 0; st < R; ++st) {
       const bool item = st < n_here;
       const int i = cr.oi + ((pos >> 3) & 7);
       const int j = cr.oj + (pos & 7);
@@ -926,11 +906,11 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
       t2 += wx * dxk[k];
     }
     const T sums[10] = {t0, t1, t2, Y0, Z0, Y1, Z1, YY, YZ, ZZ};
-    // One chunk index at a time, in increasing order: the records of one
-    // index are distinct.
+    // One chunk index at a time: the records of one index are distinct.
+    const uint32_t q_lo = static_cast<uint32_t>(s_chunk[w][cb]) >> 6;
+    const uint32_t q_hi = static_cast<uint32_t>(s_chunk[w][min(cb + 63u, n_list - 1u)]) >> 6;
 #pragma unroll 1
-    for (uint32_t qs = seen >> 16; qs != 0u; qs &= qs - 1u) {
-      const uint32_t qq = static_cast<uint32_t>(__builtin_ctz(qs));
+    for (uint32_t qq = q_lo; qq <= q_hi; ++qq) {
       if (act && q == qq) {
 #pragma unroll
         for (int c = 0; c < 10; ++c) s_acc[w][c][rl] += sums[c];
