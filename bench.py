@@ -1049,8 +1049,8 @@ def main():
             "voxelize_fwd": 52 * i3 + 4 * n_vox,
             # list 12 + payload 40 + row 40 per record; v_volume read
             "voxelize_bwd_rows": 92 * i3 + 4 * n_vox,
-            # row 48 + emission id 4 per record; 40 B per Gaussian out
-            "voxelize_bwd_reduce": 52 * i3 + 40 * N_VOX,
+            # row 40 + emission id 4 per record; 40 B per Gaussian out
+            "voxelize_bwd_reduce": 44 * i3 + 40 * N_VOX,
         }
         vdom = max(vsec, key=vsec.get)
         result["voxelize"] = {

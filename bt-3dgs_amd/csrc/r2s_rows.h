@@ -5,7 +5,7 @@
 // Gaussian's gradient with device-scope float atomics runs at about 21 G
 // atomics/s on MI355X (measured for scattered fp32 adds), which dominates the
 // backward passes.  Instead a kernel stores each record's partials as one
-// 12-value row of a workspace at the record's emission index; in emission
+// row of a workspace at the record's emission index; in emission
 // order the records of one Gaussian are consecutive, so a streaming pass sums
 // each Gaussian's rows with a segmented wave reduction and writes the sums
 // once with plain stores.  The result does not depend on scheduling.
@@ -15,14 +15,17 @@
 
 namespace r2s {
 
-// Values per row: a row of up to 8 values takes 8 slots (32 bytes in float,
-// one 32-byte sector, so a row written at a scattered index costs one
-// sector), a longer one 12 (48 bytes, three 16-byte vectors).  The
-// rasterizer stores 8 values (6 without absolute gradients), the voxelizer
-// 10.
+// Slots per row: a row of up to 8 values takes 8 (32 bytes in float, one
+// 32-byte sector, so a row written at a scattered index costs one sector), a
+// longer one its value count rounded up to even (the voxelizer's 10 values:
+// 40 bytes in float, five 8-byte vectors).  Rows are written at scattered
+// indices, and fewer bytes per row beat sector-aligned rows there: measured
+// on the voxelizer's rows pass, 48-byte rows were 4 % slower than 40-byte
+// ones and 64-byte rows 9 %.  The rasterizer stores 8 values (6 without
+// absolute gradients).
 template <int NV>
 constexpr int row_stride() {
-  return NV <= 8 ? 8 : 12;
+  return NV <= 8 ? 8 : (NV + 1) / 2 * 2;
 }
 
 template <typename T>
@@ -38,13 +41,36 @@ struct Quad<double> {
   static constexpr int n = 2;
 };
 
-// Rows start at multiples of the row size from a 16-byte-aligned
-// workspace, so they are written and read as 16-byte vectors.
+template <typename T>
+struct Pair;
+template <>
+struct Pair<float> {
+  using type = float2;  // 8 bytes
+  static constexpr int n = 2;
+};
+template <>
+struct Pair<double> {
+  using type = double;  // 8 bytes
+  static constexpr int n = 1;
+};
+
+// Rows start at multiples of the row size from a 16-byte-aligned workspace,
+// so they are written and read as 16-byte vectors when the row size is a
+// multiple of 16 bytes, else as 8-byte vectors (an even slot count makes
+// every row size a multiple of 8 bytes).
+template <typename T, int NV>
+struct RowVec {
+  static constexpr bool kWide = (row_stride<NV>() * sizeof(T)) % 16 == 0;
+  using type = typename std::conditional<kWide, typename Quad<T>::type,
+                                         typename Pair<T>::type>::type;
+  static constexpr int n = kWide ? Quad<T>::n : Pair<T>::n;
+};
+
 template <typename T, int NV>
 __device__ __forceinline__ void store_row(T *__restrict__ rows, int64_t e, const T (&v)[NV]) {
   static_assert(NV <= 12, "row too long");
-  using Q = typename Quad<T>::type;
-  constexpr int kq = Quad<T>::n, nq = (NV + kq - 1) / kq;
+  using Q = typename RowVec<T, NV>::type;
+  constexpr int kq = RowVec<T, NV>::n, nq = (NV + kq - 1) / kq;
   T pad[nq * kq];
 #pragma unroll
   for (int c = 0; c < nq * kq; ++c) pad[c] = c < NV ? v[c] : static_cast<T>(0);
@@ -55,8 +81,8 @@ __device__ __forceinline__ void store_row(T *__restrict__ rows, int64_t e, const
 
 template <typename T, int NV>
 __device__ __forceinline__ void load_row(const T *__restrict__ rows, int64_t e, T (&v)[NV]) {
-  using Q = typename Quad<T>::type;
-  constexpr int kq = Quad<T>::n, nq = (NV + kq - 1) / kq;
+  using Q = typename RowVec<T, NV>::type;
+  constexpr int kq = RowVec<T, NV>::n, nq = (NV + kq - 1) / kq;
   T pad[nq * kq];
   const Q *src = reinterpret_cast<const Q *>(rows + e * row_stride<NV>());
 #pragma unroll

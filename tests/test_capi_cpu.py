@@ -112,6 +112,17 @@ def test_workspace_queries(lib):
     assert rc in (1001, 1004)
 
 
+def test_row_workspaces_hold_the_slots_the_tests_read(lib):
+    # One row per record at its emission index: the GPU tests index the
+    # workspace with these slot counts.
+    from helpers import RASTER_ROW_SLOTS, VOXEL_ROW_SLOTS
+    n = 1000
+    assert lib.r2s_voxelize_bwd_workspace_bytes(n, 4) == n * VOXEL_ROW_SLOTS * 4
+    assert lib.r2s_voxelize_bwd_workspace_bytes(n, 8) == n * VOXEL_ROW_SLOTS * 8
+    for b in (4, 8):  # rows, then the packed payload of 8 values per (view, Gaussian)
+        assert lib.r2s_rasterize_bwd_workspace_bytes(n, 7, b) == (n * RASTER_ROW_SLOTS + 7 * 8) * b
+
+
 def test_noalloc_forward_rejects_partial_tiles_beyond_its_array(lib):
     # 64x64 tiles of 16 with 8192 records each split 8 ways: 4096 * 8 * 256
     # pixels, 32 MiB in float32 (fits) and 64 MiB in float64 (does not).  The
