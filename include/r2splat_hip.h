@@ -597,7 +597,7 @@ int r2s_voxelize_bwd_f64(const double *means3d, const double *conics,
                          double *v_means3d, double *v_conics,
                          double *v_opacities, r2s_stream_t stream);
 
-/* Workspace of r2s_voxelize_bwd_emit_*: one row of 12 values of
+/* Workspace of r2s_voxelize_bwd_emit_*: one row of 10 values of
  * dtype_bytes per record. */
 int64_t r2s_voxelize_bwd_workspace_bytes(int64_t n_isects, int dtype_bytes);
 
