@@ -487,7 +487,14 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
   const uint32_t tile = xcd_swizzle(blockIdx.x, nblocks);
   const int64_t n = *n_dev;
   const int64_t block_first = static_cast<int64_t>(tile) * kSortTile;
-  if (n > cap || block_first >= n) return;  // uniform per block
+  if (n > cap) return;  // uniform per block
+  if (block_first >= n) {
+    // Block 0 has no records only when there are none at all (a capacity
+    // guessed before the count was known): then every key starts at 0.
+    if (kFinal && tile_offsets != nullptr && tile == 0)
+      for (uint32_t d = threadIdx.x; d < n_keys; d += kSortThreads) tile_offsets[d] = 0;
+    return;
+  }
   const uint32_t w = threadIdx.x / 64, lane = threadIdx.x % 64;
   for (uint32_t k = threadIdx.x; k < 4 * digits; k += kSortThreads)
     cnt[k / digits][k % digits] = 0;

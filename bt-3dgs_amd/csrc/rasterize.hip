@@ -1184,7 +1184,9 @@ int raster_bwd_impl(const T *means2d, const T *conics, const T *opac, const T *m
 }
 
 // Device address of `scratch` on the current device, looked up once per
-// device and cached (each GPU holds its own copy at its own address).
+// device and cached (each GPU holds its own copy at its own address).  A
+// hipDeviceReset() would leave the cached address stale; the header states
+// that the entry point is not to be called on a device after one.
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_lock;
 void *g_scratch_ptr[kMaxDevices] = {};

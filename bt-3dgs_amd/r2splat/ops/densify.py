@@ -75,36 +75,35 @@ def _plan(model, optimizers, state, trainable_param_keys, param_role, moment_rol
 
 
 def _install(model, optimizers, state, trainable_param_keys, slots, outs) -> None:
-    """Write the new arrays back in the reference's order (utils/ops.py:85-103)."""
-    new_params, new_moments, new_state = {}, {}, {}
-    for (kind, name, key), t in zip(slots, outs):
-        if kind == "param":
-            new_params[name] = t
-        elif kind == "moment":
-            new_moments[(name, key)] = t
-        else:
-            new_state[name] = t
+    """Put the rewritten arrays in place.
+
+    Each trainable parameter becomes a new ``nn.Parameter`` over its rewritten
+    rows.  Its optimizer state dict moves, as one object, from the old
+    parameter to the new one, with every tensor moment (each key but "step")
+    swapped for its rewritten array, and the optimizer's groups point at the
+    new parameter.  That is the effect of utils/ops.py:85-103 for optimizers
+    of one parameter group each, which is how the model builds them.  A
+    parameter without an optimizer must be frozen; the assertion message is
+    the reference's.
+    """
+    written = dict(zip(slots, outs))
     for name in trainable_param_keys:
-        param = getattr(model, name)
-        new_param = torch.nn.Parameter(new_params[name], requires_grad=param.requires_grad)
-        setattr(model, name, new_param)
-        if name not in optimizers:
-            assert not param.requires_grad, (
+        old = getattr(model, name)
+        new = torch.nn.Parameter(written[("param", name, None)], requires_grad=old.requires_grad)
+        setattr(model, name, new)
+        opt = optimizers.get(name)
+        if opt is None:
+            assert not old.requires_grad, (
                 f"Optimizer for {name} is not found, but parameter is trainable "
-                f"(requires_grad={param.requires_grad})."
+                f"(requires_grad={old.requires_grad})."
             )
             continue
-        optimizer = optimizers[name]
-        for i in range(len(optimizer.param_groups)):
-            param_state = optimizer.state[param]
-            del optimizer.state[param]
-            for key in list(param_state.keys()):
-                if key != "step":
-                    param_state[key] = new_moments[(name, key)]
-            optimizer.param_groups[i]["params"] = [new_param]
-            optimizer.state[new_param] = param_state
-    for k, v in new_state.items():
-        state[k] = v
+        moved = opt.state.pop(old, {})
+        moved.update({k: written[("moment", name, k)] for k in moved if k != "step"})
+        for group in opt.param_groups:
+            group["params"] = [new]
+        opt.state[new] = moved
+    state.update({name: t for (kind, name, _), t in written.items() if kind == "state"})
 
 
 def _history_rows(model) -> int:

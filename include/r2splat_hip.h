@@ -401,7 +401,9 @@ int r2s_rasterize_fwd_f64(const double *means2d, const double *conics,
  * until the process ends; a call whose partial tiles
  * (r2s_rasterize_workspace_bytes) exceed it fails with R2S_ERANGE.  The
  * array's address is looked up on the first call on each device, which must
- * be the current device and the stream's.  All calls on one GPU share the
+ * be the current device and the stream's, and kept for the process: after a
+ * hipDeviceReset() that address is stale, so a process that resets a device
+ * must not call this entry point on it again.  All calls on one GPU share the
  * array: calls that overlap on one GPU (concurrent streams) race; calls on
  * one stream do not.  The image equals r2s_rasterize_fwd_*'s bit for bit. */
 #define R2S_RASTER_SCRATCH_BYTES (32u << 20)

@@ -60,13 +60,15 @@ def assert_close(actual, expected, name, rtol=RTOL, atol=ATOL):
 #   in the kernel's precision (the oracle run in float32 / float64), for sums
 #   that cancel below the bar's reach;
 # * KAPPA u |terms|: the sum of the absolute values of the terms that make
-#   the output (oracle/c/r2s_oracle.c `mag`) times the kernel precision's
-#   unit roundoff u and KAPPA = 8, the roundings one term of these sums
-#   carries (offset, exponent, exp, the products): what any evaluation order
-#   may differ by when the terms cancel.  A single realisation of the
-#   reference order's error is no bound for another order: at config 2 a
-#   v_conic sum of 1.99 over 38,400 pixel terms has |terms| = 1.5e6 (u |terms|
-#   = 0.088); the kernel's result was 2.9e-3 off, the reference order's 1.1e-3;
+#   the output (oracle/c/r2s_oracle.c `mag`: |term| (1 + S) with S the sum
+#   of |sigma's terms|) times the kernel precision's unit roundoff u and
+#   KAPPA = 2: what any evaluation order may differ by when the terms cancel.
+#   A single realisation of the reference order's error is no bound for
+#   another order: at config 2 a v_conic sum of 1.99 over 38,400 pixel terms
+#   has u |terms| = 0.088; the kernel's result was 2.9e-3 off, the reference
+#   order's 1.1e-3.  Elements that need this clause are the "conditioning"
+#   class; the report gives the largest err / (u |terms|) among them
+#   (`kappa_max`), so a widening shows as a number, not only as a count;
 # * band: the summed |contribution| of the terms whose alpha test lies within
 #   the flip bracket (oracle/c/r2s_oracle.c), non-zero only for outputs that
 #   contain a term at an alpha cut-off.  An element that needs it is an alpha
@@ -81,7 +83,7 @@ def assert_close(actual, expected, name, rtol=RTOL, atol=ATOL):
 
 U32 = 2.0 ** -24
 U64 = 2.0 ** -53
-KAPPA = 8
+KAPPA = 2
 UNIT = {np.dtype(np.float32): U32, np.dtype(np.float64): U64}
 ETA = {np.dtype(np.float32): 8 * U32, np.dtype(np.float64): 8 * U64}
 BAR = {np.dtype(np.float32): (1e-4, 1e-5), np.dtype(np.float64): (1e-9, 1e-12)}
@@ -90,14 +92,30 @@ ANCHOR = {np.dtype(np.float32): np.float64, np.dtype(np.float64): np.longdouble}
 
 class ParityReport(dict):
     """Counts of one check: elements, those inside the bar, those that needed
-    the reference-order term, and alpha flips (those that needed the band)."""
+    the reference-order term, those that needed the conditioning term, and
+    alpha flips (those that needed the band); kappa_max is the largest
+    err / (u |terms|) of the conditioning class."""
 
     def __str__(self):
         return ", ".join(f"{k}={v}" for k, v in self.items())
 
 
+# Default cap on the elements of one output that need the conditioning term
+# or the flip band, as a fraction of the output's elements (check_raster,
+# check_voxel and the sampled checks; a test may pass a measured cap of its
+# own, e.g. for needle-like stress footprints).  At most MIN_CAPPED such
+# elements are always allowed, so small outputs are not failed by one flip.
+MAX_FRAC = 1e-3
+MIN_CAPPED = 4
+
+
 def assert_parity(actual, anchor, lowp, band, name, rtol=None, atol=None, max_flips=None,
-                  excused=None, mag=None):
+                  mag=None, max_frac=None):
+    """Every element within the bar described above, else AssertionError.
+
+    ``max_flips``: most alpha flips allowed; ``max_frac``: most elements of
+    the conditioning and flip classes together, as a fraction of the
+    elements (at least MIN_CAPPED).  Returns the ParityReport."""
     a = np.asarray(actual)
     kdt = np.dtype(a.dtype)
     r0, a0 = BAR.get(kdt, BAR[np.dtype(np.float32)])
@@ -121,8 +139,8 @@ def assert_parity(actual, anchor, lowp, band, name, rtol=None, atol=None, max_fl
     order = 2 * np.abs(L - A)
     cond = order
     if mag is not None:
-        M = KAPPA * UNIT.get(kdt, U32) * np.asarray(mag, dtype=np.longdouble)
-        cond = np.maximum(order, M)
+        uM = UNIT.get(kdt, U32) * np.asarray(mag, dtype=np.longdouble)
+        cond = np.maximum(order, KAPPA * uM)
     ok_bar = err <= bar
     ok_order = err <= np.maximum(bar, order)
     ok_cond = err <= np.maximum(bar, cond)
@@ -130,17 +148,10 @@ def assert_parity(actual, anchor, lowp, band, name, rtol=None, atol=None, max_fl
     rep["within_bar"] = int(ok_bar.sum())
     rep["reference_order"] = int((ok_order & ~ok_bar).sum())
     rep["conditioning"] = int((ok_cond & ~ok_order).sum())
-    if mag is not None and (~ok_bar).any():
-        # Largest error outside the plain bar in units of u |terms|.
-        um = UNIT.get(kdt, U32) * np.asarray(mag, dtype=np.longdouble)
-        ratio = np.where(~ok_bar & (um > 0), err / np.where(um > 0, um, 1), 0)
-        rep["max_err_per_u_terms"] = round(float(ratio.max()), 4)
-    if excused is not None:
-        # Elements of Gaussians with a term at an alpha cut-off whose band is
-        # not propagated to this output (composed gradients): the caller
-        # checks them separately and they count as flips here.
-        ok_flip = ok_flip | np.broadcast_to(np.asarray(excused, bool), ok_flip.shape)
     rep["alpha_flips"] = int((ok_flip & ~ok_cond).sum())
+    if rep["conditioning"]:
+        need = ok_cond & ~ok_order
+        rep["kappa_max"] = round(float((err[need] / uM[need]).max()), 4)
     bad = ~ok_flip & fin
     if bad.any():
         i = np.unravel_index(np.argmax(np.where(bad, err - np.maximum(bar, cond) - B, -1)),
@@ -152,6 +163,10 @@ def assert_parity(actual, anchor, lowp, band, name, rtol=None, atol=None, max_fl
             + ("" if mag is None else f" |terms|={float(np.asarray(mag)[i])!r}"))
     if max_flips is not None:
         assert rep["alpha_flips"] <= max_flips, f"{name}: {rep}"
+    if max_frac is not None:
+        cap = max(int(round(max_frac * X.size)), MIN_CAPPED)
+        assert rep["conditioning"] + rep["alpha_flips"] <= cap, \
+            f"{name}: conditioning + alpha flips above {cap} ({max_frac:g} of {X.size}): {rep}"
     return rep
 
 
@@ -208,32 +223,36 @@ RASTER_GRAD_NAMES = ("v_means2d_abs", "v_means2d", "v_conics", "v_opacities", "v
 VOXEL_GRAD_NAMES = ("v_means3d", "v_conics", "v_opacities")
 
 
-def check_raster(refs, image=None, grads=None, tag="", max_flips=None):
-    """assert_parity over a rasterizer's image and / or 5-tuple of gradients;
-    returns {name: ParityReport}."""
+def check_raster(refs, image=None, grads=None, tag="", max_flips=None, max_frac=MAX_FRAC):
+    """assert_parity over a rasterizer's image and / or 5-tuple of gradients,
+    each output's conditioning + flip classes capped at max_frac of its
+    elements; returns {name: ParityReport}."""
     reps = {}
     if image is not None:
         an, lo, bd, mg = refs["fwd"]
         reps["image"] = assert_parity(image, an, lo, bd, f"{tag}image", max_flips=max_flips,
-                                      mag=mg)
+                                      mag=mg, max_frac=max_frac)
     if grads is not None:
         for g, (an, lo, bd, mg), n in zip(grads, refs["bwd"], RASTER_GRAD_NAMES):
             if an is None:
                 assert g is None, f"{tag}{n}: expected None"
                 continue
-            reps[n] = assert_parity(g, an, lo, bd, f"{tag}{n}", max_flips=max_flips, mag=mg)
+            reps[n] = assert_parity(g, an, lo, bd, f"{tag}{n}", max_flips=max_flips, mag=mg,
+                                    max_frac=max_frac)
     return reps
 
 
-def check_voxel(refs, volume=None, grads=None, tag="", max_flips=None):
+def check_voxel(refs, volume=None, grads=None, tag="", max_flips=None, max_frac=MAX_FRAC):
+    """As check_raster for the voxelizer: volume and / or the 3-tuple."""
     reps = {}
     if volume is not None:
         an, lo, bd, mg = refs["fwd"]
         reps["volume"] = assert_parity(volume, an, lo, bd, f"{tag}volume", max_flips=max_flips,
-                                       mag=mg)
+                                       mag=mg, max_frac=max_frac)
     if grads is not None:
         for g, (an, lo, bd, mg), n in zip(grads, refs["bwd"], VOXEL_GRAD_NAMES):
-            reps[n] = assert_parity(g, an, lo, bd, f"{tag}{n}", max_flips=max_flips, mag=mg)
+            reps[n] = assert_parity(g, an, lo, bd, f"{tag}{n}", max_flips=max_flips, mag=mg,
+                                    max_frac=max_frac)
     return reps
 
 
@@ -253,7 +272,7 @@ def assert_equal(actual, expected, name):
 PARAM_GRADS = ("means", "quats", "raw_scales", "raw_opacities")
 
 
-def check_parameter_gradients(got, args, raster_grads, voxel_grads=None):
+def check_parameter_gradients(got, args, raster_grads, voxel_grads=None, min_plain=0.999):
     """Composed parameter gradients of explicit_backward against the oracle.
 
     ``got``: {name: array} for PARAM_GRADS from the kernels; ``args``: the
@@ -269,9 +288,10 @@ def check_parameter_gradients(got, args, raster_grads, voxel_grads=None):
     them, with the float32 chain on them as the reference order.  Together
     with the raster / voxel check this covers every composed gradient.  The
     composition from scratch (float64 vs float32, the reference order end to
-    end) is returned as a report: its differences are those of the raster /
-    voxel sums, carried through the chain.  Returns ({name: ParityReport} of
-    the chain check, {name: fraction within the plain bar end to end})."""
+    end) differs by what the raster / voxel sums differ, carried through the
+    chain: at least ``min_plain`` of each parameter gradient's elements must
+    be within the plain bar of it (all but MIN_CAPPED in small outputs).  Returns ({name: ParityReport} of the chain
+    check, {name: fraction within the plain bar end to end})."""
     from oracle import compose
 
     chain = dict(raster_grads=raster_grads, voxel_grads=voxel_grads)
@@ -280,13 +300,19 @@ def check_parameter_gradients(got, args, raster_grads, voxel_grads=None):
     reports = {}
     for name in PARAM_GRADS:
         reports[name] = assert_parity(np.asarray(got[name]), chain_hi[name], chain_lo[name], None,
-                                      f"grad {name} (chain on the kernels' raster / voxel VJPs)")
+                                      f"grad {name} (chain on the kernels' raster / voxel VJPs)",
+                                      max_frac=MAX_FRAC)
     hi64 = compose.explicit_backward(*args, dtype=np.float64)
     plain = {}
     for name in PARAM_GRADS:
         g = np.asarray(got[name], np.float64)
         a = np.asarray(hi64[name], np.float64)
-        plain[name] = float((np.abs(g - a) <= 1e-5 + 1e-4 * np.abs(a)).mean())
+        inside = np.abs(g - a) <= 1e-5 + 1e-4 * np.abs(a)
+        plain[name] = float(inside.mean())
+        cap = max(int(round((1 - min_plain) * inside.size)), MIN_CAPPED)
+        assert int((~inside).sum()) <= cap, (
+            f"grad {name}: {int((~inside).sum())} of {inside.size} elements outside the plain "
+            f"bar of the float64 composition end to end (at most {cap}: {min_plain} within)")
     return reports, plain
 
 
@@ -329,7 +355,7 @@ def _row_values(rows_f32, src, rec, order, slots, n_values):
 
 
 def check_raster_sampled(m2, con, op, mu, off, fl, v_image, W, H, ts, keys, image=None,
-                         rows=None, isect_src=None, tag=""):
+                         rows=None, isect_src=None, tag="", max_frac=MAX_FRAC):
     """assert_parity over the sampled tiles' pixels of ``image`` and over
     their records' rows (``rows`` [n_isects * 8] float32 at emission index
     ``isect_src``; the opacity and mu partials formed as mu T0 and o T0 from
@@ -352,7 +378,8 @@ def check_raster_sampled(m2, con, op, mu, off, fl, v_image, W, H, ts, keys, imag
             ty, tx = divmod(t, tw)
             mask[c, ty * ts:(ty + 1) * ts, tx * ts:(tx + 1) * ts] = True
         reps["image"] = assert_parity(np.asarray(image)[mask], an[mask], lw[mask], bd[mask],
-                                      f"{tag}image (sampled tiles)", mag=mg[mask])
+                                      f"{tag}image (sampled tiles)", mag=mg[mask],
+                                      max_frac=max_frac)
     if rows is not None:
         rec, val, bd, mg = native.raster_records(*hi, off, fl, np.asarray(v_image, np.float64),
                                                  W, H, ts, keys, eta=eta)
@@ -364,13 +391,14 @@ def check_raster_sampled(m2, con, op, mu, off, fl, v_image, W, H, ts, keys, imag
         got[:, 7] = hi[3].reshape(-1)[g] * r[:, 5]
         got[:, 8] = hi[2].reshape(-1)[g] * r[:, 5]
         reps["records"] = assert_parity(got.astype(np.float32), val, lv, bd,
-                                        f"{tag}record partials (sampled)", mag=mg)
+                                        f"{tag}record partials (sampled)", mag=mg,
+                                        max_frac=max_frac)
         reps["records"]["records"] = int(rec.size)
     return reps
 
 
 def check_voxel_sampled(m3, con, op, off, fl, v_volume, d2, d1, d0, ts, keys, volume=None,
-                        rows=None, isect_src=None, tag="", key_offset=0):
+                        rows=None, isect_src=None, tag="", key_offset=0, max_frac=MAX_FRAC):
     """As check_raster_sampled for the voxelizer (rows of 10 values).  With
     ``key_offset`` the lists are one z-slab's (keys relative to the slab's
     first brick layer) and ``volume`` is the whole volume."""
@@ -391,7 +419,8 @@ def check_voxel_sampled(m3, con, op, off, fl, v_volume, d2, d1, d0, ts, keys, vo
             b1, b2 = divmod(rem, n2)
             mask[b0 * ts:(b0 + 1) * ts, b1 * ts:(b1 + 1) * ts, b2 * ts:(b2 + 1) * ts] = True
         reps["volume"] = assert_parity(np.asarray(volume)[mask], an[mask], lw[mask], bd[mask],
-                                       f"{tag}volume (sampled bricks)", mag=mg[mask])
+                                       f"{tag}volume (sampled bricks)", mag=mg[mask],
+                                       max_frac=max_frac)
     if rows is not None:
         rec, val, bd, mg = native.voxel_records(*hi, off, fl, np.asarray(v_volume, np.float64),
                                                 d2, d1, d0, ts, keys, eta=eta,
@@ -400,6 +429,7 @@ def check_voxel_sampled(m3, con, op, off, fl, v_volume, d2, d1, d0, ts, keys, vo
                                            d0, ts, keys, key_offset=key_offset)
         got, _ = _row_values(rows, isect_src, rec, VOXEL_ROW, VOXEL_ROW_SLOTS, 10)
         reps["records"] = assert_parity(got.astype(np.float32), val, lv, bd,
-                                        f"{tag}record partials (sampled)", mag=mg)
+                                        f"{tag}record partials (sampled)", mag=mg,
+                                        max_frac=max_frac)
         reps["records"]["records"] = int(rec.size)
     return reps

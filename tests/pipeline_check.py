@@ -99,6 +99,39 @@ def run(raw, viewmats, Ks, width, height, volume_shape=None, mode="primitive", s
                 v_vol=None if v_vol is None else v_vol[..., 0].contiguous())
 
 
+def _slab_lists(v):
+    """(lists, tile offsets, first layer) of each z-slab of a slabbed VolumePass."""
+    n2, n1, n0 = (-(-d // v.tile_size) for d in (v.dim2, v.dim1, v.dim0))
+    for z0, z1 in v.slabs:
+        lists, off = _ops.bin_tiles_3d_slab(v.means3d, v.radii, v.tile_size, n2, n1, n0, z0, z1)
+        yield lists, off, z0
+
+
+def _voxel_lists(v):
+    """A VolumePass's whole brick list (isect_ids, flatten_ids) as numpy; a
+    slabbed pass's slab lists are concatenated with their keys made absolute."""
+    if not v.slabs:
+        return np32(v.lists.isect_ids), np32(v.lists.flatten_ids)
+    plane = (-(-v.dim2 // v.tile_size)) * (-(-v.dim1 // v.tile_size))
+    parts = [(np32(lists.isect_ids) + z0 * plane, np32(lists.flatten_ids))
+             for lists, _, z0 in _slab_lists(v)]
+    return np.concatenate([p[0] for p in parts]), np.concatenate([p[1] for p in parts])
+
+
+def _voxel_vjp(v, v_volume):
+    """The kernels' voxel VJP outputs for a VolumePass, the slabs' partials
+    added in slab order as VolumePass.vjp adds them."""
+    if not v.slabs:
+        return _ops.voxel_backward(v.means3d, v.conics, v.weights, v.tile_offsets, v.lists,
+                                   v_volume, v.dim2, v.dim1, v.dim0, v.tile_size)
+    total = None
+    for lists, off, z0 in _slab_lists(v):
+        part = _ops.voxel_backward_slab(v.means3d, v.conics, v.weights, off, lists,
+                                        v_volume.contiguous(), v.tile_size, z0)
+        total = list(part) if total is None else [a.add_(b) for a, b in zip(total, part)]
+    return total
+
+
 def check_against_oracle(out, raw, viewmats, Ks, width, height, volume_shape=None):
     """Every output of a run() step against the oracle (see module docstring)."""
     st = out["state"]
@@ -130,8 +163,9 @@ def check_against_oracle(out, raw, viewmats, Ks, width, height, volume_shape=Non
         lo, hi = out["bbox"]
         vox = compose.voxelize_forward(r["means"], gc, go, hi - lo, (lo + hi) / 2, W_, D_, H_, 8,
                                        1e-8, 3.0)
-        assert_equal(np32(st.voxel.lists.isect_ids), vox["isect_ids"], "isect_ids 3d")
-        assert_equal(np32(st.voxel.lists.flatten_ids), vox["flatten_ids"], "flatten_ids 3d")
+        ids3, fl3 = _voxel_lists(st.voxel)
+        assert_equal(ids3, vox["isect_ids"], "isect_ids 3d")
+        assert_equal(fl3, vox["flatten_ids"], "flatten_ids 3d")
         vin = [vox[k].astype(np.float64) for k in ("means3d", "conics", "opacity")]
         vol_a, vol_b, vol_m = native.voxel_fwd(*vin, vox["tile_offsets"], vox["flatten_ids"],
                                                W_, D_, H_, 8, eta=ETA32, band=True, mag=True)
@@ -152,9 +186,7 @@ def check_against_oracle(out, raw, viewmats, Ks, width, height, volume_shape=Non
     reports = {f"raster {k}": r for k, r in check_raster(refs, grads=rg).items()}
     vg = None
     if vox is not None:
-        vg = _ops.voxel_backward(v.means3d, v.conics, v.weights, v.tile_offsets, v.lists,
-                                 v.volume.grad, v.dim2, v.dim1, v.dim0, v.tile_size)
-        vg = [np32(t) for t in vg]
+        vg = [np32(t) for t in _voxel_vjp(v, v.volume.grad)]
         vrefs = voxel_references(vox["means3d"], vox["conics"], vox["opacity"],
                                  vox["tile_offsets"], vox["flatten_ids"], W_, D_, H_, 8,
                                  v_volume=out["v_vol"].numpy())

@@ -7,9 +7,9 @@
   N(0,1); the image, the volume, every raster / voxel gradient and the four
   parameter gradients.
 * Config 2: 50,000 Gaussians of the same distributions, a 256^2 detector,
-  one view per call at angles k 2 pi / 64; every 8th of the 64 angles is
-  checked (projection fwd+bwd only, dL/d means, raw scales, quats, raw
-  opacities), each on its own explicit state as the trainer calls it.
+  one view per call at angles k 2 pi / 64; all 64 angles are checked
+  (projection fwd+bwd only, dL/d means, raw scales, quats, raw opacities),
+  each on its own explicit state as the trainer calls it.
 
 The check is tests/pipeline_check.py's: fp64-anchored, alpha flips counted.
 """
@@ -44,7 +44,7 @@ def config2_scene():
     return scenes.random_gaussians(50_000, g, -4.0, 0.5), g
 
 
-@pytest.mark.parametrize("k", list(range(0, 64, 8)))
+@pytest.mark.parametrize("k", list(range(64)))
 def test_config2_view(config2_scene, k):
     raw, _ = config2_scene
     viewmats, Ks = geometry.cone_beam_views([k * 2.0 * math.pi / 64], 256)

@@ -1,6 +1,6 @@
 """Oracle parity at BASELINE's full sizes: config 4 (500k binary-tree
-Gaussians, 512^2 detector, view 0, and the trainer's 128^3 volume of the same
-tree) and config 3 (200k Gaussians, 256^3 volume).
+Gaussians, 512^2 detector, views 0 and 180 degrees, and the trainer's 128^3
+volume of the same tree) and config 3 (200k Gaussians, 256^3 volume).
 
 * Projection outputs (means2d, cov2d, conics, mus, radii) of all 500k
   Gaussians and the tile / brick lists and offsets equal the oracle's bit for
@@ -124,6 +124,41 @@ def test_config4_one_pass_backward(config4, config4_refs):
     got = _ops.raster_backward(d["m2"], d["conics"], d["op"], d["mus"], d["off"], one,
                                d["v"].to(DEV), 512, 512, 16, True)
     _report("one-pass", check_raster(config4_refs, grads=_grads(got)))
+
+
+def test_config4_second_view_full_size(config4):
+    """The 500k tree from the opposite side (180 degrees, where the tree's
+    footprints differ from view 0's): projection and lists bit-exact, the
+    image and both backward forms' gradients against the oracle."""
+    d = config4
+    vm, Ks = geometry.cone_beam_views([np.pi], 512)
+    m2, cov2d, radii, conics, mus, op = W.project_gaussians_fwd(
+        d["means"], d["covars"], d["opac"], vm.to(DEV), Ks.to(DEV), 512, 512, 1e-8, 3.0)
+    pm2, pc2, pr = ops.world_to_image_projection_fwd(d["raw"].means.numpy(), np32(d["covars"]),
+                                                     vm.numpy(), Ks.numpy(), 512, 512, 1e-8,
+                                                     3.0)
+    pcon, pmu = ops.conics_mu_fwd(pc2, 1e-8)
+    for got, want, n in ((m2, pm2, "means2d"), (cov2d, pc2, "cov2d"), (radii, pr, "radii"),
+                         (conics, pcon, "conics"), (mus, pmu, "mus")):
+        assert_equal(np32(got), want, n)
+    lists = _ops.bin_tiles_2d(m2, radii, 16, 32, 32)
+    off = W.isect_offset_encode(lists.isect_ids, 1, 32, 32)
+    tpg, ids, fl = binning.isect_tiles(pm2, pr, 16, 32, 32)
+    assert ids.size > 4_000_000 and ids.size != d["lists"].isect_ids.numel()
+    assert_equal(np32(lists.isect_ids), ids, "isect_ids")
+    assert_equal(np32(lists.flatten_ids), fl, "flatten_ids")
+    assert_equal(np32(off), binning.isect_offset_encode(ids, 1, 32, 32), "tile_offsets")
+    print(f"config 4 at 180 degrees: {ids.size} tile records", flush=True)
+    v = torch.randn((1, 512, 512), generator=torch.Generator().manual_seed(180))
+    refs = raster_references(np32(m2), np32(conics), np32(op), np32(mus), np32(off), fl, 512,
+                             512, 16, v_image=v.numpy())
+    img = W.rasterize_to_pixels_fwd(m2, conics, op, mus, off, lists.flatten_ids, 512, 512, 16)
+    _report("180 fwd", check_raster(refs, image=np32(img)))
+    got = _ops.raster_backward(m2, conics, op, mus, off, lists, v.to(DEV), 512, 512, 16, True)
+    _report("180 two-pass", check_raster(refs, grads=_grads(got)))
+    one = _ops.TileLists(*lists[:3], None, None)
+    got1 = _ops.raster_backward(m2, conics, op, mus, off, one, v.to(DEV), 512, 512, 16, True)
+    _report("180 one-pass", check_raster(refs, grads=_grads(got1)))
 
 
 def test_config4_volume_regulariser_voxelization(config4):

@@ -284,6 +284,37 @@ def test_isect_tiles_capacity_guess():
     assert guessed == [False, True, False, True, True]
 
 
+@pytest.mark.parametrize("n_tiles", [(32, 32), (64, 48)])
+def test_isect_emit_sort_guessed_capacity_without_records(n_tiles):
+    # A capacity guessed before the count is known, and no records on the
+    # device: the emit + sort entry must still write the tile offsets that
+    # r2s_isect_offset_encode gives for an empty list (all zeros), with one
+    # sort pass (1024 tiles) and with two (3072 tiles).
+    tw, th = n_tiles
+    lib = _ops._lib()
+    C, N, cap = 1, 2000, 5000
+    m2 = torch.rand(1, N, 2, device=DEV) * 512
+    radii = torch.zeros(1, N, 2, dtype=torch.int32, device=DEV)
+    st = _ops._stream(torch.device(DEV))
+    tpg = torch.empty(C * N, dtype=torch.int32, device=DEV)
+    offsets = torch.empty(C * N + 1, dtype=torch.int64, device=DEV)
+    ws = _ops._workspace(lib.r2s_isect_workspace_bytes(C * N, 0, 0), m2.device)
+    _ops._call("r2s_isect_count_2d_f32", _ops._ptr(m2), _ops._ptr(radii), 1, C, N, 16, tw, th,
+               _ops._ptr(tpg), _ops._ptr(offsets), _ops._ptr(ws), ws.numel(), st)
+    end_bit = _ops._end_bit(C * tw * th)
+    outs = [torch.empty(cap, dtype=d, device=DEV)
+            for d in (torch.int64, torch.int32, torch.int32, torch.int32)]
+    tile_offsets = torch.full((C, th, tw), -7, dtype=torch.int32, device=DEV)
+    ws2 = _ops._workspace(lib.r2s_isect_workspace_bytes(0, cap, end_bit), m2.device)
+    _ops._call("r2s_isect_emit_sort_2d_f32", _ops._ptr(m2), _ops._ptr(radii), 1, C, N, 16, tw, th,
+               _ops._ptr(offsets), cap, end_bit, *[_ops._ptr(t) for t in outs],
+               _ops._ptr(tile_offsets), _ops._ptr(ws2), ws2.numel(), st)
+    empty = W.isect_offset_encode(torch.empty(0, dtype=torch.int64, device=DEV), C, tw, th)
+    torch.cuda.synchronize()
+    assert int(offsets[-1]) == 0
+    assert torch.equal(tile_offsets, empty) and not empty.any()
+
+
 @pytest.mark.parametrize("bricks", [(13, 13, 13), (256, 256, 160)])
 def test_isect_tiles_3d_sort_widths(bricks):
     # 2197 bricks: two 6-bit passes; 10.5 M bricks (24-bit keys): three passes.

@@ -16,17 +16,26 @@ import numpy as np
 import pytest
 import torch
 
+import pipeline_check
 from helpers import (VOXEL_ROW_SLOTS, check_voxel, check_voxel_sampled, np32, sample_keys,
                      voxel_references)
 from oracle import binning
 from r2splat import scenes
 from r2splat.cuda import _backend, _ops
 from r2splat.cuda import _wrapper as W
-from r2splat.ops import _passes, explicit
+from r2splat.ops import _passes
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 SMIN, SMAX = 5e-4, 1.0
+
+# Config 5's 5 % needles cross the middle bricks of the 512^3 volume by the
+# hundred; each voxel there sums many needle terms whose float32 sigma errs
+# by about u S (S up to ~1e4), beyond the bar's 1e-4 relative.  Measured:
+# 2.7 % and 3.6 % of the sampled voxels of the two slabs checked need the
+# conditioning term (err / (u |terms|) at most 1.2), 0.07 % of their records'
+# partials.  The cap is about twice the largest.
+SLAB_NEEDLE_FRAC = 0.08
 
 
 def _scene(n, seed, dims, log_mu=-3.2, needle_fraction=None):
@@ -107,23 +116,18 @@ def test_slabbed_volume_pass_matches_one_list(monkeypatch):
                                      v.to(DEV), d2, d1, d0, 8)
         for k, r in check_voxel(refs, grads=[np32(t) for t in got], tag=f"{name} ").items():
             print(name, k, r)
-    # Through the public API: the slabbed explicit step gives the same volume
-    # and its gradients meet the same bar (the composed chain is the same).
-    quats, scales, opac = (t.clone().to(DEV).requires_grad_(True) for t in
-                           (s["raw"].quats, s["raw"].raw_scales, s["raw"].raw_opacities))
-    means_p = means.clone().requires_grad_(True)
-    st = explicit.prepare_explicit_gaussians(quats, scales, opac, scale_min=SMIN, scale_max=SMAX)
+    # Through the public API: the slabbed explicit step gives the same volume,
+    # and every output and parameter gradient meets the bar against the
+    # oracle composition (the slabs' lists concatenated equal the oracle's
+    # whole list).
     from r2splat import geometry
 
     vm, Ks = geometry.cone_beam_views([0.3], 32)
-    res = explicit.explicit_rasterize(st, means_p, vm.to(DEV), Ks.to(DEV), img_w=32, img_h=32,
-                                      tile_size=16, eps2d=1e-8, radius_clip=3.0, absgrad=True)
-    vox = explicit.explicit_voxelize(st, means_p, rng, ctr, **kw)
-    assert st.voxel.slabs and torch.equal(vox.volume.detach(), one.volume)
-    (vox.volume * v.to(DEV)).sum().backward()
-    explicit.explicit_backward(st, means_p, quats, scales, opac)
-    assert torch.isfinite(means_p.grad).all() and float(means_p.grad.abs().sum()) > 0
-    del res
+    out = pipeline_check.run(s["raw"], vm, Ks, 32, 32, volume_shape=dims, v_volume=v)
+    assert out["state"].voxel.slabs and torch.equal(out["vox"].volume.detach(), one.volume)
+    reports = pipeline_check.check_against_oracle(out, s["raw"], vm, Ks, 32, 32,
+                                                  volume_shape=dims)
+    assert "voxel v_conics" in reports and "means (chain)" in reports
 
 
 def _rows_slab(p, lists, off, v, z0):
@@ -179,7 +183,8 @@ def test_config5_512_volume_with_needles_in_slabs():
         reps = check_voxel_sampled(np32(s["m3"]), np32(s["con"]), np32(s["op"]), np32(off),
                                    np32(lists.flatten_ids), np32(v), 512, 512, 512, 8, keys,
                                    volume=np32(vol), rows=sub.reshape(-1), isect_src=lookup,
-                                   tag=f"slab {z0}-{z1} ", key_offset=z0 * nb * nb)
+                                   tag=f"slab {z0}-{z1} ", key_offset=z0 * nb * nb,
+                                   max_frac=SLAB_NEEDLE_FRAC)
         for k, r in reps.items():
             print(f"slab [{z0}, {z1})", k, r, flush=True)
         del lists, off

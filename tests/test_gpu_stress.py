@@ -35,6 +35,15 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 N5, DET5, VOX5 = 2_000_000, 1024, 512
 
+# Needle-like footprints (axis ratio above 50, conic eigenvalue ratio above
+# 2500) make sigma's terms cancel: any float32 evaluation of sigma errs by
+# about u S, with S (the sum of |sigma's terms|) up to ~1e4, i.e. beyond the
+# bar's 1e-4 relative, so such elements need the conditioning term (with
+# err / (u |terms|) at most 1.6 measured).  Measured fractions of the
+# conditioning + flip classes: projection record partials 1.5e-3, the 0.05 %
+# needle volume's sampled voxels 1.1e-3.  The cap is about twice that.
+NEEDLE_FRAC = 3e-3
+
 
 def _config5(needle_fraction):
     g = torch.Generator().manual_seed(5)
@@ -65,8 +74,8 @@ def test_config5_volume_beyond_the_record_range_fails_cleanly(config5):
     assert torch.cuda.memory_allocated() - before < 2 ** 30
 
 
-def _project(d):
-    vm, Ks = geometry.cone_beam_views([math.radians(123.0)], DET5)
+def _project(d, degrees=123.0):
+    vm, Ks = geometry.cone_beam_views([math.radians(degrees)], DET5)
     return W.project_gaussians_fwd(d["means"], d["covars"], d["opac"], vm.to(DEV), Ks.to(DEV),
                                    DET5, DET5, 1e-8, 3.0)
 
@@ -98,8 +107,11 @@ def _sampled_rows(rows, lists, keys, off, slots):
     return sub.reshape(-1), lookup
 
 
-def test_config5_projection_lists_render_and_backward(config5):
-    m2, _, radii, con, mu, op = _project(config5)
+@pytest.mark.parametrize("degrees", [123.0, 0.0, 90.0, 237.0])
+def test_config5_projection_lists_render_and_backward(config5, degrees):
+    # Four views: the sampled tiles' pixels and record partials at each; the
+    # whole-list checks (numpy over 2e8 records) at the first.
+    m2, _, radii, con, mu, op = _project(config5, degrees)
     nt = DET5 // 16
     lists = _ops.bin_tiles_2d(m2, radii, 16, nt, nt)
     ids, fl = lists.isect_ids, lists.flatten_ids
@@ -108,28 +120,33 @@ def test_config5_projection_lists_render_and_backward(config5):
     assert n > 2_000_000
     x0, x1, y0, y1, count = binning.tile_rects_2d(np32(m2), np32(radii), 16, nt, nt)
     assert np.array_equal(np32(lists.tiles_per_gauss).reshape(-1), count) and n == int(count.sum())
-    ids_n, fl_n = np32(ids), np32(fl).astype(np.int64)
-    assert np.all((ids_n[1:] > ids_n[:-1]) | ((ids_n[1:] == ids_n[:-1]) & (fl_n[1:] > fl_n[:-1])))
-    tx, ty = ids_n % nt, ids_n // nt
-    assert np.all((tx >= x0[fl_n]) & (tx < x1[fl_n]) & (ty >= y0[fl_n]) & (ty < y1[fl_n]))
-    assert np.array_equal(np32(off).reshape(-1), np.searchsorted(ids_n, np.arange(nt * nt), "left"))
-    del ids_n, fl_n, tx, ty
+    print(f"{degrees} degrees: {n} tile records", flush=True)
+    if degrees == 123.0:
+        ids_n, fl_n = np32(ids), np32(fl).astype(np.int64)
+        assert np.all((ids_n[1:] > ids_n[:-1])
+                      | ((ids_n[1:] == ids_n[:-1]) & (fl_n[1:] > fl_n[:-1])))
+        tx, ty = ids_n % nt, ids_n // nt
+        assert np.all((tx >= x0[fl_n]) & (tx < x1[fl_n]) & (ty >= y0[fl_n]) & (ty < y1[fl_n]))
+        assert np.array_equal(np32(off).reshape(-1),
+                              np.searchsorted(ids_n, np.arange(nt * nt), "left"))
+        del ids_n, fl_n, tx, ty
 
     img = W.rasterize_to_pixels_fwd(m2, con, op, mu, off, fl, DET5, DET5, 16)
-    v = torch.randn((1, DET5, DET5), generator=config5["g"]).to(DEV)
+    v = torch.randn((1, DET5, DET5), generator=torch.Generator().manual_seed(int(degrees))).to(DEV)
     rows = _raster_rows(m2, con, op, mu, off, lists, v, DET5, DET5, 16)
-    keys = sample_keys(np32(off), n, 24, seed=5)
+    keys = sample_keys(np32(off), n, 24, seed=5 + int(degrees))
     table, lookup = _sampled_rows(rows, lists, keys, off, RASTER_ROW_SLOTS)
     del rows
     reps = check_raster_sampled(np32(m2), np32(con), np32(op), np32(mu), np32(off), np32(fl),
                                 np32(v), DET5, DET5, 16, keys, image=np32(img), rows=table,
-                                isect_src=lookup)
+                                isect_src=lookup, max_frac=NEEDLE_FRAC)
     for k, r in reps.items():
         print(k, r, flush=True)
-    two = _ops.raster_backward(m2, con, op, mu, off, lists, v, DET5, DET5, 16, True)
-    again = _ops.raster_backward(m2, con, op, mu, off, lists, v, DET5, DET5, 16, True)
-    for a, b in zip(two, again):
-        assert torch.equal(a, b)
+    if degrees == 123.0:
+        two = _ops.raster_backward(m2, con, op, mu, off, lists, v, DET5, DET5, 16, True)
+        again = _ops.raster_backward(m2, con, op, mu, off, lists, v, DET5, DET5, 16, True)
+        for a, b in zip(two, again):
+            assert torch.equal(a, b)
 
 
 def _voxel_rows(m3, con, op, off, lists, v, nb, key_offset=0):
@@ -172,7 +189,7 @@ def test_config5_voxel_lists_volume_and_backward():
     del rows
     reps = check_voxel_sampled(np32(m3), np32(con), np32(d["opac"]), np32(off), np32(fl),
                                np32(v), VOX5, VOX5, VOX5, 8, keys, volume=np32(vol), rows=table,
-                               isect_src=lookup)
+                               isect_src=lookup, max_frac=NEEDLE_FRAC)
     for k, r in reps.items():
         print(k, r, flush=True)
     two = _ops.voxel_backward(m3, con, d["opac"], off, lists, v, VOX5, VOX5, VOX5, 8)

@@ -121,6 +121,58 @@ def _dense_raster(means2d, conics, opac, mus, H, W, mask=None):
     return torch.where(keep, alpha, 0.0).sum(dim=1)
 
 
+def _pixel_mean_grads(means2d, conics, opac, mus, v, H, W, mask=None):
+    """[C, N, H, W, 2]: the gradient of v_p alpha_p with respect to the mean, for
+    every pixel p on its own.  Each pixel evaluates alpha with a private copy of
+    the mean, so autograd of the summed dense formulation returns the per-pixel
+    gradients in those copies' slots."""
+    C, N = means2d.shape[:2]
+    m = means2d.detach()[:, :, None, None, :].expand(C, N, H, W, 2).clone().requires_grad_(True)
+    py, px = torch.meshgrid(torch.arange(H) + 0.5, torch.arange(W) + 0.5, indexing="ij")
+    dx, dy = px - m[..., 0], py - m[..., 1]
+    con = conics.detach()
+    sigma = (0.5 * con[..., 0, None, None] * dx.square() + con[..., 1, None, None] * dx * dy
+             + 0.5 * con[..., 2, None, None] * dy.square())
+    alpha = (opac.detach() * mus.detach())[..., None, None] * torch.exp(-sigma)
+    keep = (sigma >= 0) & (alpha.abs() >= 1e-5)
+    if mask is not None:
+        keep = keep & mask
+    terms = torch.where(keep, alpha, 0.0) * torch.as_tensor(v)[:, None]
+    (g,) = torch.autograd.grad(terms.sum(), m)
+    return g
+
+
+def _tile_parts(g, ts, part):
+    """Sum the per-pixel gradients over each (tile, part) group: part(local index)
+    gives the group of a pixel inside its tile.  Returns [C, N, groups, 2]."""
+    C, N, H, W, _ = g.shape
+    th, tw = -(-H // ts), -(-W // ts)
+    pad = torch.zeros(C, N, th * ts, tw * ts, 2, dtype=g.dtype)
+    pad[:, :, :H, :W] = g
+    t = pad.reshape(C, N, th, ts, tw, ts, 2).permute(0, 1, 2, 4, 3, 5, 6)
+    t = t.reshape(C, N, th * tw, ts * ts, 2)
+    lab = torch.tensor([part(k) for k in range(ts * ts)])
+    n_lab = int(lab.max()) + 1
+    out = torch.zeros(C, N, th * tw, n_lab, 2, dtype=g.dtype)
+    out.index_add_(3, lab, t)
+    return out.reshape(C, N, -1, 2)
+
+
+def _check_absgrad(got_abs, t, v, H, W, ts, mask=None):
+    """The oracle's absgrad against sum_p |d(v_p alpha_p)/d mean|
+    (RasterizeToPixelsBwd.cu:444-445 per record, :218 in pixel mode), and two
+    planted mistakes that this comparison must reject: |.| taken after a lane's
+    strided pixel sum (lane l of 32 holds pixels l, l + 32, ...), and after the
+    record's whole-tile sum (after the warp sum)."""
+    g = _pixel_mean_grads(*t, v, H, W, mask)
+    want = g.abs().sum(dim=(2, 3)).numpy()
+    assert (want > 1e-6).mean() > 0.5
+    np.testing.assert_allclose(got_abs, want, rtol=1e-11, atol=1e-14)
+    for part in (lambda k: k % 32, lambda k: 0):
+        planted = _tile_parts(g, ts, part).abs().sum(dim=2).numpy()
+        assert not np.allclose(planted, want, rtol=1e-6, atol=1e-10)
+
+
 def test_raster_reference_kat():
     # tests/test_cuda_gaussian_ops.py:244-253 (two Gaussians, one 16x16 tile)
     means = np.array([[[5.2, 6.1], [10.0, 9.3]]])
@@ -138,6 +190,7 @@ def test_raster_reference_kat():
     exp = torch.autograd.grad((ref * w).sum(), t)
     for a, e in zip(got[1:], exp):
         np.testing.assert_allclose(a, e.numpy(), rtol=1e-11, atol=1e-13)
+    _check_absgrad(got[0], t, w.numpy(), 16, 16, 16)
     # float32 build of the same case within the parity bar.
     img32 = native.raster_fwd(*(a.astype(np.float32) for a in (means, conics, opac, mus)), off, fl,
                               16, 16, 16)
@@ -177,11 +230,10 @@ def test_raster_random_scene_matches_masked_dense():
     exp = torch.autograd.grad((ref * torch.tensor(v)).sum(), t)
     for a, e in zip(got[1:], exp):
         np.testing.assert_allclose(a, e.numpy(), rtol=1e-9, atol=1e-12)
-    # absgrad = sum over pixels of |per-pixel mean gradient|: bounded by the
-    # gradient and equal to it for a single-signed upstream gradient.
+    # absgrad: every pixel's own mean gradient by autograd, |.| per pixel,
+    # summed (RasterizeToPixelsBwd.cu:444-445); never below |gradient|.
+    _check_absgrad(got[0], t, v, H, W, ts, mask)
     assert (got[0] >= np.abs(got[1]) - 1e-12).all()
-    g1 = native.raster_bwd(means2d, conics, opac, mus, off, ids, np.abs(v), W, H, ts)
-    assert (g1[0] >= np.abs(g1[1]) - 1e-12).all()
     # Linear in opacity and mu once every alpha clears the cut-off.
     # Doubling opacity doubles every kept alpha; only alphas in [5e-6, 1e-5)
     # newly clear the cut-off, each adding at most 2e-5.

@@ -236,13 +236,25 @@ def test_assert_parity_reports_categories():
     assert rep == dict(n=4, within_bar=2, reference_order=1, conditioning=0, alpha_flips=1)
     with pytest.raises(AssertionError):
         assert_parity(act, anchor, lowp, band, "t", max_flips=0)
-    # |terms| = 1000 allows 8 u 1000 = 4.8e-4 of cancellation error: the
-    # element that needed its band now passes on its conditioning.
-    mag = np.array([1.0, 0.0, 5.0, 1000.0])
+    # |terms| = 4000 allows 2 u 4000 = 4.8e-4 of cancellation error: the
+    # element that needed its band now passes on its conditioning, which
+    # needed err / (u |terms|) = 1.68.
+    mag = np.array([1.0, 0.0, 5.0, 4000.0])
     rep = assert_parity(act, anchor, lowp, band, "t", mag=mag)
     assert (rep["conditioning"], rep["alpha_flips"]) == (1, 0)
+    assert rep["kappa_max"] == pytest.approx(4e-4 / (2.0 ** -24 * 4000), rel=1e-3)
     with pytest.raises(AssertionError, match="outside the parity bar"):
         assert_parity(act, anchor, lowp, None, "t", mag=mag / 10)
+    # The cap on the conditioning and flip classes: of 10,000 elements, 5
+    # that need their band pass a cap of 1e-3 (10 elements), not one of 1e-4
+    # (the floor of 4 elements).
+    big = np.zeros(10_000)
+    act5 = np.zeros(10_000, np.float32)
+    act5[:5] = 4e-4
+    band5 = np.where(np.arange(10_000) < 5, 1e-3, 0.0)
+    assert assert_parity(act5, big, big, band5, "c", max_frac=1e-3)["alpha_flips"] == 5
+    with pytest.raises(AssertionError, match="conditioning \\+ alpha flips above 4"):
+        assert_parity(act5, big, big, band5, "c", max_frac=1e-4)
     with pytest.raises(AssertionError, match="NaN pattern"):
         assert_parity(np.array([np.nan], np.float32), np.zeros(1), np.zeros(1), None, "n")
 
