@@ -509,10 +509,14 @@ def kernel_breakdown(proj: Projection, reps):
     the stream its kernels run on), averaged over the views.
 
     Entries other than ``binning_2d`` (count, scan, one host read, emit,
-    sort passes, offsets) and ``rasterize_bwd_op`` (both passes) are single
-    kernel launches: the two backward passes are timed apart through their
-    C entry points.  Returns per-stage mean seconds, the per-view times of
-    the raster kernels, and the record count of each view."""
+    sort passes, offsets), ``rasterize_bwd_op`` (pack and both passes) and
+    the forwards (the rows kernel, then the combine of a heavy tile's
+    partial tiles) are single kernel launches: r2splat.ops' pack, packed
+    forward and the two backward passes over the packed payload are timed
+    apart through their C entry points; ``rasterize_fwd`` is the
+    reference-signature forward (four-array gathers).  Returns per-stage
+    mean seconds, the per-view times of the raster kernels, and the record
+    count of each view."""
     from r2splat.cuda import _backend, _ops
     from r2splat.cuda import _wrapper as W
 
@@ -535,16 +539,39 @@ def kernel_breakdown(proj: Projection, reps):
         v_img = proj.v_images[v % 4]
         n = int(fl.numel())
         counts.append(n)
-        rows = torch.empty(lib.r2s_rasterize_bwd_workspace_bytes(n, N_PROJ, 4), dtype=torch.uint8,
+        rows = torch.empty(lib.r2s_rasterize_bwd_workspace_bytes(n, 0, 4), dtype=torch.uint8,
                            device=m2.device)
         outs = [torch.zeros_like(m2), torch.zeros_like(m2), torch.zeros_like(con),
                 torch.zeros_like(opc), torch.zeros_like(mu)]
+        payload = torch.empty(lib.r2s_rasterize_payload_bytes(N_PROJ, 4) // 4, device=m2.device)
+        fwd_ws = torch.empty(max(1, lib.r2s_rasterize_workspace_bytes(nt * nt, n, 16, 4)),
+                             dtype=torch.uint8, device=m2.device)
+        image = torch.empty((1, det, det), device=m2.device)
+
+        def pack():
+            # r2splat.ops' pack launch: the payload, and zeros into the
+            # backward's five outputs.
+            stream = torch.cuda.current_stream().cuda_stream
+            rc = lib.r2s_rasterize_pack_f32(P(m2), P(con), P(opc), P(mu), 1, N_PROJ, P(payload),
+                                            P(outs[0]), P(outs[1]), P(outs[2]), P(outs[3]),
+                                            P(outs[4]), stream)
+            assert rc == 0, lib.r2s_last_error()
+
+        pack()
+
+        def fwd_packed():
+            stream = torch.cuda.current_stream().cuda_stream
+            rc = lib.r2s_rasterize_fwd_packed_f32(P(payload), P(off), P(fl), n, 1, N_PROJ, det,
+                                                  det, 16, nt, nt, P(image), P(fwd_ws),
+                                                  fwd_ws.numel(), stream)
+            assert rc == 0, lib.r2s_last_error()
 
         def bwd_rows():
             stream = torch.cuda.current_stream().cuda_stream
-            rc = lib.r2s_rasterize_bwd_rows_f32(P(m2), P(con), P(opc), P(mu), P(off), P(ids),
-                                                P(fl), P(isect_src), n, P(v_img), 1, N_PROJ, det,
-                                                det, 16, nt, nt, 1, P(rows), rows.numel(), stream)
+            rc = lib.r2s_rasterize_bwd_rows_packed_f32(P(payload), P(off), P(ids), P(fl),
+                                                       P(isect_src), n, P(v_img), 1, N_PROJ, det,
+                                                       det, 16, nt, nt, 1, P(rows), rows.numel(),
+                                                       stream)
             assert rc == 0, lib.r2s_last_error()
 
         def bwd_reduce():
@@ -561,6 +588,8 @@ def kernel_breakdown(proj: Projection, reps):
             "binning_2d": lambda: W.isect_tiles(m2, r, 16, nt, nt),
             "rasterize_fwd": lambda: W.rasterize_to_pixels_fwd(m2, con, opc, mu, off, fl, det,
                                                                det, 16),
+            "rasterize_pack": pack,
+            "rasterize_fwd_packed": fwd_packed,
             "rasterize_bwd_rows": bwd_rows,
             "rasterize_bwd_reduce": bwd_reduce,
             "rasterize_bwd_op": lambda: W.rasterize_to_pixels_bwd_per_gaussian(
@@ -568,10 +597,11 @@ def kernel_breakdown(proj: Projection, reps):
         }
         for name, fn in stages.items():
             per_view.setdefault(name, []).append(time_kernel(fn, reps))
-        del rows, outs
+        del rows, outs, payload, fwd_ws, image
     mean = {k: sum(v) / len(v) for k, v in per_view.items()}
     return {"n_isects_2d": counts[0], "n_isects_per_view": counts, "seconds": mean,
-            "per_view_seconds": {k: per_view[k] for k in ("rasterize_fwd", "rasterize_bwd_rows")}}
+            "per_view_seconds": {k: per_view[k] for k in ("rasterize_fwd", "rasterize_fwd_packed",
+                                                          "rasterize_bwd_rows")}}
 
 
 def voxel_breakdown(vox, reps):
@@ -635,36 +665,61 @@ def voxel_breakdown(vox, reps):
     return {"n_isects_3d": n, "seconds": t, "given_reach_seconds": given}
 
 
+# The reference's arithmetic per evaluated (pixel / voxel, record) pair, in
+# flops (each add, subtract, multiply and negation; exp and compares not
+# counted), from its loops: the forward evaluates sigma and alpha and adds
+# alpha (RasterizeToPixelsFwd.cu:154-177, VoxelizeToVoxelsFwd.cu:186-214);
+# the per-Gaussian backward evaluates sigma and alpha again (16 / 26) and,
+# for a pixel that passes the alpha test, forms its gradient terms and adds
+# them to the record's sums (35 in 2D: v_sigma, both mean components, their
+# absolute values, three conic and the opacity and mu terms,
+# RasterizeToPixelsBwd.cu:419-451; 51 in 3D: v_sigma, o e^-sigma, the
+# opacity, six conic and three mean terms, VoxelizeToVoxelsBwd.cu:393-418).
+# Charging every evaluation with the gradient terms makes the backward
+# figures an upper bound of the reference's flops.
+FLOPS_PER_EVALUATION = {"rasterize_fwd": 15, "rasterize_bwd_rows": 16 + 35,
+                        "voxelize_fwd": 24, "voxelize_bwd_rows": 26 + 51}
+
+
 def kernel_roofline(kernel, seconds, algorithmic_bytes, evaluations=None):
-    """Roofline object of one kernel: average launch ``seconds`` (live), its
-    algorithmic bytes, and the counters of its committed rocprofv3 --pmc
-    summaries (HBM bytes, VALU / transcendental instructions per launch).
-    The raster and voxel kernels are bound by vector-ALU issue: when the VALU
-    counts are committed, ``bound`` is "valu" and ``achieved`` / ``peak``
-    are the issue rate in fp32 FMA-equivalent TFLOP/s (wave64 instructions
-    x 64 lanes x 2) against MI355X's 157.3; the HBM figures follow under
-    ``hbm``."""
+    """Roofline object of one kernel: its algorithmic bytes per launch over
+    its average launch ``seconds`` (live) against MI355X's 8 TB/s HBM peak
+    (``bound`` "hbm"), with the HBM bytes per launch its committed rocprofv3
+    --pmc summary measured (``traffic``).  The raster and voxel kernels are
+    limited by vector-ALU issue, not by HBM: ``valu`` gives that limit two
+    ways, from the committed VALU counters (wave64 instructions issued per
+    launch x 64 lanes x 2 flops, the fp32 FMA-equivalent issue rate) and
+    from the reference's own arithmetic (FLOPS_PER_EVALUATION x the
+    reference's evaluations per launch), both against MI355X's 157.3
+    TFLOP/s fp32 vector peak."""
     gbs = algorithmic_bytes / seconds / 1e9
     traffic = measured_traffic(kernel)
-    valu, trans = measured_valu(kernel)
-    hbm = {"achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
+    out = {"kernel": kernel, "bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS,
+           "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": traffic,
+           "algorithmic_bytes": int(algorithmic_bytes), "avg_launch_ms": seconds * 1e3,
            "source": f"profiles/pmc_{kernel}.txt"}
-    out = {"kernel": kernel, "algorithmic_bytes": int(algorithmic_bytes),
-           "avg_launch_ms": seconds * 1e3, "traffic": traffic}
-    if valu is None:
-        out.update({"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": gbs / HBM_PEAK_GBS})
+    valu, trans = measured_valu(kernel)
+    fpe = FLOPS_PER_EVALUATION.get(kernel)
+    if valu is None and fpe is None:
         return out
-    rate = valu / seconds / 1e9
-    tflops = rate * 128 / 1e3
-    out.update({"bound": "valu", "achieved": tflops, "peak": VALU_PEAK_TFLOPS,
-                "unit": "TFLOP/s", "frac": tflops / VALU_PEAK_TFLOPS, "hbm": hbm})
-    out["valu"] = {"reference_evaluations": evaluations,
-                   "executed_evaluations": None if trans is None else trans * 64,
-                   "wave_instructions_per_launch": valu,
-                   "achieved_g_wave_instructions_per_s": rate,
-                   "peak_g_wave_instructions_per_s": VALU_PEAK_G_WAVE_INSTR,
-                   "source": f"profiles/pmc_valu_{kernel}.txt"}
+    v = {"limit": "fp32 vector ALU issue", "peak_tflops": VALU_PEAK_TFLOPS,
+         "reference_evaluations": evaluations}
+    if fpe is not None and evaluations is not None:
+        flops = fpe * evaluations
+        v.update({"reference_flops_per_evaluation": fpe,
+                  "algorithmic_flops_per_launch": flops,
+                  "algorithmic_tflops": flops / seconds / 1e12,
+                  "algorithmic_flop_frac": flops / seconds / 1e12 / VALU_PEAK_TFLOPS})
+    if valu is not None:
+        rate = valu / seconds / 1e9
+        v.update({"executed_evaluations": None if trans is None else trans * 64,
+                  "wave_instructions_per_launch": valu,
+                  "achieved_g_wave_instructions_per_s": rate,
+                  "peak_g_wave_instructions_per_s": VALU_PEAK_G_WAVE_INSTR,
+                  "issue_tflops": rate * 128 / 1e3,
+                  "issue_frac": rate * 128 / 1e3 / VALU_PEAK_TFLOPS,
+                  "source": f"profiles/pmc_valu_{kernel}.txt"})
+    out["valu"] = v
     return out
 
 
@@ -997,15 +1052,18 @@ def main():
     # Dominant single kernel and its roofline (binning_2d and the backward op
     # span several launches and are not candidates).
     secs = kb["seconds"]
-    single = {k: v for k, v in secs.items() if k not in ("binning_2d", "rasterize_bwd_op")}
+    single = {k: v for k, v in secs.items()
+              if k not in ("binning_2d", "rasterize_bwd_op", "rasterize_fwd")}
     dom = max(single, key=single.get)
     n_pix = DET * DET
     dom_bytes = {
-        # list (key 8 + id 4) + payload 28 + partials 32 per record; v_image read
-        "rasterize_bwd_rows": 72 * i2_mean + 4 * n_pix,
+        # per record: list (key 8 + id 4) + payload 28 (mean 8, conic 12, opacity 4,
+        # mu 4) + partials 36 (8 + 8 + 12 + 4 + 4); v_image read once
+        "rasterize_bwd_rows": 76 * i2_mean + 4 * n_pix,
         # rows 32 + emission id 4 per record; o, mu in, 36 B out per Gaussian
         "rasterize_bwd_reduce": 36 * i2_mean + 44 * N_PROJ,
-        "rasterize_fwd": 32 * i2_mean + 4 * n_pix,   # id 4 + payload 28; image write
+        "rasterize_fwd_packed": 32 * i2_mean + 4 * n_pix,   # id 4 + payload 28; image write
+        "rasterize_pack": 64 * N_PROJ,   # 28 in, 36 zeros out per Gaussian
         "project_fwd": 108 * N_PROJ,
         "prepare": 76 * N_PROJ,
     }[dom]

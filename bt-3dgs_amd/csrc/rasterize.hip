@@ -136,6 +136,8 @@ __global__ __launch_bounds__(1024) void raster_fwd_kernel(
 // per-pixel order differs from a plain list-order sum only by rounding).
 constexpr int kFwdWaves = 8;
 constexpr int kFwdBatch = 64 * kFwdWaves;
+// Values per (view, Gaussian) of the packed payload (raster_pack_kernel).
+constexpr int kPayloadValues = 8;
 
 // One staged forward record: {x, y, h_a, h_b} and {h_c, o mu, limit bits, 0}.
 template <typename T>
@@ -156,13 +158,17 @@ inline uint32_t fwd_splits(int64_t n_keys, int64_t n_isects) {
   return static_cast<uint32_t>(s < 1 ? 1 : (s > 8 ? 8 : s));
 }
 
-template <typename T, int TS>
+// kPacked: each record's mean, conic and o mu come from the packed
+// per-(view, Gaussian) payload (raster_pack_kernel: 32 bytes in float, one
+// sector) instead of four arrays; the staged values, and so the image, are
+// the same bit for bit.
+template <typename T, int TS, bool kPacked>
 __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
     const T *__restrict__ means2d, const T *__restrict__ conics, const T *__restrict__ opac,
     const T *__restrict__ mus, const int32_t *__restrict__ tile_offsets,
     const int32_t *__restrict__ flatten_ids, int64_t n_isects, uint32_t n_keys, int64_t n_items,
     uint32_t W, uint32_t H, uint32_t tw, uint32_t th, uint32_t splits, T *__restrict__ image,
-    T *__restrict__ partial) {
+    T *__restrict__ partial, const T *__restrict__ payload) {
   using V2 = typename Vec<T>::v2;
   using V4 = typename Vec<T>::v4;
   constexpr int R = TS < 16 ? TS : 16;  // pixels per lane (a tile row, at most 16)
@@ -222,13 +228,25 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
       FwdRecord<T> rec;
       V4 &p = rec.p, &q = rec.q;
       if (g >= 0 && g < n_items) {
-        const V2 xy = *reinterpret_cast<const V2 *>(means2d + 2 * g);
-        p.x = xy.x;
-        p.y = xy.y;
-        p.z = hl * conics[3 * g];
-        p.w = l * conics[3 * g + 1];
-        q.x = hl * conics[3 * g + 2];
-        q.y = opac[g] * mus[g];
+        if (kPacked) {
+          // Payload: {x, y, a, b} {c, o mu, limit, hy}.
+          const V4 *src = reinterpret_cast<const V4 *>(payload + kPayloadValues * g);
+          const V4 a = src[0], b = src[1];
+          p.x = a.x;
+          p.y = a.y;
+          p.z = hl * a.z;
+          p.w = l * a.w;
+          q.x = hl * b.x;
+          q.y = b.y;
+        } else {
+          const V2 xy = *reinterpret_cast<const V2 *>(means2d + 2 * g);
+          p.x = xy.x;
+          p.y = xy.y;
+          p.z = hl * conics[3 * g];
+          p.w = l * conics[3 * g + 1];
+          q.x = hl * conics[3 * g + 2];
+          q.y = opac[g] * mus[g];
+        }
         // The alpha test's limit on the bits of sl (alpha_limit), kept in q.z.
         const bool fin = isfinite(p.x) && isfinite(p.y) && isfinite(p.z) && isfinite(p.w) &&
                          isfinite(q.x);
@@ -356,14 +374,14 @@ __device__ __forceinline__ void load_raster_record(
   if (cu.ok && !index_range<T>(rec.my, -cu.hy, cu.hy, oy, y1, rec.i0, rec.i1)) rec.live = false;
 }
 
-// Per-(view, Gaussian) payload of the two-pass backward: what its rows pass
-// needs, packed as 8 values of T (32 bytes in float) -- mean, conic, o mu,
-// the alpha limit's bits and the culling half-height hy (negative when the
-// conic is not positive definite) -- so that a record's gather touches one
-// sector instead of four arrays' lines, and the per-record culling setup
-// runs once per Gaussian.  The rows need no o or mu apart from o mu: the
-// reduction forms the opacity and mu partials from T0.
-constexpr int kPayloadValues = 8;
+// Per-(view, Gaussian) payload of the packed forward and of the two-pass
+// backward: what their record loads need, packed as kPayloadValues values of
+// T (32 bytes in float) -- mean, conic, o mu, the alpha limit's bits and the
+// culling half-height hy (negative when the conic is not positive definite)
+// -- so that a record's gather touches one sector instead of four arrays'
+// lines, and the per-record culling setup runs once per Gaussian.  The rows
+// need no o or mu apart from o mu: the reduction forms the opacity and mu
+// partials from T0.
 
 // With z_xy non-null it also stores zeros into the backward's outputs
 // (v_xy_abs may be null), which the reduction then overwrites for every pair
@@ -972,20 +990,29 @@ int check_raster_args(int64_t n_isects, int64_t C, int64_t N, uint32_t W, uint32
   return R2S_OK;
 }
 
+// payload != null: the records' data come from the packed payload
+// (raster_pack_kernel) and means2d .. mus are not read; tile sizes 8, 16, 32.
 template <typename T>
 int raster_fwd_impl(const T *means2d, const T *conics, const T *opac, const T *mus,
                     const int32_t *tile_offsets, const int32_t *flatten_ids, int64_t n_isects,
                     int64_t C, int64_t N, uint32_t W, uint32_t H, uint32_t ts, uint32_t tw,
-                    uint32_t th, T *image, void *ws, size_t ws_bytes, r2s_stream_t st) {
+                    uint32_t th, T *image, void *ws, size_t ws_bytes, r2s_stream_t st,
+                    const T *payload = nullptr) {
   clear_error();
-  const char *name = "rasterize_to_pixels_fwd";
+  const char *name = payload != nullptr ? "rasterize_to_pixels_fwd (packed)"
+                                        : "rasterize_to_pixels_fwd";
   R2S_RETURN_IF(check_raster_args(n_isects, C, N, W, H, ts, tw, th, name));
+  R2S_REQUIRE(payload == nullptr || ts == 8 || ts == 16 || ts == 32,
+              "%s: tile_size %u; the packed forward takes 8, 16 or 32", name, ts);
+  R2S_REQUIRE(payload == nullptr || reinterpret_cast<uintptr_t>(payload) % 16 == 0,
+              "%s: payload not 16-byte aligned", name);
   hipStream_t stream = as_stream(st);
   const int64_t n_pix = C * static_cast<int64_t>(W) * H;
   if (n_pix == 0) return R2S_OK;
   R2S_REQUIRE(image != nullptr, "%s: null image", name);
   if (N == 0 || n_isects == 0) return device_fill<T>(image, n_pix, static_cast<T>(0), stream, name);
-  R2S_REQUIRE(means2d && conics && opac && mus && tile_offsets && flatten_ids,
+  R2S_REQUIRE((payload != nullptr || (means2d && conics && opac && mus)) && tile_offsets &&
+                  flatten_ids,
               "%s: null pointer", name);
   const uint32_t n_keys = static_cast<uint32_t>(C) * tw * th;
   uint32_t splits = 1;
@@ -1004,9 +1031,14 @@ int raster_fwd_impl(const T *means2d, const T *conics, const T *opac, const T *m
   R2S_REQUIRE(static_cast<uint64_t>(n_keys) * splits <= 0x7fffffffull, "%s: too many tiles",
               name);
 #define R2S_RASTER_FWD_ROWS(TS)                                                                  \
-  raster_fwd_rows_kernel<T, TS><<<dim3(n_keys * splits), dim3(kFwdBatch), 0, stream>>>(        \
-      means2d, conics, opac, mus, tile_offsets, flatten_ids, n_isects, n_keys, C * N, W, H, tw,  \
-      th, splits, image, partial);                                                               \
+  if (payload != nullptr)                                                                        \
+    raster_fwd_rows_kernel<T, TS, true><<<dim3(n_keys * splits), dim3(kFwdBatch), 0, stream>>>( \
+        nullptr, nullptr, nullptr, nullptr, tile_offsets, flatten_ids, n_isects, n_keys, C * N,  \
+        W, H, tw, th, splits, image, partial, payload);                                          \
+  else                                                                                           \
+    raster_fwd_rows_kernel<T, TS, false><<<dim3(n_keys * splits), dim3(kFwdBatch), 0, stream>>>( \
+        means2d, conics, opac, mus, tile_offsets, flatten_ids, n_isects, n_keys, C * N, W, H,    \
+        tw, th, splits, image, partial, nullptr);                                                \
   if (splits > 1)                                                                                \
   fwd_combine_kernel<T, TS><<<dim3(n_keys), dim3(TS * TS), 0, stream>>>(partial, splits, W, H,   \
                                                                         tw, th, image)
@@ -1108,6 +1140,10 @@ int raster_reduce_impl(const T *rows, const int32_t *emit_ids, int64_t n_isects,
 
 // two_pass: emit_ids / isect_src / ws give the two-pass form (r2s_rows.h);
 // rows_only stops after the first pass (the rows are left in ws).
+// given_payload (two-pass only): the packed payload was written by
+// r2s_rasterize_pack_* already, ws holds only the rows, and means2d / conics
+// are not read; zeroed: the outputs hold zeros already (that pack launch
+// stored them).
 template <typename T>
 int raster_bwd_impl(const T *means2d, const T *conics, const T *opac, const T *mus,
                     const int32_t *tile_offsets, const int64_t *isect_ids,
@@ -1116,25 +1152,33 @@ int raster_bwd_impl(const T *means2d, const T *conics, const T *opac, const T *m
                     int64_t N, uint32_t W, uint32_t H, uint32_t ts, uint32_t tw, uint32_t th,
                     T *v_xy_abs, T *v_xy, T *v_conic, T *v_opac, T *v_mu, void *ws,
                     size_t ws_bytes, bool two_pass, r2s_stream_t st, bool rows_only = false,
-                    bool absgrad = true) {
+                    bool absgrad = true, const T *given_payload = nullptr, bool zeroed = false) {
   clear_error();
-  const char *name = two_pass   ? "rasterize_to_pixels_bwd (two-pass)"
-                     : isect_ids ? "rasterize_to_pixels_bwd_per_gaussian"
-                                 : "rasterize_to_pixels_bwd";
+  const char *name = given_payload ? "rasterize_to_pixels_bwd (two-pass, packed)"
+                     : two_pass    ? "rasterize_to_pixels_bwd (two-pass)"
+                     : isect_ids   ? "rasterize_to_pixels_bwd_per_gaussian"
+                                   : "rasterize_to_pixels_bwd";
   R2S_RETURN_IF(check_raster_args(n_isects, C, N, W, H, ts, tw, th, name));
+  R2S_REQUIRE(given_payload == nullptr || two_pass, "%s: a given payload needs the two-pass form",
+              name);
+  R2S_REQUIRE(given_payload == nullptr || reinterpret_cast<uintptr_t>(given_payload) % 16 == 0,
+              "%s: payload not 16-byte aligned", name);
   if (C * N == 0) return R2S_OK;
   if (n_isects == 0) {  // the two-pass form still stores its (zero) outputs
     if (!two_pass || rows_only) return R2S_OK;
     return raster_reduce_impl<T>(nullptr, nullptr, 0, C, N, opac, mus, v_xy_abs, v_xy,
-                                 v_conic, v_opac, v_mu, st);
+                                 v_conic, v_opac, v_mu, st, zeroed);
   }
   R2S_REQUIRE(tile_offsets && flatten_ids, "%s: null tile lists", name);
-  R2S_REQUIRE(means2d && conics && opac && mus && v_image, "%s: null pointer", name);
+  R2S_REQUIRE((given_payload != nullptr || (means2d && conics && opac && mus)) &&
+                  (rows_only || (opac && mus)) && v_image,
+              "%s: null pointer", name);
   R2S_REQUIRE(rows_only || (v_xy && v_conic && v_opac && v_mu), "%s: null output", name);
   T *rows = nullptr, *payload = nullptr;
   if (two_pass) {
     R2S_REQUIRE(isect_src && (rows_only || emit_ids), "%s: null emit_ids / isect_src", name);
-    const int64_t need = raster_bwd_ws_bytes(n_isects, C * N, sizeof(T));
+    const int64_t need = given_payload != nullptr ? raster_rows_bytes(n_isects, sizeof(T))
+                                                  : raster_bwd_ws_bytes(n_isects, C * N, sizeof(T));
     if (ws == nullptr || static_cast<int64_t>(ws_bytes) < need) {
       set_error("%s: workspace of %zu bytes, %lld required", name, ws_bytes, (long long)need);
       return R2S_EWORKSPACE;
@@ -1147,8 +1191,10 @@ int raster_bwd_impl(const T *means2d, const T *conics, const T *opac, const T *m
   const uint32_t n_keys = static_cast<uint32_t>(C) * tw * th;
   hipStream_t stream = as_stream(st);
   // The full two-pass call zeroes its outputs in the pack launch.
-  const bool zero_in_pack = two_pass && !rows_only;
-  if (two_pass)
+  const bool zero_in_pack = given_payload != nullptr ? zeroed : two_pass && !rows_only;
+  if (given_payload != nullptr)
+    payload = const_cast<T *>(given_payload);
+  else if (two_pass)
     raster_pack_kernel<T><<<dim3(static_cast<uint32_t>(ceil_div(C * N, 256))), dim3(256), 0,
                             stream>>>(means2d, conics, opac, mus, C * N, payload,
                                       zero_in_pack ? v_xy : nullptr, v_xy_abs, v_conic, v_opac,
@@ -1181,6 +1227,29 @@ int raster_bwd_impl(const T *means2d, const T *conics, const T *opac, const T *m
   if (!two_pass || rows_only) return R2S_OK;
   return raster_reduce_impl<T>(rows, emit_ids, n_isects, C, N, opac, mus, v_xy_abs, v_xy,
                                v_conic, v_opac, v_mu, st, zero_in_pack);
+}
+
+// The packed payload of the C N (view, Gaussian) pairs (raster_pack_kernel),
+// and with v_xy non-null zeros in the two-pass backward's outputs (v_xy_abs
+// may be null).
+template <typename T>
+int raster_pack_impl(const T *means2d, const T *conics, const T *opac, const T *mus, int64_t C,
+                     int64_t N, T *payload, T *v_xy_abs, T *v_xy, T *v_conic, T *v_opac, T *v_mu,
+                     r2s_stream_t st) {
+  clear_error();
+  const char *name = "rasterize_pack";
+  R2S_REQUIRE(C >= 0 && N >= 0 && C * N <= kInt32Max, "%s: bad size C=%lld N=%lld", name,
+              (long long)C, (long long)N);
+  if (C * N == 0) return R2S_OK;
+  R2S_REQUIRE(means2d && conics && opac && mus && payload, "%s: null pointer", name);
+  R2S_REQUIRE(reinterpret_cast<uintptr_t>(payload) % 16 == 0, "%s: payload not 16-byte aligned",
+              name);
+  R2S_REQUIRE(v_xy == nullptr || (v_conic && v_opac && v_mu),
+              "%s: zero targets need v_means2d, v_conics, v_opacities and v_mus", name);
+  raster_pack_kernel<T><<<dim3(static_cast<uint32_t>(ceil_div(C * N, 256))), dim3(256), 0,
+                          as_stream(st)>>>(means2d, conics, opac, mus, C * N, payload, v_xy,
+                                           v_xy_abs, v_conic, v_opac, v_mu);
+  return check_launch(name);
 }
 
 // Device address of `scratch` on the current device, looked up once per
@@ -1322,7 +1391,7 @@ int64_t r2s_rasterize_workspace_bytes(int64_t n_keys, int64_t n_isects, uint32_t
     return r2s::raster_bwd_impl<T>(means2d, conics, opac, mus, tile_offsets, isect_ids,       \
                                    flatten_ids, emit_ids, isect_src, n_isects, v_image, C, N, \
                                    W, H, ts, tw, th, v_xy_abs, v_xy, v_conic, v_opac, v_mu,   \
-                                   ws, ws_bytes, true, st);                                   \
+                                   ws, ws_bytes, true, st, false, v_xy_abs != nullptr);       \
   }
 
 #define R2S_RASTER_STAGE_API(SUF, T)                                                          \
@@ -1350,6 +1419,58 @@ R2S_RASTER_STAGE_API(f32, float)
 R2S_RASTER_STAGE_API(f64, double)
 
 #undef R2S_RASTER_STAGE_API
+
+int64_t r2s_rasterize_payload_bytes(int64_t n_items, int dtype_bytes) {
+  if (n_items <= 0 || (dtype_bytes != 4 && dtype_bytes != 8)) return 0;
+  return n_items * r2s::kPayloadValues * static_cast<int64_t>(dtype_bytes);
+}
+
+#define R2S_RASTER_PACKED_API(SUF, T)                                                         \
+  int r2s_rasterize_pack_##SUF(const T *means2d, const T *conics, const T *opac,              \
+                               const T *mus, int64_t C, int64_t N, T *payload, T *v_xy_abs,   \
+                               T *v_xy, T *v_conic, T *v_opac, T *v_mu, r2s_stream_t st) {    \
+    return r2s::raster_pack_impl<T>(means2d, conics, opac, mus, C, N, payload, v_xy_abs,      \
+                                    v_xy, v_conic, v_opac, v_mu, st);                         \
+  }                                                                                           \
+  int r2s_rasterize_fwd_packed_##SUF(const T *payload, const int32_t *tile_offsets,           \
+                                     const int32_t *flatten_ids, int64_t n_isects, int64_t C, \
+                                     int64_t N, uint32_t W, uint32_t H, uint32_t ts,          \
+                                     uint32_t tw, uint32_t th, T *image, void *ws,            \
+                                     size_t ws_bytes, r2s_stream_t st) {                      \
+    return r2s::raster_fwd_impl<T>(nullptr, nullptr, nullptr, nullptr, tile_offsets,         \
+                                   flatten_ids, n_isects, C, N, W, H, ts, tw, th, image, ws,  \
+                                   ws_bytes, st, payload);                                    \
+  }                                                                                           \
+  int r2s_rasterize_bwd_packed_##SUF(                                                         \
+      const T *payload, const T *opac, const T *mus, const int32_t *tile_offsets,             \
+      const int64_t *isect_ids, const int32_t *flatten_ids, const int32_t *emit_ids,          \
+      const int32_t *isect_src, int64_t n_isects, const T *v_image, int64_t C, int64_t N,     \
+      uint32_t W, uint32_t H, uint32_t ts, uint32_t tw, uint32_t th, T *v_xy_abs, T *v_xy,    \
+      T *v_conic, T *v_opac, T *v_mu, int zeroed, void *ws, size_t ws_bytes,                  \
+      r2s_stream_t st) {                                                                      \
+    return r2s::raster_bwd_impl<T>(nullptr, nullptr, opac, mus, tile_offsets, isect_ids,      \
+                                   flatten_ids, emit_ids, isect_src, n_isects, v_image, C, N, \
+                                   W, H, ts, tw, th, v_xy_abs, v_xy, v_conic, v_opac, v_mu,   \
+                                   ws, ws_bytes, true, st, false, v_xy_abs != nullptr,        \
+                                   payload, zeroed != 0);                                     \
+  }                                                                                           \
+  int r2s_rasterize_bwd_rows_packed_##SUF(                                                    \
+      const T *payload, const int32_t *tile_offsets, const int64_t *isect_ids,                \
+      const int32_t *flatten_ids, const int32_t *isect_src, int64_t n_isects,                 \
+      const T *v_image, int64_t C, int64_t N, uint32_t W, uint32_t H, uint32_t ts,            \
+      uint32_t tw, uint32_t th, int absgrad, void *rows, size_t rows_bytes,                   \
+      r2s_stream_t st) {                                                                      \
+    return r2s::raster_bwd_impl<T>(nullptr, nullptr, nullptr, nullptr, tile_offsets,         \
+                                   isect_ids, flatten_ids, nullptr, isect_src, n_isects,      \
+                                   v_image, C, N, W, H, ts, tw, th, nullptr, nullptr,         \
+                                   nullptr, nullptr, nullptr, rows, rows_bytes, true, st,     \
+                                   true, absgrad != 0, payload);                              \
+  }
+
+R2S_RASTER_PACKED_API(f32, float)
+R2S_RASTER_PACKED_API(f64, double)
+
+#undef R2S_RASTER_PACKED_API
 
 R2S_RASTER_API(f32, float)
 R2S_RASTER_API(f64, double)

@@ -52,6 +52,13 @@ _FLOAT_OPS = {
     "rasterize_bwd_rows": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _u32, _u32, _u32,
                            _u32, _u32, _i32, _p, _sz, _p],
     "rasterize_bwd_reduce": [_p, _p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p],
+    "rasterize_pack": [_p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p],
+    "rasterize_fwd_packed": [_p, _p, _p, _i64, _i64, _i64, _u32, _u32, _u32, _u32, _u32, _p, _p,
+                             _sz, _p],
+    "rasterize_bwd_packed": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _u32, _u32,
+                             _u32, _u32, _u32, _p, _p, _p, _p, _p, _i32, _p, _sz, _p],
+    "rasterize_bwd_rows_packed": [_p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _u32, _u32, _u32,
+                                  _u32, _u32, _i32, _p, _sz, _p],
     "world_to_volume_mapping_fwd": [_p, _p, _p, _p, _u32, _u32, _u32, _f64, _f64, _p, _p, _p,
                                     _i64, _p],
     "world_to_volume_mapping_bwd": [_p, _p, _p, _p, _u32, _u32, _u32, _f64, _p, _p, _p, _p,
@@ -91,6 +98,7 @@ _PLAIN = {
     "r2s_isect_offset_encode": (_i32, [_p, _i64, _i64, _p, _p]),
     "r2s_rasterize_workspace_bytes": (_i64, [_i64, _i64, _u32, _i32]),
     "r2s_rasterize_bwd_workspace_bytes": (_i64, [_i64, _i64, _i32]),
+    "r2s_rasterize_payload_bytes": (_i64, [_i64, _i32]),
     "r2s_voxelize_bwd_workspace_bytes": (_i64, [_i64, _i32]),
     "r2s_mask_workspace_bytes": (_i64, [_i64]),
     "r2s_mask_split": (_i32, [_p, _i64, _p, _p, _p, _sz, _p]),
@@ -143,7 +151,7 @@ DENSIFY_MAX_WIDTH = 16
 
 SYMBOLS = sorted(list(_PLAIN) + [f"r2s_{n}_{s}" for n in _FLOAT_OPS for s in ("f32", "f64")])
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 
 def load(path: str = LIB_PATH) -> ctypes.CDLL:

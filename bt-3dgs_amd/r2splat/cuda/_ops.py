@@ -1022,6 +1022,120 @@ def raster_backward(means2d: Tensor, conics: Tensor, opacities: Tensor, mus: Ten
                        "raster_backward", emission=lists.emission)
 
 
+# The packed passes of r2splat.ops: the mean, conic, o mu and the alpha
+# test's limit of every (view, Gaussian) pair packed once per call into 32
+# bytes (float32), read by the forward and the two-pass backward as one load
+# per record instead of four arrays' lines.
+
+PACKED_TILE_SIZES = (8, 16, 32)
+
+
+def raster_pack(means2d: Tensor, conics: Tensor, opacities: Tensor, mus: Tensor,
+                zero_outputs: bool = False, absgrad: bool = False):
+    """-> (payload [C*N*8] of the inputs' dtype, outputs): with
+    ``zero_outputs`` the raster backward's five outputs (v_means2d_abs only
+    with ``absgrad``), zeroed by the same launch, else None."""
+    for t, n in ((means2d, "means2d"), (conics, "conics"), (opacities, "opacities"),
+                 (mus, "mus")):
+        _check_input(t, n)
+    _check(means2d.dim() == 3 and means2d.size(2) == 2, "means2d must be [C, N, 2]")
+    C, N = means2d.size(0), means2d.size(1)
+    _check(conics.shape == (C, N, 3) and opacities.shape == (C, N) and mus.shape == (C, N),
+           "conics [C,N,3], opacities and mus [C,N] must match means2d")
+    _check(conics.dtype == means2d.dtype and opacities.dtype == means2d.dtype
+           and mus.dtype == means2d.dtype, "means2d, conics, opacities and mus must share a dtype")
+    dev = means2d.device
+    payload = torch.empty((C * N * 8,), dtype=means2d.dtype, device=dev)
+    outs = None
+    if zero_outputs:
+        outs = (torch.empty_like(means2d) if absgrad else None, torch.empty_like(means2d),
+                torch.empty_like(conics), torch.empty_like(opacities), torch.empty_like(mus))
+    if C * N == 0:
+        return payload, outs
+    sfx = _suffix(means2d, "rasterize_pack")
+    z = (None,) * 5 if outs is None else outs
+    with torch.cuda.device(dev):
+        _call(f"r2s_rasterize_pack_{sfx}", _ptr(means2d), _ptr(conics), _ptr(opacities),
+              _ptr(mus), C, N, _ptr(payload), *[_ptr(t) for t in z], _stream(dev))
+    return payload, outs
+
+
+def rasterize_packed(payload: Tensor, tile_offsets: Tensor, flatten_ids: Tensor, C: int, N: int,
+                     img_w: int, img_h: int, tile_size: int) -> Tensor:
+    """The rasterizer forward over a payload of :func:`raster_pack` (tile
+    sizes 8, 16 and 32) -> image [C, img_h, img_w], the same as
+    rasterize_to_pixels_fwd's bit for bit."""
+    for t, n in ((payload, "payload"), (tile_offsets, "tile_offsets"),
+                 (flatten_ids, "flatten_ids")):
+        _check_input(t, n)
+    C, N, W, H, ts = int(C), int(N), int(img_w), int(img_h), int(tile_size)
+    _check(ts in PACKED_TILE_SIZES, "the packed rasterizer takes tile sizes 8, 16 and 32")
+    _check(payload.numel() == C * N * 8, "payload must hold 8 values per (view, Gaussian)")
+    _check(tile_offsets.dim() == 3 and tile_offsets.size(0) == C, "tile_offsets must be [C,th,tw]")
+    th, tw = tile_offsets.size(1), tile_offsets.size(2)
+    dev = payload.device
+    out = torch.empty((C, H, W), dtype=payload.dtype, device=dev)
+    n_isects = flatten_ids.numel()
+    if C == 0 or N == 0 or n_isects == 0:
+        return out.zero_()
+    sfx = _suffix(payload, "rasterize_packed")
+    lib = _lib()
+    with torch.cuda.device(dev):
+        nbytes = lib.r2s_rasterize_workspace_bytes(C * tw * th, n_isects, ts,
+                                                   payload.element_size())
+        ws = _workspace(nbytes, dev) if nbytes > 0 else None
+        _call(f"r2s_rasterize_fwd_packed_{sfx}", _ptr(payload), _ptr(tile_offsets),
+              _ptr(flatten_ids), n_isects, C, N, W, H, ts, tw, th, _ptr(out), _ptr(ws),
+              0 if ws is None else ws.numel(), _stream(dev))
+    return out
+
+
+def raster_backward_packed(payload: Tensor, opacities: Tensor, mus: Tensor,
+                           tile_offsets: Tensor, lists: TileLists, v_image: Tensor, img_w: int,
+                           img_h: int, tile_size: int, absgrad: bool, zeroed_outputs=None):
+    """:func:`raster_backward` over a payload of :func:`raster_pack` (the
+    two-pass kernels without their own pack launch) -> (v_means2d_abs or None,
+    v_means2d, v_conics, v_opacities, v_mus).  ``zeroed_outputs``: the
+    outputs raster_pack zeroed (written in place and returned), else new."""
+    for t, n in ((payload, "payload"), (opacities, "opacities"), (mus, "mus"),
+                 (tile_offsets, "tile_offsets"), (lists.flatten_ids, "flatten_ids"),
+                 (v_image, "v_render_output")):
+        _check_input(t, n)
+    _check(opacities.dim() == 2, "opacities must be [C, N]")
+    C, N = opacities.size(0), opacities.size(1)
+    W, H, ts = int(img_w), int(img_h), int(tile_size)
+    _check(payload.numel() == C * N * 8, "payload must hold 8 values per (view, Gaussian)")
+    _check(v_image.shape == (C, H, W), "v_render_output shape must be [C, dim0, dim1]")
+    dev, dt = payload.device, payload.dtype
+    zeroed = zeroed_outputs is not None and (zeroed_outputs[0] is not None or not absgrad)
+    if zeroed:
+        outs = (zeroed_outputs[0] if absgrad else None,) + tuple(zeroed_outputs[1:])
+    else:
+        outs = (torch.empty((C, N, 2), dtype=dt, device=dev) if absgrad else None,
+                torch.empty((C, N, 2), dtype=dt, device=dev),
+                torch.empty((C, N, 3), dtype=dt, device=dev),
+                torch.empty((C, N), dtype=dt, device=dev),
+                torch.empty((C, N), dtype=dt, device=dev))
+    if C * N == 0:
+        return outs
+    n_isects = lists.flatten_ids.numel()
+    th, tw = tile_offsets.size(1), tile_offsets.size(2)
+    if n_isects > 0:
+        _check(lists.emission is not None, "raster_backward_packed needs the emission order")
+        _note_path(True, "raster_backward_packed")
+    emit, src = lists.emission if n_isects > 0 else (None, None)
+    sfx = _suffix(payload, "raster_backward_packed")
+    with torch.cuda.device(dev):
+        nbytes = _lib().r2s_rasterize_bwd_workspace_bytes(n_isects, 0, payload.element_size())
+        ws = _workspace(nbytes, dev) if nbytes > 0 else None
+        _call(f"r2s_rasterize_bwd_packed_{sfx}", _ptr(payload), _ptr(opacities), _ptr(mus),
+              _ptr(tile_offsets), _ptr(lists.isect_ids), _ptr(lists.flatten_ids), _ptr(emit),
+              _ptr(src), n_isects, _ptr(v_image), C, N, W, H, ts, tw, th,
+              *[_ptr(t) for t in outs], 1 if zeroed else 0, _ptr(ws),
+              0 if ws is None else ws.numel(), _stream(dev))
+    return outs
+
+
 # ------------------------------------------------------------ voxelization --
 
 def world_to_volume_mapping_fwd(means: Tensor, covars: Tensor, max_scales: Tensor,

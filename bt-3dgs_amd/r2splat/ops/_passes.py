@@ -108,12 +108,18 @@ class ImagePass:
     lists: object  # r2splat.cuda._ops.TileLists
     image: Tensor
     absgrad: bool = False
+    # Tile sizes 8, 16 and 32 with records: the packed per-(view, Gaussian)
+    # payload both raster passes read, and (for_backward) the raster
+    # backward's outputs, zeroed by the launch that wrote it; handed to the
+    # first vjp.
+    payload: Optional[Tensor] = None
+    zeroed_outputs: Optional[tuple] = None
 
     @classmethod
     @torch.no_grad()
     def run(cls, means: Tensor, covars: Tensor, opacities: Tensor, viewmats: Tensor, Ks: Tensor,
-            *, img_w: int, img_h: int, tile_size: int, eps2d: float,
-            radius_clip: float) -> "ImagePass":
+            *, img_w: int, img_h: int, tile_size: int, eps2d: float, radius_clip: float,
+            absgrad: bool = False, for_backward: bool = False) -> "ImagePass":
         ts = int(tile_size)
         if ts <= 0 or ts * ts > 1024:
             raise ValueError(TILE_2D)
@@ -129,17 +135,35 @@ class ImagePass:
         if tile_offsets is None:  # no records
             tile_offsets = ops.isect_offset_encode(lists.isect_ids, int(viewmats.shape[0]),
                                                    across, down)
-        image = ops.rasterize_to_pixels_fwd(means2d, conics, weights, mus, tile_offsets,
-                                            lists.flatten_ids, width, height, ts)
+        payload = zeroed = None
+        if ts in ops.PACKED_TILE_SIZES and lists.flatten_ids.numel() > 0:
+            payload, zeroed = ops.raster_pack(means2d, conics, weights, mus,
+                                              zero_outputs=for_backward, absgrad=absgrad)
+            image = ops.rasterize_packed(payload, tile_offsets, lists.flatten_ids,
+                                         means2d.shape[0], means2d.shape[1], width, height, ts)
+        else:
+            image = ops.rasterize_to_pixels_fwd(means2d, conics, weights, mus, tile_offsets,
+                                                lists.flatten_ids, width, height, ts)
         return cls(width, height, ts, float(eps2d), viewmats, Ks, means2d, cov2d, conics, mus,
-                   weights, radii, tile_offsets, lists, image)
+                   weights, radii, tile_offsets, lists, image, bool(absgrad), payload, zeroed)
+
+    def _raster_vjp(self, v_image: Tensor):
+        """The rasterizer's VJP: (v_abs or None, v_means2d, v_conics, v_weights, v_mus)."""
+        ops = _ops()
+        if self.payload is None:
+            return ops.raster_backward(self.means2d, self.conics, self.weights, self.mus,
+                                       self.tile_offsets, self.lists, v_image.contiguous(),
+                                       self.width, self.height, self.tile_size, self.absgrad)
+        zeroed, self.zeroed_outputs = self.zeroed_outputs, None
+        return ops.raster_backward_packed(self.payload, self.weights, self.mus,
+                                          self.tile_offsets, self.lists, v_image.contiguous(),
+                                          self.width, self.height, self.tile_size, self.absgrad,
+                                          zeroed)
 
     @torch.no_grad()
     def vjp(self, v_image: Tensor, means: Tensor, covars: Tensor) -> ImageVJP:
         ops = _ops()
-        v_abs, v_means2d, v_conics, v_weights, v_mus = ops.raster_backward(
-            self.means2d, self.conics, self.weights, self.mus, self.tile_offsets, self.lists,
-            v_image.contiguous(), self.width, self.height, self.tile_size, self.absgrad)
+        v_abs, v_means2d, v_conics, v_weights, v_mus = self._raster_vjp(v_image)
         v_means, v_covars = ops.project_gaussians_bwd(
             means.contiguous(), covars, self.viewmats, self.Ks, self.width, self.height,
             self.eps2d, self.cov2d, self.conics, self.mus, v_means2d, v_conics, v_mus)
@@ -156,9 +180,7 @@ class ImagePass:
         and opacity VJPs (bit-identical to vjp + parameter_transform_bwd +
         opacity_bwd with the world-space gradients summed image + volume)."""
         ops = _ops()
-        v_abs, v_means2d, v_conics, v_weights, v_mus = ops.raster_backward(
-            self.means2d, self.conics, self.weights, self.mus, self.tile_offsets, self.lists,
-            v_image.contiguous(), self.width, self.height, self.tile_size, self.absgrad)
+        v_abs, v_means2d, v_conics, v_weights, v_mus = self._raster_vjp(v_image)
         v_means, v_quats, v_raw_scales, v_raw_opac = ops.explicit_backward_tail(
             means.contiguous(), covars.contiguous(), self.viewmats, self.Ks, self.width,
             self.height, self.eps2d, self.cov2d, self.conics, self.mus, v_means2d, v_conics,

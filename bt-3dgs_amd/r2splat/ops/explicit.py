@@ -99,7 +99,7 @@ def explicit_rasterize(
         raise RuntimeError("An explicit Gaussian state can only be rasterized once.")
     image_pass = ImagePass.run(means, state.covars, state.opacities, viewmats, Ks, img_w=img_w,
                                img_h=img_h, tile_size=tile_size, eps2d=eps2d,
-                               radius_clip=radius_clip)
+                               radius_clip=radius_clip, absgrad=bool(absgrad), for_backward=True)
     image_pass.image = _leaf(image_pass.image)
     image_pass.means2d = _leaf(image_pass.means2d)
     image_pass.absgrad = bool(absgrad)

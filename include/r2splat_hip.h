@@ -528,6 +528,82 @@ int r2s_rasterize_bwd_reduce_f64(const double *rows, const int32_t *emit_ids,
                                  double *v_means2d_abs, double *v_means2d, double *v_conics,
                                  double *v_opacities, double *v_mus, r2s_stream_t stream);
 
+/* The rasterizer over a packed per-(view, Gaussian) payload: the same
+ * operations as RasterizeToPixelsFwd.cu:57-186 / RasterizeToPixelsBwd.cu:
+ * 350-480 (the reference reads the four arrays directly; it has no payload).
+ * r2s_rasterize_pack_* writes the payload [C*N*8] of T
+ * (r2s_rasterize_payload_bytes, 16-byte aligned): per pair the mean, the
+ * conic, o mu = opacities * mus, the alpha test's limit and the culling
+ * half-height; with v_means2d non-NULL it also stores zeros into the
+ * two-pass backward's outputs (v_means2d_abs may be NULL).  Written once per
+ * call, it serves both passes: r2s_rasterize_fwd_packed_* (tile sizes 8, 16
+ * and 32; the same image as r2s_rasterize_fwd_* bit for bit; workspace as
+ * r2s_rasterize_workspace_bytes) reads a record's data as one 32-byte load
+ * instead of four arrays' lines, and r2s_rasterize_bwd_packed_* is
+ * r2s_rasterize_bwd_emit_* without its own pack launch (workspace: the rows
+ * only, r2s_rasterize_bwd_workspace_bytes(n_isects, 0, dtype_bytes); zeroed:
+ * the outputs hold zeros already, from the pack call).  _bwd_rows_packed:
+ * its first pass alone, as r2s_rasterize_bwd_rows_* over the given payload
+ * (rows: r2s_rasterize_bwd_workspace_bytes(n_isects, 0, dtype_bytes)).
+ * Used by r2splat.ops. */
+int64_t r2s_rasterize_payload_bytes(int64_t n_items, int dtype_bytes);
+int r2s_rasterize_pack_f32(const float *means2d, const float *conics,
+                           const float *opacities, const float *mus, int64_t C, int64_t N,
+                           float *payload, float *v_means2d_abs, float *v_means2d,
+                           float *v_conics, float *v_opacities, float *v_mus,
+                           r2s_stream_t stream);
+int r2s_rasterize_pack_f64(const double *means2d, const double *conics,
+                           const double *opacities, const double *mus, int64_t C, int64_t N,
+                           double *payload, double *v_means2d_abs, double *v_means2d,
+                           double *v_conics, double *v_opacities, double *v_mus,
+                           r2s_stream_t stream);
+int r2s_rasterize_fwd_packed_f32(const float *payload, const int32_t *tile_offsets,
+                                 const int32_t *flatten_ids, int64_t n_isects, int64_t C,
+                                 int64_t N, uint32_t width, uint32_t height,
+                                 uint32_t tile_size, uint32_t n_tiles_w, uint32_t n_tiles_h,
+                                 float *image, void *workspace, size_t workspace_bytes,
+                                 r2s_stream_t stream);
+int r2s_rasterize_fwd_packed_f64(const double *payload, const int32_t *tile_offsets,
+                                 const int32_t *flatten_ids, int64_t n_isects, int64_t C,
+                                 int64_t N, uint32_t width, uint32_t height,
+                                 uint32_t tile_size, uint32_t n_tiles_w, uint32_t n_tiles_h,
+                                 double *image, void *workspace, size_t workspace_bytes,
+                                 r2s_stream_t stream);
+int r2s_rasterize_bwd_packed_f32(const float *payload, const float *opacities,
+                                 const float *mus, const int32_t *tile_offsets,
+                                 const int64_t *isect_ids, const int32_t *flatten_ids,
+                                 const int32_t *emit_ids, const int32_t *isect_src,
+                                 int64_t n_isects, const float *v_image, int64_t C, int64_t N,
+                                 uint32_t width, uint32_t height, uint32_t tile_size,
+                                 uint32_t n_tiles_w, uint32_t n_tiles_h, float *v_means2d_abs,
+                                 float *v_means2d, float *v_conics, float *v_opacities,
+                                 float *v_mus, int zeroed, void *workspace,
+                                 size_t workspace_bytes, r2s_stream_t stream);
+int r2s_rasterize_bwd_packed_f64(const double *payload, const double *opacities,
+                                 const double *mus, const int32_t *tile_offsets,
+                                 const int64_t *isect_ids, const int32_t *flatten_ids,
+                                 const int32_t *emit_ids, const int32_t *isect_src,
+                                 int64_t n_isects, const double *v_image, int64_t C, int64_t N,
+                                 uint32_t width, uint32_t height, uint32_t tile_size,
+                                 uint32_t n_tiles_w, uint32_t n_tiles_h,
+                                 double *v_means2d_abs, double *v_means2d, double *v_conics,
+                                 double *v_opacities, double *v_mus, int zeroed,
+                                 void *workspace, size_t workspace_bytes, r2s_stream_t stream);
+int r2s_rasterize_bwd_rows_packed_f32(const float *payload, const int32_t *tile_offsets,
+                                      const int64_t *isect_ids, const int32_t *flatten_ids,
+                                      const int32_t *isect_src, int64_t n_isects,
+                                      const float *v_image, int64_t C, int64_t N,
+                                      uint32_t width, uint32_t height, uint32_t tile_size,
+                                      uint32_t n_tiles_w, uint32_t n_tiles_h, int absgrad,
+                                      void *rows, size_t rows_bytes, r2s_stream_t stream);
+int r2s_rasterize_bwd_rows_packed_f64(const double *payload, const int32_t *tile_offsets,
+                                      const int64_t *isect_ids, const int32_t *flatten_ids,
+                                      const int32_t *isect_src, int64_t n_isects,
+                                      const double *v_image, int64_t C, int64_t N,
+                                      uint32_t width, uint32_t height, uint32_t tile_size,
+                                      uint32_t n_tiles_w, uint32_t n_tiles_h, int absgrad,
+                                      void *rows, size_t rows_bytes, r2s_stream_t stream);
+
 /* ---------------------------------------------------------------------- */
 /* Volume mapping and voxelizer                                           */
 /* ---------------------------------------------------------------------- */

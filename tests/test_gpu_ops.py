@@ -588,6 +588,59 @@ def test_rasterize_empty():
     assert all(float(t.abs().sum()) == 0.0 for t in g)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("shape,log_mu", [((64, 64, 16), -4.0), ((70, 45, 16), -4.0),
+                                          ((40, 40, 8), -4.0), ((96, 72, 32), -4.0),
+                                          ((32, 32, 16), -2.0)])
+def test_packed_rasterizer_equals_the_array_form(dtype, shape, log_mu):
+    """The packed payload's forward and two-pass backward (r2splat.ops' path)
+    against the four-array forward and the two-pass backward with its own
+    pack: bit for bit, absgrad on and off, with the outputs zeroed by the
+    pack launch and without; heavy tiles (log_mu -2) take the split
+    forward."""
+    W_img, H_img, ts = shape
+    d, m2, con, mu, op, ids, fl, off = _raster_case(3000, 17, W_img, H_img, ts, 2, dtype,
+                                                    log_mu=log_mu)
+    C, N = m2.shape[:2]
+    lists = _ops.TileLists(None, ids, fl, *_ops.emission_order(fl, fl_keys(off)))
+    want_img = W.rasterize_to_pixels_fwd(m2, con, op, mu, off, fl, W_img, H_img, ts)
+    v = torch.randn(want_img.shape, generator=d["gen"], dtype=dtype).to(DEV)
+    for absgrad in (True, False):
+        payload, zeroed = _ops.raster_pack(m2, con, op, mu, zero_outputs=True, absgrad=absgrad)
+        assert payload.numel() == C * N * 8 and (zeroed[0] is None) == (not absgrad)
+        assert all(t is None or not t.any() for t in zeroed)
+        img = _ops.rasterize_packed(payload, off, fl, C, N, W_img, H_img, ts)
+        assert torch.equal(img, want_img)
+        want = _ops.raster_backward(m2, con, op, mu, off, lists, v, W_img, H_img, ts, absgrad)
+        in_place = _ops.raster_backward_packed(payload, op, mu, off, lists, v, W_img, H_img, ts,
+                                               absgrad, zeroed)
+        assert in_place[1].data_ptr() == zeroed[1].data_ptr()  # the zeroed outputs, filled
+        fresh = _ops.raster_backward_packed(payload, op, mu, off, lists, v, W_img, H_img, ts,
+                                            absgrad)
+        for got in (in_place, fresh):
+            for a, b in zip(got, want):
+                assert (a is None and b is None) or torch.equal(a, b)
+
+
+def test_packed_rasterizer_rejects_other_tile_sizes_and_empty_lists():
+    d, m2, con, mu, op, ids, fl, off = _raster_case(500, 3, 50, 38, 12, 1, torch.float32)
+    payload, _ = _ops.raster_pack(m2, con, op, mu)
+    with pytest.raises(RuntimeError, match="tile sizes 8, 16 and 32"):
+        _ops.rasterize_packed(payload, off, fl, 1, m2.shape[1], 50, 38, 12)
+    empty = torch.zeros(0, dtype=torch.int32, device=DEV)
+    off16 = torch.zeros(1, 3, 4, dtype=torch.int32, device=DEV)
+    img = _ops.rasterize_packed(payload, off16, empty, 1, m2.shape[1], 50, 38, 16)
+    assert img.shape == (1, 38, 50) and not img.any()
+    lists = _ops.TileLists(None, torch.zeros(0, dtype=torch.int64, device=DEV), empty, None, None)
+    _, zeroed = _ops.raster_pack(m2, con, op, mu, zero_outputs=True, absgrad=True)
+    got = _ops.raster_backward_packed(payload, op, mu, off16, lists,
+                                      torch.ones(1, 38, 50, device=DEV), 50, 38, 16, True, zeroed)
+    assert all(not t.any() for t in got)
+    got = _ops.raster_backward_packed(payload, op, mu, off16, lists,
+                                      torch.ones(1, 38, 50, device=DEV), 50, 38, 16, True)
+    assert all(not t.any() for t in got)
+
+
 def _voxel_case(n, seed, dims, ts, dtype=torch.float32, log_mu=-3.2):
     d = _prepared(n, seed, dtype, log_mu=log_mu)
     ranges = torch.full((3,), 2.0, dtype=dtype, device=DEV)
