@@ -685,7 +685,8 @@ __global__ __launch_bounds__(kBwdThreads) void voxel_bwd_kernel(
 // appears at most once per chunk index, and the chunk sums are added to the
 // record's LDS accumulators one chunk index at a time in increasing order,
 // so the result does not depend on scheduling.  Every brick must lie inside
-// the volume with 16-byte gradient rows (the caller checks).
+// the volume with 16-byte gradient rows, and a slice must hold fewer than
+// 2^24 voxels (the caller checks).
 
 constexpr int kChunkRows = 8;
 constexpr int kChunkWaves = 4;
@@ -846,6 +847,11 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
     }
     const int n_here = act ? min(R, cr.n_items - static_cast<int>(q) * R) : 0;
     const T cdx0 = (static_cast<T>(cr.ok) + half) - cr.m[0];
+    // The brick's first voxel; a row's offset adds li plane + lj D2 with
+    // li, lj < 8 and plane < 2^24 (the caller checks), so two full-rate
+    // 24-bit multiply-adds per row instead of 32-bit multiplies.
+    const uint32_t brick0 = static_cast<uint32_t>(cr.oi) * plane +
+                            static_cast<uint32_t>(cr.oj) * D2 + static_cast<uint32_t>(cr.ok);
     T dxk[R], wk[R];
 #pragma unroll
     for (int k = 0; k < R; ++k) {
@@ -856,17 +862,16 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
 #pragma unroll 1
     for (int st = 0; st < R; ++st) {
       const bool item = st < n_here;
-      const int i = cr.oi + ((pos >> 3) & 7);
-      const int j = cr.oj + (pos & 7);
+      const uint32_t li = static_cast<uint32_t>(pos >> 3) & 7u, lj = static_cast<uint32_t>(pos) & 7u;
+      const int i = cr.oi + static_cast<int>(li);
+      const int j = cr.oj + static_cast<int>(lj);
       const T dz = (static_cast<T>(i) + half) - cr.m[2];
       const T dy = (static_cast<T>(j) + half) - cr.m[1];
       const T B = fma(cr.h[1], dy, cr.h[2] * dz);
       const T C = fma(fma(cr.h[3], dy, cr.h[4] * dz), dy, cr.h[5] * dz * dz);
       const typename Bits<T>::type lim = item ? cr.lim : 0;
       // 32-bit offsets; a step without an item reads the volume's first row.
-      const uint32_t off = item ? static_cast<uint32_t>(i) * plane +
-                                      static_cast<uint32_t>(j) * D2 + static_cast<uint32_t>(cr.ok)
-                                : 0u;
+      const uint32_t off = item ? brick0 + __umul24(li, plane) + __umul24(lj, D2) : 0u;
       const T *__restrict__ vrow = v_vol + off;
       T vv[R];
 #pragma unroll
@@ -1119,7 +1124,7 @@ int voxel_bwd_impl(const T *means3d, const T *conics, const T *opac,
                                  isect_src, n_isects, n_keys, koff, N, v_vol, D2, D1, D0, ts,  \
                                  n2, n1, vec, v_means, v_conics, v_opac, rows, stream)
   if (ts == 8 && rows != nullptr && vec && D2 % 8 == 0 && D1 % 8 == 0 && D0 % 8 == 0 &&
-      n_vox < (int64_t{1} << 31)) {
+      n_vox < (int64_t{1} << 31) && static_cast<int64_t>(D1) * D2 < (int64_t{1} << 24)) {
     const dim3 grid(static_cast<uint32_t>(ceil_div(n_isects, 64 * kChunkWaves)));
     if (reach != nullptr)
       voxel_bwd_chunk_kernel<T, true><<<grid, dim3(64 * kChunkWaves), 0, stream>>>(

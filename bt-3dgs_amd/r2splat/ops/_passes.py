@@ -130,15 +130,19 @@ class ImagePass:
             means.contiguous(), covars.contiguous(), opacities.contiguous(), viewmats, Ks,
             width, height, float(eps2d), float(radius_clip))
         across, down = _tiles_along(width, ts), _tiles_along(height, ts)
+        # The payload depends on the projection only: packed before the
+        # binning, whose record count the host waits for, so that the launch
+        # is queued while the device bins.
+        payload = zeroed = None
+        if ts in ops.PACKED_TILE_SIZES:
+            payload, zeroed = ops.raster_pack(means2d, conics, weights, mus,
+                                              zero_outputs=for_backward, absgrad=absgrad)
         lists = ops.bin_tiles_2d(means2d, radii, ts, across, down)
         tile_offsets = lists.tile_offsets
         if tile_offsets is None:  # no records
             tile_offsets = ops.isect_offset_encode(lists.isect_ids, int(viewmats.shape[0]),
                                                    across, down)
-        payload = zeroed = None
-        if ts in ops.PACKED_TILE_SIZES and lists.flatten_ids.numel() > 0:
-            payload, zeroed = ops.raster_pack(means2d, conics, weights, mus,
-                                              zero_outputs=for_backward, absgrad=absgrad)
+        if payload is not None and lists.flatten_ids.numel() > 0:
             image = ops.rasterize_packed(payload, tile_offsets, lists.flatten_ids,
                                          means2d.shape[0], means2d.shape[1], width, height, ts)
         else:

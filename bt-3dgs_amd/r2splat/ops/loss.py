@@ -14,7 +14,10 @@ Drop-in for the projection and volume terms of ``src/utils/loss.py`` and for
   parent, measures it in the parent's scaled frame and stores its gradient
   in one launch; the backward scales it.
 * ``LossComputer`` / ``BinaryTreeLossComputer`` keep the reference's
-  constructor arguments and output dictionary (loss.py:74-172).
+  constructor arguments and output dictionary (loss.py:74-172); their
+  projection terms, TV term and weighted total are the outputs of one
+  autograd node (``_TrainerLoss``), so the trainer's ``total.backward()``
+  walks one node for them instead of one per term and sum.
 
 Images and volumes are float32 CUDA tensors, as the trainer produces them;
 gradients flow to the renders / volume only (targets, masks and edge
@@ -58,6 +61,7 @@ class _ProjectionLoss(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, render, target, edge_target, edge_mask, window_size):
+        ctx.set_materialize_grads(False)  # unused outputs' gradients stay None
         losses, ws = W.projection_loss_fwd(render, target, edge_target, edge_mask, window_size)
         ctx.save_for_backward(render, target, edge_target, edge_mask, ws)
         ctx.window_size = window_size
@@ -78,33 +82,91 @@ class _ProjectionLoss(torch.autograd.Function):
 _WEIGHTS = {}
 
 
-class _WeightedTotal(torch.autograd.Function):
-    """sum_i w_i t_i over scalar terms in two launches; the backward hands
-    each term w_i g from one launch (the weighted sums of loss.py:90-101 and
-    166-171, without a graph node per product and sum)."""
+class _TrainerLoss(torch.autograd.Function):
+    """The loss computers' terms and weighted total as outputs of one graph
+    node: forward = the projection-loss launch, the TV launch and one
+    weighted sum; backward = the effective scale of each term (its own
+    upstream gradient plus its weight times the total's), then one
+    projection-loss launch and one TV launch.  Terms are ordered (l1, ssim,
+    edge, tv, hierarchy); the hierarchy term is an input (computed by the
+    caller), so its gradient is passed back."""
 
     @staticmethod
-    def forward(ctx, weights, *terms):
-        ctx.save_for_backward(weights)
-        ctx.dtypes = [t.dtype for t in terms]
-        return torch.dot(_grad_vector(terms, weights.device), weights)
+    def forward(ctx, weights, r, t, e, m, vol, hier, window_size, tv_mean):
+        # Outputs that receive no gradient (the terms, in a trainer's
+        # total.backward()) pass None instead of a zero tensor each.
+        ctx.set_materialize_grads(False)
+        losses, ws = W.projection_loss_fwd(r, t, e, m, window_size)
+        z = _zero(r.device).reshape(1)
+        tv = z if vol is None else W.tv_fwd(vol, tv_mean).reshape(1)
+        terms = torch.cat((losses, tv, hier.detach().reshape(1).to(torch.float32)))
+        total = torch.dot(terms, weights)
+        ctx.save_for_backward(weights, r, t, e, m, ws, vol)
+        ctx.window_size, ctx.tv_mean = window_size, tv_mean
+        ctx.hier_dtype, ctx.hier_shape = hier.dtype, hier.shape
+        return terms[0], terms[1], terms[2], terms[3], total
 
     @staticmethod
-    def backward(ctx, grad):
-        (weights,) = ctx.saved_tensors
-        parts = (weights * grad.to(torch.float32)).unbind(0)
-        return (None,) + tuple(p.to(dt) for p, dt in zip(parts, ctx.dtypes))
+    def backward(ctx, g_l1, g_ssim, g_edge, g_tv, g_total):
+        if any(ctx.needs_input_grad[2:5]):
+            raise NotImplementedError("gradients w.r.t. targets, edge targets or edge masks "
+                                      "are not provided")
+        weights, r, t, e, m, ws, vol = ctx.saved_tensors
+        dev = weights.device
+        if g_total is None:
+            g_total = _zero(dev)
+        if g_l1 is None and g_ssim is None and g_edge is None and g_tv is None:
+            eff = weights * g_total.to(torch.float32)
+        else:
+            own = _grad_vector((g_l1, g_ssim, g_edge, g_tv, None), dev)
+            eff = torch.addcmul(own, weights, g_total.to(torch.float32))
+        v_r = None
+        if ctx.needs_input_grad[1]:
+            v_r = W.projection_loss_bwd(r, t, e, m, eff[:3], ws, ctx.window_size)
+        v_vol = None
+        if vol is not None and ctx.needs_input_grad[5]:
+            v_vol = W.tv_bwd(vol, eff[3:4], ctx.tv_mean)
+        v_hier = None
+        if ctx.needs_input_grad[6]:
+            v_hier = eff[4].reshape(ctx.hier_shape).to(ctx.hier_dtype)
+        return None, v_r, None, None, None, v_vol, v_hier, None, None
 
 
-def _weighted_total(pairs, device) -> Tensor:
-    """Weighted sum of (weight, scalar term) pairs, in one graph node."""
-    key = (device, tuple(float(w) for w, _ in pairs))
+def _trainer_terms(renders, targets, edge_mask, edge_targets, volume_pred, hierarchy_loss,
+                   weights, ssim_window, w_tv):
+    """(l1, ssim, edge, tv, total) of the loss computers through _TrainerLoss;
+    weights = (l1, ssim, edge, tv, hierarchy)."""
+    if renders.shape != targets.shape:
+        raise AssertionError("Input shapes must match for SSIM")
+    if renders.dtype != torch.float32:
+        raise TypeError(f"renders must be float32, got {renders.dtype}")
+    dev = renders.device
+    r = _planes(renders)
+    t = _planes(_as_float(targets.detach()))
+    e = m = None
+    if edge_mask is not None:
+        et = targets if edge_targets is None else edge_targets
+        if torch.broadcast_shapes(edge_mask.shape, et.shape, renders.shape) != renders.shape:
+            raise ValueError("edge_mask and edge_targets must broadcast to the renders' shape")
+        e = _planes(_as_float(et.detach()).expand(renders.shape))
+        m = _planes(_as_float(edge_mask.detach()).expand(renders.shape))
+    vol = None
+    if w_tv > 0 and volume_pred is not None:
+        # loss.py:93-99 / 159-165: a volume that is not 3-D after squeezing gives 0.
+        v = volume_pred.squeeze()
+        if v.dim() == 4 and v.size(0) == 1:
+            v = v[0]
+        if v.dim() == 3 and v.is_cuda and v.dtype == torch.float32:
+            vol = v.contiguous()
+    if hierarchy_loss is None:
+        hierarchy_loss = _zero(dev)
+    elif not isinstance(hierarchy_loss, Tensor):  # a plain number
+        hierarchy_loss = torch.tensor(float(hierarchy_loss), dtype=torch.float32, device=dev)
+    key = (dev, weights)
     w = _WEIGHTS.get(key)
     if w is None:
-        w = _WEIGHTS[key] = torch.tensor(key[1], dtype=torch.float32, device=device)
-    terms = [t if isinstance(t, Tensor) else torch.as_tensor(t, dtype=torch.float32,
-                                                             device=device) for _, t in pairs]
-    return _WeightedTotal.apply(w, *terms)
+        w = _WEIGHTS[key] = torch.tensor(weights, dtype=torch.float32, device=dev)
+    return _TrainerLoss.apply(w, r, t, e, m, vol, hierarchy_loss, int(ssim_window), True)
 
 
 def _planes(t: Tensor) -> Tensor:
@@ -227,14 +289,10 @@ class LossComputer:
 
     def __call__(self, renders: Tensor, targets: Tensor,
                  volume_pred: Optional[Tensor] = None) -> Dict[str, Tensor]:
-        out: Dict[str, Tensor] = {}
-        l1, ssim_loss, _ = projection_losses(renders, targets, ssim_window=self.ssim_window)
-        out["proj_l1"] = l1
-        out["proj_ssim"] = ssim_loss
-        out["vol_tv"] = _tv_term(self.w_tv, volume_pred, renders.device)
-        out["total"] = _weighted_total(((self.w_l1, l1), (self.w_ssim, ssim_loss),
-                                        (self.w_tv, out["vol_tv"])), renders.device)
-        return out
+        weights = (float(self.w_l1), float(self.w_ssim), 0.0, float(self.w_tv), 0.0)
+        l1, ssim_loss, _, tv, total = _trainer_terms(renders, targets, None, None, volume_pred,
+                                                     None, weights, self.ssim_window, self.w_tv)
+        return {"proj_l1": l1, "proj_ssim": ssim_loss, "vol_tv": tv, "total": total}
 
 
 class BinaryTreeLossComputer:
@@ -255,31 +313,17 @@ class BinaryTreeLossComputer:
                  hierarchy_loss: Optional[Tensor] = None,
                  edge_targets: Optional[Tensor] = None,
                  edge_weight_override: Optional[float] = None) -> Dict[str, Tensor]:
-        out: Dict[str, Tensor] = {}
         if edge_targets is None:
             edge_targets = targets
-        l1, ssim_loss, edge_loss = projection_losses(renders, targets, edge_mask, edge_targets,
-                                                     self.ssim_window)
-        out["proj_l1"] = l1
-        out["proj_ssim"] = ssim_loss
-        out["vol_tv"] = _tv_term(self.w_tv, volume_pred, renders.device)
-        out["edge"] = edge_loss
         if hierarchy_loss is None:
             hierarchy_loss = torch.zeros((), device=renders.device)
-        out["hierarchy"] = hierarchy_loss
         edge_weight = self.w_edge if edge_weight_override is None else float(edge_weight_override)
-        out["edge_weight"] = torch.full((), edge_weight, device=renders.device)
-        out["total"] = _weighted_total(((self.w_l1, l1), (self.w_ssim, ssim_loss),
-                                        (self.w_tv, out["vol_tv"]), (edge_weight, edge_loss),
-                                        (self.w_hierarchy, hierarchy_loss)), renders.device)
-        return out
-
-
-def _tv_term(w_tv: float, volume_pred: Optional[Tensor], device) -> Tensor:
-    # loss.py:93-99 / 159-165: a volume that is not 3-D after squeezing gives 0.
-    if w_tv > 0 and volume_pred is not None:
-        try:
-            return compute_tv_loss(volume_pred.squeeze(), reduction="mean")
-        except Exception:
-            return torch.zeros((), device=device)
-    return torch.zeros((), device=device)
+        weights = (float(self.w_l1), float(self.w_ssim), float(edge_weight), float(self.w_tv),
+                   float(self.w_hierarchy))
+        l1, ssim_loss, edge_loss, tv, total = _trainer_terms(
+            renders, targets, edge_mask, edge_targets, volume_pred, hierarchy_loss, weights,
+            self.ssim_window, self.w_tv)
+        return {"proj_l1": l1, "proj_ssim": ssim_loss, "vol_tv": tv, "edge": edge_loss,
+                "hierarchy": hierarchy_loss,
+                "edge_weight": torch.full((), edge_weight, device=renders.device),
+                "total": total}
