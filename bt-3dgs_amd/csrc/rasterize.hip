@@ -238,6 +238,7 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
           p.w = l * a.w;
           q.x = hl * b.x;
           q.y = b.y;
+          q.z = b.z;  // alpha_limit(o mu, finite unscaled geometry)
         } else {
           const V2 xy = *reinterpret_cast<const V2 *>(means2d + 2 * g);
           p.x = xy.x;
@@ -248,9 +249,15 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
           q.y = opac[g] * mus[g];
         }
         // The alpha test's limit on the bits of sl (alpha_limit), kept in q.z.
+        // Packed: finite scaled geometry implies finite unscaled geometry, so
+        // the payload's limit is alpha_limit's value, and non-finite scaled
+        // geometry gives the sign-bit limit either way (no log2 here).
         const bool fin = isfinite(p.x) && isfinite(p.y) && isfinite(p.z) && isfinite(p.w) &&
                          isfinite(q.x);
-        q.z = limit_as_value(alpha_limit(q.y, fin, kThr2));
+        if (kPacked)
+          q.z = fin ? q.z : limit_as_value(Bits<T>::kSign);
+        else
+          q.z = limit_as_value(alpha_limit(q.y, fin, kThr2));
       } else {  // never passes
         p.x = p.y = p.z = p.w = 0;
         q.x = q.y = 0;

@@ -604,6 +604,19 @@ def test_packed_rasterizer_equals_the_array_form(dtype, shape, log_mu):
     C, N = m2.shape[:2]
     lists = _ops.TileLists(None, ids, fl, *_ops.emission_order(fl, fl_keys(off)))
     want_img = W.rasterize_to_pixels_fwd(m2, con, op, mu, off, fl, W_img, H_img, ts)
+    # Non-finite records (a NaN opacity, infinite and huge conic entries) take
+    # the alpha limit's non-finite branch in both forms.
+    listed = torch.unique(fl.long())
+    g0, g1, g2 = (int(listed[k]) for k in (3, len(listed) // 2, -4))
+    bad_op, bad_con = op.clone(), con.clone()
+    bad_op.view(-1)[g0] = float("nan")
+    bad_con.view(-1, 3)[g1, 1] = float("inf")
+    bad_con.view(-1, 3)[g2, 1] = torch.finfo(dtype).max  # finite; log2(e) times it is not
+    bad_want = W.rasterize_to_pixels_fwd(m2, bad_con, bad_op, mu, off, fl, W_img, H_img, ts)
+    bad_payload, _ = _ops.raster_pack(m2, bad_con, bad_op, mu)
+    bad_img = _ops.rasterize_packed(bad_payload, off, fl, C, N, W_img, H_img, ts)
+    assert bad_img.isnan().any() and torch.equal(bad_img.isnan(), bad_want.isnan())
+    assert torch.equal(bad_img.nan_to_num(0.0), bad_want.nan_to_num(0.0))
     v = torch.randn(want_img.shape, generator=d["gen"], dtype=dtype).to(DEV)
     for absgrad in (True, False):
         payload, zeroed = _ops.raster_pack(m2, con, op, mu, zero_outputs=True, absgrad=absgrad)
