@@ -352,10 +352,11 @@ __global__ __launch_bounds__(64 * S) void voxel_fwd_reach_kernel(
     uint64_t *__restrict__ reach_out) {
   constexpr int R = 8;
   using V4 = typename Vec<T>::v4;
-  // Per staged record {mx, my, mz, o}, {h0, h1, h2, h3}, {h4, h5, limit bits,
-  // 0}: three vector reads per use; the 12-word stride spreads 8
-  // consecutive records over all banks.
-  __shared__ V4 s_rec[S][64][3];
+  // Per staged record {my, mz, o, h0}, {h1, h2, h3, h4}, {h5, limit bits,
+  // 0, 0} and its eight column offsets dx_k = (x_k + 1/2) - mx, the same for
+  // every row of the brick: five vector reads per use; the 20-word stride
+  // spreads 8 consecutive records over all banks.
+  __shared__ V4 s_rec[S][64][5];
   __shared__ T s_part[S > 1 ? S - 1 : 1][R][64];
   const uint32_t key = xcd_swizzle(blockIdx.x, n_keys);  // in the lists (koff: the grid's)
   const Brick b = brick_of(key + koff, n2, n1, R, D2, D1, D0);
@@ -368,15 +369,9 @@ __global__ __launch_bounds__(64 * S) void voxel_fwd_reach_kernel(
   const T px0 = static_cast<T>(b.ok) + half;
   const int64_t start = tile_offsets[key];
   const int64_t end = (key == n_keys - 1) ? n_isects : static_cast<int64_t>(tile_offsets[key + 1]);
-  T acc[R], px[R];
+  T acc[R];
 #pragma unroll
-  for (int k = 0; k < R; ++k) {
-    acc[k] = 0;
-    // The voxel centres stay in registers (opaque to the compiler, which
-    // would otherwise recompute some of them at every walked record).
-    px[k] = px0 + static_cast<T>(k);
-    asm volatile("" : "+v"(px[k]));
-  }
+  for (int k = 0; k < R; ++k) acc[k] = 0;
   for (int64_t base = start + 64 * w; base < end; base += 64 * S) {
     const int64_t idx = base + lane;
     const bool in = idx < end;
@@ -385,19 +380,32 @@ __global__ __launch_bounds__(64 * S) void voxel_fwd_reach_kernel(
     load_bwd_record(means3d, conics, opac, g, N, in, b, rec);
     const uint64_t reach = rec.live ? reach_mask(rec, b, px0 - rec.m[0]) : 0ull;
     if (reach_out != nullptr && in) reach_out[idx] = reach;
-    V4 a, hq, hr;
-    a.x = rec.m[0];
-    a.y = rec.m[1];
-    a.z = rec.m[2];
-    a.w = rec.o;
-    hq.x = rec.h[0];
-    hq.y = rec.h[1];
-    hq.z = rec.h[2];
-    hq.w = rec.h[3];
-    hr.x = rec.h[4];
-    hr.y = rec.h[5];
-    hr.z = limit_as_value(rec.lim);
+    V4 a, hq, hr, d0, d1;
+    a.x = rec.m[1];
+    a.y = rec.m[2];
+    a.z = rec.o;
+    a.w = rec.h[0];
+    hq.x = rec.h[1];
+    hq.y = rec.h[2];
+    hq.z = rec.h[3];
+    hq.w = rec.h[4];
+    hr.x = rec.h[5];
+    hr.y = limit_as_value(rec.lim);
+    hr.z = 0;
     hr.w = 0;
+    // The column offsets from the voxel centres x_k + 1/2 = px0 + k (exact),
+    // computed once per record instead of once per walked row.
+    T dxs[R];
+#pragma unroll
+    for (int k = 0; k < R; ++k) dxs[k] = (px0 + static_cast<T>(k)) - rec.m[0];
+    d0.x = dxs[0];
+    d0.y = dxs[1];
+    d0.z = dxs[2];
+    d0.w = dxs[3];
+    d1.x = dxs[4];
+    d1.y = dxs[5];
+    d1.z = dxs[6];
+    d1.w = dxs[7];
     // The wave's LDS operations complete in order: the fences keep the
     // compiler from moving this batch's writes above the previous batch's
     // reads, or the reads below above the writes.
@@ -407,30 +415,29 @@ __global__ __launch_bounds__(64 * S) void voxel_fwd_reach_kernel(
     s_rec[w][lane][0] = a;
     s_rec[w][lane][1] = hq;
     s_rec[w][lane][2] = hr;
+    s_rec[w][lane][3] = d0;
+    s_rec[w][lane][4] = d1;
     // Bit t of lane r's set: batch record t reaches row r.
-    const uint64_t mine = transpose_bits64(reach, static_cast<uint32_t>(lane));
-    uint32_t mine_lo = static_cast<uint32_t>(mine), mine_hi = static_cast<uint32_t>(mine >> 32);
+    uint64_t mine = transpose_bits64(reach, static_cast<uint32_t>(lane));
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    while ((mine_lo | mine_hi) != 0u) {
-      const bool low = mine_lo != 0u;
-      const uint32_t word = low ? mine_lo : mine_hi;
-      const int t = static_cast<int>(__builtin_ctz(word)) + (low ? 0 : 32);
-      const uint32_t rest = word & (word - 1u);
-      mine_lo = low ? rest : mine_lo;
-      mine_hi = low ? mine_hi : rest;
+    while (mine != 0ull) {
+      const int t = static_cast<int>(__builtin_ctzll(mine));
+      mine &= mine - 1ull;
       const V4 qa = s_rec[w][t][0], qh = s_rec[w][t][1], qr = s_rec[w][t][2];
-      const typename Bits<T>::type lim = bits_of(qr.z);
-      const T dy = py - qa.y, dz = pz - qa.z;
-      const T B = qh.y * dy + qh.z * dz;
-      const T C = (qh.w * dy + qr.x * dz) * dy + qr.y * dz * dz;
+      const V4 q0 = s_rec[w][t][3], q1 = s_rec[w][t][4];
+      const T dxs[R] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+      const typename Bits<T>::type lim = bits_of(qr.y);
+      const T dy = py - qa.x, dz = pz - qa.y;
+      const T B = qh.x * dy + qh.y * dz;
+      const T C = (qh.z * dy + qh.w * dz) * dy + qr.x * dz * dz;
 #pragma unroll
       for (int k = 0; k < R; ++k) {
-        const T dx = px[k] - qa.x;
-        const T sl = (qh.x * dx + B) * dx + C;
+        const T dx = dxs[k];
+        const T sl = (qa.w * dx + B) * dx + C;
         const T e = neg_exp2(sl);
-        acc[k] = fma(qa.w, alpha_pass(sl, lim) ? e : static_cast<T>(0), acc[k]);
+        acc[k] = fma(qa.z, alpha_pass(sl, lim) ? e : static_cast<T>(0), acc[k]);
       }
     }
   }
@@ -685,8 +692,8 @@ __global__ __launch_bounds__(kBwdThreads) void voxel_bwd_kernel(
 // appears at most once per chunk index, and the chunk sums are added to the
 // record's LDS accumulators one chunk index at a time in increasing order,
 // so the result does not depend on scheduling.  Every brick must lie inside
-// the volume with 16-byte gradient rows, and a slice must hold fewer than
-// 2^24 voxels (the caller checks).
+// the volume with 16-byte gradient rows, the gradient volume must span at
+// most 2^32 bytes and a slice fewer than 2^24 (the caller checks).
 
 constexpr int kChunkRows = 8;
 constexpr int kChunkWaves = 4;
@@ -698,9 +705,11 @@ constexpr int kDenseItems = 3072;
 
 template <typename T>
 struct ChunkRecord {
-  T m[3], h[6];
+  T c[3];  // the brick's first voxel centre minus the mean (x, y, z)
+  T h[6];
   typename Bits<T>::type lim;  // 0 for dead records
-  int ok, oj, oi, n_items;
+  uint32_t brick0;             // byte offset of the brick's first voxel in v_vol
+  int n_items;
 };
 
 // kGiven: each record's reach mask comes from `reach` (stored by the forward
@@ -746,7 +755,9 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
   else
     load_bwd_record(means3d, conics, opac, g, N, key_ok, b, rec);
   const T half = static_cast<T>(0.5);
-  const uint32_t plane = D1 * D2;  // the caller checks D2 D1 D0 < 2^31
+  const uint32_t plane = D1 * D2;  // the caller checks D2 D1 D0 sizeof(T) <= 2^32
+  const uint32_t plane_b = plane * static_cast<uint32_t>(sizeof(T)),
+                 row_b = D2 * static_cast<uint32_t>(sizeof(T));
   const T dx0 = (static_cast<T>(b.ok) + half) - rec.m[0];
 
   // The record's reached rows; the items are its set bits in increasing order.
@@ -779,14 +790,15 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
   }
   {
     ChunkRecord<T> cr;
-#pragma unroll
-    for (int c = 0; c < 3; ++c) cr.m[c] = rec.m[c];
+    cr.c[0] = dx0;
+    cr.c[1] = (static_cast<T>(b.oj) + half) - rec.m[1];
+    cr.c[2] = (static_cast<T>(b.oi) + half) - rec.m[2];
 #pragma unroll
     for (int c = 0; c < 6; ++c) cr.h[c] = rec.h[c];
     cr.lim = rec.live ? rec.lim : 0;
-    cr.ok = b.ok;
-    cr.oj = b.oj;
-    cr.oi = b.oi;
+    // Below 2^32: the caller checks D2 D1 D0 sizeof(T) <= 2^32.
+    cr.brick0 = (static_cast<uint32_t>(b.oi) * plane + static_cast<uint32_t>(b.oj) * D2 +
+                 static_cast<uint32_t>(b.ok)) * static_cast<uint32_t>(sizeof(T));
     cr.n_items = n_items;
     s_rec[w].store(static_cast<int>(lane), cr);
     s_rows[w][lane] = reached;
@@ -846,33 +858,39 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
                      static_cast<int>(t - before);
     }
     const int n_here = act ? min(R, cr.n_items - static_cast<int>(q) * R) : 0;
-    const T cdx0 = (static_cast<T>(cr.ok) + half) - cr.m[0];
-    // The brick's first voxel; a row's offset adds li plane + lj D2 with
-    // li, lj < 8 and plane < 2^24 (the caller checks), so two full-rate
-    // 24-bit multiply-adds per row instead of 32-bit multiplies.
-    const uint32_t brick0 = static_cast<uint32_t>(cr.oi) * plane +
-                            static_cast<uint32_t>(cr.oj) * D2 + static_cast<uint32_t>(cr.ok);
+    // The record's rows from the chunk's first on: the chunk's items are
+    // its n_here lowest set bits.
+    uint64_t rest = act ? rows_m & (~0ull << pos) : 0ull;
     T dxk[R], wk[R];
 #pragma unroll
     for (int k = 0; k < R; ++k) {
-      dxk[k] = cdx0 + static_cast<T>(k);
+      dxk[k] = cr.c[0] + static_cast<T>(k);
       wk[k] = 0;
     }
     T Y0 = 0, Z0 = 0, Y1 = 0, Z1 = 0, YY = 0, YZ = 0, ZZ = 0;
 #pragma unroll 1
     for (int st = 0; st < R; ++st) {
       const bool item = st < n_here;
-      const uint32_t li = static_cast<uint32_t>(pos >> 3) & 7u, lj = static_cast<uint32_t>(pos) & 7u;
-      const int i = cr.oi + static_cast<int>(li);
-      const int j = cr.oj + static_cast<int>(lj);
-      const T dz = (static_cast<T>(i) + half) - cr.m[2];
-      const T dy = (static_cast<T>(j) + half) - cr.m[1];
+      // The next row (bit 63 when none is left: a step without an item
+      // still reads a row of the record's own brick, which lies inside the
+      // volume, and tests against a zero limit).
+      const uint32_t p = static_cast<uint32_t>(__builtin_ctzll(rest | (1ull << 63)));
+      rest &= rest - 1ull;
+      const uint32_t li = p >> 3, lj = p & 7u;
+      // The row centre's offsets from the mean as the columns' (dxk): the
+      // brick corner's offset plus the row's index in the brick.
+      const T dz = static_cast<T>(li) + cr.c[2];
+      const T dy = static_cast<T>(lj) + cr.c[1];
       const T B = fma(cr.h[1], dy, cr.h[2] * dz);
       const T C = fma(fma(cr.h[3], dy, cr.h[4] * dz), dy, cr.h[5] * dz * dz);
       const typename Bits<T>::type lim = item ? cr.lim : 0;
-      // 32-bit offsets; a step without an item reads the volume's first row.
-      const uint32_t off = item ? brick0 + __umul24(li, plane) + __umul24(lj, D2) : 0u;
-      const T *__restrict__ vrow = v_vol + off;
+      // 32-bit byte offsets: li, lj < 8 and plane_b = D1 D2 sizeof(T) < 2^24
+      // (the caller checks), so two full-rate 24-bit multiply-adds per row.
+      uint32_t off = __umul24(lj, row_b) + cr.brick0;
+      asm volatile("" : "+v"(off));  // two multiply-adds, not two products and a sum
+      off += __umul24(li, plane_b);
+      const T *__restrict__ vrow =
+          reinterpret_cast<const T *>(reinterpret_cast<const char *>(v_vol) + off);
       T vv[R];
 #pragma unroll
       for (int c = 0; c < R / kq; ++c)
@@ -898,9 +916,6 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
       ZZ = fma(dz, dzs0, ZZ);
       Y1 = fma(dy, s1, Y1);
       Z1 = fma(dz, s1, Z1);
-      // The next reached row (64 when there is none).
-      const uint64_t rest = pos < 63 ? rows_m >> (pos + 1) : 0ull;
-      pos = rest != 0ull ? pos + 1 + static_cast<int>(__builtin_ctzll(rest)) : 64;
     }
     T t0 = 0, t1 = 0, t2 = 0;
 #pragma unroll
@@ -1123,8 +1138,12 @@ int voxel_bwd_impl(const T *means3d, const T *conics, const T *opac,
   launch_voxel_bwd<T, RR, EXACT>(means3d, conics, opac, tile_offsets, isect_ids, flatten_ids,  \
                                  isect_src, n_isects, n_keys, koff, N, v_vol, D2, D1, D0, ts,  \
                                  n2, n1, vec, v_means, v_conics, v_opac, rows, stream)
+  // The chunked walk addresses the gradient with 32-bit byte offsets and
+  // 24-bit plane and row strides.
+  const int64_t elem = static_cast<int64_t>(sizeof(T));
   if (ts == 8 && rows != nullptr && vec && D2 % 8 == 0 && D1 % 8 == 0 && D0 % 8 == 0 &&
-      n_vox < (int64_t{1} << 31) && static_cast<int64_t>(D1) * D2 < (int64_t{1} << 24)) {
+      n_vox * elem <= (int64_t{1} << 32) &&
+      static_cast<int64_t>(D1) * D2 * elem < (int64_t{1} << 24)) {
     const dim3 grid(static_cast<uint32_t>(ceil_div(n_isects, 64 * kChunkWaves)));
     if (reach != nullptr)
       voxel_bwd_chunk_kernel<T, true><<<grid, dim3(64 * kChunkWaves), 0, stream>>>(
