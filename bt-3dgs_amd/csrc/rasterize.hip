@@ -490,7 +490,8 @@ __device__ __forceinline__ void raster_row(const RasterRecord<T> &rec, const T (
     const T e = neg_exp2(sl);
     bool skip = !alpha_pass(sl, rec.lim);
     if (kGuard) skip = skip || k >= nx;
-    const T w = skip ? static_cast<T>(0) : vv[kk] * e;
+    const T p = vv[kk] * e;  // unconditional, not a branch around the load and exp
+    const T w = skip ? static_cast<T>(0) : p;
     s0 += w;
     const T wx = w * dx;
     s1 += wx;
@@ -548,7 +549,10 @@ __device__ __forceinline__ void raster_tile_full(const RasterRecord<T> &rec,
         const T dx = dxk[h + kk];
         const T sl = fma(fma(rec.ha, dx, B), dx, C);
         const T e = neg_exp2(sl);
-        const T w = alpha_pass(sl, lim) ? vv[kk] * e : static_cast<T>(0);
+        // The product is formed unconditionally: as an operand of the
+        // conditional it would become a branch around its load and exp.
+        const T p = vv[kk] * e;
+        const T w = alpha_pass(sl, lim) ? p : static_cast<T>(0);
         wk[h + kk] += w;
         s0 += w;
         s1 = fma(w, dx, s1);
@@ -813,7 +817,10 @@ __device__ __forceinline__ TileSums<T> raster_tile_signed(const RasterRecord<T> 
         const T dx = dxk[h + kk];
         const T sl = fma(fma(rec.ha, dx, B), dx, C);
         const T e = neg_exp2(sl);
-        const T w = alpha_pass(sl, lim) ? vv[kk] * e : static_cast<T>(0);
+        // The product is formed unconditionally: as an operand of the
+        // conditional it would become a branch around its load and exp.
+        const T p = vv[kk] * e;
+        const T w = alpha_pass(sl, lim) ? p : static_cast<T>(0);
         wk[h + kk] += w;
         s0 += w;
         s1 = fma(w, dx, s1);

@@ -260,7 +260,8 @@ __device__ __forceinline__ void voxel_row(const BwdRecord<T> &rec, const T (&vv)
     const T e = neg_exp2(sl);
     bool skip = !alpha_pass(sl, rec.lim);
     if (kGuard) skip = skip || k >= nk;
-    const T w = skip ? static_cast<T>(0) : vv[k] * e;
+    const T p = vv[k] * e;  // unconditional, not a branch around the load and exp
+    const T w = skip ? static_cast<T>(0) : p;
     s0 += w;
     const T wx = w * dx;
     s1 += wx;
@@ -528,7 +529,8 @@ __device__ __forceinline__ void voxel_brick_full(const BwdRecord<T> &rec, const 
         const T dx = dxk[k];
         const T sl = fma(fma(rec.h[0], dx, B), dx, C);
         const T e = neg_exp2(sl);
-        const T w = alpha_pass(sl, lim) ? vv[k] * e : static_cast<T>(0);
+        const T p = vv[k] * e;  // unconditional, not a branch around the load and exp
+        const T w = alpha_pass(sl, lim) ? p : static_cast<T>(0);
         wk[k] += w;
         s0 += w;
         s1 = fma(w, dx, s1);
@@ -900,10 +902,12 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
       for (int k = 0; k < R; ++k) {
         const T dx = dxk[k];
         const T slv = fma(fma(cr.h[0], dx, B), dx, C);
-        // The select on e (not on the product) keeps every gradient load
-        // unconditional.
-        const T e = alpha_pass(slv, lim) ? neg_exp2(slv) : static_cast<T>(0);
-        const T wv = vv[k] * e;
+        // A failing voxel adds an exact zero whatever its upstream gradient
+        // (a non-finite one included), as when the voxel is skipped.  The
+        // product is formed unconditionally: as an operand of the
+        // conditional it would become a branch around its load and exp.
+        const T p = vv[k] * neg_exp2(slv);
+        const T wv = alpha_pass(slv, lim) ? p : static_cast<T>(0);
         wk[k] += wv;
         s0 += wv;
         s1 = fma(wv, dx, s1);
