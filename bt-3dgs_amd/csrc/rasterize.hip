@@ -177,10 +177,19 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
   constexpr int LPR = TS / R;            // lanes per tile row
   constexpr int NP = kFwdWaves * G;      // records in flight per block
   static_assert(G * NL == 64 && LPR * R == TS, "unsupported tile size");
+  // Tile sizes up to 16: a lane covers a whole tile row, so all lanes use
+  // the same column offsets dx_c = (x_c + 1/2) - mx of a record; they are
+  // staged with it (TS values at a stride of TS + 4, which spreads a round's
+  // records over the banks) instead of formed per lane and record.  The
+  // batch is halved then, which keeps four blocks per CU.
+  constexpr bool kStageDx = TS <= 16;
+  constexpr int kBatch = kStageDx ? kFwdBatch / 2 : kFwdBatch;
+  constexpr int kDxStride = TS + 4;
   // G - 1 records of padding after the batch: the record loop's last round
   // reads up to G - 1 entries past the batch's end.  Entries past the end
   // hold dead records (zero limit, which no pixel passes).
-  __shared__ FwdRecord<T> s_rec[kFwdBatch + G];
+  __shared__ FwdRecord<T> s_rec[kBatch + G];
+  __shared__ __align__(16) T s_dx[kStageDx ? (kBatch + G) * kDxStride : 1];
   __shared__ T s_part[kFwdWaves][TS * TS];
 
   // The splits of one tile are consecutive logical blocks (same XCD).
@@ -209,7 +218,7 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
     // The lane's pixel centres, kept in registers across the record loop
     // (otherwise some are recomputed per record).
     pxk[q] = px0 + static_cast<T>(q);
-    asm volatile("" : "+v"(pxk[q]));
+    if (!kStageDx) asm volatile("" : "+v"(pxk[q]));
   }
   const int wave_first = wave * G;  // uniform: the record loop below is a scalar loop
   const int group = lane / NL;
@@ -218,12 +227,18 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
     dead.p.x = dead.p.y = dead.p.z = dead.p.w = 0;
     dead.q.x = dead.q.y = dead.q.w = 0;
     dead.q.z = limit_as_value(static_cast<typename Bits<T>::type>(0));
-    s_rec[kFwdBatch + tid] = dead;
+    s_rec[kBatch + tid] = dead;
+    if (kStageDx) {
+#pragma unroll
+      for (int c = 0; c < TS; ++c) s_dx[(kBatch + tid) * kDxStride + c] = 0;
+    }
   }
-  for (int64_t base = start; base < end; base += kFwdBatch) {
+  // The tile's first pixel centre; x_c + 1/2 = px_tile + c exactly.
+  const T px_tile = static_cast<T>(static_cast<int>(tx) * TS) + half;
+  for (int64_t base = start; base < end; base += kBatch) {
     __syncthreads();
     const int64_t idx = base + tid;
-    {
+    if (tid < kBatch) {
       const int64_t g = idx < end ? static_cast<int64_t>(flatten_ids[idx]) : -1;
       FwdRecord<T> rec;
       V4 &p = rec.p, &q = rec.q;
@@ -265,13 +280,33 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
       }
       q.w = 0;
       s_rec[tid] = rec;
+      if (kStageDx) {
+        // The walking lanes' px_k - mx (px_k = px_tile + k for every lane),
+        // with the one rounding they would give it.
+#pragma unroll
+        for (int c = 0; c < TS; c += 4) {
+          V4 d;
+          d.x = (px_tile + static_cast<T>(c)) - p.x;
+          d.y = (px_tile + static_cast<T>(c + 1)) - p.x;
+          d.z = (px_tile + static_cast<T>(c + 2)) - p.x;
+          d.w = (px_tile + static_cast<T>(c + 3)) - p.x;
+          *reinterpret_cast<V4 *>(s_dx + tid * kDxStride + c) = d;
+        }
+      }
     }
     __syncthreads();
-    const int cnt = static_cast<int>(min(static_cast<int64_t>(kFwdBatch), end - base));
+    const int cnt = static_cast<int>(min(static_cast<int64_t>(kBatch), end - base));
     for (int jb = wave_first; jb < cnt; jb += NP) {
       // A group past the batch's end reads a dead record.
       const V4 p = s_rec[jb + group].p;
       const V4 q = s_rec[jb + group].q;
+      T dxs[R];
+      if (kStageDx) {
+#pragma unroll
+        for (int c = 0; c < R; c += 4)
+          *reinterpret_cast<V4 *>(dxs + c) =
+              *reinterpret_cast<const V4 *>(s_dx + (jb + group) * kDxStride + c);
+      }
       const typename Bits<T>::type lim = bits_of(q.z);
       const T dy = py - p.y;
       const T B = p.w * dy, C = q.x * dy * dy;
@@ -281,7 +316,7 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
       // footprints far along the row).
 #pragma unroll
       for (int k = 0; k < R; ++k) {
-        const T dx = pxk[k] - p.x;
+        const T dx = kStageDx ? dxs[k] : pxk[k] - p.x;
         const T sl = (p.z * dx + B) * dx + C;
         const T e = neg_exp2(sl);
         acc[k] = fma(q.y, alpha_pass(sl, lim) ? e : static_cast<T>(0), acc[k]);
