@@ -711,8 +711,11 @@ struct ChunkRecord {
   T h[6];
   typename Bits<T>::type lim;  // 0 for dead records
   uint32_t brick0;             // byte offset of the brick's first voxel in v_vol
-  int n_items;
 };
+
+// Chunks of one chunked wave: its records reach at most kDenseItems rows, in
+// chunks of up to kChunkRows, at most one short chunk per record.
+constexpr int kMaxChunks = kDenseItems / kChunkRows + 64;
 
 // kGiven: each record's reach mask comes from `reach` (stored by the forward
 // over the same lists, voxel_fwd_reach_kernel) instead of the culling
@@ -730,10 +733,9 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
   constexpr int kq = Quad<T>::n;
   __shared__ WordMajor<ChunkRecord<T>, 64> s_rec[kChunkWaves];
   __shared__ uint64_t s_rows[kChunkWaves][64];  // reached rows: bit 8 * slice + row
-  // Per record, byte li: the reached rows of the slices before li (0..56).
-  __shared__ uint64_t s_pref[kChunkWaves][64];
   __shared__ T s_acc[kChunkWaves][10][64];
-  __shared__ uint16_t s_chunk[kChunkWaves][64 * R];
+  // Chunk entries: record lane | first row << 6 | chunk index << 12.
+  __shared__ uint16_t s_chunk[kChunkWaves][kMaxChunks];
   const uint32_t w = wave_index(), lane = lane_id();
   const int64_t rb = static_cast<int64_t>(xcd_swizzle(blockIdx.x, gridDim.x)) *
                          (64 * kChunkWaves) + 64 * static_cast<int64_t>(w);
@@ -801,21 +803,22 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
     // Below 2^32: the caller checks D2 D1 D0 sizeof(T) <= 2^32.
     cr.brick0 = (static_cast<uint32_t>(b.oi) * plane + static_cast<uint32_t>(b.oj) * D2 +
                  static_cast<uint32_t>(b.ok)) * static_cast<uint32_t>(sizeof(T));
-    cr.n_items = n_items;
     s_rec[w].store(static_cast<int>(lane), cr);
     s_rows[w][lane] = reached;
-    uint64_t pref = 0;
+#pragma unroll
+    for (int c = 0; c < 10; ++c) s_acc[w][c][lane] = 0;
+  }
+  // Chunk list in (chunk index, record) order.  Byte li of pref: the reached
+  // rows of the slices before li (0..56).
+  uint64_t pref = 0;
+  {
     uint32_t run = 0;
 #pragma unroll
     for (int li = 0; li < R; ++li) {
       pref |= static_cast<uint64_t>(run) << (8 * li);
       run += static_cast<uint32_t>(__popc(static_cast<uint32_t>(reached >> (8 * li)) & 0xFFu));
     }
-    s_pref[w][lane] = pref;
-#pragma unroll
-    for (int c = 0; c < 10; ++c) s_acc[w][c][lane] = 0;
   }
-  // Chunk list in (chunk index, record) order.
   const int n_chunks = (n_items + R - 1) / R;
   uint32_t n_list = 0;
   const uint64_t lt = lanemask_lt();
@@ -823,9 +826,22 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
   for (int q = 0; q < R; ++q) {
     const bool has = n_chunks > q;
     const uint64_t m = ballot(has);
-    if (has)
+    if (has) {
+      // The chunk's first row, the t-th set bit (t = 8 q): its slice li is
+      // the last whose byte of pref is <= t, found for all eight bytes at
+      // once (each byte | 0x80, minus t + 1, keeps its high bit exactly when
+      // the byte exceeds t); within a slice the reached rows are contiguous.
+      const uint32_t t = static_cast<uint32_t>(q) * static_cast<uint32_t>(R);
+      constexpr uint64_t kHigh = 0x8080808080808080ull, kOnes = 0x0101010101010101ull;
+      const uint64_t above = ((pref | kHigh) - static_cast<uint64_t>(t + 1u) * kOnes) & kHigh;
+      const int li = 7 - __popcll(above);
+      const uint32_t byte = static_cast<uint32_t>(reached >> (8 * li)) & 0xFFu;
+      const uint32_t before = static_cast<uint32_t>(pref >> (8 * li)) & 0xFFu;
+      const uint32_t first = 8u * static_cast<uint32_t>(li) + __builtin_ctz(byte | 0x100u) +
+                             (t - before);
       s_chunk[w][n_list + static_cast<uint32_t>(__popcll(m & lt))] =
-          static_cast<uint16_t>(lane | (static_cast<uint32_t>(q) << 6));
+          static_cast<uint16_t>(lane | (first << 6) | (static_cast<uint32_t>(q) << 12));
+    }
     n_list += static_cast<uint32_t>(__popcll(m));
   }
   // The wave's LDS operations complete in order, so its own lanes' writes
@@ -839,27 +855,11 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
     const uint32_t ci = cb + lane;
     const bool act = ci < n_list;
     const uint32_t ent = act ? static_cast<uint32_t>(s_chunk[w][ci]) : 0u;
-    const uint32_t rl = ent & 63u, q = ent >> 6;
+    const uint32_t rl = ent & 63u, pos = (ent >> 6) & 63u, q = ent >> 12;
     const ChunkRecord<T> cr = s_rec[w].load(static_cast<int>(rl));
     const uint64_t rows_m = s_rows[w][rl];
-    // The chunk's first item, the t-th set bit (t = 8 q): its slice li is the
-    // last whose byte of s_pref (reached rows before it) is <= t, found for
-    // all eight bytes at once (each byte | 0x80, minus t + 1, keeps its high
-    // bit exactly when the byte exceeds t); within a slice the reached rows
-    // are contiguous.
-    int pos = 64;
-    {
-      const uint64_t pref = s_pref[w][rl];
-      const uint32_t t = q * static_cast<uint32_t>(R);
-      constexpr uint64_t kHigh = 0x8080808080808080ull, kOnes = 0x0101010101010101ull;
-      const uint64_t above = ((pref | kHigh) - static_cast<uint64_t>(t + 1u) * kOnes) & kHigh;
-      const int li = 7 - __popcll(above);
-      const uint32_t byte = static_cast<uint32_t>(rows_m >> (8 * li)) & 0xFFu;
-      const uint32_t before = static_cast<uint32_t>(pref >> (8 * li)) & 0xFFu;
-      if (act) pos = 8 * li + static_cast<int>(__builtin_ctz(byte | 0x100u)) +
-                     static_cast<int>(t - before);
-    }
-    const int n_here = act ? min(R, cr.n_items - static_cast<int>(q) * R) : 0;
+    const int n_here =
+        act ? min(R, __popcll(rows_m) - static_cast<int>(q) * R) : 0;
     // The record's rows from the chunk's first on: the chunk's items are
     // its n_here lowest set bits.
     uint64_t rest = act ? rows_m & (~0ull << pos) : 0ull;
@@ -931,8 +931,8 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
     }
     const T sums[10] = {t0, t1, t2, Y0, Z0, Y1, Z1, YY, YZ, ZZ};
     // One chunk index at a time: the records of one index are distinct.
-    const uint32_t q_lo = static_cast<uint32_t>(s_chunk[w][cb]) >> 6;
-    const uint32_t q_hi = static_cast<uint32_t>(s_chunk[w][min(cb + 63u, n_list - 1u)]) >> 6;
+    const uint32_t q_lo = static_cast<uint32_t>(s_chunk[w][cb]) >> 12;
+    const uint32_t q_hi = static_cast<uint32_t>(s_chunk[w][min(cb + 63u, n_list - 1u)]) >> 12;
 #pragma unroll 1
     for (uint32_t qq = q_lo; qq <= q_hi; ++qq) {
       if (act && q == qq) {
