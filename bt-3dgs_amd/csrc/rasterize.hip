@@ -728,6 +728,9 @@ __global__ __launch_bounds__(kBwdThreads) void raster_bwd_kernel(
   const int nts = kExact ? R : static_cast<int>(ts);
   uint32_t key;
   bool key_ok = in_list;
+  // Issued with the key's load, not after its check (one memory round trip
+  // fewer before the record's own loads).
+  const int32_t fid = in_list ? flatten_ids[r] : -1;
   if (isect_ids != nullptr) {
     const int64_t k = in_list ? isect_ids[r] : 0;
     key_ok = key_ok && k >= 0 && k < static_cast<int64_t>(n_keys);
@@ -735,7 +738,7 @@ __global__ __launch_bounds__(kBwdThreads) void raster_bwd_kernel(
   } else {
     key = wave_record_key(tile_offsets, n_keys, n_isects, rb, r);
   }
-  const int64_t g = key_ok ? static_cast<int64_t>(flatten_ids[r]) : -1;
+  const int64_t g = key_ok ? static_cast<int64_t>(fid) : -1;
   const uint32_t n_tiles = tw * th;
   const uint32_t cam = key / n_tiles, t = key - cam * n_tiles;
   const uint32_t ty = t / tw, tx = t - ty * tw;
@@ -956,6 +959,9 @@ __global__ __launch_bounds__(kSplitThreads) void raster_bwd_split_kernel(
   // Load and classify each record in list order.  A record whose key is out
   // of range gets no row, as in raster_bwd_kernel.
   uint32_t key = 0;
+  // Issued with the key's load, not after its check (one memory round trip
+  // fewer before the record's own loads).
+  const int32_t fid = in_list ? flatten_ids[r] : -1;
   if (rb < n_isects) {  // uniform per wave
     if (isect_ids != nullptr) {
       const int64_t k = in_list ? isect_ids[r] : 0;
@@ -965,7 +971,7 @@ __global__ __launch_bounds__(kSplitThreads) void raster_bwd_split_kernel(
       key = wave_record_key(tile_offsets, n_keys, n_isects, rb, r);
     }
   }
-  const int64_t g = in_list ? static_cast<int64_t>(flatten_ids[r]) : -1;
+  const int64_t g = in_list ? static_cast<int64_t>(fid) : -1;
   bool fast = false;
   RasterRecord<T> rec;
   {

@@ -577,6 +577,9 @@ __global__ __launch_bounds__(kBwdThreads) void voxel_bwd_kernel(
   const int nts = kExact ? R : static_cast<int>(ts);
   uint32_t key;
   bool key_ok = in_list;
+  // Issued with the key's load, not after its check (one memory round trip
+  // fewer before the record's own loads).
+  const int32_t fid = in_list ? flatten_ids[r] : -1;
   if (isect_ids != nullptr) {
     const int64_t k = in_list ? isect_ids[r] : 0;
     key_ok = key_ok && k >= 0 && k < static_cast<int64_t>(n_keys);
@@ -584,7 +587,7 @@ __global__ __launch_bounds__(kBwdThreads) void voxel_bwd_kernel(
   } else {
     key = wave_record_key(tile_offsets, n_keys, n_isects, rb, r);
   }
-  const int64_t g = key_ok ? static_cast<int64_t>(flatten_ids[r]) : -1;
+  const int64_t g = key_ok ? static_cast<int64_t>(fid) : -1;
   const Brick b = brick_of(key + koff, n2, n1, static_cast<uint32_t>(nts), D2, D1, D0);
   BwdRecord<T> rec;
   load_bwd_record(means3d, conics, opac, g, N, key_ok, b, rec);
@@ -744,6 +747,10 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
   const bool in_list = r < n_isects;
   uint32_t key;
   bool key_ok = in_list;
+  // Issued with the key's load, not after its check (one memory round trip
+  // fewer before the record's own loads).
+  const int32_t fid = in_list ? flatten_ids[r] : -1;
+  const uint64_t reach_r = kGiven && in_list ? reach[r] : 0ull;
   if (isect_ids != nullptr) {
     const int64_t k = in_list ? isect_ids[r] : 0;
     key_ok = key_ok && k >= 0 && k < static_cast<int64_t>(n_keys);
@@ -751,7 +758,7 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
   } else {
     key = wave_record_key(tile_offsets, n_keys, n_isects, rb, r);
   }
-  const int64_t g = key_ok ? static_cast<int64_t>(flatten_ids[r]) : -1;
+  const int64_t g = key_ok ? static_cast<int64_t>(fid) : -1;
   const Brick b = brick_of(key + koff, n2, n1, R, D2, D1, D0);
   BwdRecord<T> rec;
   if constexpr (kGiven)
@@ -767,7 +774,7 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
   // The record's reached rows; the items are its set bits in increasing order.
   uint64_t reached;
   if constexpr (kGiven)
-    reached = key_ok && rec.live ? reach[r] : 0ull;
+    reached = key_ok && rec.live ? reach_r : 0ull;
   else
     reached = reach_mask(rec, b, dx0);
   const int n_items = __popcll(reached);
