@@ -337,23 +337,36 @@ __global__ __launch_bounds__(256) void row_reduce_kernel(const T *__restrict__ r
     T carry[NV];
 #pragma unroll
     for (int c = 0; c < NV; ++c) carry[c] = 0;
-    for (int64_t base = past; base < n; base += 64) {
-      const int64_t e2 = base + lane;
-      const bool first = base == past;  // uniform: the prefetched rows
-      const int32_t id2 = first ? t_id : (e2 < n ? emit_ids[e2] : -1);
-      const bool take = e2 < n && id2 == seg_last;
-      if (take) {
-        T wv[NV];
-        if (first) {
+    // The prefetched 64 rows, then K x 64 rows a round with their ids loaded
+    // together, so a long tail (a Gaussian over hundreds of tiles) takes a
+    // K-th of the memory round trips.  Each lane adds its rows in increasing
+    // order either way.
+    const bool take0 = t_e < n && t_id == seg_last;
+    if (take0) {
 #pragma unroll
-          for (int c = 0; c < NV; ++c) wv[c] = t_row[c];
-        } else {
-          load_row(rows, e2, wv);
-        }
+      for (int c = 0; c < NV; ++c) carry[c] += t_row[c];
+    }
+    bool more = past + 63 < n && __shfl(static_cast<int>(take0), 63, 64);
+    for (int64_t base = past + 64; more && base < n; base += kReduceWaveRows) {  // uniform
+      int32_t id2[K];
 #pragma unroll
-        for (int c = 0; c < NV; ++c) carry[c] += wv[c];
+      for (int r = 0; r < K; ++r) {
+        const int64_t e2 = base + 64 * r + lane;
+        id2[r] = e2 < n ? emit_ids[e2] : -1;
       }
-      if (!(base + 63 < n && __shfl(static_cast<int>(take), 63, 64))) break;
+      bool take = false;
+#pragma unroll
+      for (int r = 0; r < K; ++r) {
+        const int64_t e2 = base + 64 * r + lane;
+        take = e2 < n && id2[r] == seg_last;
+        if (take) {
+          T wv[NV];
+          load_row(rows, e2, wv);
+#pragma unroll
+          for (int c = 0; c < NV; ++c) carry[c] += wv[c];
+        }
+      }
+      more = base + kReduceWaveRows - 1 < n && __shfl(static_cast<int>(take), 63, 64);
     }
 #pragma unroll
     for (int c = 0; c < NV; ++c) carry[c] = wave_sum(carry[c]);
