@@ -692,11 +692,14 @@ __global__ __launch_bounds__(kBwdThreads) void voxel_bwd_kernel(
 // wave, the (record, slice, row) items the records reach -- slice by slice,
 // row by row, as slice_rows gives them -- and hands them out in chunks of up
 // to kChunkRows consecutive items of one record, one chunk per lane and
-// round, so lanes spend their steps on reached rows.  Chunks are ordered by
-// (chunk index within the record, record): within a round each record
-// appears at most once per chunk index, and the chunk sums are added to the
-// record's LDS accumulators one chunk index at a time in increasing order,
-// so the result does not depend on scheduling.  Every brick must lie inside
+// round, so lanes spend their steps on reached rows.  The full chunks come
+// first, ordered by (chunk index within the record, record), then each
+// record's short last chunk, longest first; a round takes as many steps as
+// its first (longest) chunk.  Within a round each record appears at most
+// once per chunk index, and the chunk sums are added to the record's LDS
+// accumulators one chunk index at a time in increasing order, so each
+// record's chunks add in index order and the result does not depend on
+// scheduling.  Every brick must lie inside
 // the volume with 16-byte gradient rows, the gradient volume must span at
 // most 2^32 bytes and a slice fewer than 2^24 (the caller checks).
 
@@ -815,8 +818,11 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
 #pragma unroll
     for (int c = 0; c < 10; ++c) s_acc[w][c][lane] = 0;
   }
-  // Chunk list in (chunk index, record) order.  Byte li of pref: the reached
-  // rows of the slices before li (0..56).
+  // Chunk list: the full chunks in (chunk index, record) order, then each
+  // record's short last chunk, longest first, so that the rounds of short
+  // chunks take as many steps as their longest.  Each record's chunks keep
+  // increasing chunk indices.  Byte li of pref: the reached rows of the
+  // slices before li (0..56).
   uint64_t pref = 0;
   {
     uint32_t run = 0;
@@ -826,29 +832,40 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
       run += static_cast<uint32_t>(__popc(static_cast<uint32_t>(reached >> (8 * li)) & 0xFFu));
     }
   }
-  const int n_chunks = (n_items + R - 1) / R;
+  // The chunk's first row, the t-th set bit (t = 8 q): its slice li is the
+  // last whose byte of pref is <= t, found for all eight bytes at once (each
+  // byte | 0x80, minus t + 1, keeps its high bit exactly when the byte
+  // exceeds t); within a slice the reached rows are contiguous.
+  auto entry = [&](uint32_t q) {
+    const uint32_t t = q * static_cast<uint32_t>(R);
+    constexpr uint64_t kHigh = 0x8080808080808080ull, kOnes = 0x0101010101010101ull;
+    const uint64_t above = ((pref | kHigh) - static_cast<uint64_t>(t + 1u) * kOnes) & kHigh;
+    const int li = 7 - __popcll(above);
+    const uint32_t byte = static_cast<uint32_t>(reached >> (8 * li)) & 0xFFu;
+    const uint32_t before = static_cast<uint32_t>(pref >> (8 * li)) & 0xFFu;
+    const uint32_t first =
+        8u * static_cast<uint32_t>(li) + __builtin_ctz(byte | 0x100u) + (t - before);
+    return static_cast<uint16_t>(lane | (first << 6) | (q << 12));
+  };
+  const int n_full = n_items / R, tail = n_items - n_full * R;
   uint32_t n_list = 0;
   const uint64_t lt = lanemask_lt();
 #pragma unroll
   for (int q = 0; q < R; ++q) {
-    const bool has = n_chunks > q;
+    const bool has = n_full > q;
     const uint64_t m = ballot(has);
-    if (has) {
-      // The chunk's first row, the t-th set bit (t = 8 q): its slice li is
-      // the last whose byte of pref is <= t, found for all eight bytes at
-      // once (each byte | 0x80, minus t + 1, keeps its high bit exactly when
-      // the byte exceeds t); within a slice the reached rows are contiguous.
-      const uint32_t t = static_cast<uint32_t>(q) * static_cast<uint32_t>(R);
-      constexpr uint64_t kHigh = 0x8080808080808080ull, kOnes = 0x0101010101010101ull;
-      const uint64_t above = ((pref | kHigh) - static_cast<uint64_t>(t + 1u) * kOnes) & kHigh;
-      const int li = 7 - __popcll(above);
-      const uint32_t byte = static_cast<uint32_t>(reached >> (8 * li)) & 0xFFu;
-      const uint32_t before = static_cast<uint32_t>(pref >> (8 * li)) & 0xFFu;
-      const uint32_t first = 8u * static_cast<uint32_t>(li) + __builtin_ctz(byte | 0x100u) +
-                             (t - before);
+    if (has)
       s_chunk[w][n_list + static_cast<uint32_t>(__popcll(m & lt))] =
-          static_cast<uint16_t>(lane | (first << 6) | (static_cast<uint32_t>(q) << 12));
-    }
+          entry(static_cast<uint32_t>(q));
+    n_list += static_cast<uint32_t>(__popcll(m));
+  }
+#pragma unroll
+  for (int len = R - 1; len > 0; --len) {
+    const bool has = tail == len;
+    const uint64_t m = ballot(has);
+    if (has)
+      s_chunk[w][n_list + static_cast<uint32_t>(__popcll(m & lt))] =
+          entry(static_cast<uint32_t>(n_full));
     n_list += static_cast<uint32_t>(__popcll(m));
   }
   // The wave's LDS operations complete in order, so its own lanes' writes
@@ -877,8 +894,10 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
       wk[k] = 0;
     }
     T Y0 = 0, Z0 = 0, Y1 = 0, Z1 = 0, YY = 0, YZ = 0, ZZ = 0;
+    // The round's longest chunk is its first (lane 0 is always active).
+    const int steps = __builtin_amdgcn_readfirstlane(n_here);
 #pragma unroll 1
-    for (int st = 0; st < R; ++st) {
+    for (int st = 0; st < steps; ++st) {
       const bool item = st < n_here;
       // The next row (bit 63 when none is left: a step without an item
       // still reads a row of the record's own brick, which lies inside the
@@ -937,11 +956,15 @@ __global__ __launch_bounds__(64 * kChunkWaves) void voxel_bwd_chunk_kernel(
       t2 += wx * dxk[k];
     }
     const T sums[10] = {t0, t1, t2, Y0, Z0, Y1, Z1, YY, YZ, ZZ};
-    // One chunk index at a time: the records of one index are distinct.
-    const uint32_t q_lo = static_cast<uint32_t>(s_chunk[w][cb]) >> 12;
-    const uint32_t q_hi = static_cast<uint32_t>(s_chunk[w][min(cb + 63u, n_list - 1u)]) >> 12;
+    // One chunk index at a time, in increasing order: the records of one
+    // index are distinct, and each record's chunks are added in index order.
+    uint32_t qmask = 0;
+#pragma unroll
+    for (int b = 0; b < R; ++b)
+      if (ballot(act && q == static_cast<uint32_t>(b)) != 0) qmask |= 1u << b;
 #pragma unroll 1
-    for (uint32_t qq = q_lo; qq <= q_hi; ++qq) {
+    for (uint32_t mq = qmask; mq != 0u; mq &= mq - 1u) {
+      const uint32_t qq = static_cast<uint32_t>(__builtin_ctz(mq));
       if (act && q == qq) {
 #pragma unroll
         for (int c = 0; c < 10; ++c) s_acc[w][c][rl] += sums[c];
