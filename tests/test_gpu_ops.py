@@ -516,6 +516,78 @@ def test_absgrad_sign_split_backward(dtype, shape):
         print(n, r)
 
 
+def _same_grads(a, b, exact):
+    for x, y in zip(a, b):
+        if x is None:
+            assert y is None
+            continue
+        assert bool(torch.isfinite(x).all())
+        if exact:
+            assert torch.equal(x, y)
+        else:  # one-pass forms: device atomics add in any order
+            torch.testing.assert_close(x, y, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("order", ["emission", "tile"])
+def test_non_finite_upstream_gradient_where_nothing_passes(order):
+    # The reference skips a (record, pixel / voxel) pair that fails the alpha
+    # test before it reads the upstream gradient there, so an inf or NaN
+    # gradient where no record passes changes nothing.  The kernels add exact
+    # zeros for failing pairs: the gradients equal those with zeros there,
+    # bit for bit in the two-pass forms.
+    # Sparse small Gaussians: tiles with records hold pixels no record passes.
+    d, m2, con, mu, op, ids, fl, off = _raster_case(150, 21, 64, 64, 16, 1, torch.float32,
+                                                    log_mu=-4.3)
+    assert fl.numel() > 50
+    img = W.rasterize_to_pixels_fwd(m2, con, op, mu, off, fl, 64, 64, 16)
+    v = torch.randn(img.shape, generator=d["gen"]).to(DEV)
+    dead = img == 0  # no record passes there: a passing alpha is at least 1e-5
+    starts = off.reshape(-1).long()
+    ends = torch.cat([starts[1:], torch.tensor([fl.numel()], device=DEV)])
+    live = (ends > starts).reshape(4, 4).repeat_interleave(16, 0).repeat_interleave(16, 1)
+    assert int((dead.reshape(64, 64) & live).sum()) > 20  # inside tiles the kernels walk
+    v_zero = torch.where(dead, torch.zeros_like(v), v)
+    fl_run = fl if order == "emission" else fl.clone()
+    for bad in (float("inf"), float("nan")):
+        v_bad = torch.where(dead, torch.full_like(v, bad), v)
+        for absgrad in (True, False):
+            a = W.rasterize_to_pixels_bwd_per_gaussian(m2, con, op, mu, off, ids, fl_run, v_bad,
+                                                       64, 64, 16, absgrad)
+            b = W.rasterize_to_pixels_bwd_per_gaussian(m2, con, op, mu, off, ids, fl_run, v_zero,
+                                                       64, 64, 16, absgrad)
+            _same_grads(a, b, exact=order == "emission")
+    d3, m3, con3, ids3, fl3, off3 = _voxel_case(300, 8, (32, 32, 32), 8)
+    assert fl3.numel() > 100
+    op3 = d3["opac"]
+    vol = W.voxelize_to_voxels_fwd(m3, con3, op3, off3, fl3, 32, 32, 32, 8)
+    v3 = torch.randn(vol.shape, generator=d3["gen"]).to(DEV)
+    dead3 = vol == 0
+    starts3 = off3.reshape(-1).long()
+    ends3 = torch.cat([starts3[1:], torch.tensor([fl3.numel()], device=DEV)])
+    live3 = (ends3 > starts3).reshape(4, 4, 4)
+    live3 = live3.repeat_interleave(8, 0).repeat_interleave(8, 1).repeat_interleave(8, 2)
+    assert int((dead3 & live3).sum()) > 100  # inside bricks the kernels walk
+    v3_zero = torch.where(dead3, torch.zeros_like(v3), v3)
+    fl3_run = fl3 if order == "emission" else fl3.clone()
+    lists = _ops.bin_tiles_3d(m3, W.world_to_volume_mapping_fwd(
+        d3["means"], d3["covars"], op3, torch.full((3,), 2.0, device=DEV),
+        torch.zeros(3, device=DEV), 32, 32, 32, 1e-8, 3.0)[2], 8, 4, 4, 4)
+    _, reach = _ops.voxelize_with_reach(m3, con3, op3, off3, lists.flatten_ids, 32, 32, 32)
+    for bad in (float("inf"), float("nan")):
+        v3_bad = torch.where(dead3, torch.full_like(v3, bad), v3)
+        a = W.voxelize_to_voxels_bwd_per_gaussian(m3, con3, op3, off3, ids3, fl3_run, v3_bad, 32,
+                                                  32, 32, 8)
+        b = W.voxelize_to_voxels_bwd_per_gaussian(m3, con3, op3, off3, ids3, fl3_run, v3_zero,
+                                                  32, 32, 32, 8)
+        _same_grads(a, b, exact=order == "emission")
+        if order == "emission":  # the chunked walk given the forward's reach masks
+            a = _ops.voxel_backward(m3, con3, op3, off3, lists, v3_bad, 32, 32, 32, 8,
+                                    reach=reach)
+            b = _ops.voxel_backward(m3, con3, op3, off3, lists, v3_zero, 32, 32, 32, 8,
+                                    reach=reach)
+            _same_grads(a, b, exact=True)
+
+
 @pytest.mark.parametrize("order", ["emission", "tile"])
 def test_nan_opacity_propagates_as_in_the_reference(order):
     # A NaN alpha is not below the cut-off, so the reference does not skip it:
