@@ -24,6 +24,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import math
 import os
@@ -482,6 +483,12 @@ def time_adam(proj: Projection, reps):
 def time_steps(fn, steps, warmup):
     for _ in range(warmup):
         fn()
+    # The objects built so far leave the collector's view: a full collection
+    # over them (about 270k objects: torch's and the workloads') stalls the
+    # host some 80 ms every ~150 training steps, which a long training
+    # process avoids the same way.
+    gc.collect()
+    gc.freeze()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
