@@ -453,7 +453,9 @@ __global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(const uint32_t
 // of the destination.  Each item carries its key, its flat id (gid) and,
 // with kTwo, its emission index e.  kFirst: the input is the emission-order
 // array itself, so e is the input index and only keys and gids are read.
-// kFinal: writes keys_out64 / vals_out32 = gid / src_out = e.
+// kFinal: writes keys_out64 / vals_out32 = gid / src_out = e; with
+// keys_out64 null (a caller keeping only the tile offsets) the keys go to
+// keys_out when it is given (for a later offset search) and nowhere else.
 // The LDS footprint follows the sort: digit tables for 2^kDBits digits,
 // keys staged as 16 bits when every key fits (kKey16), and in a single-pass
 // sort the emission index staged as its 16-bit block-local position.  At
@@ -612,7 +614,10 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     const uint32_t d = (k >> shift) & mask;
     const int64_t dest = static_cast<int64_t>(gbase[d]) + (lp - static_cast<int>(dbase[d]));
     if (kFinal) {
-      keys_out64[dest] = static_cast<int64_t>(k);
+      if (keys_out64 != nullptr)
+        keys_out64[dest] = static_cast<int64_t>(k);
+      else if (keys_out != nullptr)
+        keys_out[dest] = k;
       vals_out32[dest] = static_cast<int32_t>(s_gid[lp]);
       if (kTwo)
         src_out[dest] = static_cast<int32_t>(kLocalE ? block_first + s_e[lp] : s_e[lp]);
@@ -627,9 +632,11 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
 // ------------------------------------------------------------- offsets ---
 
 // n_dev: the record count on the device, at most n (else nothing is
-// written); null: n records.
-__global__ __launch_bounds__(256) void offset_encode_kernel(const int64_t *__restrict__ ids,
-                                                            int64_t n, int64_t n_keys,
+// written); null: n records.  K: the sorted keys' type (int64 isect_ids, or
+// the sort's 32-bit keys).
+template <typename K>
+__global__ __launch_bounds__(256) void offset_encode_kernel(const K *__restrict__ ids, int64_t n,
+                                                            int64_t n_keys,
                                                             int32_t *__restrict__ out,
                                                             const int64_t *__restrict__ n_dev) {
   const int64_t k = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
@@ -639,12 +646,32 @@ __global__ __launch_bounds__(256) void offset_encode_kernel(const int64_t *__res
   int64_t lo = 0, hi = nn;
   while (lo < hi) {
     const int64_t mid = (lo + hi) >> 1;
-    if (ids[mid] < k)
+    if (static_cast<int64_t>(ids[mid]) < k)
       lo = mid + 1;
     else
       hi = mid;
   }
   out[k] = static_cast<int32_t>(lo);
+}
+
+// The inverse: each of the n sorted records' key from the keys' first
+// indices (offsets[0] = 0), the last key whose first index is at most the
+// record's.  Empty keys share their successor's first index, so a record
+// never lands on one.
+__global__ __launch_bounds__(256) void keys_from_offsets_kernel(const int32_t *__restrict__ offsets,
+                                                                int64_t n_keys, int64_t n,
+                                                                int64_t *__restrict__ keys) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (r >= n) return;
+  int64_t lo = 0, hi = n_keys;  // offsets[lo] <= r; offsets[hi] > r (offsets[n_keys] = n)
+  while (hi - lo > 1) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (static_cast<int64_t>(offsets[mid]) <= r)
+      lo = mid;
+    else
+      hi = mid;
+  }
+  keys[r] = lo;
 }
 
 // ----------------------------------------------------------- workspace ---
@@ -766,6 +793,9 @@ int launch_scatter(bool first, bool last, bool two, uint32_t bits, bool key16,
 // (optional): each of the n_keys keys' first index in the sorted list, as
 // offset_encode_kernel computes it -- taken from a single pass's digit
 // offsets when one pass covers the key, else searched in the sorted keys.
+// keys64 may be null when tile_offsets is given: a single pass then writes
+// no keys, and the last of several passes leaves 32-bit keys in the
+// workspace for the search.
 int radix_sort(SortSpace &s, const int64_t *n_dev, int64_t cap, uint32_t key_bits,
                int64_t *keys64, int32_t *vals32, bool two, int32_t *src,
                int32_t *tile_offsets, int64_t n_keys, hipStream_t stream) {
@@ -785,6 +815,7 @@ int radix_sort(SortSpace &s, const int64_t *n_dev, int64_t cap, uint32_t key_bit
                                                             "isect sort scan"));
     const bool first = p == 0, last = p == passes - 1;
     uint32_t *kout = (p % 2 == 0) ? s.k1 : s.k0;
+    if (last && keys64 == nullptr && passes == 1) kout = nullptr;
     uint32_t *eout = (p % 2 == 0) ? s.e1 : s.e0;
     uint32_t *gout = (p % 2 == 0) ? s.g1 : s.g0;
     R2S_RETURN_IF(launch_scatter(first, last, two, bits, key_bits <= 16, kin, ein, gin, n_dev,
@@ -796,8 +827,13 @@ int radix_sort(SortSpace &s, const int64_t *n_dev, int64_t cap, uint32_t key_bit
     gin = gout;
   }
   if (tile_offsets != nullptr && passes > 1) {
-    offset_encode_kernel<<<dim3(static_cast<uint32_t>(ceil_div(n_keys, 256))), dim3(256), 0,
-                           stream>>>(keys64, cap, n_keys, tile_offsets, n_dev);
+    const dim3 grid(static_cast<uint32_t>(ceil_div(n_keys, 256)));
+    if (keys64 != nullptr)
+      offset_encode_kernel<int64_t><<<grid, dim3(256), 0, stream>>>(keys64, cap, n_keys,
+                                                                     tile_offsets, n_dev);
+    else
+      offset_encode_kernel<uint32_t><<<grid, dim3(256), 0, stream>>>(kin, cap, n_keys,
+                                                                      tile_offsets, n_dev);
     return check_launch("isect offsets");
   }
   return R2S_OK;
@@ -866,7 +902,8 @@ int count_3d_impl(const T *means3d, const int32_t *radii, int64_t N, uint32_t ts
 }
 
 int check_sort_args(int64_t n_isects, uint32_t end_bit, int64_t n_keys, void *ws,
-                    size_t ws_bytes, int64_t *keys, int32_t *vals, const char *name) {
+                    size_t ws_bytes, int64_t *keys, int32_t *vals, const int32_t *tile_offsets,
+                    const char *name) {
   R2S_REQUIRE(n_isects >= 0, "%s: negative n_isects", name);
   if (n_isects > kInt32Max) {
     set_error("%s: %lld intersections exceed the int32 offset range", name,
@@ -877,7 +914,8 @@ int check_sort_args(int64_t n_isects, uint32_t end_bit, int64_t n_keys, void *ws
   R2S_REQUIRE(n_keys <= (1ll << end_bit), "%s: end_bit %u too small for %lld keys", name,
               end_bit, (long long)n_keys);
   if (n_isects == 0) return R2S_OK;
-  R2S_REQUIRE(keys && vals, "%s: null output", name);
+  R2S_REQUIRE(vals, "%s: null flatten_ids", name);
+  R2S_REQUIRE(keys || tile_offsets, "%s: null isect_ids without tile_offsets", name);
   return check_workspace(ws, ws_bytes, sort_space_bytes(n_isects, end_bit), name);
 }
 
@@ -891,7 +929,8 @@ int emit_sort_2d_impl(const T *means2d, const int32_t *radii, int rect, int64_t 
   const char *name = "isect_tiles";
   R2S_REQUIRE(C >= 0 && N >= 0 && C * N <= kInt32Max, "%s: bad size", name);
   R2S_REQUIRE(ts > 0, "%s: tile_size must be positive", name);
-  R2S_RETURN_IF(check_sort_args(n_isects, end_bit, C * tw * th, ws, ws_bytes, keys, vals, name));
+  R2S_RETURN_IF(check_sort_args(n_isects, end_bit, C * tw * th, ws, ws_bytes, keys, vals,
+                                tile_offsets, name));
   const int64_t n_keys = C * tw * th;
   if (n_isects == 0)
     return tile_offsets == nullptr || n_keys == 0
@@ -926,7 +965,8 @@ int emit_sort_3d_impl(const T *means3d, const int32_t *radii, int64_t N, uint32_
   R2S_REQUIRE(z0 <= z1 && z1 <= n0, "%s: brick layers [%u, %u) outside [0, %u)", name, z0,
               z1, n0);
   const int64_t n_keys = static_cast<int64_t>(n2) * n1 * (z1 - z0);
-  R2S_RETURN_IF(check_sort_args(n_isects, end_bit, n_keys, ws, ws_bytes, keys, vals, name));
+  R2S_RETURN_IF(check_sort_args(n_isects, end_bit, n_keys, ws, ws_bytes, keys, vals,
+                                tile_offsets, name));
   if (n_isects == 0)
     return tile_offsets == nullptr || n_keys == 0
                ? R2S_OK
@@ -1058,9 +1098,28 @@ int r2s_isect_offset_encode(const int64_t *ids, int64_t n_isects, int64_t n_keys
   hipStream_t stream = r2s::as_stream(st);
   if (n_isects == 0) return r2s::device_fill<int32_t>(out, n_keys, 0, stream, "isect_offset_encode");
   R2S_REQUIRE(ids != nullptr, "isect_offset_encode: null isect_ids");
-  r2s::offset_encode_kernel<<<dim3(static_cast<uint32_t>(r2s::ceil_div(n_keys, 256))), dim3(256), 0,
-                              stream>>>(ids, n_isects, n_keys, out, nullptr);
+  r2s::offset_encode_kernel<int64_t>
+      <<<dim3(static_cast<uint32_t>(r2s::ceil_div(n_keys, 256))), dim3(256), 0, stream>>>(
+          ids, n_isects, n_keys, out, nullptr);
   return r2s::check_launch("isect_offset_encode");
+}
+
+int r2s_isect_keys_from_offsets(const int32_t *tile_offsets, int64_t n_keys, int64_t n_isects,
+                                int64_t *isect_ids, r2s_stream_t st) {
+  r2s::clear_error();
+  const char *name = "isect_keys_from_offsets";
+  R2S_REQUIRE(n_isects >= 0 && n_keys >= 0, "%s: negative size", name);
+  if (n_isects == 0) return R2S_OK;
+  if (n_isects > r2s::kInt32Max) {
+    r2s::set_error("%s: %lld records exceed the int32 offset range", name, (long long)n_isects);
+    return R2S_ERANGE;
+  }
+  R2S_REQUIRE(n_keys >= 1, "%s: records without keys", name);
+  R2S_REQUIRE(tile_offsets != nullptr && isect_ids != nullptr, "%s: null pointer", name);
+  r2s::keys_from_offsets_kernel<<<dim3(static_cast<uint32_t>(r2s::ceil_div(n_isects, 256))),
+                                  dim3(256), 0, r2s::as_stream(st)>>>(tile_offsets, n_keys,
+                                                                      n_isects, isect_ids);
+  return r2s::check_launch(name);
 }
 
 }  // extern "C"

@@ -86,10 +86,14 @@ __device__ __forceinline__ double limit_as_value(uint64_t b) {
 // Keys of the records of a wave: `rb` is the wave's first record (uniform),
 // `r` the lane's; the key of record r is the last k with offsets[k] <= r
 // (offsets[0] = 0, non-decreasing).  One uniform binary search for rb, then a
-// uniform walk over the boundaries inside the wave's 64 records.
+// uniform walk over the next few keys' first indices; a window holding more
+// boundaries than that (empty keys share their successor's first index, so
+// a run of them is many boundaries at one index) finishes with a per-lane
+// binary search above the walk's last key.
 __device__ __forceinline__ uint32_t wave_record_key(const int32_t *__restrict__ offsets,
                                                     uint32_t n_keys, int64_t n_isects, int64_t rb,
                                                     int64_t r) {
+  constexpr uint32_t kWalk = 4;
   uint32_t lo = 0, hi = n_keys;
   while (hi - lo > 1) {
     const uint32_t mid = (lo + hi) >> 1;
@@ -100,12 +104,23 @@ __device__ __forceinline__ uint32_t wave_record_key(const int32_t *__restrict__ 
   }
   const int64_t r_last = min(rb + 63, n_isects - 1);
   uint32_t key = lo;
-  for (uint32_t k = lo + 1; k < n_keys; ++k) {
+  uint32_t k = lo + 1;
+  for (uint32_t step = 0; step < kWalk; ++step, ++k) {
+    if (k >= n_keys) return key;
     const int64_t bnd = offsets[k];
-    if (bnd > r_last) break;
+    if (bnd > r_last) return key;
     if (r >= bnd) key = k;
   }
-  return key;
+  // offsets[key] <= r: the last such key at or above it.
+  uint32_t a = key, b = n_keys;
+  while (b - a > 1) {
+    const uint32_t mid = (a + b) >> 1;
+    if (static_cast<int64_t>(offsets[mid]) <= r)
+      a = mid;
+    else
+      b = mid;
+  }
+  return a;
 }
 
 // Square root for culling bounds: the hardware v_sqrt_f32 (about 1 ulp),

@@ -96,6 +96,7 @@ _PLAIN = {
     "r2s_abi_version": (_i32, []),
     "r2s_isect_workspace_bytes": (_i64, [_i64, _i64, _u32]),
     "r2s_isect_offset_encode": (_i32, [_p, _i64, _i64, _p, _p]),
+    "r2s_isect_keys_from_offsets": (_i32, [_p, _i64, _i64, _p, _p]),
     "r2s_rasterize_workspace_bytes": (_i64, [_i64, _i64, _u32, _i32]),
     "r2s_rasterize_bwd_workspace_bytes": (_i64, [_i64, _i64, _i32]),
     "r2s_rasterize_payload_bytes": (_i64, [_i64, _i32]),
@@ -151,7 +152,7 @@ DENSIFY_MAX_WIDTH = 16
 
 SYMBOLS = sorted(list(_PLAIN) + [f"r2s_{n}_{s}" for n in _FLOAT_OPS for s in ("f32", "f64")])
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 
 def load(path: str = LIB_PATH) -> ctypes.CDLL:

@@ -121,18 +121,20 @@ TOO_MANY = object()  # _emit_and_sort: the count exceeds max_records
 
 
 def _emit_and_sort(launch, offsets: Tensor, n_items: int, n_keys: int, op: str,
-                   dev: torch.device, kind: str, max_records: Optional[int] = None):
+                   dev: torch.device, kind: str, max_records: Optional[int] = None,
+                   keep_ids: bool = True):
     """The emit + sort half of a binning op (IsectTiles.cpp:100-169): returns
     (isect_ids, flatten_ids, emit_ids, isect_src), or None without records,
     or TOO_MANY when there are more than max_records records (nothing
     allocated for them).  launch(capacity, end_bit, outputs, workspace)
-    enqueues the library call."""
+    enqueues the library call.  keep_ids=False: isect_ids is None and the
+    sort writes no keys (the caller's launch passes the tile offsets)."""
     lib = _lib()
     end_bit = _end_bit(n_keys)
     key = (dev.index, kind, n_items, n_keys)
 
     def alloc(cap):
-        outs = (torch.empty((cap,), dtype=torch.int64, device=dev),
+        outs = (torch.empty((cap,), dtype=torch.int64, device=dev) if keep_ids else None,
                 torch.empty((cap,), dtype=torch.int32, device=dev),
                 torch.empty((cap,), dtype=torch.int32, device=dev),
                 torch.empty((cap,), dtype=torch.int32, device=dev))
@@ -161,7 +163,7 @@ def _emit_and_sort(launch, offsets: Tensor, n_items: int, n_keys: int, op: str,
         n = int(host[0])
         _note_count(key, n)
         if n <= cap:
-            return None if n == 0 else tuple(t[:n] for t in outs)
+            return None if n == 0 else tuple(None if t is None else t[:n] for t in outs)
     else:
         n = int(offsets[n_items].item())  # the one host read-back (IsectTiles.cpp:100)
         _note_count(key, n)
@@ -188,7 +190,9 @@ class TileLists(NamedTuple):
     """Output of :func:`bin_tiles_2d` / :func:`bin_tiles_3d`."""
 
     tiles_per_gauss: Tensor
-    isect_ids: Tensor   # int64 tile keys, sorted
+    # int64 tile keys, sorted; None for a list binned with keep_ids=False
+    # (read isect_ids, which then recovers them from tile_offsets).
+    keys: Optional[Tensor]
     flatten_ids: Tensor  # int32 ids in (key, emission) order
     emit_ids: Optional[Tensor]   # None when there are no records
     isect_src: Optional[Tensor]
@@ -200,6 +204,15 @@ class TileLists(NamedTuple):
     @property
     def emission(self) -> Optional[Tuple[Tensor, Tensor]]:
         return None if self.emit_ids is None else (self.emit_ids, self.isect_src)
+
+    @property
+    def isect_ids(self) -> Tensor:
+        """The sorted int64 tile keys (IsectTiles.cpp:113-169's isect_ids):
+        the stored array, or, for a list binned without it, a new array
+        recovered from tile_offsets (one launch per access)."""
+        if self.keys is not None:
+            return self.keys
+        return keys_from_offsets(self.tile_offsets, self.flatten_ids.numel())
 
 
 # The reference's operator signatures (isect_tiles -> rasterize_to_pixels_bwd*)
@@ -589,9 +602,11 @@ def explicit_backward_tail(means: Tensor, covars: Tensor, viewmats: Tensor, Ks: 
 # ---------------------------------------------------------------- binning --
 
 def bin_tiles_2d(means2d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim1: int,
-                 n_tiles_dim0: int) -> TileLists:
+                 n_tiles_dim0: int, keep_ids: bool = True) -> TileLists:
     """IsectTiles.cpp:31-170: the records of every (view, Gaussian, tile) overlap,
-    sorted by (tile key, emission index), with their emission order."""
+    sorted by (tile key, emission index), with their emission order.
+    keep_ids=False: the int64 keys are not stored (lists.keys is None; the
+    backward ops find each record's key from tile_offsets)."""
     _check_input(means2d, "means2d")
     _check_input(radii, "radii")
     _check(means2d.dim() == 3, "means2d must be 3D [C, N, 2]")
@@ -626,7 +641,8 @@ def bin_tiles_2d(means2d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim1: i
                   tw, th, _ptr(offsets), cap, end_bit, *[_ptr(t) for t in outs],
                   _ptr(tile_offsets), _ptr(ws), ws.numel(), st)
 
-        res = _emit_and_sort(launch, offsets, C * N, C * tw * th, "isect_tiles", dev, "2d")
+        res = _emit_and_sort(launch, offsets, C * N, C * tw * th, "isect_tiles", dev, "2d",
+                             keep_ids=keep_ids)
     if res is None:
         return empty
     return TileLists(tiles_per_gauss, *res, tile_offsets)
@@ -638,6 +654,21 @@ def isect_tiles(means2d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim1: in
     lists = bin_tiles_2d(means2d, radii, tile_size, n_tiles_dim1, n_tiles_dim0)
     _remember_emission(lists, means2d.size(0) * int(n_tiles_dim1) * int(n_tiles_dim0))
     return lists.tiles_per_gauss, lists.isect_ids, lists.flatten_ids
+
+
+def keys_from_offsets(tile_offsets: Tensor, n_isects: int) -> Tensor:
+    """The sorted int64 keys of a list of n_isects records from its
+    tile_offsets (each key's first index): the inverse of
+    isect_offset_encode / isect_offset_encode_3d."""
+    _check_input(tile_offsets, "tile_offsets")
+    _check(tile_offsets.dtype == torch.int32, "tile_offsets must be int32")
+    dev = tile_offsets.device
+    keys = torch.empty((int(n_isects),), dtype=torch.int64, device=dev)
+    if keys.numel() > 0:
+        with torch.cuda.device(dev):
+            _call("r2s_isect_keys_from_offsets", _ptr(tile_offsets), tile_offsets.numel(),
+                  keys.numel(), _ptr(keys), _stream(dev))
+    return keys
 
 
 def isect_offset_encode(isect_ids: Tensor, C: int, n_tiles_dim1: int,
@@ -658,11 +689,12 @@ def isect_offset_encode(isect_ids: Tensor, C: int, n_tiles_dim1: int,
 
 def bin_tiles_3d(means3d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim2: int,
                  n_tiles_dim1: int, n_tiles_dim0: int,
-                 max_records: Optional[int] = None) -> Optional[TileLists]:
+                 max_records: Optional[int] = None, keep_ids: bool = True) -> Optional[TileLists]:
     """IsectTiles3D.cpp:31-162: the (Gaussian, brick) records, sorted by
     (brick key, emission index), with their emission order.  With
     ``max_records``, None when there would be more records than that (the
-    caller then bins the volume in z-slabs, bin_tiles_3d_slab)."""
+    caller then bins the volume in z-slabs, bin_tiles_3d_slab).  keep_ids as
+    for bin_tiles_2d."""
     _check_input(means3d, "means3d")
     _check_input(radii, "radii")
     _check(means3d.dim() == 2, "means3d must be 2D [N, 3]")
@@ -697,7 +729,7 @@ def bin_tiles_3d(means3d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim2: i
 
         # IsectTiles3D.cpp:96 reads the count back here.
         res = _emit_and_sort(launch, offsets, N, n2 * n1 * n0, "isect_tiles_3d", dev, "3d",
-                             max_records)
+                             max_records, keep_ids=keep_ids)
     if res is TOO_MANY:
         return None
     if res is None:
@@ -775,11 +807,12 @@ def plan_slabs(layer_counts, limit: Optional[int] = None) -> list:
 
 
 def bin_tiles_3d_slab(means3d: Tensor, radii: Tensor, tile_size: int, n_tiles_dim2: int,
-                      n_tiles_dim1: int, n_tiles_dim0: int, z0: int,
-                      z1: int) -> Tuple[TileLists, Tensor]:
+                      n_tiles_dim1: int, n_tiles_dim0: int, z0: int, z1: int,
+                      keep_ids: bool = True) -> Tuple[TileLists, Tensor]:
     """(lists, tile_offsets [z1 - z0, n1, n2]) of the brick layers [z0, z1):
     the records of the whole volume's list (bin_tiles_3d) whose brick lies in
-    those layers, in the same order, with keys relative to layer z0."""
+    those layers, in the same order, with keys relative to layer z0.
+    keep_ids as for bin_tiles_2d."""
     _check_input(means3d, "means3d")
     _check_input(radii, "radii")
     _check(means3d.dim() == 2 and means3d.size(1) == 3, "means3d must be 2D [N, 3]")
@@ -809,7 +842,7 @@ def bin_tiles_3d_slab(means3d: Tensor, radii: Tensor, tile_size: int, n_tiles_di
             offs.zero_()
             return empty, offs
         end_bit = _end_bit(n_keys)
-        outs = (torch.empty((n,), dtype=torch.int64, device=dev),
+        outs = (torch.empty((n,), dtype=torch.int64, device=dev) if keep_ids else None,
                 torch.empty((n,), dtype=torch.int32, device=dev),
                 torch.empty((n,), dtype=torch.int32, device=dev),
                 torch.empty((n,), dtype=torch.int32, device=dev))
@@ -862,7 +895,7 @@ def voxel_backward_slab(means3d: Tensor, conics: Tensor, opacities: Tensor,
         ws = _workspace(_lib().r2s_voxelize_bwd_workspace_bytes(n, means3d.element_size()), dev)
         _call(f"r2s_voxelize_bwd_emit_slab_{_suffix(means3d, 'voxelize_to_voxels_bwd')}",
               _ptr(means3d), _ptr(conics), _ptr(opacities), _ptr(tile_offsets),
-              _ptr(lists.isect_ids), _ptr(lists.flatten_ids), _ptr(lists.emit_ids),
+              _ptr(lists.keys), _ptr(lists.flatten_ids), _ptr(lists.emit_ids),
               _ptr(lists.isect_src), n, _ptr(v_volume), N, d2, d1, d0, int(tile_size), n2, n1,
               int(z0), nz, _ptr(v_m), _ptr(v_c), _ptr(v_o), _ptr(ws), ws.numel(), _stream(dev))
     return v_m, v_c, v_o
@@ -1017,7 +1050,7 @@ def raster_backward(means2d: Tensor, conics: Tensor, opacities: Tensor, mus: Ten
                  (mus, "mus"), (tile_offsets, "tile_offsets"), (lists.flatten_ids, "flatten_ids"),
                  (v_image, "v_render_output")):
         _check_input(t, n)
-    return _raster_bwd(means2d, conics, opacities, mus, tile_offsets, lists.isect_ids,
+    return _raster_bwd(means2d, conics, opacities, mus, tile_offsets, lists.keys,
                        lists.flatten_ids, v_image, img_w, img_h, tile_size, bool(absgrad),
                        "raster_backward", emission=lists.emission)
 
@@ -1129,7 +1162,7 @@ def raster_backward_packed(payload: Tensor, opacities: Tensor, mus: Tensor,
         nbytes = _lib().r2s_rasterize_bwd_workspace_bytes(n_isects, 0, payload.element_size())
         ws = _workspace(nbytes, dev) if nbytes > 0 else None
         _call(f"r2s_rasterize_bwd_packed_{sfx}", _ptr(payload), _ptr(opacities), _ptr(mus),
-              _ptr(tile_offsets), _ptr(lists.isect_ids), _ptr(lists.flatten_ids), _ptr(emit),
+              _ptr(tile_offsets), _ptr(lists.keys), _ptr(lists.flatten_ids), _ptr(emit),
               _ptr(src), n_isects, _ptr(v_image), C, N, W, H, ts, tw, th,
               *[_ptr(t) for t in outs], 1 if zeroed else 0, _ptr(ws),
               0 if ws is None else ws.numel(), _stream(dev))
@@ -1367,7 +1400,7 @@ def voxel_backward(means3d: Tensor, conics: Tensor, opacities: Tensor, tile_offs
                  (tile_offsets, "tile_offsets"), (lists.flatten_ids, "flatten_ids"),
                  (v_volume, "v_render_output")):
         _check_input(t, n)
-    return _voxel_bwd(means3d, conics, opacities, tile_offsets, lists.isect_ids,
+    return _voxel_bwd(means3d, conics, opacities, tile_offsets, lists.keys,
                       lists.flatten_ids, v_volume, dim2, dim1, dim0, tile_size,
                       "voxel_backward", emission=lists.emission, reach=reach)
 

@@ -137,7 +137,9 @@ class ImagePass:
         if ts in ops.PACKED_TILE_SIZES:
             payload, zeroed = ops.raster_pack(means2d, conics, weights, mus,
                                               zero_outputs=for_backward, absgrad=absgrad)
-        lists = ops.bin_tiles_2d(means2d, radii, ts, across, down)
+        # The sorted int64 keys are not stored: the backward finds each
+        # record's tile from the tile offsets (lists.isect_ids recovers them).
+        lists = ops.bin_tiles_2d(means2d, radii, ts, across, down, keep_ids=False)
         tile_offsets = lists.tile_offsets
         if tile_offsets is None:  # no records
             tile_offsets = ops.isect_offset_encode(lists.isect_ids, int(viewmats.shape[0]),
@@ -241,14 +243,15 @@ class VolumePass:
             d2, d1, d0, float(eps3d), float(radius_clip))
         n2, n1, n0 = _tiles_along(d2, ts), _tiles_along(d1, ts), _tiles_along(d0, ts)
         weights = opacities.contiguous()
-        lists = ops.bin_tiles_3d(means3d, radii, ts, n2, n1, n0, max_records=ops.SLAB_RECORDS)
+        lists = ops.bin_tiles_3d(means3d, radii, ts, n2, n1, n0, max_records=ops.SLAB_RECORDS,
+                                 keep_ids=False)
         if lists is None:
             slabs = tuple(ops.plan_slabs(ops.layer_counts_3d(means3d, radii, ts, n2, n1, n0),
                                          ops.SLAB_RECORDS))
             volume = torch.empty((d0, d1, d2), dtype=means3d.dtype, device=means3d.device)
             for z0, z1 in slabs:
                 slab_lists, slab_offsets = ops.bin_tiles_3d_slab(means3d, radii, ts, n2, n1, n0,
-                                                                 z0, z1)
+                                                                 z0, z1, keep_ids=False)
                 ops.voxelize_slab(means3d, conics, weights, slab_offsets, slab_lists, volume, ts,
                                   z0)
                 del slab_lists, slab_offsets
@@ -277,7 +280,8 @@ class VolumePass:
             total = None
             for z0, z1 in self.slabs:
                 slab_lists, slab_offsets = ops.bin_tiles_3d_slab(self.means3d, self.radii, ts,
-                                                                 n2, n1, n0, z0, z1)
+                                                                 n2, n1, n0, z0, z1,
+                                                                 keep_ids=False)
                 part = ops.voxel_backward_slab(self.means3d, self.conics, self.weights,
                                                slab_offsets, slab_lists, v_volume, ts, z0)
                 total = list(part) if total is None else [a.add_(b) for a, b in zip(total, part)]

@@ -38,7 +38,8 @@ typedef void *r2s_stream_t; /* hipStream_t */
 
 /* Message describing the last failure on the calling thread ("" if none). */
 const char *r2s_last_error(void);
-/* ABI revision of this header; bumped whenever a signature changes. */
+/* ABI revision of this header; bumped whenever a signature changes or an
+ * entry is added. */
 int r2s_abi_version(void);
 
 /* ---------------------------------------------------------------------- */
@@ -243,6 +244,10 @@ int r2s_isect_count_2d_f64(const double *means2d, const int32_t *radii,
  * is read off that pass's digit offsets at no extra cost, else searched in
  * the sorted keys.  Not in the reference (whose isect_tiles returns no
  * offsets); r2splat.ops uses it in place of a separate encode call.
+ * isect_ids may be NULL when tile_offsets is not: the keys are then not
+ * written (the offsets and flatten_ids determine the list;
+ * r2s_isect_keys_from_offsets recovers them), which r2splat.ops does, its
+ * backward kernels finding each record's key from the offsets.
  * n_isects is the capacity of the outputs and the size the workspace is
  * queried for; the kernels read the record count from offsets[C*N] on the
  * device and write nothing when it exceeds n_isects.  A caller may thus
@@ -363,6 +368,16 @@ int r2s_isect_emit_sort_3d_slab_f64(const double *means3d, const int32_t *radii,
 int r2s_isect_offset_encode(const int64_t *isect_ids, int64_t n_isects,
                             int64_t n_keys, int32_t *tile_offsets,
                             r2s_stream_t stream);
+
+/* The isect_ids output of IsectTiles.cpp:113-169 / IsectTiles3D.cpp:109-161
+ * recovered from a list's tile_offsets (the inverse of
+ * r2s_isect_offset_encode; no entry of its own in the reference), for lists
+ * sorted with isect_ids NULL: isect_ids[r] = the last key k with
+ * tile_offsets[k] <= r, for the n_isects records; tile_offsets [n_keys],
+ * tile_offsets[0] = 0. */
+int r2s_isect_keys_from_offsets(const int32_t *tile_offsets, int64_t n_keys,
+                                int64_t n_isects, int64_t *isect_ids,
+                                r2s_stream_t stream);
 
 /* ---------------------------------------------------------------------- */
 /* Line-integral rasterizer                                               */

@@ -336,6 +336,112 @@ def test_isect_tiles_3d_sort_widths(bricks):
                  "sort tile_offsets")
 
 
+def _windows_past_empty_keys(tile_offsets, n, walk=4):
+    """Whether some 64-record window of a list of n records holds more than
+    `walk` keys whose first index lies inside it after its first record's
+    key (empty keys count: they share their successor's first index), so
+    that the backward's key search bisects per lane there."""
+    o = np32(tile_offsets).reshape(-1).astype(np.int64)
+    rb = np.arange(0, n, 64)
+    lo = np.searchsorted(o, rb, side="right") - 1
+    hi = np.searchsorted(o, np.minimum(rb + 63, n - 1), side="right") - 1
+    return bool(((hi - lo) > walk).any())
+
+
+@pytest.mark.parametrize("views", [1, 3])
+def test_lists_without_keys(views):
+    # r2splat.ops bins without storing the sorted int64 keys: the sort writes
+    # none (1024 tiles: one pass; 3072: two passes, the tile offsets searched
+    # in the sort's own 32-bit keys) and the backward finds each record's tile
+    # from the tile offsets.  Footprints clustered in a few tiles leave runs of
+    # empty tiles inside 64-record windows, where that search bisects per
+    # lane.  Everything equals the lists binned with their keys, bit for bit.
+    g = torch.Generator().manual_seed(41 + views)
+    N, W_img, H_img, ts = 3000, 512, 512, 16
+    tw, th = W_img // ts, H_img // ts
+    cells = torch.randint(0, tw * th, (views, N // 20), generator=g)
+    pick = torch.gather(cells, 1, torch.randint(0, N // 20, (views, N), generator=g))
+    centre = torch.stack([(pick % tw).float(), (pick // tw).float()], -1) * ts + ts / 2
+    m2 = centre + (torch.rand(views, N, 2, generator=g) - 0.5) * 12
+    a = 0.05 + 0.1 * torch.rand(views, N, generator=g)
+    c = 0.05 + 0.1 * torch.rand(views, N, generator=g)
+    b = (torch.rand(views, N, generator=g) - 0.5) * 0.5 * (a * c).sqrt()
+    con = torch.stack([a, b, c], -1)
+    op = 0.2 + 0.8 * torch.rand(views, N, generator=g)
+    mu = 0.5 + torch.rand(views, N, generator=g)
+    r = torch.randint(2, 10, (views, N, 2), generator=g).int()
+    m2, con, op, mu, r = (t.to(DEV) for t in (m2, con, op, mu, r))
+    with_ids = _ops.bin_tiles_2d(m2, r, ts, tw, th)
+    without = _ops.bin_tiles_2d(m2, r, ts, tw, th, keep_ids=False)
+    assert without.keys is None and with_ids.keys is not None
+    for name in ("tiles_per_gauss", "flatten_ids", "emit_ids", "isect_src", "tile_offsets"):
+        assert torch.equal(getattr(without, name), getattr(with_ids, name)), name
+    assert torch.equal(without.isect_ids, with_ids.keys)
+    n = with_ids.flatten_ids.numel()
+    off = with_ids.tile_offsets
+    assert n > 3000 and _windows_past_empty_keys(off, n)
+    v = torch.randn(views, H_img, W_img, generator=g).to(DEV)
+    payload, _ = _ops.raster_pack(m2, con, op, mu)
+    for absgrad in (True, False):
+        want = _ops.raster_backward(m2, con, op, mu, off, with_ids, v, W_img, H_img, ts, absgrad)
+        got = _ops.raster_backward(m2, con, op, mu, off, without, v, W_img, H_img, ts, absgrad)
+        _same_grads(got, want, exact=True)
+        got = _ops.raster_backward_packed(payload, op, mu, off, without, v, W_img, H_img, ts,
+                                          absgrad)
+        _same_grads(got, want, exact=True)
+        # Tile order (one-pass kernels, atomics): keys from the offsets too.
+        one = _ops.TileLists(None, None, with_ids.flatten_ids.clone(), None, None, off)
+        got = _ops.raster_backward(m2, con, op, mu, off, one, v, W_img, H_img, ts, absgrad)
+        _same_grads(got, want, exact=False)
+
+
+@pytest.mark.parametrize("bricks", [(8, 8, 8), (16, 16, 16), (40, 36, 32), (256, 256, 160)])
+def test_volume_lists_without_keys(bricks):
+    # As test_lists_without_keys for brick lists: 512 bricks (one sort pass),
+    # 4096 and 46080 (two passes) and 10.5 M (three passes; lists only), and
+    # the slab lists of a large volume's z-slabs.  Gaussians in a few
+    # clusters; the backward in its two emission-order forms (with and
+    # without the forward's reach masks).
+    n2, n1, n0 = bricks
+    dims = (8 * n2, 8 * n1, 8 * n0)
+    d = _prepared(3000, 43, log_mu=-4.0)
+    g = d["gen"]
+    centres = torch.rand(30, 3, generator=g) * 1.8 - 0.9
+    means = centres[torch.randint(0, 30, (3000,), generator=g)]
+    means = (means + 0.02 * torch.randn(3000, 3, generator=g)).to(DEV)
+    m3, con, r3 = W.world_to_volume_mapping_fwd(means, d["covars"], d["opac"],
+                                                torch.full((3,), 2.0, device=DEV),
+                                                torch.zeros(3, device=DEV), *dims, 1e-8, 3.0)
+    op = d["opac"]
+    with_ids = _ops.bin_tiles_3d(m3, r3, 8, n2, n1, n0)
+    without = _ops.bin_tiles_3d(m3, r3, 8, n2, n1, n0, keep_ids=False)
+    assert without.keys is None
+    for name in ("tiles_per_gauss", "flatten_ids", "emit_ids", "isect_src", "tile_offsets"):
+        assert torch.equal(getattr(without, name), getattr(with_ids, name)), name
+    assert torch.equal(without.isect_ids, with_ids.keys)
+    n = with_ids.flatten_ids.numel()
+    off = with_ids.tile_offsets
+    assert n > 3000 and _windows_past_empty_keys(off, n)
+    z0, z1 = n0 // 4, n0 // 2 + 1
+    sl_k, off_k = _ops.bin_tiles_3d_slab(m3, r3, 8, n2, n1, n0, z0, z1)
+    sl_n, off_n = _ops.bin_tiles_3d_slab(m3, r3, 8, n2, n1, n0, z0, z1, keep_ids=False)
+    assert sl_n.keys is None and torch.equal(off_n, off_k)
+    assert torch.equal(sl_n.flatten_ids, sl_k.flatten_ids)
+    assert torch.equal(sl_n.isect_ids, sl_k.keys)
+    if n2 * n1 * n0 > 50_000:
+        return
+    d2, d1, d0 = dims
+    vol, reach = _ops.voxelize_with_reach(m3, con, op, off, with_ids.flatten_ids, d2, d1, d0)
+    v = torch.randn(vol.shape, generator=g).to(DEV)
+    for rc in (reach, None):
+        want = _ops.voxel_backward(m3, con, op, off, with_ids, v, d2, d1, d0, 8, reach=rc)
+        got = _ops.voxel_backward(m3, con, op, off, without, v, d2, d1, d0, 8, reach=rc)
+        _same_grads(got, want, exact=True)
+    want = _ops.voxel_backward_slab(m3, con, op, off_k, sl_k, v, 8, z0)
+    got = _ops.voxel_backward_slab(m3, con, op, off_n, sl_n, v, 8, z0)
+    _same_grads(got, want, exact=True)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
 def test_volume_mapping_bit_exact(dtype):
     d = _prepared(4000, 6, dtype, log_mu=-3.0)
