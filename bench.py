@@ -573,9 +573,11 @@ def kernel_breakdown(proj: Projection, reps):
                                                   fwd_ws.numel(), stream)
             assert rc == 0, lib.r2s_last_error()
 
+        # The rows pass as r2splat.ops calls it: no int64 keys (each wave's
+        # keys come from the tile offsets).
         def bwd_rows():
             stream = torch.cuda.current_stream().cuda_stream
-            rc = lib.r2s_rasterize_bwd_rows_packed_f32(P(payload), P(off), P(ids), P(fl),
+            rc = lib.r2s_rasterize_bwd_rows_packed_f32(P(payload), P(off), None, P(fl),
                                                        P(isect_src), n, P(v_img), 1, N_PROJ, det,
                                                        det, 16, nt, nt, 1, P(rows), rows.numel(),
                                                        stream)
@@ -638,8 +640,9 @@ def voxel_breakdown(vox, reps):
                                       8, nb, nb, nb, P(volume), stream())
         assert rc == 0, lib.r2s_last_error()
 
+    # The rows passes without int64 keys, as r2splat.ops calls them.
     def bwd_rows():
-        rc = lib.r2s_voxelize_bwd_rows_f32(P(m3), P(con), P(vox.opac), P(off), P(ids), P(fl),
+        rc = lib.r2s_voxelize_bwd_rows_f32(P(m3), P(con), P(vox.opac), P(off), None, P(fl),
                                            P(isect_src), n, P(vox.v_volume), N, d, d, d, 8, nb,
                                            nb, nb, P(rows), rows.numel(), stream())
         assert rc == 0, lib.r2s_last_error()
@@ -657,7 +660,7 @@ def voxel_breakdown(vox, reps):
         assert rc == 0, lib.r2s_last_error()
 
     def bwd_rows_reach():
-        rc = lib.r2s_voxelize_bwd_rows_reach_f32(P(m3), P(con), P(vox.opac), P(off), P(ids),
+        rc = lib.r2s_voxelize_bwd_rows_reach_f32(P(m3), P(con), P(vox.opac), P(off), None,
                                                  P(fl), P(isect_src), n, P(vox.v_volume), N, d,
                                                  d, d, 8, nb, nb, nb, P(reach), P(rows),
                                                  rows.numel(), stream())
