@@ -77,6 +77,21 @@ __device__ __forceinline__ bool alpha_pass(T sl, typename Bits<T>::type limit) {
   return bits_of(sl) < limit;
 }
 
+// acc += w 2^-sl where the alpha test passes.  As a branch, not a select:
+// the empty asm statement cannot be speculated, so the compiler keeps the
+// branch, the test masks the exp and the FMA through EXEC with scalar
+// instructions instead of a vector select (one vector instruction fewer per
+// pixel / voxel), and a wave whose lanes all fail skips both.  A failing
+// pair adds nothing, where the select added w * 0: the same sum for a finite
+// w, and for a non-finite one no NaN from a pair the reference skips.
+template <typename T>
+__device__ __forceinline__ void add_passing(T sl, typename Bits<T>::type limit, T w, T &acc) {
+  if (alpha_pass(sl, limit)) {
+    asm volatile("");
+    acc = fma(w, neg_exp2(sl), acc);
+  }
+}
+
 // Bits of a limit kept in a T slot (forward records stage it in LDS).
 __device__ __forceinline__ float limit_as_value(uint32_t b) { return __uint_as_float(b); }
 __device__ __forceinline__ double limit_as_value(uint64_t b) {

@@ -318,8 +318,7 @@ __global__ __launch_bounds__(kFwdBatch) void raster_fwd_rows_kernel(
       for (int k = 0; k < R; ++k) {
         const T dx = kStageDx ? dxs[k] : pxk[k] - p.x;
         const T sl = (p.z * dx + B) * dx + C;
-        const T e = neg_exp2(sl);
-        acc[k] = fma(q.y, alpha_pass(sl, lim) ? e : static_cast<T>(0), acc[k]);
+        add_passing(sl, lim, q.y, acc[k]);
       }
     }
   }

@@ -165,8 +165,7 @@ __global__ __launch_bounds__(1024) void voxel_fwd_kernel(
       for (int r = 0; r < R; ++r) {
         const T dx = (px0 + static_cast<T>(r)) - mo.x;
         const T sl = (h0.x * dx + B) * dx + C;
-        const T e = neg_exp2(sl);
-        acc[r] = fma(mo.w, alpha_pass(sl, lim) ? e : static_cast<T>(0), acc[r]);
+        add_passing(sl, lim, mo.w, acc[r]);
       }
     }
   }
@@ -437,8 +436,7 @@ __global__ __launch_bounds__(64 * S) void voxel_fwd_reach_kernel(
       for (int k = 0; k < R; ++k) {
         const T dx = dxs[k];
         const T sl = (qa.w * dx + B) * dx + C;
-        const T e = neg_exp2(sl);
-        acc[k] = fma(qa.z, alpha_pass(sl, lim) ? e : static_cast<T>(0), acc[k]);
+        add_passing(sl, lim, qa.z, acc[k]);
       }
     }
   }
