@@ -31,31 +31,66 @@ struct AdamTable {
   r2s_adam_tensor_t t[kAdamMaxTensors];
 };
 
+// The roundings are spelled out (explicit FMAs, __fmul_rn / __fdiv_rn /
+// __fadd_rn where torch's kernels round a product, quotient or sum on its
+// own), so the compiler's contraction choices, which differ between the two
+// load paths below, cannot change them.
+
 // ATen's lerp: weight below one half from the start, else from the end.
 __device__ __forceinline__ float lerp(float a, float b, float w) {
-  return fabsf(w) < 0.5f ? a + w * (b - a) : b - (b - a) * (1.0f - w);
+  const float d = b - a;
+  return fabsf(w) < 0.5f ? fmaf(w, d, a) : fmaf(-d, 1.0f - w, b);
 }
 
+struct AdamScalars {
+  float w1, b2, omb2, wd, bc2s, eps, ss;
+};
+
+__device__ __forceinline__ void adam_one(const AdamScalars &c, float &p, float g, float &m,
+                                         float &v) {
+  if (c.wd != 0.0f) g = fmaf(c.wd, p, g);  // grad.add(param, alpha=wd)
+  m = lerp(m, g, c.w1);
+  // mul_(beta2), then ATen's pointwise addcmul: self + value * (t1 * t2).
+  v = fmaf(c.omb2, __fmul_rn(g, g), __fmul_rn(v, c.b2));
+  const float den = __fadd_rn(__fdiv_rn(sqrtf(v), c.bc2s), c.eps);
+  p = fmaf(c.ss, __fdiv_rn(m, den), p);  // addcdiv_: self + value * (t1 / t2)
+}
+
+// Each thread's four elements move as one 16-byte load or store per array
+// when all four arrays are 16-byte aligned and the four are in range (the
+// usual case); otherwise element by element.
 __global__ __launch_bounds__(kAdamThreads) void adam_kernel(AdamTable tab) {
   const r2s_adam_tensor_t &d = tab.t[blockIdx.y];
   const int64_t base =
       (static_cast<int64_t>(blockIdx.x) * kAdamThreads + threadIdx.x) * kAdamPerThread;
   if (base >= d.n) return;
-  const float w1 = d.lerp_weight, b2 = d.beta2, omb2 = d.one_minus_beta2;
-  const float wd = d.weight_decay, bc2s = d.bias_correction2_sqrt, eps = d.eps;
-  const float ss = d.step_size;
+  const AdamScalars c{d.lerp_weight, d.beta2, d.one_minus_beta2, d.weight_decay,
+                      d.bias_correction2_sqrt, d.eps, d.step_size};
+  const uintptr_t any = reinterpret_cast<uintptr_t>(d.param) |
+                        reinterpret_cast<uintptr_t>(d.grad) |
+                        reinterpret_cast<uintptr_t>(d.exp_avg) |
+                        reinterpret_cast<uintptr_t>(d.exp_avg_sq);
+  if (any % 16 == 0 && base + kAdamPerThread <= d.n) {
+    static_assert(kAdamPerThread == 4, "one float4 per thread and array");
+    float4 p = *reinterpret_cast<const float4 *>(d.param + base);
+    const float4 g = *reinterpret_cast<const float4 *>(d.grad + base);
+    float4 m = *reinterpret_cast<const float4 *>(d.exp_avg + base);
+    float4 v = *reinterpret_cast<const float4 *>(d.exp_avg_sq + base);
+    adam_one(c, p.x, g.x, m.x, v.x);
+    adam_one(c, p.y, g.y, m.y, v.y);
+    adam_one(c, p.z, g.z, m.z, v.z);
+    adam_one(c, p.w, g.w, m.w, v.w);
+    *reinterpret_cast<float4 *>(d.exp_avg + base) = m;
+    *reinterpret_cast<float4 *>(d.exp_avg_sq + base) = v;
+    *reinterpret_cast<float4 *>(d.param + base) = p;
+    return;
+  }
 #pragma unroll
   for (int k = 0; k < kAdamPerThread; ++k) {
     const int64_t i = base + k;
     if (i >= d.n) break;
-    float p = d.param[i];
-    float g = d.grad[i];
-    if (wd != 0.0f) g = g + wd * p;
-    const float m = lerp(d.exp_avg[i], g, w1);
-    float v = d.exp_avg_sq[i] * b2;
-    v = v + omb2 * (g * g);  // ATen's pointwise addcmul: self + value * (t1 * t2)
-    const float den = sqrtf(v) / bc2s + eps;
-    p = p + ss * (m / den);
+    float p = d.param[i], m = d.exp_avg[i], v = d.exp_avg_sq[i];
+    adam_one(c, p, d.grad[i], m, v);
     d.exp_avg[i] = m;
     d.exp_avg_sq[i] = v;
     d.param[i] = p;

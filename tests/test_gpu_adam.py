@@ -65,6 +65,36 @@ def test_fused_step_equals_torch_adam(wd):
             assert u[0] <= 1 and u[1] <= 1 and u[2] <= 2, (k, step, u)
 
 
+def test_misaligned_parameters_take_the_element_path():
+    # Parameters viewing their storage one element in: the kernel's 16-byte
+    # loads do not apply, so every element goes through the element loop,
+    # which must give the same values as torch's Adam (and as the aligned
+    # path, which test_fused_step_equals_torch_adam checks).
+    init, grads = _params(6), _grads(7, 3)
+    ref_p, ref_o = _build(init, torch.optim.Adam, foreach=True)
+    our_p = {}
+    for k, v in init.items():
+        flat = torch.empty(v.numel() + 1, device=DEV)
+        view = flat[1:].view(v.shape)
+        view.copy_(v)
+        our_p[k] = torch.nn.Parameter(view)
+        assert our_p[k].data_ptr() % 16 != 0
+    our_o = {k: optim.Adam([{"params": p, "name": k}], lr=LRS[k], eps=1e-15)
+             for k, p in our_p.items()}
+    for gr in grads:
+        for k in SHAPES:
+            ref_p[k].grad = gr[k].clone()
+            our_p[k].grad = gr[k].clone()
+        for o in ref_o.values():
+            o.step()
+        optim.step_all(our_o)
+        for k in SHAPES:
+            rs, os_ = ref_o[k].state[ref_p[k]], our_o[k].state[our_p[k]]
+            u = (_ulps(rs["exp_avg"], os_["exp_avg"]), _ulps(rs["exp_avg_sq"], os_["exp_avg_sq"]),
+                 _ulps(ref_p[k].detach(), our_p[k].detach()))
+            assert u[0] <= 1 and u[1] <= 1 and u[2] <= 2, (k, u)
+
+
 def test_fused_step_matches_the_oracle():
     init, grads = _params(2), _grads(3, 5)
     our_p, our_o = _build(init, optim.Adam, betas=(0.8, 0.99))
