@@ -78,20 +78,21 @@ __device__ __forceinline__ bool alpha_pass(T sl, typename Bits<T>::type limit) {
 }
 
 // acc += w 2^-sl where the alpha test passes.  As a branch, not a select:
-// the empty asm statement in it cannot be speculated, so the compiler keeps
-// the branch, and the test masks the FMA through EXEC with scalar
+// the scheduling barrier in it cannot be speculated, so the compiler keeps
+// the branch, and the test masks the FMA through EXEC with two scalar
 // instructions instead of a vector select (one vector instruction fewer per
-// pixel / voxel, and no wait on the compare's VCC); a wave whose lanes all
-// fail skips the FMA.  The exp is formed before the branch (the asm statement
-// on it keeps it there), so the compare and the mask cover its latency.  A
-// failing pair adds nothing, where the select added w * 0: the same sum for
-// a finite w, and for a non-finite one no NaN from a pair the reference skips.
+// pixel / voxel, and no wait on the compare's VCC); the barrier emits no
+// code, so no skip branch is added around the one FMA either.  The exp is
+// formed before the branch (the asm statement on it keeps it there), so the
+// compare and the mask cover its latency.  A failing pair adds nothing,
+// where the select added w * 0: the same sum for a finite w, and for a
+// non-finite one no NaN from a pair the reference skips.
 template <typename T>
 __device__ __forceinline__ void add_passing(T sl, typename Bits<T>::type limit, T w, T &acc) {
   T e = neg_exp2(sl);
   asm volatile("" : "+v"(e));
   if (alpha_pass(sl, limit)) {
-    asm volatile("");
+    __builtin_amdgcn_sched_barrier(0);
     acc = fma(w, e, acc);
   }
 }
