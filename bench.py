@@ -565,6 +565,16 @@ def kernel_breakdown(proj: Projection, reps):
             assert rc == 0, lib.r2s_last_error()
 
         pack()
+        proj_out = [torch.empty_like(t) for t in (m2, c2, r, con, mu, opc)]
+
+        def project_pack():
+            # r2splat.ops' projection launch: the projection, the payload and
+            # the zeros of the backward's outputs in one kernel.
+            stream = torch.cuda.current_stream().cuda_stream
+            rc = lib.r2s_project_pack_fwd_f32(P(means), P(cov), P(op), P(vm), P(Ks), det, det,
+                                              EPS, 3.0, *[P(t) for t in proj_out], P(payload),
+                                              *[P(t) for t in outs], 1, N_PROJ, stream)
+            assert rc == 0, lib.r2s_last_error()
 
         def fwd_packed():
             stream = torch.cuda.current_stream().cuda_stream
@@ -594,6 +604,7 @@ def kernel_breakdown(proj: Projection, reps):
             "prepare": lambda: W.prepare_gaussians(quats, scales, opac, SMIN, SMAX),
             "project_fwd": lambda: W.project_gaussians_fwd(means, cov, op, vm, Ks, det, det,
                                                            EPS, 3.0),
+            "project_pack_fwd": project_pack,
             "binning_2d": lambda: W.isect_tiles(m2, r, 16, nt, nt),
             "rasterize_fwd": lambda: W.rasterize_to_pixels_fwd(m2, con, opc, mu, off, fl, det,
                                                                det, 16),
@@ -606,7 +617,7 @@ def kernel_breakdown(proj: Projection, reps):
         }
         for name, fn in stages.items():
             per_view.setdefault(name, []).append(time_kernel(fn, reps))
-        del rows, outs, payload, fwd_ws, image
+        del rows, outs, payload, fwd_ws, image, proj_out
     mean = {k: sum(v) / len(v) for k, v in per_view.items()}
     return {"n_isects_2d": counts[0], "n_isects_per_view": counts, "seconds": mean,
             "per_view_seconds": {k: per_view[k] for k in ("rasterize_fwd", "rasterize_fwd_packed",
@@ -1079,6 +1090,7 @@ def main():
         "rasterize_fwd_packed": 32 * i2_mean + 4 * n_pix,   # id 4 + payload 28; image write
         "rasterize_pack": 64 * N_PROJ,   # 28 in, 36 zeros out per Gaussian
         "project_fwd": 108 * N_PROJ,
+        "project_pack_fwd": 176 * N_PROJ,  # the projection's 108, payload 32, zeros 36
         "prepare": 76 * N_PROJ,
     }[dom]
     result["roofline"] = kernel_roofline(dom, secs[dom], dom_bytes, 256 * i2_mean)

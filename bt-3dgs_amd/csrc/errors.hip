@@ -33,4 +33,4 @@ int check_launch(const char *what) {
 extern "C" const char *r2s_last_error(void) { return r2s::g_message; }
 
 // ABI revision of include/r2splat_hip.h.
-extern "C" int r2s_abi_version(void) { return 9; }
+extern "C" int r2s_abi_version(void) { return 10; }

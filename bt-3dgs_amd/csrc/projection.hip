@@ -11,6 +11,11 @@
 // WorldToImageProjectionBwd.cu, ConicsMuFwd.cu and ConicsMuBwd.cu term by
 // term with contraction off; with IEEE division and square root the float32
 // outputs are reproducible bit-for-bit by an IEEE CPU restatement.
+// The rasterizer's payload writer, included before the pragma below so that
+// it is compiled as in the rasterizer (the fused projection writes the same
+// bits as raster_pack_kernel).
+#include "r2s_payload.h"
+
 #pragma clang fp contract(off)
 
 #include "r2s_common.h"
@@ -317,14 +322,19 @@ __device__ __forceinline__ void project_bwd_one(const Camera<T> &c, const T p[3]
 // ---------------------------------------------------------------- kernels --
 
 // Projection forward; optionally fused with conics/mu and the opacity
-// broadcast (conics == nullptr selects the plain operator).
+// broadcast (conics == nullptr selects the plain operator), and then with the
+// rasterizer's packed payload (payload != nullptr: what raster_pack_kernel
+// writes from these outputs) and the zeros of the raster backward's outputs
+// (z_xy != nullptr).
 template <typename T>
 __global__ __launch_bounds__(256) void project_fwd_kernel(
     const T *__restrict__ means, const T *__restrict__ covars, const T *__restrict__ opac,
     const T *__restrict__ viewmats, const T *__restrict__ Ks, uint32_t width, uint32_t height,
     T eps, T eps_conic, T clip, T *__restrict__ means2d, T *__restrict__ cov2d,
     int32_t *__restrict__ radii, T *__restrict__ conics, T *__restrict__ mus,
-    T *__restrict__ opac_cn, int64_t C, int64_t N) {
+    T *__restrict__ opac_cn, int64_t C, int64_t N, T *__restrict__ payload,
+    T *__restrict__ z_xy, T *__restrict__ z_abs, T *__restrict__ z_conic,
+    T *__restrict__ z_opac, T *__restrict__ z_mu) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (idx >= C * N) return;
   const int64_t cam = idx / N, g = idx - cam * N;
@@ -347,7 +357,12 @@ __global__ __launch_bounds__(256) void project_fwd_kernel(
     conics[3 * idx + 1] = con[1];
     conics[3 * idx + 2] = con[2];
     mus[idx] = mu;
-    opac_cn[idx] = opac[g];
+    const T o_g = opac[g];
+    opac_cn[idx] = o_g;
+    if (payload != nullptr) {
+      if (z_xy != nullptr) store_raster_zeros(idx, z_xy, z_abs, z_conic, z_opac, z_mu);
+      store_payload(payload, idx, o.mx, o.my, con[0], con[1], con[2], o_g * mu);
+    }
   }
 }
 
@@ -506,19 +521,27 @@ template <typename T>
 int project_fwd_impl(const T *means, const T *covars, const T *opac, const T *viewmats,
                      const T *Ks, uint32_t width, uint32_t height, double eps2d, float clip,
                      T *means2d, T *cov2d, int32_t *radii, T *conics, T *mus, T *opac_cn,
-                     int64_t C, int64_t N, r2s_stream_t stream, const char *name) {
+                     int64_t C, int64_t N, r2s_stream_t stream, const char *name,
+                     T *payload = nullptr, T *v_xy_abs = nullptr, T *v_xy = nullptr,
+                     T *v_conic = nullptr, T *v_opac = nullptr, T *v_mu = nullptr) {
   clear_error();
   R2S_RETURN_IF(check_sizes(C, N, name));
   R2S_REQUIRE(clip > 0.0f, "radius_clip must be positive, got %g", (double)clip);
+  R2S_REQUIRE(payload == nullptr || reinterpret_cast<uintptr_t>(payload) % 16 == 0,
+              "%s: payload not 16-byte aligned", name);
+  R2S_REQUIRE(v_xy == nullptr || (v_conic && v_opac && v_mu),
+              "%s: zero targets need v_means2d, v_conics, v_opacities and v_mus", name);
   if (C * N == 0) return R2S_OK;
   R2S_REQUIRE(means && covars && viewmats && Ks && means2d && cov2d && radii,
               "%s: null pointer", name);
   R2S_REQUIRE(conics == nullptr || (mus && opac && opac_cn), "%s: null pointer", name);
+  R2S_REQUIRE(payload == nullptr || conics != nullptr, "%s: null conics", name);
   const int64_t blocks = ceil_div(C * N, 256);
   project_fwd_kernel<T><<<dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, as_stream(stream)>>>(
       means, covars, opac, viewmats, Ks, width, height,
       static_cast<T>(static_cast<float>(eps2d)), static_cast<T>(eps2d), static_cast<T>(clip),
-      means2d, cov2d, radii, conics, mus, opac_cn, C, N);
+      means2d, cov2d, radii, conics, mus, opac_cn, C, N, payload, payload ? v_xy : nullptr,
+      v_xy_abs, v_conic, v_opac, v_mu);
   return check_launch(name);
 }
 
@@ -624,6 +647,20 @@ extern "C" {
     return r2s::project_fwd_impl<T>(means, covars, opac, viewmats, Ks, width, height, eps2d,  \
                                     clip, means2d, cov2d, radii, conics, mus, opac_cn, C, N,  \
                                     st, "project_gaussians_fwd");                             \
+  }                                                                                           \
+  int r2s_project_pack_fwd_##SUF(                                                             \
+      const T *means, const T *covars, const T *opac, const T *viewmats, const T *Ks,         \
+      uint32_t width, uint32_t height, double eps2d, float clip, T *means2d, T *cov2d,        \
+      int32_t *radii, T *conics, T *mus, T *opac_cn, T *payload, T *v_xy_abs, T *v_xy,        \
+      T *v_conic, T *v_opac, T *v_mu, int64_t C, int64_t N, r2s_stream_t st) {                \
+    if (conics == nullptr || payload == nullptr) {                                            \
+      r2s::set_error("project_pack_fwd: null conics or payload");                            \
+      return R2S_EINVAL;                                                                      \
+    }                                                                                         \
+    return r2s::project_fwd_impl<T>(means, covars, opac, viewmats, Ks, width, height, eps2d,  \
+                                    clip, means2d, cov2d, radii, conics, mus, opac_cn, C, N,  \
+                                    st, "project_pack_fwd", payload, v_xy_abs, v_xy,          \
+                                    v_conic, v_opac, v_mu);                                   \
   }                                                                                           \
   int r2s_world_to_image_projection_bwd_##SUF(                                                \
       const T *means, const T *covars, const T *viewmats, const T *Ks, uint32_t width,        \

@@ -24,6 +24,7 @@
 // share these kernels.
 #include "r2s_common.h"
 #include "r2s_cull.h"
+#include "r2s_payload.h"
 #include "r2s_rows.h"
 #include "r2s_scan.h"
 
@@ -55,7 +56,6 @@ struct Vec<double> {
 __device__ __forceinline__ float fast_exp(float x) { return __expf(x); }
 __device__ __forceinline__ double fast_exp(double x) { return exp(x); }
 
-constexpr double kThr2 = 1e-5;
 constexpr int kBwdThreads = 256;
 // Pixels of a row evaluated together: an unrolled 8-pixel body in a rolled
 // loop keeps the kernel at 62 VGPRs (8 waves per SIMD) without spills.
@@ -136,8 +136,6 @@ __global__ __launch_bounds__(1024) void raster_fwd_kernel(
 // per-pixel order differs from a plain list-order sum only by rounding).
 constexpr int kFwdWaves = 8;
 constexpr int kFwdBatch = 64 * kFwdWaves;
-// Values per (view, Gaussian) of the packed payload (raster_pack_kernel).
-constexpr int kPayloadValues = 8;
 
 // One staged forward record: {x, y, h_a, h_b} and {h_c, o mu, limit bits, 0}.
 template <typename T>
@@ -422,7 +420,8 @@ __device__ __forceinline__ void load_raster_record(
 // -- so that a record's gather touches one sector instead of four arrays'
 // lines, and the per-record culling setup runs once per Gaussian.  The rows
 // need no o or mu apart from o mu: the reduction forms the opacity and mu
-// partials from T0.
+// partials from T0.  The fused projection (r2s_project_pack_fwd_*) writes
+// the same payload (store_payload) from its own results.
 
 // With z_xy non-null it also stores zeros into the backward's outputs
 // (v_xy_abs may be null), which the reduction then overwrites for every pair
@@ -433,31 +432,11 @@ __global__ __launch_bounds__(256) void raster_pack_kernel(
     const T *__restrict__ mus, int64_t n_items, T *__restrict__ payload, T *__restrict__ z_xy,
     T *__restrict__ z_abs, T *__restrict__ z_conic, T *__restrict__ z_opac,
     T *__restrict__ z_mu) {
-  using V4 = typename Vec<T>::v4;
   const int64_t g = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (g >= n_items) return;
-  if (z_xy != nullptr) {
-    z_xy[2 * g] = z_xy[2 * g + 1] = static_cast<T>(0);
-    if (z_abs != nullptr) z_abs[2 * g] = z_abs[2 * g + 1] = static_cast<T>(0);
-    z_conic[3 * g] = z_conic[3 * g + 1] = z_conic[3 * g + 2] = static_cast<T>(0);
-    z_opac[g] = static_cast<T>(0);
-    z_mu[g] = static_cast<T>(0);
-  }
-  V4 p0, p1;
-  p0.x = means2d[2 * g];
-  p0.y = means2d[2 * g + 1];
-  p0.z = conics[3 * g];
-  p0.w = conics[3 * g + 1];
-  p1.x = conics[3 * g + 2];
-  p1.y = opac[g] * mus[g];
-  const bool fin = isfinite(p0.x) && isfinite(p0.y) && isfinite(p0.z) && isfinite(p0.w) &&
-                   isfinite(p1.x);
-  p1.z = limit_as_value(alpha_limit(p1.y, fin, kThr2));
-  const Cull2<T> cu = cull2_setup(p0.z, p0.w, p1.x, fabs(p1.y), kThr2);
-  p1.w = cu.ok ? cu.hy : static_cast<T>(-1);
-  V4 *dst = reinterpret_cast<V4 *>(payload + kPayloadValues * g);
-  dst[0] = p0;
-  dst[1] = p1;
+  if (z_xy != nullptr) store_raster_zeros(g, z_xy, z_abs, z_conic, z_opac, z_mu);
+  store_payload(payload, g, means2d[2 * g], means2d[2 * g + 1], conics[3 * g],
+                conics[3 * g + 1], conics[3 * g + 2], opac[g] * mus[g]);
 }
 
 // load_raster_record from the packed payload (o and mu are left zero).

@@ -33,6 +33,8 @@ _FLOAT_OPS = {
     "conics_mu_bwd": [_p, _f64, _p, _p, _p, _p, _p, _i64, _p],
     "project_gaussians_fwd": [_p, _p, _p, _p, _p, _u32, _u32, _f64, _f32, _p, _p, _p, _p, _p,
                               _p, _i64, _i64, _p],
+    "project_pack_fwd": [_p, _p, _p, _p, _p, _u32, _u32, _f64, _f32, _p, _p, _p, _p, _p, _p,
+                         _p, _p, _p, _p, _p, _p, _i64, _i64, _p],
     "project_gaussians_bwd": [_p, _p, _p, _p, _u32, _u32, _f64, _p, _p, _p, _p, _p, _p, _p, _p,
                               _i64, _i64, _p],
     "isect_count_2d": [_p, _p, _i32, _i64, _i64, _u32, _u32, _u32, _p, _p, _p, _sz, _p],
@@ -152,7 +154,7 @@ DENSIFY_MAX_WIDTH = 16
 
 SYMBOLS = sorted(list(_PLAIN) + [f"r2s_{n}_{s}" for n in _FLOAT_OPS for s in ("f32", "f64")])
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 
 def load(path: str = LIB_PATH) -> ctypes.CDLL:

@@ -513,6 +513,42 @@ def project_gaussians_fwd(means: Tensor, covars: Tensor, opacities: Tensor, view
     return means2d, cov2d, radii, conics, mus, opac
 
 
+def project_pack_fwd(means: Tensor, covars: Tensor, opacities: Tensor, viewmats: Tensor,
+                     Ks: Tensor, img_w: int, img_h: int, eps2d: float, radius_clip: float,
+                     zero_outputs: bool = False, absgrad: bool = False):
+    """:func:`project_gaussians_fwd` and :func:`raster_pack` on its outputs in
+    one launch -> (means2d, cov2d, radii, conics, mus, opacity[C,N], payload,
+    outputs), each bit for bit what the two calls return."""
+    for t, n in ((means, "means"), (covars, "covars"), (opacities, "opacities"),
+                 (viewmats, "viewmats"), (Ks, "Ks")):
+        _check_input(t, n)
+    C, N = _check_cameras(means, covars, viewmats, Ks)
+    _check(opacities.dim() == 1 and opacities.size(0) == N, "opacities must be 1D [N]")
+    _check(float(radius_clip) > 0.0, "radius_clip must be positive, got ", float(radius_clip))
+    dev, dt = means.device, means.dtype
+    means2d = torch.empty((C, N, 2), dtype=dt, device=dev)
+    cov2d = torch.empty((C, N, 6), dtype=dt, device=dev)
+    radii = torch.empty((C, N, 2), dtype=torch.int32, device=dev)
+    conics = torch.empty((C, N, 3), dtype=dt, device=dev)
+    mus = torch.empty((C, N), dtype=dt, device=dev)
+    opac = torch.empty((C, N), dtype=dt, device=dev)
+    payload = torch.empty((C * N * 8,), dtype=dt, device=dev)
+    outs = None
+    if zero_outputs:
+        outs = (torch.empty_like(means2d) if absgrad else None, torch.empty_like(means2d),
+                torch.empty_like(conics), torch.empty_like(opac), torch.empty_like(mus))
+    if C * N == 0:
+        return means2d, cov2d, radii, conics, mus, opac, payload, outs
+    sfx = _suffix(means, "project_pack_fwd")
+    z = (None,) * 5 if outs is None else outs
+    with torch.cuda.device(dev):
+        _call(f"r2s_project_pack_fwd_{sfx}", _ptr(means), _ptr(covars), _ptr(opacities),
+              _ptr(viewmats), _ptr(Ks), int(img_w), int(img_h), float(eps2d),
+              float(radius_clip), _ptr(means2d), _ptr(cov2d), _ptr(radii), _ptr(conics),
+              _ptr(mus), _ptr(opac), _ptr(payload), *[_ptr(t) for t in z], C, N, _stream(dev))
+    return means2d, cov2d, radii, conics, mus, opac, payload, outs
+
+
 def project_gaussians_bwd(means: Tensor, covars: Tensor, viewmats: Tensor, Ks: Tensor,
                           img_w: int, img_h: int, eps2d: float, cov2d: Tensor, conics: Tensor,
                           mus: Tensor, v_means2d: Tensor, v_conics: Tensor,

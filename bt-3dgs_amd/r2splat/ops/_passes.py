@@ -126,17 +126,20 @@ class ImagePass:
         width, height = int(img_w), int(img_h)
         ops = _ops()
         viewmats, Ks = viewmats.contiguous(), Ks.contiguous()
-        means2d, cov2d, radii, conics, mus, weights = ops.project_gaussians_fwd(
-            means.contiguous(), covars.contiguous(), opacities.contiguous(), viewmats, Ks,
-            width, height, float(eps2d), float(radius_clip))
-        across, down = _tiles_along(width, ts), _tiles_along(height, ts)
-        # The payload depends on the projection only: packed before the
-        # binning, whose record count the host waits for, so that the launch
-        # is queued while the device bins.
+        # The payload depends on the projection only: the projection's launch
+        # writes it (and, for the backward, zeros its outputs) from its own
+        # results, before the binning, whose record count the host waits for.
         payload = zeroed = None
         if ts in ops.PACKED_TILE_SIZES:
-            payload, zeroed = ops.raster_pack(means2d, conics, weights, mus,
-                                              zero_outputs=for_backward, absgrad=absgrad)
+            means2d, cov2d, radii, conics, mus, weights, payload, zeroed = ops.project_pack_fwd(
+                means.contiguous(), covars.contiguous(), opacities.contiguous(), viewmats, Ks,
+                width, height, float(eps2d), float(radius_clip), zero_outputs=for_backward,
+                absgrad=absgrad)
+        else:
+            means2d, cov2d, radii, conics, mus, weights = ops.project_gaussians_fwd(
+                means.contiguous(), covars.contiguous(), opacities.contiguous(), viewmats, Ks,
+                width, height, float(eps2d), float(radius_clip))
+        across, down = _tiles_along(width, ts), _tiles_along(height, ts)
         # The sorted int64 keys are not stored: the backward finds each
         # record's tile from the tile offsets (lists.isect_ids recovers them).
         lists = ops.bin_tiles_2d(means2d, radii, ts, across, down, keep_ids=False)

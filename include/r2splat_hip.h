@@ -572,6 +572,24 @@ int r2s_rasterize_pack_f64(const double *means2d, const double *conics,
                            double *payload, double *v_means2d_abs, double *v_means2d,
                            double *v_conics, double *v_opacities, double *v_mus,
                            r2s_stream_t stream);
+/* r2s_project_gaussians_fwd_* and r2s_rasterize_pack_* on its outputs in one
+ * launch (no counterpart in the reference, whose rasterizer has no payload):
+ * the same outputs, payload and zeros bit for bit, without the pack's reads
+ * of the projection's outputs.  payload (16-byte aligned) is required. */
+int r2s_project_pack_fwd_f32(
+    const float *means, const float *covars, const float *opacities,
+    const float *viewmats, const float *Ks, uint32_t width, uint32_t height,
+    double eps2d, float radius_clip, float *means2d, float *cov2d,
+    int32_t *radii, float *conics, float *mus, float *opacity_cn, float *payload,
+    float *v_means2d_abs, float *v_means2d, float *v_conics, float *v_opacities,
+    float *v_mus, int64_t C, int64_t N, r2s_stream_t stream);
+int r2s_project_pack_fwd_f64(
+    const double *means, const double *covars, const double *opacities,
+    const double *viewmats, const double *Ks, uint32_t width, uint32_t height,
+    double eps2d, float radius_clip, double *means2d, double *cov2d,
+    int32_t *radii, double *conics, double *mus, double *opacity_cn, double *payload,
+    double *v_means2d_abs, double *v_means2d, double *v_conics, double *v_opacities,
+    double *v_mus, int64_t C, int64_t N, r2s_stream_t stream);
 int r2s_rasterize_fwd_packed_f32(const float *payload, const int32_t *tile_offsets,
                                  const int32_t *flatten_ids, int64_t n_isects, int64_t C,
                                  int64_t N, uint32_t width, uint32_t height,

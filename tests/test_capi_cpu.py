@@ -57,6 +57,24 @@ def test_invalid_arguments_are_rejected_without_a_device(lib):
     assert rc == 1001 and b"tile_size" in lib.r2s_last_error()
 
 
+def test_fused_projection_pack_checks_its_arguments(lib):
+    args = [None] * 5 + [16, 16, 1e-8, 3.0] + [None] * 6
+    # No payload (or conics): the fused entry needs both.
+    rc = lib.r2s_project_pack_fwd_f32(*args, None, None, None, None, None, None, 1, 4, None)
+    assert rc == 1001 and b"null conics or payload" in lib.r2s_last_error()
+    conics = ctypes.c_void_p(64)  # never dereferenced: the checks come first
+    args[12] = conics
+    misaligned = ctypes.c_void_p(64 + 4)
+    rc = lib.r2s_project_pack_fwd_f32(*args, misaligned, None, None, None, None, None, 0, 4,
+                                      None)
+    assert rc == 1001 and b"16-byte aligned" in lib.r2s_last_error()
+    aligned = ctypes.c_void_p(128)
+    rc = lib.r2s_project_pack_fwd_f32(*args, aligned, None, aligned, None, None, None, 0, 4, None)
+    assert rc == 1001 and b"zero targets need" in lib.r2s_last_error()
+    rc = lib.r2s_project_pack_fwd_f32(*args, aligned, None, None, None, None, None, 0, 4, None)
+    assert rc == 0  # C * N == 0: nothing to do
+
+
 def test_tile_sizes_whose_products_wrap_are_rejected(lib):
     # 65536^2 and 2048^3 wrap to 0 in 32 bits; both must fail the tile-size
     # check before any launch (the backward would otherwise pick a kernel for

@@ -832,6 +832,45 @@ def test_packed_rasterizer_rejects_other_tile_sizes_and_empty_lists():
     assert all(not t.any() for t in got)
 
 
+def _bits(t):
+    """The tensor's bit patterns (NaNs compare equal to themselves)."""
+    if t.dtype == torch.float32:
+        return t.view(torch.int32)
+    if t.dtype == torch.float64:
+        return t.view(torch.int64)
+    return t
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("n_views,log_mu", [(1, -3.6), (3, -3.6), (2, -2.0)])
+def test_fused_projection_pack_equals_projection_then_pack(dtype, n_views, log_mu):
+    """r2s_project_pack_fwd_* against r2s_project_gaussians_fwd_* followed by
+    r2s_rasterize_pack_* on its outputs: the six projection outputs, the
+    payload and the zeroed raster backward outputs bit for bit, with and
+    without the zeros and with absgrad on and off; a NaN opacity and an
+    infinite covariance entry take the same non-finite branches in both."""
+    d = _prepared(3000, 23, dtype, n_det=64, n_views=n_views, log_mu=log_mu)
+    opac, covars = d["opac"].clone(), d["covars"].clone()
+    opac[5] = float("nan")
+    covars[9, 1] = float("inf")
+    args = (d["means"], covars, opac, d["viewmats"], d["Ks"], 64, 64, 1e-8, 3.0)
+    want = _ops.project_gaussians_fwd(*args)
+    m2, _, _, con, mu, op = want
+    want_payload, _ = _ops.raster_pack(m2, con, op, mu)
+    assert want_payload.isnan().any() and (want_payload.view(-1, 8)[:, 7] > 0).any()
+    for zero, absgrad in ((False, False), (True, False), (True, True)):
+        got = _ops.project_pack_fwd(*args, zero_outputs=zero, absgrad=absgrad)
+        for a, b in zip(got[:6], want):
+            assert a.shape == b.shape and torch.equal(_bits(a), _bits(b))
+        assert torch.equal(_bits(got[6]), _bits(want_payload))
+        outs = got[7]
+        if not zero:
+            assert outs is None
+            continue
+        assert (outs[0] is None) == (not absgrad)
+        assert all(t is None or (t.numel() > 0 and not t.any()) for t in outs)
+
+
 def _voxel_case(n, seed, dims, ts, dtype=torch.float32, log_mu=-3.2):
     d = _prepared(n, seed, dtype, log_mu=log_mu)
     ranges = torch.full((3,), 2.0, dtype=dtype, device=DEV)
